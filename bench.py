@@ -1,0 +1,158 @@
+"""Benchmark of the MI355X decode megakernel (BASELINE.json metric).
+
+Workload (the north-star): Qwen3-0.6B-shaped decoder
+(28 layers, hidden 1024, 16/8 heads, head_dim 64, SwiGLU 2816, tied vocab
+151936), random bf16 weights N(0, 0.02) generated on the device, KV cache
+prefilled to 1024 positions with N(0, 1) bf16, batch 1, greedy decode.
+
+A step is one greedy decode token.  After W warm-up tokens, the timed region
+is ONE resident launch (megakernel_generate) that decodes exactly K tokens
+starting at position `--ctx`, bracketed by device synchronisation; it is
+repeated `--reps` times (KV re-prefilled before each) and the median is
+reported.  `value` = K / wall seconds of that launch (inputs already in HBM).
+
+Also reported: the kernel's HIP-event time, the roofline of the decode kernel
+(algorithmic bytes = weights + KV read + KV write per token, over its event
+time, against 8 TB/s), and the CPU baseline: the repo's PyTorch oracle timed
+on the host's cores on a bounded sample of BASELINE configs[0].
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "batch-1 decode tok/s at ctx 1024; achieved HBM GB/s as % of 8 TB/s peak"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="decode tokens in the timed launch")
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--reps", type=int, default=5)
+    ap.add_argument("--ctx", type=int, default=1024)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
+                    help="measured HBM bytes per launch (rocprofv3 --pmc), if present")
+    return ap.parse_args()
+
+
+def cpu_baseline(dw, shape, seed: int, budget_s: float) -> dict:
+    """Oracle (PyTorch, fp32 activations, bf16 weights upcast once to fp32) on
+    the host cores: BASELINE configs[0] = 16-token prompt then greedy decode,
+    timed over as many decode tokens as fit in `budget_s` (at least 3)."""
+    import torch
+
+    from oracle import layout as olayout
+    from oracle import qwen3_ref, synth
+    osh = olayout.Shape(shape.hidden, shape.n_q_heads, shape.n_kv_heads, shape.head_dim, shape.ffn,
+                        shape.n_layers, shape.vocab)
+    bits = qwen3_ref.unpack_flat(osh, dw.to_host(), dw.layout.offsets)
+    orc = qwen3_ref.Qwen3Oracle(osh, bits, 128)
+    prompt = synth.prompt_tokens(seed, 16, shape.vocab)
+    for t in prompt[:-1]:
+        orc.step(t)
+    tok = orc.step(prompt[-1])["token"]
+    tok = orc.step(tok)["token"]  # warm-up decode steps
+    tok = orc.step(tok)["token"]
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or (time.perf_counter() - t0 < budget_s and n < 64):
+        tok = orc.step(tok)["token"]
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"BASELINE configs[0] (full 28-layer model, 16-token prompt), {n} greedy decode "
+                      f"tokens at positions 18..{17 + n} timed after 2 warm-up tokens; "
+                      "PyTorch CPU oracle, bf16 weights upcast to fp32"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the batch-1 decode path does not "
+                                   "shard (see DESIGN.md); run with --gpus 1"}))
+        sys.exit(2)
+    from megakernel_amd import launcher
+    from megakernel_amd.bridge import MegakernelEngine
+    from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
+    from megakernel_amd.weights import DeviceWeights
+
+    shape = BASELINE
+    K, W = args.steps, args.warmup
+    dw = DeviceWeights(shape, args.seed, std=0.02, gain_std=0.0)
+    eng = MegakernelEngine(shape=shape, max_seq=args.ctx + K + 8, device_weights=dw)
+    info = launcher.detect_gpu()
+    grid = eng.grid_size
+    print(f"# device {info['name']} CUs {info['cu_count']} grid {grid}", file=sys.stderr, flush=True)
+
+    first = 1
+    eng.fill_kv_synthetic(args.ctx, args.seed)
+    eng.decode_many(first, max(W, 1))  # warm-up launch
+    walls, kernels = [], []
+    for r in range(args.reps):
+        eng.fill_kv_synthetic(args.ctx, args.seed)
+        eng.lib.megakernel_sync()
+        t0 = time.perf_counter()
+        toks = eng.decode_many(first, K)
+        eng.lib.megakernel_sync()
+        walls.append(time.perf_counter() - t0)
+        kernels.append(eng.lib.megakernel_last_kernel_ms(eng._handle) / 1e3)
+        print(f"# rep {r}: wall {walls[-1] * 1e3:.2f} ms kernel {kernels[-1] * 1e3:.2f} ms "
+              f"-> {K / walls[-1]:.1f} tok/s; last tokens {toks[-4:]}", file=sys.stderr, flush=True)
+    wall = statistics.median(walls)
+    kern = statistics.median(kernels)
+    nbytes = sum(shape.token_bytes(args.ctx + i) for i in range(K))
+    achieved = nbytes / kern / 1e9
+    traffic = None
+    if os.path.exists(args.traffic_json):
+        with open(args.traffic_json) as f:
+            tj = json.load(f)
+        if tj.get("ctx") == args.ctx and tj.get("tokens") == K:
+            traffic = tj.get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(dw, shape, args.seed, args.cpu_seconds)
+    eng.close()
+    dw.free()
+
+    out = {
+        "metric": METRIC,
+        "value": round(K / wall, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"Qwen3-0.6B-shaped batch-1 greedy decode, KV prefilled to {args.ctx}, "
+                               f"{K} tokens in one resident launch (BASELINE configs[2])",
+                   "ctx": args.ctx, "tokens": K, "batch": 1, "layers": shape.n_layers,
+                   "hidden": shape.hidden, "heads": "16q/8kv x 64", "ffn": shape.ffn, "vocab": shape.vocab,
+                   "weights": "bf16 N(0,0.02) (Irwin-Hall(4) approx), unit norm gains",
+                   "accumulation": "fp32", "reps": args.reps, "grid": grid,
+                   "device": info["name"]},
+        "kernel_ms_per_step": round(kern * 1e3 / K, 5),
+        "hbm_gbps_achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

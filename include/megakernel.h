@@ -1,0 +1,148 @@
+/* megakernel.h - C ABI of megakernel.so, the MI355X (gfx950) persistent
+ * decode megakernel for a Qwen3-0.6B-shaped decoder.
+ *
+ * Drop-in boundary: the first six functions have exactly the signatures and
+ * meaning of the reference library built by `make lib`
+ * (/root/reference/src/megakernel.cu:535-624, bound through ctypes in
+ * /root/reference/host/bridge.py:39-67).  Everything after them is additive.
+ *
+ * Conventions (all functions):
+ *   - plain pointers and sizes only; no framework types cross the boundary;
+ *   - the device is the caller's current HIP device;
+ *   - functions returning int return >= 0 on success and -1 on failure, with
+ *     a message available from megakernel_last_error(); functions returning a
+ *     handle return NULL on failure (the reference never does, but its bridge
+ *     already treats NULL as failure, bridge.py:106-107);
+ *   - a handle is not reentrant: one host thread drives it at a time, as in
+ *     the reference.
+ *
+ * Flat weight format (reference host/weight_loader.py:141-192): bf16 tensors
+ * stored back to back; the offset array lists byte offsets in the order
+ *   [embedding, final_norm, then per layer: attn_norm, w_q, w_k, w_v, q_norm,
+ *    k_norm, w_o, ffn_norm, w_gate, w_up, w_down]
+ * (reference megakernel.cu:518-532, bridge.py:86-93); matrices are row-major
+ * [out, in].  The library repacks the weights into its own device layout at
+ * init, so the caller's buffer is no longer read afterwards (the reference
+ * requires it to outlive the handle; keeping it alive remains harmless).
+ */
+#ifndef MEGAKERNEL_H
+#define MEGAKERNEL_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MK_DEFAULT_VOCAB 151936
+#define MK_DEFAULT_MAX_SEQ 33024 /* >= 32768 prefill + 128 decode */
+
+#define MK_PRESET_BASELINE 0  /* hidden 1024, 16/8 heads, head_dim 64, ffn 2816 */
+#define MK_PRESET_QWEN3_06B 1 /* hidden 1024, 16/8 heads, head_dim 128, ffn 3072 */
+#define MK_PRESET_TINY 2      /* hidden 256, 4/2 heads, head_dim 64, ffn 512 */
+
+/* ---- reference entry points ------------------------------------------- */
+
+/* Replaces megakernel_init (reference src/megakernel.cu:544-585).
+ * d_weights: device pointer to the flat weight buffer; offsets: host array of
+ * num_offsets = 2 + 11 * layers byte offsets (310 for 28 layers).  Shapes are
+ * the BASELINE preset with vocab MK_DEFAULT_VOCAB and KV capacity
+ * MK_DEFAULT_MAX_SEQ.  Returns an opaque handle, or NULL on failure. */
+void* megakernel_init(void* d_weights, long long* offsets, int num_offsets);
+
+/* Replaces megakernel_decode (reference src/megakernel.cu:588-591).
+ * Consumes input_token at the current position, returns the greedy next token
+ * (argmax of fp32 logits, lowest index on ties) and advances the position by
+ * one.  Blocking.  Returns -1 on error (bad token, KV full, device fault). */
+int megakernel_decode(void* handle, int input_token);
+
+/* Replaces megakernel_reset (reference src/megakernel.cu:594-601): zeroes the
+ * KV cache and sets the position to 0. */
+void megakernel_reset(void* handle);
+
+/* Replaces megakernel_get_pos (reference src/megakernel.cu:604-607). */
+int megakernel_get_pos(void* handle);
+
+/* Replaces megakernel_free (reference src/megakernel.cu:610-617). */
+void megakernel_free(void* handle);
+
+/* Replaces megakernel_sync (reference src/megakernel.cu:620-622):
+ * device-wide synchronize. */
+void megakernel_sync(void);
+
+/* ---- additive extensions ------------------------------------------------ */
+
+/* Message of the last failure on this thread ("" if none). */
+const char* megakernel_last_error(void);
+
+/* megakernel_init with an explicit preset (MK_PRESET_*), vocabulary size
+ * (multiple of 16) and KV capacity in positions. */
+void* megakernel_init_ex(void* d_weights, const long long* offsets, int num_offsets, int preset, int vocab,
+                         int max_seq);
+
+/* Same, from a host copy of the flat weight file: the library uploads it, so
+ * a caller needs no GPU framework at all (the reference bridge uploads with
+ * torch, host/bridge.py:80-84). */
+void* megakernel_init_from_host(const void* host_weights, unsigned long long nbytes, const long long* offsets,
+                                int num_offsets, int preset, int vocab, int max_seq);
+
+/* n greedy steps in ONE resident kernel launch: step 0 consumes first_token,
+ * step i consumes the token step i-1 produced; out_tokens[i] (host, n ints)
+ * receives step i's output.  Equivalent to n calls of megakernel_decode
+ * without a host round trip per token.  Returns 0 or -1. */
+int megakernel_generate(void* handle, int first_token, int n, int* out_tokens);
+
+/* One decode step that also returns the residual stream after the embedding
+ * and after every layer (layers_out: host float[(layers + 1) * hidden]) and
+ * the fp32 logits (logits_out: host float[vocab]).  Validation only; either
+ * pointer may be NULL.  Returns the next token or -1. */
+int megakernel_debug_forward(void* handle, int token, float* layers_out, float* logits_out);
+
+/* Set the decode position without touching the cache. */
+int megakernel_set_pos(void* handle, int pos);
+
+/* Copy a host KV prefix into the cache and set the position to len.
+ * host_kv: bf16 [layers][2 (K, V)][n_kv_heads][len][head_dim], K after
+ * QK-norm + RoPE (the reference's cache layout, src/kv_cache.cuh:11-32, with
+ * len in place of MAX_SEQ_LEN). */
+int megakernel_set_kv(void* handle, const void* host_kv, int len);
+
+/* Copy positions [0, len) of the cache out in the megakernel_set_kv layout. */
+int megakernel_get_kv(void* handle, void* host_kv, int len);
+
+/* Fill positions [0, len) of the cache on the device with the synthetic
+ * N(0, std^2) stream of oracle/synth.py (kv_prefill_bits) and set the
+ * position to len. */
+int megakernel_fill_kv_synthetic(void* handle, int len, unsigned long long seed, float std);
+
+/* Device time of the last decode launch in milliseconds (HIP events). */
+float megakernel_last_kernel_ms(void* handle);
+
+/* Number of resident workgroups of the decode kernel (one per CU). */
+int megakernel_grid_size(void* handle);
+
+/* Minimum positions per attention work item (default 256). */
+int megakernel_set_attention_chunk(void* handle, int chunk_min);
+
+/* Device fill of n bf16 values: bf16(float32(S_i - 131070) * c [+ 1.0f]),
+ * S_i the Irwin-Hall(4) sum of the 16-bit fields of splitmix64(key, i). */
+int megakernel_synth_fill(void* d_dst, unsigned long long n, unsigned long long key, float c, int add_one);
+
+/* splitmix64 stream key of (seed, tensor_id); host-only arithmetic. */
+unsigned long long megakernel_synth_key(unsigned long long seed, unsigned long long tensor_id);
+
+/* The RoPE inverse-frequency table the kernel uses (host-only). Returns the
+ * number of entries (head_dim / 2) or -1. */
+int megakernel_rope_inv_freq(int preset, float* out, int n);
+
+/* Thin device-memory helpers so ctypes callers need no GPU framework.
+ * kind: 0 host->device, 1 device->host, 2 device->device. */
+void* megakernel_device_alloc(unsigned long long nbytes);
+void megakernel_device_free(void* d);
+int megakernel_memcpy(void* dst, const void* src, unsigned long long nbytes, int kind);
+
+/* CU count, wall-clock rate (kHz) and "name (gcnArch)" of the current device. */
+int megakernel_device_info(int* cus, int* wall_clock_khz, char* name, int name_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MEGAKERNEL_H */

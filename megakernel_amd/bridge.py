@@ -1,0 +1,200 @@
+"""Python bridge: ``MegakernelEngine`` over megakernel.so via ctypes.
+
+Mirrors /root/reference/host/bridge.py (same class name, constructor
+arguments and methods: reset, decode_token, generate, benchmark,
+benchmark_sweep, close) with three deliberate differences:
+
+* no torch in the product path: weights are read with numpy and uploaded by
+  the library (``megakernel_init_from_host``);
+* ``generate`` prefills the prompt once (the reference prefills it twice,
+  bridge.py:136-163) and can decode all new tokens in one resident launch;
+* throughput accounting counts KV bytes as well as weight bytes, from the
+  model shape instead of a fixed 926e6 constant (bridge.py:229).
+
+Errors raise ``MegakernelError`` with the library's message.
+"""
+from __future__ import annotations
+
+import ctypes
+import time
+
+import numpy as np
+
+from . import _lib
+from .config import BASELINE, HBM_PEAK_GBPS, ModelShape
+from .weights import load_offsets, ordered_from_dict
+
+
+class MegakernelEngine:
+    """Python wrapper around the megakernel shared library."""
+
+    def __init__(self, weights_path=None, offsets_path=None, lib_path=None, tokenizer=None,
+                 shape: ModelShape = BASELINE, max_seq: int | None = None,
+                 device_weights=None):
+        self.tokenizer = tokenizer
+        self.shape = shape
+        self.lib = _lib.load(lib_path)
+        self.max_seq = max_seq or 33024
+        if device_weights is not None:
+            self._init_from_device(device_weights)
+        else:
+            self._load_weights(weights_path, offsets_path)
+
+    # ------------------------------------------------------------ set-up
+    def _load_weights(self, weights_path, offsets_path):
+        offs = load_offsets(offsets_path)
+        order = ordered_from_dict(self.shape, offs)
+        data = np.fromfile(weights_path, dtype=np.uint8)
+        arr = (ctypes.c_longlong * len(order))(*order)
+        self._handle = self.lib.megakernel_init_from_host(
+            data.ctypes.data_as(ctypes.c_void_p), data.nbytes, arr, len(order),
+            self.shape.preset, self.shape.vocab, self.max_seq)
+        if not self._handle:
+            raise _lib.MegakernelError(f"megakernel_init failed: {_lib.last_error(self.lib)}")
+
+    def _init_from_device(self, dw):
+        arr = dw.layout.c_offsets()
+        self._handle = self.lib.megakernel_init_ex(
+            ctypes.c_void_p(dw.ptr), arr, len(arr), self.shape.preset, self.shape.vocab, self.max_seq)
+        if not self._handle:
+            raise _lib.MegakernelError(f"megakernel_init failed: {_lib.last_error(self.lib)}")
+
+    # ---------------------------------------------------- reference methods
+    def reset(self):
+        """Reset KV cache and position for a new generation."""
+        self.lib.megakernel_reset(self._handle)
+
+    def decode_token(self, token_id):
+        """Run one forward pass: input token -> next token."""
+        return _lib.check(self.lib, self.lib.megakernel_decode(self._handle, int(token_id)), "decode")
+
+    @property
+    def pos(self) -> int:
+        return self.lib.megakernel_get_pos(self._handle)
+
+    def decode_many(self, first_token: int, n: int) -> list[int]:
+        """n greedy steps in one resident launch (megakernel_generate)."""
+        out = (ctypes.c_int * n)()
+        _lib.check(self.lib, self.lib.megakernel_generate(self._handle, int(first_token), n, out), "generate")
+        return list(out)
+
+    def generate_ids(self, prompt_ids, max_tokens=100, eos_id=None, one_launch=True):
+        """Greedy continuation of token ids.  Returns (generated_ids, tok/s)."""
+        self.reset()
+        for tok in prompt_ids[:-1]:
+            self.decode_token(tok)
+        nxt = self.decode_token(prompt_ids[-1])
+        self.lib.megakernel_sync()
+        start = time.perf_counter()
+        generated = [nxt]
+        if one_launch and eos_id is None and max_tokens > 1:
+            generated += self.decode_many(nxt, max_tokens - 1)
+        else:
+            while len(generated) < max_tokens and nxt != eos_id:
+                nxt = self.decode_token(nxt)
+                generated.append(nxt)
+        self.lib.megakernel_sync()
+        elapsed = time.perf_counter() - start
+        if eos_id is not None and eos_id in generated:
+            generated = generated[:generated.index(eos_id) + 1]
+        return generated, (len(generated) - 1) / elapsed if elapsed > 0 and len(generated) > 1 else 0.0
+
+    def generate(self, prompt, max_tokens=100, print_stream=False):
+        """Generate text from a prompt (needs a tokenizer).  Returns (text, tok/s)."""
+        if self.tokenizer is None:
+            raise ValueError("generate(prompt) needs a tokenizer; use generate_ids for token ids")
+        ids = self.tokenizer.encode(prompt)
+        eos = getattr(self.tokenizer, "eos_token_id", None)
+        gen, tps = self.generate_ids(ids, max_tokens, eos_id=eos, one_launch=eos is None)
+        if print_stream:
+            print(self.tokenizer.decode(gen))
+        return self.tokenizer.decode(list(ids) + gen, skip_special_tokens=True), tps
+
+    def benchmark(self, num_tokens=50, prompt_token=1):
+        """Raw per-call decode throughput (one launch + host sync per token)."""
+        self.reset()
+        token = prompt_token
+        for _ in range(5):
+            token = self.decode_token(token)
+        self.reset()
+        self.lib.megakernel_sync()
+        token = prompt_token
+        start = time.perf_counter()
+        for _ in range(num_tokens):
+            token = self.decode_token(token)
+        self.lib.megakernel_sync()
+        return num_tokens / (time.perf_counter() - start)
+
+    def benchmark_sweep(self, positions=None, bench_tokens=20, seed=1):
+        """Throughput at several context positions (KV prefilled synthetically
+        instead of decoding pos tokens one by one).  Returns a list of dicts."""
+        positions = positions or [1, 10, 50, 100, 500, 1000, 2000]
+        results = []
+        for pos in positions:
+            self.fill_kv_synthetic(pos, seed)
+            self.decode_many(1, bench_tokens)  # warm-up at this position
+            self.fill_kv_synthetic(pos, seed)
+            ms = self.timed_generate(1, bench_tokens)
+            tps = bench_tokens / (ms / 1e3)
+            nbytes = sum(self.shape.token_bytes(pos + i) for i in range(bench_tokens))
+            gbps = nbytes / (ms / 1e3) / 1e9
+            results.append({"position": pos, "tok_per_sec": tps, "latency_us": ms * 1e3 / bench_tokens,
+                            "bw_gbps": gbps, "bw_util": gbps / HBM_PEAK_GBPS})
+        return results
+
+    # --------------------------------------------------------- extensions
+    def timed_generate(self, first_token: int, n: int) -> float:
+        """Decode n tokens in one launch; returns the kernel's device time (ms)."""
+        self.decode_many(first_token, n)
+        return float(self.lib.megakernel_last_kernel_ms(self._handle))
+
+    def fill_kv_synthetic(self, length: int, seed: int, std: float = 1.0):
+        _lib.check(self.lib, self.lib.megakernel_fill_kv_synthetic(self._handle, length, seed, std),
+                   "fill_kv_synthetic")
+
+    def set_kv(self, kv_bits: np.ndarray):
+        """kv_bits: uint16 [L][2][NKV][len][D] (bf16 bits)."""
+        kv_bits = np.ascontiguousarray(kv_bits, dtype=np.uint16)
+        _lib.check(self.lib, self.lib.megakernel_set_kv(
+            self._handle, kv_bits.ctypes.data_as(ctypes.c_void_p), kv_bits.shape[3]), "set_kv")
+
+    def get_kv(self, length: int) -> np.ndarray:
+        s = self.shape
+        out = np.empty((s.n_layers, 2, s.n_kv_heads, length, s.head_dim), dtype=np.uint16)
+        _lib.check(self.lib, self.lib.megakernel_get_kv(
+            self._handle, out.ctypes.data_as(ctypes.c_void_p), length), "get_kv")
+        return out
+
+    def set_pos(self, pos: int):
+        _lib.check(self.lib, self.lib.megakernel_set_pos(self._handle, pos), "set_pos")
+
+    def debug_forward(self, token: int):
+        """One step returning (next_token, layers[(L+1), H], logits[V])."""
+        s = self.shape
+        layers = np.empty((s.n_layers + 1, s.hidden), dtype=np.float32)
+        logits = np.empty(s.vocab, dtype=np.float32)
+        nxt = self.lib.megakernel_debug_forward(
+            self._handle, int(token), layers.ctypes.data_as(_lib.P_float),
+            logits.ctypes.data_as(_lib.P_float))
+        _lib.check(self.lib, nxt, "debug_forward")
+        return nxt, layers, logits
+
+    def set_attention_chunk(self, chunk_min: int):
+        _lib.check(self.lib, self.lib.megakernel_set_attention_chunk(self._handle, chunk_min),
+                   "set_attention_chunk")
+
+    @property
+    def grid_size(self) -> int:
+        return self.lib.megakernel_grid_size(self._handle)
+
+    def close(self):
+        """Free GPU resources."""
+        if getattr(self, "_handle", None):
+            self.lib.megakernel_free(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

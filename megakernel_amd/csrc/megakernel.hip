@@ -1,0 +1,644 @@
+// megakernel.so: host runtime and C ABI of the MI355X persistent decode
+// megakernel.  The six reference entry points keep their exact signatures and
+// meaning (/root/reference/src/megakernel.cu:535-624); everything else is an
+// additive extension declared in include/megakernel.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "mk_config.h"
+#include "mk_device.h"
+#include "mk_kernel.h"
+
+#include "../../include/megakernel.h"
+
+namespace mk {
+
+// ------------------------------------------------------------ error state
+static thread_local char g_err[512] = "";
+
+static void set_err(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+#define HIPCHK(expr, ret)                                                                  \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess) {                                                                \
+      ::mk::set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+      return ret;                                                                          \
+    }                                                                                      \
+  } while (0)
+
+// --------------------------------------------------------- device helpers
+// Repack a row-major bf16 matrix W[R][K] into the tile stream.  Destination
+// 16-row block of source block rb is rb * blk_stride + blk_off (in blocks of
+// K/32 tiles), so gate/up can be interleaved.  One thread per 16-byte unit.
+__global__ void repack_kernel(const u32x4* __restrict__ src, int R, int K, u32x4* __restrict__ dst,
+                              int blk_stride, int blk_off) {
+  const int KT = K / 32;
+  const long long units = (long long)R * K / 8;
+  for (long long u = (long long)blockIdx.x * blockDim.x + threadIdx.x; u < units;
+       u += (long long)gridDim.x * blockDim.x) {
+    const int lane = (int)(u % 64);
+    const long long tile = u / 64;
+    const int kt = (int)(tile % KT);
+    const long long rb = tile / KT;
+    const long long row = rb * 16 + (lane & 15);
+    const long long chunk = (long long)kt * 4 + (lane >> 4);
+    dst[((rb * blk_stride + blk_off) * KT + kt) * 64 + lane] = src[row * (K / 8) + chunk];
+  }
+}
+
+__global__ void synth_fill_kernel(uint16_t* __restrict__ dst, unsigned long long n, unsigned long long key,
+                                  float c, int add_one) {
+  for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (unsigned long long)gridDim.x * blockDim.x)
+    dst[i] = synth_bf16(key, i, c, add_one);
+}
+
+// Synthetic KV prefill straight into the cache layout [L][2][NKV][S][D] for
+// positions [0, len).  Stream id KV_ID_BASE + 2*layer + kv; element index
+// (t * NKV + g) * D + d (matches oracle/synth.py:kv_prefill_bits).
+__global__ void synth_kv_kernel(uint16_t* __restrict__ kv, int L, int NKV, int S, int D, int len,
+                                unsigned long long seed, float c) {
+  const unsigned long long per = (unsigned long long)len * NKV * D;
+  const unsigned long long total = per * 2ull * L;
+  for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (unsigned long long)gridDim.x * blockDim.x) {
+    const unsigned long long plane = i / per;  // layer*2 + kv
+    const unsigned long long e = i % per;      // (t*NKV + g)*D + d
+    const int d = (int)(e % D);
+    const int g = (int)((e / D) % NKV);
+    const long long t = (long long)(e / ((unsigned long long)D * NKV));
+    const unsigned long long key = sm_h(seed, 0x40000000ull + plane);
+    kv[((plane * NKV + g) * (unsigned long long)S + t) * D + d] = synth_bf16(key, e, c, 0);
+  }
+}
+
+// -------------------------------------------------------------- the handle
+struct ShapeInfo {
+  int H, NQ, NKV, D, F, QD, KVD, QKV, GQA;
+  long long u_layer, off_qkv, off_o, off_gu, off_down;
+  int norm_stride, norm_attn, norm_q, norm_k, norm_ffn;
+};
+
+template <class S>
+static ShapeInfo shape_info() {
+  return ShapeInfo{S::H, S::NQ, S::NKV, S::D, S::F, S::QD, S::KVD, S::QKV, S::GQA,
+                   S::U_LAYER, S::OFF_QKV, S::OFF_O, S::OFF_GU, S::OFF_DOWN,
+                   S::NORM_STRIDE, S::NORM_ATTN, S::NORM_Q, S::NORM_K, S::NORM_FFN};
+}
+
+struct Handle {
+  int device = 0, preset = 0, G = 0;
+  ShapeInfo sh{};
+  int L = 0, V = 0, S = 0;
+  int max_launch_tokens = 0;
+  int nsplit_max = 1, chunk_min = 256;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  float last_ms = 0.f;
+  unsigned long long timeout_ticks = 0;
+  // device memory (owned)
+  u32x4* layers = nullptr;
+  uint16_t* norms = nullptr;
+  uint16_t* final_norm = nullptr;
+  u32x4* lmhead = nullptr;
+  uint16_t* kv = nullptr;
+  float *x = nullptr, *qkv = nullptr, *part = nullptr, *act = nullptr;
+  unsigned long long* amax = nullptr;
+  int* out_tokens = nullptr;
+  unsigned* sync = nullptr;
+  int* err = nullptr;
+  float* inv_freq = nullptr;
+  float* dbg_layers = nullptr;
+  float* dbg_logits = nullptr;
+  void* owned_flat = nullptr;
+  unsigned sync_base = 0;
+  int pos = 0;
+  long long kv_bytes = 0;
+  hipError_t (*launch)(Handle*, const Params&) = nullptr;
+};
+
+template <class S>
+static hipError_t launch_decode(Handle* h, const Params& p) {
+  hipLaunchKernelGGL(decode_kernel<S>, dim3(h->G), dim3(NT), 0, h->stream, p);
+  return hipGetLastError();
+}
+
+template <class S>
+static int occupancy_ok(int* nblk) {
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(nblk, decode_kernel<S>, NT, 0) == hipSuccess;
+}
+
+static void free_all(Handle* h) {
+  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part, h->act,
+                  h->amax, h->out_tokens, h->sync, h->err, h->inv_freq, h->dbg_layers, h->dbg_logits,
+                  h->owned_flat};
+  for (void* q : ptrs)
+    if (q) (void)hipFree(q);
+  if (h->ev0) (void)hipEventDestroy(h->ev0);
+  if (h->ev1) (void)hipEventDestroy(h->ev1);
+  if (h->stream) (void)hipStreamDestroy(h->stream);
+}
+
+static int repack(Handle* h, const char* base, long long off, int R, int K, u32x4* dst, int stride,
+                  int blk_off) {
+  if (off < 0 || (off & 15)) {
+    set_err("weight offset %lld is negative or not 16-byte aligned", off);
+    return -1;
+  }
+  const long long units = (long long)R * K / 8;
+  const int threads = 256;
+  const int blocks = (int)((units + threads - 1) / threads < 65536 ? (units + threads - 1) / threads : 65536);
+  hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, h->stream,
+                     reinterpret_cast<const u32x4*>(base + off), R, K, dst, stride, blk_off);
+  HIPCHK(hipGetLastError(), -1);
+  return 0;
+}
+
+static int init_device_state(Handle* h, const char* base, const long long* off, int n_off) {
+  const ShapeInfo& s = h->sh;
+  if (n_off < 13 || (n_off - 2) % 11 != 0) {
+    set_err("num_offsets=%d is not 2 + 11*layers", n_off);
+    return -1;
+  }
+  h->L = (n_off - 2) / 11;
+  if (h->V <= 0 || h->V % 16) {
+    set_err("vocab %d must be a positive multiple of 16", h->V);
+    return -1;
+  }
+  HIPCHK(hipGetDevice(&h->device), -1);
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, h->device), -1);
+  h->G = prop.multiProcessorCount;
+  int wall_khz = 0;
+  HIPCHK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, h->device), -1);
+  h->timeout_ticks = (unsigned long long)(wall_khz > 0 ? wall_khz : 100000) * 10000ull;  // 10 s
+  h->nsplit_max = h->G / s.NKV > 0 ? h->G / s.NKV : 1;
+  if ((long long)h->nsplit_max * CHUNK_MAX < h->S) {
+    set_err("max_seq %d exceeds %d splits x %d positions", h->S, h->nsplit_max, CHUNK_MAX);
+    return -1;
+  }
+  HIPCHK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), -1);
+  HIPCHK(hipEventCreate(&h->ev0), -1);
+  HIPCHK(hipEventCreate(&h->ev1), -1);
+
+  const long long layer_bytes = s.u_layer * 16;
+  HIPCHK(hipMalloc(&h->layers, layer_bytes * h->L), -1);
+  HIPCHK(hipMalloc(&h->norms, (size_t)s.norm_stride * 2 * h->L), -1);
+  HIPCHK(hipMalloc(&h->final_norm, (size_t)s.H * 2), -1);
+  HIPCHK(hipMalloc(&h->lmhead, (size_t)h->V * s.H * 2), -1);
+  h->kv_bytes = 2LL * h->L * s.NKV * (long long)h->S * s.D * 2;
+  HIPCHK(hipMalloc(&h->kv, h->kv_bytes), -1);
+  HIPCHK(hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream), -1);
+  HIPCHK(hipMalloc(&h->x, (size_t)s.H * 4), -1);
+  HIPCHK(hipMalloc(&h->qkv, (size_t)s.QKV * 4), -1);
+  HIPCHK(hipMalloc(&h->part, (size_t)s.NKV * h->nsplit_max * s.GQA * (s.D + PART_STRIDE_PAD) * 4), -1);
+  HIPCHK(hipMalloc(&h->act, (size_t)s.F * 4), -1);
+  h->max_launch_tokens = 1 << 16;
+  HIPCHK(hipMalloc(&h->amax, (size_t)h->max_launch_tokens * 8), -1);
+  HIPCHK(hipMalloc(&h->out_tokens, (size_t)h->max_launch_tokens * 4), -1);
+  HIPCHK(hipMalloc(&h->sync, 256), -1);
+  HIPCHK(hipMemsetAsync(h->sync, 0, 256, h->stream), -1);
+  HIPCHK(hipMalloc(&h->err, 256), -1);
+  HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
+  HIPCHK(hipMalloc(&h->dbg_layers, (size_t)(h->L + 1) * s.H * 4), -1);
+  HIPCHK(hipMalloc(&h->dbg_logits, (size_t)h->V * 4), -1);
+
+  // RoPE inverse frequencies, computed as HF does in fp32:
+  // 1 / theta ** (float(2i) / D)  (transformers Qwen3RotaryEmbedding).
+  std::vector<float> invf(s.D / 2);
+  for (int i = 0; i < s.D / 2; ++i) invf[i] = 1.0f / powf((float)kRopeTheta, (float)(2 * i) / (float)s.D);
+  HIPCHK(hipMalloc(&h->inv_freq, invf.size() * 4), -1);
+  HIPCHK(hipMemcpyAsync(h->inv_freq, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, h->stream), -1);
+
+  // Repack matrices (offset order: reference megakernel.cu:518-532).
+  const int KTH = s.H / 32;
+  if (repack(h, base, off[0], h->V, s.H, h->lmhead, 1, 0)) return -1;
+  HIPCHK(hipMemcpyAsync(h->final_norm, base + off[1], (size_t)s.H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+  for (int i = 0; i < h->L; ++i) {
+    const long long* o = off + 2 + 11 * i;
+    u32x4* wl = h->layers + (long long)i * s.u_layer;
+    uint16_t* nl = h->norms + (long long)i * s.norm_stride;
+    HIPCHK(hipMemcpyAsync(nl + s.norm_attn, base + o[0], (size_t)s.H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    HIPCHK(hipMemcpyAsync(nl + s.norm_q, base + o[4], (size_t)s.D * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    HIPCHK(hipMemcpyAsync(nl + s.norm_k, base + o[5], (size_t)s.D * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    HIPCHK(hipMemcpyAsync(nl + s.norm_ffn, base + o[7], (size_t)s.H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    u32x4* qkv = wl + s.off_qkv;
+    if (repack(h, base, o[1], s.QD, s.H, qkv, 1, 0)) return -1;
+    if (repack(h, base, o[2], s.KVD, s.H, qkv, 1, s.QD / 16)) return -1;
+    if (repack(h, base, o[3], s.KVD, s.H, qkv, 1, (s.QD + s.KVD) / 16)) return -1;
+    if (repack(h, base, o[6], s.H, s.QD, wl + s.off_o, 1, 0)) return -1;
+    if (repack(h, base, o[8], s.F, s.H, wl + s.off_gu, 2, 0)) return -1;
+    if (repack(h, base, o[9], s.F, s.H, wl + s.off_gu, 2, 1)) return -1;
+    if (repack(h, base, o[10], s.H, s.F, wl + s.off_down, 1, 0)) return -1;
+  }
+  (void)KTH;
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  return 0;
+}
+
+static Handle* create(int preset, int vocab, int max_seq) {
+  Handle* h = new (std::nothrow) Handle();
+  if (!h) {
+    set_err("out of host memory");
+    return nullptr;
+  }
+  h->preset = preset;
+  h->V = vocab;
+  h->S = max_seq;
+  switch (preset) {
+    case PRESET_BASELINE:
+      h->sh = shape_info<ShapeBaseline>();
+      h->launch = launch_decode<ShapeBaseline>;
+      break;
+    case PRESET_QWEN3_06B:
+      h->sh = shape_info<ShapeQwen3>();
+      h->launch = launch_decode<ShapeQwen3>;
+      break;
+    case PRESET_TINY:
+      h->sh = shape_info<ShapeTiny>();
+      h->launch = launch_decode<ShapeTiny>;
+      break;
+    default:
+      set_err("unknown preset %d", preset);
+      delete h;
+      return nullptr;
+  }
+  if (max_seq <= 0) {
+    set_err("max_seq must be positive");
+    delete h;
+    return nullptr;
+  }
+  return h;
+}
+
+static int check_occupancy(Handle* h) {
+  int nblk = 0, ok = 0;
+  switch (h->preset) {
+    case PRESET_BASELINE: ok = occupancy_ok<ShapeBaseline>(&nblk); break;
+    case PRESET_QWEN3_06B: ok = occupancy_ok<ShapeQwen3>(&nblk); break;
+    default: ok = occupancy_ok<ShapeTiny>(&nblk); break;
+  }
+  if (!ok || nblk < 1) {
+    set_err("persistent kernel cannot keep one workgroup resident per CU (occupancy %d)", nblk);
+    return -1;
+  }
+  return 0;
+}
+
+static int reset_sync_state(Handle* h) {
+  HIPCHK(hipMemsetAsync(h->sync, 0, 256, h->stream), -1);
+  HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  h->sync_base = 0;
+  return 0;
+}
+
+// One resident launch decoding n tokens starting at h->pos.
+static int run(Handle* h, int first_token, int n, int* out_host, bool debug) {
+  if (n <= 0 || n > h->max_launch_tokens) {
+    set_err("token count %d outside [1, %d]", n, h->max_launch_tokens);
+    return -1;
+  }
+  if (first_token < 0 || first_token >= h->V) {
+    set_err("token id %d outside [0, %d)", first_token, h->V);
+    return -1;
+  }
+  if (h->pos + n > h->S) {
+    set_err("position %d + %d tokens exceeds KV capacity %d", h->pos, n, h->S);
+    return -1;
+  }
+  Params p{};
+  p.layers = h->layers;
+  p.norms = h->norms;
+  p.final_norm = h->final_norm;
+  p.lmhead = h->lmhead;
+  p.kv = h->kv;
+  p.x = h->x;
+  p.qkv = h->qkv;
+  p.part = h->part;
+  p.act = h->act;
+  p.amax = h->amax;
+  p.out_tokens = h->out_tokens;
+  p.sync = h->sync;
+  p.err = h->err;
+  p.dbg_layers = debug ? h->dbg_layers : nullptr;
+  p.dbg_logits = debug ? h->dbg_logits : nullptr;
+  p.inv_freq = h->inv_freq;
+  p.timeout_ticks = h->timeout_ticks;
+  p.sync_base = h->sync_base;
+  p.n_layers = h->L;
+  p.vocab = h->V;
+  p.max_seq = h->S;
+  p.pos0 = h->pos;
+  p.n_tokens = n;
+  p.first_token = first_token;
+  p.nsplit_max = h->nsplit_max;
+  p.chunk_min = h->chunk_min;
+  HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
+  HIPCHK(h->launch(h, p), -1);
+  HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  HIPCHK(hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1), -1);
+  int err = 0;
+  HIPCHK(hipMemcpy(&err, h->err, 4, hipMemcpyDeviceToHost), -1);
+  if (err != MK_OK) {
+    reset_sync_state(h);
+    set_err("decode kernel aborted: %s", err == MK_ERR_TIMEOUT ? "grid sync timed out" : "device error");
+    return -1;
+  }
+  h->sync_base += (unsigned)n * (unsigned)(5 * h->L + 1) * (unsigned)h->G;
+  if (out_host) HIPCHK(hipMemcpy(out_host, h->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost), -1);
+  h->pos += n;
+  return 0;
+}
+
+static Handle* init_common(const void* d_weights, const long long* offsets, int n_off, int preset, int vocab,
+                           int max_seq, void* owned) {
+  if (!d_weights || !offsets) {
+    set_err("null weights or offsets");
+    return nullptr;
+  }
+  Handle* h = create(preset, vocab, max_seq);
+  if (!h) return nullptr;
+  h->owned_flat = owned;
+  if (check_occupancy(h) || init_device_state(h, static_cast<const char*>(d_weights), offsets, n_off)) {
+    free_all(h);
+    delete h;
+    return nullptr;
+  }
+  return h;
+}
+
+}  // namespace mk
+
+using mk::Handle;
+
+// =========================================================================
+// C ABI
+// =========================================================================
+extern "C" {
+
+void* megakernel_init(void* d_weights, long long* offsets, int num_offsets) {
+  return mk::init_common(d_weights, offsets, num_offsets, mk::PRESET_BASELINE, MK_DEFAULT_VOCAB,
+                         MK_DEFAULT_MAX_SEQ, nullptr);
+}
+
+int megakernel_decode(void* handle, int input_token) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  int out = -1;
+  if (mk::run(h, input_token, 1, &out, false)) return -1;
+  return out;
+}
+
+void megakernel_reset(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return;
+  (void)hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream);
+  (void)hipStreamSynchronize(h->stream);
+  h->pos = 0;
+}
+
+int megakernel_get_pos(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  return h ? h->pos : -1;
+}
+
+void megakernel_free(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return;
+  (void)hipStreamSynchronize(h->stream);
+  mk::free_all(h);
+  delete h;
+}
+
+void megakernel_sync(void) { (void)hipDeviceSynchronize(); }
+
+// ------------------------------------------------------------- extensions
+const char* megakernel_last_error(void) { return mk::g_err; }
+
+void* megakernel_init_ex(void* d_weights, const long long* offsets, int num_offsets, int preset, int vocab,
+                         int max_seq) {
+  return mk::init_common(d_weights, offsets, num_offsets, preset, vocab, max_seq, nullptr);
+}
+
+void* megakernel_init_from_host(const void* host_weights, unsigned long long nbytes, const long long* offsets,
+                                int num_offsets, int preset, int vocab, int max_seq) {
+  if (!host_weights || nbytes == 0) {
+    mk::set_err("null or empty host weight buffer");
+    return nullptr;
+  }
+  void* d = nullptr;
+  hipError_t e = hipMalloc(&d, nbytes);
+  if (e != hipSuccess) {
+    mk::set_err("hipMalloc(%llu) failed: %s", nbytes, hipGetErrorString(e));
+    return nullptr;
+  }
+  e = hipMemcpy(d, host_weights, nbytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    mk::set_err("weight upload failed: %s", hipGetErrorString(e));
+    (void)hipFree(d);
+    return nullptr;
+  }
+  void* h = mk::init_common(d, offsets, num_offsets, preset, vocab, max_seq, d);
+  if (!h) (void)hipFree(d);
+  return h;
+}
+
+int megakernel_generate(void* handle, int first_token, int n, int* out_tokens) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  return mk::run(h, first_token, n, out_tokens, false);
+}
+
+int megakernel_debug_forward(void* handle, int token, float* layers_out, float* logits_out) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  int out = -1;
+  if (mk::run(h, token, 1, &out, true)) return -1;
+  if (layers_out &&
+      hipMemcpy(layers_out, h->dbg_layers, (size_t)(h->L + 1) * h->sh.H * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+    mk::set_err("debug copy failed");
+    return -1;
+  }
+  if (logits_out && hipMemcpy(logits_out, h->dbg_logits, (size_t)h->V * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+    mk::set_err("debug copy failed");
+    return -1;
+  }
+  return out;
+}
+
+int megakernel_set_pos(void* handle, int pos) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || pos < 0 || pos > h->S) {
+    mk::set_err("invalid handle or position %d", pos);
+    return -1;
+  }
+  h->pos = pos;
+  return 0;
+}
+
+int megakernel_set_kv(void* handle, const void* host_kv, int len) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !host_kv || len < 0 || len > h->S) {
+    mk::set_err("invalid set_kv arguments (len %d)", len);
+    return -1;
+  }
+  const size_t row = (size_t)len * h->sh.D * 2;
+  if (len > 0) {
+    hipError_t e = hipMemcpy2D(h->kv, (size_t)h->S * h->sh.D * 2, host_kv, row, row,
+                               (size_t)h->L * 2 * h->sh.NKV, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      mk::set_err("set_kv copy failed: %s", hipGetErrorString(e));
+      return -1;
+    }
+  }
+  h->pos = len;
+  return 0;
+}
+
+int megakernel_get_kv(void* handle, void* host_kv, int len) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !host_kv || len < 0 || len > h->S) {
+    mk::set_err("invalid get_kv arguments (len %d)", len);
+    return -1;
+  }
+  const size_t row = (size_t)len * h->sh.D * 2;
+  if (len > 0) {
+    hipError_t e = hipMemcpy2D(host_kv, row, h->kv, (size_t)h->S * h->sh.D * 2, row,
+                               (size_t)h->L * 2 * h->sh.NKV, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+      mk::set_err("get_kv copy failed: %s", hipGetErrorString(e));
+      return -1;
+    }
+  }
+  return 0;
+}
+
+int megakernel_fill_kv_synthetic(void* handle, int len, unsigned long long seed, float std) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || len < 0 || len > h->S) {
+    mk::set_err("invalid fill_kv arguments (len %d)", len);
+    return -1;
+  }
+  if (len > 0) {
+    const float c = (float)(std * sqrt(3.0) / 65536.0);
+    hipLaunchKernelGGL(mk::synth_kv_kernel, dim3(4096), dim3(256), 0, h->stream, h->kv, h->L, h->sh.NKV, h->S,
+                       h->sh.D, len, seed, c);
+    HIPCHK(hipGetLastError(), -1);
+    HIPCHK(hipStreamSynchronize(h->stream), -1);
+  }
+  h->pos = len;
+  return 0;
+}
+
+float megakernel_last_kernel_ms(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  return h ? h->last_ms : -1.f;
+}
+
+int megakernel_grid_size(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  return h ? h->G : -1;
+}
+
+int megakernel_set_attention_chunk(void* handle, int chunk_min) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || chunk_min < 1 || (long long)chunk_min > mk::CHUNK_MAX) {
+    mk::set_err("attention chunk %d outside [1, %d]", chunk_min, mk::CHUNK_MAX);
+    return -1;
+  }
+  h->chunk_min = chunk_min;
+  return 0;
+}
+
+int megakernel_synth_fill(void* d_dst, unsigned long long n, unsigned long long key, float c, int add_one) {
+  if (!d_dst) {
+    mk::set_err("null destination");
+    return -1;
+  }
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(mk::synth_fill_kernel, dim3(4096), dim3(256), 0, 0, static_cast<uint16_t*>(d_dst), n, key, c,
+                     add_one);
+  HIPCHK(hipGetLastError(), -1);
+  HIPCHK(hipDeviceSynchronize(), -1);
+  return 0;
+}
+
+unsigned long long megakernel_synth_key(unsigned long long seed, unsigned long long tensor_id) {
+  return mk::sm_h(seed, tensor_id);
+}
+
+int megakernel_rope_inv_freq(int preset, float* out, int n) {
+  int D = preset == mk::PRESET_QWEN3_06B ? 128 : 64;
+  if (!out || n < D / 2) {
+    mk::set_err("output buffer too small");
+    return -1;
+  }
+  for (int i = 0; i < D / 2; ++i) out[i] = 1.0f / powf((float)mk::kRopeTheta, (float)(2 * i) / (float)D);
+  return D / 2;
+}
+
+void* megakernel_device_alloc(unsigned long long nbytes) {
+  void* d = nullptr;
+  hipError_t e = hipMalloc(&d, nbytes);
+  if (e != hipSuccess) {
+    mk::set_err("hipMalloc(%llu) failed: %s", nbytes, hipGetErrorString(e));
+    return nullptr;
+  }
+  return d;
+}
+
+void megakernel_device_free(void* d) {
+  if (d) (void)hipFree(d);
+}
+
+int megakernel_memcpy(void* dst, const void* src, unsigned long long nbytes, int kind) {
+  hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+  hipError_t e = hipMemcpy(dst, src, nbytes, k);
+  if (e != hipSuccess) {
+    mk::set_err("hipMemcpy failed: %s", hipGetErrorString(e));
+    return -1;
+  }
+  return 0;
+}
+
+int megakernel_device_info(int* cus, int* wall_clock_khz, char* name, int name_len) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    mk::set_err("no HIP device");
+    return -1;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+    mk::set_err("hipGetDeviceProperties failed");
+    return -1;
+  }
+  if (cus) *cus = prop.multiProcessorCount;
+  if (wall_clock_khz) (void)hipDeviceGetAttribute(wall_clock_khz, hipDeviceAttributeWallClockRate, dev);
+  if (name && name_len > 0) snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  return 0;
+}
+
+}  // extern "C"

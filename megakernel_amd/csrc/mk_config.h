@@ -1,0 +1,70 @@
+// Model shape presets and the on-device packed weight layout.
+//
+// Shapes: the BASELINE preset is the one BASELINE.json quotes (head_dim 64,
+// SwiGLU 2816); QWEN3_06B is the reference's src/config.cuh:13-22 (head_dim
+// 128, 3072); TINY is a small shape used by fast parity tests.  Layer count,
+// vocabulary and KV capacity are runtime values.
+#pragma once
+#include <stdint.h>
+
+namespace mk {
+
+enum Preset : int { PRESET_BASELINE = 0, PRESET_QWEN3_06B = 1, PRESET_TINY = 2 };
+
+constexpr float kRmsEps = 1e-6f;     // reference src/config.cuh:22
+constexpr double kRopeTheta = 1e6;   // reference src/config.cuh:21
+
+template <int H_, int NQ_, int NKV_, int D_, int F_>
+struct Shape {
+  static constexpr int H = H_, NQ = NQ_, NKV = NKV_, D = D_, F = F_;
+  static constexpr int QD = NQ * D;          // q rows / O-proj input width
+  static constexpr int KVD = NKV * D;
+  static constexpr int QKV = QD + 2 * KVD;   // fused q|k|v rows
+  static constexpr int GQA = NQ / NKV;       // q heads per kv head
+  // Packed weights are stored as 16-row x 32-column tiles (see below).
+  static constexpr int KT_H = H / 32;        // k-tiles of a K = H row
+  static constexpr int KT_Q = QD / 32;       // k-tiles of an O-proj row
+  static constexpr int KT_F = F / 32;        // k-tiles of a down-proj row
+  static constexpr int RB_QKV = QKV / 16;    // 16-row blocks of the fused QKV
+  static constexpr int RB_H = H / 16;        // 16-row blocks of O / down outputs
+  static constexpr int RB_F = F / 16;        // 16-row blocks of gate (and of up)
+  // Packed per-layer sizes in 16-byte units (one tile = 64 units = 1 KiB).
+  static constexpr long long U_QKV = (long long)RB_QKV * KT_H * 64;
+  static constexpr long long U_O = (long long)RB_H * KT_Q * 64;
+  static constexpr long long U_GU = (long long)RB_F * 2 * KT_H * 64;
+  static constexpr long long U_DOWN = (long long)RB_H * KT_F * 64;
+  static constexpr long long OFF_QKV = 0;
+  static constexpr long long OFF_O = U_QKV;
+  static constexpr long long OFF_GU = U_QKV + U_O;
+  static constexpr long long OFF_DOWN = U_QKV + U_O + U_GU;
+  static constexpr long long U_LAYER = U_QKV + U_O + U_GU + U_DOWN;
+  // Per-layer norm gains, bf16: attn_norm[H] | q_norm[D] | k_norm[D] | ffn_norm[H]
+  static constexpr int NORM_ATTN = 0, NORM_Q = H, NORM_K = H + D, NORM_FFN = H + 2 * D;
+  static constexpr int NORM_STRIDE = 2 * H + 2 * D;
+
+  static_assert(H % 32 == 0 && QD % 32 == 0 && F % 32 == 0, "K dims must be multiples of 32");
+  static_assert(QKV % 16 == 0 && F % 16 == 0 && H % 16 == 0, "row dims must be multiples of 16");
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static_assert(NQ % NKV == 0, "GQA");
+};
+
+using ShapeBaseline = Shape<1024, 16, 8, 64, 2816>;
+using ShapeQwen3 = Shape<1024, 16, 8, 128, 3072>;
+using ShapeTiny = Shape<256, 4, 2, 64, 512>;
+
+// ---------------------------------------------------------------------------
+// Packed weight layout ("tile stream").
+//
+// A row-major bf16 matrix W[R][K] (R % 16 == 0, K % 32 == 0) is stored as
+// tiles of 16 rows x 32 columns, tile (rb, kt) at index rb * (K/32) + kt, so one
+// 16-row block's whole K extent is contiguous.  Inside a tile, 16-byte unit
+// `lane` (0..63) holds the 8 bf16 W[rb*16 + (lane & 15)][kt*32 + (lane >> 4)*8 + e],
+// e = 0..7.  This is exactly the A-operand register layout of
+// v_mfma_f32_16x16x32_bf16, and it makes every wave-wide 16-byte load one
+// contiguous, fully coalesced 1 KiB request.
+//
+// Per layer: fused QKV (q rows, then k rows, then v rows) | O | gate/up with
+// blocks interleaved (gate block p at 2p, up block p at 2p+1) | down.
+// ---------------------------------------------------------------------------
+
+}  // namespace mk
