@@ -41,6 +41,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--trace", action="store_true", help="print a per-phase critical-path summary")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                     help="measured HBM bytes per launch (rocprofv3 --pmc), if present")
     return ap.parse_args()
@@ -73,6 +74,51 @@ def cpu_baseline(dw, shape, seed: int, budget_s: float) -> dict:
             "sample": f"BASELINE configs[0] (full 28-layer model, 16-token prompt), {n} greedy decode "
                       f"tokens at positions 18..{17 + n} timed after 2 warm-up tokens; "
                       "PyTorch CPU oracle, bf16 weights upcast to fp32"}
+
+
+def trace_summary(eng, shape, args, info):
+    """Device timestamps of one decode step: per phase type, the mean over
+    layers of (a) the gap from the previous phase's last finish to this phase's
+    last 'inputs ready' and (b) from there to this phase's last finish."""
+    import ctypes
+
+    import numpy as np
+    L, G = shape.n_layers, eng.grid_size
+    n = 5 * L + 1
+    buf = (ctypes.c_ulonglong * (n * 2 * G))()
+    eng.fill_kv_synthetic(args.ctx, args.seed)
+    r = eng.lib.megakernel_trace_generate(eng._handle, 1, 8, 4, buf)
+    if r < 0:
+        print("# trace failed", file=sys.stderr)
+        return
+    tr = np.frombuffer(buf, dtype=np.uint64).reshape(n, 2, G).astype(np.float64)
+    khz = info["wall_clock_khz"] or 100000
+    us = 1e3 / khz  # microseconds per tick
+    names = ["qkv", "attn", "o", "gate_up", "down"]
+    prev_done = None
+    wait = {k: [] for k in names + ["lm_head"]}
+    work = {k: [] for k in names + ["lm_head"]}
+    t_first = None
+    for slot in range(n):
+        rd, dn = tr[slot, 0], tr[slot, 1]
+        act = dn > 0
+        if not act.any():
+            continue
+        last_ready, last_done = rd[act].max(), dn[act].max()
+        if t_first is None:
+            t_first = rd[act].min()
+        name = "lm_head" if slot == n - 1 else names[slot % 5]
+        if prev_done is not None:
+            wait[name].append((last_ready - prev_done) * us)
+        work[name].append((last_done - last_ready) * us)
+        prev_done = last_done
+    total = (prev_done - t_first) * us
+    print(f"# trace of one token at ctx {args.ctx + 4}: {total:.1f} us from first ready to last done", file=sys.stderr)
+    for k in names + ["lm_head"]:
+        w = np.mean(wait[k]) if wait[k] else 0.0
+        d = np.mean(work[k]) if work[k] else 0.0
+        print(f"#   {k:8s} handoff {w:7.2f} us   last-ready->last-done {d:7.2f} us   (x{len(work[k])})",
+              file=sys.stderr)
 
 
 def main():
@@ -119,6 +165,8 @@ def main():
         if tj.get("ctx") == args.ctx and tj.get("tokens") == K:
             traffic = tj.get("hbm_bytes_per_launch")
 
+    if args.trace:
+        trace_summary(eng, shape, args, info)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(dw, shape, args.seed, args.cpu_seconds)

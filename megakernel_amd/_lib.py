@@ -38,6 +38,7 @@ SIGNATURES = {
     "megakernel_set_kv": (c_int, [c_void_p, c_void_p, c_int]),
     "megakernel_get_kv": (c_int, [c_void_p, c_void_p, c_int]),
     "megakernel_fill_kv_synthetic": (c_int, [c_void_p, c_int, c_ull, c_float]),
+    "megakernel_trace_generate": (c_int, [c_void_p, c_int, c_int, c_int, ctypes.POINTER(ctypes.c_ulonglong)]),
     "megakernel_last_kernel_ms": (c_float, [c_void_p]),
     "megakernel_grid_size": (c_int, [c_void_p]),
     "megakernel_set_attention_chunk": (c_int, [c_void_p, c_int]),

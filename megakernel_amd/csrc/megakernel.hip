@@ -114,16 +114,17 @@ struct Handle {
   uint16_t* final_norm = nullptr;
   u32x4* lmhead = nullptr;
   uint16_t* kv = nullptr;
-  float *x = nullptr, *qkv = nullptr, *part = nullptr, *act = nullptr;
-  unsigned long long* amax = nullptr;
+  u64 *x = nullptr, *qkv = nullptr, *part_ml = nullptr, *part_acc = nullptr, *act = nullptr;
+  u64* amax = nullptr;
+  size_t tagged_bytes[6] = {0, 0, 0, 0, 0, 0};
   int* out_tokens = nullptr;
-  unsigned* sync = nullptr;
   int* err = nullptr;
+  u64* trace = nullptr;
   float* inv_freq = nullptr;
   float* dbg_layers = nullptr;
   float* dbg_logits = nullptr;
   void* owned_flat = nullptr;
-  unsigned sync_base = 0;
+  unsigned tag_base = 1;  // tag of the next launch's first phase (0 never valid)
   int pos = 0;
   long long kv_bytes = 0;
   hipError_t (*launch)(Handle*, const Params&) = nullptr;
@@ -141,9 +142,9 @@ static int occupancy_ok(int* nblk) {
 }
 
 static void free_all(Handle* h) {
-  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part, h->act,
-                  h->amax, h->out_tokens, h->sync, h->err, h->inv_freq, h->dbg_layers, h->dbg_logits,
-                  h->owned_flat};
+  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part_ml,
+                  h->part_acc, h->act, h->amax, h->out_tokens, h->err, h->inv_freq, h->dbg_layers,
+                  h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
   if (h->ev0) (void)hipEventDestroy(h->ev0);
@@ -173,8 +174,8 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
     return -1;
   }
   h->L = (n_off - 2) / 11;
-  if (h->V <= 0 || h->V % 16) {
-    set_err("vocab %d must be a positive multiple of 16", h->V);
+  if (h->V <= 0 || h->V % 16 || h->V > (int)IDX_MAX + 1) {
+    set_err("vocab %d must be a positive multiple of 16 and at most %u", h->V, IDX_MAX + 1);
     return -1;
   }
   HIPCHK(hipGetDevice(&h->device), -1);
@@ -185,6 +186,7 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   HIPCHK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, h->device), -1);
   h->timeout_ticks = (unsigned long long)(wall_khz > 0 ? wall_khz : 100000) * 10000ull;  // 10 s
   h->nsplit_max = h->G / s.NKV > 0 ? h->G / s.NKV : 1;
+  if (h->nsplit_max * s.NQ * 2 > ML_CAP) h->nsplit_max = ML_CAP / (s.NQ * 2);
   if ((long long)h->nsplit_max * CHUNK_MAX < h->S) {
     set_err("max_seq %d exceeds %d splits x %d positions", h->S, h->nsplit_max, CHUNK_MAX);
     return -1;
@@ -201,15 +203,18 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   h->kv_bytes = 2LL * h->L * s.NKV * (long long)h->S * s.D * 2;
   HIPCHK(hipMalloc(&h->kv, h->kv_bytes), -1);
   HIPCHK(hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream), -1);
-  HIPCHK(hipMalloc(&h->x, (size_t)s.H * 4), -1);
-  HIPCHK(hipMalloc(&h->qkv, (size_t)s.QKV * 4), -1);
-  HIPCHK(hipMalloc(&h->part, (size_t)s.NKV * h->nsplit_max * s.GQA * (s.D + PART_STRIDE_PAD) * 4), -1);
-  HIPCHK(hipMalloc(&h->act, (size_t)s.F * 4), -1);
-  h->max_launch_tokens = 1 << 16;
-  HIPCHK(hipMalloc(&h->amax, (size_t)h->max_launch_tokens * 8), -1);
+  // tagged activation words (zero = tag 0, never a valid tag)
+  u64** tagged[6] = {&h->x, &h->qkv, &h->part_ml, &h->part_acc, &h->act, &h->amax};
+  const size_t words[6] = {(size_t)s.H, (size_t)s.QKV, (size_t)h->nsplit_max * s.NQ * 2,
+                           (size_t)h->nsplit_max * s.QD, (size_t)s.F, (size_t)2 * h->G};
+  for (int i = 0; i < 6; ++i) {
+    h->tagged_bytes[i] = words[i] * 8;
+    HIPCHK(hipMalloc(tagged[i], h->tagged_bytes[i]), -1);
+    HIPCHK(hipMemsetAsync(*tagged[i], 0, h->tagged_bytes[i], h->stream), -1);
+  }
+  h->max_launch_tokens = 1 << 20;
   HIPCHK(hipMalloc(&h->out_tokens, (size_t)h->max_launch_tokens * 4), -1);
-  HIPCHK(hipMalloc(&h->sync, 256), -1);
-  HIPCHK(hipMemsetAsync(h->sync, 0, 256, h->stream), -1);
+  HIPCHK(hipMalloc(&h->trace, (size_t)(5 * h->L + 1) * 2 * h->G * 8), -1);
   HIPCHK(hipMalloc(&h->err, 256), -1);
   HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
   HIPCHK(hipMalloc(&h->dbg_layers, (size_t)(h->L + 1) * s.H * 4), -1);
@@ -297,16 +302,17 @@ static int check_occupancy(Handle* h) {
   return 0;
 }
 
-static int reset_sync_state(Handle* h) {
-  HIPCHK(hipMemsetAsync(h->sync, 0, 256, h->stream), -1);
+// Clear every tagged word (tag 0 is never expected) and the error word.
+static int clear_tagged_state(Handle* h) {
+  u64* bufs[6] = {h->x, h->qkv, h->part_ml, h->part_acc, h->act, h->amax};
+  for (int i = 0; i < 6; ++i) HIPCHK(hipMemsetAsync(bufs[i], 0, h->tagged_bytes[i], h->stream), -1);
   HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
-  h->sync_base = 0;
   return 0;
 }
 
 // One resident launch decoding n tokens starting at h->pos.
-static int run(Handle* h, int first_token, int n, int* out_host, bool debug) {
+static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int trace_token = -1) {
   if (n <= 0 || n > h->max_launch_tokens) {
     set_err("token count %d outside [1, %d]", n, h->max_launch_tokens);
     return -1;
@@ -325,19 +331,26 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug) {
   p.final_norm = h->final_norm;
   p.lmhead = h->lmhead;
   p.kv = h->kv;
+  const unsigned per_token = (unsigned)(5 * h->L + 1);
+  if ((unsigned long long)h->tag_base + (unsigned long long)n * per_token >= 0x7fffffffull) {
+    if (clear_tagged_state(h)) return -1;  // restart the tag sequence well before it wraps
+    h->tag_base = 1;
+  }
   p.x = h->x;
   p.qkv = h->qkv;
-  p.part = h->part;
+  p.part_ml = h->part_ml;
+  p.part_acc = h->part_acc;
   p.act = h->act;
   p.amax = h->amax;
   p.out_tokens = h->out_tokens;
-  p.sync = h->sync;
   p.err = h->err;
+  p.trace = trace_token >= 0 ? h->trace : nullptr;
+  p.trace_token = trace_token;
   p.dbg_layers = debug ? h->dbg_layers : nullptr;
   p.dbg_logits = debug ? h->dbg_logits : nullptr;
   p.inv_freq = h->inv_freq;
   p.timeout_ticks = h->timeout_ticks;
-  p.sync_base = h->sync_base;
+  p.tag_base = h->tag_base;
   p.n_layers = h->L;
   p.vocab = h->V;
   p.max_seq = h->S;
@@ -353,12 +366,12 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug) {
   HIPCHK(hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1), -1);
   int err = 0;
   HIPCHK(hipMemcpy(&err, h->err, 4, hipMemcpyDeviceToHost), -1);
+  h->tag_base += (unsigned)n * per_token;  // tags of this launch are never expected again
   if (err != MK_OK) {
-    reset_sync_state(h);
-    set_err("decode kernel aborted: %s", err == MK_ERR_TIMEOUT ? "grid sync timed out" : "device error");
+    clear_tagged_state(h);
+    set_err("decode kernel aborted: %s", err == MK_ERR_TIMEOUT ? "a dataflow wait timed out" : "device error");
     return -1;
   }
-  h->sync_base += (unsigned)n * (unsigned)(5 * h->L + 1) * (unsigned)h->G;
   if (out_host) HIPCHK(hipMemcpy(out_host, h->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost), -1);
   h->pos += n;
   return 0;
@@ -551,6 +564,26 @@ int megakernel_fill_kv_synthetic(void* handle, int len, unsigned long long seed,
   }
   h->pos = len;
   return 0;
+}
+
+int megakernel_trace_generate(void* handle, int first_token, int n, int trace_token,
+                              unsigned long long* host_trace) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !host_trace || trace_token < 0 || trace_token >= n) {
+    mk::set_err("invalid trace arguments");
+    return -1;
+  }
+  const size_t bytes = (size_t)(5 * h->L + 1) * 2 * h->G * 8;
+  if (hipMemsetAsync(h->trace, 0, bytes, h->stream) != hipSuccess) {
+    mk::set_err("trace clear failed");
+    return -1;
+  }
+  if (mk::run(h, first_token, n, nullptr, false, trace_token)) return -1;
+  if (hipMemcpy(host_trace, h->trace, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+    mk::set_err("trace copy failed");
+    return -1;
+  }
+  return (5 * h->L + 1) * 2 * h->G;
 }
 
 float megakernel_last_kernel_ms(void* handle) {

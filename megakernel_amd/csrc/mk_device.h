@@ -126,54 +126,100 @@ __device__ __forceinline__ uint16_t synth_bf16(unsigned long long key, unsigned 
   return f32_to_bf16(f);
 }
 
-// ------------------------------------------------------ grid synchronisation
-// The grid synchronises through one monotonically increasing 32-bit arrival
-// counter.  Sync point k of a launch completes when the counter reaches
-// base + (k+1) * G; comparisons are wrap-safe.  Each workgroup publishes its
-// phase results with an agent-scope release fence before its arrival
-// (buffer_wbl2 + vmcnt wait on gfx950) and the waiting thread issues an
-// agent-scope acquire fence (buffer_inv) after observing completion, so plain
-// loads/stores of the activation buffers are ordered across XCDs by the
-// HIP/C++ memory model.  Waits are bounded: on timeout (or when another
-// workgroup already failed) the error word is set and the kernel unwinds.
+// ------------------------------------------------ tagged dataflow words
+// Workgroups never meet at a barrier.  Every value one workgroup hands to
+// another is a single 64-bit word  (tag << 32) | fp32 bits, written with ONE
+// agent-scope relaxed atomic store (global_store_dwordx2 sc1 on gfx950: write
+// through to the device coherence point) and read with agent-scope relaxed
+// atomic loads (sc1: miss the non-coherent per-XCD caches).  The tag is the
+// global number of the phase that produced the value, so a consumer spins on
+// exactly the words it needs until every tag equals the producing phase's
+// number.  Because value and tag travel in one single-copy-atomic word, no
+// release/acquire fence (L2 write-back / invalidate) and no read-modify-write
+// is needed: a word with the right tag carries the right value.  Waits are
+// bounded: on timeout the error word is set and every workgroup unwinds.
+typedef unsigned long long u64;
 enum : int { MK_OK = 0, MK_ERR_TIMEOUT = 1 };
 
-__device__ __forceinline__ void grid_arrive(unsigned* ctr) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+__device__ __forceinline__ u64 ll_pack(float v, unsigned tag) {
+  return ((u64)tag << 32) | (u64)__float_as_uint(v);
 }
+__device__ __forceinline__ void ll_put(u64* p, u64 w) {
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ll_get(u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
+__device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigned)w); }
 
-// Returns false (uniformly across the workgroup) if the launch must abort.
-__device__ __forceinline__ bool grid_wait(unsigned* ctr, unsigned target, int* err,
-                                          unsigned long long timeout_ticks, int* s_flag) {
-  if (threadIdx.x == 0) {
-    int ok = 1;
-    unsigned long long t0 = wall_clock64();
-    unsigned spins = 0;
-    while ((int)(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-      __builtin_amdgcn_s_sleep(1);
-      if ((++spins & 255u) == 0) {
-        if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != MK_OK) {
-          ok = 0;
-          break;
-        }
-        if (wall_clock64() - t0 > timeout_ticks) {
-          __hip_atomic_store(err, (int)MK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = 0;
-          break;
-        }
+// Bounded spinning of one thread.  step() returns false when the wait must be
+// abandoned (this thread timed out, or another workgroup already failed).
+struct Spin {
+  u64 t0 = 0;
+  unsigned n = 0;
+  __device__ __forceinline__ bool step(int* err, u64 timeout_ticks) {
+    if (n == 0) t0 = wall_clock64();
+    ++n;
+    __builtin_amdgcn_s_sleep(1);
+    if ((n & 1023u) == 0) {
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != MK_OK) return false;
+      if (wall_clock64() - t0 > timeout_ticks) {
+        __hip_atomic_store(err, (int)MK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    *s_flag = ok;
+    return true;
   }
-  __syncthreads();
-  const int ok = *s_flag;
-  __syncthreads();
-  return ok != 0;
+};
+
+// Wait until src[0..n) all carry `tag`, then copy their values to dst (LDS).
+// Called by the whole workgroup (NT threads); returns false uniformly if the
+// launch must abort.  Each thread polls B words per round with independent
+// loads so the round costs one memory latency.
+template <int NT, int B>
+__device__ __forceinline__ bool ll_fetch(u64* src, int n, unsigned tag, float* dst, int* err,
+                                         u64 timeout_ticks) {
+  int failed = 0;
+  for (int base = 0; base < n && !failed; base += NT * B) {
+    u64 w[B];
+    Spin sp;
+    while (true) {
+      bool ready = true;
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int i = base + b * NT + (int)threadIdx.x;
+        if (i < n) {
+          w[b] = ll_get(src + i);
+          ready = ready && ll_tag(w[b]) == tag;
+        }
+      }
+      if (ready) break;
+      if (!sp.step(err, timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    }
+    if (!failed) {
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int i = base + b * NT + (int)threadIdx.x;
+        if (i < n) dst[i] = ll_val(w[b]);
+      }
+    }
+  }
+  return __syncthreads_or(failed) == 0;
+}
+
+// One word, one thread (residual rows).  Returns false on abort.
+__device__ __forceinline__ bool ll_wait1(u64* src, unsigned tag, float* out, int* err, u64 timeout_ticks) {
+  Spin sp;
+  while (true) {
+    const u64 w = ll_get(src);
+    if (ll_tag(w) == tag) {
+      *out = ll_val(w);
+      return true;
+    }
+    if (!sp.step(err, timeout_ticks)) return false;
+  }
 }
 
 }  // namespace mk

@@ -3,15 +3,22 @@
 //
 // Per token (reference phase order: /root/reference/src/megakernel.cu:132-332):
 //   for each layer:
-//     P1  rmsnorm(x) -> fused QKV GEMV          owners of 16-row QKV blocks
+//     P1  rmsnorm(x) -> fused QKV GEMV                          row-block owners
 //     P2  QK-norm + RoPE + KV append + split-position GQA attention partials
-//     P3  combine partials -> O GEMV -> x[rows] = x[rows] + o[rows]  (row owners)
-//     P4  rmsnorm(x) -> gate/up GEMV -> silu(g) * u                   (row owners)
-//     P5  down GEMV -> x[rows] += d[rows]                             (row owners)
-//   final rmsnorm -> tied LM head -> fused argmax (64-bit atomic max)
-// Each phase ends at a grid sync point (5 * layers + 1 per token).  Every
-// residual element has exactly one writer (the owner of its 16-row block), so
-// there is no read-modify-write race on x (unlike megakernel.cu:243-245,288-290).
+//     P3  merge partials -> O GEMV -> x[rows] = x[rows] + o[rows] row-block owners
+//     P4  rmsnorm(x) -> gate/up GEMV -> silu(g) * u               row-block owners
+//     P5  down GEMV -> x[rows] += d[rows]                         row-block owners
+//   final rmsnorm -> tied LM head -> per-workgroup argmax -> next token
+//
+// There is no grid barrier.  Each phase instance has a global number (its
+// tag); every activation word carries the tag of the phase that wrote it, and
+// a consumer waits for exactly the words it reads (tagged dataflow, see
+// mk_device.h).  Every residual element has exactly one writer per phase (the
+// owner of its 16-row block), so there is no read-modify-write race on x
+// (unlike megakernel.cu:243-245,288-290), and the per-token tags make the
+// reference's never-re-armed KV flag problem (barriers.cuh:112-134)
+// impossible.  Buffers are single-buffered: every write of a buffer depends
+// (through the phase chain) on every read of its previous contents.
 #pragma once
 #include "mk_config.h"
 #include "mk_device.h"
@@ -21,7 +28,12 @@ namespace mk {
 constexpr int NT = 512;               // threads per workgroup (8 waves)
 constexpr int NW = NT / kWave;
 constexpr int CHUNK_MAX = 2048;       // max positions per attention work item
-constexpr int PART_STRIDE_PAD = 4;    // partial row = m, l, pad, pad, acc[D]
+constexpr int PHASES_PER_LAYER = 5;
+constexpr int ML_CAP = 1024;          // LDS floats for split (max, sum): nsplit_max * NQ * 2
+constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
+__device__ __forceinline__ unsigned tag14(unsigned tag) { return tag % 16383u + 1u; }
+constexpr int IDX_BITS = 18;          // ... and an 18-bit vocabulary index
+constexpr unsigned IDX_MAX = (1u << IDX_BITS) - 1;
 
 struct Params {
   const u32x4* layers;        // packed per-layer weights (L * U_LAYER units)
@@ -29,36 +41,42 @@ struct Params {
   const uint16_t* final_norm; // [H] bf16
   const u32x4* lmhead;        // packed tied embedding [V/16][KT_H][64]
   uint16_t* kv;               // [L][2][NKV][max_seq][D] bf16
-  float* x;                   // [H] residual stream
-  float* qkv;                 // [QKV] projections of the current layer
-  float* part;                // attention partials [NKV*nsplit_max][GQA][PART_STRIDE]
-  float* act;                 // [F] silu(gate)*up
-  unsigned long long* amax;   // [n_tokens] argmax keys
+  u64* x;                     // [H] residual stream (tagged)
+  u64* qkv;                   // [QKV] projections of the current layer (tagged)
+  u64* part_ml;               // [nsplit_max][NQ][2] split max / sum (tagged)
+  u64* part_acc;              // [nsplit_max][NQ][D] split unnormalised outputs (tagged)
+  u64* act;                   // [F] silu(gate)*up (tagged)
+  u64* amax;                  // [2][G] per-workgroup argmax words (token parity)
   int* out_tokens;            // [n_tokens]
-  unsigned* sync;             // grid arrival counter
   int* err;                   // error word
   float* dbg_layers;          // optional [(L+1)][H]: embedding, then x after each layer
   float* dbg_logits;          // optional [V]
+  u64* trace;                 // optional [(5L+1)][2][G] wall-clock ready/done per phase
   const float* inv_freq;      // [D/2] RoPE inverse frequencies
-  unsigned long long timeout_ticks;
-  unsigned sync_base;
+  u64 timeout_ticks;
+  unsigned tag_base;          // tag of the first phase of this launch
   int n_layers, vocab, max_seq;
   int pos0, n_tokens, first_token;
   int nsplit_max, chunk_min;
+  int trace_token;
 };
 
 template <class S>
 struct Smem {
   static constexpr int VEC = (S::F > S::QD ? (S::F > S::H ? S::F : S::H) : (S::QD > S::H ? S::QD : S::H));
   float vec[VEC];                     // GEMV input vector
+  float xin[S::H];                    // residual stream as read
   float red[2 * NW * 16];             // GEMV cross-wave partials
-  float qk[(S::GQA + 1) * S::D];      // normed + rotated q heads, then k
+  float qk[(S::GQA + 1) * S::D];      // q heads, then k (normed + rotated in place)
   float vv[S::D];                     // v of the current position
+  u32x4 kvcur[2][S::D / 8];           // bf16 K/V of the current position
   float sc[S::GQA * CHUNK_MAX];       // attention scores / probabilities
   float pv[NW * S::GQA * S::D];       // attention P*V cross-wave partials
+  float ml[ML_CAP];                    // merge: per split/head (max, sum) -> (scale)
+  float hl[S::NQ];                    // merge: per head 1 / total sum
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
   float scratch[4 * NW];
-  unsigned long long amax[NW];
+  u64 amax[NW];
   int flag;
 };
 
@@ -151,9 +169,9 @@ __device__ __forceinline__ void gemv16x2(const u32x4* __restrict__ ta, const u32
 }
 
 // out[i] = v[i] * rsqrt(mean(v^2) + eps) * gain[i]  (reference rmsnorm.cuh:87-108).
-// The source is the fp32 residual stream, or (layer 0) the embedding row.
+// The source is the residual stream in LDS, or (layer 0) the embedding row.
 template <class S>
-__device__ __forceinline__ void rmsnorm_to(Smem<S>& sm, const float* x, const u32x4* emb, int tok,
+__device__ __forceinline__ void rmsnorm_to(Smem<S>& sm, const float* xl, const u32x4* emb, int tok,
                                            const uint16_t* gain, float* out) {
   constexpr int VPT = (S::H + NT - 1) / NT;
   float v[VPT];
@@ -162,7 +180,7 @@ __device__ __forceinline__ void rmsnorm_to(Smem<S>& sm, const float* x, const u3
   for (int c = 0; c < VPT; ++c) {
     const int i = threadIdx.x + c * NT;
     float t = 0.f;
-    if (i < S::H) t = emb ? packed_elem<S::KT_H>(emb, tok, i) : x[i];
+    if (i < S::H) t = emb ? packed_elem<S::KT_H>(emb, tok, i) : xl[i];
     v[c] = t;
     ss = fmaf(t, t, ss);
   }
@@ -176,51 +194,50 @@ __device__ __forceinline__ void rmsnorm_to(Smem<S>& sm, const float* x, const u3
   __syncthreads();
 }
 
-template <class S>
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  return g / (1.0f + __expf(-g)) * u;
-}
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
-// Work item i of a phase with `n` items runs on workgroup (i + off) mod G.
+// Work item i of a phase runs on workgroup (i + off) mod G.
 __device__ __forceinline__ int first_item(int wg, int off, int G) { return (wg + G - (off % G)) % G; }
 
+__device__ __forceinline__ void trace_mark(const Params& p, int t, int slot, int which) {
+  if (p.trace && t == p.trace_token && threadIdx.x == 0)
+    p.trace[((long long)slot * 2 + which) * gridDim.x + blockIdx.x] = wall_clock64();
+}
+
 // ---------------------------------------------------------------- phase P2
+// One attention work item: kv head g, positions [s*chunk, min((s+1)*chunk, pos+1)).
 template <class S>
-__device__ void attention_item(const Params& p, Smem<S>& sm, int layer, int pos, int g, int s,
-                               int nsplit, int chunk) {
+__device__ bool attention_item(const Params& p, Smem<S>& sm, int layer, int pos, int g, int s, int chunk,
+                               unsigned tag_in, unsigned tag_out) {
   constexpr int D = S::D, GQA = S::GQA, LPP = D / 8, PPW = kWave / LPP;
-  constexpr int PS = D + PART_STRIDE_PAD;
   const int tid = threadIdx.x, w = tid / kWave, l = opaque_v(tid % kWave);
   const int n = pos + 1;
+  // splits are never empty (nsplit = ceil(n / chunk)), so every item reads
+  // its group's q/k/v before writing: no item can overwrite partials that an
+  // O-projection owner of the previous layer is still merging.
   const int t0 = s * chunk, t1 = min(n, t0 + chunk);
-  float* prow = p.part + ((long long)(g * p.nsplit_max + s) * GQA) * PS;
-  if (t0 >= t1) {  // empty split: neutral partial
-    for (int e = tid; e < GQA * PS; e += NT) {
-      const int j = e / PS, c = e % PS;
-      prow[j * PS + c] = (c == 0) ? -INFINITY : 0.f;
-    }
-    return;
-  }
+  u64* mlw = p.part_ml + ((long long)s * S::NQ + g * GQA) * 2;
+  u64* accw = p.part_acc + ((long long)s * S::NQ + g * GQA) * D;
+  // inputs: the group's q heads, its k and v rows
+  if (!ll_fetch<NT, 1>(p.qkv + g * GQA * D, GQA * D, tag_in, sm.qk, p.err, p.timeout_ticks)) return false;
+  if (!ll_fetch<NT, 1>(p.qkv + S::QD + g * D, D, tag_in, sm.qk + GQA * D, p.err, p.timeout_ticks)) return false;
+  if (!ll_fetch<NT, 1>(p.qkv + S::QD + S::KVD + g * D, D, tag_in, sm.vv, p.err, p.timeout_ticks)) return false;
   const uint16_t* nrm = p.norms + (long long)layer * S::NORM_STRIDE;
-  // 1. per-head RMSNorm of the GQA q heads and the k head (reference
-  //    rmsnorm.cuh:57-84), v copied; one wave per head.
+  // 1. per-head RMSNorm of the q heads and the k head (reference
+  //    rmsnorm.cuh:57-84); one wave per head.
   if (w < GQA + 1) {
-    const float* src = (w < GQA) ? p.qkv + (g * GQA + w) * D : p.qkv + S::QD + g * D;
     const uint16_t* gain = nrm + (w < GQA ? S::NORM_Q : S::NORM_K);
     float v[D / kWave];
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < D / kWave; ++c) {
-      v[c] = src[l + c * kWave];
+      v[c] = sm.qk[w * D + l + c * kWave];
       ss = fmaf(v[c], v[c], ss);
     }
     ss = wave_sum(ss);
     const float r = rsqrtf(ss / (float)D + kRmsEps);
 #pragma unroll
     for (int c = 0; c < D / kWave; ++c) sm.qk[w * D + l + c * kWave] = v[c] * r * bf16_to_f32(gain[l + c * kWave]);
-  } else if (w == GQA + 1) {
-#pragma unroll
-    for (int c = 0; c < D / kWave; ++c) sm.vv[l + c * kWave] = p.qkv[S::QD + S::KVD + g * D + l + c * kWave];
   }
   __syncthreads();
   // 2. RoPE, rotate-half pairs (d, d + D/2) (reference attention.cuh:22-44).
@@ -234,13 +251,22 @@ __device__ void attention_item(const Params& p, Smem<S>& sm, int layer, int pos,
   __syncthreads();
   uint16_t* kb = p.kv + ((long long)(layer * 2 + 0) * S::NKV + g) * (long long)p.max_seq * D;
   uint16_t* vb = p.kv + ((long long)(layer * 2 + 1) * S::NKV + g) * (long long)p.max_seq * D;
-  // 3. the split that owns position `pos` appends bf16 K/V (kv_cache.cuh:58-78).
-  if (t0 <= pos && pos < t1) {
-    for (int d = tid; d < D; d += NT) {
-      kb[(long long)pos * D + d] = f32_to_bf16(sm.qk[GQA * D + d]);
-      vb[(long long)pos * D + d] = f32_to_bf16(sm.vv[d]);
+  // 3. bf16 K/V of the current position (reference kv_cache.cuh:58-78); the
+  //    split that owns `pos` appends them to the cache with write-through
+  //    stores and uses its LDS copy for this token.
+  const bool own = (t0 <= pos && pos < t1);
+  if (tid < D / 2) {
+    const int d = 2 * tid;
+    const unsigned kw = (unsigned)f32_to_bf16(sm.qk[GQA * D + d]) | ((unsigned)f32_to_bf16(sm.qk[GQA * D + d + 1]) << 16);
+    const unsigned vw = (unsigned)f32_to_bf16(sm.vv[d]) | ((unsigned)f32_to_bf16(sm.vv[d + 1]) << 16);
+    reinterpret_cast<unsigned*>(sm.kvcur[0])[tid] = kw;
+    reinterpret_cast<unsigned*>(sm.kvcur[1])[tid] = vw;
+    if (own) {
+      __hip_atomic_store(reinterpret_cast<unsigned*>(kb + (long long)pos * D) + tid, kw, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(reinterpret_cast<unsigned*>(vb + (long long)pos * D) + tid, vw, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   }
   __syncthreads();
   // 4. scores s_j[t] = (q_j . K[t]) / sqrt(D); LPP lanes per position.
@@ -258,8 +284,8 @@ __device__ void attention_item(const Params& p, Smem<S>& sm, int layer, int pos,
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = tb + u * NW * PPW + po;
-      kk[u] = (t < t1) ? ld_nt(reinterpret_cast<const u32x4*>(kb + (long long)t * D + c * 8))
-                       : u32x4{0u, 0u, 0u, 0u};
+      kk[u] = (t < t1 && t != pos) ? ld_nt(reinterpret_cast<const u32x4*>(kb + (long long)t * D + c * 8))
+                                   : sm.kvcur[0][c];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -303,8 +329,8 @@ __device__ void attention_item(const Params& p, Smem<S>& sm, int layer, int pos,
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = tb + u * NW * PPW + po;
-      vk[u] = (t < t1) ? ld_nt(reinterpret_cast<const u32x4*>(vb + (long long)t * D + c * 8))
-                       : u32x4{0u, 0u, 0u, 0u};
+      vk[u] = (t < t1 && t != pos) ? ld_nt(reinterpret_cast<const u32x4*>(vb + (long long)t * D + c * 8))
+                                   : sm.kvcur[1][c];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -338,38 +364,62 @@ __device__ void attention_item(const Params& p, Smem<S>& sm, int layer, int pos,
   }
   __syncthreads();
   for (int e = tid; e < GQA * D; e += NT) {
-    const int j = e / D, d = e % D;
     float v = 0.f;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) v += sm.pv[(i * GQA + j) * D + d];
-    prow[j * PS + PART_STRIDE_PAD + d] = v;
+    for (int i = 0; i < NW; ++i) v += sm.pv[i * GQA * D + e];
+    ll_put(accw + e, ll_pack(v, tag_out));
   }
-  if (tid < GQA) {
-    prow[tid * PS + 0] = mj[tid];
-    prow[tid * PS + 1] = lj[tid];
-  }
+  if (tid < GQA * 2) ll_put(mlw + tid, ll_pack((tid & 1) ? lj[tid >> 1] : mj[tid >> 1], tag_out));
+  return true;
 }
 
 // ---------------------------------------------------------------- phase P3
 // Merge the split partials of every q head (log-sum-exp) into vec[QD].
 template <class S>
-__device__ void combine_attention(const Params& p, Smem<S>& sm, int nsplit) {
-  constexpr int D = S::D, GQA = S::GQA, PS = D + PART_STRIDE_PAD;
-  for (int e = threadIdx.x; e < S::QD; e += NT) {
-    const int h = e / D, d = e % D, g = h / GQA, j = h % GQA;
-    const float* base = p.part + ((long long)(g * p.nsplit_max) * GQA + j) * PS;
+__device__ bool merge_attention(const Params& p, Smem<S>& sm, int nsplit, unsigned tag) {
+  constexpr int D = S::D, NQ = S::NQ;
+  if (!ll_fetch<NT, 2>(p.part_ml, nsplit * NQ * 2, tag, sm.ml, p.err, p.timeout_ticks)) return false;
+  if (threadIdx.x < NQ) {
+    const int h = threadIdx.x;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, base[(long long)s * GQA * PS]);
-    float L = 0.f, o = 0.f;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, sm.ml[(s * NQ + h) * 2]);
+    float L = 0.f;
     for (int s = 0; s < nsplit; ++s) {
-      const float* r = base + (long long)s * GQA * PS;
-      const float f = __expf(r[0] - M);
-      L = fmaf(f, r[1], L);
-      o = fmaf(f, r[PART_STRIDE_PAD + d], o);
+      const float f = __expf(sm.ml[(s * NQ + h) * 2] - M);
+      L = fmaf(f, sm.ml[(s * NQ + h) * 2 + 1], L);
+      sm.ml[(s * NQ + h) * 2] = f;  // becomes the split's scale
     }
-    sm.vec[e] = o / L;
+    sm.hl[h] = 1.0f / L;
   }
   __syncthreads();
+  int failed = 0;
+  for (int e = threadIdx.x; e < S::QD && !failed; e += NT) {
+    const int h = e / D;
+    float o = 0.f;
+    for (int s0 = 0; s0 < nsplit && !failed; s0 += 8) {
+      u64 wv[8];
+      Spin sp;
+      while (true) {
+        bool ready = true;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+          if (s0 + b < nsplit) {
+            wv[b] = ll_get(p.part_acc + (long long)(s0 + b) * S::QD + e);
+            ready = ready && ll_tag(wv[b]) == tag;
+          }
+        if (ready) break;
+        if (!sp.step(p.err, p.timeout_ticks)) {
+          failed = 1;
+          break;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        if (s0 + b < nsplit) o = fmaf(sm.ml[((s0 + b) * NQ + h) * 2], ll_val(wv[b]), o);
+    }
+    sm.vec[e] = o * sm.hl[h];
+  }
+  return __syncthreads_or(failed) == 0;
 }
 
 // ------------------------------------------------------------------ kernel
@@ -378,27 +428,44 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   __shared__ Smem<S> sm;
   const int G = gridDim.x, wg = blockIdx.x, tid = threadIdx.x;
   const int w = tid / kWave, l = tid % kWave;
-  unsigned k = 0;  // sync points passed
+  const int L = p.n_layers;
+  const unsigned per_token = (unsigned)(PHASES_PER_LAYER * L + 1);
   // Phase -> workgroup offsets spread the per-layer byte load across CUs.
   const int off_qkv = G / 4, off_gu = G / 4, off_o = (3 * G) / 4, off_down = 0, off_att = 0;
-
-  if (wg == 0)
-    for (int i = tid; i < p.n_tokens; i += NT) p.amax[i] = 0ull;
-
-#define MK_SYNC()                                                                        \
-  do {                                                                                   \
-    grid_arrive(p.sync);                                                                 \
-    ++k;                                                                                 \
-    if (!grid_wait(p.sync, p.sync_base + k * (unsigned)G, p.err, p.timeout_ticks, &sm.flag)) \
-      return;                                                                            \
-  } while (0)
 
   int tok = p.first_token;
   for (int t = 0; t < p.n_tokens; ++t) {
     const int pos = p.pos0 + t;
+    const unsigned tb = p.tag_base + (unsigned)t * per_token;  // tag of this token's first phase
     if (t > 0) {
-      const unsigned idx = argmax_key_index(p.amax[t - 1]);
-      tok = idx < (unsigned)p.vocab ? (int)idx : 0;  // always in range (keys are never 0)
+      // next token = argmax over every workgroup's word of the previous token
+      const unsigned want = tag14(tb - 1u);
+      u64* slots = p.amax + ((t - 1) & 1) * G;
+      int failed = 0;
+      u64 best = 0;
+      for (int i = tid; i < G && !failed; i += NT) {
+        Spin sp;
+        u64 v;
+        while (((v = ll_get(slots + i)) & TAG14) != want)
+          if (!sp.step(p.err, p.timeout_ticks)) {
+            failed = 1;
+            break;
+          }
+        best = v > best ? v : best;
+      }
+      if (__syncthreads_or(failed)) return;
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        const u64 o = __shfl_xor(best, m);
+        best = o > best ? o : best;
+      }
+      if (l == 0) sm.amax[w] = best;
+      __syncthreads();
+      best = sm.amax[0];
+      for (int i = 1; i < NW; ++i) best = sm.amax[i] > best ? sm.amax[i] : best;
+      __syncthreads();
+      const unsigned idx = IDX_MAX - (unsigned)((best >> 14) & IDX_MAX);
+      tok = idx < (unsigned)p.vocab ? (int)idx : 0;
       if (wg == 0 && tid == 0) p.out_tokens[t - 1] = tok;
     }
     if (tid < S::D / 2) {
@@ -411,89 +478,116 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       for (int i = tid; i < S::H; i += NT) p.dbg_layers[i] = packed_elem<S::KT_H>(p.lmhead, tok, i);
     __syncthreads();
     const int n = pos + 1;
-    int nsplit = (n + p.chunk_min - 1) / p.chunk_min;
-    nsplit = nsplit < 1 ? 1 : (nsplit > p.nsplit_max ? p.nsplit_max : nsplit);
-    const int chunk = (n + nsplit - 1) / nsplit;
+    int ns0 = (n + p.chunk_min - 1) / p.chunk_min;
+    ns0 = ns0 < 1 ? 1 : (ns0 > p.nsplit_max ? p.nsplit_max : ns0);
+    const int chunk = (n + ns0 - 1) / ns0;
+    const int nsplit = (n + chunk - 1) / chunk;  // <= ns0, and no split is empty
 
-    for (int layer = 0; layer < p.n_layers; ++layer) {
+    for (int layer = 0; layer < L; ++layer) {
       const u32x4* wl = p.layers + (long long)layer * S::U_LAYER;
       const uint16_t* nrm = p.norms + (long long)layer * S::NORM_STRIDE;
-      const u32x4* emb0 = (layer == 0) ? p.lmhead : nullptr;
+      const unsigned tg = tb + (unsigned)(PHASES_PER_LAYER * layer);  // tag of P1 of this layer
+      const unsigned tg_x = tg - 1u;  // tag of the x rows this layer starts from (layer > 0)
+      const int slot = PHASES_PER_LAYER * layer;
       // P1: QKV
       {
         bool have = false;
         for (int rb = first_item(wg, off_qkv, G); rb < S::RB_QKV; rb += G) {
           if (!have) {
-            rmsnorm_to<S>(sm, p.x, emb0, tok, nrm + S::NORM_ATTN, sm.vec);
+            if (layer > 0 && !ll_fetch<NT, 2>(p.x, S::H, tg_x, sm.xin, p.err, p.timeout_ticks)) return;
+            trace_mark(p, t, slot + 0, 0);
+            rmsnorm_to<S>(sm, sm.xin, layer == 0 ? p.lmhead : nullptr, tok, nrm + S::NORM_ATTN, sm.vec);
             have = true;
           }
           const float y = gemv16<S::KT_H>(wl + S::OFF_QKV + (long long)rb * S::KT_H * 64, sm.vec, sm.red);
-          if (tid < 16) p.qkv[rb * 16 + tid] = y;
+          if (tid < 16) ll_put(p.qkv + rb * 16 + tid, ll_pack(y, tg));
         }
+        if (have) trace_mark(p, t, slot + 0, 1);
       }
-      MK_SYNC();
       // P2: attention partials
-      for (int it = first_item(wg, off_att, G); it < S::NKV * nsplit; it += G)
-        attention_item<S>(p, sm, layer, pos, it / nsplit, it % nsplit, nsplit, chunk);
-      MK_SYNC();
+      {
+        bool any = false;
+        for (int it = first_item(wg, off_att, G); it < S::NKV * nsplit; it += G) {
+          if (!attention_item<S>(p, sm, layer, pos, it / nsplit, it % nsplit, chunk, tg, tg + 1u)) return;
+          if (!any) trace_mark(p, t, slot + 1, 0);
+          any = true;
+        }
+        if (any) trace_mark(p, t, slot + 1, 1);
+      }
       // P3: O projection + residual
       {
         bool have = false;
         for (int rb = first_item(wg, off_o, G); rb < S::RB_H; rb += G) {
           if (!have) {
-            combine_attention<S>(p, sm, nsplit);
+            if (!merge_attention<S>(p, sm, nsplit, tg + 1u)) return;
+            trace_mark(p, t, slot + 2, 0);
             have = true;
           }
           const float y = gemv16<S::KT_Q>(wl + S::OFF_O + (long long)rb * S::KT_Q * 64, sm.vec, sm.red);
+          int failed = 0;
           if (tid < 16) {
             const int row = rb * 16 + tid;
-            const float xo = emb0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : p.x[row];
-            p.x[row] = xo + y;
+            float xo;
+            if (layer == 0) xo = packed_elem<S::KT_H>(p.lmhead, tok, row);
+            else failed = !ll_wait1(p.x + row, tg_x, &xo, p.err, p.timeout_ticks);
+            if (!failed) ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
           }
+          if (__syncthreads_or(failed)) return;
         }
+        if (have) trace_mark(p, t, slot + 2, 1);
       }
-      MK_SYNC();
       // P4: gate/up + SiLU
       {
         bool have = false;
         for (int pr = first_item(wg, off_gu, G); pr < S::RB_F; pr += G) {
           if (!have) {
-            rmsnorm_to<S>(sm, p.x, nullptr, tok, nrm + S::NORM_FFN, sm.vec);
+            if (!ll_fetch<NT, 2>(p.x, S::H, tg + 2u, sm.xin, p.err, p.timeout_ticks)) return;
+            trace_mark(p, t, slot + 3, 0);
+            rmsnorm_to<S>(sm, sm.xin, nullptr, tok, nrm + S::NORM_FFN, sm.vec);
             have = true;
           }
           float yg, yu;
-          const u32x4* tg = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
-          gemv16x2<S::KT_H>(tg, tg + S::KT_H * 64, sm.vec, sm.red, yg, yu);
-          if (tid < 16) p.act[pr * 16 + tid] = silu_mul<S>(yg, yu);
+          const u32x4* tgp = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
+          gemv16x2<S::KT_H>(tgp, tgp + S::KT_H * 64, sm.vec, sm.red, yg, yu);
+          if (tid < 16) ll_put(p.act + pr * 16 + tid, ll_pack(silu_mul(yg, yu), tg + 3u));
         }
+        if (have) trace_mark(p, t, slot + 3, 1);
       }
-      MK_SYNC();
       // P5: down projection + residual
       {
         bool have = false;
         for (int rb = first_item(wg, off_down, G); rb < S::RB_H; rb += G) {
           if (!have) {
-            for (int i = tid; i < S::F; i += NT) sm.vec[i] = p.act[i];
-            __syncthreads();
+            if (!ll_fetch<NT, 6>(p.act, S::F, tg + 3u, sm.vec, p.err, p.timeout_ticks)) return;
+            trace_mark(p, t, slot + 4, 0);
             have = true;
           }
           const float y = gemv16<S::KT_F>(wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64, sm.vec, sm.red);
+          int failed = 0;
           if (tid < 16) {
             const int row = rb * 16 + tid;
-            const float xn = p.x[row] + y;
-            p.x[row] = xn;
-            if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
+            float xo;
+            failed = !ll_wait1(p.x + row, tg + 2u, &xo, p.err, p.timeout_ticks);
+            if (!failed) {
+              const float xn = xo + y;
+              ll_put(p.x + row, ll_pack(xn, tg + 4u));
+              if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
+            }
           }
+          if (__syncthreads_or(failed)) return;
         }
+        if (have) trace_mark(p, t, slot + 4, 1);
       }
-      MK_SYNC();
     }
-    // Final norm + tied LM head + argmax (reference sampling.cuh:32-117).
+    // Final norm + tied LM head + per-workgroup argmax (reference sampling.cuh:32-117).
     {
-      rmsnorm_to<S>(sm, p.x, nullptr, tok, p.final_norm, sm.vec);
+      const unsigned tl = tb + (unsigned)(PHASES_PER_LAYER * L);
+      if (!ll_fetch<NT, 2>(p.x, S::H, tl - 1u, sm.xin, p.err, p.timeout_ticks)) return;
+      trace_mark(p, t, PHASES_PER_LAYER * L, 0);
+      rmsnorm_to<S>(sm, sm.xin, nullptr, tok, p.final_norm, sm.vec);
       const long long nb = p.vocab / 16;
       const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G;
-      unsigned long long best = 0ull;
+      u64 best = 0ull;
       for (long long b = b0 + w; b < b1; b += NW) {
         // re-derived per block so the LDS reads of the hidden vector are not
         // hoisted out of the block loop (256 floats per lane would not fit)
@@ -517,27 +611,59 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         if (l < 16) {
           const unsigned idx = (unsigned)(b * 16 + l);
           if (p.dbg_logits) p.dbg_logits[idx] = acc;
-          const unsigned long long key = argmax_key(acc, idx);
+          // key: ordered value | (IDX_MAX - idx) | tag: an unsigned max picks
+          // the largest logit and, among equal logits, the lowest index
+          // (torch.argmax semantics)
+          const u64 key = ((u64)f32_order_key(acc) << 32) | ((u64)(IDX_MAX - idx) << 14);
           best = key > best ? key : best;
         }
       }
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) {
-        const unsigned long long o = __shfl_xor(best, m);
+        const u64 o = __shfl_xor(best, m);
         best = o > best ? o : best;
       }
       if (l == 0) sm.amax[w] = best;
       __syncthreads();
       if (tid == 0) {
-        unsigned long long b = 0ull;
+        u64 b = 0ull;
         for (int i = 0; i < NW; ++i) b = sm.amax[i] > b ? sm.amax[i] : b;
-        if (b) __hip_atomic_fetch_max(p.amax + t, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ll_put(p.amax + (t & 1) * G + wg, b | (u64)tag14(tl));
       }
+      trace_mark(p, t, PHASES_PER_LAYER * L, 1);
+      __syncthreads();
     }
-    MK_SYNC();
   }
-  if (wg == 0 && tid == 0) p.out_tokens[p.n_tokens - 1] = (int)argmax_key_index(p.amax[p.n_tokens - 1]);
-#undef MK_SYNC
+  if (wg == 0) {  // the last token's id
+    const int t = p.n_tokens;
+    const unsigned want = tag14(p.tag_base + (unsigned)t * per_token - 1u);
+    u64* slots = p.amax + ((t - 1) & 1) * G;
+    int failed = 0;
+    u64 best = 0;
+    for (int i = tid; i < G && !failed; i += NT) {
+      Spin sp;
+      u64 v;
+      while (((v = ll_get(slots + i)) & TAG14) != want)
+        if (!sp.step(p.err, p.timeout_ticks)) {
+          failed = 1;
+          break;
+        }
+      best = v > best ? v : best;
+    }
+    if (__syncthreads_or(failed)) return;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const u64 o = __shfl_xor(best, m);
+      best = o > best ? o : best;
+    }
+    if (l == 0) sm.amax[w] = best;
+    __syncthreads();
+    if (tid == 0) {
+      for (int i = 0; i < NW; ++i) best = sm.amax[i] > best ? sm.amax[i] : best;
+      const unsigned idx = IDX_MAX - (unsigned)((best >> 14) & IDX_MAX);
+      p.out_tokens[t - 1] = idx < (unsigned)p.vocab ? (int)idx : 0;
+    }
+  }
 }
 
 }  // namespace mk
