@@ -85,13 +85,16 @@ def trace_summary(eng, shape, args, info):
     import numpy as np
     L, G = shape.n_layers, eng.grid_size
     n = 5 * L + 1
-    buf = (ctypes.c_ulonglong * (n * 2 * G))()
+    n_evt = 16
+    buf = (ctypes.c_ulonglong * ((n * 2 + n_evt) * G))()
     eng.fill_kv_synthetic(args.ctx, args.seed)
     r = eng.lib.megakernel_trace_generate(eng._handle, 1, 8, 4, buf)
     if r < 0:
         print("# trace failed", file=sys.stderr)
         return
-    tr = np.frombuffer(buf, dtype=np.uint64).reshape(n, 2, G).astype(np.float64)
+    allv = np.frombuffer(buf, dtype=np.uint64).astype(np.float64)
+    tr = allv[:n * 2 * G].reshape(n, 2, G)
+    ev = allv[n * 2 * G:].reshape(n_evt, G)
     khz = info["wall_clock_khz"] or 100000
     us = 1e3 / khz  # microseconds per tick
     names = ["qkv", "attn", "o", "gate_up", "down"]
@@ -119,6 +122,18 @@ def trace_summary(eng, shape, args, info):
         d = np.mean(work[k]) if work[k] else 0.0
         print(f"#   {k:8s} handoff {w:7.2f} us   last-ready->last-done {d:7.2f} us   (x{len(work[k])})",
               file=sys.stderr)
+    evn = ["att_ready", "att_rope", "att_softmax", "att_stored", "att_partial", "att_gathered", "o_ready",
+           "o_stored", "qkv_stored", "gu_stored", "dn_stored", "dn_ready"]
+    base = min(ev[e][ev[e] > 0].min() for e in range(len(evn)) if (ev[e] > 0).any())
+    print(f"# events of layer {L // 2} (us from the first event; min / median / max over workgroups):",
+          file=sys.stderr)
+    order = sorted(range(len(evn)), key=lambda e: np.median(ev[e][ev[e] > 0]) if (ev[e] > 0).any() else 1e30)
+    for e in order:
+        v = ev[e][ev[e] > 0]
+        if v.size:
+            v = (v - base) * us
+            print(f"#   {evn[e]:12s} n={v.size:3d}  {v.min():7.2f} {np.median(v):7.2f} {v.max():7.2f}",
+                  file=sys.stderr)
 
 
 def main():

@@ -115,9 +115,10 @@ int megakernel_fill_kv_synthetic(void* handle, int len, unsigned long long seed,
 
 /* megakernel_generate that also records, for step trace_token, the device
  * wall clock (100 MHz on MI355X) when each workgroup's inputs of every phase
- * were ready and when it finished the phase: host_trace receives
- * u64[(5 * layers + 1)][2][grid] (0 = the workgroup had no work in that
- * phase).  Profiling only.  Returns the number of entries or -1. */
+ * were ready and when it finished the phase, followed by 16 finer events of
+ * the middle layer: host_trace receives u64[(5 * layers + 1) * 2 + 16][grid]
+ * (0 = the workgroup had no such event).  Profiling only.  Returns the number
+ * of entries or -1. */
 int megakernel_trace_generate(void* handle, int first_token, int n, int trace_token,
                               unsigned long long* host_trace);
 

@@ -114,7 +114,7 @@ struct Handle {
   uint16_t* final_norm = nullptr;
   u32x4* lmhead = nullptr;
   uint16_t* kv = nullptr;
-  u64 *x = nullptr, *qkv = nullptr, *part_ml = nullptr, *part_acc = nullptr, *act = nullptr;
+  u64 *x = nullptr, *qkv = nullptr, *part = nullptr, *attn = nullptr, *act = nullptr;
   u64* amax = nullptr;
   size_t tagged_bytes[6] = {0, 0, 0, 0, 0, 0};
   int* out_tokens = nullptr;
@@ -142,8 +142,8 @@ static int occupancy_ok(int* nblk) {
 }
 
 static void free_all(Handle* h) {
-  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part_ml,
-                  h->part_acc, h->act, h->amax, h->out_tokens, h->err, h->inv_freq, h->dbg_layers,
+  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part,
+                  h->attn, h->act, h->amax, h->out_tokens, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
@@ -186,11 +186,7 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   HIPCHK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, h->device), -1);
   h->timeout_ticks = (unsigned long long)(wall_khz > 0 ? wall_khz : 100000) * 10000ull;  // 10 s
   h->nsplit_max = h->G / s.NKV > 0 ? h->G / s.NKV : 1;
-  if (h->nsplit_max * s.NQ * 2 > ML_CAP) h->nsplit_max = ML_CAP / (s.NQ * 2);
-  if ((long long)h->nsplit_max * CHUNK_MAX < h->S) {
-    set_err("max_seq %d exceeds %d splits x %d positions", h->S, h->nsplit_max, CHUNK_MAX);
-    return -1;
-  }
+  if (h->nsplit_max > NSPLIT_CAP) h->nsplit_max = NSPLIT_CAP;
   HIPCHK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), -1);
   HIPCHK(hipEventCreate(&h->ev0), -1);
   HIPCHK(hipEventCreate(&h->ev1), -1);
@@ -204,9 +200,10 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   HIPCHK(hipMalloc(&h->kv, h->kv_bytes), -1);
   HIPCHK(hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream), -1);
   // tagged activation words (zero = tag 0, never a valid tag)
-  u64** tagged[6] = {&h->x, &h->qkv, &h->part_ml, &h->part_acc, &h->act, &h->amax};
-  const size_t words[6] = {(size_t)s.H, (size_t)s.QKV, (size_t)h->nsplit_max * s.NQ * 2,
-                           (size_t)h->nsplit_max * s.QD, (size_t)s.F, (size_t)2 * h->G};
+  u64** tagged[6] = {&h->x, &h->qkv, &h->part, &h->attn, &h->act, &h->amax};
+  const size_t words[6] = {(size_t)s.H, (size_t)s.QKV,
+                           (size_t)s.NKV * h->nsplit_max * s.GQA * (s.D + 2), (size_t)s.QD, (size_t)s.F,
+                           (size_t)2 * h->G};
   for (int i = 0; i < 6; ++i) {
     h->tagged_bytes[i] = words[i] * 8;
     HIPCHK(hipMalloc(tagged[i], h->tagged_bytes[i]), -1);
@@ -214,7 +211,7 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   }
   h->max_launch_tokens = 1 << 20;
   HIPCHK(hipMalloc(&h->out_tokens, (size_t)h->max_launch_tokens * 4), -1);
-  HIPCHK(hipMalloc(&h->trace, (size_t)(5 * h->L + 1) * 2 * h->G * 8), -1);
+  HIPCHK(hipMalloc(&h->trace, ((size_t)(5 * h->L + 1) * 2 + EVT_N) * h->G * 8), -1);
   HIPCHK(hipMalloc(&h->err, 256), -1);
   HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
   HIPCHK(hipMalloc(&h->dbg_layers, (size_t)(h->L + 1) * s.H * 4), -1);
@@ -304,7 +301,7 @@ static int check_occupancy(Handle* h) {
 
 // Clear every tagged word (tag 0 is never expected) and the error word.
 static int clear_tagged_state(Handle* h) {
-  u64* bufs[6] = {h->x, h->qkv, h->part_ml, h->part_acc, h->act, h->amax};
+  u64* bufs[6] = {h->x, h->qkv, h->part, h->attn, h->act, h->amax};
   for (int i = 0; i < 6; ++i) HIPCHK(hipMemsetAsync(bufs[i], 0, h->tagged_bytes[i], h->stream), -1);
   HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
@@ -338,14 +335,15 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   }
   p.x = h->x;
   p.qkv = h->qkv;
-  p.part_ml = h->part_ml;
-  p.part_acc = h->part_acc;
+  p.part = h->part;
+  p.attn = h->attn;
   p.act = h->act;
   p.amax = h->amax;
   p.out_tokens = h->out_tokens;
   p.err = h->err;
   p.trace = trace_token >= 0 ? h->trace : nullptr;
   p.trace_token = trace_token;
+  p.trace_layer = h->L / 2;
   p.dbg_layers = debug ? h->dbg_layers : nullptr;
   p.dbg_logits = debug ? h->dbg_logits : nullptr;
   p.inv_freq = h->inv_freq;
@@ -573,7 +571,7 @@ int megakernel_trace_generate(void* handle, int first_token, int n, int trace_to
     mk::set_err("invalid trace arguments");
     return -1;
   }
-  const size_t bytes = (size_t)(5 * h->L + 1) * 2 * h->G * 8;
+  const size_t bytes = ((size_t)(5 * h->L + 1) * 2 + mk::EVT_N) * h->G * 8;
   if (hipMemsetAsync(h->trace, 0, bytes, h->stream) != hipSuccess) {
     mk::set_err("trace clear failed");
     return -1;
@@ -583,7 +581,7 @@ int megakernel_trace_generate(void* handle, int first_token, int n, int trace_to
     mk::set_err("trace copy failed");
     return -1;
   }
-  return (5 * h->L + 1) * 2 * h->G;
+  return ((5 * h->L + 1) * 2 + mk::EVT_N) * h->G;
 }
 
 float megakernel_last_kernel_ms(void* handle) {
@@ -598,8 +596,8 @@ int megakernel_grid_size(void* handle) {
 
 int megakernel_set_attention_chunk(void* handle, int chunk_min) {
   Handle* h = static_cast<Handle*>(handle);
-  if (!h || chunk_min < 1 || (long long)chunk_min > mk::CHUNK_MAX) {
-    mk::set_err("attention chunk %d outside [1, %d]", chunk_min, mk::CHUNK_MAX);
+  if (!h || chunk_min < 1) {
+    mk::set_err("attention chunk %d must be >= 1", chunk_min);
     return -1;
   }
   h->chunk_min = chunk_min;

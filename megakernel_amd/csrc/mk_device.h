@@ -42,6 +42,25 @@ __device__ __forceinline__ float dot8(u32x4 w, const float* h, float acc) {
 
 __device__ __forceinline__ u32x4 ld_nt(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
+// Raw buffer loads: a wave-uniform base in a buffer descriptor (SGPRs), a
+// 32-bit per-lane byte offset (one VGPR shared by every load of a stream) and
+// a wave-uniform byte offset (SGPR).  Streamed loads then carry no per-load
+// 64-bit address registers.  Dword 3 selects 32-bit raw data for gfx9-class
+// descriptors; out-of-range offsets (>= num_records) read as zero.
+// The base must be wave-uniform; it is passed through readfirstlane so the
+// descriptor is built in SGPRs (otherwise each load becomes a waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+  void* ub = reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, 0x7fffffff, 0x00020000);
+}
+// Non-temporal 16-byte load at base + voff + soff.
+__device__ __forceinline__ u32x4 buf_ld_nt(__amdgpu_buffer_rsrc_t rs, unsigned voff, unsigned soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 2);
+}
+
 // Returns v unchanged but opaque to the optimiser.  Values derived from it
 // cannot be hoisted above this point, which keeps loop-invariant per-lane
 // addresses of later phases from being held in registers across the whole
@@ -50,6 +69,20 @@ __device__ __forceinline__ int opaque_v(int v) {
   asm volatile("" : "+v"(v));
   return v;
 }
+
+// The thread index, opaque to the optimiser (see opaque_v): every helper that
+// derives per-lane addresses reads it through here, so those addresses are
+// recomputed where they are used instead of living in registers across the
+// whole persistent loop.
+__device__ __forceinline__ int ltid() { return opaque_v((int)threadIdx.x); }
+
+// Wave index as a wave-uniform (scalar) value and the lane index.  Loads are
+// written as  uniform_base + (unsigned)lane_offset  so the compiler can use the
+// SGPR-base + 32-bit VGPR-offset form: prefetched loads then need no per-load
+// 64-bit address registers, which would otherwise alias the destinations of
+// loads still in flight and force a wait before the next load is issued.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave); }
+__device__ __forceinline__ unsigned lane_id() { return (unsigned)opaque_v((int)threadIdx.x) & (kWave - 1u); }
 
 // ------------------------------------------------------------ reductions
 __device__ __forceinline__ float wave_sum(float v) {
@@ -68,7 +101,7 @@ __device__ __forceinline__ float wave_max(float v) {
 template <int NW>
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
-  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
   if (l == 0) red[w] = v;
   __syncthreads();
   float s = 0.f;
@@ -80,7 +113,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 template <int NW>
 __device__ __forceinline__ float block_max(float v, float* red) {
   v = wave_max(v);
-  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
   if (l == 0) red[w] = v;
   __syncthreads();
   float s = red[0];
@@ -186,7 +219,7 @@ __device__ __forceinline__ bool ll_fetch(u64* src, int n, unsigned tag, float* d
       bool ready = true;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        const int i = base + b * NT + (int)threadIdx.x;
+        const int i = base + b * NT + ltid();
         if (i < n) {
           w[b] = ll_get(src + i);
           ready = ready && ll_tag(w[b]) == tag;
@@ -201,7 +234,7 @@ __device__ __forceinline__ bool ll_fetch(u64* src, int n, unsigned tag, float* d
     if (!failed) {
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        const int i = base + b * NT + (int)threadIdx.x;
+        const int i = base + b * NT + ltid();
         if (i < n) dst[i] = ll_val(w[b]);
       }
     }

@@ -10,15 +10,21 @@
 //     P5  down GEMV -> x[rows] += d[rows]                         row-block owners
 //   final rmsnorm -> tied LM head -> per-workgroup argmax -> next token
 //
-// There is no grid barrier.  Each phase instance has a global number (its
-// tag); every activation word carries the tag of the phase that wrote it, and
-// a consumer waits for exactly the words it reads (tagged dataflow, see
-// mk_device.h).  Every residual element has exactly one writer per phase (the
-// owner of its 16-row block), so there is no read-modify-write race on x
-// (unlike megakernel.cu:243-245,288-290), and the per-token tags make the
+// Synchronisation: there is no grid barrier.  Each phase instance has a
+// global number (its tag); every activation word carries the tag of the phase
+// that wrote it, and a consumer waits for exactly the words it reads (tagged
+// dataflow, see mk_device.h).  Every residual element has exactly one writer
+// per phase (the owner of its 16-row block), so there is no read-modify-write
+// race on x (unlike megakernel.cu:243-245,288-290), and per-token tags make the
 // reference's never-re-armed KV flag problem (barriers.cuh:112-134)
 // impossible.  Buffers are single-buffered: every write of a buffer depends
 // (through the phase chain) on every read of its previous contents.
+//
+// Streaming: weights do not depend on activations, so each workgroup issues
+// the loads of its NEXT phase's weight slice (and, one phase ahead of the
+// attention, its K/V slice) into registers right after its current inputs
+// arrive, and computes the current phase from registers loaded one phase
+// earlier.  The wait for the next inputs therefore overlaps the HBM transfer.
 #pragma once
 #include "mk_config.h"
 #include "mk_device.h"
@@ -27,9 +33,9 @@ namespace mk {
 
 constexpr int NT = 512;               // threads per workgroup (8 waves)
 constexpr int NW = NT / kWave;
-constexpr int CHUNK_MAX = 2048;       // max positions per attention work item
 constexpr int PHASES_PER_LAYER = 5;
-constexpr int ML_CAP = 1024;          // LDS floats for split (max, sum): nsplit_max * NQ * 2
+constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
+constexpr int KV_ROWS = 4;            // K/V register rows per lane per attention sub-chunk
 constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
 __device__ __forceinline__ unsigned tag14(unsigned tag) { return tag % 16383u + 1u; }
 constexpr int IDX_BITS = 18;          // ... and an 18-bit vocabulary index
@@ -43,15 +49,18 @@ struct Params {
   uint16_t* kv;               // [L][2][NKV][max_seq][D] bf16
   u64* x;                     // [H] residual stream (tagged)
   u64* qkv;                   // [QKV] projections of the current layer (tagged)
-  u64* part_ml;               // [nsplit_max][NQ][2] split max / sum (tagged)
-  u64* part_acc;              // [nsplit_max][NQ][D] split unnormalised outputs (tagged)
+  u64* part;                  // [NKV][nsplit_max][GQA*(D+2)] split partials (tagged):
+                              //   m[GQA], l[GQA], acc[GQA][D] (unnormalised)
+  u64* attn;                  // [QD] merged attention output (tagged)
   u64* act;                   // [F] silu(gate)*up (tagged)
   u64* amax;                  // [2][G] per-workgroup argmax words (token parity)
   int* out_tokens;            // [n_tokens]
   int* err;                   // error word
   float* dbg_layers;          // optional [(L+1)][H]: embedding, then x after each layer
   float* dbg_logits;          // optional [V]
-  u64* trace;                 // optional [(5L+1)][2][G] wall-clock ready/done per phase
+  u64* trace;                 // optional [(5L+1)][2][G] wall-clock ready/done per phase,
+                              // then [EVT_N][G] events of layer trace_layer
+  int trace_layer;
   const float* inv_freq;      // [D/2] RoPE inverse frequencies
   u64 timeout_ticks;
   unsigned tag_base;          // tag of the first phase of this launch
@@ -67,17 +76,15 @@ struct Smem {
   float vec[VEC];                     // GEMV input vector
   float xin[S::H];                    // residual stream as read
   float red[2 * NW * 16];             // GEMV cross-wave partials
-  float qk[(S::GQA + 1) * S::D];      // q heads, then k (normed + rotated in place)
-  float vv[S::D];                     // v of the current position
+  float qk[(S::GQA + 2) * S::D];      // q heads, k, v of the current position
   u32x4 kvcur[2][S::D / 8];           // bf16 K/V of the current position
-  float sc[S::GQA * CHUNK_MAX];       // attention scores / probabilities
-  float pv[NW * S::GQA * S::D];       // attention P*V cross-wave partials
-  float ml[ML_CAP];                    // merge: per split/head (max, sum) -> (scale)
-  float hl[S::NQ];                    // merge: per head 1 / total sum
+  float pv[NW * S::GQA * S::D];       // attention: per-wave unnormalised outputs
+  float mw[NW * S::GQA], lw[NW * S::GQA];  // attention: per-wave max / sum
+  float gm[S::GQA], gl[S::GQA];       // this item's (max, sum) per q head
+  float mbuf[(NSPLIT_CAP - 1) * S::GQA * (S::D + 2)];  // other splits' partials (merger)
+  float xres[16];                     // residual rows of this workgroup's O / down block
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
-  float scratch[4 * NW];
   u64 amax[NW];
-  int flag;
 };
 
 // Element `col` of row `row` of a packed [R][K] matrix (K = 32 * KT).
@@ -89,107 +96,82 @@ __device__ __forceinline__ float packed_elem(const u32x4* base, int row, int col
   return bf16_to_f32(u[e]);
 }
 
-// y[r] = sum_k W[rb*16 + r][k] * vec[k] for one packed 16-row block.  Wave w
-// takes k-tiles w, w+NW, ...; lane l covers row l & 15 and columns
-// (l >> 4) * 8 .. +8 of each tile.  Result valid in threads 0..15.
+// ------------------------------------------------------------------ GEMV
+// One packed 16-row block: wave w holds k-tiles w, w+NW, ...; lane l covers
+// row l & 15 and columns (l >> 4) * 8 .. +8 of each tile.
 template <int KT>
-__device__ __forceinline__ float gemv16(const u32x4* __restrict__ tiles, const float* vec, float* red) {
-  const int w = threadIdx.x / kWave, l = opaque_v(threadIdx.x % kWave);
-  constexpr int PER = (KT + NW - 1) / NW;
-  u32x4 wv[PER];
+struct Blk {
+  static constexpr int PER = (KT + NW - 1) / NW;
+  u32x4 w[PER];
+};
+
+template <int KT>
+__device__ __forceinline__ void blk_load(Blk<KT>& b, const u32x4* __restrict__ tiles) {
+  const int w = wave_id();
+  const unsigned lb = lane_id() * 16u;
+  const auto rs = make_rsrc(tiles);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int kt = w + i * NW;
-    if (kt < KT) wv[i] = ld_nt(tiles + kt * 64 + l);
+  for (int i = 0; i < Blk<KT>::PER; ++i) {
+    const unsigned so = (unsigned)(w + i * NW) * 1024u;  // k-tile of this wave, bytes
+    if constexpr (KT % NW == 0) {
+      b.w[i] = buf_ld_nt(rs, lb, so);
+    } else if (w + i * NW < KT) {
+      b.w[i] = buf_ld_nt(rs, lb, so);
+    }
   }
-  float acc = 0.f;
+}
+
+// Per-lane partial dot product of the block against vec (LDS).
+template <int KT>
+__device__ __forceinline__ float blk_dot(const Blk<KT>& b, const float* vec) {
+  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
   const float* hv = vec + (l >> 4) * 8;
+  float acc = 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
+  for (int i = 0; i < Blk<KT>::PER; ++i) {
     const int kt = w + i * NW;
-    if (kt < KT) acc = dot8(wv[i], hv + kt * 32, acc);
+    if (KT % NW == 0 || kt < KT) acc = dot8(b.w[i], hv + kt * 32, acc);
   }
   acc += __shfl_xor(acc, 16);
   acc += __shfl_xor(acc, 32);
-  if (l < 16) red[w * 16 + l] = acc;
+  return acc;
+}
+
+// Cross-wave sum of per-wave row partials: red[w*16 + r] -> threads 0..15.
+__device__ __forceinline__ float rows_sum(float part, float* red) {
+  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
+  if (l < 16) red[w * 16 + l] = part;
   __syncthreads();
   float y = 0.f;
-  if (threadIdx.x < 16) {
+  if (t_ < 16) {
 #pragma unroll
-    for (int i = 0; i < NW; ++i) y += red[i * 16 + threadIdx.x];
+    for (int i = 0; i < NW; ++i) y += red[i * 16 + t_];
   }
-  __syncthreads();
   return y;
 }
 
-// Two blocks (gate and up) against the same input vector.
-template <int KT>
-__device__ __forceinline__ void gemv16x2(const u32x4* __restrict__ ta, const u32x4* __restrict__ tb,
-                                         const float* vec, float* red, float& ya, float& yb) {
-  const int w = threadIdx.x / kWave, l = opaque_v(threadIdx.x % kWave);
-  constexpr int PER = (KT + NW - 1) / NW;
-  u32x4 wa[PER], wb[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int kt = w + i * NW;
-    if (kt < KT) {
-      wa[i] = ld_nt(ta + kt * 64 + l);
-      wb[i] = ld_nt(tb + kt * 64 + l);
-    }
-  }
-  float a = 0.f, b = 0.f;
-  const float* hv = vec + (l >> 4) * 8;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int kt = w + i * NW;
-    if (kt < KT) {
-      a = dot8(wa[i], hv + kt * 32, a);
-      b = dot8(wb[i], hv + kt * 32, b);
-    }
-  }
-  a += __shfl_xor(a, 16);
-  a += __shfl_xor(a, 32);
-  b += __shfl_xor(b, 16);
-  b += __shfl_xor(b, 32);
-  if (l < 16) {
-    red[w * 16 + l] = a;
-    red[NW * 16 + w * 16 + l] = b;
-  }
-  __syncthreads();
-  ya = 0.f;
-  yb = 0.f;
-  if (threadIdx.x < 16) {
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      ya += red[i * 16 + threadIdx.x];
-      yb += red[NW * 16 + i * 16 + threadIdx.x];
-    }
-  }
-  __syncthreads();
+// The two bf16 gains of elements 2t, 2t+1 of an H-vector, loaded before the
+// phase's input wait so the load is never on the critical path.
+template <class S>
+__device__ __forceinline__ unsigned gain_pair(const uint16_t* gain) {
+  static_assert(S::H <= 2 * NT, "two elements per thread");
+  const int t_ = ltid();
+  return t_ < S::H / 2 ? reinterpret_cast<const unsigned*>(gain)[t_] : 0u;
 }
 
-// out[i] = v[i] * rsqrt(mean(v^2) + eps) * gain[i]  (reference rmsnorm.cuh:87-108).
-// The source is the residual stream in LDS, or (layer 0) the embedding row.
+// out[i] = xl[i] * rsqrt(mean(xl^2) + eps) * gain[i] (reference rmsnorm.cuh:87-108).
+// Every wave computes the sum of squares itself from LDS (no block reduction).
 template <class S>
-__device__ __forceinline__ void rmsnorm_to(Smem<S>& sm, const float* xl, const u32x4* emb, int tok,
-                                           const uint16_t* gain, float* out) {
-  constexpr int VPT = (S::H + NT - 1) / NT;
-  float v[VPT];
+__device__ __forceinline__ void rmsnorm_lds(const float* xl, unsigned gp, float* out) {
+  const int t_ = ltid(), l = t_ % kWave;
   float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < VPT; ++c) {
-    const int i = threadIdx.x + c * NT;
-    float t = 0.f;
-    if (i < S::H) t = emb ? packed_elem<S::KT_H>(emb, tok, i) : xl[i];
-    v[c] = t;
-    ss = fmaf(t, t, ss);
-  }
-  ss = block_sum<NW>(ss, sm.scratch);
+#pragma unroll 4
+  for (int i = l; i < S::H; i += kWave) ss = fmaf(xl[i], xl[i], ss);
+  ss = wave_sum(ss);
   const float r = rsqrtf(ss / (float)S::H + kRmsEps);
-#pragma unroll
-  for (int c = 0; c < VPT; ++c) {
-    const int i = threadIdx.x + c * NT;
-    if (i < S::H) out[i] = v[c] * r * bf16_to_f32(gain[i]);
+  if (t_ < S::H / 2) {
+    out[2 * t_] = xl[2 * t_] * r * bf16_lo(gp);
+    out[2 * t_ + 1] = xl[2 * t_ + 1] * r * bf16_hi(gp);
   }
   __syncthreads();
 }
@@ -200,65 +182,234 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 __device__ __forceinline__ int first_item(int wg, int off, int G) { return (wg + G - (off % G)) % G; }
 
 __device__ __forceinline__ void trace_mark(const Params& p, int t, int slot, int which) {
-  if (p.trace && t == p.trace_token && threadIdx.x == 0)
+  if (p.trace && t == p.trace_token && ltid() == 0)
     p.trace[((long long)slot * 2 + which) * gridDim.x + blockIdx.x] = wall_clock64();
 }
 
-// ---------------------------------------------------------------- phase P2
-// One attention work item: kv head g, positions [s*chunk, min((s+1)*chunk, pos+1)).
+// Fine-grained events of one layer of the traced token.
+constexpr int EVT_N = 16;
+enum Evt : int {
+  EV_ATT_READY = 0, EV_ATT_ROPE, EV_ATT_SOFTMAX, EV_ATT_STORED,
+  EV_ATT_PARTIAL, EV_ATT_GATHERED, EV_O_READY, EV_O_STORED,
+  EV_QKV_STORED, EV_GU_STORED, EV_DN_STORED, EV_DN_READY
+};
+__device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
+  if (p.trace && t == p.trace_token && layer == p.trace_layer && ltid() == 0)
+    p.trace[((long long)(5 * p.n_layers + 1) * 2 + e) * gridDim.x + blockIdx.x] = wall_clock64();
+}
+
+// --------------------------------------------------------- tagged fetches
+// Wait until every word of up to three ranges carries its range's tag and copy
+// the values to LDS.  Waiting is two-level so that idle consumers do not flood
+// the memory system: wave 0 polls one sentinel word per producer block (every
+// `ss`-th word of a range) until all carry the tag, then the whole workgroup
+// reads the ranges once, re-polling only if some word is still stale (values
+// and tags of different words become visible in no particular order).
+struct Range {
+  u64* src;
+  int n;
+  float* dst;
+  unsigned tag;
+  int ss;  // sentinel stride (words per producer block)
+};
+
+__device__ __forceinline__ int range_sentinels(const Range& r) { return r.n > 0 ? (r.n + r.ss - 1) / r.ss : 0; }
+
+template <int B>
+__device__ __forceinline__ bool fetch3(Range a, Range b, Range c, const Params& p) {
+  const int tid = ltid();
+  int failed = 0;
+  // 1. light wait on sentinels (wave 0 only), for inputs over 2 words a thread
+  if (a.n + b.n + c.n > 2 * NT && tid < kWave) {
+    const int na = range_sentinels(a), nb = range_sentinels(b), nc = range_sentinels(c);
+    const int ns = na + nb + nc;
+    Spin sp;
+    for (int base = 0; base < ns && !failed;) {
+      bool ready = true;
+      for (int i = base + tid; i < ns && i < base + 4 * kWave; i += kWave) {
+        u64* s;
+        unsigned tg;
+        if (i < na) { s = a.src + i * a.ss; tg = a.tag; }
+        else if (i < na + nb) { s = b.src + (i - na) * b.ss; tg = b.tag; }
+        else { s = c.src + (i - na - nb) * c.ss; tg = c.tag; }
+        ready = ready && ll_tag(ll_get(s)) == tg;
+      }
+      // every lane must see its sentinels ready before the window advances
+      if (__all(ready)) {
+        base += 4 * kWave;
+        continue;
+      }
+      if (!sp.step(p.err, p.timeout_ticks)) failed = 1;
+    }
+  }
+  if (__syncthreads_or(failed)) return false;
+  // 2. bulk read with verification
+  const int total = a.n + b.n + c.n;
+  for (int base = 0; base < total && !failed; base += NT * B) {
+    u64 wv[B];
+    Spin sp;
+    while (true) {
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        int i = base + k * NT + tid;
+        if (i < total) {
+          u64* s = i < a.n ? a.src + i : (i < a.n + b.n ? b.src + (i - a.n) : c.src + (i - a.n - b.n));
+          const unsigned tg = i < a.n ? a.tag : (i < a.n + b.n ? b.tag : c.tag);
+          wv[k] = ll_get(s);
+          ready = ready && ll_tag(wv[k]) == tg;
+        }
+      }
+      if (ready) break;
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    }
+    if (!failed) {
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        int i = base + k * NT + tid;
+        if (i < total) {
+          float* d = i < a.n ? a.dst + i : (i < a.n + b.n ? b.dst + (i - a.n) : c.dst + (i - a.n - b.n));
+          *d = ll_val(wv[k]);
+        }
+      }
+    }
+  }
+  return __syncthreads_or(failed) == 0;
+}
+
+constexpr Range kNoRange = {nullptr, 0, nullptr, 0u, 1};
+
+template <int B>
+__device__ __forceinline__ bool fetch1(u64* src, int n, float* dst, unsigned tag, const Params& p, int ss = 16) {
+  return fetch3<B>(Range{src, n, dst, tag, ss}, kNoRange, kNoRange, p);
+}
+
+// Light wait only (wave 0 polls the sentinels of one range); no data copied.
+__device__ __forceinline__ bool await_sentinels(u64* src, int n, int ss, unsigned tag, const Params& p) {
+  const int tid = ltid();
+  int failed = 0;
+  if (tid < kWave) {
+    const int ns = (n + ss - 1) / ss;
+    Spin sp;
+    for (int base = 0; base < ns && !failed;) {
+      bool ready = true;
+      for (int i = base + tid; i < ns && i < base + 4 * kWave; i += kWave) ready = ready && ll_tag(ll_get(src + i * ss)) == tag;
+      if (__all(ready)) {
+        base += 4 * kWave;
+        continue;
+      }
+      if (!sp.step(p.err, p.timeout_ticks)) failed = 1;
+    }
+  }
+  return __syncthreads_or(failed) == 0;
+}
+
+// ------------------------------------------------------------ attention
+// Work item (kv head g, split s) covers positions [t0, t1).  Lane l of wave w
+// handles dims (l % LPP) * 8 .. +8 of position t0 + sub*SUB + r*NW*PPW + w*PPW + l/LPP.
 template <class S>
-__device__ bool attention_item(const Params& p, Smem<S>& sm, int layer, int pos, int g, int s, int chunk,
-                               unsigned tag_in, unsigned tag_out) {
-  constexpr int D = S::D, GQA = S::GQA, LPP = D / 8, PPW = kWave / LPP;
-  const int tid = threadIdx.x, w = tid / kWave, l = opaque_v(tid % kWave);
-  const int n = pos + 1;
-  // splits are never empty (nsplit = ceil(n / chunk)), so every item reads
-  // its group's q/k/v before writing: no item can overwrite partials that an
-  // O-projection owner of the previous layer is still merging.
-  const int t0 = s * chunk, t1 = min(n, t0 + chunk);
-  u64* mlw = p.part_ml + ((long long)s * S::NQ + g * GQA) * 2;
-  u64* accw = p.part_acc + ((long long)s * S::NQ + g * GQA) * D;
-  // inputs: the group's q heads, its k and v rows
-  if (!ll_fetch<NT, 1>(p.qkv + g * GQA * D, GQA * D, tag_in, sm.qk, p.err, p.timeout_ticks)) return false;
-  if (!ll_fetch<NT, 1>(p.qkv + S::QD + g * D, D, tag_in, sm.qk + GQA * D, p.err, p.timeout_ticks)) return false;
-  if (!ll_fetch<NT, 1>(p.qkv + S::QD + S::KVD + g * D, D, tag_in, sm.vv, p.err, p.timeout_ticks)) return false;
+struct KV {
+  static constexpr int LPP = S::D / 8, PPW = kWave / LPP, SUB = KV_ROWS * NW * PPW;
+  u32x4 k[KV_ROWS], v[KV_ROWS];
+  uint16_t gn[S::D / kWave];  // QK-norm gain(s) of this lane's dim(s) for its wave's head
+};
+
+template <class S>
+__device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, int g, int t0, int t1, int pos,
+                                        int sub) {
+  constexpr int D = S::D, LPP = KV<S>::LPP, PPW = KV<S>::PPW;
+  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
+  const int c = l % LPP, po = l / LPP;
+  const uint16_t* kb = p.kv + ((long long)(layer * 2 + 0) * S::NKV + g) * (long long)p.max_seq * D + c * 8;
+  const uint16_t* vb = p.kv + ((long long)(layer * 2 + 1) * S::NKV + g) * (long long)p.max_seq * D + c * 8;
+  // Rows past the split, and `pos` itself (taken from LDS), load position
+  // (pos + 1) mod max_seq instead -- settled data nobody writes during this
+  // token -- and are zeroed, so every lane issues the same unconditional loads.
+  const int tsafe = (pos + 1) % p.max_seq;
+  const auto rk = make_rsrc(kb), rv = make_rsrc(vb);
+  u32x4 kk[KV_ROWS], vv[KV_ROWS];
+  bool ok[KV_ROWS];
+#pragma unroll
+  for (int i = 0; i < KV_ROWS; ++i) {
+    const int t = t0 + sub * KV<S>::SUB + i * NW * PPW + w * PPW + po;
+    ok[i] = (t < t1 && t != pos);
+    const unsigned ta = (unsigned)(ok[i] ? t : tsafe);
+    // byte offset from the uniform (layer, head) base: position * D + dim chunk
+    const unsigned off = (ta * (unsigned)D + (unsigned)c * 8u) * 2u;
+    kk[i] = buf_ld_nt(rk, off, 0u);
+    vv[i] = buf_ld_nt(rv, off, 0u);
+  }
+#pragma unroll
+  for (int i = 0; i < KV_ROWS; ++i) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    r.k[i] = ok[i] ? kk[i] : z;
+    r.v[i] = ok[i] ? vv[i] : z;
+  }
+}
+
+// QK-norm gains of this lane's dims: waves 0..GQA-1 normalise q heads, wave
+// GQA the k head.
+template <class S>
+__device__ __forceinline__ void gain_load_qk(KV<S>& r, const Params& p, int layer) {
+  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
+  const uint16_t* g = p.norms + (long long)layer * S::NORM_STRIDE + (w < S::GQA ? S::NORM_Q : S::NORM_K);
+#pragma unroll
+  for (int c = 0; c < S::D / kWave; ++c) r.gn[c] = g[l + c * kWave];
+}
+
+// Inputs are already fetched into sm.qk (q heads | k | v).  Writes the split's
+// (max, sum, unnormalised output) words for the GQA heads of group g.
+template <class S>
+__device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int layer, int pos, int g, int s,
+                                  int nsplit, int t0, int t1, unsigned tag_out, int tt) {
+  constexpr int D = S::D, GQA = S::GQA, LPP = KV<S>::LPP, PPW = KV<S>::PPW, DPL = D / kWave;
+  const int tid = ltid(), w = tid / kWave, l = tid % kWave;
   const uint16_t* nrm = p.norms + (long long)layer * S::NORM_STRIDE;
-  // 1. per-head RMSNorm of the q heads and the k head (reference
-  //    rmsnorm.cuh:57-84); one wave per head.
-  if (w < GQA + 1) {
-    const uint16_t* gain = nrm + (w < GQA ? S::NORM_Q : S::NORM_K);
-    float v[D / kWave];
+  // 1. per-head RMSNorm (reference rmsnorm.cuh:57-84) + RoPE rotate-half
+  //    (attention.cuh:22-44) of the q heads and the k head, one wave per head,
+  //    in registers; lane l holds dims l + 64 c.
+  (void)nrm;
+  if (w <= GQA) {
+    float v[DPL];
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < D / kWave; ++c) {
+    for (int c = 0; c < DPL; ++c) {
       v[c] = sm.qk[w * D + l + c * kWave];
       ss = fmaf(v[c], v[c], ss);
     }
     ss = wave_sum(ss);
     const float r = rsqrtf(ss / (float)D + kRmsEps);
 #pragma unroll
-    for (int c = 0; c < D / kWave; ++c) sm.qk[w * D + l + c * kWave] = v[c] * r * bf16_to_f32(gain[l + c * kWave]);
+    for (int c = 0; c < DPL; ++c) v[c] = v[c] * r * bf16_to_f32(kvr.gn[c]);
+    float o[DPL];
+    if constexpr (DPL == 1) {  // partner of dim l is l ^ 32, in another lane
+      const float partner = __shfl_xor(v[0], 32);
+      const int d = l & 31;
+      o[0] = l < 32 ? v[0] * sm.rc[d] - partner * sm.rs[d] : v[0] * sm.rc[d] + partner * sm.rs[d];
+    } else {  // D = 128: dims l and l + 64 pair up in the same lane
+      o[0] = v[0] * sm.rc[l] - v[1] * sm.rs[l];
+      o[1] = v[1] * sm.rc[l] + v[0] * sm.rs[l];
+    }
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) sm.qk[w * D + l + c * kWave] = o[c];
   }
   __syncthreads();
-  // 2. RoPE, rotate-half pairs (d, d + D/2) (reference attention.cuh:22-44).
-  for (int e = tid; e < (GQA + 1) * (D / 2); e += NT) {
-    const int hh = e / (D / 2), d = e % (D / 2);
-    const float a = sm.qk[hh * D + d], b = sm.qk[hh * D + d + D / 2];
-    const float c = sm.rc[d], sn = sm.rs[d];
-    sm.qk[hh * D + d] = a * c - b * sn;
-    sm.qk[hh * D + d + D / 2] = b * c + a * sn;
-  }
-  __syncthreads();
+  // 2. bf16 K/V of the current position (reference kv_cache.cuh:58-78).  The
+  //    split that owns `pos` appends them to the cache (write-through
+  //    agent-scope stores, read by later tokens on any XCD); every split uses
+  //    the LDS copy for `pos`.
   uint16_t* kb = p.kv + ((long long)(layer * 2 + 0) * S::NKV + g) * (long long)p.max_seq * D;
   uint16_t* vb = p.kv + ((long long)(layer * 2 + 1) * S::NKV + g) * (long long)p.max_seq * D;
-  // 3. bf16 K/V of the current position (reference kv_cache.cuh:58-78); the
-  //    split that owns `pos` appends them to the cache with write-through
-  //    stores and uses its LDS copy for this token.
   const bool own = (t0 <= pos && pos < t1);
   if (tid < D / 2) {
     const int d = 2 * tid;
     const unsigned kw = (unsigned)f32_to_bf16(sm.qk[GQA * D + d]) | ((unsigned)f32_to_bf16(sm.qk[GQA * D + d + 1]) << 16);
-    const unsigned vw = (unsigned)f32_to_bf16(sm.vv[d]) | ((unsigned)f32_to_bf16(sm.vv[d + 1]) << 16);
+    const unsigned vw = (unsigned)f32_to_bf16(sm.qk[(GQA + 1) * D + d]) |
+                        ((unsigned)f32_to_bf16(sm.qk[(GQA + 1) * D + d + 1]) << 16);
+    if (tid == 0) evt(p, tt, layer, EV_ATT_ROPE);
     reinterpret_cast<unsigned*>(sm.kvcur[0])[tid] = kw;
     reinterpret_cast<unsigned*>(sm.kvcur[1])[tid] = vw;
     if (own) {
@@ -269,7 +420,7 @@ __device__ bool attention_item(const Params& p, Smem<S>& sm, int layer, int pos,
     }
   }
   __syncthreads();
-  // 4. scores s_j[t] = (q_j . K[t]) / sqrt(D); LPP lanes per position.
+  // 3. per-wave online softmax over this wave's positions (fp32); scale 1/sqrt(D).
   const float scale = 1.0f / sqrtf((float)D);
   const int c = l % LPP, po = l / LPP;
   float qr[GQA][8];
@@ -277,149 +428,185 @@ __device__ bool attention_item(const Params& p, Smem<S>& sm, int layer, int pos,
   for (int j = 0; j < GQA; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) qr[j][e] = sm.qk[j * D + c * 8 + e];
-  const int cnt = t1 - t0;
-  constexpr int U = 4;
-  for (int tb = t0 + w * PPW; tb < t1; tb += NW * PPW * U) {
-    u32x4 kk[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = tb + u * NW * PPW + po;
-      kk[u] = (t < t1 && t != pos) ? ld_nt(reinterpret_cast<const u32x4*>(kb + (long long)t * D + c * 8))
-                                   : sm.kvcur[0][c];
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = tb + u * NW * PPW + po;
-#pragma unroll
-      for (int j = 0; j < GQA; ++j) {
-        float d = dot8(kk[u], qr[j], 0.f);
-#pragma unroll
-        for (int m = LPP / 2; m >= 1; m >>= 1) d += __shfl_xor(d, m);
-        if (c == 0 && t < t1) sm.sc[j * CHUNK_MAX + (t - t0)] = d * scale;
-      }
-    }
-  }
-  __syncthreads();
-  // 5. softmax statistics of this split (fp32).
-  float mj[GQA], lj[GQA];
+  float m[GQA], lsum[GQA], acc[GQA][8];
 #pragma unroll
   for (int j = 0; j < GQA; ++j) {
-    float m = -INFINITY;
-    for (int i = tid; i < cnt; i += NT) m = fmaxf(m, sm.sc[j * CHUNK_MAX + i]);
-    mj[j] = block_max<NW>(m, sm.scratch);
-  }
-#pragma unroll
-  for (int j = 0; j < GQA; ++j) {
-    float sum = 0.f;
-    for (int i = tid; i < cnt; i += NT) {
-      const float e = __expf(sm.sc[j * CHUNK_MAX + i] - mj[j]);
-      sm.sc[j * CHUNK_MAX + i] = e;
-      sum += e;
-    }
-    lj[j] = block_sum<NW>(sum, sm.scratch);
-  }
-  // 6. acc_j = sum_t p_j[t] V[t]  (unnormalised).
-  float acc[GQA][8];
-#pragma unroll
-  for (int j = 0; j < GQA; ++j)
+    m[j] = -INFINITY;
+    lsum[j] = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-  for (int tb = t0 + w * PPW; tb < t1; tb += NW * PPW * U) {
-    u32x4 vk[U];
+  }
+  const int nsub = (t1 - t0 + KV<S>::SUB - 1) / KV<S>::SUB;
+  for (int sub = 0; sub < nsub; ++sub) {
+    if (sub > 0) kv_load<S>(kvr, p, layer, g, t0, t1, pos, sub);
+    float sc[GQA][KV_ROWS];
+    float mx[GQA];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = tb + u * NW * PPW + po;
-      vk[u] = (t < t1 && t != pos) ? ld_nt(reinterpret_cast<const u32x4*>(vb + (long long)t * D + c * 8))
-                                   : sm.kvcur[1][c];
+    for (int j = 0; j < GQA; ++j) mx[j] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < KV_ROWS; ++i) {
+      const int t = t0 + sub * KV<S>::SUB + i * NW * PPW + w * PPW + po;
+      const u32x4 kk = (t == pos) ? sm.kvcur[0][c] : kvr.k[i];
+#pragma unroll
+      for (int j = 0; j < GQA; ++j) {
+        float d = dot8(kk, qr[j], 0.f);
+#pragma unroll
+        for (int mm = LPP / 2; mm >= 1; mm >>= 1) d += __shfl_xor(d, mm);
+        sc[j][i] = (t < t1) ? d * scale : -INFINITY;
+        mx[j] = fmaxf(mx[j], sc[j][i]);
+      }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = tb + u * NW * PPW + po;
-      if (t < t1) {
-        float vf[8] = {bf16_lo(vk[u].x), bf16_hi(vk[u].x), bf16_lo(vk[u].y), bf16_hi(vk[u].y),
-                       bf16_lo(vk[u].z), bf16_hi(vk[u].z), bf16_lo(vk[u].w), bf16_hi(vk[u].w)};
+    for (int j = 0; j < GQA; ++j) {
+      const float mn = fmaxf(m[j], wave_max(mx[j]));
+      const float alpha = (m[j] == -INFINITY) ? 0.f : __expf(m[j] - mn);
+      lsum[j] *= alpha;
 #pragma unroll
-        for (int j = 0; j < GQA; ++j) {
-          const float pj = sm.sc[j * CHUNK_MAX + (t - t0)];
+      for (int e = 0; e < 8; ++e) acc[j][e] *= alpha;
+      m[j] = mn;
+    }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[e], acc[j][e]);
-        }
+    for (int i = 0; i < KV_ROWS; ++i) {
+      const int t = t0 + sub * KV<S>::SUB + i * NW * PPW + w * PPW + po;
+      const u32x4 vk = (t == pos) ? sm.kvcur[1][c] : kvr.v[i];
+      const float vf[8] = {bf16_lo(vk.x), bf16_hi(vk.x), bf16_lo(vk.y), bf16_hi(vk.y),
+                           bf16_lo(vk.z), bf16_hi(vk.z), bf16_lo(vk.w), bf16_hi(vk.w)};
+#pragma unroll
+      for (int j = 0; j < GQA; ++j) {
+        const float pj = (t < t1) ? __expf(sc[j][i] - m[j]) : 0.f;
+        lsum[j] += (c == 0) ? pj : 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[e], acc[j][e]);
       }
     }
   }
+  evt(p, tt, layer, EV_ATT_SOFTMAX);
+  // 4. per-wave partials -> LDS, then merge the NW waves.
 #pragma unroll
-  for (int j = 0; j < GQA; ++j)
+  for (int j = 0; j < GQA; ++j) {
+    lsum[j] = wave_sum(lsum[j]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v = acc[j][e];
 #pragma unroll
-      for (int m = LPP; m < kWave; m <<= 1) v += __shfl_xor(v, m);
+      for (int mm = LPP; mm < kWave; mm <<= 1) v += __shfl_xor(v, mm);
       acc[j][e] = v;
     }
+  }
   if (po == 0) {
 #pragma unroll
     for (int j = 0; j < GQA; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) sm.pv[(w * GQA + j) * D + c * 8 + e] = acc[j][e];
   }
-  __syncthreads();
-  for (int e = tid; e < GQA * D; e += NT) {
-    float v = 0.f;
+  if (l == 0) {
 #pragma unroll
-    for (int i = 0; i < NW; ++i) v += sm.pv[i * GQA * D + e];
-    ll_put(accw + e, ll_pack(v, tag_out));
+    for (int j = 0; j < GQA; ++j) {
+      sm.mw[w * GQA + j] = m[j];
+      sm.lw[w * GQA + j] = lsum[j];
+    }
   }
-  if (tid < GQA * 2) ll_put(mlw + tid, ll_pack((tid & 1) ? lj[tid >> 1] : mj[tid >> 1], tag_out));
+  __syncthreads();
+  // 5. this item's partial over its NW waves: (M, L, acc) per q head.
+  constexpr int W = GQA * (D + 2);
+  if (tid < GQA) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) M = fmaxf(M, sm.mw[i * GQA + tid]);
+    float Lw = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const float mi = sm.mw[i * GQA + tid];
+      if (mi != -INFINITY) Lw = fmaf(__expf(mi - M), sm.lw[i * GQA + tid], Lw);
+    }
+    sm.gm[tid] = M;
+    sm.gl[tid] = Lw;
+  }
+  float av[(GQA * D + NT - 1) / NT];
+#pragma unroll
+  for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
+    const int e = tid + k * NT;
+    av[k] = 0.f;
+    if (e < GQA * D) {
+      const int j = e / D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) M = fmaxf(M, sm.mw[i * GQA + j]);
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const float mi = sm.mw[i * GQA + j];
+        if (mi != -INFINITY) av[k] = fmaf(__expf(mi - M), sm.pv[i * GQA * D + e], av[k]);
+      }
+    }
+  }
+  __syncthreads();
+  u64* prow = p.part + ((long long)g * p.nsplit_max + s) * W;
+  if (s != 0) {  // publish the partial for this group's merger (split 0)
+    if (tid < GQA) {
+      ll_put(prow + tid, ll_pack(sm.gm[tid], tag_out));
+      ll_put(prow + GQA + tid, ll_pack(sm.gl[tid], tag_out));
+    }
+#pragma unroll
+    for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
+      const int e = tid + k * NT;
+      if (e < GQA * D) ll_put(prow + 2 * GQA + e, ll_pack(av[k], tag_out));
+    }
+    evt(p, tt, layer, EV_ATT_PARTIAL);
+    return true;
+  }
+  // 6. split 0 merges the group's other splits (log-sum-exp) and publishes the
+  //    normalised attention output of its GQA heads.
+  if (nsplit > 1 && !fetch1<8>(prow + W, (nsplit - 1) * W, sm.mbuf, tag_out, p, W)) return false;
+  evt(p, tt, layer, EV_ATT_GATHERED);
+#pragma unroll
+  for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
+    const int e = tid + k * NT;
+    if (e < GQA * D) {
+      const int j = e / D;
+      float M = sm.gm[j];
+      for (int q = 0; q < nsplit - 1; ++q) M = fmaxf(M, sm.mbuf[q * W + j]);
+      const float f0 = __expf(sm.gm[j] - M);
+      float Lt = f0 * sm.gl[j], o = f0 * av[k];
+      for (int q = 0; q < nsplit - 1; ++q) {
+        const float f = __expf(sm.mbuf[q * W + j] - M);
+        Lt = fmaf(f, sm.mbuf[q * W + GQA + j], Lt);
+        o = fmaf(f, sm.mbuf[q * W + 2 * GQA + e], o);
+      }
+      ll_put(p.attn + (long long)g * GQA * D + e, ll_pack(o / Lt, tag_out));
+    }
+  }
   return true;
 }
 
-// ---------------------------------------------------------------- phase P3
-// Merge the split partials of every q head (log-sum-exp) into vec[QD].
-template <class S>
-__device__ bool merge_attention(const Params& p, Smem<S>& sm, int nsplit, unsigned tag) {
-  constexpr int D = S::D, NQ = S::NQ;
-  if (!ll_fetch<NT, 2>(p.part_ml, nsplit * NQ * 2, tag, sm.ml, p.err, p.timeout_ticks)) return false;
-  if (threadIdx.x < NQ) {
-    const int h = threadIdx.x;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, sm.ml[(s * NQ + h) * 2]);
-    float L = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float f = __expf(sm.ml[(s * NQ + h) * 2] - M);
-      L = fmaf(f, sm.ml[(s * NQ + h) * 2 + 1], L);
-      sm.ml[(s * NQ + h) * 2] = f;  // becomes the split's scale
-    }
-    sm.hl[h] = 1.0f / L;
-  }
-  __syncthreads();
+// argmax over the G per-workgroup words of a token (tag t14): the token id.
+__device__ __forceinline__ bool token_from_slots(const Params& p, u64* slots, unsigned t14, u64* red, int* tok) {
+  const int G = gridDim.x, tid = ltid(), w = tid / kWave, l = tid % kWave;
   int failed = 0;
-  for (int e = threadIdx.x; e < S::QD && !failed; e += NT) {
-    const int h = e / D;
-    float o = 0.f;
-    for (int s0 = 0; s0 < nsplit && !failed; s0 += 8) {
-      u64 wv[8];
-      Spin sp;
-      while (true) {
-        bool ready = true;
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-          if (s0 + b < nsplit) {
-            wv[b] = ll_get(p.part_acc + (long long)(s0 + b) * S::QD + e);
-            ready = ready && ll_tag(wv[b]) == tag;
-          }
-        if (ready) break;
-        if (!sp.step(p.err, p.timeout_ticks)) {
-          failed = 1;
-          break;
-        }
+  u64 best = 0;
+  for (int i = tid; i < G && !failed; i += NT) {
+    Spin sp;
+    u64 v;
+    while (((v = ll_get(slots + i)) & TAG14) != t14)
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
       }
-#pragma unroll
-      for (int b = 0; b < 8; ++b)
-        if (s0 + b < nsplit) o = fmaf(sm.ml[((s0 + b) * NQ + h) * 2], ll_val(wv[b]), o);
-    }
-    sm.vec[e] = o * sm.hl[h];
+    best = v > best ? v : best;
   }
-  return __syncthreads_or(failed) == 0;
+  if (__syncthreads_or(failed)) return false;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const u64 o = __shfl_xor(best, m);
+    best = o > best ? o : best;
+  }
+  if (l == 0) red[w] = best;
+  __syncthreads();
+  best = red[0];
+  for (int i = 1; i < NW; ++i) best = red[i] > best ? red[i] : best;
+  __syncthreads();
+  const unsigned idx = IDX_MAX - (unsigned)((best >> 14) & IDX_MAX);
+  *tok = idx < (unsigned)p.vocab ? (int)idx : 0;
+  return true;
 }
 
 // ------------------------------------------------------------------ kernel
@@ -430,42 +617,31 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   const int w = tid / kWave, l = tid % kWave;
   const int L = p.n_layers;
   const unsigned per_token = (unsigned)(PHASES_PER_LAYER * L + 1);
-  // Phase -> workgroup offsets spread the per-layer byte load across CUs.
+  // Phase -> workgroup offsets spread the per-layer byte load across CUs:
+  // with 256 CUs, down (88 KiB) on 0..63, QKV (32 KiB) on 64..191, gate/up
+  // (64 KiB) on 64..239, O (32 KiB) on 192..255, attention from 0 upwards.
   const int off_qkv = G / 4, off_gu = G / 4, off_o = (3 * G) / 4, off_down = 0, off_att = 0;
+  const int it_qkv = first_item(wg, off_qkv, G), it_o = first_item(wg, off_o, G);
+  const int it_gu = first_item(wg, off_gu, G), it_dn = first_item(wg, off_down, G);
+  const int it_att = first_item(wg, off_att, G);
+
+  Blk<S::KT_H> rq;      // QKV block
+  KV<S> rkv;            // attention K/V sub-chunk
+  Blk<S::KT_Q> ro;      // O block
+  Blk<S::KT_H> rg, ru;  // gate / up blocks
+  Blk<S::KT_F> rd;      // down block
+  unsigned gq = 0, gf = 0;  // attn_norm / ffn_norm gain pairs of the current layer
 
   int tok = p.first_token;
   for (int t = 0; t < p.n_tokens; ++t) {
     const int pos = p.pos0 + t;
     const unsigned tb = p.tag_base + (unsigned)t * per_token;  // tag of this token's first phase
+    if (it_qkv < S::RB_QKV) {
+      blk_load(rq, p.layers + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
+      gq = gain_pair<S>(p.norms + S::NORM_ATTN);
+    }
     if (t > 0) {
-      // next token = argmax over every workgroup's word of the previous token
-      const unsigned want = tag14(tb - 1u);
-      u64* slots = p.amax + ((t - 1) & 1) * G;
-      int failed = 0;
-      u64 best = 0;
-      for (int i = tid; i < G && !failed; i += NT) {
-        Spin sp;
-        u64 v;
-        while (((v = ll_get(slots + i)) & TAG14) != want)
-          if (!sp.step(p.err, p.timeout_ticks)) {
-            failed = 1;
-            break;
-          }
-        best = v > best ? v : best;
-      }
-      if (__syncthreads_or(failed)) return;
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        const u64 o = __shfl_xor(best, m);
-        best = o > best ? o : best;
-      }
-      if (l == 0) sm.amax[w] = best;
-      __syncthreads();
-      best = sm.amax[0];
-      for (int i = 1; i < NW; ++i) best = sm.amax[i] > best ? sm.amax[i] : best;
-      __syncthreads();
-      const unsigned idx = IDX_MAX - (unsigned)((best >> 14) & IDX_MAX);
-      tok = idx < (unsigned)p.vocab ? (int)idx : 0;
+      if (!token_from_slots(p, p.amax + ((t - 1) & 1) * G, tag14(tb - 1u), sm.amax, &tok)) return;
       if (wg == 0 && tid == 0) p.out_tokens[t - 1] = tok;
     }
     if (tid < S::D / 2) {
@@ -477,123 +653,162 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     if (p.dbg_layers && wg == 0)
       for (int i = tid; i < S::H; i += NT) p.dbg_layers[i] = packed_elem<S::KT_H>(p.lmhead, tok, i);
     __syncthreads();
+    // attention split: nsplit <= nsplit_max items per kv head, none empty
     const int n = pos + 1;
     int ns0 = (n + p.chunk_min - 1) / p.chunk_min;
     ns0 = ns0 < 1 ? 1 : (ns0 > p.nsplit_max ? p.nsplit_max : ns0);
     const int chunk = (n + ns0 - 1) / ns0;
-    const int nsplit = (n + chunk - 1) / chunk;  // <= ns0, and no split is empty
+    const int nsplit = (n + chunk - 1) / chunk;
+    const bool has_att = it_att < S::NKV * nsplit;
+    const int ag = has_att ? it_att / nsplit : 0, as = has_att ? it_att % nsplit : 0;
+    const int at0 = as * chunk, at1 = min(n, at0 + chunk);
 
     for (int layer = 0; layer < L; ++layer) {
+      const int tid = ltid();
       const u32x4* wl = p.layers + (long long)layer * S::U_LAYER;
       const uint16_t* nrm = p.norms + (long long)layer * S::NORM_STRIDE;
       const unsigned tg = tb + (unsigned)(PHASES_PER_LAYER * layer);  // tag of P1 of this layer
       const unsigned tg_x = tg - 1u;  // tag of the x rows this layer starts from (layer > 0)
       const int slot = PHASES_PER_LAYER * layer;
-      // P1: QKV
-      {
-        bool have = false;
-        for (int rb = first_item(wg, off_qkv, G); rb < S::RB_QKV; rb += G) {
-          if (!have) {
-            if (layer > 0 && !ll_fetch<NT, 2>(p.x, S::H, tg_x, sm.xin, p.err, p.timeout_ticks)) return;
-            trace_mark(p, t, slot + 0, 0);
-            rmsnorm_to<S>(sm, sm.xin, layer == 0 ? p.lmhead : nullptr, tok, nrm + S::NORM_ATTN, sm.vec);
-            have = true;
-          }
-          const float y = gemv16<S::KT_H>(wl + S::OFF_QKV + (long long)rb * S::KT_H * 64, sm.vec, sm.red);
+      // ---------------- P1: QKV (prefetch: attention K/V + QK-norm gains)
+      if (it_qkv < S::RB_QKV) {
+        if (layer > 0 && !fetch1<2>(p.x, S::H, sm.xin, tg_x, p)) return;
+        trace_mark(p, t, slot + 0, 0);
+      }
+      if (has_att) {
+        kv_load<S>(rkv, p, layer, ag, at0, at1, pos, 0);
+        gain_load_qk<S>(rkv, p, layer);
+      }
+      if (it_qkv < S::RB_QKV) {
+        if (layer == 0) {
+          for (int i = tid; i < S::H; i += NT) sm.xin[i] = packed_elem<S::KT_H>(p.lmhead, tok, i);
+          __syncthreads();
+        }
+        rmsnorm_lds<S>(sm.xin, gq, sm.vec);
+        for (int rb = it_qkv, k = 0; rb < S::RB_QKV; rb += G, ++k) {
+          if (k > 0) blk_load(rq, wl + S::OFF_QKV + (long long)rb * S::KT_H * 64);
+          const float y = rows_sum(blk_dot(rq, sm.vec), sm.red);
           if (tid < 16) ll_put(p.qkv + rb * 16 + tid, ll_pack(y, tg));
+          if (k == 0) evt(p, t, layer, EV_QKV_STORED);
+          __syncthreads();
         }
-        if (have) trace_mark(p, t, slot + 0, 1);
+        trace_mark(p, t, slot + 0, 1);
       }
-      // P2: attention partials
-      {
-        bool any = false;
-        for (int it = first_item(wg, off_att, G); it < S::NKV * nsplit; it += G) {
-          if (!attention_item<S>(p, sm, layer, pos, it / nsplit, it % nsplit, chunk, tg, tg + 1u)) return;
-          if (!any) trace_mark(p, t, slot + 1, 0);
-          any = true;
+      // ---------------- P2: attention partials (prefetch: O)
+      if (has_att) {
+        const int D = S::D, GQA = S::GQA;
+        if (!fetch3<1>(Range{p.qkv + ag * GQA * D, GQA * D, sm.qk, tg, 16},
+                       Range{p.qkv + S::QD + ag * D, D, sm.qk + GQA * D, tg, 16},
+                       Range{p.qkv + S::QD + S::KVD + ag * D, D, sm.qk + (GQA + 1) * D, tg, 16}, p))
+          return;
+        trace_mark(p, t, slot + 1, 0);
+      }
+      if (it_o < S::RB_H) blk_load(ro, wl + S::OFF_O + (long long)it_o * S::KT_Q * 64);
+      if (has_att) {
+        evt(p, t, layer, EV_ATT_READY);
+        if (!attention_compute<S>(p, sm, rkv, layer, pos, ag, as, nsplit, at0, at1, tg + 1u, t)) return;
+        evt(p, t, layer, EV_ATT_STORED);
+        trace_mark(p, t, slot + 1, 1);
+      }
+      // ---------------- P3: O projection + residual (prefetch: gate/up + ffn gains)
+      if (it_o < S::RB_H) {
+        if (!fetch3<2>(Range{p.attn, S::QD, sm.vec, tg + 1u, 16},
+                       layer > 0 ? Range{p.x + it_o * 16, 16, sm.xres, tg_x, 16} : kNoRange, kNoRange, p))
+          return;
+        trace_mark(p, t, slot + 2, 0);
+        evt(p, t, layer, EV_O_READY);
+      }
+      if (it_gu < S::RB_F) {
+        const u32x4* gp = wl + S::OFF_GU + (long long)(2 * it_gu) * S::KT_H * 64;
+        blk_load(rg, gp);
+        blk_load(ru, gp + S::KT_H * 64);
+        gf = gain_pair<S>(nrm + S::NORM_FFN);
+      }
+      for (int rb = it_o, k = 0; rb < S::RB_H; rb += G, ++k) {
+        if (k > 0) {  // more blocks than workgroups: later blocks load now
+          blk_load(ro, wl + S::OFF_O + (long long)rb * S::KT_Q * 64);
+          if (layer > 0 && !fetch1<1>(p.x + rb * 16, 16, sm.xres, tg_x, p)) return;
         }
-        if (any) trace_mark(p, t, slot + 1, 1);
-      }
-      // P3: O projection + residual
-      {
-        bool have = false;
-        for (int rb = first_item(wg, off_o, G); rb < S::RB_H; rb += G) {
-          if (!have) {
-            if (!merge_attention<S>(p, sm, nsplit, tg + 1u)) return;
-            trace_mark(p, t, slot + 2, 0);
-            have = true;
-          }
-          const float y = gemv16<S::KT_Q>(wl + S::OFF_O + (long long)rb * S::KT_Q * 64, sm.vec, sm.red);
-          int failed = 0;
-          if (tid < 16) {
-            const int row = rb * 16 + tid;
-            float xo;
-            if (layer == 0) xo = packed_elem<S::KT_H>(p.lmhead, tok, row);
-            else failed = !ll_wait1(p.x + row, tg_x, &xo, p.err, p.timeout_ticks);
-            if (!failed) ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
-          }
-          if (__syncthreads_or(failed)) return;
+        const float y = rows_sum(blk_dot(ro, sm.vec), sm.red);
+        if (tid < 16) {
+          const int row = rb * 16 + tid;
+          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres[tid];
+          ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
         }
-        if (have) trace_mark(p, t, slot + 2, 1);
+        if (k == 0) evt(p, t, layer, EV_O_STORED);
+        __syncthreads();
+        if (k == 0) trace_mark(p, t, slot + 2, 1);
       }
-      // P4: gate/up + SiLU
-      {
-        bool have = false;
-        for (int pr = first_item(wg, off_gu, G); pr < S::RB_F; pr += G) {
-          if (!have) {
-            if (!ll_fetch<NT, 2>(p.x, S::H, tg + 2u, sm.xin, p.err, p.timeout_ticks)) return;
-            trace_mark(p, t, slot + 3, 0);
-            rmsnorm_to<S>(sm, sm.xin, nullptr, tok, nrm + S::NORM_FFN, sm.vec);
-            have = true;
+      // ---------------- P4: gate/up + SiLU (prefetch: down)
+      if (it_gu < S::RB_F) {
+        if (!fetch1<2>(p.x, S::H, sm.xin, tg + 2u, p)) return;
+        trace_mark(p, t, slot + 3, 0);
+      }
+      if (it_dn < S::RB_H) blk_load(rd, wl + S::OFF_DOWN + (long long)it_dn * S::KT_F * 64);
+      if (it_gu < S::RB_F) {
+        rmsnorm_lds<S>(sm.xin, gf, sm.vec);
+        for (int pr = it_gu, k = 0; pr < S::RB_F; pr += G, ++k) {
+          if (k > 0) {
+            const u32x4* gp = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
+            blk_load(rg, gp);
+            blk_load(ru, gp + S::KT_H * 64);
           }
-          float yg, yu;
-          const u32x4* tgp = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
-          gemv16x2<S::KT_H>(tgp, tgp + S::KT_H * 64, sm.vec, sm.red, yg, yu);
+          const float yg = rows_sum(blk_dot(rg, sm.vec), sm.red);
+          const float yu = rows_sum(blk_dot(ru, sm.vec), sm.red + NW * 16);
           if (tid < 16) ll_put(p.act + pr * 16 + tid, ll_pack(silu_mul(yg, yu), tg + 3u));
+          if (k == 0) evt(p, t, layer, EV_GU_STORED);
+          __syncthreads();
         }
-        if (have) trace_mark(p, t, slot + 3, 1);
+        trace_mark(p, t, slot + 3, 1);
       }
-      // P5: down projection + residual
-      {
-        bool have = false;
-        for (int rb = first_item(wg, off_down, G); rb < S::RB_H; rb += G) {
-          if (!have) {
-            if (!ll_fetch<NT, 6>(p.act, S::F, tg + 3u, sm.vec, p.err, p.timeout_ticks)) return;
-            trace_mark(p, t, slot + 4, 0);
-            have = true;
-          }
-          const float y = gemv16<S::KT_F>(wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64, sm.vec, sm.red);
-          int failed = 0;
-          if (tid < 16) {
-            const int row = rb * 16 + tid;
-            float xo;
-            failed = !ll_wait1(p.x + row, tg + 2u, &xo, p.err, p.timeout_ticks);
-            if (!failed) {
-              const float xn = xo + y;
-              ll_put(p.x + row, ll_pack(xn, tg + 4u));
-              if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
-            }
-          }
-          if (__syncthreads_or(failed)) return;
+      // ---------------- P5: down projection + residual (prefetch: next QKV + attn gains)
+      if (it_dn < S::RB_H) {
+        if (!fetch3<6>(Range{p.act, S::F, sm.vec, tg + 3u, 16}, Range{p.x + it_dn * 16, 16, sm.xres, tg + 2u, 16},
+                       kNoRange, p))
+          return;
+        trace_mark(p, t, slot + 4, 0);
+        evt(p, t, layer, EV_DN_READY);
+      }
+      if (layer + 1 < L && it_qkv < S::RB_QKV) {
+        blk_load(rq, wl + S::U_LAYER + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
+        gq = gain_pair<S>(nrm + S::NORM_STRIDE + S::NORM_ATTN);
+      }
+      for (int rb = it_dn, k = 0; rb < S::RB_H; rb += G, ++k) {
+        if (k > 0) {
+          blk_load(rd, wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64);
+          if (!fetch1<1>(p.x + rb * 16, 16, sm.xres, tg + 2u, p)) return;
         }
-        if (have) trace_mark(p, t, slot + 4, 1);
+        const float y = rows_sum(blk_dot(rd, sm.vec), sm.red);
+        if (tid < 16) {
+          const int row = rb * 16 + tid;
+          const float xn = sm.xres[tid] + y;
+          ll_put(p.x + row, ll_pack(xn, tg + 4u));
+          if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
+        }
+        if (k == 0) evt(p, t, layer, EV_DN_STORED);
+        __syncthreads();
+        if (k == 0) trace_mark(p, t, slot + 4, 1);
       }
     }
-    // Final norm + tied LM head + per-workgroup argmax (reference sampling.cuh:32-117).
+    // ---------------- final norm + tied LM head + per-workgroup argmax
+    // (reference sampling.cuh:32-117)
     {
+      const int tid = ltid(), w = tid / kWave, l = tid % kWave;
       const unsigned tl = tb + (unsigned)(PHASES_PER_LAYER * L);
-      if (!ll_fetch<NT, 2>(p.x, S::H, tl - 1u, sm.xin, p.err, p.timeout_ticks)) return;
+      const unsigned gfin = gain_pair<S>(p.final_norm);
+      if (!fetch1<2>(p.x, S::H, sm.xin, tl - 1u, p)) return;
       trace_mark(p, t, PHASES_PER_LAYER * L, 0);
-      rmsnorm_to<S>(sm, sm.xin, nullptr, tok, p.final_norm, sm.vec);
+      rmsnorm_lds<S>(sm.xin, gfin, sm.vec);
       const long long nb = p.vocab / 16;
       const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G;
       u64 best = 0ull;
-      for (long long b = b0 + w; b < b1; b += NW) {
+      const int wv_ = wave_id();
+      for (long long b = b0 + wv_; b < b1; b += NW) {
         // re-derived per block so the LDS reads of the hidden vector are not
         // hoisted out of the block loop (256 floats per lane would not fit)
-        const int lo = opaque_v(l);
+        const unsigned lo = lane_id();
         const float* hv = sm.vec + (lo >> 4) * 8;
-        const u32x4* tiles = p.lmhead + b * S::KT_H * 64 + lo;
+        const auto rs = make_rsrc(p.lmhead + b * S::KT_H * 64);  // wave-uniform block base
         float acc = 0.f;
         constexpr int U = 16;
 #pragma unroll 1
@@ -601,7 +816,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           u32x4 wv[U];
 #pragma unroll
           for (int u = 0; u < U; ++u)
-            if (k0 + u < S::KT_H) wv[u] = ld_nt(tiles + (k0 + u) * 64);
+            if (k0 + u < S::KT_H) wv[u] = buf_ld_nt(rs, lo * 16u, (unsigned)(k0 + u) * 1024u);
 #pragma unroll
           for (int u = 0; u < U; ++u)
             if (k0 + u < S::KT_H) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
@@ -636,33 +851,11 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   }
   if (wg == 0) {  // the last token's id
     const int t = p.n_tokens;
-    const unsigned want = tag14(p.tag_base + (unsigned)t * per_token - 1u);
-    u64* slots = p.amax + ((t - 1) & 1) * G;
-    int failed = 0;
-    u64 best = 0;
-    for (int i = tid; i < G && !failed; i += NT) {
-      Spin sp;
-      u64 v;
-      while (((v = ll_get(slots + i)) & TAG14) != want)
-        if (!sp.step(p.err, p.timeout_ticks)) {
-          failed = 1;
-          break;
-        }
-      best = v > best ? v : best;
-    }
-    if (__syncthreads_or(failed)) return;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const u64 o = __shfl_xor(best, m);
-      best = o > best ? o : best;
-    }
-    if (l == 0) sm.amax[w] = best;
-    __syncthreads();
-    if (tid == 0) {
-      for (int i = 0; i < NW; ++i) best = sm.amax[i] > best ? sm.amax[i] : best;
-      const unsigned idx = IDX_MAX - (unsigned)((best >> 14) & IDX_MAX);
-      p.out_tokens[t - 1] = idx < (unsigned)p.vocab ? (int)idx : 0;
-    }
+    int last = 0;
+    if (!token_from_slots(p, p.amax + ((t - 1) & 1) * G, tag14(p.tag_base + (unsigned)t * per_token - 1u),
+                          sm.amax, &last))
+      return;
+    if (tid == 0) p.out_tokens[t - 1] = last;
   }
 }
 
