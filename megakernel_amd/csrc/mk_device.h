@@ -85,16 +85,81 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 __device__ __forceinline__ unsigned lane_id() { return (unsigned)opaque_v((int)threadIdx.x) & (kWave - 1u); }
 
 // ------------------------------------------------------------ reductions
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+// Cross-lane steps use DPP lane selects (folded into the ALU op) inside a row
+// of 16 lanes and the gfx950 permlane swaps across rows, so no step goes
+// through LDS.  Every pattern pairs each lane with exactly one partner, and
+// both partners add the same two values, so all lanes of a group end with
+// identical bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_sel(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7 - i within 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15 - i within 16
+constexpr int DPP_ROR8 = 0x128;        // lane i <- (i + 8) mod 16, i.e. i ^ 8
+
+// x of lane l ^ 16 / l ^ 32 (v_permlane16_swap / v_permlane32_swap with both
+// operands x: the first result holds the even-row / low-half copy, the second
+// the odd-row / high-half copy).
+__device__ __forceinline__ float lane_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(((int)lane_id() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(((int)lane_id() & 32) ? r[0] : r[1]);
+}
+// x + x(l ^ 16), x + x(l ^ 32): the two swap results are the pair in row order.
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Sum over aligned groups of N = 8 or 16 consecutive lanes (result in all of them).
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  v += dpp_sel<DPP_XOR1>(v);
+  v += dpp_sel<DPP_XOR2>(v);
+  v += dpp_sel<DPP_HALF_MIRROR>(v);  // quads are uniform: pairs quad 0 with quad 1
+  if constexpr (N == 16) v += dpp_sel<DPP_MIRROR>(v);  // pairs the two 8-lane halves
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  v = fmaxf(v, dpp_sel<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_sel<DPP_XOR2>(v));
+  v = fmaxf(v, dpp_sel<DPP_HALF_MIRROR>(v));
+  if constexpr (N == 16) v = fmaxf(v, dpp_sel<DPP_MIRROR>(v));
   return v;
 }
+
+// Sum over the lanes l, l ^ S, ... with the same l mod S (S = 8 or 16): the
+// per-lane reduction of S-lane-strided partials.
+template <int S>
+__device__ __forceinline__ float stride_sum(float v) {
+  static_assert(S == 8 || S == 16, "stride 8 or 16");
+  if constexpr (S == 8) v += dpp_sel<DPP_ROR8>(v);
+  return sum_xor32(sum_xor16(v));
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return sum_xor32(sum_xor16(group_sum<16>(v))); }
+__device__ __forceinline__ float wave_max(float v) { return max_xor32(max_xor16(group_max<16>(v))); }
 
 // Block-wide sum/max.  `red` is LDS scratch of >= NW floats.  Every thread
 // combines the per-wave values in the same order, so all get identical bits.

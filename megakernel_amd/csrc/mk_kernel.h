@@ -132,9 +132,7 @@ __device__ __forceinline__ float blk_dot(const Blk<KT>& b, const float* vec) {
     const int kt = w + i * NW;
     if (KT % NW == 0 || kt < KT) acc = dot8(b.w[i], hv + kt * 32, acc);
   }
-  acc += __shfl_xor(acc, 16);
-  acc += __shfl_xor(acc, 32);
-  return acc;
+  return stride_sum<16>(acc);
 }
 
 // Cross-wave sum of per-wave row partials: red[w*16 + r] -> threads 0..15.
@@ -191,7 +189,8 @@ constexpr int EVT_N = 16;
 enum Evt : int {
   EV_ATT_READY = 0, EV_ATT_ROPE, EV_ATT_SOFTMAX, EV_ATT_STORED,
   EV_ATT_PARTIAL, EV_ATT_GATHERED, EV_O_READY, EV_O_STORED,
-  EV_QKV_STORED, EV_GU_STORED, EV_DN_STORED, EV_DN_READY
+  EV_QKV_STORED, EV_GU_STORED, EV_DN_STORED, EV_DN_READY,
+  EV_ATT_REDUCED, EV_ATT_COMBINED, EV_O_DOT
 };
 __device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
   if (p.trace && t == p.trace_token && layer == p.trace_layer && ltid() == 0)
@@ -200,11 +199,13 @@ __device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
 
 // --------------------------------------------------------- tagged fetches
 // Wait until every word of up to three ranges carries its range's tag and copy
-// the values to LDS.  Waiting is two-level so that idle consumers do not flood
-// the memory system: wave 0 polls one sentinel word per producer block (every
-// `ss`-th word of a range) until all carry the tag, then the whole workgroup
-// reads the ranges once, re-polling only if some word is still stale (values
-// and tags of different words become visible in no particular order).
+// the values to LDS.  Inputs of at most B words a thread are polled in bulk:
+// every thread re-reads its words until all carry the tag (one load round trip
+// after the last producer's store lands).  Larger inputs first let wave 0 poll
+// one sentinel word per producer block (every `ss`-th word of a range) so that
+// idle consumers do not flood the memory system, then read in bulk rounds,
+// re-polling a round only if some word is still stale (values and tags of
+// different words become visible in no particular order).
 struct Range {
   u64* src;
   int n;
@@ -219,21 +220,32 @@ template <int B>
 __device__ __forceinline__ bool fetch3(Range a, Range b, Range c, const Params& p) {
   const int tid = ltid();
   int failed = 0;
-  // 1. light wait on sentinels (wave 0 only), for inputs over 2 words a thread
-  if (a.n + b.n + c.n > 2 * NT && tid < kWave) {
+  // 1. light wait on sentinels (wave 0 only), for inputs that need more than
+  //    one bulk round
+  if (a.n + b.n + c.n > B * NT && tid < kWave) {
     const int na = range_sentinels(a), nb = range_sentinels(b), nc = range_sentinels(c);
     const int ns = na + nb + nc;
     Spin sp;
     for (int base = 0; base < ns && !failed;) {
-      bool ready = true;
-      for (int i = base + tid; i < ns && i < base + 4 * kWave; i += kWave) {
-        u64* s;
-        unsigned tg;
-        if (i < na) { s = a.src + i * a.ss; tg = a.tag; }
-        else if (i < na + nb) { s = b.src + (i - na) * b.ss; tg = b.tag; }
-        else { s = c.src + (i - na - nb) * c.ss; tg = c.tag; }
-        ready = ready && ll_tag(ll_get(s)) == tg;
+      // all loads of a round are issued before any is tested
+      u64 v[4];
+      unsigned tgk[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = base + tid + k * kWave;
+        tgk[k] = 0u;
+        v[k] = 0ull;
+        if (i < ns) {
+          u64* s;
+          if (i < na) { s = a.src + i * a.ss; tgk[k] = a.tag; }
+          else if (i < na + nb) { s = b.src + (i - na) * b.ss; tgk[k] = b.tag; }
+          else { s = c.src + (i - na - nb) * c.ss; tgk[k] = c.tag; }
+          v[k] = ll_get(s);
+        }
       }
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ready &= (base + tid + k * kWave >= ns) || ll_tag(v[k]) == tgk[k];
       // every lane must see its sentinels ready before the window advances
       if (__all(ready)) {
         base += 4 * kWave;
@@ -257,7 +269,7 @@ __device__ __forceinline__ bool fetch3(Range a, Range b, Range c, const Params& 
           u64* s = i < a.n ? a.src + i : (i < a.n + b.n ? b.src + (i - a.n) : c.src + (i - a.n - b.n));
           const unsigned tg = i < a.n ? a.tag : (i < a.n + b.n ? b.tag : c.tag);
           wv[k] = ll_get(s);
-          ready = ready && ll_tag(wv[k]) == tg;
+          ready &= ll_tag(wv[k]) == tg;
         }
       }
       if (ready) break;
@@ -285,26 +297,6 @@ constexpr Range kNoRange = {nullptr, 0, nullptr, 0u, 1};
 template <int B>
 __device__ __forceinline__ bool fetch1(u64* src, int n, float* dst, unsigned tag, const Params& p, int ss = 16) {
   return fetch3<B>(Range{src, n, dst, tag, ss}, kNoRange, kNoRange, p);
-}
-
-// Light wait only (wave 0 polls the sentinels of one range); no data copied.
-__device__ __forceinline__ bool await_sentinels(u64* src, int n, int ss, unsigned tag, const Params& p) {
-  const int tid = ltid();
-  int failed = 0;
-  if (tid < kWave) {
-    const int ns = (n + ss - 1) / ss;
-    Spin sp;
-    for (int base = 0; base < ns && !failed;) {
-      bool ready = true;
-      for (int i = base + tid; i < ns && i < base + 4 * kWave; i += kWave) ready = ready && ll_tag(ll_get(src + i * ss)) == tag;
-      if (__all(ready)) {
-        base += 4 * kWave;
-        continue;
-      }
-      if (!sp.step(p.err, p.timeout_ticks)) failed = 1;
-    }
-  }
-  return __syncthreads_or(failed) == 0;
 }
 
 // ------------------------------------------------------------ attention
@@ -386,7 +378,7 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
     for (int c = 0; c < DPL; ++c) v[c] = v[c] * r * bf16_to_f32(kvr.gn[c]);
     float o[DPL];
     if constexpr (DPL == 1) {  // partner of dim l is l ^ 32, in another lane
-      const float partner = __shfl_xor(v[0], 32);
+      const float partner = lane_xor32(v[0]);
       const int d = l & 31;
       o[0] = l < 32 ? v[0] * sm.rc[d] - partner * sm.rs[d] : v[0] * sm.rc[d] + partner * sm.rs[d];
     } else {  // D = 128: dims l and l + 64 pair up in the same lane
@@ -450,8 +442,7 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
 #pragma unroll
       for (int j = 0; j < GQA; ++j) {
         float d = dot8(kk, qr[j], 0.f);
-#pragma unroll
-        for (int mm = LPP / 2; mm >= 1; mm >>= 1) d += __shfl_xor(d, mm);
+        d = group_sum<LPP>(d);
         sc[j][i] = (t < t1) ? d * scale : -INFINITY;
         mx[j] = fmaxf(mx[j], sc[j][i]);
       }
@@ -487,12 +478,10 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
     lsum[j] = wave_sum(lsum[j]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float v = acc[j][e];
-#pragma unroll
-      for (int mm = LPP; mm < kWave; mm <<= 1) v += __shfl_xor(v, mm);
-      acc[j][e] = v;
+      acc[j][e] = stride_sum<LPP>(acc[j][e]);
     }
   }
+  evt(p, tt, layer, EV_ATT_REDUCED);
   if (po == 0) {
 #pragma unroll
     for (int j = 0; j < GQA; ++j)
@@ -540,6 +529,7 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
     }
   }
   __syncthreads();
+  evt(p, tt, layer, EV_ATT_COMBINED);
   u64* prow = p.part + ((long long)g * p.nsplit_max + s) * W;
   if (s != 0) {  // publish the partial for this group's merger (split 0)
     if (tid < GQA) {
@@ -685,11 +675,16 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           __syncthreads();
         }
         rmsnorm_lds<S>(sm.xin, gq, sm.vec);
-        for (int rb = it_qkv, k = 0; rb < S::RB_QKV; rb += G, ++k) {
-          if (k > 0) blk_load(rq, wl + S::OFF_QKV + (long long)rb * S::KT_H * 64);
+        {  // the prefetched block
+          const float y = rows_sum(blk_dot(rq, sm.vec), sm.red);
+          if (tid < 16) ll_put(p.qkv + it_qkv * 16 + tid, ll_pack(y, tg));
+          evt(p, t, layer, EV_QKV_STORED);
+          __syncthreads();
+        }
+        for (int rb = it_qkv + G; rb < S::RB_QKV; rb += G) {  // grids smaller than the block count
+          blk_load(rq, wl + S::OFF_QKV + (long long)rb * S::KT_H * 64);
           const float y = rows_sum(blk_dot(rq, sm.vec), sm.red);
           if (tid < 16) ll_put(p.qkv + rb * 16 + tid, ll_pack(y, tg));
-          if (k == 0) evt(p, t, layer, EV_QKV_STORED);
           __syncthreads();
         }
         trace_mark(p, t, slot + 0, 1);
@@ -711,33 +706,45 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         trace_mark(p, t, slot + 1, 1);
       }
       // ---------------- P3: O projection + residual (prefetch: gate/up + ffn gains)
-      if (it_o < S::RB_H) {
-        if (!fetch3<2>(Range{p.attn, S::QD, sm.vec, tg + 1u, 16},
-                       layer > 0 ? Range{p.x + it_o * 16, 16, sm.xres, tg_x, 16} : kNoRange, kNoRange, p))
-          return;
-        trace_mark(p, t, slot + 2, 0);
-        evt(p, t, layer, EV_O_READY);
-      }
+      // The prefetch is issued before this phase's wait: loads complete in
+      // order, so the wait absorbs it, and the O product (whose block is
+      // older) never waits behind it.
       if (it_gu < S::RB_F) {
         const u32x4* gp = wl + S::OFF_GU + (long long)(2 * it_gu) * S::KT_H * 64;
         blk_load(rg, gp);
         blk_load(ru, gp + S::KT_H * 64);
         gf = gain_pair<S>(nrm + S::NORM_FFN);
       }
-      for (int rb = it_o, k = 0; rb < S::RB_H; rb += G, ++k) {
-        if (k > 0) {  // more blocks than workgroups: later blocks load now
-          blk_load(ro, wl + S::OFF_O + (long long)rb * S::KT_Q * 64);
-          if (layer > 0 && !fetch1<1>(p.x + rb * 16, 16, sm.xres, tg_x, p)) return;
+      if (it_o < S::RB_H) {
+        if (!fetch3<3>(Range{p.attn, S::QD, sm.vec, tg + 1u, 16},
+                       layer > 0 ? Range{p.x + it_o * 16, 16, sm.xres, tg_x, 16} : kNoRange, kNoRange, p))
+          return;
+        trace_mark(p, t, slot + 2, 0);
+        evt(p, t, layer, EV_O_READY);
+      }
+      if (it_o < S::RB_H) {  // the prefetched block
+        const float part = blk_dot(ro, sm.vec);
+        evt(p, t, layer, EV_O_DOT);
+        const float y = rows_sum(part, sm.red);
+        if (tid < 16) {
+          const int row = it_o * 16 + tid;
+          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres[tid];
+          ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
         }
+        evt(p, t, layer, EV_O_STORED);
+        __syncthreads();
+        trace_mark(p, t, slot + 2, 1);
+      }
+      for (int rb = it_o + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
+        blk_load(ro, wl + S::OFF_O + (long long)rb * S::KT_Q * 64);
+        if (layer > 0 && !fetch1<1>(p.x + rb * 16, 16, sm.xres, tg_x, p)) return;
         const float y = rows_sum(blk_dot(ro, sm.vec), sm.red);
         if (tid < 16) {
           const int row = rb * 16 + tid;
           const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres[tid];
           ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
         }
-        if (k == 0) evt(p, t, layer, EV_O_STORED);
         __syncthreads();
-        if (k == 0) trace_mark(p, t, slot + 2, 1);
       }
       // ---------------- P4: gate/up + SiLU (prefetch: down)
       if (it_gu < S::RB_F) {
@@ -747,23 +754,27 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       if (it_dn < S::RB_H) blk_load(rd, wl + S::OFF_DOWN + (long long)it_dn * S::KT_F * 64);
       if (it_gu < S::RB_F) {
         rmsnorm_lds<S>(sm.xin, gf, sm.vec);
-        for (int pr = it_gu, k = 0; pr < S::RB_F; pr += G, ++k) {
-          if (k > 0) {
-            const u32x4* gp = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
-            blk_load(rg, gp);
-            blk_load(ru, gp + S::KT_H * 64);
-          }
+        {  // the prefetched block pair
+          const float yg = rows_sum(blk_dot(rg, sm.vec), sm.red);
+          const float yu = rows_sum(blk_dot(ru, sm.vec), sm.red + NW * 16);
+          if (tid < 16) ll_put(p.act + it_gu * 16 + tid, ll_pack(silu_mul(yg, yu), tg + 3u));
+          evt(p, t, layer, EV_GU_STORED);
+          __syncthreads();
+        }
+        for (int pr = it_gu + G; pr < S::RB_F; pr += G) {  // grids smaller than the block count
+          const u32x4* gp = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
+          blk_load(rg, gp);
+          blk_load(ru, gp + S::KT_H * 64);
           const float yg = rows_sum(blk_dot(rg, sm.vec), sm.red);
           const float yu = rows_sum(blk_dot(ru, sm.vec), sm.red + NW * 16);
           if (tid < 16) ll_put(p.act + pr * 16 + tid, ll_pack(silu_mul(yg, yu), tg + 3u));
-          if (k == 0) evt(p, t, layer, EV_GU_STORED);
           __syncthreads();
         }
         trace_mark(p, t, slot + 3, 1);
       }
       // ---------------- P5: down projection + residual (prefetch: next QKV + attn gains)
       if (it_dn < S::RB_H) {
-        if (!fetch3<6>(Range{p.act, S::F, sm.vec, tg + 3u, 16}, Range{p.x + it_dn * 16, 16, sm.xres, tg + 2u, 16},
+        if (!fetch3<7>(Range{p.act, S::F, sm.vec, tg + 3u, 16}, Range{p.x + it_dn * 16, 16, sm.xres, tg + 2u, 16},
                        kNoRange, p))
           return;
         trace_mark(p, t, slot + 4, 0);
@@ -773,11 +784,21 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         blk_load(rq, wl + S::U_LAYER + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
         gq = gain_pair<S>(nrm + S::NORM_STRIDE + S::NORM_ATTN);
       }
-      for (int rb = it_dn, k = 0; rb < S::RB_H; rb += G, ++k) {
-        if (k > 0) {
-          blk_load(rd, wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64);
-          if (!fetch1<1>(p.x + rb * 16, 16, sm.xres, tg + 2u, p)) return;
+      if (it_dn < S::RB_H) {  // the prefetched block
+        const float y = rows_sum(blk_dot(rd, sm.vec), sm.red);
+        if (tid < 16) {
+          const int row = it_dn * 16 + tid;
+          const float xn = sm.xres[tid] + y;
+          ll_put(p.x + row, ll_pack(xn, tg + 4u));
+          if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
         }
+        evt(p, t, layer, EV_DN_STORED);
+        __syncthreads();
+        trace_mark(p, t, slot + 4, 1);
+      }
+      for (int rb = it_dn + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
+        blk_load(rd, wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64);
+        if (!fetch1<1>(p.x + rb * 16, 16, sm.xres, tg + 2u, p)) return;
         const float y = rows_sum(blk_dot(rd, sm.vec), sm.red);
         if (tid < 16) {
           const int row = rb * 16 + tid;
@@ -785,9 +806,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           ll_put(p.x + row, ll_pack(xn, tg + 4u));
           if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
         }
-        if (k == 0) evt(p, t, layer, EV_DN_STORED);
         __syncthreads();
-        if (k == 0) trace_mark(p, t, slot + 4, 1);
       }
     }
     // ---------------- final norm + tied LM head + per-workgroup argmax
@@ -821,8 +840,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           for (int u = 0; u < U; ++u)
             if (k0 + u < S::KT_H) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
         }
-        acc += __shfl_xor(acc, 16);
-        acc += __shfl_xor(acc, 32);
+        acc = stride_sum<16>(acc);
         if (l < 16) {
           const unsigned idx = (unsigned)(b * 16 + l);
           if (p.dbg_logits) p.dbg_logits[idx] = acc;
