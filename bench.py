@@ -38,6 +38,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--ctx", type=int, default=1024)
+    ap.add_argument("--chunk", type=int, default=0, help="minimum positions per attention work item (0: library default)")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
@@ -151,6 +152,8 @@ def main():
     K, W = args.steps, args.warmup
     dw = DeviceWeights(shape, args.seed, std=0.02, gain_std=0.0)
     eng = MegakernelEngine(shape=shape, max_seq=args.ctx + K + 8, device_weights=dw)
+    if args.chunk > 0:
+        eng.set_attention_chunk(args.chunk)
     info = launcher.detect_gpu()
     grid = eng.grid_size
     print(f"# device {info['name']} CUs {info['cu_count']} grid {grid}", file=sys.stderr, flush=True)

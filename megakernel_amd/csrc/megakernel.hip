@@ -571,6 +571,10 @@ int megakernel_trace_generate(void* handle, int first_token, int n, int trace_to
     mk::set_err("invalid trace arguments");
     return -1;
   }
+  if (h->L > mk::TRACE_MAX_LAYERS) {
+    mk::set_err("tracing supports at most 48 layers");
+    return -1;
+  }
   const size_t bytes = ((size_t)(5 * h->L + 1) * 2 + mk::EVT_N) * h->G * 8;
   if (hipMemsetAsync(h->trace, 0, bytes, h->stream) != hipSuccess) {
     mk::set_err("trace clear failed");

@@ -35,7 +35,10 @@ constexpr int NT = 512;               // threads per workgroup (8 waves)
 constexpr int NW = NT / kWave;
 constexpr int PHASES_PER_LAYER = 5;
 constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
-constexpr int KV_ROWS = 4;            // K/V register rows per lane per attention sub-chunk
+#ifndef MK_KV_ROWS
+#define MK_KV_ROWS 4
+#endif
+constexpr int KV_ROWS = MK_KV_ROWS;            // K/V register rows per lane per attention sub-chunk
 constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
 __device__ __forceinline__ unsigned tag14(unsigned tag) { return tag % 16383u + 1u; }
 constexpr int IDX_BITS = 18;          // ... and an 18-bit vocabulary index
@@ -179,13 +182,21 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // Work item i of a phase runs on workgroup (i + off) mod G.
 __device__ __forceinline__ int first_item(int wg, int off, int G) { return (wg + G - (off % G)) % G; }
 
+// Phase trace of one token (profiling only).  Timestamps go to an LDS buffer
+// and are written out once at the end of the traced token, so recording them
+// adds no global stores (and no store waits) inside the phases being timed.
+constexpr int TRACE_MAX_LAYERS = 48;
+constexpr int EVT_N = 16;
+constexpr int TRACE_LDS = (5 * TRACE_MAX_LAYERS + 1) * 2 + EVT_N;
+__shared__ u64 trace_lds[TRACE_LDS];
+
+__device__ __forceinline__ bool tracing(const Params& p, int t) { return p.trace && t == p.trace_token; }
+
 __device__ __forceinline__ void trace_mark(const Params& p, int t, int slot, int which) {
-  if (p.trace && t == p.trace_token && ltid() == 0)
-    p.trace[((long long)slot * 2 + which) * gridDim.x + blockIdx.x] = wall_clock64();
+  if (tracing(p, t) && ltid() == 0) trace_lds[slot * 2 + which] = wall_clock64();
 }
 
 // Fine-grained events of one layer of the traced token.
-constexpr int EVT_N = 16;
 enum Evt : int {
   EV_ATT_READY = 0, EV_ATT_ROPE, EV_ATT_SOFTMAX, EV_ATT_STORED,
   EV_ATT_PARTIAL, EV_ATT_GATHERED, EV_O_READY, EV_O_STORED,
@@ -193,8 +204,21 @@ enum Evt : int {
   EV_ATT_REDUCED, EV_ATT_COMBINED, EV_O_DOT
 };
 __device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
-  if (p.trace && t == p.trace_token && layer == p.trace_layer && ltid() == 0)
-    p.trace[((long long)(5 * p.n_layers + 1) * 2 + e) * gridDim.x + blockIdx.x] = wall_clock64();
+  if (tracing(p, t) && layer == p.trace_layer && ltid() == 0)
+    trace_lds[(5 * p.n_layers + 1) * 2 + e] = wall_clock64();
+}
+
+// Clear before the traced token; write out after it ([entry][G] layout).
+__device__ __forceinline__ void trace_begin(const Params& p, int t) {
+  if (!tracing(p, t)) return;
+  for (int i = ltid(); i < TRACE_LDS; i += NT) trace_lds[i] = 0ull;
+  __syncthreads();
+}
+__device__ __forceinline__ void trace_end(const Params& p, int t) {
+  if (!tracing(p, t)) return;
+  __syncthreads();
+  const int n = (5 * p.n_layers + 1) * 2 + EVT_N;
+  for (int i = ltid(); i < n; i += NT) p.trace[(long long)i * gridDim.x + blockIdx.x] = trace_lds[i];
 }
 
 // --------------------------------------------------------- tagged fetches
@@ -624,6 +648,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
 
   int tok = p.first_token;
   for (int t = 0; t < p.n_tokens; ++t) {
+    trace_begin(p, t);
     const int pos = p.pos0 + t;
     const unsigned tb = p.tag_base + (unsigned)t * per_token;  // tag of this token's first phase
     if (it_qkv < S::RB_QKV) {
@@ -660,16 +685,17 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       const unsigned tg = tb + (unsigned)(PHASES_PER_LAYER * layer);  // tag of P1 of this layer
       const unsigned tg_x = tg - 1u;  // tag of the x rows this layer starts from (layer > 0)
       const int slot = PHASES_PER_LAYER * layer;
+      // Each phase issues the next phase's prefetch before its own wait:
+      // loads complete in order, so the wait absorbs the prefetch, and no
+      // product ever waits behind loads issued after its own block.
       // ---------------- P1: QKV (prefetch: attention K/V + QK-norm gains)
-      if (it_qkv < S::RB_QKV) {
-        if (layer > 0 && !fetch1<2>(p.x, S::H, sm.xin, tg_x, p)) return;
-        trace_mark(p, t, slot + 0, 0);
-      }
       if (has_att) {
         kv_load<S>(rkv, p, layer, ag, at0, at1, pos, 0);
         gain_load_qk<S>(rkv, p, layer);
       }
       if (it_qkv < S::RB_QKV) {
+        if (layer > 0 && !fetch1<2>(p.x, S::H, sm.xin, tg_x, p)) return;
+        trace_mark(p, t, slot + 0, 0);
         if (layer == 0) {
           for (int i = tid; i < S::H; i += NT) sm.xin[i] = packed_elem<S::KT_H>(p.lmhead, tok, i);
           __syncthreads();
@@ -690,6 +716,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         trace_mark(p, t, slot + 0, 1);
       }
       // ---------------- P2: attention partials (prefetch: O)
+      if (it_o < S::RB_H) blk_load(ro, wl + S::OFF_O + (long long)it_o * S::KT_Q * 64);
       if (has_att) {
         const int D = S::D, GQA = S::GQA;
         if (!fetch3<1>(Range{p.qkv + ag * GQA * D, GQA * D, sm.qk, tg, 16},
@@ -697,18 +724,12 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
                        Range{p.qkv + S::QD + S::KVD + ag * D, D, sm.qk + (GQA + 1) * D, tg, 16}, p))
           return;
         trace_mark(p, t, slot + 1, 0);
-      }
-      if (it_o < S::RB_H) blk_load(ro, wl + S::OFF_O + (long long)it_o * S::KT_Q * 64);
-      if (has_att) {
         evt(p, t, layer, EV_ATT_READY);
         if (!attention_compute<S>(p, sm, rkv, layer, pos, ag, as, nsplit, at0, at1, tg + 1u, t)) return;
         evt(p, t, layer, EV_ATT_STORED);
         trace_mark(p, t, slot + 1, 1);
       }
       // ---------------- P3: O projection + residual (prefetch: gate/up + ffn gains)
-      // The prefetch is issued before this phase's wait: loads complete in
-      // order, so the wait absorbs it, and the O product (whose block is
-      // older) never waits behind it.
       if (it_gu < S::RB_F) {
         const u32x4* gp = wl + S::OFF_GU + (long long)(2 * it_gu) * S::KT_H * 64;
         blk_load(rg, gp);
@@ -747,12 +768,10 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         __syncthreads();
       }
       // ---------------- P4: gate/up + SiLU (prefetch: down)
+      if (it_dn < S::RB_H) blk_load(rd, wl + S::OFF_DOWN + (long long)it_dn * S::KT_F * 64);
       if (it_gu < S::RB_F) {
         if (!fetch1<2>(p.x, S::H, sm.xin, tg + 2u, p)) return;
         trace_mark(p, t, slot + 3, 0);
-      }
-      if (it_dn < S::RB_H) blk_load(rd, wl + S::OFF_DOWN + (long long)it_dn * S::KT_F * 64);
-      if (it_gu < S::RB_F) {
         rmsnorm_lds<S>(sm.xin, gf, sm.vec);
         {  // the prefetched block pair
           const float yg = rows_sum(blk_dot(rg, sm.vec), sm.red);
@@ -773,18 +792,17 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         trace_mark(p, t, slot + 3, 1);
       }
       // ---------------- P5: down projection + residual (prefetch: next QKV + attn gains)
+      if (layer + 1 < L && it_qkv < S::RB_QKV) {
+        blk_load(rq, wl + S::U_LAYER + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
+        gq = gain_pair<S>(nrm + S::NORM_STRIDE + S::NORM_ATTN);
+      }
       if (it_dn < S::RB_H) {
         if (!fetch3<7>(Range{p.act, S::F, sm.vec, tg + 3u, 16}, Range{p.x + it_dn * 16, 16, sm.xres, tg + 2u, 16},
                        kNoRange, p))
           return;
         trace_mark(p, t, slot + 4, 0);
         evt(p, t, layer, EV_DN_READY);
-      }
-      if (layer + 1 < L && it_qkv < S::RB_QKV) {
-        blk_load(rq, wl + S::U_LAYER + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
-        gq = gain_pair<S>(nrm + S::NORM_STRIDE + S::NORM_ATTN);
-      }
-      if (it_dn < S::RB_H) {  // the prefetched block
+        // the prefetched block
         const float y = rows_sum(blk_dot(rd, sm.vec), sm.red);
         if (tid < 16) {
           const int row = it_dn * 16 + tid;
@@ -866,6 +884,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       trace_mark(p, t, PHASES_PER_LAYER * L, 1);
       __syncthreads();
     }
+    trace_end(p, t);
   }
   if (wg == 0) {  // the last token's id
     const int t = p.n_tokens;
