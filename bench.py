@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
     ap.add_argument("--trace", action="store_true", help="print a per-phase critical-path summary")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 5 plain device copies of 1 GiB (known bytes) for scaling rocprof counters")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                     help="measured HBM bytes per launch (rocprofv3 --pmc), if present")
     return ap.parse_args()
@@ -137,8 +139,24 @@ def trace_summary(eng, shape, args, info):
                   file=sys.stderr)
 
 
+def calibrate_copy():
+    """Five device-to-device copies of exactly 1 GiB (read 1 GiB, write 1 GiB):
+    the reference point that scales FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+    n = 1 << 28  # float32 elements = 1 GiB
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n * 4, "copies": 5}))
+
+
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the batch-1 decode path does not "
                                    "shard (see DESIGN.md); run with --gpus 1"}))

@@ -672,7 +672,8 @@ int megakernel_device_info(int* cus, int* wall_clock_khz, char* name, int name_l
   }
   if (cus) *cus = prop.multiProcessorCount;
   if (wall_clock_khz) (void)hipDeviceGetAttribute(wall_clock_khz, hipDeviceAttributeWallClockRate, dev);
-  if (name && name_len > 0) snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  if (name && name_len > 0)
+    snprintf(name, name_len, "%s (%s)", prop.name[0] ? prop.name : "AMD Instinct GPU", prop.gcnArchName);
   return 0;
 }
 
