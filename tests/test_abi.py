@@ -1,0 +1,86 @@
+"""The C-ABI library on the CPU: it loads, exports every function that
+include/megakernel.h declares (and the ctypes table matches the header), and
+its host-only entry points and argument checks behave.  No GPU work is
+launched here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from megakernel_amd import _lib
+from oracle import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "megakernel.h")
+
+
+def header_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(megakernel_[a-z_0-9]+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def clib():
+    if not os.path.exists(_lib.DEFAULT_LIB):
+        from megakernel_amd import launcher
+        launcher.compile_shared_library()
+    return _lib.load()
+
+
+def test_header_declares_the_reference_entry_points():
+    fns = header_functions()
+    for name in ("megakernel_init", "megakernel_decode", "megakernel_reset", "megakernel_get_pos",
+                 "megakernel_free", "megakernel_sync"):
+        assert name in fns
+    assert len(fns) == len(set(fns))
+
+
+def test_library_exports_every_declared_symbol(clib):
+    raw = ctypes.CDLL(_lib.DEFAULT_LIB)
+    for name in header_functions():
+        assert hasattr(raw, name), name
+    assert set(header_functions()) == set(_lib.SIGNATURES)
+
+
+def test_reference_signatures_unchanged():
+    # host/bridge.py:41-67 of the reference declares exactly these
+    S = _lib.SIGNATURES
+    assert S["megakernel_init"] == (ctypes.c_void_p, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_longlong),
+                                                      ctypes.c_int])
+    assert S["megakernel_decode"] == (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int])
+    assert S["megakernel_reset"] == (None, [ctypes.c_void_p])
+    assert S["megakernel_get_pos"] == (ctypes.c_int, [ctypes.c_void_p])
+    assert S["megakernel_free"] == (None, [ctypes.c_void_p])
+    assert S["megakernel_sync"] == (None, [])
+
+
+def test_synth_key_matches_oracle(clib):
+    for seed, tid in [(0, 0), (2024, 7), (123, 0x40000003), (2**63 + 5, 0x7F000000)]:
+        assert clib.megakernel_synth_key(seed, tid) == synth.stream_key(seed, tid)
+
+
+@pytest.mark.parametrize("preset,d", [(_lib.PRESET_BASELINE, 64), (_lib.PRESET_QWEN3_06B, 128),
+                                      (_lib.PRESET_TINY, 64)])
+def test_rope_inv_freq_table(clib, preset, d):
+    out = (ctypes.c_float * d)()
+    n = clib.megakernel_rope_inv_freq(preset, out, d)
+    assert n == d // 2
+    got = np.frombuffer(out, dtype=np.float32)[:n].astype(np.float64)
+    ref = 1.0 / (1e6 ** (np.arange(0, d, 2) / d))
+    np.testing.assert_allclose(got, ref, rtol=3e-7)
+    assert clib.megakernel_rope_inv_freq(preset, out, 1) == -1  # buffer too small
+
+
+def test_null_handle_errors_are_reported(clib):
+    assert clib.megakernel_decode(None, 1) == -1
+    assert "handle" in _lib.last_error(clib)
+    assert clib.megakernel_get_pos(None) == -1
+    assert clib.megakernel_set_pos(None, 0) == -1
+    assert clib.megakernel_generate(None, 1, 1, None) == -1
+    assert clib.megakernel_set_attention_chunk(None, 64) == -1
+    assert clib.megakernel_grid_size(None) == -1
+    clib.megakernel_reset(None)  # no-ops, as in the reference
+    clib.megakernel_free(None)
