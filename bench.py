@@ -126,7 +126,7 @@ def trace_summary(eng, shape, args, info):
         print(f"#   {k:8s} handoff {w:7.2f} us   last-ready->last-done {d:7.2f} us   (x{len(work[k])})",
               file=sys.stderr)
     evn = ["att_ready", "att_rope", "att_softmax", "att_stored", "att_partial", "att_gathered", "o_ready",
-           "o_stored", "qkv_stored", "gu_stored", "dn_stored", "dn_ready", "att_reduced", "att_combined", "o_dot"]
+           "o_stored", "qkv_stored", "gu_stored", "dn_stored", "dn_ready", "att_reduced", "att_combined", "merge_scaled", "merge_done"]
     base = min(ev[e][ev[e] > 0].min() for e in range(len(evn)) if (ev[e] > 0).any())
     print(f"# events of layer {L // 2} (us from the first event; min / median / max over workgroups):",
           file=sys.stderr)

@@ -22,9 +22,12 @@ struct Shape {
   static constexpr int QKV = QD + 2 * KVD;   // fused q|k|v rows
   static constexpr int GQA = NQ / NKV;       // q heads per kv head
   // Packed weights are stored as 16-row x 32-column tiles (see below).
-  static constexpr int KT_H = H / 32;        // k-tiles of a K = H row
-  static constexpr int KT_Q = QD / 32;       // k-tiles of an O-proj row
-  static constexpr int KT_F = F / 32;        // k-tiles of a down-proj row
+  static constexpr int KT_H = H / 32;        // 1 KiB units per 16 rows of a K = H matrix
+  static constexpr int KT_Q = QD / 32;       // ... of the O projection (K = QD)
+  static constexpr int KT_F = F / 32;        // ... of the down projection (K = F)
+  static constexpr int KC_H = H / 256;       // 256-column chunks of a K = H row
+  static constexpr int KC_Q = QD / 256;
+  static constexpr int KC_F = F / 256;
   static constexpr int RB_QKV = QKV / 16;    // 16-row blocks of the fused QKV
   static constexpr int RB_H = H / 16;        // 16-row blocks of O / down outputs
   static constexpr int RB_F = F / 16;        // 16-row blocks of gate (and of up)
@@ -42,7 +45,7 @@ struct Shape {
   static constexpr int NORM_ATTN = 0, NORM_Q = H, NORM_K = H + D, NORM_FFN = H + 2 * D;
   static constexpr int NORM_STRIDE = 2 * H + 2 * D;
 
-  static_assert(H % 32 == 0 && QD % 32 == 0 && F % 32 == 0, "K dims must be multiples of 32");
+  static_assert(H % 256 == 0 && QD % 256 == 0 && F % 256 == 0, "K dims must be multiples of 256");
   static_assert(QKV % 16 == 0 && F % 16 == 0 && H % 16 == 0, "row dims must be multiples of 16");
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(NQ % NKV == 0, "GQA");
@@ -53,15 +56,20 @@ using ShapeQwen3 = Shape<1024, 16, 8, 128, 3072>;
 using ShapeTiny = Shape<256, 4, 2, 64, 512>;
 
 // ---------------------------------------------------------------------------
-// Packed weight layout ("tile stream").
+// Packed weight layouts.  Both cut a row-major bf16 matrix W[R][K]
+// (R % 16 == 0) into 16-row blocks of 16*K*2 bytes, block rb's bytes
+// contiguous, so a workgroup streams one block with wave-wide 1 KiB loads.
 //
-// A row-major bf16 matrix W[R][K] (R % 16 == 0, K % 32 == 0) is stored as
-// tiles of 16 rows x 32 columns, tile (rb, kt) at index rb * (K/32) + kt, so one
-// 16-row block's whole K extent is contiguous.  Inside a tile, 16-byte unit
-// `lane` (0..63) holds the 8 bf16 W[rb*16 + (lane & 15)][kt*32 + (lane >> 4)*8 + e],
-// e = 0..7.  This is exactly the A-operand register layout of
-// v_mfma_f32_16x16x32_bf16, and it makes every wave-wide 16-byte load one
-// contiguous, fully coalesced 1 KiB request.
+// Layer matrices ("row-pair" layout, K % 256 == 0): inside block rb, the
+// 1 KiB unit (w, kc) at index w * (K/256) + kc holds rows 16rb + 2w and
+// 16rb + 2w + 1, columns 256kc .. 256kc + 255: 16-byte lane l holds the 8 bf16
+// W[16rb + 2w + (l >> 5)][256kc + 8(l & 31) + e], e = 0..7.  Wave w of the
+// owning workgroup reads exactly its two rows, so a row's dot product is
+// reduced inside one wave (no cross-wave exchange).
+//
+// LM head / embedding ("tile" layout, K % 32 == 0): inside block rb, unit kt
+// holds the 16 x 32 tile at columns 32kt: lane l holds
+// W[16rb + (l & 15)][32kt + 8(l >> 4) + e].  A wave reduces a whole block.
 //
 // Per layer: fused QKV (q rows, then k rows, then v rows) | O | gate/up with
 // blocks interleaved (gate block p at 2p, up block p at 2p+1) | down.

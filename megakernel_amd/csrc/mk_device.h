@@ -269,55 +269,4 @@ struct Spin {
   }
 };
 
-// Wait until src[0..n) all carry `tag`, then copy their values to dst (LDS).
-// Called by the whole workgroup (NT threads); returns false uniformly if the
-// launch must abort.  Each thread polls B words per round with independent
-// loads so the round costs one memory latency.
-template <int NT, int B>
-__device__ __forceinline__ bool ll_fetch(u64* src, int n, unsigned tag, float* dst, int* err,
-                                         u64 timeout_ticks) {
-  int failed = 0;
-  for (int base = 0; base < n && !failed; base += NT * B) {
-    u64 w[B];
-    Spin sp;
-    while (true) {
-      bool ready = true;
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        const int i = base + b * NT + ltid();
-        if (i < n) {
-          w[b] = ll_get(src + i);
-          ready = ready && ll_tag(w[b]) == tag;
-        }
-      }
-      if (ready) break;
-      if (!sp.step(err, timeout_ticks)) {
-        failed = 1;
-        break;
-      }
-    }
-    if (!failed) {
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        const int i = base + b * NT + ltid();
-        if (i < n) dst[i] = ll_val(w[b]);
-      }
-    }
-  }
-  return __syncthreads_or(failed) == 0;
-}
-
-// One word, one thread (residual rows).  Returns false on abort.
-__device__ __forceinline__ bool ll_wait1(u64* src, unsigned tag, float* out, int* err, u64 timeout_ticks) {
-  Spin sp;
-  while (true) {
-    const u64 w = ll_get(src);
-    if (ll_tag(w) == tag) {
-      *out = ll_val(w);
-      return true;
-    }
-    if (!sp.step(err, timeout_ticks)) return false;
-  }
-}
-
 }  // namespace mk

@@ -75,22 +75,84 @@ struct Params {
 
 template <class S>
 struct Smem {
-  static constexpr int VEC = (S::F > S::QD ? (S::F > S::H ? S::F : S::H) : (S::QD > S::H ? S::QD : S::H));
-  float vec[VEC];                     // GEMV input vector
-  float xin[S::H];                    // residual stream as read
-  float red[2 * NW * 16];             // GEMV cross-wave partials
+  // GEMV input vectors, one per phase type (a phase's GEMV ends without a
+  // barrier, so the next phase must not overwrite the vector it reads)
+  float vec_q[S::H];                  // QKV: x * attn_norm gain
+  float vec_o[S::QD];                 // O: attention output
+  float vec_g[S::H];                  // gate/up: x * ffn_norm gain
+  float vec_d[S::F];                  // down: SiLU(gate) * up
+  float vec_l[S::H];                  // LM head: x * final_norm gain
+  float xres_o[16], xres_d[16];       // residual rows of this workgroup's O / down block
+  float ssw[3][NW];                   // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
+  float rowbuf[4][16];                // a block's 16 results, stored by one wave
   float qk[(S::GQA + 2) * S::D];      // q heads, k, v of the current position
   u32x4 kvcur[2][S::D / 8];           // bf16 K/V of the current position
   float pv[NW * S::GQA * S::D];       // attention: per-wave unnormalised outputs
   float mw[NW * S::GQA], lw[NW * S::GQA];  // attention: per-wave max / sum
   float gm[S::GQA], gl[S::GQA];       // this item's (max, sum) per q head
   float mbuf[(NSPLIT_CAP - 1) * S::GQA * (S::D + 2)];  // other splits' partials (merger)
-  float xres[16];                     // residual rows of this workgroup's O / down block
+  float mscale[NSPLIT_CAP * S::GQA];  // merger: per-split weight f_q / L per head
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
   u64 amax[NW];
 };
 
 // Element `col` of row `row` of a packed [R][K] matrix (K = 32 * KT).
+
+// Workgroup-wide "did any thread give up waiting".  A failure aborts the
+// launch, so the flag is only ever set after its initial clear: one LDS word
+// serves every wait, and the check is a plain barrier plus one LDS read (the
+// device library's __syncthreads_or is a full work-group reduction, about
+// ten times slower).
+__shared__ int wg_abort;
+__device__ __forceinline__ bool block_failed(int failed) {
+  if (failed) wg_abort = 1;
+  __syncthreads();
+  return *static_cast<volatile int*>(&wg_abort) != 0;
+}
+
+// ------------------------------------------------------------------ GEMV
+// One packed 16-row block in the row-pair layout: wave w holds chunks
+// 0..KC-1 of rows 2w, 2w+1; lane l covers row 2w + (l >> 5) and columns
+// 256 kc + 8 (l & 31) .. +8.
+template <int KC>
+struct Blk {
+  u32x4 w[KC];
+};
+
+template <int KC>
+__device__ __forceinline__ void blk_load(Blk<KC>& b, const u32x4* __restrict__ block) {
+  const int w = wave_id();
+  const unsigned lb = lane_id() * 16u;
+  const auto rs = make_rsrc(block);
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) b.w[kc] = buf_ld_nt(rs, lb, (unsigned)(w * KC + kc) * 1024u);
+}
+
+// Row of the block this lane's dot product belongs to, and the lane that
+// stores it (lanes 0 and 32).
+__device__ __forceinline__ int blk_row() { return 2 * wave_id() + (int)(lane_id() >> 5); }
+__device__ __forceinline__ bool row_owner() { return (lane_id() & 31u) == 0u; }
+
+// Dot product of this lane's row with vec (LDS fp32): every lane of the half
+// wave gets the full sum (reduced inside the wave, no LDS exchange).
+template <int KC>
+__device__ __forceinline__ float blk_dot(const Blk<KC>& b, const float* vec) {
+  const float* hv = vec + 8 * (int)(lane_id() & 31u);
+  float acc = 0.f;
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) acc = dot8(b.w[kc], hv + 256 * kc, acc);
+  return sum_xor16(group_sum<16>(acc));
+}
+
+// The 16 row results of a block, published by one wave as one 128-byte store.
+__device__ __forceinline__ void store_rows(float* rowbuf, u64* dst16, float v, unsigned tag) {
+  if (row_owner()) rowbuf[blk_row()] = v;
+  __syncthreads();
+  const int t_ = ltid();
+  if (t_ < 16) ll_put(dst16 + t_, ll_pack(rowbuf[t_], tag));
+}
+
+// Element of the tile-layout LM head / embedding (row, col).
 template <int KT>
 __device__ __forceinline__ float packed_elem(const u32x4* base, int row, int col) {
   const int kt = col >> 5, q = (col >> 3) & 3, e = col & 7;
@@ -99,82 +161,97 @@ __device__ __forceinline__ float packed_elem(const u32x4* base, int row, int col
   return bf16_to_f32(u[e]);
 }
 
-// ------------------------------------------------------------------ GEMV
-// One packed 16-row block: wave w holds k-tiles w, w+NW, ...; lane l covers
-// row l & 15 and columns (l >> 4) * 8 .. +8 of each tile.
-template <int KT>
-struct Blk {
-  static constexpr int PER = (KT + NW - 1) / NW;
-  u32x4 w[PER];
+// RMSNorm (reference rmsnorm.cuh:87-108) is folded into the GEMVs that consume
+// it: the input vector is stored as x * gain, and the row results are scaled
+// by r = rsqrt(mean(x^2) + eps).  Each thread owns elements tid + k*NT.
+template <class S>
+struct NormIn {
+  static constexpr int PER = (S::H + NT - 1) / NT;
+  float g[PER];
 };
 
-template <int KT>
-__device__ __forceinline__ void blk_load(Blk<KT>& b, const u32x4* __restrict__ tiles) {
-  const int w = wave_id();
-  const unsigned lb = lane_id() * 16u;
-  const auto rs = make_rsrc(tiles);
+// The gains of this thread's elements, loaded before the phase's wait.
+template <class S>
+__device__ __forceinline__ void gains_load(NormIn<S>& n, const uint16_t* gain) {
+  const int t_ = ltid();
 #pragma unroll
-  for (int i = 0; i < Blk<KT>::PER; ++i) {
-    const unsigned so = (unsigned)(w + i * NW) * 1024u;  // k-tile of this wave, bytes
-    if constexpr (KT % NW == 0) {
-      b.w[i] = buf_ld_nt(rs, lb, so);
-    } else if (w + i * NW < KT) {
-      b.w[i] = buf_ld_nt(rs, lb, so);
+  for (int k = 0; k < NormIn<S>::PER; ++k) {
+    const int i = t_ + k * NT;
+    n.g[k] = i < S::H ? bf16_to_f32(gain[i]) : 0.f;
+  }
+}
+
+// Block-wide sum of squares from per-thread partials -> r.  ssw: NW floats
+// used only by this call site (so no wave can overwrite a slot another wave
+// of a previous call still reads).
+__device__ __forceinline__ bool norm_finish(float ss, float* ssw, int failed, float h, float* r) {
+  const int t_ = ltid();
+  ss = wave_sum(ss);
+  if (t_ % kWave == 0) ssw[t_ / kWave] = ss;
+  if (block_failed(failed)) return false;
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) tot += ssw[i];
+  *r = rsqrtf(tot / h + kRmsEps);
+  return true;
+}
+
+// Wait for the tagged H-vector x (one bulk round), store x * gain to dst and
+// return the RMSNorm scale of x.
+template <class S>
+__device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned tag, const NormIn<S>& n,
+                                           float* dst, float* ssw, float* r) {
+  constexpr int PER = NormIn<S>::PER;
+  const int tid = ltid();
+  int failed = 0;
+  __syncthreads();  // every wave is done with the LDS of its previous phase
+  u64 wv[PER];
+  Spin sp;
+  while (true) {
+    bool ready = true;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = tid + k * NT;
+      if (i < S::H) {
+        wv[k] = ll_get(src + i);
+        ready &= ll_tag(wv[k]) == tag;
+      }
+    }
+    if (ready) break;
+    if (!sp.step(p.err, p.timeout_ticks)) {
+      failed = 1;
+      break;
     }
   }
-}
-
-// Per-lane partial dot product of the block against vec (LDS).
-template <int KT>
-__device__ __forceinline__ float blk_dot(const Blk<KT>& b, const float* vec) {
-  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
-  const float* hv = vec + (l >> 4) * 8;
-  float acc = 0.f;
-#pragma unroll
-  for (int i = 0; i < Blk<KT>::PER; ++i) {
-    const int kt = w + i * NW;
-    if (KT % NW == 0 || kt < KT) acc = dot8(b.w[i], hv + kt * 32, acc);
-  }
-  return stride_sum<16>(acc);
-}
-
-// Cross-wave sum of per-wave row partials: red[w*16 + r] -> threads 0..15.
-__device__ __forceinline__ float rows_sum(float part, float* red) {
-  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
-  if (l < 16) red[w * 16 + l] = part;
-  __syncthreads();
-  float y = 0.f;
-  if (t_ < 16) {
-#pragma unroll
-    for (int i = 0; i < NW; ++i) y += red[i * 16 + t_];
-  }
-  return y;
-}
-
-// The two bf16 gains of elements 2t, 2t+1 of an H-vector, loaded before the
-// phase's input wait so the load is never on the critical path.
-template <class S>
-__device__ __forceinline__ unsigned gain_pair(const uint16_t* gain) {
-  static_assert(S::H <= 2 * NT, "two elements per thread");
-  const int t_ = ltid();
-  return t_ < S::H / 2 ? reinterpret_cast<const unsigned*>(gain)[t_] : 0u;
-}
-
-// out[i] = xl[i] * rsqrt(mean(xl^2) + eps) * gain[i] (reference rmsnorm.cuh:87-108).
-// Every wave computes the sum of squares itself from LDS (no block reduction).
-template <class S>
-__device__ __forceinline__ void rmsnorm_lds(const float* xl, unsigned gp, float* out) {
-  const int t_ = ltid(), l = t_ % kWave;
   float ss = 0.f;
-#pragma unroll 4
-  for (int i = l; i < S::H; i += kWave) ss = fmaf(xl[i], xl[i], ss);
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / (float)S::H + kRmsEps);
-  if (t_ < S::H / 2) {
-    out[2 * t_] = xl[2 * t_] * r * bf16_lo(gp);
-    out[2 * t_ + 1] = xl[2 * t_ + 1] * r * bf16_hi(gp);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = tid + k * NT;
+    if (i < S::H) {
+      const float v = ll_val(wv[k]);
+      ss = fmaf(v, v, ss);
+      dst[i] = v * n.g[k];
+    }
   }
-  __syncthreads();
+  return norm_finish(ss, ssw, failed, (float)S::H, r);
+}
+
+// Layer 0: the embedding row of `tok` (gathered from the tied LM head).
+template <class S>
+__device__ __forceinline__ void embed_norm(const Params& p, int tok, const NormIn<S>& n, float* dst, float* ssw,
+                                           float* r) {
+  const int tid = ltid();
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NormIn<S>::PER; ++k) {
+    const int i = tid + k * NT;
+    if (i < S::H) {
+      const float v = packed_elem<S::KT_H>(p.lmhead, tok, i);
+      ss = fmaf(v, v, ss);
+      dst[i] = v * n.g[k];
+    }
+  }
+  (void)norm_finish(ss, ssw, 0, (float)S::H, r);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
@@ -192,6 +269,7 @@ __shared__ u64 trace_lds[TRACE_LDS];
 
 __device__ __forceinline__ bool tracing(const Params& p, int t) { return p.trace && t == p.trace_token; }
 
+
 __device__ __forceinline__ void trace_mark(const Params& p, int t, int slot, int which) {
   if (tracing(p, t) && ltid() == 0) trace_lds[slot * 2 + which] = wall_clock64();
 }
@@ -201,7 +279,7 @@ enum Evt : int {
   EV_ATT_READY = 0, EV_ATT_ROPE, EV_ATT_SOFTMAX, EV_ATT_STORED,
   EV_ATT_PARTIAL, EV_ATT_GATHERED, EV_O_READY, EV_O_STORED,
   EV_QKV_STORED, EV_GU_STORED, EV_DN_STORED, EV_DN_READY,
-  EV_ATT_REDUCED, EV_ATT_COMBINED, EV_O_DOT
+  EV_ATT_REDUCED, EV_ATT_COMBINED, EV_MERGE_SCALED, EV_MERGE_DONE
 };
 __device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
   if (tracing(p, t) && layer == p.trace_layer && ltid() == 0)
@@ -244,6 +322,7 @@ template <int B>
 __device__ __forceinline__ bool fetch3(Range a, Range b, Range c, const Params& p) {
   const int tid = ltid();
   int failed = 0;
+  __syncthreads();  // every wave is done with the LDS of its previous phase
   // 1. light wait on sentinels (wave 0 only), for inputs that need more than
   //    one bulk round
   if (a.n + b.n + c.n > B * NT && tid < kWave) {
@@ -278,7 +357,7 @@ __device__ __forceinline__ bool fetch3(Range a, Range b, Range c, const Params& 
       if (!sp.step(p.err, p.timeout_ticks)) failed = 1;
     }
   }
-  if (__syncthreads_or(failed)) return false;
+  if (block_failed(failed)) return false;
   // 2. bulk read with verification
   const int total = a.n + b.n + c.n;
   for (int base = 0; base < total && !failed; base += NT * B) {
@@ -313,7 +392,7 @@ __device__ __forceinline__ bool fetch3(Range a, Range b, Range c, const Params& 
       }
     }
   }
-  return __syncthreads_or(failed) == 0;
+  return !block_failed(failed);
 }
 
 constexpr Range kNoRange = {nullptr, 0, nullptr, 0u, 1};
@@ -522,16 +601,22 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
   __syncthreads();
   // 5. this item's partial over its NW waves: (M, L, acc) per q head.
   constexpr int W = GQA * (D + 2);
+  // Every wave's max is read first (independent LDS reads, no branches); a
+  // wave without positions has max -inf and weight exp(-inf) = 0.  The item's
+  // max is finite (every split has positions).
   if (tid < GQA) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) M = fmaxf(M, sm.mw[i * GQA + tid]);
-    float Lw = 0.f;
+    float mi[NW], li[NW];
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
-      const float mi = sm.mw[i * GQA + tid];
-      if (mi != -INFINITY) Lw = fmaf(__expf(mi - M), sm.lw[i * GQA + tid], Lw);
+      mi[i] = sm.mw[i * GQA + tid];
+      li[i] = sm.lw[i * GQA + tid];
     }
+    float M = mi[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) M = fmaxf(M, mi[i]);
+    float Lw = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) Lw = fmaf(__expf(mi[i] - M), li[i], Lw);
     sm.gm[tid] = M;
     sm.gl[tid] = Lw;
   }
@@ -542,14 +627,17 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
     av[k] = 0.f;
     if (e < GQA * D) {
       const int j = e / D;
-      float M = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < NW; ++i) M = fmaxf(M, sm.mw[i * GQA + j]);
+      float mi[NW], pi[NW];
 #pragma unroll
       for (int i = 0; i < NW; ++i) {
-        const float mi = sm.mw[i * GQA + j];
-        if (mi != -INFINITY) av[k] = fmaf(__expf(mi - M), sm.pv[i * GQA * D + e], av[k]);
+        mi[i] = sm.mw[i * GQA + j];
+        pi[i] = sm.pv[i * GQA * D + e];
       }
+      float M = mi[0];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) M = fmaxf(M, mi[i]);
+#pragma unroll
+      for (int i = 0; i < NW; ++i) av[k] = fmaf(__expf(mi[i] - M), pi[i], av[k]);
     }
   }
   __syncthreads();
@@ -572,23 +660,45 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
   //    normalised attention output of its GQA heads.
   if (nsplit > 1 && !fetch1<8>(prow + W, (nsplit - 1) * W, sm.mbuf, tag_out, p, W)) return false;
   evt(p, tt, layer, EV_ATT_GATHERED);
+  // per-split weights f_q / L (log-sum-exp), one lane per split (q = 0: this
+  // split's own partial), computed once per head
+  if (tid < kWave) {
+#pragma unroll
+    for (int j = 0; j < GQA; ++j) {
+      const bool valid = tid < nsplit;
+      const float mq = tid == 0 ? sm.gm[j] : (valid ? sm.mbuf[(tid - 1) * W + j] : -INFINITY);
+      const float lq = tid == 0 ? sm.gl[j] : (valid ? sm.mbuf[(tid - 1) * W + GQA + j] : 0.f);
+      const float M = wave_max(mq);
+      const float f = valid ? __expf(mq - M) : 0.f;
+      const float Lt = wave_sum(f * lq);
+      if (valid) sm.mscale[tid * GQA + j] = f / Lt;
+    }
+  }
+  __syncthreads();
+  evt(p, tt, layer, EV_MERGE_SCALED);
 #pragma unroll
   for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
     const int e = tid + k * NT;
     if (e < GQA * D) {
       const int j = e / D;
-      float M = sm.gm[j];
-      for (int q = 0; q < nsplit - 1; ++q) M = fmaxf(M, sm.mbuf[q * W + j]);
-      const float f0 = __expf(sm.gm[j] - M);
-      float Lt = f0 * sm.gl[j], o = f0 * av[k];
-      for (int q = 0; q < nsplit - 1; ++q) {
-        const float f = __expf(sm.mbuf[q * W + j] - M);
-        Lt = fmaf(f, sm.mbuf[q * W + GQA + j], Lt);
-        o = fmaf(f, sm.mbuf[q * W + 2 * GQA + e], o);
+      float o = sm.mscale[j] * av[k];
+      // eight splits per step: unconditional (in-bounds) LDS reads issued
+      // together, splits past nsplit selected away
+      for (int q0 = 1; q0 < nsplit; q0 += 8) {
+        float wq[8], xq[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int q = q0 + u < NSPLIT_CAP ? q0 + u : NSPLIT_CAP - 1;
+          wq[u] = sm.mscale[q * GQA + j];
+          xq[u] = sm.mbuf[(q - 1) * W + 2 * GQA + e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) o = q0 + u < nsplit ? fmaf(wq[u], xq[u], o) : o;
       }
-      ll_put(p.attn + (long long)g * GQA * D + e, ll_pack(o / Lt, tag_out));
+      ll_put(p.attn + (long long)g * GQA * D + e, ll_pack(o, tag_out));
     }
   }
+  evt(p, tt, layer, EV_MERGE_DONE);
   return true;
 }
 
@@ -607,7 +717,7 @@ __device__ __forceinline__ bool token_from_slots(const Params& p, u64* slots, un
       }
     best = v > best ? v : best;
   }
-  if (__syncthreads_or(failed)) return false;
+  if (block_failed(failed)) return false;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     const u64 o = __shfl_xor(best, m);
@@ -627,6 +737,8 @@ __device__ __forceinline__ bool token_from_slots(const Params& p, u64* slots, un
 template <class S>
 __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   __shared__ Smem<S> sm;
+  if (threadIdx.x == 0) wg_abort = 0;
+  __syncthreads();
   const int G = gridDim.x, wg = blockIdx.x, tid = threadIdx.x;
   const int w = tid / kWave, l = tid % kWave;
   const int L = p.n_layers;
@@ -639,12 +751,12 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   const int it_gu = first_item(wg, off_gu, G), it_dn = first_item(wg, off_down, G);
   const int it_att = first_item(wg, off_att, G);
 
-  Blk<S::KT_H> rq;      // QKV block
+  Blk<S::KC_H> rq;      // QKV block
   KV<S> rkv;            // attention K/V sub-chunk
-  Blk<S::KT_Q> ro;      // O block
-  Blk<S::KT_H> rg, ru;  // gate / up blocks
-  Blk<S::KT_F> rd;      // down block
-  unsigned gq = 0, gf = 0;  // attn_norm / ffn_norm gain pairs of the current layer
+  Blk<S::KC_Q> ro;      // O block
+  Blk<S::KC_H> rg, ru;  // gate / up blocks
+  Blk<S::KC_F> rd;      // down block
+  NormIn<S> gq, gf;     // attn_norm / ffn_norm gains of this thread's elements
 
   int tok = p.first_token;
   for (int t = 0; t < p.n_tokens; ++t) {
@@ -653,7 +765,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     const unsigned tb = p.tag_base + (unsigned)t * per_token;  // tag of this token's first phase
     if (it_qkv < S::RB_QKV) {
       blk_load(rq, p.layers + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
-      gq = gain_pair<S>(p.norms + S::NORM_ATTN);
+      gains_load(gq, p.norms + S::NORM_ATTN);
     }
     if (t > 0) {
       if (!token_from_slots(p, p.amax + ((t - 1) & 1) * G, tag14(tb - 1u), sm.amax, &tok)) return;
@@ -694,24 +806,22 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         gain_load_qk<S>(rkv, p, layer);
       }
       if (it_qkv < S::RB_QKV) {
-        if (layer > 0 && !fetch1<2>(p.x, S::H, sm.xin, tg_x, p)) return;
-        trace_mark(p, t, slot + 0, 0);
-        if (layer == 0) {
-          for (int i = tid; i < S::H; i += NT) sm.xin[i] = packed_elem<S::KT_H>(p.lmhead, tok, i);
-          __syncthreads();
+        float r;
+        if (layer > 0) {
+          if (!fetch_norm<S>(p, p.x, tg_x, gq, sm.vec_q, sm.ssw[0], &r)) return;
+        } else {
+          embed_norm<S>(p, tok, gq, sm.vec_q, sm.ssw[0], &r);
         }
-        rmsnorm_lds<S>(sm.xin, gq, sm.vec);
+        trace_mark(p, t, slot + 0, 0);
         {  // the prefetched block
-          const float y = rows_sum(blk_dot(rq, sm.vec), sm.red);
-          if (tid < 16) ll_put(p.qkv + it_qkv * 16 + tid, ll_pack(y, tg));
+          const float y = blk_dot(rq, sm.vec_q);
+          store_rows(sm.rowbuf[0], p.qkv + it_qkv * 16, y * r, tg);
           evt(p, t, layer, EV_QKV_STORED);
-          __syncthreads();
         }
         for (int rb = it_qkv + G; rb < S::RB_QKV; rb += G) {  // grids smaller than the block count
           blk_load(rq, wl + S::OFF_QKV + (long long)rb * S::KT_H * 64);
-          const float y = rows_sum(blk_dot(rq, sm.vec), sm.red);
-          if (tid < 16) ll_put(p.qkv + rb * 16 + tid, ll_pack(y, tg));
-          __syncthreads();
+          const float y = blk_dot(rq, sm.vec_q);
+          if (row_owner()) ll_put(p.qkv + rb * 16 + blk_row(), ll_pack(y * r, tg));
         }
         trace_mark(p, t, slot + 0, 1);
       }
@@ -734,97 +844,86 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         const u32x4* gp = wl + S::OFF_GU + (long long)(2 * it_gu) * S::KT_H * 64;
         blk_load(rg, gp);
         blk_load(ru, gp + S::KT_H * 64);
-        gf = gain_pair<S>(nrm + S::NORM_FFN);
+        gains_load(gf, nrm + S::NORM_FFN);
       }
       if (it_o < S::RB_H) {
-        if (!fetch3<3>(Range{p.attn, S::QD, sm.vec, tg + 1u, 16},
-                       layer > 0 ? Range{p.x + it_o * 16, 16, sm.xres, tg_x, 16} : kNoRange, kNoRange, p))
+        if (!fetch3<3>(Range{p.attn, S::QD, sm.vec_o, tg + 1u, 16},
+                       layer > 0 ? Range{p.x + it_o * 16, 16, sm.xres_o, tg_x, 16} : kNoRange, kNoRange, p))
           return;
         trace_mark(p, t, slot + 2, 0);
         evt(p, t, layer, EV_O_READY);
-      }
-      if (it_o < S::RB_H) {  // the prefetched block
-        const float part = blk_dot(ro, sm.vec);
-        evt(p, t, layer, EV_O_DOT);
-        const float y = rows_sum(part, sm.red);
-        if (tid < 16) {
-          const int row = it_o * 16 + tid;
-          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres[tid];
-          ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
+        const float y = blk_dot(ro, sm.vec_o);
+        {
+          const int row = it_o * 16 + blk_row();
+          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres_o[blk_row()];
+          store_rows(sm.rowbuf[1], p.x + it_o * 16, xo + y, tg + 2u);
         }
         evt(p, t, layer, EV_O_STORED);
-        __syncthreads();
         trace_mark(p, t, slot + 2, 1);
       }
       for (int rb = it_o + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
         blk_load(ro, wl + S::OFF_O + (long long)rb * S::KT_Q * 64);
-        if (layer > 0 && !fetch1<1>(p.x + rb * 16, 16, sm.xres, tg_x, p)) return;
-        const float y = rows_sum(blk_dot(ro, sm.vec), sm.red);
-        if (tid < 16) {
-          const int row = rb * 16 + tid;
-          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres[tid];
+        if (layer > 0 && !fetch1<1>(p.x + rb * 16, 16, sm.xres_o, tg_x, p)) return;
+        const float y = blk_dot(ro, sm.vec_o);
+        if (row_owner()) {
+          const int row = rb * 16 + blk_row();
+          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres_o[blk_row()];
           ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
         }
-        __syncthreads();
       }
       // ---------------- P4: gate/up + SiLU (prefetch: down)
       if (it_dn < S::RB_H) blk_load(rd, wl + S::OFF_DOWN + (long long)it_dn * S::KT_F * 64);
       if (it_gu < S::RB_F) {
-        if (!fetch1<2>(p.x, S::H, sm.xin, tg + 2u, p)) return;
+        float r;
+        if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return;
         trace_mark(p, t, slot + 3, 0);
-        rmsnorm_lds<S>(sm.xin, gf, sm.vec);
         {  // the prefetched block pair
-          const float yg = rows_sum(blk_dot(rg, sm.vec), sm.red);
-          const float yu = rows_sum(blk_dot(ru, sm.vec), sm.red + NW * 16);
-          if (tid < 16) ll_put(p.act + it_gu * 16 + tid, ll_pack(silu_mul(yg, yu), tg + 3u));
+          const float yg = blk_dot(rg, sm.vec_g);
+          const float yu = blk_dot(ru, sm.vec_g);
+          store_rows(sm.rowbuf[2], p.act + it_gu * 16, silu_mul(yg * r, yu * r), tg + 3u);
           evt(p, t, layer, EV_GU_STORED);
-          __syncthreads();
         }
         for (int pr = it_gu + G; pr < S::RB_F; pr += G) {  // grids smaller than the block count
           const u32x4* gp = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
           blk_load(rg, gp);
           blk_load(ru, gp + S::KT_H * 64);
-          const float yg = rows_sum(blk_dot(rg, sm.vec), sm.red);
-          const float yu = rows_sum(blk_dot(ru, sm.vec), sm.red + NW * 16);
-          if (tid < 16) ll_put(p.act + pr * 16 + tid, ll_pack(silu_mul(yg, yu), tg + 3u));
-          __syncthreads();
+          const float yg = blk_dot(rg, sm.vec_g);
+          const float yu = blk_dot(ru, sm.vec_g);
+          if (row_owner()) ll_put(p.act + pr * 16 + blk_row(), ll_pack(silu_mul(yg * r, yu * r), tg + 3u));
         }
         trace_mark(p, t, slot + 3, 1);
       }
       // ---------------- P5: down projection + residual (prefetch: next QKV + attn gains)
       if (layer + 1 < L && it_qkv < S::RB_QKV) {
         blk_load(rq, wl + S::U_LAYER + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
-        gq = gain_pair<S>(nrm + S::NORM_STRIDE + S::NORM_ATTN);
+        gains_load(gq, nrm + S::NORM_STRIDE + S::NORM_ATTN);
       }
       if (it_dn < S::RB_H) {
-        if (!fetch3<7>(Range{p.act, S::F, sm.vec, tg + 3u, 16}, Range{p.x + it_dn * 16, 16, sm.xres, tg + 2u, 16},
-                       kNoRange, p))
+        if (!fetch3<7>(Range{p.act, S::F, sm.vec_d, tg + 3u, 16},
+                       Range{p.x + it_dn * 16, 16, sm.xres_d, tg + 2u, 16}, kNoRange, p))
           return;
         trace_mark(p, t, slot + 4, 0);
         evt(p, t, layer, EV_DN_READY);
-        // the prefetched block
-        const float y = rows_sum(blk_dot(rd, sm.vec), sm.red);
-        if (tid < 16) {
-          const int row = it_dn * 16 + tid;
-          const float xn = sm.xres[tid] + y;
-          ll_put(p.x + row, ll_pack(xn, tg + 4u));
-          if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
+        const float y = blk_dot(rd, sm.vec_d);
+        {
+          const int row = it_dn * 16 + blk_row();
+          const float xn = sm.xres_d[blk_row()] + y;
+          if (p.dbg_layers && row_owner()) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
+          store_rows(sm.rowbuf[3], p.x + it_dn * 16, xn, tg + 4u);
         }
         evt(p, t, layer, EV_DN_STORED);
-        __syncthreads();
         trace_mark(p, t, slot + 4, 1);
       }
       for (int rb = it_dn + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
         blk_load(rd, wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64);
-        if (!fetch1<1>(p.x + rb * 16, 16, sm.xres, tg + 2u, p)) return;
-        const float y = rows_sum(blk_dot(rd, sm.vec), sm.red);
-        if (tid < 16) {
-          const int row = rb * 16 + tid;
-          const float xn = sm.xres[tid] + y;
+        if (!fetch1<1>(p.x + rb * 16, 16, sm.xres_d, tg + 2u, p)) return;
+        const float y = blk_dot(rd, sm.vec_d);
+        if (row_owner()) {
+          const int row = rb * 16 + blk_row();
+          const float xn = sm.xres_d[blk_row()] + y;
           ll_put(p.x + row, ll_pack(xn, tg + 4u));
           if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
         }
-        __syncthreads();
       }
     }
     // ---------------- final norm + tied LM head + per-workgroup argmax
@@ -832,10 +931,11 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     {
       const int tid = ltid(), w = tid / kWave, l = tid % kWave;
       const unsigned tl = tb + (unsigned)(PHASES_PER_LAYER * L);
-      const unsigned gfin = gain_pair<S>(p.final_norm);
-      if (!fetch1<2>(p.x, S::H, sm.xin, tl - 1u, p)) return;
+      NormIn<S> gfin;
+      gains_load(gfin, p.final_norm);
+      float rn;
+      if (!fetch_norm<S>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return;
       trace_mark(p, t, PHASES_PER_LAYER * L, 0);
-      rmsnorm_lds<S>(sm.xin, gfin, sm.vec);
       const long long nb = p.vocab / 16;
       const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G;
       u64 best = 0ull;
@@ -844,7 +944,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         // re-derived per block so the LDS reads of the hidden vector are not
         // hoisted out of the block loop (256 floats per lane would not fit)
         const unsigned lo = lane_id();
-        const float* hv = sm.vec + (lo >> 4) * 8;
+        const float* hv = sm.vec_l + (lo >> 4) * 8;
         const auto rs = make_rsrc(p.lmhead + b * S::KT_H * 64);  // wave-uniform block base
         float acc = 0.f;
         constexpr int U = 16;
@@ -858,7 +958,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           for (int u = 0; u < U; ++u)
             if (k0 + u < S::KT_H) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
         }
-        acc = stride_sum<16>(acc);
+        acc = stride_sum<16>(acc) * rn;
         if (l < 16) {
           const unsigned idx = (unsigned)(b * 16 + l);
           if (p.dbg_logits) p.dbg_logits[idx] = acc;
