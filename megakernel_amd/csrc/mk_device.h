@@ -249,6 +249,24 @@ __device__ __forceinline__ u64 ll_get(u64* p) { return __hip_atomic_load(p, __AT
 __device__ __forceinline__ unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
 __device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigned)w); }
 
+// Packed pair: two values in one tagged word, each rounded to a 19-bit
+// mantissa (relative error <= 2^-20) with a 4-bit tag in its low bits, so a
+// large vector needs half the words.  The 4-bit tag (1..15, never 0) only has
+// to differ from the tag of the previous write to the same word; the buffer
+// is cleared (tag 0) before every launch.
+__device__ __forceinline__ unsigned tag4(unsigned tag) { return tag % 15u + 1u; }
+__device__ __forceinline__ unsigned pk_half(float v, unsigned t4) {
+  return ((__float_as_uint(v) + 8u) & ~15u) | t4;
+}
+__device__ __forceinline__ u64 pk_pack(float a, float b, unsigned t4) {
+  return ((u64)pk_half(b, t4) << 32) | pk_half(a, t4);
+}
+__device__ __forceinline__ bool pk_ready(u64 w, unsigned t4) {
+  return ((unsigned)w & 15u) == t4 && ((unsigned)(w >> 32) & 15u) == t4;
+}
+__device__ __forceinline__ float pk_lo(u64 w) { return __uint_as_float((unsigned)w & ~15u); }
+__device__ __forceinline__ float pk_hi(u64 w) { return __uint_as_float((unsigned)(w >> 32) & ~15u); }
+
 // Bounded spinning of one thread.  step() returns false when the wait must be
 // abandoned (this thread timed out, or another workgroup already failed).
 struct Spin {

@@ -152,6 +152,14 @@ __device__ __forceinline__ void store_rows(float* rowbuf, u64* dst16, float v, u
   if (t_ < 16) ll_put(dst16 + t_, ll_pack(rowbuf[t_], tag));
 }
 
+// The same for a packed-pair vector: 8 words of two values each.
+__device__ __forceinline__ void store_rows_pk(float* rowbuf, u64* dst8, float v, unsigned t4) {
+  if (row_owner()) rowbuf[blk_row()] = v;
+  __syncthreads();
+  const int t_ = ltid();
+  if (t_ < 8) ll_put(dst8 + t_, pk_pack(rowbuf[2 * t_], rowbuf[2 * t_ + 1], t4));
+}
+
 // Element of the tile-layout LM head / embedding (row, col).
 template <int KT>
 __device__ __forceinline__ float packed_elem(const u32x4* base, int row, int col) {
@@ -234,6 +242,49 @@ __device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned t
     }
   }
   return norm_finish(ss, ssw, failed, (float)S::H, r);
+}
+
+// Wait for the packed-pair SiLU(gate)*up vector (F/2 words) and the 16
+// residual rows of this workgroup's down block, in one bulk round.
+template <class S>
+__device__ __forceinline__ bool fetch_act(const Params& p, unsigned t4, u64* xrows, unsigned xtag, float* act,
+                                          float* xres) {
+  constexpr int NPK = S::F / 2, TOT = NPK + 16, PER = (TOT + NT - 1) / NT;
+  const int tid = ltid();
+  int failed = 0;
+  __syncthreads();  // every wave is done with the LDS of its previous phase
+  u64 wv[PER];
+  Spin sp;
+  while (true) {
+    bool ready = true;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = tid + k * NT;
+      if (i < NPK) {
+        wv[k] = ll_get(p.act + i);
+        ready &= pk_ready(wv[k], t4);
+      } else if (i < TOT) {
+        wv[k] = ll_get(xrows + (i - NPK));
+        ready &= ll_tag(wv[k]) == xtag;
+      }
+    }
+    if (ready) break;
+    if (!sp.step(p.err, p.timeout_ticks)) {
+      failed = 1;
+      break;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = tid + k * NT;
+    if (i < NPK) {
+      act[2 * i] = pk_lo(wv[k]);
+      act[2 * i + 1] = pk_hi(wv[k]);
+    } else if (i < TOT) {
+      xres[i - NPK] = ll_val(wv[k]);
+    }
+  }
+  return !block_failed(failed);
 }
 
 // Layer 0: the embedding row of `tok` (gathered from the tied LM head).
@@ -880,7 +931,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         {  // the prefetched block pair
           const float yg = blk_dot(rg, sm.vec_g);
           const float yu = blk_dot(ru, sm.vec_g);
-          store_rows(sm.rowbuf[2], p.act + it_gu * 16, silu_mul(yg * r, yu * r), tg + 3u);
+          store_rows_pk(sm.rowbuf[2], p.act + it_gu * 8, silu_mul(yg * r, yu * r), tag4(tg + 3u));
           evt(p, t, layer, EV_GU_STORED);
         }
         for (int pr = it_gu + G; pr < S::RB_F; pr += G) {  // grids smaller than the block count
@@ -889,7 +940,8 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           blk_load(ru, gp + S::KT_H * 64);
           const float yg = blk_dot(rg, sm.vec_g);
           const float yu = blk_dot(ru, sm.vec_g);
-          if (row_owner()) ll_put(p.act + pr * 16 + blk_row(), ll_pack(silu_mul(yg * r, yu * r), tg + 3u));
+          store_rows_pk(sm.rowbuf[2], p.act + pr * 8, silu_mul(yg * r, yu * r), tag4(tg + 3u));
+          __syncthreads();
         }
         trace_mark(p, t, slot + 3, 1);
       }
@@ -899,9 +951,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         gains_load(gq, nrm + S::NORM_STRIDE + S::NORM_ATTN);
       }
       if (it_dn < S::RB_H) {
-        if (!fetch3<7>(Range{p.act, S::F, sm.vec_d, tg + 3u, 16},
-                       Range{p.x + it_dn * 16, 16, sm.xres_d, tg + 2u, 16}, kNoRange, p))
-          return;
+        if (!fetch_act<S>(p, tag4(tg + 3u), p.x + it_dn * 16, tg + 2u, sm.vec_d, sm.xres_d)) return;
         trace_mark(p, t, slot + 4, 0);
         evt(p, t, layer, EV_DN_READY);
         const float y = blk_dot(rd, sm.vec_d);
