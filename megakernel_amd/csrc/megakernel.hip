@@ -73,11 +73,20 @@ __global__ void synth_fill_kernel(uint16_t* __restrict__ dst, unsigned long long
     dst[i] = synth_bf16(key, i, c, add_one);
 }
 
-// Synthetic KV prefill straight into the cache layout [L][2][NKV][S][D] for
-// positions [0, len).  Stream id KV_ID_BASE + 2*layer + kv; element index
-// (t * NKV + g) * D + d (matches oracle/synth.py:kv_prefill_bits).
-__global__ void synth_kv_kernel(uint16_t* __restrict__ kv, int L, int NKV, int S, int D, int len,
-                                unsigned long long seed, float c) {
+// Device KV cache addressing (see mk_kernel.h): K [L][NKV][s_pad][D], V^T
+// blocks [L][NKV][s_pad/32][D][32], both bf16; kv points at K, kvt at V^T.
+__device__ __forceinline__ long long k_index(int l, int g, long long t, int d, int NKV, int s_pad, int D) {
+  return (((long long)l * NKV + g) * s_pad + t) * D + d;
+}
+__device__ __forceinline__ long long vt_index(int l, int g, long long t, int d, int NKV, int s_pad, int D) {
+  return ((long long)l * NKV + g) * (long long)s_pad * D + (t / 32) * 32LL * D + (long long)d * 32 + (t % 32);
+}
+
+// Synthetic KV prefill of positions [0, len).  Stream id KV_ID_BASE +
+// 2*layer + kv; element index (t * NKV + g) * D + d (matches
+// oracle/synth.py:kv_prefill_bits).
+__global__ void synth_kv_kernel(uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt, int L, int NKV, int s_pad,
+                                int D, int len, unsigned long long seed, float c) {
   const unsigned long long per = (unsigned long long)len * NKV * D;
   const unsigned long long total = per * 2ull * L;
   for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -88,7 +97,28 @@ __global__ void synth_kv_kernel(uint16_t* __restrict__ kv, int L, int NKV, int S
     const int g = (int)((e / D) % NKV);
     const long long t = (long long)(e / ((unsigned long long)D * NKV));
     const unsigned long long key = sm_h(seed, 0x40000000ull + plane);
-    kv[((plane * NKV + g) * (unsigned long long)S + t) * D + d] = synth_bf16(key, e, c, 0);
+    const int l = (int)(plane / 2);
+    const uint16_t v = synth_bf16(key, e, c, 0);
+    if (plane % 2 == 0) kv[k_index(l, g, t, d, NKV, s_pad, D)] = v;
+    else kvt[vt_index(l, g, t, d, NKV, s_pad, D)] = v;
+  }
+}
+
+// Copy between the reference layout [L][2][NKV][len][D] (buf) and the cache:
+// to_cache = 1 imports, 0 exports.
+__global__ void kv_convert_kernel(uint16_t* __restrict__ buf, uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt,
+                                  int L, int NKV, int s_pad, int D, int len, int to_cache) {
+  const unsigned long long total = 2ull * L * NKV * (unsigned long long)len * D;
+  for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (unsigned long long)gridDim.x * blockDim.x) {
+    const int d = (int)(i % D);
+    const long long t = (long long)((i / D) % len);
+    const int g = (int)((i / ((unsigned long long)D * len)) % NKV);
+    const unsigned long long plane = i / ((unsigned long long)D * len * NKV);  // layer*2 + kv
+    const int l = (int)(plane / 2);
+    uint16_t* c = plane % 2 == 0 ? kv + k_index(l, g, t, d, NKV, s_pad, D) : kvt + vt_index(l, g, t, d, NKV, s_pad, D);
+    if (to_cache) *c = buf[i];
+    else buf[i] = *c;
   }
 }
 
@@ -135,6 +165,8 @@ struct Handle {
   unsigned tag_base = 1;  // tag of the next launch's first phase (0 never valid)
   int pos = 0;
   long long kv_bytes = 0;
+  int s_pad = 0;               // KV capacity rounded up to whole 32-position blocks
+  uint16_t* kvt = nullptr;     // V^T region inside the kv allocation
   hipError_t (*launch)(Handle*, const Params&) = nullptr;
 };
 
@@ -204,8 +236,10 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   HIPCHK(hipMalloc(&h->norms, (size_t)s.norm_stride * 2 * h->L), -1);
   HIPCHK(hipMalloc(&h->final_norm, (size_t)s.H * 2), -1);
   HIPCHK(hipMalloc(&h->lmhead, (size_t)h->V * s.H * 2), -1);
-  h->kv_bytes = 2LL * h->L * s.NKV * (long long)h->S * s.D * 2;
+  h->s_pad = (h->S + 31) / 32 * 32;
+  h->kv_bytes = 2LL * h->L * s.NKV * (long long)h->s_pad * s.D * 2;
   HIPCHK(hipMalloc(&h->kv, h->kv_bytes), -1);
+  h->kvt = h->kv + (long long)h->L * s.NKV * h->s_pad * s.D;
   HIPCHK(hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream), -1);
   // tagged activation words (zero = tag 0, never a valid tag)
   u64** tagged[6] = {&h->x, &h->qkv, &h->part, &h->attn, &h->act, &h->amax};
@@ -336,6 +370,8 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.final_norm = h->final_norm;
   p.lmhead = h->lmhead;
   p.kv = h->kv;
+  p.kvt = h->kvt;
+  p.s_pad = h->s_pad;
   const unsigned per_token = (unsigned)(5 * h->L + 1);
   if ((unsigned long long)h->tag_base + (unsigned long long)n * per_token >= 0x7fffffffull) {
     if (clear_tagged_state(h)) return -1;  // restart the tag sequence well before it wraps
@@ -520,21 +556,40 @@ int megakernel_set_pos(void* handle, int pos) {
   return 0;
 }
 
+// Converts through a device staging buffer in the reference layout.
+static int kv_transfer(Handle* h, void* host_kv, int len, int to_cache) {
+  const size_t bytes = (size_t)2 * h->L * h->sh.NKV * (size_t)len * h->sh.D * 2;
+  void* stage = nullptr;
+  HIPCHK(hipMalloc(&stage, bytes), -1);
+  int rc = -1;
+  do {
+    if (to_cache && hipMemcpy(stage, host_kv, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+      mk::set_err("KV upload failed");
+      break;
+    }
+    hipLaunchKernelGGL(mk::kv_convert_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                       h->kv, h->kvt, h->L, h->sh.NKV, h->s_pad, h->sh.D, len, to_cache);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(h->stream) != hipSuccess) {
+      mk::set_err("KV layout conversion failed");
+      break;
+    }
+    if (!to_cache && hipMemcpy(host_kv, stage, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+      mk::set_err("KV download failed");
+      break;
+    }
+    rc = 0;
+  } while (0);
+  (void)hipFree(stage);
+  return rc;
+}
+
 int megakernel_set_kv(void* handle, const void* host_kv, int len) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h || !host_kv || len < 0 || len > h->S) {
     mk::set_err("invalid set_kv arguments (len %d)", len);
     return -1;
   }
-  const size_t row = (size_t)len * h->sh.D * 2;
-  if (len > 0) {
-    hipError_t e = hipMemcpy2D(h->kv, (size_t)h->S * h->sh.D * 2, host_kv, row, row,
-                               (size_t)h->L * 2 * h->sh.NKV, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-      mk::set_err("set_kv copy failed: %s", hipGetErrorString(e));
-      return -1;
-    }
-  }
+  if (len > 0 && kv_transfer(h, const_cast<void*>(host_kv), len, 1)) return -1;
   h->pos = len;
   return 0;
 }
@@ -545,15 +600,7 @@ int megakernel_get_kv(void* handle, void* host_kv, int len) {
     mk::set_err("invalid get_kv arguments (len %d)", len);
     return -1;
   }
-  const size_t row = (size_t)len * h->sh.D * 2;
-  if (len > 0) {
-    hipError_t e = hipMemcpy2D(host_kv, row, h->kv, (size_t)h->S * h->sh.D * 2, row,
-                               (size_t)h->L * 2 * h->sh.NKV, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) {
-      mk::set_err("get_kv copy failed: %s", hipGetErrorString(e));
-      return -1;
-    }
-  }
+  if (len > 0 && kv_transfer(h, host_kv, len, 0)) return -1;
   return 0;
 }
 
@@ -565,8 +612,8 @@ int megakernel_fill_kv_synthetic(void* handle, int len, unsigned long long seed,
   }
   if (len > 0) {
     const float c = (float)(std * sqrt(3.0) / 65536.0);
-    hipLaunchKernelGGL(mk::synth_kv_kernel, dim3(4096), dim3(256), 0, h->stream, h->kv, h->L, h->sh.NKV, h->S,
-                       h->sh.D, len, seed, c);
+    hipLaunchKernelGGL(mk::synth_kv_kernel, dim3(4096), dim3(256), 0, h->stream, h->kv, h->kvt, h->L, h->sh.NKV,
+                       h->s_pad, h->sh.D, len, seed, c);
     HIPCHK(hipGetLastError(), -1);
     HIPCHK(hipStreamSynchronize(h->stream), -1);
   }

@@ -7,6 +7,8 @@
 namespace mk {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
@@ -28,6 +30,31 @@ __host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 
 // 8 bf16 (one 16-byte unit) dotted with 8 fp32 values.
+// x = hi + mid + lo, three bf16 parts taken by truncation: hi holds the top
+// 8 significant bits of x, mid the next 8 of the (exact) remainder, lo the
+// rest, which has at most 8 significant bits -- so the split is exact (up to
+// underflow) and bf16 x bf16 products on the matrix cores, exact in fp32,
+// reproduce an fp32 operand.  Results are the raw 32-bit patterns whose upper
+// halves are the bf16 parts.
+struct Split3 {
+  unsigned hi, mid, lo;
+};
+__device__ __forceinline__ Split3 split3(float v) {
+  const unsigned u = __float_as_uint(v);
+  const float r1 = v - __uint_as_float(u & 0xffff0000u);
+  const unsigned u1 = __float_as_uint(r1);
+  const float r2 = r1 - __uint_as_float(u1 & 0xffff0000u);
+  return Split3{u, u1, __float_as_uint(r2)};
+}
+// upper halves of a (low 16 bits of the result) and b (high 16 bits)
+__device__ __forceinline__ unsigned pack_hi16(unsigned a, unsigned b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
+  const Split3 t = split3(v);
+  hi = (uint16_t)(t.hi >> 16);
+  mid = (uint16_t)(t.mid >> 16);
+  lo = (uint16_t)(t.lo >> 16);
+}
+
 __device__ __forceinline__ float dot8(u32x4 w, const float* h, float acc) {
   acc = fmaf(bf16_lo(w.x), h[0], acc);
   acc = fmaf(bf16_hi(w.x), h[1], acc);

@@ -35,10 +35,6 @@ constexpr int NT = 512;               // threads per workgroup (8 waves)
 constexpr int NW = NT / kWave;
 constexpr int PHASES_PER_LAYER = 5;
 constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
-#ifndef MK_KV_ROWS
-#define MK_KV_ROWS 4
-#endif
-constexpr int KV_ROWS = MK_KV_ROWS;            // K/V register rows per lane per attention sub-chunk
 constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
 __device__ __forceinline__ unsigned tag14(unsigned tag) { return tag % 16383u + 1u; }
 constexpr int IDX_BITS = 18;          // ... and an 18-bit vocabulary index
@@ -49,13 +45,14 @@ struct Params {
   const uint16_t* norms;      // [L][NORM_STRIDE] bf16 gains
   const uint16_t* final_norm; // [H] bf16
   const u32x4* lmhead;        // packed tied embedding [V/16][KT_H][64]
-  uint16_t* kv;               // [L][2][NKV][max_seq][D] bf16
+  uint16_t* kv;               // K cache [L][NKV][s_pad][D] bf16
+  uint16_t* kvt;              // V cache, transposed blocks [L][NKV][s_pad/32][D][32] bf16
   u64* x;                     // [H] residual stream (tagged)
   u64* qkv;                   // [QKV] projections of the current layer (tagged)
   u64* part;                  // [NKV][nsplit_max][GQA*(D+2)] split partials (tagged):
                               //   m[GQA], l[GQA], acc[GQA][D] (unnormalised)
   u64* attn;                  // [QD] merged attention output (tagged)
-  u64* act;                   // [F] silu(gate)*up (tagged)
+  u64* act;                   // [F/2] silu(gate)*up (packed pairs)
   u64* amax;                  // [2][G] per-workgroup argmax words (token parity)
   int* out_tokens;            // [n_tokens]
   int* err;                   // error word
@@ -67,7 +64,7 @@ struct Params {
   const float* inv_freq;      // [D/2] RoPE inverse frequencies
   u64 timeout_ticks;
   unsigned tag_base;          // tag of the first phase of this launch
-  int n_layers, vocab, max_seq;
+  int n_layers, vocab, max_seq, s_pad;
   int pos0, n_tokens, first_token;
   int nsplit_max, chunk_min;
   int trace_token;
@@ -86,6 +83,8 @@ struct Smem {
   float ssw[3][NW];                   // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
   float rowbuf[4][16];                // a block's 16 results, stored by one wave
   float qk[(S::GQA + 2) * S::D];      // q heads, k, v of the current position
+  __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score B operand
+  __attribute__((aligned(16))) uint16_t pb[NW][16][32];  // attention: weight parts, output B operand
   u32x4 kvcur[2][S::D / 8];           // bf16 K/V of the current position
   float pv[NW * S::GQA * S::D];       // attention: per-wave unnormalised outputs
   float mw[NW * S::GQA], lw[NW * S::GQA];  // attention: per-wave max / sum
@@ -454,46 +453,64 @@ __device__ __forceinline__ bool fetch1(u64* src, int n, float* dst, unsigned tag
 }
 
 // ------------------------------------------------------------ attention
-// Work item (kv head g, split s) covers positions [t0, t1).  Lane l of wave w
-// handles dims (l % LPP) * 8 .. +8 of position t0 + sub*SUB + r*NW*PPW + w*PPW + l/LPP.
+// KV cache on the device (the C ABI's set/get convert from/to the reference's
+// [L][2][NKV][S][D] layout):
+//   K:  [L][NKV][S_pad][D] bf16, row-major per position;
+//   V^T: [L][NKV][S_pad/32][D][32] bf16, 32-position blocks with each dim's
+//        32 values contiguous,
+// so both products of a 32-position block run on the matrix cores
+// (v_mfma_f32_16x16x32_bf16) with the cache bytes as the A operand:
+//   scores^T[pos][col] = K[pos][:] . Qb[:][col]   (A = K rows, k = dims)
+//   out^T[dim][col]    = V^T[dim][:] . Pb[:][col] (A = V^T rows, k = positions)
+// Columns col = 4 j + part carry q head j (resp. its softmax weights) split
+// into three bf16 parts hi + mid + lo, which reproduces fp32 activations; the
+// three output columns of a head are summed.
+// A work item (kv head g, split s) covers positions [t0, t1), t0 a multiple of
+// 32; wave w takes the item's blocks w, w + NW, ...
 template <class S>
 struct KV {
-  static constexpr int LPP = S::D / 8, PPW = kWave / LPP, SUB = KV_ROWS * NW * PPW;
-  u32x4 k[KV_ROWS], v[KV_ROWS];
+  static constexpr int KC = S::D / 32;  // k-steps of the score product
+  static constexpr int DT = S::D / 16;  // dim tiles of the output product
+  u32x4 k[2][KC];  // K of the wave's block: [16-position half][k-step]
+  u32x4 v[DT];     // V^T of the block: [dim tile]
   uint16_t gn[S::D / kWave];  // QK-norm gain(s) of this lane's dim(s) for its wave's head
 };
 
+// u32x4 holding 8 bf16 with element e (0..7) replaced by v (register-only).
+__device__ __forceinline__ u32x4 set_bf16(u32x4 x, int e, uint16_t v) {
+  const unsigned lo_mask = (e & 1) ? 0x0000ffffu : 0xffff0000u;
+  const unsigned put = (e & 1) ? ((unsigned)v << 16) : (unsigned)v;
+  u32x4 r = x;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) r[c] = (c == (e >> 1)) ? ((x[c] & lo_mask) | put) : x[c];
+  return r;
+}
+
+__device__ __forceinline__ long long kt_base(const Params& p, int layer, int g, int nkv, int d) {
+  return ((long long)layer * nkv + g) * (long long)p.s_pad * d;
+}
+
+// KV cache loads use agent-scope (sc1) reads: positions appended by another
+// workgroup in an earlier token must not be served from a stale L2 line.
+__device__ __forceinline__ u32x4 buf_ld_kv(__amdgpu_buffer_rsrc_t rs, unsigned voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0u, 16 | 2);
+}
+
+// Loads block `blk` of positions (starting at position 32 blk) for this wave.
 template <class S>
-__device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, int g, int t0, int t1, int pos,
-                                        int sub) {
-  constexpr int D = S::D, LPP = KV<S>::LPP, PPW = KV<S>::PPW;
-  const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
-  const int c = l % LPP, po = l / LPP;
-  const uint16_t* kb = p.kv + ((long long)(layer * 2 + 0) * S::NKV + g) * (long long)p.max_seq * D + c * 8;
-  const uint16_t* vb = p.kv + ((long long)(layer * 2 + 1) * S::NKV + g) * (long long)p.max_seq * D + c * 8;
-  // Rows past the split, and `pos` itself (taken from LDS), load position
-  // (pos + 1) mod max_seq instead -- settled data nobody writes during this
-  // token -- and are zeroed, so every lane issues the same unconditional loads.
-  const int tsafe = (pos + 1) % p.max_seq;
-  const auto rk = make_rsrc(kb), rv = make_rsrc(vb);
-  u32x4 kk[KV_ROWS], vv[KV_ROWS];
-  bool ok[KV_ROWS];
+__device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, int g, int blk) {
+  constexpr int D = S::D;
+  const unsigned l = lane_id();
+  const long long base = kt_base(p, layer, g, S::NKV, D);
+  const auto rk = make_rsrc(p.kv + base + (long long)blk * 32 * D);
+  const auto rv = make_rsrc(p.kvt + base + (long long)blk * 32 * D);
 #pragma unroll
-  for (int i = 0; i < KV_ROWS; ++i) {
-    const int t = t0 + sub * KV<S>::SUB + i * NW * PPW + w * PPW + po;
-    ok[i] = (t < t1 && t != pos);
-    const unsigned ta = (unsigned)(ok[i] ? t : tsafe);
-    // byte offset from the uniform (layer, head) base: position * D + dim chunk
-    const unsigned off = (ta * (unsigned)D + (unsigned)c * 8u) * 2u;
-    kk[i] = buf_ld_nt(rk, off, 0u);
-    vv[i] = buf_ld_nt(rv, off, 0u);
-  }
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-  for (int i = 0; i < KV_ROWS; ++i) {
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    r.k[i] = ok[i] ? kk[i] : z;
-    r.v[i] = ok[i] ? vv[i] : z;
-  }
+    for (int kc = 0; kc < KV<S>::KC; ++kc)
+      r.k[h][kc] = buf_ld_kv(rk, ((16u * h + (l & 15u)) * D + 32u * kc + 8u * (l >> 4)) * 2u);
+#pragma unroll
+  for (int dt = 0; dt < KV<S>::DT; ++dt) r.v[dt] = buf_ld_kv(rv, ((16u * dt + (l & 15u)) * 32u + 8u * (l >> 4)) * 2u);
 }
 
 // QK-norm gains of this lane's dims: waves 0..GQA-1 normalise q heads, wave
@@ -506,18 +523,25 @@ __device__ __forceinline__ void gain_load_qk(KV<S>& r, const Params& p, int laye
   for (int c = 0; c < S::D / kWave; ++c) r.gn[c] = g[l + c * kWave];
 }
 
+// The first block of this wave's share of an item (or block 0 of the item,
+// as harmless valid addresses, when the wave has none).
+__device__ __forceinline__ int first_block(int t0, int t1) {
+  const int b0 = t0 / 32, nb = (t1 - t0 + 31) / 32, w = wave_id();
+  return b0 + (w < nb ? w : 0);
+}
+
 // Inputs are already fetched into sm.qk (q heads | k | v).  Writes the split's
 // (max, sum, unnormalised output) words for the GQA heads of group g.
 template <class S>
 __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int layer, int pos, int g, int s,
                                   int nsplit, int t0, int t1, unsigned tag_out, int tt) {
-  constexpr int D = S::D, GQA = S::GQA, LPP = KV<S>::LPP, PPW = KV<S>::PPW, DPL = D / kWave;
+  constexpr int D = S::D, GQA = S::GQA, DPL = D / kWave, KC = KV<S>::KC, DT = KV<S>::DT;
+  static_assert(GQA <= 4, "q heads of a group fit the 16 MFMA columns (4 per head)");
   const int tid = ltid(), w = tid / kWave, l = tid % kWave;
-  const uint16_t* nrm = p.norms + (long long)layer * S::NORM_STRIDE;
   // 1. per-head RMSNorm (reference rmsnorm.cuh:57-84) + RoPE rotate-half
   //    (attention.cuh:22-44) of the q heads and the k head, one wave per head,
-  //    in registers; lane l holds dims l + 64 c.
-  (void)nrm;
+  //    in registers; lane l holds dims l + 64 c.  q heads are written as the
+  //    score product's B operand (hi / mid / lo bf16 in columns 4j .. 4j+2).
   if (w <= GQA) {
     float v[DPL];
     float ss = 0.f;
@@ -540,113 +564,144 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
       o[1] = v[1] * sm.rc[l] + v[0] * sm.rs[l];
     }
 #pragma unroll
-    for (int c = 0; c < DPL; ++c) sm.qk[w * D + l + c * kWave] = o[c];
+    for (int c = 0; c < DPL; ++c) {
+      sm.qk[w * D + l + c * kWave] = o[c];
+      if (w < GQA) {
+        uint16_t hi, mid, lo;
+        split_bf16(o[c], hi, mid, lo);
+        sm.qb[4 * w + 0][l + c * kWave] = hi;
+        sm.qb[4 * w + 1][l + c * kWave] = mid;
+        sm.qb[4 * w + 2][l + c * kWave] = lo;
+      }
+    }
   }
   __syncthreads();
   // 2. bf16 K/V of the current position (reference kv_cache.cuh:58-78).  The
   //    split that owns `pos` appends them to the cache (write-through
-  //    agent-scope stores, read by later tokens on any XCD); every split uses
-  //    the LDS copy for `pos`.
-  uint16_t* kb = p.kv + ((long long)(layer * 2 + 0) * S::NKV + g) * (long long)p.max_seq * D;
-  uint16_t* vb = p.kv + ((long long)(layer * 2 + 1) * S::NKV + g) * (long long)p.max_seq * D;
+  //    agent-scope stores, read by later tokens on any XCD); the blocks that
+  //    hold `pos` take them from LDS.
+  const long long base = kt_base(p, layer, g, S::NKV, D);
   const bool own = (t0 <= pos && pos < t1);
   if (tid < D / 2) {
     const int d = 2 * tid;
     const unsigned kw = (unsigned)f32_to_bf16(sm.qk[GQA * D + d]) | ((unsigned)f32_to_bf16(sm.qk[GQA * D + d + 1]) << 16);
-    const unsigned vw = (unsigned)f32_to_bf16(sm.qk[(GQA + 1) * D + d]) |
-                        ((unsigned)f32_to_bf16(sm.qk[(GQA + 1) * D + d + 1]) << 16);
+    const uint16_t v0 = f32_to_bf16(sm.qk[(GQA + 1) * D + d]), v1 = f32_to_bf16(sm.qk[(GQA + 1) * D + d + 1]);
     if (tid == 0) evt(p, tt, layer, EV_ATT_ROPE);
     reinterpret_cast<unsigned*>(sm.kvcur[0])[tid] = kw;
-    reinterpret_cast<unsigned*>(sm.kvcur[1])[tid] = vw;
+    reinterpret_cast<unsigned*>(sm.kvcur[1])[tid] = (unsigned)v0 | ((unsigned)v1 << 16);
     if (own) {
-      __hip_atomic_store(reinterpret_cast<unsigned*>(kb + (long long)pos * D) + tid, kw, __ATOMIC_RELAXED,
+      __hip_atomic_store(reinterpret_cast<unsigned*>(p.kv + base + (long long)pos * D) + tid, kw, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(reinterpret_cast<unsigned*>(vb + (long long)pos * D) + tid, vw, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      uint16_t* vt = p.kvt + base + (long long)(pos / 32) * 32 * D + (pos % 32);
+      __hip_atomic_store(vt + (long long)d * 32, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(vt + (long long)(d + 1) * 32, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __syncthreads();
-  // 3. per-wave online softmax over this wave's positions (fp32); scale 1/sqrt(D).
+  // 3. per-wave online softmax over the wave's blocks (fp32); scale 1/sqrt(D).
   const float scale = 1.0f / sqrtf((float)D);
-  const int c = l % LPP, po = l / LPP;
-  float qr[GQA][8];
+  const unsigned lu = lane_id();
+  const int col = (int)(lu & 15u), rg = (int)(lu >> 4);  // MFMA column, row group
+  const int hj = col >> 2;                                // head of this column
+  const bool head_lane = (col & 3) == 0 && hj < GQA;      // lane holding head hj's sums
+  u32x4 qbf[KC];  // B operand of the score product
 #pragma unroll
-  for (int j = 0; j < GQA; ++j)
+  for (int kc = 0; kc < KC; ++kc) qbf[kc] = *reinterpret_cast<const u32x4*>(&sm.qb[col][32 * kc + 8 * rg]);
+  float m = -INFINITY, lsum = 0.f;  // per head (valid in head lanes)
+  f32x4 acc[DT];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qr[j][e] = sm.qk[j * D + c * 8 + e];
-  float m[GQA], lsum[GQA], acc[GQA][8];
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int b0 = t0 / 32, nb = (t1 - t0 + 31) / 32;
+  for (int bi = w; bi < nb; bi += NW) {
+    if (bi != w) kv_load<S>(kvr, p, layer, g, b0 + bi);
+    const int bp = 32 * (b0 + bi);  // first position of the block
+    if (bp <= pos && pos < bp + 32) {  // the block holding pos: K / V from LDS
+      const int rp = pos - bp;
+      if ((int)(lu & 15u) == (rp & 15)) {
 #pragma unroll
-  for (int j = 0; j < GQA; ++j) {
-    m[j] = -INFINITY;
-    lsum[j] = 0.f;
+        for (int kc = 0; kc < KC; ++kc)
+          if (rp >> 4) kvr.k[1][kc] = sm.kvcur[0][4 * kc + rg];
+          else kvr.k[0][kc] = sm.kvcur[0][4 * kc + rg];
+      }
+      if (rg == (rp >> 3)) {
+        const uint16_t* vc = reinterpret_cast<const uint16_t*>(sm.kvcur[1]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-  }
-  const int nsub = (t1 - t0 + KV<S>::SUB - 1) / KV<S>::SUB;
-  for (int sub = 0; sub < nsub; ++sub) {
-    if (sub > 0) kv_load<S>(kvr, p, layer, g, t0, t1, pos, sub);
-    float sc[GQA][KV_ROWS];
-    float mx[GQA];
-#pragma unroll
-    for (int j = 0; j < GQA; ++j) mx[j] = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < KV_ROWS; ++i) {
-      const int t = t0 + sub * KV<S>::SUB + i * NW * PPW + w * PPW + po;
-      const u32x4 kk = (t == pos) ? sm.kvcur[0][c] : kvr.k[i];
-#pragma unroll
-      for (int j = 0; j < GQA; ++j) {
-        float d = dot8(kk, qr[j], 0.f);
-        d = group_sum<LPP>(d);
-        sc[j][i] = (t < t1) ? d * scale : -INFINITY;
-        mx[j] = fmaxf(mx[j], sc[j][i]);
+        for (int dt = 0; dt < DT; ++dt) kvr.v[dt] = set_bf16(kvr.v[dt], rp & 7, vc[16 * dt + col]);
       }
     }
+    // scores: sc[h][i] = position bp + 16 h + 4 rg + i, column col
+    f32x4 sc[2];
 #pragma unroll
-    for (int j = 0; j < GQA; ++j) {
-      const float mn = fmaxf(m[j], wave_max(mx[j]));
-      const float alpha = (m[j] == -INFINITY) ? 0.f : __expf(m[j] - mn);
-      lsum[j] *= alpha;
+    for (int h = 0; h < 2; ++h) {
+      sc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[j][e] *= alpha;
-      m[j] = mn;
+      for (int kc = 0; kc < KC; ++kc)
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.k[h][kc]),
+                                                       __builtin_bit_cast(bf16x8, qbf[kc]), sc[h], 0, 0, 0);
     }
+    float bmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < KV_ROWS; ++i) {
-      const int t = t0 + sub * KV<S>::SUB + i * NW * PPW + w * PPW + po;
-      const u32x4 vk = (t == pos) ? sm.kvcur[1][c] : kvr.v[i];
-      const float vf[8] = {bf16_lo(vk.x), bf16_hi(vk.x), bf16_lo(vk.y), bf16_hi(vk.y),
-                           bf16_lo(vk.z), bf16_hi(vk.z), bf16_lo(vk.w), bf16_hi(vk.w)};
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int j = 0; j < GQA; ++j) {
-        const float pj = (t < t1) ? __expf(sc[j][i] - m[j]) : 0.f;
-        lsum[j] += (c == 0) ? pj : 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[e], acc[j][e]);
+      for (int i = 0; i < 4; ++i) {
+        const float v = (sc[h][i] + dpp_sel<DPP_XOR1>(sc[h][i])) + dpp_sel<DPP_XOR2>(sc[h][i]);
+        const int t = bp + 16 * h + 4 * rg + i;
+        sc[h][i] = (t < t1 && head_lane) ? v * scale : -INFINITY;
+        bmax = fmaxf(bmax, sc[h][i]);
       }
+    bmax = max_xor32(max_xor16(bmax));
+    const float mn = fmaxf(m, bmax);  // finite in head lanes (the block has a valid position)
+    const float alpha = __expf(m - mn);
+    m = mn;
+    float bsum = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[h][i] = head_lane ? __expf(sc[h][i] - mn) : 0.f;
+        bsum += sc[h][i];
+      }
+    lsum = lsum * alpha + sum_xor32(sum_xor16(bsum));
+    // weights -> the output product's B operand via LDS: each head lane
+    // writes the hi / mid / lo parts of its 8 weights into columns 4j .. 4j+2
+    // (LDS operations of one wave complete in order; the other columns stay 0)
+    if (head_lane) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const Split3 a = split3(sc[h][0]), b = split3(sc[h][1]), c = split3(sc[h][2]), d = split3(sc[h][3]);
+        *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 0][16 * h + 4 * rg]) =
+            uint2{pack_hi16(a.hi, b.hi), pack_hi16(c.hi, d.hi)};
+        *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 1][16 * h + 4 * rg]) =
+            uint2{pack_hi16(a.mid, b.mid), pack_hi16(c.mid, d.mid)};
+        *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 2][16 * h + 4 * rg]) =
+            uint2{pack_hi16(a.lo, b.lo), pack_hi16(c.lo, d.lo)};
+      }
+    }
+    asm volatile("" ::: "memory");
+    const float aq = dpp_sel<0x00>(alpha);  // quad_perm [0,0,0,0]: the head lane's factor
+    const u32x4 pb = *reinterpret_cast<const u32x4*>(&sm.pb[w][col][8 * rg]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[dt][i] *= aq;
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.v[dt]),
+                                                       __builtin_bit_cast(bf16x8, pb), acc[dt], 0, 0, 0);
     }
   }
   evt(p, tt, layer, EV_ATT_SOFTMAX);
-  // 4. per-wave partials -> LDS, then merge the NW waves.
+  // 4. per-wave partials -> LDS (head lanes: dims 16 dt + 4 rg + i), then merge the NW waves.
 #pragma unroll
-  for (int j = 0; j < GQA; ++j) {
-    lsum[j] = wave_sum(lsum[j]);
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      acc[j][e] = stride_sum<LPP>(acc[j][e]);
-    }
-  }
+    for (int i = 0; i < 4; ++i) acc[dt][i] = (acc[dt][i] + dpp_sel<DPP_XOR1>(acc[dt][i])) + dpp_sel<DPP_XOR2>(acc[dt][i]);
   evt(p, tt, layer, EV_ATT_REDUCED);
-  if (po == 0) {
+  if (head_lane) {
 #pragma unroll
-    for (int j = 0; j < GQA; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.pv[(w * GQA + j) * D + c * 8 + e] = acc[j][e];
-  }
-  if (l == 0) {
-#pragma unroll
-    for (int j = 0; j < GQA; ++j) {
-      sm.mw[w * GQA + j] = m[j];
-      sm.lw[w * GQA + j] = lsum[j];
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4*>(&sm.pv[(w * GQA + hj) * D + 16 * dt + 4 * rg]) = acc[dt];
+    if (rg == 0) {
+      sm.mw[w * GQA + hj] = m;
+      sm.lw[w * GQA + hj] = lsum;
     }
   }
   __syncthreads();
@@ -789,6 +844,8 @@ template <class S>
 __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   __shared__ Smem<S> sm;
   if (threadIdx.x == 0) wg_abort = 0;
+  for (int i = threadIdx.x; i < 16 * S::D; i += NT) (&sm.qb[0][0])[i] = 0;  // unused columns stay 0
+  for (int i = threadIdx.x; i < NW * 16 * 32; i += NT) (&sm.pb[0][0][0])[i] = 0;
   __syncthreads();
   const int G = gridDim.x, wg = blockIdx.x, tid = threadIdx.x;
   const int w = tid / kWave, l = tid % kWave;
@@ -835,7 +892,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     const int n = pos + 1;
     int ns0 = (n + p.chunk_min - 1) / p.chunk_min;
     ns0 = ns0 < 1 ? 1 : (ns0 > p.nsplit_max ? p.nsplit_max : ns0);
-    const int chunk = (n + ns0 - 1) / ns0;
+    const int chunk = ((n + ns0 - 1) / ns0 + 31) / 32 * 32;  // whole 32-position blocks
     const int nsplit = (n + chunk - 1) / chunk;
     const bool has_att = it_att < S::NKV * nsplit;
     const int ag = has_att ? it_att / nsplit : 0, as = has_att ? it_att % nsplit : 0;
@@ -853,7 +910,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       // product ever waits behind loads issued after its own block.
       // ---------------- P1: QKV (prefetch: attention K/V + QK-norm gains)
       if (has_att) {
-        kv_load<S>(rkv, p, layer, ag, at0, at1, pos, 0);
+        kv_load<S>(rkv, p, layer, ag, first_block(at0, at1));
         gain_load_qk<S>(rkv, p, layer);
       }
       if (it_qkv < S::RB_QKV) {
