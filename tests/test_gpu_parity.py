@@ -155,9 +155,10 @@ def test_set_get_kv_roundtrip_and_synthetic_prefill():
         dw.free()
 
 
-@pytest.mark.parametrize("ctx,chunk", [(200, 256), (1500, 64), (5000, 256)])
+@pytest.mark.parametrize("ctx,chunk", [(200, 256), (1500, 64), (5000, 256), (8192, 256), (32768, 256)])
 def test_long_context_split_attention(ctx, chunk):
-    """Prefilled cache + multi-split attention vs the oracle."""
+    """Prefilled cache + multi-split attention vs the oracle (BASELINE configs[3]
+    positions 8192 and 32768 included: 32 splits of up to 32 blocks)."""
     shape = BASELINE.with_(n_layers=2, vocab=2048)
     eng, orc, dw = make_pair(shape, 21, ctx + 8)
     try:
