@@ -401,7 +401,8 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.first_token = first_token;
   p.nsplit_max = h->nsplit_max;
   p.chunk_min = h->chunk_min;
-  // the packed-pair act words carry 4-bit tags: start every launch from zeros
+  // the packed-pair words (attn, act) carry 4-bit tags: start every launch from zeros
+  HIPCHK(hipMemsetAsync(h->attn, 0, h->tagged_bytes[3], h->stream), -1);
   HIPCHK(hipMemsetAsync(h->act, 0, h->tagged_bytes[4], h->stream), -1);
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
   HIPCHK(h->launch(h, p), -1);

@@ -51,7 +51,7 @@ struct Params {
   u64* qkv;                   // [QKV] projections of the current layer (tagged)
   u64* part;                  // [NKV][nsplit_max][GQA*(D+2)] split partials (tagged):
                               //   m[GQA], l[GQA], acc[GQA][D] (unnormalised)
-  u64* attn;                  // [QD] merged attention output (tagged)
+  u64* attn;                  // [QD/2] merged attention output (packed pairs)
   u64* act;                   // [F/2] silu(gate)*up (packed pairs)
   u64* amax;                  // [2][G] per-workgroup argmax words (token parity)
   int* out_tokens;            // [n_tokens]
@@ -90,7 +90,6 @@ struct Smem {
   float mw[NW * S::GQA], lw[NW * S::GQA];  // attention: per-wave max / sum
   float gm[S::GQA], gl[S::GQA];       // this item's (max, sum) per q head
   float mbuf[(NSPLIT_CAP - 1) * S::GQA * (S::D + 2)];  // other splits' partials (merger)
-  float mscale[NSPLIT_CAP * S::GQA];  // merger: per-split weight f_q / L per head
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
   u64 amax[NW];
 };
@@ -243,13 +242,15 @@ __device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned t
   return norm_finish(ss, ssw, failed, (float)S::H, r);
 }
 
-// Wait for the packed-pair SiLU(gate)*up vector (F/2 words) and the 16
-// residual rows of this workgroup's down block, in one bulk round.
-template <class S>
-__device__ __forceinline__ bool fetch_act(const Params& p, unsigned t4, u64* xrows, unsigned xtag, float* act,
-                                          float* xres) {
-  constexpr int NPK = S::F / 2, TOT = NPK + 16, PER = (TOT + NT - 1) / NT;
+// Wait for a packed-pair vector of 2*NPK values (NPK words, 4-bit tag t4) and,
+// unless xrows is null, the 16 tagged residual rows of this workgroup's block,
+// in one bulk round.
+template <int NPK>
+__device__ __forceinline__ bool fetch_pk(const Params& p, u64* src, unsigned t4, u64* xrows, unsigned xtag,
+                                         float* dst, float* xres) {
+  constexpr int TOT = NPK + 16, PER = (TOT + NT - 1) / NT;
   const int tid = ltid();
+  const int tot = xrows ? TOT : NPK;
   int failed = 0;
   __syncthreads();  // every wave is done with the LDS of its previous phase
   u64 wv[PER];
@@ -260,9 +261,9 @@ __device__ __forceinline__ bool fetch_act(const Params& p, unsigned t4, u64* xro
     for (int k = 0; k < PER; ++k) {
       const int i = tid + k * NT;
       if (i < NPK) {
-        wv[k] = ll_get(p.act + i);
+        wv[k] = ll_get(src + i);
         ready &= pk_ready(wv[k], t4);
-      } else if (i < TOT) {
+      } else if (i < tot) {
         wv[k] = ll_get(xrows + (i - NPK));
         ready &= ll_tag(wv[k]) == xtag;
       }
@@ -277,9 +278,9 @@ __device__ __forceinline__ bool fetch_act(const Params& p, unsigned t4, u64* xro
   for (int k = 0; k < PER; ++k) {
     const int i = tid + k * NT;
     if (i < NPK) {
-      act[2 * i] = pk_lo(wv[k]);
-      act[2 * i + 1] = pk_hi(wv[k]);
-    } else if (i < TOT) {
+      dst[2 * i] = pk_lo(wv[k]);
+      dst[2 * i + 1] = pk_hi(wv[k]);
+    } else if (i < tot) {
       xres[i - NPK] = ll_val(wv[k]);
     }
   }
@@ -766,42 +767,46 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
   //    normalised attention output of its GQA heads.
   if (nsplit > 1 && !fetch1<8>(prow + W, (nsplit - 1) * W, sm.mbuf, tag_out, p, W)) return false;
   evt(p, tt, layer, EV_ATT_GATHERED);
-  // per-split weights f_q / L (log-sum-exp), one lane per split (q = 0: this
-  // split's own partial), computed once per head
-  if (tid < kWave) {
-#pragma unroll
-    for (int j = 0; j < GQA; ++j) {
-      const bool valid = tid < nsplit;
-      const float mq = tid == 0 ? sm.gm[j] : (valid ? sm.mbuf[(tid - 1) * W + j] : -INFINITY);
-      const float lq = tid == 0 ? sm.gl[j] : (valid ? sm.mbuf[(tid - 1) * W + GQA + j] : 0.f);
-      const float M = wave_max(mq);
-      const float f = valid ? __expf(mq - M) : 0.f;
-      const float Lt = wave_sum(f * lq);
-      if (valid) sm.mscale[tid * GQA + j] = f / Lt;
-    }
-  }
-  __syncthreads();
-  evt(p, tt, layer, EV_MERGE_SCALED);
+  // log-sum-exp merge, each output element on its own thread: all LDS reads
+  // are independent (eight splits per step, splits past nsplit selected away)
 #pragma unroll
   for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
     const int e = tid + k * NT;
     if (e < GQA * D) {
       const int j = e / D;
-      float o = sm.mscale[j] * av[k];
-      // eight splits per step: unconditional (in-bounds) LDS reads issued
-      // together, splits past nsplit selected away
+      const float m0 = sm.gm[j];
+      float M = m0;
       for (int q0 = 1; q0 < nsplit; q0 += 8) {
-        float wq[8], xq[8];
+        float mq[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) mq[u] = sm.mbuf[(min(q0 + u, NSPLIT_CAP - 1) - 1) * W + j];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) M = q0 + u < nsplit ? fmaxf(M, mq[u]) : M;
+      }
+      const float f0 = __expf(m0 - M);
+      float o = f0 * av[k], Lt = f0 * sm.gl[j];
+      for (int q0 = 1; q0 < nsplit; q0 += 8) {
+        float mq[8], lq[8], xq[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          const int q = q0 + u < NSPLIT_CAP ? q0 + u : NSPLIT_CAP - 1;
-          wq[u] = sm.mscale[q * GQA + j];
-          xq[u] = sm.mbuf[(q - 1) * W + 2 * GQA + e];
+          const int r = (min(q0 + u, NSPLIT_CAP - 1) - 1) * W;
+          mq[u] = sm.mbuf[r + j];
+          lq[u] = sm.mbuf[r + GQA + j];
+          xq[u] = sm.mbuf[r + 2 * GQA + e];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) o = q0 + u < nsplit ? fmaf(wq[u], xq[u], o) : o;
+        for (int u = 0; u < 8; ++u) {
+          const bool ok = q0 + u < nsplit;  // select, not multiply: stale LDS may hold anything
+          const float f = __expf(mq[u] - M);
+          o = ok ? fmaf(f, xq[u], o) : o;
+          Lt = ok ? fmaf(f, lq[u], Lt) : Lt;
+        }
       }
-      ll_put(p.attn + (long long)g * GQA * D + e, ll_pack(o, tag_out));
+      // packed pairs: even lanes store (own, neighbour) -- e and e ^ 1 are
+      // adjacent lanes of the same wave
+      const float val = o / Lt;
+      const float nb = dpp_sel<DPP_XOR1>(val);
+      if ((e & 1) == 0) ll_put(p.attn + ((long long)g * GQA * D + e) / 2, pk_pack(val, nb, tag4(tag_out)));
     }
   }
   evt(p, tt, layer, EV_MERGE_DONE);
@@ -955,8 +960,8 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         gains_load(gf, nrm + S::NORM_FFN);
       }
       if (it_o < S::RB_H) {
-        if (!fetch3<3>(Range{p.attn, S::QD, sm.vec_o, tg + 1u, 16},
-                       layer > 0 ? Range{p.x + it_o * 16, 16, sm.xres_o, tg_x, 16} : kNoRange, kNoRange, p))
+        if (!fetch_pk<S::QD / 2>(p, p.attn, tag4(tg + 1u), layer > 0 ? p.x + it_o * 16 : nullptr, tg_x, sm.vec_o,
+                                 sm.xres_o))
           return;
         trace_mark(p, t, slot + 2, 0);
         evt(p, t, layer, EV_O_READY);
@@ -1008,7 +1013,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         gains_load(gq, nrm + S::NORM_STRIDE + S::NORM_ATTN);
       }
       if (it_dn < S::RB_H) {
-        if (!fetch_act<S>(p, tag4(tg + 3u), p.x + it_dn * 16, tg + 2u, sm.vec_d, sm.xres_d)) return;
+        if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x + it_dn * 16, tg + 2u, sm.vec_d, sm.xres_d)) return;
         trace_mark(p, t, slot + 4, 0);
         evt(p, t, layer, EV_DN_READY);
         const float y = blk_dot(rd, sm.vec_d);
