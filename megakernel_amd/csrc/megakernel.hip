@@ -141,7 +141,7 @@ struct Handle {
   ShapeInfo sh{};
   int L = 0, V = 0, S = 0;
   int max_launch_tokens = 0;
-  int nsplit_max = 1, chunk_min = 256;
+  int nsplit_max = 1, chunk_min = 256 * KVB;  // one 32-position block per wave and register set
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = 0.f;

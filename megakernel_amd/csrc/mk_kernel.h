@@ -34,6 +34,11 @@ namespace mk {
 constexpr int NT = 512;               // threads per workgroup (8 waves)
 constexpr int NW = NT / kWave;
 constexpr int PHASES_PER_LAYER = 5;
+#ifndef MK_KV_BLOCKS
+#define MK_KV_BLOCKS 1
+#endif
+constexpr int KVB = MK_KV_BLOCKS;  // 32-position blocks a wave holds in registers
+
 constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
 constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
 __device__ __forceinline__ unsigned tag14(unsigned tag) { return tag % 16383u + 1u; }
@@ -84,7 +89,7 @@ struct Smem {
   float rowbuf[4][16];                // a block's 16 results, stored by one wave
   float qk[(S::GQA + 2) * S::D];      // q heads, k, v of the current position
   __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score B operand
-  __attribute__((aligned(16))) uint16_t pb[NW][16][32];  // attention: weight parts, output B operand
+  __attribute__((aligned(16))) uint16_t pb[NW][16][32 * KVB];  // attention: weight parts, output B operand
   u32x4 kvcur[2][S::D / 8];           // bf16 K/V of the current position
   float pv[NW * S::GQA * S::D];       // attention: per-wave unnormalised outputs
   float mw[NW * S::GQA], lw[NW * S::GQA];  // attention: per-wave max / sum
@@ -472,8 +477,8 @@ template <class S>
 struct KV {
   static constexpr int KC = S::D / 32;  // k-steps of the score product
   static constexpr int DT = S::D / 16;  // dim tiles of the output product
-  u32x4 k[2][KC];  // K of the wave's block: [16-position half][k-step]
-  u32x4 v[DT];     // V^T of the block: [dim tile]
+  u32x4 k[KVB][2][KC];  // K of the wave's blocks: [block][16-position half][k-step]
+  u32x4 v[KVB][DT];     // V^T of the blocks: [block][dim tile]
   uint16_t gn[S::D / kWave];  // QK-norm gain(s) of this lane's dim(s) for its wave's head
 };
 
@@ -497,21 +502,29 @@ __device__ __forceinline__ u32x4 buf_ld_kv(__amdgpu_buffer_rsrc_t rs, unsigned v
   return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0u, 16 | 2);
 }
 
-// Loads block `blk` of positions (starting at position 32 blk) for this wave.
+// Loads this wave's KVB blocks of an item starting at block index `bi`
+// (item blocks bi, bi + NW, ...; blocks past the item's nb repeat a valid
+// block and are masked by the caller).
 template <class S>
-__device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, int g, int blk) {
+__device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, int g, int b0, int nb, int bi) {
   constexpr int D = S::D;
   const unsigned l = lane_id();
   const long long base = kt_base(p, layer, g, S::NKV, D);
-  const auto rk = make_rsrc(p.kv + base + (long long)blk * 32 * D);
-  const auto rv = make_rsrc(p.kvt + base + (long long)blk * 32 * D);
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int q = 0; q < KVB; ++q) {
+    const int bq = bi + q * NW;
+    const int blk = b0 + (bq < nb ? bq : 0);
+    const auto rk = make_rsrc(p.kv + base + (long long)blk * 32 * D);
+    const auto rv = make_rsrc(p.kvt + base + (long long)blk * 32 * D);
 #pragma unroll
-    for (int kc = 0; kc < KV<S>::KC; ++kc)
-      r.k[h][kc] = buf_ld_kv(rk, ((16u * h + (l & 15u)) * D + 32u * kc + 8u * (l >> 4)) * 2u);
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-  for (int dt = 0; dt < KV<S>::DT; ++dt) r.v[dt] = buf_ld_kv(rv, ((16u * dt + (l & 15u)) * 32u + 8u * (l >> 4)) * 2u);
+      for (int kc = 0; kc < KV<S>::KC; ++kc)
+        r.k[q][h][kc] = buf_ld_kv(rk, ((16u * h + (l & 15u)) * D + 32u * kc + 8u * (l >> 4)) * 2u);
+#pragma unroll
+    for (int dt = 0; dt < KV<S>::DT; ++dt)
+      r.v[q][dt] = buf_ld_kv(rv, ((16u * dt + (l & 15u)) * 32u + 8u * (l >> 4)) * 2u);
+  }
 }
 
 // QK-norm gains of this lane's dims: waves 0..GQA-1 normalise q heads, wave
@@ -522,13 +535,6 @@ __device__ __forceinline__ void gain_load_qk(KV<S>& r, const Params& p, int laye
   const uint16_t* g = p.norms + (long long)layer * S::NORM_STRIDE + (w < S::GQA ? S::NORM_Q : S::NORM_K);
 #pragma unroll
   for (int c = 0; c < S::D / kWave; ++c) r.gn[c] = g[l + c * kWave];
-}
-
-// The first block of this wave's share of an item (or block 0 of the item,
-// as harmless valid addresses, when the wave has none).
-__device__ __forceinline__ int first_block(int t0, int t1) {
-  const int b0 = t0 / 32, nb = (t1 - t0 + 31) / 32, w = wave_id();
-  return b0 + (w < nb ? w : 0);
 }
 
 // Inputs are already fetched into sm.qk (q heads | k | v).  Writes the split's
@@ -613,80 +619,97 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int b0 = t0 / 32, nb = (t1 - t0 + 31) / 32;
-  for (int bi = w; bi < nb; bi += NW) {
-    if (bi != w) kv_load<S>(kvr, p, layer, g, b0 + bi);
-    const int bp = 32 * (b0 + bi);  // first position of the block
-    if (bp <= pos && pos < bp + 32) {  // the block holding pos: K / V from LDS
-      const int rp = pos - bp;
-      if ((int)(lu & 15u) == (rp & 15)) {
+  // groups of KVB blocks (w + NW * (KVB * gi + q)); the first group was
+  // prefetched, later ones (long contexts) are loaded here
+  for (int bi = w; bi < nb; bi += KVB * NW) {
+    if (bi != w) kv_load<S>(kvr, p, layer, g, b0, nb, bi);
+    // the block holding pos takes K / V of pos from LDS
+#pragma unroll
+    for (int q = 0; q < KVB; ++q) {
+      const int bp = 32 * (b0 + bi + q * NW);
+      if (bi + q * NW < nb && bp <= pos && pos < bp + 32) {
+        const int rp = pos - bp;
+        if ((int)(lu & 15u) == (rp & 15)) {
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc)
+            if (rp >> 4) kvr.k[q][1][kc] = sm.kvcur[0][4 * kc + rg];
+            else kvr.k[q][0][kc] = sm.kvcur[0][4 * kc + rg];
+        }
+        if (rg == (rp >> 3)) {
+          const uint16_t* vc = reinterpret_cast<const uint16_t*>(sm.kvcur[1]);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) kvr.v[q][dt] = set_bf16(kvr.v[q][dt], rp & 7, vc[16 * dt + col]);
+        }
+      }
+    }
+    // scores: sc[q][h][i] = position 32 (b0 + bi + q NW) + 16 h + 4 rg + i, column col
+    f32x4 sc[KVB][2];
+#pragma unroll
+    for (int q = 0; q < KVB; ++q)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        sc[q][h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc)
-          if (rp >> 4) kvr.k[1][kc] = sm.kvcur[0][4 * kc + rg];
-          else kvr.k[0][kc] = sm.kvcur[0][4 * kc + rg];
+          sc[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.k[q][h][kc]),
+                                                            __builtin_bit_cast(bf16x8, qbf[kc]), sc[q][h], 0, 0, 0);
       }
-      if (rg == (rp >> 3)) {
-        const uint16_t* vc = reinterpret_cast<const uint16_t*>(sm.kvcur[1]);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) kvr.v[dt] = set_bf16(kvr.v[dt], rp & 7, vc[16 * dt + col]);
-      }
-    }
-    // scores: sc[h][i] = position bp + 16 h + 4 rg + i, column col
-    f32x4 sc[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      sc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
-        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.k[h][kc]),
-                                                       __builtin_bit_cast(bf16x8, qbf[kc]), sc[h], 0, 0, 0);
-    }
     float bmax = -INFINITY;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int q = 0; q < KVB; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = (sc[h][i] + dpp_sel<DPP_XOR1>(sc[h][i])) + dpp_sel<DPP_XOR2>(sc[h][i]);
-        const int t = bp + 16 * h + 4 * rg + i;
-        sc[h][i] = (t < t1 && head_lane) ? v * scale : -INFINITY;
-        bmax = fmaxf(bmax, sc[h][i]);
-      }
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = (sc[q][h][i] + dpp_sel<DPP_XOR1>(sc[q][h][i])) + dpp_sel<DPP_XOR2>(sc[q][h][i]);
+          const int t = 32 * (b0 + bi + q * NW) + 16 * h + 4 * rg + i;
+          sc[q][h][i] = (bi + q * NW < nb && t < t1 && head_lane) ? v * scale : -INFINITY;
+          bmax = fmaxf(bmax, sc[q][h][i]);
+        }
     bmax = max_xor32(max_xor16(bmax));
-    const float mn = fmaxf(m, bmax);  // finite in head lanes (the block has a valid position)
+    const float mn = fmaxf(m, bmax);  // finite in head lanes (block bi has a valid position)
     const float alpha = __expf(m - mn);
     m = mn;
     float bsum = 0.f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int q = 0; q < KVB; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[h][i] = head_lane ? __expf(sc[h][i] - mn) : 0.f;
-        bsum += sc[h][i];
-      }
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[q][h][i] = head_lane ? __expf(sc[q][h][i] - mn) : 0.f;
+          bsum += sc[q][h][i];
+        }
     lsum = lsum * alpha + sum_xor32(sum_xor16(bsum));
     // weights -> the output product's B operand via LDS: each head lane
-    // writes the hi / mid / lo parts of its 8 weights into columns 4j .. 4j+2
+    // writes the hi / mid / lo parts of its weights into columns 4j .. 4j+2
     // (LDS operations of one wave complete in order; the other columns stay 0)
     if (head_lane) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const Split3 a = split3(sc[h][0]), b = split3(sc[h][1]), c = split3(sc[h][2]), d = split3(sc[h][3]);
-        *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 0][16 * h + 4 * rg]) =
-            uint2{pack_hi16(a.hi, b.hi), pack_hi16(c.hi, d.hi)};
-        *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 1][16 * h + 4 * rg]) =
-            uint2{pack_hi16(a.mid, b.mid), pack_hi16(c.mid, d.mid)};
-        *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 2][16 * h + 4 * rg]) =
-            uint2{pack_hi16(a.lo, b.lo), pack_hi16(c.lo, d.lo)};
-      }
+      for (int q = 0; q < KVB; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const Split3 a = split3(sc[q][h][0]), b = split3(sc[q][h][1]), c = split3(sc[q][h][2]),
+                       d = split3(sc[q][h][3]);
+          const int o = 32 * q + 16 * h + 4 * rg;
+          *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 0][o]) = uint2{pack_hi16(a.hi, b.hi), pack_hi16(c.hi, d.hi)};
+          *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 1][o]) = uint2{pack_hi16(a.mid, b.mid), pack_hi16(c.mid, d.mid)};
+          *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 2][o]) = uint2{pack_hi16(a.lo, b.lo), pack_hi16(c.lo, d.lo)};
+        }
     }
     asm volatile("" ::: "memory");
     const float aq = dpp_sel<0x00>(alpha);  // quad_perm [0,0,0,0]: the head lane's factor
-    const u32x4 pb = *reinterpret_cast<const u32x4*>(&sm.pb[w][col][8 * rg]);
+    u32x4 pbq[KVB];
+#pragma unroll
+    for (int q = 0; q < KVB; ++q) pbq[q] = *reinterpret_cast<const u32x4*>(&sm.pb[w][col][32 * q + 8 * rg]);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[dt][i] *= aq;
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.v[dt]),
-                                                       __builtin_bit_cast(bf16x8, pb), acc[dt], 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < KVB; ++q)
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.v[q][dt]),
+                                                         __builtin_bit_cast(bf16x8, pbq[q]), acc[dt], 0, 0, 0);
     }
   }
   evt(p, tt, layer, EV_ATT_SOFTMAX);
@@ -850,7 +873,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   __shared__ Smem<S> sm;
   if (threadIdx.x == 0) wg_abort = 0;
   for (int i = threadIdx.x; i < 16 * S::D; i += NT) (&sm.qb[0][0])[i] = 0;  // unused columns stay 0
-  for (int i = threadIdx.x; i < NW * 16 * 32; i += NT) (&sm.pb[0][0][0])[i] = 0;
+  for (int i = threadIdx.x; i < NW * 16 * 32 * KVB; i += NT) (&sm.pb[0][0][0])[i] = 0;
   __syncthreads();
   const int G = gridDim.x, wg = blockIdx.x, tid = threadIdx.x;
   const int w = tid / kWave, l = tid % kWave;
@@ -915,7 +938,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       // product ever waits behind loads issued after its own block.
       // ---------------- P1: QKV (prefetch: attention K/V + QK-norm gains)
       if (has_att) {
-        kv_load<S>(rkv, p, layer, ag, first_block(at0, at1));
+        kv_load<S>(rkv, p, layer, ag, at0 / 32, (at1 - at0 + 31) / 32, wave_id());
         gain_load_qk<S>(rkv, p, layer);
       }
       if (it_qkv < S::RB_QKV) {
