@@ -134,3 +134,74 @@ class DeviceWeights:
             self.free()
         except Exception:
             pass
+
+
+# ------------------------------------------------------------------ real weights
+# HF Qwen3 state-dict key of each flat tensor (reference host/weight_loader.py:62-110).
+_HF_KEYS = {
+    "attn_norm": "input_layernorm.weight", "w_q": "self_attn.q_proj.weight",
+    "w_k": "self_attn.k_proj.weight", "w_v": "self_attn.v_proj.weight",
+    "q_norm": "self_attn.q_norm.weight", "k_norm": "self_attn.k_norm.weight",
+    "w_o": "self_attn.o_proj.weight", "ffn_norm": "post_attention_layernorm.weight",
+    "w_gate": "mlp.gate_proj.weight", "w_up": "mlp.up_proj.weight", "w_down": "mlp.down_proj.weight",
+}
+
+
+def shape_from_hf_config(cfg: dict) -> ModelShape:
+    """ModelShape of a Qwen3 config.json (the preset is chosen by head_dim /
+    intermediate size; other shapes are rejected by the library at init)."""
+    from . import config as _cfg
+    hidden, nq, nkv = cfg["hidden_size"], cfg["num_attention_heads"], cfg["num_key_value_heads"]
+    d = cfg.get("head_dim", hidden // nq)
+    shape = ModelShape(hidden, nq, nkv, d, cfg["intermediate_size"], cfg["num_hidden_layers"],
+                       cfg["vocab_size"], _lib.PRESET_BASELINE)
+    for preset in (_cfg.BASELINE, _cfg.QWEN3_06B, _cfg.TINY):
+        if (preset.hidden, preset.n_q_heads, preset.n_kv_heads, preset.head_dim, preset.ffn) == \
+                (hidden, nq, nkv, d, cfg["intermediate_size"]):
+            return preset.with_(n_layers=shape.n_layers, vocab=shape.vocab)
+    raise ValueError(f"no compiled preset for hidden {hidden}, heads {nq}/{nkv}, head_dim {d}, "
+                     f"ffn {cfg['intermediate_size']}")
+
+
+def flat_from_state(state: dict, shape: ModelShape) -> np.ndarray:
+    """The flat bf16 image (uint8 bytes, reference order) of an HF Qwen3 state
+    dict of torch tensors.  The tied embedding is the LM head, as in the
+    reference kernel; a separate lm_head.weight is ignored."""
+    import torch
+    layout = flat_layout(shape)
+    buf = np.zeros(layout.total_bytes, dtype=np.uint8)
+
+    def put(name: str, key: str):
+        t = state[key]
+        want = tensor_dims(shape, name.split(".")[-1])
+        if tuple(t.shape) != want:
+            raise ValueError(f"{key}: shape {tuple(t.shape)}, expected {want}")
+        raw = t.detach().to(torch.bfloat16).contiguous().view(torch.int16).cpu().numpy().view(np.uint8).reshape(-1)
+        off = layout.offsets[name]
+        buf[off:off + raw.size] = raw
+
+    put("embedding", "model.embed_tokens.weight")
+    put("final_norm", "model.norm.weight")
+    for i in range(shape.n_layers):
+        for k, hk in _HF_KEYS.items():
+            put(f"layer.{i}.{k}", f"model.layers.{i}.{hk}")
+    return buf
+
+
+def convert_safetensors(model_dir: str, output_path: str) -> tuple[str, ModelShape]:
+    """Convert a local HF Qwen3 checkpoint directory (config.json +
+    *.safetensors; no download) to weights.bin + weights_offsets.json
+    (reference host/weight_loader.py:141-206).  Returns (offsets path, shape)."""
+    import glob
+    import os
+
+    from safetensors.torch import load_file
+    with open(os.path.join(model_dir, "config.json")) as f:
+        shape = shape_from_hf_config(json.load(f))
+    state = {}
+    for fn in sorted(glob.glob(os.path.join(model_dir, "*.safetensors"))):
+        state.update(load_file(fn))
+    if not state:
+        raise FileNotFoundError(f"no .safetensors files in {model_dir}")
+    buf = flat_from_state(state, shape)
+    return save_flat(output_path, buf, flat_layout(shape)), shape
