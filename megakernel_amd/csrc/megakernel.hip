@@ -127,13 +127,14 @@ struct ShapeInfo {
   int H, NQ, NKV, D, F, QD, KVD, QKV, GQA;
   long long u_layer, off_qkv, off_o, off_gu, off_down;
   int norm_stride, norm_attn, norm_q, norm_k, norm_ffn;
+  int part_words;  // words of one attention item's published partial
 };
 
 template <class S>
 static ShapeInfo shape_info() {
   return ShapeInfo{S::H, S::NQ, S::NKV, S::D, S::F, S::QD, S::KVD, S::QKV, S::GQA,
                    S::U_LAYER, S::OFF_QKV, S::OFF_O, S::OFF_GU, S::OFF_DOWN,
-                   S::NORM_STRIDE, S::NORM_ATTN, S::NORM_Q, S::NORM_K, S::NORM_FFN};
+                   S::NORM_STRIDE, S::NORM_ATTN, S::NORM_Q, S::NORM_K, S::NORM_FFN, part_words<S>()};
 }
 
 struct Handle {
@@ -152,9 +153,9 @@ struct Handle {
   uint16_t* final_norm = nullptr;
   u32x4* lmhead = nullptr;
   uint16_t* kv = nullptr;
-  u64 *x = nullptr, *qkv = nullptr, *part = nullptr, *attn = nullptr, *act = nullptr;
+  u64 *x = nullptr, *qkv = nullptr, *part = nullptr, *act = nullptr;
   u64* amax = nullptr;
-  size_t tagged_bytes[6] = {0, 0, 0, 0, 0, 0};
+  size_t tagged_bytes[5] = {0, 0, 0, 0, 0};
   int* out_tokens = nullptr;
   int* err = nullptr;
   u64* trace = nullptr;
@@ -183,7 +184,7 @@ static int occupancy_ok(int* nblk) {
 
 static void free_all(Handle* h) {
   void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part,
-                  h->attn, h->act, h->amax, h->out_tokens, h->err, h->inv_freq, h->dbg_layers,
+                  h->act, h->amax, h->out_tokens, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
@@ -242,11 +243,11 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   h->kvt = h->kv + (long long)h->L * s.NKV * h->s_pad * s.D;
   HIPCHK(hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream), -1);
   // tagged activation words (zero = tag 0, never a valid tag)
-  u64** tagged[6] = {&h->x, &h->qkv, &h->part, &h->attn, &h->act, &h->amax};
-  const size_t words[6] = {(size_t)s.H, (size_t)s.QKV,
-                           (size_t)s.NKV * h->nsplit_max * s.GQA * (s.D + 2), (size_t)s.QD, (size_t)s.F,
+  u64** tagged[5] = {&h->x, &h->qkv, &h->part, &h->act, &h->amax};
+  const size_t words[5] = {(size_t)s.H, (size_t)s.QKV,
+                           (size_t)h->nsplit_max * s.NKV * s.part_words, (size_t)s.F / 2,
                            (size_t)2 * h->G};
-  for (int i = 0; i < 6; ++i) {
+  for (int i = 0; i < 5; ++i) {
     h->tagged_bytes[i] = words[i] * 8;
     HIPCHK(hipMalloc(tagged[i], h->tagged_bytes[i]), -1);
     HIPCHK(hipMemsetAsync(*tagged[i], 0, h->tagged_bytes[i], h->stream), -1);
@@ -343,8 +344,8 @@ static int check_occupancy(Handle* h) {
 
 // Clear every tagged word (tag 0 is never expected) and the error word.
 static int clear_tagged_state(Handle* h) {
-  u64* bufs[6] = {h->x, h->qkv, h->part, h->attn, h->act, h->amax};
-  for (int i = 0; i < 6; ++i) HIPCHK(hipMemsetAsync(bufs[i], 0, h->tagged_bytes[i], h->stream), -1);
+  u64* bufs[5] = {h->x, h->qkv, h->part, h->act, h->amax};
+  for (int i = 0; i < 5; ++i) HIPCHK(hipMemsetAsync(bufs[i], 0, h->tagged_bytes[i], h->stream), -1);
   HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
   return 0;
@@ -380,7 +381,6 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.x = h->x;
   p.qkv = h->qkv;
   p.part = h->part;
-  p.attn = h->attn;
   p.act = h->act;
   p.amax = h->amax;
   p.out_tokens = h->out_tokens;
@@ -401,9 +401,9 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.first_token = first_token;
   p.nsplit_max = h->nsplit_max;
   p.chunk_min = h->chunk_min;
-  // the packed-pair words (attn, act) carry 4-bit tags: start every launch from zeros
-  HIPCHK(hipMemsetAsync(h->attn, 0, h->tagged_bytes[3], h->stream), -1);
-  HIPCHK(hipMemsetAsync(h->act, 0, h->tagged_bytes[4], h->stream), -1);
+  // the packed-pair words (part, act) carry 4-bit tags: start every launch from zeros
+  HIPCHK(hipMemsetAsync(h->part, 0, h->tagged_bytes[2], h->stream), -1);
+  HIPCHK(hipMemsetAsync(h->act, 0, h->tagged_bytes[3], h->stream), -1);
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
   HIPCHK(h->launch(h, p), -1);
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);

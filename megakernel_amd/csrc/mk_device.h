@@ -156,22 +156,23 @@ __device__ __forceinline__ float max_xor32(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Sum over aligned groups of N = 8 or 16 consecutive lanes (result in all of them).
+// Sum over aligned groups of N = 1, 2, 4, 8 or 16 consecutive lanes (result
+// in all of them).
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
-  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
-  v += dpp_sel<DPP_XOR1>(v);
-  v += dpp_sel<DPP_XOR2>(v);
-  v += dpp_sel<DPP_HALF_MIRROR>(v);  // quads are uniform: pairs quad 0 with quad 1
-  if constexpr (N == 16) v += dpp_sel<DPP_MIRROR>(v);  // pairs the two 8-lane halves
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group of 1, 2, 4, 8 or 16 lanes");
+  if constexpr (N >= 2) v += dpp_sel<DPP_XOR1>(v);
+  if constexpr (N >= 4) v += dpp_sel<DPP_XOR2>(v);
+  if constexpr (N >= 8) v += dpp_sel<DPP_HALF_MIRROR>(v);  // quads are uniform: pairs quad 0 with quad 1
+  if constexpr (N == 16) v += dpp_sel<DPP_MIRROR>(v);      // pairs the two 8-lane halves
   return v;
 }
 template <int N>
 __device__ __forceinline__ float group_max(float v) {
-  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
-  v = fmaxf(v, dpp_sel<DPP_XOR1>(v));
-  v = fmaxf(v, dpp_sel<DPP_XOR2>(v));
-  v = fmaxf(v, dpp_sel<DPP_HALF_MIRROR>(v));
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group of 1, 2, 4, 8 or 16 lanes");
+  if constexpr (N >= 2) v = fmaxf(v, dpp_sel<DPP_XOR1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp_sel<DPP_XOR2>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp_sel<DPP_HALF_MIRROR>(v));
   if constexpr (N == 16) v = fmaxf(v, dpp_sel<DPP_MIRROR>(v));
   return v;
 }

@@ -54,9 +54,8 @@ struct Params {
   uint16_t* kvt;              // V cache, transposed blocks [L][NKV][s_pad/32][D][32] bf16
   u64* x;                     // [H] residual stream (tagged)
   u64* qkv;                   // [QKV] projections of the current layer (tagged)
-  u64* part;                  // [NKV][nsplit_max][GQA*(D+2)] split partials (tagged):
-                              //   m[GQA], l[GQA], acc[GQA][D] (unnormalised)
-  u64* attn;                  // [QD/2] merged attention output (packed pairs)
+  u64* part;                  // [nsplit_max][NKV][GQA*D/2 + GQA] attention partials (packed
+                              //   pairs): unnormalised output, then (max, sum) per q head
   u64* act;                   // [F/2] silu(gate)*up (packed pairs)
   u64* amax;                  // [2][G] per-workgroup argmax words (token parity)
   int* out_tokens;            // [n_tokens]
@@ -87,14 +86,11 @@ struct Smem {
   float xres_o[16], xres_d[16];       // residual rows of this workgroup's O / down block
   float ssw[3][NW];                   // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
   float rowbuf[4][16];                // a block's 16 results, stored by one wave
-  float qk[(S::GQA + 2) * S::D];      // q heads, k, v of the current position
-  __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score B operand
-  __attribute__((aligned(16))) uint16_t pb[NW][16][32 * KVB];  // attention: weight parts, output B operand
+  __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score A operand
+  __attribute__((aligned(16))) uint16_t pb[NW][16][32 * KVB];  // attention: weight parts, output A operand
   u32x4 kvcur[2][S::D / 8];           // bf16 K/V of the current position
-  float pv[NW * S::GQA * S::D];       // attention: per-wave unnormalised outputs
-  float mw[NW * S::GQA], lw[NW * S::GQA];  // attention: per-wave max / sum
-  float gm[S::GQA], gl[S::GQA];       // this item's (max, sum) per q head
-  float mbuf[(NSPLIT_CAP - 1) * S::GQA * (S::D + 2)];  // other splits' partials (merger)
+  __attribute__((aligned(16))) float pv[NW][S::GQA * S::D];  // attention: per-wave unnormalised outputs
+  float mw[S::GQA][NW], lw[S::GQA][NW];  // attention: per-wave max / sum per q head
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
   u64 amax[NW];
 };
@@ -463,16 +459,19 @@ __device__ __forceinline__ bool fetch1(u64* src, int n, float* dst, unsigned tag
 // [L][2][NKV][S][D] layout):
 //   K:  [L][NKV][S_pad][D] bf16, row-major per position;
 //   V^T: [L][NKV][S_pad/32][D][32] bf16, 32-position blocks with each dim's
-//        32 values contiguous,
-// so both products of a 32-position block run on the matrix cores
-// (v_mfma_f32_16x16x32_bf16) with the cache bytes as the A operand:
-//   scores^T[pos][col] = K[pos][:] . Qb[:][col]   (A = K rows, k = dims)
-//   out^T[dim][col]    = V^T[dim][:] . Pb[:][col] (A = V^T rows, k = positions)
-// Columns col = 4 j + part carry q head j (resp. its softmax weights) split
-// into three bf16 parts hi + mid + lo, which reproduces fp32 activations; the
-// three output columns of a head are summed.
-// A work item (kv head g, split s) covers positions [t0, t1), t0 a multiple of
-// 32; wave w takes the item's blocks w, w + NW, ...
+//        32 values contiguous.
+// Both products of a 32-position block run on the matrix cores
+// (v_mfma_f32_16x16x32_bf16: D[m][n] = sum_k A[m][k] B[k][n]; lane l holds
+// A[l & 15][8 (l >> 4) + e], B[8 (l >> 4) + e][l & 15] and
+// D[4 (l >> 4) + i][l & 15]):
+//   scores[r][pos] = Qb[r][:] . K[pos][:]   (B = K^T: a lane's 8 dims of one cached row)
+//   out[r][dim]    = Pb[r][:] . V[:][dim]   (B = V:   a lane's 8 positions of one V^T row)
+// Row r = 4 j + part carries q head j (resp. its softmax weights) split into
+// three bf16 parts hi + mid + lo, which reproduces fp32 activations.  Lanes
+// 16 j .. 16 j + 15 therefore hold head j's three part rows (i = 0..2), sum
+// them in-register and own 16 positions (resp. dims) of head j each.
+// A work item (kv head g, split s) covers whole 32-position blocks
+// [t0, t1); wave w takes the item's blocks w, w + NW, ...
 template <class S>
 struct KV {
   static constexpr int KC = S::D / 32;  // k-steps of the score product
@@ -481,6 +480,12 @@ struct KV {
   u32x4 v[KVB][DT];     // V^T of the blocks: [block][dim tile]
   uint16_t gn[S::D / kWave];  // QK-norm gain(s) of this lane's dim(s) for its wave's head
 };
+
+// Words of one item's published partial: GQA * D / 2 packed pairs of the
+// unnormalised output, then one packed (max, sum) pair per q head, padded to
+// whole 128-byte lines (no line is shared by two items).
+template <class S>
+constexpr int part_words() { return (S::GQA * S::D / 2 + S::GQA + 15) / 16 * 16; }
 
 // u32x4 holding 8 bf16 with element e (0..7) replaced by v (register-only).
 __device__ __forceinline__ u32x4 set_bf16(u32x4 x, int e, uint16_t v) {
@@ -537,26 +542,75 @@ __device__ __forceinline__ void gain_load_qk(KV<S>& r, const Params& p, int laye
   for (int c = 0; c < S::D / kWave; ++c) r.gn[c] = g[l + c * kWave];
 }
 
-// Inputs are already fetched into sm.qk (q heads | k | v).  Writes the split's
-// (max, sum, unnormalised output) words for the GQA heads of group g.
+// The split of the n = pos + 1 cached positions among items: nsplit splits of
+// whole 32-position blocks, as even as possible (every split non-empty).
+// nsplit never decreases as the position grows, so a consumer of split slot
+// s < nsplit only ever finds this layer's word or an older one with another
+// tag there.
+__device__ __forceinline__ int split_count(int n, int chunk_min, int nsplit_max) {
+  const int nbt = (n + 31) / 32;
+  int ns = (n + chunk_min - 1) / chunk_min;
+  ns = ns < 1 ? 1 : ns;
+  ns = ns > nsplit_max ? nsplit_max : ns;
+  return ns > nbt ? nbt : ns;
+}
+// Positions [t0, t1) of split s of ns.
+__device__ __forceinline__ void split_range(int n, int ns, int s, int* t0, int* t1) {
+  const int nbt = (n + 31) / 32;
+  *t0 = 32 * (s * nbt / ns);
+  *t1 = min(n, 32 * ((s + 1) * nbt / ns));
+}
+
+// Stage 1 of an attention item: wait for q, k and v of kv head g (wave
+// w < GQA: q head g GQA + w; wave GQA: k; wave GQA + 1: v; lane l holds dims
+// l + 64 c), then per-head RMSNorm (reference rmsnorm.cuh:57-84) and RoPE
+// rotate-half (attention.cuh:22-44) in registers:
+//   q waves write the three bf16 parts of q as the score product's A rows;
+//   the k / v waves put bf16 K / V of `pos` in LDS (for the block holding pos)
+//   and, in the split that owns pos, append them to the cache (reference
+//   kv_cache.cuh:58-78; write-through agent-scope stores, read by later
+//   tokens on any XCD).
 template <class S>
-__device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int layer, int pos, int g, int s,
-                                  int nsplit, int t0, int t1, unsigned tag_out, int tt) {
-  constexpr int D = S::D, GQA = S::GQA, DPL = D / kWave, KC = KV<S>::KC, DT = KV<S>::DT;
-  static_assert(GQA <= 4, "q heads of a group fit the 16 MFMA columns (4 per head)");
-  const int tid = ltid(), w = tid / kWave, l = tid % kWave;
-  // 1. per-head RMSNorm (reference rmsnorm.cuh:57-84) + RoPE rotate-half
-  //    (attention.cuh:22-44) of the q heads and the k head, one wave per head,
-  //    in registers; lane l holds dims l + 64 c.  q heads are written as the
-  //    score product's B operand (hi / mid / lo bf16 in columns 4j .. 4j+2).
+__device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm, const KV<S>& kvr, int layer,
+                                                   int pos, int g, bool own, unsigned tg, int tt) {
+  constexpr int D = S::D, GQA = S::GQA, DPL = D / kWave;
+  const int w = wave_id();
+  const int l = (int)lane_id();
+  int failed = 0;
+  float v[DPL];
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) v[c] = 0.f;
+  __syncthreads();  // every wave is done with the LDS of its previous phase
+  if (w < GQA + 2) {
+    u64* src = p.qkv + (w < GQA ? (g * GQA + w) * D : (w == GQA ? S::QD + g * D : S::QD + S::KVD + g * D));
+    Spin sp;
+    while (true) {
+      u64 wv[DPL];
+      bool ready = true;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) {
+        wv[c] = ll_get(src + l + kWave * c);
+        ready &= ll_tag(wv[c]) == tg;
+      }
+      if (ready) {
+#pragma unroll
+        for (int c = 0; c < DPL; ++c) v[c] = ll_val(wv[c]);
+        break;
+      }
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    }
+  }
+  trace_mark(p, tt, PHASES_PER_LAYER * layer + 1, 0);
+  evt(p, tt, layer, EV_ATT_READY);
+  const bool append = own && __ballot(failed) == 0ull;  // never append values of a failed wait
+  const long long base = kt_base(p, layer, g, S::NKV, D);
   if (w <= GQA) {
-    float v[DPL];
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < DPL; ++c) {
-      v[c] = sm.qk[w * D + l + c * kWave];
-      ss = fmaf(v[c], v[c], ss);
-    }
+    for (int c = 0; c < DPL; ++c) ss = fmaf(v[c], v[c], ss);
     ss = wave_sum(ss);
     const float r = rsqrtf(ss / (float)D + kRmsEps);
 #pragma unroll
@@ -570,51 +624,57 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
       o[0] = v[0] * sm.rc[l] - v[1] * sm.rs[l];
       o[1] = v[1] * sm.rc[l] + v[0] * sm.rs[l];
     }
+    if (w < GQA) {
 #pragma unroll
-    for (int c = 0; c < DPL; ++c) {
-      sm.qk[w * D + l + c * kWave] = o[c];
-      if (w < GQA) {
+      for (int c = 0; c < DPL; ++c) {
         uint16_t hi, mid, lo;
         split_bf16(o[c], hi, mid, lo);
         sm.qb[4 * w + 0][l + c * kWave] = hi;
         sm.qb[4 * w + 1][l + c * kWave] = mid;
         sm.qb[4 * w + 2][l + c * kWave] = lo;
       }
+    } else {
+      uint16_t* krow = p.kv + base + (long long)pos * D;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) {
+        const uint16_t kb = f32_to_bf16(o[c]);
+        reinterpret_cast<uint16_t*>(sm.kvcur[0])[l + c * kWave] = kb;
+        if (append) __hip_atomic_store(krow + l + c * kWave, kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  } else if (w == GQA + 1) {
+    uint16_t* vt = p.kvt + base + (long long)(pos / 32) * 32 * D + (pos % 32);
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) {
+      const uint16_t vb = f32_to_bf16(v[c]);
+      reinterpret_cast<uint16_t*>(sm.kvcur[1])[l + c * kWave] = vb;
+      if (append)
+        __hip_atomic_store(vt + (long long)(l + c * kWave) * 32, vb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  __syncthreads();
-  // 2. bf16 K/V of the current position (reference kv_cache.cuh:58-78).  The
-  //    split that owns `pos` appends them to the cache (write-through
-  //    agent-scope stores, read by later tokens on any XCD); the blocks that
-  //    hold `pos` take them from LDS.
-  const long long base = kt_base(p, layer, g, S::NKV, D);
-  const bool own = (t0 <= pos && pos < t1);
-  if (tid < D / 2) {
-    const int d = 2 * tid;
-    const unsigned kw = (unsigned)f32_to_bf16(sm.qk[GQA * D + d]) | ((unsigned)f32_to_bf16(sm.qk[GQA * D + d + 1]) << 16);
-    const uint16_t v0 = f32_to_bf16(sm.qk[(GQA + 1) * D + d]), v1 = f32_to_bf16(sm.qk[(GQA + 1) * D + d + 1]);
-    if (tid == 0) evt(p, tt, layer, EV_ATT_ROPE);
-    reinterpret_cast<unsigned*>(sm.kvcur[0])[tid] = kw;
-    reinterpret_cast<unsigned*>(sm.kvcur[1])[tid] = (unsigned)v0 | ((unsigned)v1 << 16);
-    if (own) {
-      __hip_atomic_store(reinterpret_cast<unsigned*>(p.kv + base + (long long)pos * D) + tid, kw, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      uint16_t* vt = p.kvt + base + (long long)(pos / 32) * 32 * D + (pos % 32);
-      __hip_atomic_store(vt + (long long)d * 32, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(vt + (long long)(d + 1) * 32, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  __syncthreads();
-  // 3. per-wave online softmax over the wave's blocks (fp32); scale 1/sqrt(D).
+  return !block_failed(failed);
+}
+
+// One attention item (kv head g, split s of nsplit over positions [t0, t1)):
+// per-wave online softmax over the wave's blocks on the matrix cores, the NW
+// waves combined in LDS, and the item's partial -- unnormalised output and
+// (max, sum) per q head -- published as packed pairs for the O phase, which
+// merges the splits.  K / V of the wave's first blocks are already in kvr.
+template <class S>
+__device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int layer, int pos, int g, int s,
+                                  int t0, int t1, unsigned tg, int tt) {
+  constexpr int D = S::D, GQA = S::GQA, KC = KV<S>::KC, DT = KV<S>::DT;
+  static_assert(GQA <= 4, "q heads of a group fit the 16 MFMA rows (4 per head)");
+  if (!attention_prologue<S>(p, sm, kvr, layer, pos, g, t0 <= pos && pos < t1, tg, tt)) return false;
+  evt(p, tt, layer, EV_ATT_ROPE);
+  const int tid = ltid(), w = tid / kWave;
   const float scale = 1.0f / sqrtf((float)D);
   const unsigned lu = lane_id();
-  const int col = (int)(lu & 15u), rg = (int)(lu >> 4);  // MFMA column, row group
-  const int hj = col >> 2;                                // head of this column
-  const bool head_lane = (col & 3) == 0 && hj < GQA;      // lane holding head hj's sums
-  u32x4 qbf[KC];  // B operand of the score product
+  const int c16 = (int)(lu & 15u), rg = (int)(lu >> 4);  // MFMA column / row group (= head)
+  u32x4 qa[KC];  // A operand of the score product
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc) qbf[kc] = *reinterpret_cast<const u32x4*>(&sm.qb[col][32 * kc + 8 * rg]);
-  float m = -INFINITY, lsum = 0.f;  // per head (valid in head lanes)
+  for (int kc = 0; kc < KC; ++kc) qa[kc] = *reinterpret_cast<const u32x4*>(&sm.qb[c16][32 * kc + 8 * rg]);
+  float m = -INFINITY, lsum = 0.f;  // of head rg (meaningful for rg < GQA)
   f32x4 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -629,7 +689,7 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
       const int bp = 32 * (b0 + bi + q * NW);
       if (bi + q * NW < nb && bp <= pos && pos < bp + 32) {
         const int rp = pos - bp;
-        if ((int)(lu & 15u) == (rp & 15)) {
+        if (c16 == (rp & 15)) {
 #pragma unroll
           for (int kc = 0; kc < KC; ++kc)
             if (rp >> 4) kvr.k[q][1][kc] = sm.kvcur[0][4 * kc + rg];
@@ -638,202 +698,194 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
         if (rg == (rp >> 3)) {
           const uint16_t* vc = reinterpret_cast<const uint16_t*>(sm.kvcur[1]);
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) kvr.v[q][dt] = set_bf16(kvr.v[q][dt], rp & 7, vc[16 * dt + col]);
+          for (int dt = 0; dt < DT; ++dt) kvr.v[q][dt] = set_bf16(kvr.v[q][dt], rp & 7, vc[16 * dt + c16]);
         }
       }
     }
-    // scores: sc[q][h][i] = position 32 (b0 + bi + q NW) + 16 h + 4 rg + i, column col
-    f32x4 sc[KVB][2];
-#pragma unroll
-    for (int q = 0; q < KVB; ++q)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        sc[q][h] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc)
-          sc[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.k[q][h][kc]),
-                                                            __builtin_bit_cast(bf16x8, qbf[kc]), sc[q][h], 0, 0, 0);
-      }
+    // scores: lane (rg, c16) gets head rg at positions 32 (b0 + bi + q NW) + 16 h + c16
+    float sc[KVB][2];
     float bmax = -INFINITY;
 #pragma unroll
     for (int q = 0; q < KVB; ++q)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h) {
+        f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = (sc[q][h][i] + dpp_sel<DPP_XOR1>(sc[q][h][i])) + dpp_sel<DPP_XOR2>(sc[q][h][i]);
-          const int t = 32 * (b0 + bi + q * NW) + 16 * h + 4 * rg + i;
-          sc[q][h][i] = (bi + q * NW < nb && t < t1 && head_lane) ? v * scale : -INFINITY;
-          bmax = fmaxf(bmax, sc[q][h][i]);
-        }
-    bmax = max_xor32(max_xor16(bmax));
-    const float mn = fmaxf(m, bmax);  // finite in head lanes (block bi has a valid position)
+        for (int kc = 0; kc < KC; ++kc)
+          d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[kc]),
+                                                      __builtin_bit_cast(bf16x8, kvr.k[q][h][kc]), d4, 0, 0, 0);
+        const float v = (d4[0] + d4[1]) + d4[2];
+        const int t = 32 * (b0 + bi + q * NW) + 16 * h + c16;
+        sc[q][h] = (bi + q * NW < nb && t < t1) ? v * scale : -INFINITY;
+        bmax = fmaxf(bmax, sc[q][h]);
+      }
+    bmax = group_max<16>(bmax);
+    const float mn = fmaxf(m, bmax);  // finite: block bi has a valid position
     const float alpha = __expf(m - mn);
     m = mn;
     float bsum = 0.f;
 #pragma unroll
     for (int q = 0; q < KVB; ++q)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[q][h][i] = head_lane ? __expf(sc[q][h][i] - mn) : 0.f;
-          bsum += sc[q][h][i];
-        }
-    lsum = lsum * alpha + sum_xor32(sum_xor16(bsum));
-    // weights -> the output product's B operand via LDS: each head lane
-    // writes the hi / mid / lo parts of its weights into columns 4j .. 4j+2
-    // (LDS operations of one wave complete in order; the other columns stay 0)
-    if (head_lane) {
+      for (int h = 0; h < 2; ++h) {
+        sc[q][h] = __expf(sc[q][h] - mn);
+        bsum += sc[q][h];
+      }
+    lsum = lsum * alpha + group_sum<16>(bsum);
+    // weights -> the output product's A rows via LDS (rows 4 rg .. 4 rg + 2;
+    // LDS operations of one wave complete in order; the other rows stay 0)
+    if (rg < GQA) {
 #pragma unroll
       for (int q = 0; q < KVB; ++q)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const Split3 a = split3(sc[q][h][0]), b = split3(sc[q][h][1]), c = split3(sc[q][h][2]),
-                       d = split3(sc[q][h][3]);
-          const int o = 32 * q + 16 * h + 4 * rg;
-          *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 0][o]) = uint2{pack_hi16(a.hi, b.hi), pack_hi16(c.hi, d.hi)};
-          *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 1][o]) = uint2{pack_hi16(a.mid, b.mid), pack_hi16(c.mid, d.mid)};
-          *reinterpret_cast<uint2*>(&sm.pb[w][4 * hj + 2][o]) = uint2{pack_hi16(a.lo, b.lo), pack_hi16(c.lo, d.lo)};
+          const Split3 a = split3(sc[q][h]);
+          const int o = 32 * q + 16 * h + c16;
+          sm.pb[w][4 * rg + 0][o] = (uint16_t)(a.hi >> 16);
+          sm.pb[w][4 * rg + 1][o] = (uint16_t)(a.mid >> 16);
+          sm.pb[w][4 * rg + 2][o] = (uint16_t)(a.lo >> 16);
         }
     }
     asm volatile("" ::: "memory");
-    const float aq = dpp_sel<0x00>(alpha);  // quad_perm [0,0,0,0]: the head lane's factor
-    u32x4 pbq[KVB];
+    u32x4 pa[KVB];
 #pragma unroll
-    for (int q = 0; q < KVB; ++q) pbq[q] = *reinterpret_cast<const u32x4*>(&sm.pb[w][col][32 * q + 8 * rg]);
+    for (int q = 0; q < KVB; ++q) pa[q] = *reinterpret_cast<const u32x4*>(&sm.pb[w][c16][32 * q + 8 * rg]);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[dt][i] *= aq;
+      for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
 #pragma unroll
       for (int q = 0; q < KVB; ++q)
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kvr.v[q][dt]),
-                                                         __builtin_bit_cast(bf16x8, pbq[q]), acc[dt], 0, 0, 0);
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa[q]),
+                                                         __builtin_bit_cast(bf16x8, kvr.v[q][dt]), acc[dt], 0, 0, 0);
     }
   }
   evt(p, tt, layer, EV_ATT_SOFTMAX);
-  // 4. per-wave partials -> LDS (head lanes: dims 16 dt + 4 rg + i), then merge the NW waves.
+  // per-wave partials -> LDS (lane (rg, c16): head rg, dims 16 dt + c16)
+  if (rg < GQA) {
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[dt][i] = (acc[dt][i] + dpp_sel<DPP_XOR1>(acc[dt][i])) + dpp_sel<DPP_XOR2>(acc[dt][i]);
-  evt(p, tt, layer, EV_ATT_REDUCED);
-  if (head_lane) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<f32x4*>(&sm.pv[(w * GQA + hj) * D + 16 * dt + 4 * rg]) = acc[dt];
-    if (rg == 0) {
-      sm.mw[w * GQA + hj] = m;
-      sm.lw[w * GQA + hj] = lsum;
+    for (int dt = 0; dt < DT; ++dt) sm.pv[w][rg * D + 16 * dt + c16] = (acc[dt][0] + acc[dt][1]) + acc[dt][2];
+    if (c16 == 0) {
+      sm.mw[rg][w] = m;
+      sm.lw[rg][w] = lsum;
     }
   }
   __syncthreads();
-  // 5. this item's partial over its NW waves: (M, L, acc) per q head.
-  constexpr int W = GQA * (D + 2);
-  // Every wave's max is read first (independent LDS reads, no branches); a
-  // wave without positions has max -inf and weight exp(-inf) = 0.  The item's
-  // max is finite (every split has positions).
-  if (tid < GQA) {
-    float mi[NW], li[NW];
+  evt(p, tt, layer, EV_ATT_REDUCED);
+  // The item's partial over its NW waves: one output pair (two dims of one
+  // head) per lane of the first NPAIR / 64 waves, so each of those waves
+  // publishes whole 128-byte lines.  A wave without positions has max -inf
+  // and weight exp(-inf) = 0; the item's max is finite.
+  constexpr int NPAIR = GQA * D / 2;
+  static_assert(NPAIR <= NT, "pairs of a group fit the workgroup");
+  if (tid < NPAIR) {
+    const int pi = tid, j = (2 * pi) / D;
+    float mv[NW], lv[NW];
+    float2 pv[NW];
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
-      mi[i] = sm.mw[i * GQA + tid];
-      li[i] = sm.lw[i * GQA + tid];
+      mv[i] = sm.mw[j][i];
+      lv[i] = sm.lw[j][i];
+      pv[i] = *reinterpret_cast<const float2*>(&sm.pv[i][2 * pi]);
     }
-    float M = mi[0];
+    float M = mv[0];
 #pragma unroll
-    for (int i = 1; i < NW; ++i) M = fmaxf(M, mi[i]);
-    float Lw = 0.f;
+    for (int i = 1; i < NW; ++i) M = fmaxf(M, mv[i]);
+    float o0 = 0.f, o1 = 0.f, ls = 0.f;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) Lw = fmaf(__expf(mi[i] - M), li[i], Lw);
-    sm.gm[tid] = M;
-    sm.gl[tid] = Lw;
+    for (int i = 0; i < NW; ++i) {
+      const float f = __expf(mv[i] - M);
+      o0 = fmaf(f, pv[i].x, o0);
+      o1 = fmaf(f, pv[i].y, o1);
+      ls = fmaf(f, lv[i], ls);
+    }
+    const unsigned t4 = tag4(tg + 1u);
+    u64* dst = p.part + ((long long)s * S::NKV + g) * part_words<S>();
+    ll_put(dst + pi, pk_pack(o0, o1, t4));
+    if ((2 * pi) % D == 0) ll_put(dst + NPAIR + j, pk_pack(M, ls, t4));
   }
-  float av[(GQA * D + NT - 1) / NT];
-#pragma unroll
-  for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
-    const int e = tid + k * NT;
-    av[k] = 0.f;
-    if (e < GQA * D) {
-      const int j = e / D;
-      float mi[NW], pi[NW];
-#pragma unroll
-      for (int i = 0; i < NW; ++i) {
-        mi[i] = sm.mw[i * GQA + j];
-        pi[i] = sm.pv[i * GQA * D + e];
-      }
-      float M = mi[0];
-#pragma unroll
-      for (int i = 1; i < NW; ++i) M = fmaxf(M, mi[i]);
-#pragma unroll
-      for (int i = 0; i < NW; ++i) av[k] = fmaf(__expf(mi[i] - M), pi[i], av[k]);
-    }
-  }
-  __syncthreads();
-  evt(p, tt, layer, EV_ATT_COMBINED);
-  u64* prow = p.part + ((long long)g * p.nsplit_max + s) * W;
-  if (s != 0) {  // publish the partial for this group's merger (split 0)
-    if (tid < GQA) {
-      ll_put(prow + tid, ll_pack(sm.gm[tid], tag_out));
-      ll_put(prow + GQA + tid, ll_pack(sm.gl[tid], tag_out));
-    }
-#pragma unroll
-    for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
-      const int e = tid + k * NT;
-      if (e < GQA * D) ll_put(prow + 2 * GQA + e, ll_pack(av[k], tag_out));
-    }
-    evt(p, tt, layer, EV_ATT_PARTIAL);
-    return true;
-  }
-  // 6. split 0 merges the group's other splits (log-sum-exp) and publishes the
-  //    normalised attention output of its GQA heads.
-  if (nsplit > 1 && !fetch1<8>(prow + W, (nsplit - 1) * W, sm.mbuf, tag_out, p, W)) return false;
-  evt(p, tt, layer, EV_ATT_GATHERED);
-  // log-sum-exp merge, each output element on its own thread: all LDS reads
-  // are independent (eight splits per step, splits past nsplit selected away)
-#pragma unroll
-  for (int k = 0; k < (GQA * D + NT - 1) / NT; ++k) {
-    const int e = tid + k * NT;
-    if (e < GQA * D) {
-      const int j = e / D;
-      const float m0 = sm.gm[j];
-      float M = m0;
-      for (int q0 = 1; q0 < nsplit; q0 += 8) {
-        float mq[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) mq[u] = sm.mbuf[(min(q0 + u, NSPLIT_CAP - 1) - 1) * W + j];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) M = q0 + u < nsplit ? fmaxf(M, mq[u]) : M;
-      }
-      const float f0 = __expf(m0 - M);
-      float o = f0 * av[k], Lt = f0 * sm.gl[j];
-      for (int q0 = 1; q0 < nsplit; q0 += 8) {
-        float mq[8], lq[8], xq[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int r = (min(q0 + u, NSPLIT_CAP - 1) - 1) * W;
-          mq[u] = sm.mbuf[r + j];
-          lq[u] = sm.mbuf[r + GQA + j];
-          xq[u] = sm.mbuf[r + 2 * GQA + e];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const bool ok = q0 + u < nsplit;  // select, not multiply: stale LDS may hold anything
-          const float f = __expf(mq[u] - M);
-          o = ok ? fmaf(f, xq[u], o) : o;
-          Lt = ok ? fmaf(f, lq[u], Lt) : Lt;
-        }
-      }
-      // packed pairs: even lanes store (own, neighbour) -- e and e ^ 1 are
-      // adjacent lanes of the same wave
-      const float val = o / Lt;
-      const float nb = dpp_sel<DPP_XOR1>(val);
-      if ((e & 1) == 0) ll_put(p.attn + ((long long)g * GQA * D + e) / 2, pk_pack(val, nb, tag4(tag_out)));
-    }
-  }
-  evt(p, tt, layer, EV_MERGE_DONE);
+  evt(p, tt, layer, EV_ATT_PARTIAL);
   return true;
+}
+
+// O phase input: wait for the partials of the nsplit splits of every kv head
+// and merge them (log-sum-exp, reference attention.cuh:96-140 computes the
+// same softmax in one pass) into dst[QD], in batches of SB splits with a
+// running max; plus, unless xrows is null, the 16 tagged residual rows of this
+// workgroup's block.  Thread t owns output pairs t + k NT.
+template <class S>
+__device__ __forceinline__ bool fetch_attn(const Params& p, int nsplit, unsigned t4, u64* xrows, unsigned xtag,
+                                           float* dst, float* xres) {
+  constexpr int NPG = S::GQA * S::D / 2;  // pairs per kv head
+  constexpr int WP = part_words<S>();
+  constexpr int PPT = (S::QD / 2 + NT - 1) / NT;
+  constexpr int SB = 8;
+  const int tid = ltid();
+  int failed = 0;
+  __syncthreads();  // every wave is done with the LDS of its previous phase
+  float M[PPT], L[PPT], o0[PPT], o1[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) M[k] = -INFINITY, L[k] = 0.f, o0[k] = 0.f, o1[k] = 0.f;
+  for (int s0 = 0; s0 < nsplit && !failed; s0 += SB) {
+    u64 wa[PPT][SB], wm[PPT][SB], wx = 0ull;
+    const bool want_x = s0 == 0 && xrows && tid < 16;
+    Spin sp;
+    while (true) {
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < PPT; ++k) {
+        const int pi = tid + k * NT;
+        const int g = pi / NPG, pg = pi % NPG, j = (2 * pg) / S::D;
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          wa[k][u] = 0ull;
+          wm[k][u] = 0ull;
+          if (pi < S::QD / 2 && s0 + u < nsplit) {
+            u64* src = p.part + ((long long)(s0 + u) * S::NKV + g) * WP;
+            wa[k][u] = ll_get(src + pg);
+            wm[k][u] = ll_get(src + NPG + j);
+            ready &= pk_ready(wa[k][u], t4) && pk_ready(wm[k][u], t4);
+          }
+        }
+      }
+      if (want_x) {
+        wx = ll_get(xrows + tid);
+        ready &= ll_tag(wx) == xtag;
+      }
+      if (ready) break;
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    }
+    if (want_x) xres[tid] = ll_val(wx);
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      float Mb = M[k];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) Mb = s0 + u < nsplit ? fmaxf(Mb, pk_lo(wm[k][u])) : Mb;
+      const float r = __expf(M[k] - Mb);  // 0 on the first batch
+      o0[k] *= r, o1[k] *= r, L[k] *= r;
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const bool ok = s0 + u < nsplit;  // select, not multiply: skipped words hold anything
+        const float f = __expf(pk_lo(wm[k][u]) - Mb);
+        o0[k] = ok ? fmaf(f, pk_lo(wa[k][u]), o0[k]) : o0[k];
+        o1[k] = ok ? fmaf(f, pk_hi(wa[k][u]), o1[k]) : o1[k];
+        L[k] = ok ? fmaf(f, pk_hi(wm[k][u]), L[k]) : L[k];
+      }
+      M[k] = Mb;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int pi = tid + k * NT;
+    if (pi < S::QD / 2) {
+      dst[2 * pi] = o0[k] / L[k];
+      dst[2 * pi + 1] = o1[k] / L[k];
+    }
+  }
+  return !block_failed(failed);
 }
 
 // argmax over the G per-workgroup words of a token (tag t14): the token id.
@@ -918,13 +970,11 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     __syncthreads();
     // attention split: nsplit <= nsplit_max items per kv head, none empty
     const int n = pos + 1;
-    int ns0 = (n + p.chunk_min - 1) / p.chunk_min;
-    ns0 = ns0 < 1 ? 1 : (ns0 > p.nsplit_max ? p.nsplit_max : ns0);
-    const int chunk = ((n + ns0 - 1) / ns0 + 31) / 32 * 32;  // whole 32-position blocks
-    const int nsplit = (n + chunk - 1) / chunk;
+    const int nsplit = split_count(n, p.chunk_min, p.nsplit_max);
     const bool has_att = it_att < S::NKV * nsplit;
     const int ag = has_att ? it_att / nsplit : 0, as = has_att ? it_att % nsplit : 0;
-    const int at0 = as * chunk, at1 = min(n, at0 + chunk);
+    int at0, at1;
+    split_range(n, nsplit, as, &at0, &at1);
 
     for (int layer = 0; layer < L; ++layer) {
       const int tid = ltid();
@@ -964,14 +1014,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       // ---------------- P2: attention partials (prefetch: O)
       if (it_o < S::RB_H) blk_load(ro, wl + S::OFF_O + (long long)it_o * S::KT_Q * 64);
       if (has_att) {
-        const int D = S::D, GQA = S::GQA;
-        if (!fetch3<1>(Range{p.qkv + ag * GQA * D, GQA * D, sm.qk, tg, 16},
-                       Range{p.qkv + S::QD + ag * D, D, sm.qk + GQA * D, tg, 16},
-                       Range{p.qkv + S::QD + S::KVD + ag * D, D, sm.qk + (GQA + 1) * D, tg, 16}, p))
-          return;
-        trace_mark(p, t, slot + 1, 0);
-        evt(p, t, layer, EV_ATT_READY);
-        if (!attention_compute<S>(p, sm, rkv, layer, pos, ag, as, nsplit, at0, at1, tg + 1u, t)) return;
+        if (!attention_compute<S>(p, sm, rkv, layer, pos, ag, as, at0, at1, tg, t)) return;
         evt(p, t, layer, EV_ATT_STORED);
         trace_mark(p, t, slot + 1, 1);
       }
@@ -983,8 +1026,8 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         gains_load(gf, nrm + S::NORM_FFN);
       }
       if (it_o < S::RB_H) {
-        if (!fetch_pk<S::QD / 2>(p, p.attn, tag4(tg + 1u), layer > 0 ? p.x + it_o * 16 : nullptr, tg_x, sm.vec_o,
-                                 sm.xres_o))
+        if (!fetch_attn<S>(p, nsplit, tag4(tg + 1u), layer > 0 ? p.x + it_o * 16 : nullptr, tg_x, sm.vec_o,
+                           sm.xres_o))
           return;
         trace_mark(p, t, slot + 2, 0);
         evt(p, t, layer, EV_O_READY);
