@@ -35,9 +35,12 @@ constexpr int NT = 512;               // threads per workgroup (8 waves)
 constexpr int NW = NT / kWave;
 constexpr int PHASES_PER_LAYER = 5;
 #ifndef MK_KV_BLOCKS
-#define MK_KV_BLOCKS 1
+#define MK_KV_BLOCKS 2
 #endif
-constexpr int KVB = MK_KV_BLOCKS;  // 32-position blocks a wave holds in registers
+// 32-position K/V blocks a wave holds in registers (prefetched a layer ahead).
+// Two per wave halves the attention splits (and so the partials every O
+// workgroup merges) against one, at the cost of a longer block step.
+constexpr int KVB = MK_KV_BLOCKS;
 
 constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
 constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
@@ -127,6 +130,17 @@ __device__ __forceinline__ void blk_load(Blk<KC>& b, const u32x4* __restrict__ b
   for (int kc = 0; kc < KC; ++kc) b.w[kc] = buf_ld_nt(rs, lb, (unsigned)(w * KC + kc) * 1024u);
 }
 
+// A prefetch register set that this workgroup does not load in this phase
+// gets an unspecified value: every path to its next use then defines it, so
+// the compiler does not keep the previous phase's contents alive around the
+// layer loop (loads and uses sit under the same runtime condition, which it
+// cannot see).
+template <int KC>
+__device__ __forceinline__ void blk_forget(Blk<KC>& b) {
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) b.w[kc] = __builtin_nondeterministic_value(b.w[kc]);
+}
+
 // Row of the block this lane's dot product belongs to, and the lane that
 // stores it (lanes 0 and 32).
 __device__ __forceinline__ int blk_row() { return 2 * wave_id() + (int)(lane_id() >> 5); }
@@ -176,6 +190,12 @@ struct NormIn {
   static constexpr int PER = (S::H + NT - 1) / NT;
   float g[PER];
 };
+
+template <class S>
+__device__ __forceinline__ void gains_forget(NormIn<S>& n) {
+#pragma unroll
+  for (int k = 0; k < NormIn<S>::PER; ++k) n.g[k] = __builtin_nondeterministic_value(n.g[k]);
+}
 
 // The gains of this thread's elements, loaded before the phase's wait.
 template <class S>
@@ -532,6 +552,21 @@ __device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, in
   }
 }
 
+template <class S>
+__device__ __forceinline__ void kv_forget(KV<S>& r) {
+#pragma unroll
+  for (int q = 0; q < KVB; ++q) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int kc = 0; kc < KV<S>::KC; ++kc) r.k[q][h][kc] = __builtin_nondeterministic_value(r.k[q][h][kc]);
+#pragma unroll
+    for (int dt = 0; dt < KV<S>::DT; ++dt) r.v[q][dt] = __builtin_nondeterministic_value(r.v[q][dt]);
+  }
+#pragma unroll
+  for (int c = 0; c < S::D / kWave; ++c) r.gn[c] = __builtin_nondeterministic_value(r.gn[c]);
+}
+
 // QK-norm gains of this lane's dims: waves 0..GQA-1 normalise q heads, wave
 // GQA the k head.
 template <class S>
@@ -559,6 +594,22 @@ __device__ __forceinline__ void split_range(int n, int ns, int s, int* t0, int* 
   const int nbt = (n + 31) / 32;
   *t0 = 32 * (s * nbt / ns);
   *t1 = min(n, 32 * ((s + 1) * nbt / ns));
+}
+
+// The attention item of work index `it` for n cached positions: kv head g,
+// split s of nsplit, positions [t0, t1).
+struct Item {
+  bool on;
+  int g, s, t0, t1, nsplit;
+};
+__device__ __forceinline__ Item att_item(int it, int n, int nkv, int chunk_min, int nsplit_max) {
+  Item r;
+  r.nsplit = split_count(n, chunk_min, nsplit_max);
+  r.on = it < nkv * r.nsplit;
+  r.g = r.on ? it / r.nsplit : 0;
+  r.s = r.on ? it % r.nsplit : 0;
+  split_range(n, r.nsplit, r.s, &r.t0, &r.t1);
+  return r;
 }
 
 // Stage 1 of an attention item: wait for q, k and v of kv head g (wave
@@ -954,6 +1005,9 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     if (it_qkv < S::RB_QKV) {
       blk_load(rq, p.layers + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
       gains_load(gq, p.norms + S::NORM_ATTN);
+    } else {
+      blk_forget(rq);
+      gains_forget(gq);
     }
     if (t > 0) {
       if (!token_from_slots(p, p.amax + ((t - 1) & 1) * G, tag14(tb - 1u), sm.amax, &tok)) return;
@@ -968,13 +1022,22 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     if (p.dbg_layers && wg == 0)
       for (int i = tid; i < S::H; i += NT) p.dbg_layers[i] = packed_elem<S::KT_H>(p.lmhead, tok, i);
     __syncthreads();
-    // attention split: nsplit <= nsplit_max items per kv head, none empty
+    // attention split: nsplit <= nsplit_max items per kv head, none empty;
+    // this token's item and the next token's (whose layer-0 K/V this
+    // workgroup prefetches during the last layer)
     const int n = pos + 1;
-    const int nsplit = split_count(n, p.chunk_min, p.nsplit_max);
-    const bool has_att = it_att < S::NKV * nsplit;
-    const int ag = has_att ? it_att / nsplit : 0, as = has_att ? it_att % nsplit : 0;
-    int at0, at1;
-    split_range(n, nsplit, as, &at0, &at1);
+    const Item cur = att_item(it_att, n, S::NKV, p.chunk_min, p.nsplit_max);
+    const Item nxt = att_item(it_att, n + 1, S::NKV, p.chunk_min, p.nsplit_max);
+    const int nsplit = cur.nsplit;
+    const bool has_att = cur.on;
+    if (t == 0) {
+      if (has_att) {
+        kv_load<S>(rkv, p, 0, cur.g, cur.t0 / 32, (cur.t1 - cur.t0 + 31) / 32, wave_id());
+        gain_load_qk<S>(rkv, p, 0);
+      } else {
+        kv_forget<S>(rkv);
+      }
+    }
 
     for (int layer = 0; layer < L; ++layer) {
       const int tid = ltid();
@@ -986,11 +1049,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       // Each phase issues the next phase's prefetch before its own wait:
       // loads complete in order, so the wait absorbs the prefetch, and no
       // product ever waits behind loads issued after its own block.
-      // ---------------- P1: QKV (prefetch: attention K/V + QK-norm gains)
-      if (has_att) {
-        kv_load<S>(rkv, p, layer, ag, at0 / 32, (at1 - at0 + 31) / 32, wave_id());
-        gain_load_qk<S>(rkv, p, layer);
-      }
+      // ---------------- P1: QKV
       if (it_qkv < S::RB_QKV) {
         float r;
         if (layer > 0) {
@@ -1013,10 +1072,22 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       }
       // ---------------- P2: attention partials (prefetch: O)
       if (it_o < S::RB_H) blk_load(ro, wl + S::OFF_O + (long long)it_o * S::KT_Q * 64);
+      else blk_forget(ro);
       if (has_att) {
-        if (!attention_compute<S>(p, sm, rkv, layer, pos, ag, as, at0, at1, tg, t)) return;
+        if (!attention_compute<S>(p, sm, rkv, layer, pos, cur.g, cur.s, cur.t0, cur.t1, tg, t)) return;
         evt(p, t, layer, EV_ATT_STORED);
         trace_mark(p, t, slot + 1, 1);
+      }
+      {  // K/V of this workgroup's next item (next layer, or the next token's
+         // layer 0): a whole layer ahead, so no later poll queues behind it
+        const bool last = layer + 1 == L;
+        const Item ni = last ? nxt : cur;
+        if (ni.on && (!last || t + 1 < p.n_tokens)) {
+          kv_load<S>(rkv, p, last ? 0 : layer + 1, ni.g, ni.t0 / 32, (ni.t1 - ni.t0 + 31) / 32, wave_id());
+          gain_load_qk<S>(rkv, p, last ? 0 : layer + 1);
+        } else {
+          kv_forget<S>(rkv);
+        }
       }
       // ---------------- P3: O projection + residual (prefetch: gate/up + ffn gains)
       if (it_gu < S::RB_F) {
@@ -1024,6 +1095,10 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         blk_load(rg, gp);
         blk_load(ru, gp + S::KT_H * 64);
         gains_load(gf, nrm + S::NORM_FFN);
+      } else {
+        blk_forget(rg);
+        blk_forget(ru);
+        gains_forget(gf);
       }
       if (it_o < S::RB_H) {
         if (!fetch_attn<S>(p, nsplit, tag4(tg + 1u), layer > 0 ? p.x + it_o * 16 : nullptr, tg_x, sm.vec_o,
@@ -1052,6 +1127,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       }
       // ---------------- P4: gate/up + SiLU (prefetch: down)
       if (it_dn < S::RB_H) blk_load(rd, wl + S::OFF_DOWN + (long long)it_dn * S::KT_F * 64);
+      else blk_forget(rd);
       if (it_gu < S::RB_F) {
         float r;
         if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return;
@@ -1077,6 +1153,9 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       if (layer + 1 < L && it_qkv < S::RB_QKV) {
         blk_load(rq, wl + S::U_LAYER + S::OFF_QKV + (long long)it_qkv * S::KT_H * 64);
         gains_load(gq, nrm + S::NORM_STRIDE + S::NORM_ATTN);
+      } else {
+        blk_forget(rq);
+        gains_forget(gq);
       }
       if (it_dn < S::RB_H) {
         if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x + it_dn * 16, tg + 2u, sm.vec_d, sm.xres_d)) return;
