@@ -104,10 +104,11 @@ def trace_summary(eng, shape, args, info):
     prev_done = None
     wait = {k: [] for k in names + ["lm_head"]}
     work = {k: [] for k in names + ["lm_head"]}
+    own = {k: [] for k in names + ["lm_head"]}  # per-workgroup ready -> done
     t_first = None
     for slot in range(n):
         rd, dn = tr[slot, 0], tr[slot, 1]
-        act = dn > 0
+        act = (dn > 0) & (rd > 0)
         if not act.any():
             continue
         last_ready, last_done = rd[act].max(), dn[act].max()
@@ -117,16 +118,21 @@ def trace_summary(eng, shape, args, info):
         if prev_done is not None:
             wait[name].append((last_ready - prev_done) * us)
         work[name].append((last_done - last_ready) * us)
+        own[name].append(np.median(dn[act] - rd[act]) * us)
         prev_done = last_done
     total = (prev_done - t_first) * us
     print(f"# trace of one token at ctx {args.ctx + 4}: {total:.1f} us from first ready to last done", file=sys.stderr)
     for k in names + ["lm_head"]:
         w = np.mean(wait[k]) if wait[k] else 0.0
         d = np.mean(work[k]) if work[k] else 0.0
-        print(f"#   {k:8s} handoff {w:7.2f} us   last-ready->last-done {d:7.2f} us   (x{len(work[k])})",
-              file=sys.stderr)
+        o = np.mean(own[k]) if own[k] else 0.0
+        print(f"#   {k:8s} handoff {w:7.2f} us   last-ready->last-done {d:7.2f} us   "
+              f"per-workgroup ready->done (median) {o:6.2f} us   (x{len(work[k])})", file=sys.stderr)
     evn = ["att_ready", "att_rope", "att_softmax", "att_stored", "att_partial", "att_gathered", "o_ready",
            "o_stored", "qkv_stored", "gu_stored", "dn_stored", "dn_ready", "att_reduced", "att_combined", "merge_scaled", "merge_done"]
+    if not (ev > 0).any():
+        print("# (fine-grained events are compiled in with -DMK_TRACE_EVENTS=1)", file=sys.stderr)
+        return
     base = min(ev[e][ev[e] > 0].min() for e in range(len(evn)) if (ev[e] > 0).any())
     print(f"# events of layer {L // 2} (us from the first event; min / median / max over workgroups):",
           file=sys.stderr)

@@ -41,6 +41,12 @@ constexpr int PHASES_PER_LAYER = 5;
 // Two per wave halves the attention splits (and so the partials every O
 // workgroup merges) against one, at the cost of a longer block step.
 constexpr int KVB = MK_KV_BLOCKS;
+// Cache policy of the LM-head stream (buffer-load aux bits): plain loads
+// measured 5 % faster than non-temporal ones on the LM head (part of it is
+// served from the memory-side cache across tokens).
+#ifndef MK_LMHEAD_AUX
+#define MK_LMHEAD_AUX 0
+#endif
 
 constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
 constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
@@ -202,9 +208,9 @@ template <class S>
 __device__ __forceinline__ void gains_load(NormIn<S>& n, const uint16_t* gain) {
   const int t_ = ltid();
 #pragma unroll
-  for (int k = 0; k < NormIn<S>::PER; ++k) {
+  for (int k = 0; k < NormIn<S>::PER; ++k) {  // unconditional loads: no wait until the gains are used
     const int i = t_ + k * NT;
-    n.g[k] = i < S::H ? bf16_to_f32(gain[i]) : 0.f;
+    n.g[k] = bf16_to_f32(gain[i < S::H ? i : S::H - 1]);
   }
 }
 
@@ -235,15 +241,16 @@ __device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned t
   u64 wv[PER];
   Spin sp;
   while (true) {
-    bool ready = true;
+    // every load is issued before any is tested (one round trip per poll
+    // round, not one per word); indices past the vector re-read its last word
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const int i = tid + k * NT;
-      if (i < S::H) {
-        wv[k] = ll_get(src + i);
-        ready &= ll_tag(wv[k]) == tag;
-      }
+      wv[k] = ll_get(src + (i < S::H ? i : S::H - 1));
     }
+    bool ready = true;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) ready &= tid + k * NT >= S::H || ll_tag(wv[k]) == tag;
     if (ready) break;
     if (!sp.step(p.err, p.timeout_ticks)) {
       failed = 1;
@@ -277,17 +284,18 @@ __device__ __forceinline__ bool fetch_pk(const Params& p, u64* src, unsigned t4,
   u64 wv[PER];
   Spin sp;
   while (true) {
+    // every load is issued before any is tested (one round trip per poll
+    // round); indices past the inputs re-read word 0 of the vector
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = tid + k * NT;
+      wv[k] = ll_get(i < NPK ? src + i : (i < tot ? xrows + (i - NPK) : src));
+    }
     bool ready = true;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const int i = tid + k * NT;
-      if (i < NPK) {
-        wv[k] = ll_get(src + i);
-        ready &= pk_ready(wv[k], t4);
-      } else if (i < tot) {
-        wv[k] = ll_get(xrows + (i - NPK));
-        ready &= ll_tag(wv[k]) == xtag;
-      }
+      ready &= i < NPK ? pk_ready(wv[k], t4) : (i >= tot || ll_tag(wv[k]) == xtag);
     }
     if (ready) break;
     if (!sp.step(p.err, p.timeout_ticks)) {
@@ -353,8 +361,11 @@ enum Evt : int {
   EV_QKV_STORED, EV_GU_STORED, EV_DN_STORED, EV_DN_READY,
   EV_ATT_REDUCED, EV_ATT_COMBINED, EV_MERGE_SCALED, EV_MERGE_DONE
 };
+#ifndef MK_TRACE_EVENTS
+#define MK_TRACE_EVENTS 0  // fine-grained events of one layer (investigation builds only)
+#endif
 __device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
-  if (tracing(p, t) && layer == p.trace_layer && ltid() == 0)
+  if (MK_TRACE_EVENTS && tracing(p, t) && layer == p.trace_layer && ltid() == 0)
     trace_lds[(5 * p.n_layers + 1) * 2 + e] = wall_clock64();
 }
 
@@ -882,27 +893,32 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, int nsplit, unsigned
     const bool want_x = s0 == 0 && xrows && tid < 16;
     Spin sp;
     while (true) {
-      bool ready = true;
+      // every load is issued before any is tested (one round trip per poll
+      // round): the split condition is uniform over the workgroup, pairs past
+      // QD/2 re-read pair 0, and every thread reads a residual word
 #pragma unroll
       for (int k = 0; k < PPT; ++k) {
-        const int pi = tid + k * NT;
+        const int pi = tid + k * NT < S::QD / 2 ? tid + k * NT : 0;
         const int g = pi / NPG, pg = pi % NPG, j = (2 * pg) / S::D;
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
-          wa[k][u] = 0ull;
-          wm[k][u] = 0ull;
-          if (pi < S::QD / 2 && s0 + u < nsplit) {
+          wa[k][u] = wm[k][u] = 0ull;
+          if (s0 + u < nsplit) {
             u64* src = p.part + ((long long)(s0 + u) * S::NKV + g) * WP;
             wa[k][u] = ll_get(src + pg);
             wm[k][u] = ll_get(src + NPG + j);
-            ready &= pk_ready(wa[k][u], t4) && pk_ready(wm[k][u], t4);
           }
         }
       }
-      if (want_x) {
-        wx = ll_get(xrows + tid);
-        ready &= ll_tag(wx) == xtag;
-      }
+      wx = ll_get(xrows ? xrows + (tid & 15) : p.part);
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < PPT; ++k)
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+          ready &= tid + k * NT >= S::QD / 2 || s0 + u >= nsplit ||
+                   (pk_ready(wa[k][u], t4) && pk_ready(wm[k][u], t4));
+      ready &= !want_x || ll_tag(wx) == xtag;
       if (ready) break;
       if (!sp.step(p.err, p.timeout_ticks)) {
         failed = 1;
@@ -1210,7 +1226,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           u32x4 wv[U];
 #pragma unroll
           for (int u = 0; u < U; ++u)
-            if (k0 + u < S::KT_H) wv[u] = buf_ld_nt(rs, lo * 16u, (unsigned)(k0 + u) * 1024u);
+            if (k0 + u < S::KT_H) wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lo * 16u, (unsigned)(k0 + u) * 1024u, MK_LMHEAD_AUX);
 #pragma unroll
           for (int u = 0; u < U; ++u)
             if (k0 + u < S::KT_H) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
