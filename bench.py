@@ -47,6 +47,11 @@ def parse():
                     help="only run 5 plain device copies of 1 GiB (known bytes) for scaling rocprof counters")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                     help="measured HBM bytes per launch (rocprofv3 --pmc), if present")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="BASELINE configs[4] instead: this many independent sequences (<= 16), KV lengths "
+                         "uniform in [--kv-min, --kv-max] from --seed, --steps greedy steps each")
+    ap.add_argument("--kv-min", type=int, default=512)
+    ap.add_argument("--kv-max", type=int, default=4096)
     return ap.parse_args()
 
 
@@ -158,10 +163,74 @@ def calibrate_copy():
     print(json.dumps({"copy_bytes": n * 4, "copies": 5}))
 
 
+def bench_batch(args):
+    """n independent sequences, per-sequence KV lengths
+    uniform in [kv_min, kv_max] from the seed (synthetic N(0, 1) prefill), K
+    greedy steps of all sequences, each step one replay of the step graph.
+    Timed: one megakernel_generate_batch call of K steps (HIP events around the
+    replays; inputs resident in HBM).  Algorithmic bytes of a step: the weights
+    once plus, per sequence, its KV read (positions 0..pos) and append."""
+    import numpy as np
+
+    from megakernel_amd import launcher
+    from megakernel_amd.batch import BatchEngine
+    from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
+    from megakernel_amd.weights import DeviceWeights
+
+    shape, B, K, W = BASELINE, args.batch, args.steps, args.warmup
+    rng = np.random.default_rng(args.seed)
+    lengths = [int(x) for x in rng.integers(args.kv_min, args.kv_max + 1, size=B)]
+    dw = DeviceWeights(shape, args.seed, std=0.02, gain_std=0.0)
+    eng = BatchEngine(dw, B, args.kv_max + max(K, W) + 8, shape)
+    info = launcher.detect_gpu()
+    first = [int(t) for t in rng.integers(0, shape.vocab, size=B)]
+
+    def prefill():
+        for b, n in enumerate(lengths):
+            eng.fill_kv_synthetic(b, n, args.seed + 1000 + b)
+
+    prefill()
+    eng.generate(first, max(W, 1))  # warm-up (also builds the step graph)
+    walls, kernels = [], []
+    for r in range(args.reps):
+        prefill()
+        eng.lib.megakernel_sync()
+        t0 = time.perf_counter()
+        toks = eng.generate(first, K)
+        walls.append(time.perf_counter() - t0)
+        kernels.append(eng.last_ms / 1e3)
+        print(f"# rep {r}: wall {walls[-1] * 1e3:.2f} ms device {kernels[-1] * 1e3:.2f} ms -> "
+              f"{B * K / walls[-1]:.1f} tok/s; last tokens {toks[-1][:4].tolist()}", file=sys.stderr, flush=True)
+    wall, kern = statistics.median(walls), statistics.median(kernels)
+    nbytes = sum(shape.weight_bytes + sum(shape.kv_bytes_per_pos * (n + i + 2) for n in lengths) for i in range(K))
+    achieved = nbytes / kern / 1e9
+    eng.close()
+    dw.free()
+    out = {
+        "metric": f"batched greedy decode tok/s ({B} sequences, KV {args.kv_min}-{args.kv_max})",
+        "value": round(B * K / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"Qwen3-0.6B-shaped batched decode, {B} sequences, KV lengths {lengths}, "
+                               f"{K} steps (BASELINE configs[4])", "sequences": B, "kv_lengths": lengths,
+                   "device": info["name"], "reps": args.reps},
+        "steps_per_s": round(K / wall, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.batch:
+        if args.gpus != 1:
+            print(json.dumps({"error": "this build runs on one GPU only"}))
+            sys.exit(2)
+        bench_batch(args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the batch-1 decode path does not "

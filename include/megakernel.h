@@ -151,6 +151,50 @@ int megakernel_memcpy(void* dst, const void* src, unsigned long long nbytes, int
 /* CU count, wall-clock rate (kHz) and "name (gcnArch)" of the current device. */
 int megakernel_device_info(int* cus, int* wall_clock_khz, char* name, int name_len);
 
+/* ---- batched decode ------------------------------
+ * SURVEY's boundary lists megakernel_decode_batch as the additive entry point
+ * of the 16-sequence configuration; the reference has no batched path (its
+ * engine decodes one sequence, src/megakernel.cu:377-413).  A batch handle
+ * holds its own weight copy (matrix-core tile layout) and n_seq KV caches;
+ * every call advances all n_seq sequences by one greedy step per step.
+ * Presets: MK_PRESET_BASELINE and MK_PRESET_TINY. */
+
+/* Create a batch handle for n_seq (1..16) sequences of KV capacity max_seq
+ * from the flat device weight buffer (same arguments as megakernel_init_ex).
+ * All positions start at 0.  Returns NULL on failure. */
+void* megakernel_batch_init(void* d_weights, const long long* offsets, int num_offsets, int preset, int vocab,
+                            int n_seq, int max_seq);
+void megakernel_batch_free(void* handle);
+
+/* Position (number of cached positions) of sequence seq / of all sequences
+ * (pos: host int[n_seq]). */
+int megakernel_batch_set_pos(void* handle, int seq, int pos);
+int megakernel_batch_get_pos(void* handle, int* pos);
+
+/* KV prefix of one sequence: synthetic fill (the megakernel_fill_kv_synthetic
+ * stream) or a host copy in the megakernel_set_kv layout; both set the
+ * sequence's position to len. */
+int megakernel_batch_fill_kv_synthetic(void* handle, int seq, int len, unsigned long long seed, float std);
+int megakernel_batch_set_kv(void* handle, int seq, const void* host_kv, int len);
+int megakernel_batch_get_kv(void* handle, int seq, void* host_kv, int len);
+
+/* One greedy step of every sequence: tokens_in[b] is consumed at sequence b's
+ * position, tokens_out[b] (may be NULL) receives its argmax next token
+ * (lowest index on ties); positions advance by one.  Returns 0 or -1. */
+int megakernel_decode_batch(void* handle, const int* tokens_in, int* tokens_out);
+
+/* n_steps greedy steps of every sequence (one graph replay per step, no host
+ * round trip in between): tokens_out[i * n_seq + b] receives step i's token
+ * of sequence b. */
+int megakernel_generate_batch(void* handle, const int* first_tokens, int n_steps, int* tokens_out);
+
+/* megakernel_decode_batch that also returns the fp32 logits
+ * (logits: host float[n_seq * vocab]).  Validation only. */
+int megakernel_batch_debug_logits(void* handle, const int* tokens_in, int* tokens_out, float* logits);
+
+/* Device time of the last megakernel_generate_batch / decode_batch call (ms). */
+float megakernel_batch_last_ms(void* handle);
+
 #ifdef __cplusplus
 }
 #endif

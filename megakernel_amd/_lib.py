@@ -49,6 +49,18 @@ SIGNATURES = {
     "megakernel_device_free": (None, [c_void_p]),
     "megakernel_memcpy": (c_int, [c_void_p, c_void_p, c_ull, c_int]),
     "megakernel_device_info": (c_int, [P_int, P_int, c_char_p, c_int]),
+    # batched decode
+    "megakernel_batch_init": (c_void_p, [c_void_p, P_ll, c_int, c_int, c_int, c_int, c_int]),
+    "megakernel_batch_free": (None, [c_void_p]),
+    "megakernel_batch_set_pos": (c_int, [c_void_p, c_int, c_int]),
+    "megakernel_batch_get_pos": (c_int, [c_void_p, P_int]),
+    "megakernel_batch_fill_kv_synthetic": (c_int, [c_void_p, c_int, c_int, c_ull, c_float]),
+    "megakernel_batch_set_kv": (c_int, [c_void_p, c_int, c_void_p, c_int]),
+    "megakernel_batch_get_kv": (c_int, [c_void_p, c_int, c_void_p, c_int]),
+    "megakernel_decode_batch": (c_int, [c_void_p, P_int, P_int]),
+    "megakernel_generate_batch": (c_int, [c_void_p, P_int, c_int, P_int]),
+    "megakernel_batch_debug_logits": (c_int, [c_void_p, P_int, P_int, P_float]),
+    "megakernel_batch_last_ms": (c_float, [c_void_p]),
 }
 
 PRESET_BASELINE, PRESET_QWEN3_06B, PRESET_TINY = 0, 1, 2

@@ -1,0 +1,100 @@
+"""Batched greedy decode of up to 16 independent sequences
+over the library's batch handle (``megakernel_batch_*``, ``megakernel_decode_batch``).
+
+The reference decodes one sequence per engine (/root/reference/host/bridge.py:70-261);
+``BatchEngine`` is the additive counterpart for several sequences sharing one
+weight stream: every step consumes one token per sequence at that sequence's
+own position and returns one greedy token per sequence.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from .config import BASELINE, ModelShape
+
+
+class BatchEngine:
+    def __init__(self, device_weights, n_seq: int, max_seq: int, shape: ModelShape = BASELINE,
+                 lib_path: str | None = None):
+        self.shape = shape
+        self.n_seq = n_seq
+        self.max_seq = max_seq
+        self.lib = _lib.load(lib_path)
+        arr = device_weights.layout.c_offsets()
+        self._handle = self.lib.megakernel_batch_init(
+            ctypes.c_void_p(device_weights.ptr), arr, len(arr), shape.preset, shape.vocab, n_seq, max_seq)
+        if not self._handle:
+            raise _lib.MegakernelError(f"megakernel_batch_init failed: {_lib.last_error(self.lib)}")
+
+    def _ints(self, vals) -> ctypes.Array:
+        vals = [int(v) for v in vals]
+        if len(vals) != self.n_seq:
+            raise ValueError(f"expected {self.n_seq} values, got {len(vals)}")
+        return (ctypes.c_int * self.n_seq)(*vals)
+
+    # ------------------------------------------------------------ state
+    def positions(self) -> list[int]:
+        out = (ctypes.c_int * self.n_seq)()
+        _lib.check(self.lib, self.lib.megakernel_batch_get_pos(self._handle, out), "batch_get_pos")
+        return list(out)
+
+    def set_pos(self, seq: int, pos: int):
+        _lib.check(self.lib, self.lib.megakernel_batch_set_pos(self._handle, seq, pos), "batch_set_pos")
+
+    def fill_kv_synthetic(self, seq: int, length: int, seed: int, std: float = 1.0):
+        _lib.check(self.lib, self.lib.megakernel_batch_fill_kv_synthetic(self._handle, seq, length, seed, std),
+                   "batch_fill_kv_synthetic")
+
+    def set_kv(self, seq: int, kv_bits: np.ndarray):
+        """kv_bits: uint16 [L][2][NKV][len][D] (bf16 bits), the single-sequence set_kv layout."""
+        kv_bits = np.ascontiguousarray(kv_bits, dtype=np.uint16)
+        _lib.check(self.lib, self.lib.megakernel_batch_set_kv(
+            self._handle, seq, kv_bits.ctypes.data_as(ctypes.c_void_p), kv_bits.shape[3]), "batch_set_kv")
+
+    def get_kv(self, seq: int, length: int) -> np.ndarray:
+        s = self.shape
+        out = np.empty((s.n_layers, 2, s.n_kv_heads, length, s.head_dim), dtype=np.uint16)
+        _lib.check(self.lib, self.lib.megakernel_batch_get_kv(
+            self._handle, seq, out.ctypes.data_as(ctypes.c_void_p), length), "batch_get_kv")
+        return out
+
+    # ------------------------------------------------------------ decode
+    def decode(self, tokens) -> list[int]:
+        """One greedy step of every sequence."""
+        out = (ctypes.c_int * self.n_seq)()
+        _lib.check(self.lib, self.lib.megakernel_decode_batch(self._handle, self._ints(tokens), out),
+                   "decode_batch")
+        return list(out)
+
+    def generate(self, first_tokens, n_steps: int) -> np.ndarray:
+        """n_steps greedy steps; returns int32 [n_steps][n_seq]."""
+        out = (ctypes.c_int * (n_steps * self.n_seq))()
+        _lib.check(self.lib, self.lib.megakernel_generate_batch(self._handle, self._ints(first_tokens), n_steps, out),
+                   "generate_batch")
+        return np.frombuffer(out, dtype=np.int32).reshape(n_steps, self.n_seq).copy()
+
+    def debug_logits(self, tokens):
+        """One step returning (next tokens, fp32 logits [n_seq][vocab])."""
+        out = (ctypes.c_int * self.n_seq)()
+        logits = np.empty((self.n_seq, self.shape.vocab), dtype=np.float32)
+        _lib.check(self.lib, self.lib.megakernel_batch_debug_logits(
+            self._handle, self._ints(tokens), out, logits.ctypes.data_as(_lib.P_float)), "batch_debug_logits")
+        return list(out), logits
+
+    @property
+    def last_ms(self) -> float:
+        return float(self.lib.megakernel_batch_last_ms(self._handle))
+
+    def close(self):
+        if getattr(self, "_handle", None):
+            self.lib.megakernel_batch_free(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,419 @@
+// Batched-decode handle of megakernel.so (16 independent
+// sequences, per-sequence KV lengths, greedy decode).  Additive extension of
+// the reference ABI; the kernels are in mk_batch.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "mk_batch.h"
+#include "mk_config.h"
+#include "mk_host.h"
+
+#include "../../include/megakernel.h"
+
+namespace mk {
+namespace batch {
+
+struct BHandle {
+  int device = 0, preset = 0, B = 0, L = 0, V = 0, S = 0, s_pad = 0, nsplit_max = 0, max_steps = 0;
+  int H = 0, QD = 0, KVD = 0, QKV = 0, F = 0, D = 0, NKV = 0, norm_stride = 0, G = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  float last_ms = 0.f;
+  BParams p{};
+  std::vector<void*> owned;
+  int (*launch_step)(BHandle*, const BParams&) = nullptr;
+};
+
+static void free_all(BHandle* h) {
+  if (h->exec) (void)hipGraphExecDestroy(h->exec);
+  if (h->graph) (void)hipGraphDestroy(h->graph);
+  for (void* q : h->owned) (void)hipFree(q);
+  if (h->ev0) (void)hipEventDestroy(h->ev0);
+  if (h->ev1) (void)hipEventDestroy(h->ev1);
+  if (h->stream) (void)hipStreamDestroy(h->stream);
+}
+
+template <class T>
+static int alloc(BHandle* h, T** ptr, size_t bytes, bool zero = true) {
+  void* q = nullptr;
+  HIPCHK(hipMalloc(&q, bytes), -1);
+  h->owned.push_back(q);
+  if (zero) HIPCHK(hipMemsetAsync(q, 0, bytes, h->stream), -1);
+  *ptr = static_cast<T*>(q);
+  return 0;
+}
+
+// Row-major bf16 W[R][K] (at base + off) -> tile layout, blocks rb -> rb.
+static int repack_tiles(BHandle* h, const char* base, long long off, int R, int K, u32x4* dst) {
+  if (off < 0 || (off & 15)) {
+    set_err("weight offset %lld is negative or not 16-byte aligned", off);
+    return -1;
+  }
+  const long long units = (long long)R * K / 8;
+  const int threads = 256;
+  const int blocks = (int)((units + threads - 1) / threads < 65536 ? (units + threads - 1) / threads : 65536);
+  hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, h->stream,
+                     reinterpret_cast<const u32x4*>(base + off), R, K, dst, 1, 0, 0);
+  HIPCHK(hipGetLastError(), -1);
+  return 0;
+}
+
+// One decode step of every sequence: the kernels of mk_batch.h in order.
+template <class S>
+static int launch_step(BHandle* h, const BParams& p) {
+  const int L = h->L;
+  hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
+  for (int l = 0; l < L; ++l) {
+    hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_attn<S>, dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16), dim3(GT), 0, h->stream, p, l);
+  }
+  hipLaunchKernelGGL(bk_lm<S>, dim3(h->G), dim3(GT), 0, h->stream, p);
+  hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
+  HIPCHK(hipGetLastError(), -1);
+  return 0;
+}
+
+template <class S>
+static void set_shape(BHandle* h) {
+  h->H = S::H, h->QD = S::QD, h->KVD = S::KVD, h->QKV = S::QKV, h->F = S::F, h->D = S::D, h->NKV = S::NKV;
+  h->norm_stride = S::NORM_STRIDE;
+  h->launch_step = launch_step<S>;
+}
+
+static int init_state(BHandle* h, const char* base, const long long* off, int n_off) {
+  if (n_off < 13 || (n_off - 2) % 11 != 0) {
+    set_err("num_offsets=%d is not 2 + 11*layers", n_off);
+    return -1;
+  }
+  h->L = (n_off - 2) / 11;
+  if (h->V <= 0 || h->V % 16) {
+    set_err("vocab %d must be a positive multiple of 16", h->V);
+    return -1;
+  }
+  HIPCHK(hipGetDevice(&h->device), -1);
+  HIPCHK(hipDeviceGetAttribute(&h->G, hipDeviceAttributeMultiprocessorCount, h->device), -1);
+  HIPCHK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), -1);
+  HIPCHK(hipEventCreate(&h->ev0), -1);
+  HIPCHK(hipEventCreate(&h->ev1), -1);
+  BParams& p = h->p;
+  const int L = h->L;
+  p.u_qkv = (long long)h->QKV * h->H / 8;
+  p.u_o = (long long)h->H * h->QD / 8;
+  p.u_gu = (long long)h->F * h->H / 8;
+  p.u_dn = (long long)h->H * h->F / 8;
+  u32x4 *wqkv, *wo, *wg, *wu, *wd, *lm;
+  if (alloc(h, &wqkv, p.u_qkv * 16 * L, false) || alloc(h, &wo, p.u_o * 16 * L, false) ||
+      alloc(h, &wg, p.u_gu * 16 * L, false) || alloc(h, &wu, p.u_gu * 16 * L, false) ||
+      alloc(h, &wd, p.u_dn * 16 * L, false) || alloc(h, &lm, (size_t)h->V * h->H * 2, false))
+    return -1;
+  uint16_t *norms, *fnorm;
+  if (alloc(h, &norms, (size_t)h->norm_stride * 2 * L) || alloc(h, &fnorm, (size_t)h->H * 2)) return -1;
+  // weights: tile layout for every matrix (offset order: reference megakernel.cu:518-532)
+  if (repack_tiles(h, base, off[0], h->V, h->H, lm)) return -1;
+  HIPCHK(hipMemcpyAsync(fnorm, base + off[1], (size_t)h->H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+  const int NORM_ATTN = 0, NORM_Q = h->H, NORM_K = h->H + h->D, NORM_FFN = h->H + 2 * h->D;
+  for (int i = 0; i < L; ++i) {
+    const long long* o = off + 2 + 11 * i;
+    uint16_t* nl = norms + (long long)i * h->norm_stride;
+    HIPCHK(hipMemcpyAsync(nl + NORM_ATTN, base + o[0], (size_t)h->H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    HIPCHK(hipMemcpyAsync(nl + NORM_Q, base + o[4], (size_t)h->D * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    HIPCHK(hipMemcpyAsync(nl + NORM_K, base + o[5], (size_t)h->D * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    HIPCHK(hipMemcpyAsync(nl + NORM_FFN, base + o[7], (size_t)h->H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
+    u32x4* q = wqkv + i * p.u_qkv;
+    if (repack_tiles(h, base, o[1], h->QD, h->H, q) ||
+        repack_tiles(h, base, o[2], h->KVD, h->H, q + (long long)h->QD * h->H / 8) ||
+        repack_tiles(h, base, o[3], h->KVD, h->H, q + (long long)(h->QD + h->KVD) * h->H / 8) ||
+        repack_tiles(h, base, o[6], h->H, h->QD, wo + i * p.u_o) ||
+        repack_tiles(h, base, o[8], h->F, h->H, wg + i * p.u_gu) ||
+        repack_tiles(h, base, o[9], h->F, h->H, wu + i * p.u_gu) ||
+        repack_tiles(h, base, o[10], h->H, h->F, wd + i * p.u_dn))
+      return -1;
+  }
+  p.wqkv = wqkv, p.wo = wo, p.wg = wg, p.wu = wu, p.wd = wd, p.lmhead = lm;
+  p.norms = norms, p.final_norm = fnorm;
+  // KV caches: K then V^T regions, one slice per sequence
+  h->s_pad = (h->S + 31) / 32 * 32;
+  p.s_pad = h->s_pad;
+  p.kv_seq = (long long)L * h->NKV * h->s_pad * h->D;
+  uint16_t* kv;
+  if (alloc(h, &kv, (size_t)2 * BMAX * p.kv_seq * 2)) return -1;
+  p.kv = kv;
+  p.kvt = kv + (long long)BMAX * p.kv_seq;
+  h->nsplit_max = (h->S + CH - 1) / CH;
+  p.nsplit_max = h->nsplit_max;
+  h->max_steps = 1 << 16;
+  p.max_steps = h->max_steps;
+  if (alloc(h, &p.x, (size_t)BMAX * h->H * 4) || alloc(h, &p.qkv, (size_t)BMAX * h->QKV * 4) ||
+      alloc(h, &p.att, (size_t)2 * BMAX * h->QD * 2) || alloc(h, &p.act, (size_t)2 * BMAX * h->F * 2) ||
+      alloc(h, &p.part, (size_t)BMAX * h->NKV * h->nsplit_max * PW * 4) ||
+      alloc(h, &p.cnt, (size_t)BMAX * h->NKV * 4) || alloc(h, &p.keys, (size_t)BMAX * 8) ||
+      alloc(h, &p.tok, (size_t)BMAX * 4) || alloc(h, &p.pos, (size_t)BMAX * 4) ||
+      alloc(h, &p.out, (size_t)h->max_steps * BMAX * 4) || alloc(h, &p.step, 64) ||
+      alloc(h, &p.dbg_logits, (size_t)BMAX * h->V * 4))
+    return -1;
+  std::vector<float> invf(h->D / 2);
+  for (int i = 0; i < h->D / 2; ++i) invf[i] = 1.0f / powf((float)kRopeTheta, (float)(2 * i) / (float)h->D);
+  float* inv;
+  if (alloc(h, &inv, invf.size() * 4, false)) return -1;
+  HIPCHK(hipMemcpyAsync(inv, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, h->stream), -1);
+  p.inv_freq = inv;
+  p.B = h->B, p.L = L, p.V = h->V;
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  return 0;
+}
+
+static BHandle* create(int preset, int vocab, int n_seq, int max_seq) {
+  if (n_seq < 1 || n_seq > BMAX) {
+    set_err("n_seq %d outside [1, %d]", n_seq, BMAX);
+    return nullptr;
+  }
+  if (max_seq < 1) {
+    set_err("max_seq must be positive");
+    return nullptr;
+  }
+  BHandle* h = new (std::nothrow) BHandle();
+  if (!h) {
+    set_err("out of host memory");
+    return nullptr;
+  }
+  h->preset = preset, h->V = vocab, h->B = n_seq, h->S = max_seq;
+  switch (preset) {
+    case PRESET_BASELINE: set_shape<ShapeBaseline>(h); break;
+    case PRESET_TINY: set_shape<ShapeTiny>(h); break;
+    default:
+      set_err("batched decode supports the BASELINE and TINY presets (head_dim 64, 2 q heads per kv head)");
+      delete h;
+      return nullptr;
+  }
+  return h;
+}
+
+static int check_positions(BHandle* h, int steps) {
+  std::vector<int> pos(BMAX);
+  HIPCHK(hipMemcpy(pos.data(), h->p.pos, BMAX * 4, hipMemcpyDeviceToHost), -1);
+  for (int b = 0; b < h->B; ++b)
+    if (pos[b] + steps > h->S) {
+      set_err("sequence %d: position %d + %d steps exceeds KV capacity %d", b, pos[b], steps, h->S);
+      return -1;
+    }
+  return 0;
+}
+
+static int set_tokens(BHandle* h, const int* tokens) {
+  std::vector<int> t(BMAX, 0);
+  for (int b = 0; b < h->B; ++b) {
+    if (tokens[b] < 0 || tokens[b] >= h->V) {
+      set_err("sequence %d: token id %d outside [0, %d)", b, tokens[b], h->V);
+      return -1;
+    }
+    t[b] = tokens[b];
+  }
+  HIPCHK(hipMemcpyAsync(h->p.tok, t.data(), BMAX * 4, hipMemcpyHostToDevice, h->stream), -1);
+  HIPCHK(hipMemsetAsync(h->p.step, 0, 4, h->stream), -1);
+  return 0;
+}
+
+// The step graph: the same kernels with the same arguments every step (the
+// step's inputs live in device memory), captured once.
+static int ensure_graph(BHandle* h) {
+  if (h->exec) return 0;
+  BParams p = h->p;
+  p.dbg_logits = nullptr;
+  HIPCHK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), -1);
+  const int rc = h->launch_step(h, p);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(h->stream, &g);
+  if (rc || e != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    if (!rc) set_err("graph capture failed: %s", hipGetErrorString(e));
+    return -1;
+  }
+  h->graph = g;
+  HIPCHK(hipGraphInstantiate(&h->exec, g, nullptr, nullptr, 0), -1);
+  return 0;
+}
+
+static int run_steps(BHandle* h, const int* first, int n, int* out) {
+  if (n <= 0 || n > h->max_steps) {
+    set_err("step count %d outside [1, %d]", n, h->max_steps);
+    return -1;
+  }
+  if (check_positions(h, n) || set_tokens(h, first) || ensure_graph(h)) return -1;
+  HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
+  for (int i = 0; i < n; ++i) HIPCHK(hipGraphLaunch(h->exec, h->stream), -1);
+  HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  HIPCHK(hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1), -1);
+  if (out) {
+    std::vector<int> all((size_t)n * BMAX);
+    HIPCHK(hipMemcpy(all.data(), h->p.out, all.size() * 4, hipMemcpyDeviceToHost), -1);
+    for (int i = 0; i < n; ++i)
+      for (int b = 0; b < h->B; ++b) out[(size_t)i * h->B + b] = all[(size_t)i * BMAX + b];
+  }
+  return 0;
+}
+
+}  // namespace batch
+}  // namespace mk
+
+using mk::batch::BHandle;
+
+extern "C" {
+
+void* megakernel_batch_init(void* d_weights, const long long* offsets, int num_offsets, int preset, int vocab,
+                            int n_seq, int max_seq) {
+  if (!d_weights || !offsets) {
+    mk::set_err("null weights or offsets");
+    return nullptr;
+  }
+  BHandle* h = mk::batch::create(preset, vocab, n_seq, max_seq);
+  if (!h) return nullptr;
+  if (mk::batch::init_state(h, static_cast<const char*>(d_weights), offsets, num_offsets)) {
+    mk::batch::free_all(h);
+    delete h;
+    return nullptr;
+  }
+  return h;
+}
+
+void megakernel_batch_free(void* handle) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h) return;
+  (void)hipStreamSynchronize(h->stream);
+  mk::batch::free_all(h);
+  delete h;
+}
+
+int megakernel_batch_set_pos(void* handle, int seq, int pos) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || seq < 0 || seq >= h->B || pos < 0 || pos > h->S) {
+    mk::set_err("invalid handle, sequence %d or position %d", seq, pos);
+    return -1;
+  }
+  HIPCHK(hipMemcpy(h->p.pos + seq, &pos, 4, hipMemcpyHostToDevice), -1);
+  return 0;
+}
+
+int megakernel_batch_get_pos(void* handle, int* pos) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !pos) {
+    mk::set_err("invalid arguments");
+    return -1;
+  }
+  HIPCHK(hipMemcpy(pos, h->p.pos, (size_t)h->B * 4, hipMemcpyDeviceToHost), -1);
+  return 0;
+}
+
+int megakernel_batch_fill_kv_synthetic(void* handle, int seq, int len, unsigned long long seed, float std) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || seq < 0 || seq >= h->B || len < 0 || len > h->S) {
+    mk::set_err("invalid fill arguments (sequence %d, len %d)", seq, len);
+    return -1;
+  }
+  if (len > 0) {
+    const float c = (float)(std * sqrt(3.0) / 65536.0);
+    hipLaunchKernelGGL(mk::synth_kv_kernel, dim3(4096), dim3(256), 0, h->stream, h->p.kv + seq * h->p.kv_seq,
+                       h->p.kvt + seq * h->p.kv_seq, h->L, h->NKV, h->s_pad, h->D, len, seed, c);
+    HIPCHK(hipGetLastError(), -1);
+    HIPCHK(hipStreamSynchronize(h->stream), -1);
+  }
+  return megakernel_batch_set_pos(handle, seq, len);
+}
+
+static int batch_kv_transfer(BHandle* h, int seq, void* host_kv, int len, int to_cache) {
+  const size_t bytes = (size_t)2 * h->L * h->NKV * (size_t)len * h->D * 2;
+  void* stage = nullptr;
+  HIPCHK(hipMalloc(&stage, bytes), -1);
+  int rc = -1;
+  do {
+    if (to_cache && hipMemcpy(stage, host_kv, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+      mk::set_err("KV upload failed");
+      break;
+    }
+    hipLaunchKernelGGL(mk::kv_convert_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                       h->p.kv + seq * h->p.kv_seq, h->p.kvt + seq * h->p.kv_seq, h->L, h->NKV, h->s_pad, h->D, len,
+                       to_cache);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(h->stream) != hipSuccess) {
+      mk::set_err("KV layout conversion failed");
+      break;
+    }
+    if (!to_cache && hipMemcpy(host_kv, stage, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+      mk::set_err("KV download failed");
+      break;
+    }
+    rc = 0;
+  } while (0);
+  (void)hipFree(stage);
+  return rc;
+}
+
+int megakernel_batch_set_kv(void* handle, int seq, const void* host_kv, int len) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !host_kv || seq < 0 || seq >= h->B || len < 0 || len > h->S) {
+    mk::set_err("invalid set_kv arguments (sequence %d, len %d)", seq, len);
+    return -1;
+  }
+  if (len > 0 && batch_kv_transfer(h, seq, const_cast<void*>(host_kv), len, 1)) return -1;
+  return megakernel_batch_set_pos(handle, seq, len);
+}
+
+int megakernel_batch_get_kv(void* handle, int seq, void* host_kv, int len) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !host_kv || seq < 0 || seq >= h->B || len < 0 || len > h->S) {
+    mk::set_err("invalid get_kv arguments (sequence %d, len %d)", seq, len);
+    return -1;
+  }
+  return len > 0 ? batch_kv_transfer(h, seq, host_kv, len, 0) : 0;
+}
+
+int megakernel_decode_batch(void* handle, const int* tokens_in, int* tokens_out) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !tokens_in) {
+    mk::set_err("null handle or tokens");
+    return -1;
+  }
+  return mk::batch::run_steps(h, tokens_in, 1, tokens_out);
+}
+
+int megakernel_generate_batch(void* handle, const int* first_tokens, int n_steps, int* tokens_out) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !first_tokens) {
+    mk::set_err("null handle or tokens");
+    return -1;
+  }
+  return mk::batch::run_steps(h, first_tokens, n_steps, tokens_out);
+}
+
+int megakernel_batch_debug_logits(void* handle, const int* tokens_in, int* tokens_out, float* logits) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !tokens_in || !logits) {
+    mk::set_err("null handle, tokens or logits");
+    return -1;
+  }
+  if (mk::batch::check_positions(h, 1) || mk::batch::set_tokens(h, tokens_in)) return -1;
+  if (h->launch_step(h, h->p)) return -1;  // eager launches, logits written
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  HIPCHK(hipMemcpy(logits, h->p.dbg_logits, (size_t)h->B * h->V * 4, hipMemcpyDeviceToHost), -1);
+  if (tokens_out) {
+    std::vector<int> t(mk::batch::BMAX);
+    HIPCHK(hipMemcpy(t.data(), h->p.out, mk::batch::BMAX * 4, hipMemcpyDeviceToHost), -1);
+    for (int b = 0; b < h->B; ++b) tokens_out[b] = t[b];
+  }
+  return 0;
+}
+
+float megakernel_batch_last_ms(void* handle) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  return h ? h->last_ms : -1.f;
+}
+
+}  // extern "C"

@@ -13,6 +13,7 @@
 
 #include "mk_config.h"
 #include "mk_device.h"
+#include "mk_host.h"
 #include "mk_kernel.h"
 
 #include "../../include/megakernel.h"
@@ -20,23 +21,14 @@
 namespace mk {
 
 // ------------------------------------------------------------ error state
-static thread_local char g_err[512] = "";
+thread_local char g_err[512] = "";
 
-static void set_err(const char* fmt, ...) {
+void set_err(const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
 }
-
-#define HIPCHK(expr, ret)                                                                  \
-  do {                                                                                     \
-    hipError_t e_ = (expr);                                                                \
-    if (e_ != hipSuccess) {                                                                \
-      ::mk::set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
-      return ret;                                                                          \
-    }                                                                                      \
-  } while (0)
 
 // --------------------------------------------------------- device helpers
 // Repack a row-major bf16 matrix W[R][K] into one of the packed layouts of
@@ -73,14 +65,6 @@ __global__ void synth_fill_kernel(uint16_t* __restrict__ dst, unsigned long long
     dst[i] = synth_bf16(key, i, c, add_one);
 }
 
-// Device KV cache addressing (see mk_kernel.h): K [L][NKV][s_pad][D], V^T
-// blocks [L][NKV][s_pad/32][D][32], both bf16; kv points at K, kvt at V^T.
-__device__ __forceinline__ long long k_index(int l, int g, long long t, int d, int NKV, int s_pad, int D) {
-  return (((long long)l * NKV + g) * s_pad + t) * D + d;
-}
-__device__ __forceinline__ long long vt_index(int l, int g, long long t, int d, int NKV, int s_pad, int D) {
-  return ((long long)l * NKV + g) * (long long)s_pad * D + (t / 32) * 32LL * D + (long long)d * 32 + (t % 32);
-}
 
 // Synthetic KV prefill of positions [0, len).  Stream id KV_ID_BASE +
 // 2*layer + kv; element index (t * NKV + g) * D + d (matches

@@ -1,0 +1,525 @@
+// Batched greedy decode of up to 16 independent sequences.
+//
+// One decode step of all sequences is a fixed sequence of kernels, captured
+// once into a HIP graph and replayed per step:
+//   embed                 x[b] = E[tok[b]]
+//   per layer:  qkv       rmsnorm(x) -> fused QKV GEMM           (16-row blocks)
+//               attn      QK-norm + RoPE + KV append + split attention; the last
+//                         split of each (sequence, kv head) merges the partials
+//               o         O GEMM + residual                       (16-row blocks)
+//               gu        rmsnorm(x) -> gate/up GEMM -> SiLU(g) * u
+//               down      down GEMM + residual
+//   lm                    final rmsnorm -> tied LM head GEMM -> per-sequence argmax
+//   tok                   argmax keys -> tokens, positions + 1
+// (reference phase order /root/reference/src/megakernel.cu:132-332, per sequence).
+//
+// With 16 sequences every weight block is used 16 times, so the GEMMs run on
+// the matrix cores: v_mfma_f32_16x16x32_bf16 with the weight tile as the A
+// operand (the tile layout of mk_config.h) and the 16 sequences' activations
+// as the B operand (column n = sequence n).  Activations are fp32 and enter
+// the products as two bf16 parts (hi = RNE(v), lo = RNE(v - hi); relative
+// error <= 2^-17), two products per tile.  Kernel boundaries order every
+// hand-off, so activations are ordinary cached loads and stores; only the
+// attention merge hands partials between workgroups of one launch (write-through
+// stores, an agent-scope counter, agent-scope loads).
+#pragma once
+#include "mk_config.h"
+#include "mk_device.h"
+#include "mk_host.h"
+
+namespace mk {
+namespace batch {
+
+constexpr int BMAX = 16;       // sequences per step (MFMA columns)
+constexpr int GT = 512;        // threads of the GEMM kernels (8 waves)
+constexpr int GW = GT / kWave;
+constexpr int AT = 256;        // threads of an attention item (4 waves)
+constexpr int AW = AT / kWave;
+constexpr int CH = 32 * AW;    // positions per attention split (one 32-position block per wave)
+constexpr int PW = 2 * 64 + 4; // partial words per item for GQA 2, D 64: o[2][64], (m, l) x 2
+
+struct BParams {
+  const u32x4* wqkv;        // per layer [QKV/16][H/32] tiles
+  const u32x4* wo;          // per layer [H/16][QD/32]
+  const u32x4* wg;          // per layer gate [F/16][H/32]
+  const u32x4* wu;          // per layer up
+  const u32x4* wd;          // per layer down [H/16][F/32]
+  const u32x4* lmhead;      // [V/16][H/32]
+  long long u_qkv, u_o, u_gu, u_dn;  // 16-byte units per layer of each matrix
+  const uint16_t* norms;    // [L][NORM_STRIDE] bf16
+  const uint16_t* final_norm;
+  uint16_t* kv;             // K caches [B][L][NKV][s_pad][D]
+  uint16_t* kvt;            // V^T caches [B][L][NKV][s_pad/32][D][32]
+  long long kv_seq;         // elements per sequence in each region
+  int s_pad;
+  float* x;                 // [BMAX][H] residual streams
+  float* qkv;               // [BMAX][QKV] raw projections of the current layer
+  uint16_t* att;            // [2][BMAX][QD] merged attention output, bf16 hi / lo parts
+  uint16_t* act;            // [2][BMAX][F] SiLU(g) * u, bf16 hi / lo parts
+  float* part;              // [BMAX][NKV][nsplit_max][PW] attention partials
+  int* cnt;                 // [BMAX][NKV] finished splits of the current layer
+  u64* keys;                // [BMAX] argmax keys of the step
+  int* tok;                 // [BMAX] input tokens of the step
+  int* pos;                 // [BMAX] position of the step's token
+  int* out;                 // [max_steps][BMAX] produced tokens
+  int* step;                // step counter (row of out)
+  float* dbg_logits;        // optional [BMAX][V]
+  const float* inv_freq;    // [D/2]
+  int B, L, V, nsplit_max, max_steps;
+};
+
+// ------------------------------------------------------------ helpers
+// bf16 parts of an fp32 value: hi = RNE(v), lo = RNE(v - hi).
+__device__ __forceinline__ void split2(float v, uint16_t& hi, uint16_t& lo) {
+  hi = f32_to_bf16(v);
+  lo = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+// u32x4 holding 8 bf16 with element e (0..7) replaced by v, in registers.
+__device__ __forceinline__ u32x4 with_bf16(u32x4 x, int e, uint16_t v) {
+  const unsigned keep = (e & 1) ? 0x0000ffffu : 0xffff0000u;
+  const unsigned put = (e & 1) ? ((unsigned)v << 16) : (unsigned)v;
+  u32x4 r = x;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) r[c] = (c == (e >> 1)) ? ((x[c] & keep) | put) : x[c];
+  return r;
+}
+
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// Row stride (elements) of the LDS activation planes: 8 bf16 of padding per
+// row puts the 16 sequences' rows on different LDS banks.
+template <int K>
+constexpr int ldk() { return K + 8; }
+
+// Stage rmsnorm(x[b]) * gain (b < B; zero rows for b >= B) into LDS as bf16
+// hi / lo planes [BMAX][ldk<H>()], for the B operand of a K = H product.
+// Wave w handles sequences w, w + GW.
+template <class S>
+__device__ __forceinline__ void stage_norm(const float* __restrict__ x, const uint16_t* __restrict__ gain, int B,
+                                           uint16_t* hi, uint16_t* lo) {
+  constexpr int H = S::H, PL = H / kWave;
+  const int w = wave_id();
+  const int l = (int)lane_id();
+  for (int b = w; b < BMAX; b += GW) {
+    float v[PL];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < PL; ++c) {
+      v[c] = b < B ? x[(long long)b * H + l + kWave * c] : 0.f;
+      ss = fmaf(v[c], v[c], ss);
+    }
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / (float)H + kRmsEps);
+#pragma unroll
+    for (int c = 0; c < PL; ++c) {
+      const int k = l + kWave * c;
+      uint16_t h, o;
+      split2(b < B ? v[c] * r * bf16_to_f32(gain[k]) : 0.f, h, o);
+      hi[b * ldk<H>() + k] = h;
+      lo[b * ldk<H>() + k] = o;
+    }
+  }
+}
+
+// This wave's share of one 16-row block times the 16 activation columns:
+// tiles kt = w, w + GW, ... of the block (KT tiles of 32 columns).  B-operand
+// planes: element (n, k) at hi[n * ld + k], lo[n * ld + k].  Lane (kg, n)
+// returns rows 4 kg .. 4 kg + 3 of column n.
+template <int KT>
+__device__ __forceinline__ f32x4 block_mma(const u32x4* __restrict__ blk, const uint16_t* hi, const uint16_t* lo,
+                                           int ld) {
+  static_assert(KT % GW == 0, "whole tiles per wave");
+  const unsigned l = lane_id();
+  const int w = wave_id();
+  const auto rs = make_rsrc(blk);
+  const int bo = (int)(l & 15u) * ld + 8 * (int)(l >> 4);
+  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
+  constexpr int TW = KT / GW;
+  constexpr int U = TW < 4 ? TW : 4;
+#pragma unroll 1
+  for (int j0 = 0; j0 < TW; j0 += U) {
+    u32x4 wt[U], bh[U], bl[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kt = w + GW * (j0 + u < TW ? j0 + u : j0);
+      wt[u] = buf_ld_nt(rs, l * 16u, (unsigned)kt * 1024u);
+      bh[u] = *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt);
+      bl[u] = *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j0 + u < TW) {
+        a0 = mfma(wt[u], bh[u], a0);
+        a1 = mfma(wt[u], bl[u], a1);
+      }
+    }
+  }
+  return a0 + a1;
+}
+
+// Cross-wave sum of a block's partial products: red[GW][16][17] in LDS.
+// Returns, for thread t < 256, the total of row t / 16, column t % 16.
+__device__ __forceinline__ float block_reduce(f32x4 acc, float* red) {
+  const unsigned l = lane_id();
+  const int w = wave_id();
+  const int n = (int)(l & 15u), kg = (int)(l >> 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[(w * 16 + 4 * kg + i) * 17 + n] = acc[i];
+  __syncthreads();
+  const int t = ltid();
+  float s = 0.f;
+  if (t < 256) {
+#pragma unroll
+    for (int ww = 0; ww < GW; ++ww) s += red[(ww * 16 + t / 16) * 17 + t % 16];
+  }
+  return s;
+}
+
+// ------------------------------------------------------------ kernels
+// x[b] = E[tok[b]] (the tied embedding, gathered from the tile-layout LM head).
+template <class S>
+__global__ __launch_bounds__(256) void bk_embed(BParams p) {
+  const int b = blockIdx.x;
+  if (b >= p.B) return;
+  const int t_ = p.tok[b];
+  const int tok = t_ < 0 ? 0 : (t_ >= p.V ? p.V - 1 : t_);  // tokens are validated on the host; never index outside
+  for (int k = threadIdx.x; k < S::H; k += blockDim.x) {
+    const int kt = k >> 5, q = (k >> 3) & 3, e = k & 7;
+    const uint16_t* u = reinterpret_cast<const uint16_t*>(
+        p.lmhead + ((long long)(tok >> 4) * S::KT_H + kt) * 64 + q * 16 + (tok & 15));
+    p.x[(long long)b * S::H + k] = bf16_to_f32(u[e]);
+  }
+  if (threadIdx.x == 0) p.keys[b] = 0ull;
+}
+
+// rmsnorm(x) -> q|k|v rows of block blockIdx.x for every sequence.
+template <class S>
+__global__ __launch_bounds__(GT) void bk_qkv(BParams p, int layer) {
+  __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * ldk<S::H>()], lo[BMAX * ldk<S::H>()];
+  __shared__ float red[GW * 16 * 17];
+  stage_norm<S>(p.x, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_ATTN, p.B, hi, lo);
+  __syncthreads();
+  const int rb = blockIdx.x;
+  const f32x4 acc = block_mma<S::KT_H>(p.wqkv + layer * p.u_qkv + (long long)rb * S::KT_H * 64, hi, lo, ldk<S::H>());
+  const float v = block_reduce(acc, red);
+  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
+  if (t < 256 && b < p.B) p.qkv[(long long)b * S::QKV + row] = v;
+}
+
+// O projection + residual: x[b][row] += Wo[row] . att[b].
+template <class S>
+__global__ __launch_bounds__(GT) void bk_o(BParams p, int layer) {
+  __shared__ float red[GW * 16 * 17];
+  const int rb = blockIdx.x;
+  const f32x4 acc = block_mma<S::KT_Q>(p.wo + layer * p.u_o + (long long)rb * S::KT_Q * 64, p.att,
+                                       p.att + BMAX * S::QD, S::QD);
+  const float v = block_reduce(acc, red);
+  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
+  if (t < 256 && b < p.B) p.x[(long long)b * S::H + row] += v;
+}
+
+// rmsnorm(x) -> gate and up rows of block blockIdx.x -> SiLU(g) * u parts.
+template <class S>
+__global__ __launch_bounds__(GT) void bk_gu(BParams p, int layer) {
+  __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * ldk<S::H>()], lo[BMAX * ldk<S::H>()];
+  __shared__ float red[GW * 16 * 17];
+  stage_norm<S>(p.x, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, p.B, hi, lo);
+  __syncthreads();
+  const int rb = blockIdx.x;
+  const long long off = (long long)rb * S::KT_H * 64;
+  const f32x4 ag = block_mma<S::KT_H>(p.wg + layer * p.u_gu + off, hi, lo, ldk<S::H>());
+  const float g = block_reduce(ag, red);
+  __syncthreads();
+  const f32x4 au = block_mma<S::KT_H>(p.wu + layer * p.u_gu + off, hi, lo, ldk<S::H>());
+  const float u = block_reduce(au, red);
+  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
+  if (t < 256 && b < p.B) {
+    uint16_t h, o;
+    split2(g / (1.0f + __expf(-g)) * u, h, o);  // SiLU(g) * u (reference utils.cuh:59-61)
+    p.act[(long long)b * S::F + row] = h;
+    p.act[(long long)(BMAX + b) * S::F + row] = o;
+  }
+}
+
+// Down projection + residual: x[b][row] += Wd[row] . act[b].
+template <class S>
+__global__ __launch_bounds__(GT) void bk_down(BParams p, int layer) {
+  __shared__ float red[GW * 16 * 17];
+  const int rb = blockIdx.x;
+  const f32x4 acc = block_mma<S::KT_F>(p.wd + layer * p.u_dn + (long long)rb * S::KT_F * 64, p.act,
+                                       p.act + BMAX * S::F, S::F);
+  const float v = block_reduce(acc, red);
+  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
+  if (t < 256 && b < p.B) p.x[(long long)b * S::H + row] += v;
+}
+
+// Final rmsnorm -> tied LM head -> per-sequence argmax (reference
+// sampling.cuh:32-117).  Each wave scores whole 16-row blocks; keys are
+// ordered(logit) << 32 | (0xffffffff - index), combined with an atomic max, so
+// the result is the largest logit and, among equal logits, the lowest index.
+template <class S>
+__global__ __launch_bounds__(GT) void bk_lm(BParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * ldk<S::H>()], lo[BMAX * ldk<S::H>()];
+  __shared__ u64 best_w[GW][BMAX];
+  stage_norm<S>(p.x, p.final_norm, p.B, hi, lo);
+  __syncthreads();
+  const unsigned l = lane_id();
+  const int w = wave_id();
+  const int n = (int)(l & 15u), kg = (int)(l >> 4);
+  const int nb = p.V / 16;
+  const int bo = n * ldk<S::H>() + 8 * kg;
+  u64 best = 0ull;
+  for (int rb = blockIdx.x * GW + w; rb < nb; rb += gridDim.x * GW) {
+    const auto rs = make_rsrc(p.lmhead + (long long)rb * S::KT_H * 64);
+    f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
+    constexpr int U = 8;
+#pragma unroll 1
+    for (int k0 = 0; k0 < S::KT_H; k0 += U) {
+      u32x4 wt[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) wt[u] = buf_ld_nt(rs, l * 16u, (unsigned)(k0 + u) * 1024u);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kt = k0 + u;
+        a0 = mfma(wt[u], *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt), a0);
+        a1 = mfma(wt[u], *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt), a1);
+      }
+    }
+    const f32x4 acc = a0 + a1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned idx = (unsigned)(rb * 16 + 4 * kg + i);
+      if (p.dbg_logits && n < p.B) p.dbg_logits[(long long)n * p.V + idx] = acc[i];
+      const u64 key = ((u64)f32_order_key(acc[i]) << 32) | (u64)(0xffffffffu - idx);
+      best = key > best ? key : best;
+    }
+  }
+  // lanes n, n + 16, n + 32, n + 48 hold column n
+#pragma unroll
+  for (int m = 16; m <= 32; m <<= 1) {
+    const u64 o = __shfl_xor(best, m);
+    best = o > best ? o : best;
+  }
+  if (kg == 0) best_w[w][n] = best;
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < p.B) {
+    u64 b = 0ull;
+#pragma unroll
+    for (int ww = 0; ww < GW; ++ww) b = best_w[ww][t] > b ? best_w[ww][t] : b;
+    atomicMax(reinterpret_cast<unsigned long long*>(p.keys + t), (unsigned long long)b);
+  }
+}
+
+// Tokens of the step from the argmax keys; positions advance.
+__global__ void bk_tok(BParams p) {
+  const int b = threadIdx.x;
+  const int s = *p.step;
+  if (b < p.B) {
+    const int tok = (int)(0xffffffffu - (unsigned)(p.keys[b] & 0xffffffffull));
+    p.tok[b] = tok;
+    if (s < p.max_steps) p.out[(long long)s * BMAX + b] = tok;
+    p.pos[b] += 1;
+  }
+  __syncthreads();
+  if (b == 0) *p.step = s + 1;
+}
+
+// ------------------------------------------------------------ attention
+// One item = (sequence b, kv head g, split s) of CH positions; wave w takes
+// the 32-position block 4 s + w.  Both products of a block run on the matrix
+// cores exactly as the batch-1 kernel does: scores^T = K . Qb with q split into
+// three bf16 parts in rows 4 j + 0..2 (j = q head of the group), and
+// out^T = V^T . Pb with the softmax weights split the same way.
+template <class S>
+__global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
+  static_assert(S::GQA == 2 && S::D == 64, "batched attention is built for 2 q heads of 64 per kv head");
+  constexpr int D = S::D, NKV = S::NKV;
+  __shared__ __attribute__((aligned(16))) uint16_t qb[16][D];          // q parts (A operand of the scores)
+  __shared__ __attribute__((aligned(16))) uint16_t pb[AW][16][32];     // weight parts (A operand of the output)
+  __shared__ __attribute__((aligned(16))) uint16_t kcur[D], vcur[D];   // bf16 K / V of position pos
+  __shared__ float rc[D / 2], rsn[D / 2];
+  __shared__ float mw[AW][2], lw[AW][2], ow[AW][2][D];
+  __shared__ int last;
+  const int item = blockIdx.x;
+  const int b = item / (NKV * p.nsplit_max), g = (item / p.nsplit_max) % NKV, s = item % p.nsplit_max;
+  if (b >= p.B) return;
+  const int pos = p.pos[b], n = pos + 1;
+  const int nsplit = (n + CH - 1) / CH;
+  if (s >= nsplit) return;
+  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+  const unsigned lu = (unsigned)l;
+  const int c16 = l & 15, rg = l >> 4;
+  for (int i = tid; i < 16 * D; i += AT) (&qb[0][0])[i] = 0;
+  for (int i = tid; i < AW * 16 * 32; i += AT) (&pb[0][0][0])[i] = 0;
+  if (tid < D / 2) {
+    float sn, cs;
+    sincosf((float)pos * p.inv_freq[tid], &sn, &cs);
+    rc[tid] = cs;
+    rsn[tid] = sn;
+  }
+  __syncthreads();
+  // 1. q heads (waves 0, 1), k (wave 2), v (wave 3) of position pos: QK-norm
+  //    (reference rmsnorm.cuh:57-84) and RoPE rotate-half (attention.cuh:22-44)
+  const float* src = p.qkv + (long long)b * S::QKV +
+                     (w < 2 ? (g * 2 + w) * D : (w == 2 ? S::QD + g * D : S::QD + S::KVD + g * D));
+  float v = src[l];
+  const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
+  const bool own = pos >= s * CH && pos < (s + 1) * CH;
+  if (w < 3) {
+    const float ss = wave_sum(v * v);
+    const uint16_t* gn = p.norms + (long long)layer * S::NORM_STRIDE + (w < 2 ? S::NORM_Q : S::NORM_K);
+    v = v * rsqrtf(ss / (float)D + kRmsEps) * bf16_to_f32(gn[l]);
+    const float partner = lane_xor32(v);
+    const int d = l & 31;
+    v = l < 32 ? v * rc[d] - partner * rsn[d] : v * rc[d] + partner * rsn[d];
+    if (w < 2) {
+      uint16_t h, m, o;
+      split_bf16(v, h, m, o);
+      qb[4 * w + 0][l] = h;
+      qb[4 * w + 1][l] = m;
+      qb[4 * w + 2][l] = o;
+    } else {
+      const uint16_t kb = f32_to_bf16(v);
+      kcur[l] = kb;
+      if (own) p.kv[kbase + (long long)pos * D + l] = kb;  // KV append (reference kv_cache.cuh:58-78)
+    }
+  } else {
+    const uint16_t vb = f32_to_bf16(v);
+    vcur[l] = vb;
+    if (own) p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = vb;
+  }
+  __syncthreads();
+  // 2. the wave's 32-position block
+  const float scale = 1.0f / sqrtf((float)D);
+  const int blk = s * AW + w;
+  const int t0 = 32 * blk;
+  float m = -INFINITY, lsum = 0.f;
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (t0 < n) {
+    const auto rk = make_rsrc(p.kv + kbase + (long long)t0 * D);
+    const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
+    u32x4 kr[2][2], vr[D / 16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+        kr[h][kc] = __builtin_amdgcn_raw_buffer_load_b128(rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      vr[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+    // position pos takes K / V from LDS (this item appended them)
+    if (pos >= t0 && pos < t0 + 32) {
+      const int rp = pos - t0;
+      if (c16 == (rp & 15)) {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+          kr[rp >> 4][kc] = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
+      }
+      if (rg == (rp >> 3)) {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) vr[dt] = with_bf16(vr[dt], rp & 7, vcur[16 * dt + c16]);
+      }
+    }
+    float sc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+        d4 = mfma(*reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]), kr[h][kc], d4);
+      const int t = t0 + 16 * h + c16;
+      sc[h] = t < n ? ((d4[0] + d4[1]) + d4[2]) * scale : -INFINITY;
+    }
+    m = group_max<16>(fmaxf(sc[0], sc[1]));  // finite: position t0 < n is valid
+    float ps = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sc[h] = __expf(sc[h] - m);
+      ps += sc[h];
+    }
+    lsum = group_sum<16>(ps);
+    if (rg < 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const Split3 a = split3(sc[h]);
+        pb[w][4 * rg + 0][16 * h + c16] = (uint16_t)(a.hi >> 16);
+        pb[w][4 * rg + 1][16 * h + c16] = (uint16_t)(a.mid >> 16);
+        pb[w][4 * rg + 2][16 * h + c16] = (uint16_t)(a.lo >> 16);
+      }
+    }
+    asm volatile("" ::: "memory");  // LDS operations of one wave complete in order
+    const u32x4 pa = *reinterpret_cast<const u32x4*>(&pb[w][c16][8 * rg]);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = mfma(pa, vr[dt], acc[dt]);
+  }
+  // 3. combine the waves into the item's partial
+  if (rg < 2) {
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) ow[w][rg][16 * dt + c16] = (acc[dt][0] + acc[dt][1]) + acc[dt][2];
+    if (c16 == 0) {
+      mw[w][rg] = m;
+      lw[w][rg] = lsum;
+    }
+  }
+  __syncthreads();
+  float* part = p.part + (((long long)b * NKV + g) * p.nsplit_max + s) * PW;
+  if (tid < 2 * D) {
+    const int h = tid / D, d = tid % D;
+    float M = mw[0][h];
+#pragma unroll
+    for (int i = 1; i < AW; ++i) M = fmaxf(M, mw[i][h]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int i = 0; i < AW; ++i) {
+      const float f = __expf(mw[i][h] - M);
+      o = fmaf(f, ow[i][h][d], o);
+      L = fmaf(f, lw[i][h], L);
+    }
+    __hip_atomic_store(part + tid, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == 0) {
+      __hip_atomic_store(part + 2 * D + 2 * h, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(part + 2 * D + 2 * h + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // 4. the last split of (b, g) to finish merges: the partial stores above are
+  //    acknowledged (write-through) before the counter moves
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    int* c = p.cnt + b * NKV + g;
+    const int done = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = done == nsplit - 1;
+    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed for the next layer
+  }
+  __syncthreads();
+  if (!last) return;
+  if (tid < 2 * D) {
+    const int h = tid / D;
+    const float* base = p.part + ((long long)b * NKV + g) * p.nsplit_max * PW;
+    float M = -INFINITY;
+    for (int i = 0; i < nsplit; ++i)
+      M = fmaxf(M, __hip_atomic_load(base + (long long)i * PW + 2 * D + 2 * h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float o = 0.f, L = 0.f;
+    for (int i = 0; i < nsplit; ++i) {
+      const float* pi = base + (long long)i * PW;
+      const float f = __expf(__hip_atomic_load(pi + 2 * D + 2 * h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - M);
+      o = fmaf(f, __hip_atomic_load(pi + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), o);
+      L = fmaf(f, __hip_atomic_load(pi + 2 * D + 2 * h + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), L);
+    }
+    uint16_t hi, lo;
+    split2(o / L, hi, lo);
+    const long long k = (long long)b * S::QD + g * 2 * D + tid;
+    p.att[k] = hi;
+    p.att[(long long)BMAX * S::QD + k] = lo;
+  }
+}
+
+}  // namespace batch
+}  // namespace mk

@@ -1,0 +1,41 @@
+// Host-side helpers shared by the translation units of megakernel.so: the
+// thread-local error message, the HIP error check, and the set-up kernels
+// (weight repacking, synthetic data, KV layout conversion) that both the
+// batch-1 decode handle and the batched-decode handle launch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mk_device.h"
+
+namespace mk {
+
+extern thread_local char g_err[512];
+void set_err(const char* fmt, ...);
+
+#define HIPCHK(expr, ret)                                                                  \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess) {                                                                \
+      ::mk::set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+      return ret;                                                                          \
+    }                                                                                      \
+  } while (0)
+
+// Device KV cache addressing of one sequence: K [L][NKV][s_pad][D], V^T
+// blocks [L][NKV][s_pad/32][D][32], both bf16; kv points at K, kvt at V^T.
+__device__ __forceinline__ long long k_index(int l, int g, long long t, int d, int NKV, int s_pad, int D) {
+  return (((long long)l * NKV + g) * s_pad + t) * D + d;
+}
+__device__ __forceinline__ long long vt_index(int l, int g, long long t, int d, int NKV, int s_pad, int D) {
+  return ((long long)l * NKV + g) * (long long)s_pad * D + (t / 32) * 32LL * D + (long long)d * 32 + (t % 32);
+}
+
+__global__ void repack_kernel(const u32x4* __restrict__ src, int R, int K, u32x4* __restrict__ dst,
+                              int blk_stride, int blk_off, int row_pairs);
+__global__ void synth_kv_kernel(uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt, int L, int NKV, int s_pad,
+                                int D, int len, unsigned long long seed, float c);
+__global__ void kv_convert_kernel(uint16_t* __restrict__ buf, uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt,
+                                  int L, int NKV, int s_pad, int D, int len, int to_cache);
+
+}  // namespace mk

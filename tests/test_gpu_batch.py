@@ -1,0 +1,216 @@
+"""GPU parity of the batched decode (megakernel_decode_batch and friends,
+BASELINE configs[4]) against the CPU oracle, one oracle state per sequence.
+
+Bars: fp32 logits within 2e-2 abs, greedy tokens
+identical wherever the oracle's top-1/top-2 margin exceeds 2e-2; KV bytes
+appended by a step equal the oracle's bf16 K / V (at most 1 ulp on < 1 % of
+entries, fp32 summation order).  Sequences have different cache lengths,
+including an empty cache and lengths that straddle the 128-position
+attention splits.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from megakernel_amd import _lib
+from megakernel_amd.batch import BatchEngine
+from megakernel_amd.config import BASELINE, TINY
+from megakernel_amd.weights import DeviceWeights
+from oracle import qwen3_ref, synth
+
+from ._helpers import LOGIT_ABS, MARGIN, oracle_shape
+
+pytestmark = pytest.mark.gpu
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+class MultiOracle:
+    """One Qwen3Oracle (one copy of the weights) serving several sequences:
+    each sequence has its own KV cache tensors and position."""
+
+    def __init__(self, shape, dw, n_seq: int, max_seq: int):
+        osh = oracle_shape(shape)
+        bits = qwen3_ref.unpack_flat(osh, dw.to_host(), dw.layout.offsets)
+        self.orc = qwen3_ref.Qwen3Oracle(osh, bits, max_seq)
+        self.caches = [(self.orc.k_cache.clone(), self.orc.v_cache.clone()) for _ in range(n_seq)]
+        self.pos = [0] * n_seq
+        self.shape = shape
+
+    def prefill(self, seq: int, length: int, seed: int):
+        s = self.shape
+        ks = np.stack([synth.kv_prefill_bits(seed, l, 0, length, s.n_kv_heads, s.head_dim)
+                       for l in range(s.n_layers)])
+        vs = np.stack([synth.kv_prefill_bits(seed, l, 1, length, s.n_kv_heads, s.head_dim)
+                       for l in range(s.n_layers)])
+        k, v = self.caches[seq]
+        k.zero_()
+        v.zero_()
+        k[:, :, :length] = qwen3_ref.bits_to_torch(ks)
+        v[:, :, :length] = qwen3_ref.bits_to_torch(vs)
+        self.pos[seq] = length
+
+    def step(self, seq: int, token: int) -> dict:
+        self.orc.k_cache, self.orc.v_cache = self.caches[seq]
+        self.orc.pos = self.pos[seq]
+        r = self.orc.step(int(token), capture=True)
+        self.pos[seq] = self.orc.pos
+        return r
+
+
+def _setup(shape, seed, lengths, max_seq):
+    dw = DeviceWeights(shape, seed, std=0.02, gain_std=0.1)
+    eng = BatchEngine(dw, len(lengths), max_seq, shape)
+    mo = MultiOracle(shape, dw, len(lengths), max_seq)
+    for b, n in enumerate(lengths):
+        eng.fill_kv_synthetic(b, n, 500 + b)
+        mo.prefill(b, n, 500 + b)
+    assert eng.positions() == list(lengths)
+    return dw, eng, mo
+
+
+def _check_step(logits, toks, refs, label):
+    worst = 0.0
+    for b, r in enumerate(refs):
+        err = float(np.abs(logits[b] - r["logits"].numpy()).max())
+        worst = max(worst, err)
+        assert err <= LOGIT_ABS, f"{label} seq {b}: logits max abs err {err:.3e}"
+        if toks[b] != r["token"]:
+            m = qwen3_ref.top2_margin(r["logits"])
+            assert m <= MARGIN, f"{label} seq {b}: token {toks[b]} != oracle {r['token']} (margin {m:.4f})"
+    return worst
+
+
+def test_batch_tiny_parity():
+    """4 sequences (empty cache, 5, 127 and 200 cached positions), 4 steps."""
+    lengths = [0, 5, 127, 200]
+    dw, eng, mo = _setup(TINY, 31, lengths, 256)
+    try:
+        toks = [7, 100, 3, 999]
+        for i in range(4):
+            _print(f"batch tiny step {i} tokens {toks}")
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(len(lengths))]
+            worst = _check_step(logits, out, refs, f"step {i}")
+            _print(f"  worst logits abs err {worst:.2e}")
+            toks = out
+        assert eng.positions() == [n + 4 for n in lengths]
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch_generate_equals_decode_and_oracle():
+    """generate (graph replays) == repeated decode == oracle, teacher-forced."""
+    lengths = [3, 130, 64, 1]
+    dw, eng, mo = _setup(TINY, 32, lengths, 256)
+    eng2 = BatchEngine(dw, len(lengths), 256, TINY)
+    try:
+        for b, n in enumerate(lengths):
+            eng2.fill_kv_synthetic(b, n, 500 + b)
+        first = [11, 22, 33, 44]
+        n_steps = 6
+        gen = eng.generate(first, n_steps)
+        _print(f"batch generate {gen.tolist()}")
+        toks = first
+        for i in range(n_steps):
+            out = eng2.decode(toks)
+            assert out == gen[i].tolist(), f"step {i}: decode {out} != generate {gen[i].tolist()}"
+            refs = [mo.step(b, toks[b]) for b in range(len(lengths))]
+            for b, r in enumerate(refs):
+                if out[b] != r["token"]:
+                    assert qwen3_ref.top2_margin(r["logits"]) <= MARGIN
+            toks = out
+    finally:
+        eng.close()
+        eng2.close()
+        dw.free()
+
+
+def test_batch_kv_append_bytes():
+    """The K / V a step appends equal bf16 of the oracle's post-norm, post-RoPE k and v."""
+    lengths = [0, 40, 129]
+    dw, eng, mo = _setup(TINY, 33, lengths, 256)
+    try:
+        toks = [5, 6, 7]
+        eng.decode(toks)
+        for b, n in enumerate(lengths):
+            mo.step(b, toks[b])
+            got = eng.get_kv(b, n + 1)[:, :, :, n, :]  # [L][2][NKV][D]
+            k, v = mo.caches[b]
+            want = np.stack([k[:, :, n].contiguous().view(torch.int16).numpy(),
+                             v[:, :, n].contiguous().view(torch.int16).numpy()], axis=1).view(np.uint16)
+            diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
+            assert diff.max() <= 1, f"seq {b}: KV bytes differ by up to {diff.max()} ulp"
+            assert (diff > 0).mean() < 0.01, f"seq {b}: {(diff > 0).mean():.3%} of KV entries off by 1 ulp"
+            # the prefix is untouched
+            pre = eng.get_kv(b, n)
+            ks = np.stack([synth.kv_prefill_bits(500 + b, l, 0, n, TINY.n_kv_heads, TINY.head_dim)
+                           for l in range(TINY.n_layers)])
+            assert np.array_equal(pre[:, 0], ks)
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch_baseline_2l_16_sequences():
+    """BASELINE shapes, 2 layers, 16 sequences with lengths drawn from a seed."""
+    shape = BASELINE.with_(n_layers=2, vocab=4096)
+    rng = np.random.default_rng(7)
+    lengths = [int(x) for x in rng.integers(0, 700, size=16)]
+    dw, eng, mo = _setup(shape, 34, lengths, 720)
+    try:
+        toks = [int(t) for t in rng.integers(0, shape.vocab, size=16)]
+        for i in range(3):
+            _print(f"batch baseline-2l step {i} lengths {eng.positions()}")
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(16)]
+            worst = _check_step(logits, out, refs, f"step {i}")
+            _print(f"  worst logits abs err {worst:.2e}")
+            toks = out
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch_full_model_16_sequences():
+    """The full 28-layer BASELINE model (vocab 151936), 16 sequences, 2 steps."""
+    rng = np.random.default_rng(8)
+    lengths = [int(x) for x in rng.integers(1, 300, size=16)]
+    dw, eng, mo = _setup(BASELINE, 35, lengths, 320)
+    try:
+        toks = [int(t) for t in rng.integers(0, BASELINE.vocab, size=16)]
+        for i in range(2):
+            _print(f"batch full model step {i}")
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(16)]
+            worst = _check_step(logits, out, refs, f"step {i}")
+            _print(f"  worst logits abs err {worst:.2e}")
+            toks = out
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch_error_paths():
+    dw = DeviceWeights(TINY, 36)
+    try:
+        with pytest.raises(_lib.MegakernelError, match="n_seq"):
+            BatchEngine(dw, 17, 64, TINY)
+        eng = BatchEngine(dw, 2, 16, TINY)
+        try:
+            with pytest.raises(_lib.MegakernelError, match="token id"):
+                eng.decode([0, TINY.vocab])
+            eng.fill_kv_synthetic(1, 16, 1)
+            with pytest.raises(_lib.MegakernelError, match="exceeds KV capacity"):
+                eng.decode([1, 2])
+            with pytest.raises(_lib.MegakernelError):
+                eng.fill_kv_synthetic(2, 1, 1)
+        finally:
+            eng.close()
+    finally:
+        dw.free()
