@@ -70,11 +70,11 @@ static int launch_step(BHandle* h, const BParams& p) {
   const int L = h->L;
   hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
   for (int l = 0; l < L; ++l) {
-    hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, p, l);
     hipLaunchKernelGGL(bk_attn<S>, dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16 * KS_O), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
   }
   hipLaunchKernelGGL(bk_lm<S>, dim3(h->G), dim3(GT), 0, h->stream, p);
   hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
@@ -153,9 +153,14 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
   h->max_steps = 1 << 16;
   p.max_steps = h->max_steps;
   if (alloc(h, &p.x, (size_t)BMAX * h->H * 4) || alloc(h, &p.qkv, (size_t)BMAX * h->QKV * 4) ||
+      alloc(h, &p.xg, (size_t)4 * BMAX * h->H * 2) || alloc(h, &p.ssq, (size_t)2 * (h->H / 16) * BMAX * 4) ||
       alloc(h, &p.att, (size_t)2 * BMAX * h->QD * 2) || alloc(h, &p.act, (size_t)2 * BMAX * h->F * 2) ||
       alloc(h, &p.part, (size_t)BMAX * h->NKV * h->nsplit_max * PW * 4) ||
       alloc(h, &p.cnt, (size_t)BMAX * h->NKV * 4) || alloc(h, &p.keys, (size_t)BMAX * 8) ||
+      alloc(h, &p.gcnt, (size_t)(h->F / 16 > h->QKV / 16 ? h->F / 16 : h->QKV / 16) * 4) ||
+      alloc(h, &p.gpart, (size_t)((h->F / 16) * KS_GU * 2 > (h->QKV / 16) * KS_QKV ? (h->F / 16) * KS_GU * 2
+                                                                                    : (h->QKV / 16) * KS_QKV) *
+                             256 * 4 + (size_t)(h->H / 16) * (KS_O > KS_DN ? KS_O : KS_DN) * 256 * 4) ||
       alloc(h, &p.tok, (size_t)BMAX * 4) || alloc(h, &p.pos, (size_t)BMAX * 4) ||
       alloc(h, &p.out, (size_t)h->max_steps * BMAX * 4) || alloc(h, &p.step, 64) ||
       alloc(h, &p.dbg_logits, (size_t)BMAX * h->V * 4))

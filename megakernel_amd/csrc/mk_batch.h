@@ -35,8 +35,13 @@ constexpr int GT = 512;        // threads of the GEMM kernels (8 waves)
 constexpr int GW = GT / kWave;
 constexpr int AT = 256;        // threads of an attention item (4 waves)
 constexpr int AW = AT / kWave;
-constexpr int CH = 32 * AW;    // positions per attention split (one 32-position block per wave)
+constexpr int NBW = 2;         // 32-position blocks per wave and attention item
+constexpr int CH = 32 * AW * NBW;  // positions per attention split
 constexpr int PW = 2 * 64 + 4; // partial words per item for GQA 2, D 64: o[2][64], (m, l) x 2
+// K splits of the GEMM kernels (whole 32-column tiles per split)
+// (measured: splitting pays only for the K = F down projection, 64 blocks of
+// 88 tiles; the others lose more to the reduction than they gain)
+constexpr int KS_QKV = 1, KS_O = 1, KS_GU = 1, KS_DN = 4;
 
 struct BParams {
   const u32x4* wqkv;        // per layer [QKV/16][H/32] tiles
@@ -53,11 +58,16 @@ struct BParams {
   long long kv_seq;         // elements per sequence in each region
   int s_pad;
   float* x;                 // [BMAX][H] residual streams
+  uint16_t* xg;             // [2 consumers][2 planes][BMAX][H] x * gain as bf16 hi / lo parts:
+                            //   consumer 0 = attn_norm of the next QKV (or final_norm), 1 = ffn_norm
+  float* ssq;               // [2 consumers][H/16][BMAX] sums of squares of x per 16-row block
   float* qkv;               // [BMAX][QKV] raw projections of the current layer
   uint16_t* att;            // [2][BMAX][QD] merged attention output, bf16 hi / lo parts
   uint16_t* act;            // [2][BMAX][F] SiLU(g) * u, bf16 hi / lo parts
   float* part;              // [BMAX][NKV][nsplit_max][PW] attention partials
   int* cnt;                 // [BMAX][NKV] finished splits of the current layer
+  float* gpart;             // split-K partial block sums of the GEMM kernels
+  int* gcnt;                // [256] finished K splits per 16-row block
   u64* keys;                // [BMAX] argmax keys of the step
   int* tok;                 // [BMAX] input tokens of the step
   int* pos;                 // [BMAX] position of the step's token
@@ -90,75 +100,137 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                  0, 0, 0);
 }
 
-// Row stride (elements) of the LDS activation planes: 8 bf16 of padding per
-// row puts the 16 sequences' rows on different LDS banks.
-template <int K>
-constexpr int ldk() { return K + 8; }
-
-// Stage rmsnorm(x[b]) * gain (b < B; zero rows for b >= B) into LDS as bf16
-// hi / lo planes [BMAX][ldk<H>()], for the B operand of a K = H product.
-// Wave w handles sequences w, w + GW.
+// RMSNorm (reference rmsnorm.cuh:87-108) without a normalisation pass: the
+// kernel that produces x also publishes x * gain as bf16 hi / lo parts (the B
+// operand of the consuming product) and, per 16-row block and sequence, the
+// sum of squares of its rows.  The consumer sums the H/16 partials in a fixed
+// order, r_b = rsqrt(mean(x_b^2) + eps), and scales its outputs by r_b:
+// W . (x * gain * r) = r * (W . (x * gain)).
 template <class S>
-__device__ __forceinline__ void stage_norm(const float* __restrict__ x, const uint16_t* __restrict__ gain, int B,
-                                           uint16_t* hi, uint16_t* lo) {
-  constexpr int H = S::H, PL = H / kWave;
-  const int w = wave_id();
-  const int l = (int)lane_id();
-  for (int b = w; b < BMAX; b += GW) {
-    float v[PL];
+__device__ __forceinline__ uint16_t* xg_plane(const BParams& p, int c, int lohi) {
+  return p.xg + ((long long)(2 * c + lohi) * BMAX) * S::H;
+}
+
+// Epilogue of an x-producing 16-row block: thread t < 256 holds the new x of
+// row rb * 16 + t / 16, sequence t % 16.  red: >= 256 floats of LDS.
+template <class S>
+__device__ __forceinline__ void publish_x(const BParams& p, int c, const uint16_t* gain, int rb, float xn,
+                                          float* red) {
+  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
+  if (t < 256) {
+    const bool on = b < p.B;
+    if (on) {
+      p.x[(long long)b * S::H + row] = xn;
+      uint16_t h, o;
+      split2(xn * bf16_to_f32(gain[row]), h, o);
+      xg_plane<S>(p, c, 0)[(long long)b * S::H + row] = h;
+      xg_plane<S>(p, c, 1)[(long long)b * S::H + row] = o;
+    }
+    red[t] = on ? xn * xn : 0.f;
+  }
+  __syncthreads();
+  if (t < BMAX) {
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < PL; ++c) {
-      v[c] = b < B ? x[(long long)b * H + l + kWave * c] : 0.f;
-      ss = fmaf(v[c], v[c], ss);
-    }
-    ss = wave_sum(ss);
-    const float r = rsqrtf(ss / (float)H + kRmsEps);
-#pragma unroll
-    for (int c = 0; c < PL; ++c) {
-      const int k = l + kWave * c;
-      uint16_t h, o;
-      split2(b < B ? v[c] * r * bf16_to_f32(gain[k]) : 0.f, h, o);
-      hi[b * ldk<H>() + k] = h;
-      lo[b * ldk<H>() + k] = o;
-    }
+    for (int r = 0; r < 16; ++r) ss += red[r * 16 + t];
+    p.ssq[((long long)c * (S::H / 16) + rb) * BMAX + t] = ss;
   }
 }
 
-// This wave's share of one 16-row block times the 16 activation columns:
-// tiles kt = w, w + GW, ... of the block (KT tiles of 32 columns).  B-operand
-// planes: element (n, k) at hi[n * ld + k], lo[n * ld + k].  Lane (kg, n)
-// returns rows 4 kg .. 4 kg + 3 of column n.
-template <int KT>
-__device__ __forceinline__ f32x4 block_mma(const u32x4* __restrict__ blk, const uint16_t* hi, const uint16_t* lo,
-                                           int ld) {
-  static_assert(KT % GW == 0, "whole tiles per wave");
+// r_b of consumer c for b < BMAX into rr (threads t < BMAX; read after a barrier).
+template <class S>
+__device__ __forceinline__ void rnorm(const BParams& p, int c, float* rr) {
+  const int t = threadIdx.x;
+  if (t < BMAX) {
+    const float* q = p.ssq + (long long)c * (S::H / 16) * BMAX + t;
+    float ss = 0.f;
+    for (int rb = 0; rb < S::H / 16; ++rb) ss += q[rb * BMAX];
+    rr[t] = rsqrtf(ss / (float)S::H + kRmsEps);
+  }
+}
+
+// This wave's tiles of one 16-row block (tiles kt = w, w + GW, ... of KT),
+// loaded into registers: the A operands of the block product.  Issued before
+// the activations are staged, so the two latencies overlap.
+template <int NT>
+struct ATiles {  // NT tiles of a K range; wave w holds local tiles w, w + GW, ...
+  static constexpr int TW = (NT + GW - 1) / GW;
+  u32x4 t[TW];
+};
+template <int NT>
+__device__ __forceinline__ void load_tiles(ATiles<NT>& a, const u32x4* __restrict__ blk, int kt0) {
   const unsigned l = lane_id();
   const int w = wave_id();
   const auto rs = make_rsrc(blk);
+#pragma unroll
+  for (int j = 0; j < ATiles<NT>::TW; ++j)
+    a.t[j] = w + GW * j < NT ? buf_ld_nt(rs, l * 16u, (unsigned)(kt0 + w + GW * j) * 1024u) : u32x4{0u, 0u, 0u, 0u};
+}
+
+// The tiles times the 16 activation columns.  B-operand planes: element
+// (n, k) at hi[n * ld + k], lo[n * ld + k].  Lane (kg, n) returns rows
+// 4 kg .. 4 kg + 3 of column n (this wave's share of the K sum).
+template <int NT>
+__device__ __forceinline__ f32x4 tiles_mma(const ATiles<NT>& a, const uint16_t* hi, const uint16_t* lo, int ld,
+                                           int kt0) {
+  const unsigned l = lane_id();
+  const int w = wave_id();
   const int bo = (int)(l & 15u) * ld + 8 * (int)(l >> 4);
   f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
-  constexpr int TW = KT / GW;
-  constexpr int U = TW < 4 ? TW : 4;
-#pragma unroll 1
-  for (int j0 = 0; j0 < TW; j0 += U) {
-    u32x4 wt[U], bh[U], bl[U];
+  u32x4 bh[ATiles<NT>::TW], bl[ATiles<NT>::TW];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kt = w + GW * (j0 + u < TW ? j0 + u : j0);
-      wt[u] = buf_ld_nt(rs, l * 16u, (unsigned)kt * 1024u);
-      bh[u] = *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt);
-      bl[u] = *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt);
+  for (int j = 0; j < ATiles<NT>::TW; ++j) {
+    const int kt = kt0 + w + GW * j;
+    if (w + GW * j < NT) {
+      bh[j] = *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt);
+      bl[j] = *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt);
     }
+  }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (j0 + u < TW) {
-        a0 = mfma(wt[u], bh[u], a0);
-        a1 = mfma(wt[u], bl[u], a1);
-      }
+  for (int j = 0; j < ATiles<NT>::TW; ++j) {
+    if (w + GW * j < NT) {
+      a0 = mfma(a.t[j], bh[j], a0);
+      a1 = mfma(a.t[j], bl[j], a1);
     }
   }
   return a0 + a1;
+}
+
+// K splits of a 16-row block run on KS workgroups; each publishes its block
+// sums (thread t < 256: row t / 16, column t % 16; NV values per thread) with
+// write-through stores, and the workgroup that completes the block (an
+// agent-scope counter) adds the KS partials in split order -- the same sum in
+// every run -- and runs the epilogue.  Returns true in that workgroup, with
+// v[] replaced by the totals.  `last`: one int of LDS.
+template <int NV>
+__device__ __forceinline__ bool splitk_finish(const BParams& p, int rb, int ks, int KS, float (&v)[NV], int* last) {
+  if (KS == 1) return true;  // one workgroup per block: its sums are the totals
+  const int t = threadIdx.x;
+  float* buf = p.gpart + ((long long)rb * KS) * 256 * NV;
+  if (t < 256) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      __hip_atomic_store(buf + ((long long)ks * NV + i) * 256 + t, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is acknowledged before the count moves
+  __syncthreads();
+  if (t == 0) {
+    const int done = __hip_atomic_fetch_add(p.gcnt + rb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last = done == KS - 1;
+    if (*last) __hip_atomic_store(p.gcnt + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed
+  }
+  __syncthreads();
+  if (!*last) return false;
+  if (t < 256) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float sum = 0.f;
+      for (int k = 0; k < KS; ++k)
+        sum += __hip_atomic_load(buf + ((long long)k * NV + i) * 256 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v[i] = sum;
+    }
+  }
+  return true;
 }
 
 // Cross-wave sum of a block's partial products: red[GW][16][17] in LDS.
@@ -180,64 +252,97 @@ __device__ __forceinline__ float block_reduce(f32x4 acc, float* red) {
 }
 
 // ------------------------------------------------------------ kernels
-// x[b] = E[tok[b]] (the tied embedding, gathered from the tile-layout LM head).
+// x[b] = E[tok[b]] (the tied embedding, gathered from the tile-layout LM head),
+// published for layer 0's QKV.
 template <class S>
 __global__ __launch_bounds__(256) void bk_embed(BParams p) {
+  __shared__ float xs[S::H];
   const int b = blockIdx.x;
-  if (b >= p.B) return;
-  const int t_ = p.tok[b];
+  if (b >= BMAX) return;
+  const int t = threadIdx.x;
+  const bool on = b < p.B;
+  const int t_ = on ? p.tok[b] : 0;
   const int tok = t_ < 0 ? 0 : (t_ >= p.V ? p.V - 1 : t_);  // tokens are validated on the host; never index outside
-  for (int k = threadIdx.x; k < S::H; k += blockDim.x) {
+  for (int k = t; k < S::H; k += blockDim.x) {
     const int kt = k >> 5, q = (k >> 3) & 3, e = k & 7;
     const uint16_t* u = reinterpret_cast<const uint16_t*>(
         p.lmhead + ((long long)(tok >> 4) * S::KT_H + kt) * 64 + q * 16 + (tok & 15));
-    p.x[(long long)b * S::H + k] = bf16_to_f32(u[e]);
+    const float xv = on ? bf16_to_f32(u[e]) : 0.f;
+    xs[k] = xv;
+    if (on) {
+      p.x[(long long)b * S::H + k] = xv;
+      uint16_t h, o;
+      split2(xv * bf16_to_f32(p.norms[S::NORM_ATTN + k]), h, o);
+      xg_plane<S>(p, 0, 0)[(long long)b * S::H + k] = h;
+      xg_plane<S>(p, 0, 1)[(long long)b * S::H + k] = o;
+    }
   }
-  if (threadIdx.x == 0) p.keys[b] = 0ull;
+  __syncthreads();
+  for (int rb = t; rb < S::H / 16; rb += blockDim.x) {
+    float ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ss += xs[rb * 16 + r] * xs[rb * 16 + r];
+    p.ssq[(long long)rb * BMAX + b] = ss;
+  }
+  if (t == 0) p.keys[b] = 0ull;
 }
 
 // rmsnorm(x) -> q|k|v rows of block blockIdx.x for every sequence.
 template <class S>
 __global__ __launch_bounds__(GT) void bk_qkv(BParams p, int layer) {
-  __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * ldk<S::H>()], lo[BMAX * ldk<S::H>()];
   __shared__ float red[GW * 16 * 17];
-  stage_norm<S>(p.x, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_ATTN, p.B, hi, lo);
-  __syncthreads();
-  const int rb = blockIdx.x;
-  const f32x4 acc = block_mma<S::KT_H>(p.wqkv + layer * p.u_qkv + (long long)rb * S::KT_H * 64, hi, lo, ldk<S::H>());
-  const float v = block_reduce(acc, red);
+  __shared__ float rr[BMAX];
+  __shared__ int last;
+  constexpr int NT = S::KT_H / KS_QKV;
+  const int rb = blockIdx.x / KS_QKV, ks = blockIdx.x % KS_QKV, kt0 = ks * NT;
+  ATiles<NT> a;
+  load_tiles(a, p.wqkv + layer * p.u_qkv + (long long)rb * S::KT_H * 64, kt0);
+  rnorm<S>(p, 0, rr);
+  float v[1] = {block_reduce(tiles_mma(a, xg_plane<S>(p, 0, 0), xg_plane<S>(p, 0, 1), S::H, kt0), red)};
+  if (!splitk_finish(p, rb, ks, KS_QKV, v, &last)) return;
   const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
-  if (t < 256 && b < p.B) p.qkv[(long long)b * S::QKV + row] = v;
+  if (t < 256 && b < p.B) p.qkv[(long long)b * S::QKV + row] = v[0] * rr[b];
 }
 
-// O projection + residual: x[b][row] += Wo[row] . att[b].
+// O projection + residual: x[b][row] += Wo[row] . att[b]; x published for the FFN norm.
 template <class S>
 __global__ __launch_bounds__(GT) void bk_o(BParams p, int layer) {
   __shared__ float red[GW * 16 * 17];
-  const int rb = blockIdx.x;
-  const f32x4 acc = block_mma<S::KT_Q>(p.wo + layer * p.u_o + (long long)rb * S::KT_Q * 64, p.att,
-                                       p.att + BMAX * S::QD, S::QD);
-  const float v = block_reduce(acc, red);
-  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
-  if (t < 256 && b < p.B) p.x[(long long)b * S::H + row] += v;
+  __shared__ int last;
+  constexpr int NT = S::KT_Q / KS_O;
+  const int rb = blockIdx.x / KS_O, ks = blockIdx.x % KS_O, kt0 = ks * NT;
+  ATiles<NT> a;
+  load_tiles(a, p.wo + layer * p.u_o + (long long)rb * S::KT_Q * 64, kt0);
+  float v[1] = {block_reduce(tiles_mma(a, p.att, p.att + BMAX * S::QD, S::QD, kt0), red)};
+  if (!splitk_finish(p, rb, ks, KS_O, v, &last)) return;
+  const int t = threadIdx.x, b = t % 16;
+  const float xn = t < 256 && b < p.B ? p.x[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
+  __syncthreads();  // red is reused
+  publish_x<S>(p, 1, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, rb, xn, red);
 }
 
 // rmsnorm(x) -> gate and up rows of block blockIdx.x -> SiLU(g) * u parts.
 template <class S>
 __global__ __launch_bounds__(GT) void bk_gu(BParams p, int layer) {
-  __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * ldk<S::H>()], lo[BMAX * ldk<S::H>()];
   __shared__ float red[GW * 16 * 17];
-  stage_norm<S>(p.x, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, p.B, hi, lo);
-  __syncthreads();
-  const int rb = blockIdx.x;
+  __shared__ float rr[BMAX];
+  __shared__ int last;
+  constexpr int NT = S::KT_H / KS_GU;
+  const int rb = blockIdx.x / KS_GU, ks = blockIdx.x % KS_GU, kt0 = ks * NT;
   const long long off = (long long)rb * S::KT_H * 64;
-  const f32x4 ag = block_mma<S::KT_H>(p.wg + layer * p.u_gu + off, hi, lo, ldk<S::H>());
-  const float g = block_reduce(ag, red);
+  ATiles<NT> ag, au;
+  load_tiles(ag, p.wg + layer * p.u_gu + off, kt0);
+  load_tiles(au, p.wu + layer * p.u_gu + off, kt0);
+  rnorm<S>(p, 1, rr);
+  const uint16_t *hi = xg_plane<S>(p, 1, 0), *lo = xg_plane<S>(p, 1, 1);
+  float v[2];
+  v[0] = block_reduce(tiles_mma(ag, hi, lo, S::H, kt0), red);
   __syncthreads();
-  const f32x4 au = block_mma<S::KT_H>(p.wu + layer * p.u_gu + off, hi, lo, ldk<S::H>());
-  const float u = block_reduce(au, red);
+  v[1] = block_reduce(tiles_mma(au, hi, lo, S::H, kt0), red);
+  if (!splitk_finish(p, rb, ks, KS_GU, v, &last)) return;
   const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
   if (t < 256 && b < p.B) {
+    const float g = v[0] * rr[b], u = v[1] * rr[b];
     uint16_t h, o;
     split2(g / (1.0f + __expf(-g)) * u, h, o);  // SiLU(g) * u (reference utils.cuh:59-61)
     p.act[(long long)b * S::F + row] = h;
@@ -245,16 +350,25 @@ __global__ __launch_bounds__(GT) void bk_gu(BParams p, int layer) {
   }
 }
 
-// Down projection + residual: x[b][row] += Wd[row] . act[b].
+// Down projection + residual: x[b][row] += Wd[row] . act[b]; x published for
+// the next layer's attention norm (the final norm after the last layer).
 template <class S>
 __global__ __launch_bounds__(GT) void bk_down(BParams p, int layer) {
   __shared__ float red[GW * 16 * 17];
-  const int rb = blockIdx.x;
-  const f32x4 acc = block_mma<S::KT_F>(p.wd + layer * p.u_dn + (long long)rb * S::KT_F * 64, p.act,
-                                       p.act + BMAX * S::F, S::F);
-  const float v = block_reduce(acc, red);
-  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
-  if (t < 256 && b < p.B) p.x[(long long)b * S::H + row] += v;
+  __shared__ int last;
+  static_assert(S::KT_F % KS_DN == 0, "whole tiles per K split");
+  constexpr int NT = S::KT_F / KS_DN;
+  const int rb = blockIdx.x / KS_DN, ks = blockIdx.x % KS_DN, kt0 = ks * NT;
+  ATiles<NT> a;
+  load_tiles(a, p.wd + layer * p.u_dn + (long long)rb * S::KT_F * 64, kt0);
+  float v[1] = {block_reduce(tiles_mma(a, p.act, p.act + BMAX * S::F, S::F, kt0), red)};
+  if (!splitk_finish(p, rb, ks, KS_DN, v, &last)) return;
+  const int t = threadIdx.x, b = t % 16;
+  const float xn = t < 256 && b < p.B ? p.x[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
+  __syncthreads();  // red is reused
+  const uint16_t* gain = layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE + S::NORM_ATTN
+                                         : p.final_norm;
+  publish_x<S>(p, 0, gain, rb, xn, red);
 }
 
 // Final rmsnorm -> tied LM head -> per-sequence argmax (reference
@@ -263,40 +377,66 @@ __global__ __launch_bounds__(GT) void bk_down(BParams p, int layer) {
 // the result is the largest logit and, among equal logits, the lowest index.
 template <class S>
 __global__ __launch_bounds__(GT) void bk_lm(BParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * ldk<S::H>()], lo[BMAX * ldk<S::H>()];
+  constexpr int LD = S::H + 8;  // padded LDS rows: the 16 sequences on different banks
+  __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * LD], lo[BMAX * LD];
   __shared__ u64 best_w[GW][BMAX];
-  stage_norm<S>(p.x, p.final_norm, p.B, hi, lo);
+  __shared__ float rr[BMAX];
+  {  // the final-norm parts published by the last layer, copied to LDS
+    const uint16_t *gh = xg_plane<S>(p, 0, 0), *gl = xg_plane<S>(p, 0, 1);
+    for (int i = threadIdx.x; i < BMAX * S::H / 8; i += GT) {
+      const int b = i / (S::H / 8), k = (i % (S::H / 8)) * 8;
+      *reinterpret_cast<u32x4*>(hi + b * LD + k) = *reinterpret_cast<const u32x4*>(gh + (long long)b * S::H + k);
+      *reinterpret_cast<u32x4*>(lo + b * LD + k) = *reinterpret_cast<const u32x4*>(gl + (long long)b * S::H + k);
+    }
+    rnorm<S>(p, 0, rr);
+  }
   __syncthreads();
   const unsigned l = lane_id();
   const int w = wave_id();
   const int n = (int)(l & 15u), kg = (int)(l >> 4);
   const int nb = p.V / 16;
-  const int bo = n * ldk<S::H>() + 8 * kg;
+  const int bo = n * LD + 8 * kg;
+  const float rn = rr[n];
   u64 best = 0ull;
-  for (int rb = blockIdx.x * GW + w; rb < nb; rb += gridDim.x * GW) {
+  // the wave's blocks rb0, rb0 + stride, ... as a flat sequence of chunks of
+  // U tiles; the next chunk's loads are issued before the current one's products
+  constexpr int U = 8, CPB = S::KT_H / U;  // chunks per block
+  static_assert(S::KT_H % U == 0, "whole chunks per block");
+  const int rb0 = blockIdx.x * GW + w, stride = gridDim.x * GW;
+  const int nblk = rb0 < nb ? (nb - 1 - rb0) / stride + 1 : 0;
+  const int nch = nblk * CPB;
+  u32x4 cur[U], nxt[U];
+  auto load_chunk = [&](int c, u32x4* dst) {
+    const int rb = rb0 + (c / CPB) * stride, k0 = (c % CPB) * U;
     const auto rs = make_rsrc(p.lmhead + (long long)rb * S::KT_H * 64);
-    f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
-    constexpr int U = 8;
-#pragma unroll 1
-    for (int k0 = 0; k0 < S::KT_H; k0 += U) {
-      u32x4 wt[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) wt[u] = buf_ld_nt(rs, l * 16u, (unsigned)(k0 + u) * 1024u);
+    for (int u = 0; u < U; ++u) dst[u] = buf_ld_nt(rs, l * 16u, (unsigned)(k0 + u) * 1024u);
+  };
+  if (nch > 0) load_chunk(0, cur);
+  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
+  for (int c = 0; c < nch; ++c) {
+    if (c + 1 < nch) load_chunk(c + 1, nxt);
+    const int k0 = (c % CPB) * U;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int kt = k0 + u;
-        a0 = mfma(wt[u], *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt), a0);
-        a1 = mfma(wt[u], *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt), a1);
+    for (int u = 0; u < U; ++u) {
+      const int kt = k0 + u;
+      a0 = mfma(cur[u], *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt), a0);
+      a1 = mfma(cur[u], *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt), a1);
+    }
+    if (c % CPB == CPB - 1) {  // the block is complete
+      const int rb = rb0 + (c / CPB) * stride;
+      const f32x4 acc = (a0 + a1) * rn;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const unsigned idx = (unsigned)(rb * 16 + 4 * kg + i);
+        if (p.dbg_logits && n < p.B) p.dbg_logits[(long long)n * p.V + idx] = acc[i];
+        const u64 key = ((u64)f32_order_key(acc[i]) << 32) | (u64)(0xffffffffu - idx);
+        best = key > best ? key : best;
       }
+      a0 = a1 = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    const f32x4 acc = a0 + a1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const unsigned idx = (unsigned)(rb * 16 + 4 * kg + i);
-      if (p.dbg_logits && n < p.B) p.dbg_logits[(long long)n * p.V + idx] = acc[i];
-      const u64 key = ((u64)f32_order_key(acc[i]) << 32) | (u64)(0xffffffffu - idx);
-      best = key > best ? key : best;
-    }
+    for (int u = 0; u < U; ++u) cur[u] = nxt[u];
   }
   // lanes n, n + 16, n + 32, n + 48 hold column n
 #pragma unroll
@@ -354,6 +494,26 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
   const unsigned lu = (unsigned)l;
   const int c16 = l & 15, rg = l >> 4;
+  const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
+  // 0. the wave's K / V blocks (4 s + w) + AW * q, q < NBW: issued first, so the
+  //    prologue below overlaps them (blocks past the item repeat a valid block)
+  u32x4 kr[NBW][2][2], vr[NBW][D / 16];
+#pragma unroll
+  for (int q = 0; q < NBW; ++q) {
+    int blk = s * AW * NBW + w + AW * q;
+    blk = 32 * blk < n ? blk : s * AW * NBW;
+    const auto rk = make_rsrc(p.kv + kbase + (long long)blk * 32 * D);
+    const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+        kr[q][h][kc] =
+            __builtin_amdgcn_raw_buffer_load_b128(rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      vr[q][dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+  }
   for (int i = tid; i < 16 * D; i += AT) (&qb[0][0])[i] = 0;
   for (int i = tid; i < AW * 16 * 32; i += AT) (&pb[0][0][0])[i] = 0;
   if (tid < D / 2) {
@@ -368,7 +528,6 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   const float* src = p.qkv + (long long)b * S::QKV +
                      (w < 2 ? (g * 2 + w) * D : (w == 2 ? S::QD + g * D : S::QD + S::KVD + g * D));
   float v = src[l];
-  const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
   const bool own = pos >= s * CH && pos < (s + 1) * CH;
   if (w < 3) {
     const float ss = wave_sum(v * v);
@@ -394,37 +553,30 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
     if (own) p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = vb;
   }
   __syncthreads();
-  // 2. the wave's 32-position block
+  // 2. the wave's blocks: online softmax over them on the matrix cores
   const float scale = 1.0f / sqrtf((float)D);
-  const int blk = s * AW + w;
-  const int t0 = 32 * blk;
   float m = -INFINITY, lsum = 0.f;
   f32x4 acc[D / 16];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (t0 < n) {
-    const auto rk = make_rsrc(p.kv + kbase + (long long)t0 * D);
-    const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
-    u32x4 kr[2][2], vr[D / 16];
+  u32x4 qa[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+  for (int kc = 0; kc < 2; ++kc) qa[kc] = *reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]);
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-        kr[h][kc] = __builtin_amdgcn_raw_buffer_load_b128(rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt)
-      vr[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+  for (int q = 0; q < NBW; ++q) {
+    const int t0 = 32 * (s * AW * NBW + w + AW * q);
+    if (t0 >= n) break;  // uniform over the wave
     // position pos takes K / V from LDS (this item appended them)
     if (pos >= t0 && pos < t0 + 32) {
       const int rp = pos - t0;
       if (c16 == (rp & 15)) {
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc)
-          kr[rp >> 4][kc] = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
+          kr[q][rp >> 4][kc] = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
       }
       if (rg == (rp >> 3)) {
 #pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) vr[dt] = with_bf16(vr[dt], rp & 7, vcur[16 * dt + c16]);
+        for (int dt = 0; dt < D / 16; ++dt) vr[q][dt] = with_bf16(vr[q][dt], rp & 7, vcur[16 * dt + c16]);
       }
     }
     float sc[2];
@@ -432,19 +584,20 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
     for (int h = 0; h < 2; ++h) {
       f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-        d4 = mfma(*reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]), kr[h][kc], d4);
+      for (int kc = 0; kc < 2; ++kc) d4 = mfma(qa[kc], kr[q][h][kc], d4);
       const int t = t0 + 16 * h + c16;
       sc[h] = t < n ? ((d4[0] + d4[1]) + d4[2]) * scale : -INFINITY;
     }
-    m = group_max<16>(fmaxf(sc[0], sc[1]));  // finite: position t0 < n is valid
+    const float mn = fmaxf(m, group_max<16>(fmaxf(sc[0], sc[1])));  // finite: position t0 < n is valid
+    const float alpha = __expf(m - mn);
+    m = mn;
     float ps = 0.f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       sc[h] = __expf(sc[h] - m);
       ps += sc[h];
     }
-    lsum = group_sum<16>(ps);
+    lsum = lsum * alpha + group_sum<16>(ps);
     if (rg < 2) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -457,7 +610,11 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
     asm volatile("" ::: "memory");  // LDS operations of one wave complete in order
     const u32x4 pa = *reinterpret_cast<const u32x4*>(&pb[w][c16][8 * rg]);
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = mfma(pa, vr[dt], acc[dt]);
+    for (int dt = 0; dt < D / 16; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
+      acc[dt] = mfma(pa, vr[q][dt], acc[dt]);
+    }
   }
   // 3. combine the waves into the item's partial
   if (rg < 2) {
