@@ -157,6 +157,7 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
       alloc(h, &p.att, (size_t)2 * BMAX * h->QD * 2) || alloc(h, &p.act, (size_t)2 * BMAX * h->F * 2) ||
       alloc(h, &p.part, (size_t)BMAX * h->NKV * h->nsplit_max * PW * 4) ||
       alloc(h, &p.cnt, (size_t)BMAX * h->NKV * 4) || alloc(h, &p.keys, (size_t)BMAX * 8) ||
+      alloc(h, &p.rope, (size_t)BMAX * h->D * 4) ||
       alloc(h, &p.gcnt, (size_t)(h->F / 16 > h->QKV / 16 ? h->F / 16 : h->QKV / 16) * 4) ||
       alloc(h, &p.gpart, (size_t)((h->F / 16) * KS_GU * 2 > (h->QKV / 16) * KS_QKV ? (h->F / 16) * KS_GU * 2
                                                                                     : (h->QKV / 16) * KS_QKV) *

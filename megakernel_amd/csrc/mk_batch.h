@@ -35,7 +35,10 @@ constexpr int GT = 512;        // threads of the GEMM kernels (8 waves)
 constexpr int GW = GT / kWave;
 constexpr int AT = 256;        // threads of an attention item (4 waves)
 constexpr int AW = AT / kWave;
-constexpr int NBW = 2;         // 32-position blocks per wave and attention item
+#ifndef MK_BATCH_NBW
+#define MK_BATCH_NBW 2
+#endif
+constexpr int NBW = MK_BATCH_NBW;  // 32-position blocks per wave and attention item
 constexpr int CH = 32 * AW * NBW;  // positions per attention split
 constexpr int PW = 2 * 64 + 4; // partial words per item for GQA 2, D 64: o[2][64], (m, l) x 2
 // K splits of the GEMM kernels (whole 32-column tiles per split)
@@ -75,6 +78,7 @@ struct BParams {
   int* step;                // step counter (row of out)
   float* dbg_logits;        // optional [BMAX][V]
   const float* inv_freq;    // [D/2]
+  float* rope;              // [BMAX][2][D/2] cos / sin of the step's position per sequence
   int B, L, V, nsplit_max, max_steps;
 };
 
@@ -283,6 +287,12 @@ __global__ __launch_bounds__(256) void bk_embed(BParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) ss += xs[rb * 16 + r] * xs[rb * 16 + r];
     p.ssq[(long long)rb * BMAX + b] = ss;
+  }
+  if (t < S::D / 2) {  // RoPE angles of this step's position, shared by every layer
+    float sn, cs;
+    sincosf((float)(on ? p.pos[b] : 0) * p.inv_freq[t], &sn, &cs);
+    p.rope[(b * 2 + 0) * (S::D / 2) + t] = cs;
+    p.rope[(b * 2 + 1) * (S::D / 2) + t] = sn;
   }
   if (t == 0) p.keys[b] = 0ull;
 }
@@ -517,10 +527,8 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   for (int i = tid; i < 16 * D; i += AT) (&qb[0][0])[i] = 0;
   for (int i = tid; i < AW * 16 * 32; i += AT) (&pb[0][0][0])[i] = 0;
   if (tid < D / 2) {
-    float sn, cs;
-    sincosf((float)pos * p.inv_freq[tid], &sn, &cs);
-    rc[tid] = cs;
-    rsn[tid] = sn;
+    rc[tid] = p.rope[(b * 2 + 0) * (D / 2) + tid];
+    rsn[tid] = p.rope[(b * 2 + 1) * (D / 2) + tid];
   }
   __syncthreads();
   // 1. q heads (waves 0, 1), k (wave 2), v (wave 3) of position pos: QK-norm
