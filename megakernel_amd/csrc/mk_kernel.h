@@ -41,11 +41,14 @@ constexpr int PHASES_PER_LAYER = 5;
 // Two per wave halves the attention splits (and so the partials every O
 // workgroup merges) against one, at the cost of a longer block step.
 constexpr int KVB = MK_KV_BLOCKS;
-// Cache policy of the LM-head stream (buffer-load aux bits): plain loads
-// measured 5 % faster than non-temporal ones on the LM head (part of it is
-// served from the memory-side cache across tokens).
+// Cache policy of the LM-head stream (buffer-load aux bits): plain loads on
+// 80 % of it and non-temporal loads on the rest measured fastest (part of the
+// plain-loaded share is served from the memory-side cache across tokens).
 #ifndef MK_LMHEAD_AUX
 #define MK_LMHEAD_AUX 0
+#endif
+#ifndef MK_LMHEAD_KEEP_PCT
+#define MK_LMHEAD_KEEP_PCT 80
 #endif
 
 constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
@@ -1221,12 +1224,22 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         const auto rs = make_rsrc(p.lmhead + b * S::KT_H * 64);  // wave-uniform block base
         float acc = 0.f;
         constexpr int U = 16;
+        // the first MK_LMHEAD_KEEP_PCT % of each workgroup's blocks are loaded
+        // with the plain policy (kept by the memory-side cache across tokens),
+        // the rest non-temporally
+        const bool keep = (b - b0) * 100 < (b1 - b0) * MK_LMHEAD_KEEP_PCT;
 #pragma unroll 1
         for (int k0 = 0; k0 < S::KT_H; k0 += U) {
           u32x4 wv[U];
+          if (keep) {
 #pragma unroll
-          for (int u = 0; u < U; ++u)
-            if (k0 + u < S::KT_H) wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lo * 16u, (unsigned)(k0 + u) * 1024u, MK_LMHEAD_AUX);
+            for (int u = 0; u < U; ++u)
+              if (k0 + u < S::KT_H) wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lo * 16u, (unsigned)(k0 + u) * 1024u, MK_LMHEAD_AUX);
+          } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+              if (k0 + u < S::KT_H) wv[u] = buf_ld_nt(rs, lo * 16u, (unsigned)(k0 + u) * 1024u);
+          }
 #pragma unroll
           for (int u = 0; u < U; ++u)
             if (k0 + u < S::KT_H) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
