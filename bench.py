@@ -52,6 +52,10 @@ def parse():
                          "uniform in [--kv-min, --kv-max] from --seed, --steps greedy steps each")
     ap.add_argument("--kv-min", type=int, default=512)
     ap.add_argument("--kv-max", type=int, default=4096)
+    ap.add_argument("--ops", action="store_true",
+                    help="BASELINE configs[1] instead: the operator microbench (each op of a decode step as its "
+                         "own launch, repeated in-kernel over >= 512 MiB of rotating weight / input copies)")
+    ap.add_argument("--ops-rotate-mib", type=int, default=512, help="size of the rotated copies per op")
     return ap.parse_args()
 
 
@@ -221,10 +225,148 @@ def bench_batch(args):
     print(json.dumps(out))
 
 
+def bench_ops(args):
+    """the operator microbench.  Every op of a decode step
+    at the BASELINE shapes runs as its own launch that repeats it `reps` times
+    in-kernel (megakernel_op_*), rotating through >= --ops-rotate-mib MiB of
+    weight copies (GEMVs, LM head) or of input and output vectors (RMSNorm,
+    RoPE), so no cache serves a repeat.  Weights N(0, 0.02) bf16, inputs
+    N(0, 1).  Per op: median HIP-event time of --reps launches after one
+    warm-up, divided by reps (streaming time per op); algorithmic bytes =
+    weights + input / output vectors of one op (the RMSNorm gain, shared by
+    every instance, is not counted).  Also per op: the event time of a launch
+    of ONE instance (the cost of the op as its own launch).
+    `value`: the decode-step op mix (28 x [2 RMSNorm, QKV, RoPE, O, gate/up,
+    down] + final RMSNorm + LM head) in algorithmic GB/s at the streaming
+    times."""
+    import torch
+
+    from megakernel_amd import launcher, ops
+    from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
+
+    s = BASELINE
+    H, F, V, NQ, NKV, D = s.hidden, s.ffn, s.vocab, s.n_q_heads, s.n_kv_heads, s.head_dim
+    QKV = (NQ + 2 * NKV) * D
+    rot = args.ops_rotate_mib << 20
+    target = 8 << 30  # algorithmic bytes per timed launch (about 1 ms)
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    info = launcher.detect_gpu()
+    results = {}
+
+    def timeit(name, fn, reps, nbytes, single):
+        fn()  # warm-up
+        ms = statistics.median([fn() for _ in range(args.reps)])
+        one = statistics.median([single() for _ in range(21)])
+        us = ms * 1e3 / reps
+        gbps = nbytes * reps / (ms * 1e-3) / 1e9
+        results[name] = {"us_per_op": round(us, 4), "bytes_per_op": nbytes, "reps_per_launch": reps,
+                         "launch_ms": round(ms, 4), "gbps": round(gbps, 1),
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                         "roofline_us": round(nbytes / (HBM_PEAK_GBPS * 1e3), 4),
+                         "single_launch_us": round(one * 1e3, 2)}
+        print(f"# {name}: {us:.4f} us/op streaming, {gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS:.1%} of peak), "
+              f"{reps} reps/launch; one instance per launch {one * 1e3:.2f} us", file=sys.stderr, flush=True)
+
+    def weights(rows, k, layout):
+        nb = ops.packed_bytes(rows, k)
+        nc = max(1, -(-rot // nb))
+        buf = torch.empty(nc * nb, dtype=torch.uint8, device="cuda")
+        src = (torch.randn((rows, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        ops.pack(src, rows, k, layout, buf)
+        del src
+        for c in range(1, nc):
+            buf[c * nb:(c + 1) * nb].copy_(buf[:nb])
+        torch.cuda.synchronize()
+        return buf, nb, nc
+
+    # RMSNorm over [H] bf16 -> fp32: rotated pools of input and output vectors
+    n_in = rot // (H * 2)
+    x = torch.randn((n_in, H), generator=g, device="cuda").to(torch.bfloat16)
+    gain = torch.ones(H, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((n_in, H), device="cuda")
+    nbytes = H * 2 + H * 4
+    reps = max(n_in, target // nbytes)
+    timeit("rmsnorm", lambda: ops.rmsnorm(x, gain, y, H, n_in, n_in, reps), reps, nbytes,
+           lambda: ops.rmsnorm(x, gain, y, H, n_in, n_in, 1))
+    del x, y
+
+    # RoPE on NQ + NKV heads x D, positions drawn in [0, 32768)
+    nh = NQ + NKV
+    n_in = rot // (nh * D * 4)
+    x = torch.randn((n_in, nh, D), generator=g, device="cuda")
+    pos = torch.randint(0, 32768, (n_in,), generator=g, device="cuda", dtype=torch.int32)
+    y = torch.empty((n_in, nh, D), device="cuda")
+    nbytes = nh * D * 8 + 4
+    reps = max(n_in, target // nbytes)
+    timeit("rope", lambda: ops.rope(x, pos, y, nh, D, n_in, n_in, reps), reps, nbytes,
+           lambda: ops.rope(x, pos, y, nh, D, n_in, n_in, 1))
+    del x, y, pos
+
+    gemvs = [("qkv", QKV, H, ops.GEMV_PLAIN), ("o", H, NQ * D, ops.GEMV_PLAIN),
+             ("gate_up_silu", F, H, ops.GEMV_GATE_UP), ("down_residual", H, F, ops.GEMV_RESIDUAL)]
+    n_in = 8
+    for name, rows, k, kind in gemvs:
+        gu = kind == ops.GEMV_GATE_UP
+        buf, nb, nc = weights(2 * rows if gu else rows, k, ops.LAYOUT_GATE_UP if gu else ops.LAYOUT_ROWPAIR)
+        xin = torch.randn((n_in, k), generator=g, device="cuda")
+        res = torch.randn((n_in, rows), generator=g, device="cuda") if kind == ops.GEMV_RESIDUAL else None
+        y = torch.empty((64, rows), device="cuda")
+        nbytes = nb + k * 4 + rows * 4 + (rows * 4 if res is not None else 0)
+        reps = max(nc, target // nb)
+        timeit(name, lambda: ops.gemv(buf, nb, nc, rows, k, kind, xin, res, n_in, y, 64, reps), reps, nbytes,
+               lambda: ops.gemv(buf, nb, nc, rows, k, kind, xin, res, n_in, y, 64, 1))
+        results[name]["copies"] = nc
+        del buf, xin, res, y
+        torch.cuda.empty_cache()
+
+    buf, nb, nc = weights(V, H, ops.LAYOUT_TILE)
+    h = torch.randn((n_in, H), generator=g, device="cuda")
+    reps = max(nc, target // nb)
+    keys = torch.zeros(reps, dtype=torch.int64, device="cuda")
+    toks = torch.zeros(reps, dtype=torch.int32, device="cuda")
+    timeit("lm_head_argmax", lambda: ops.lmhead_argmax(buf, nb, nc, V, H, h, n_in, None, keys, toks, reps, reps),
+           reps, nb + H * 4 + 4, lambda: ops.lmhead_argmax(buf, nb, nc, V, H, h, n_in, None, keys, toks, 1, 1))
+    results["lm_head_argmax"]["copies"] = nc
+    del buf
+    torch.cuda.empty_cache()
+
+    # one decode step's op mix
+    L = s.n_layers
+    mix = {"rmsnorm": 2 * L + 1, "rope": L, "qkv": L, "o": L, "gate_up_silu": L, "down_residual": L,
+           "lm_head_argmax": 1}
+    t_tok = sum(n * results[k]["us_per_op"] for k, n in mix.items()) * 1e-6
+    t_one = sum(n * results[k]["single_launch_us"] for k, n in mix.items()) * 1e-6
+    b_tok = sum(n * results[k]["bytes_per_op"] for k, n in mix.items())
+    share = {k: n * results[k]["us_per_op"] * 1e-6 / t_tok for k, n in mix.items()}
+    dom = max(share, key=share.get)
+    out = {
+        "metric": "operator microbench (BASELINE configs[1]): decode-step op mix, achieved HBM GB/s",
+        "value": round(b_tok / t_tok / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.reps,
+        "warmup": 1, "ms_per_step": round(t_tok * 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "each decode op at BASELINE shapes as its own launch, repeated in-kernel over "
+                               f">= {args.ops_rotate_mib} MiB of rotating copies (BASELINE configs[1])",
+                   "device": info["name"], "mix_per_token": mix},
+        "tok_s_streaming_bound": round(1.0 / t_tok, 1),
+        "tok_s_one_launch_per_op": round(1.0 / t_one, 1),
+        "ops": results,
+        "roofline": {"bound": "hbm", "achieved": results[dom]["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": results[dom]["frac"], "traffic": None, "kernel": dom,
+                     "time_share": round(share[dom], 3)},
+    }
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.ops:
+        if args.gpus != 1:
+            print(json.dumps({"error": "this build runs on one GPU only"}))
+            sys.exit(2)
+        bench_ops(args)
         return
     if args.batch:
         if args.gpus != 1:

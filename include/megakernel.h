@@ -195,6 +195,66 @@ int megakernel_batch_debug_logits(void* handle, const int* tokens_in, int* token
 /* Device time of the last megakernel_generate_batch / decode_batch call (ms). */
 float megakernel_batch_last_ms(void* handle);
 
+/* ---- operator microbench ---------------------------
+ * Each op of one decode step as a standalone launch, for measuring it against
+ * its roofline.  The reference has these only as device functions inside its
+ * kernel (no host entry points); each declaration names the device code it
+ * restates.  Every call runs `reps` independent instances of the op in ONE
+ * launch: instance r reads weight copy r % n_copies (copies copy_bytes
+ * apart), input r % n_in and writes output slot r % n_out (instances sharing
+ * a slot leave one of their results, or for the LM head the max over them).
+ * All pointers are device pointers; inputs and outputs are fp32 unless noted.
+ * Calls are blocking, run on the null stream and return 0, or -1 with
+ * megakernel_last_error() set (arguments are checked before any GPU work).
+ * megakernel_op_last_ms() gives the device time of the last call. */
+
+#define MK_OP_LAYOUT_ROWPAIR 0 /* layer matrices (GEMVs): K % 256 == 0 */
+#define MK_OP_LAYOUT_TILE 1    /* LM head 16x32 tiles: K % 32 == 0 */
+#define MK_OP_LAYOUT_GATE_UP 2 /* [gate; up] rows (2F x K) -> interleaved row-pair blocks */
+
+#define MK_OP_GEMV_PLAIN 0     /* y = W x                     (QKV, O) */
+#define MK_OP_GEMV_RESIDUAL 1  /* y = res + W x               (down + residual) */
+#define MK_OP_GEMV_GATE_UP 2   /* y = silu(Wg x) * (Wu x)     (gate/up + SiLU) */
+
+/* Bytes of one packed rows x k bf16 matrix (== rows * k * 2), or -1. */
+long long megakernel_op_packed_bytes(int rows, int k);
+
+/* Repack a row-major bf16 [rows][k] matrix (device) into `layout` at d_dst
+ * (megakernel_op_packed_bytes(rows, k) bytes); both 16-byte aligned.  For
+ * MK_OP_LAYOUT_GATE_UP, rows = 2F: gate rows first, then up rows. */
+int megakernel_op_pack(const void* d_src, int rows, int k, int layout, void* d_dst);
+
+/* rmsnorm_float_in (src/rmsnorm.cuh:87-108): y = x * rsqrt(mean(x^2) + eps) * gain
+ * over n = 512 / 1024 / 2048; x bf16 [n_in][n], gain bf16 [n], y fp32 [n_out][n]. */
+int megakernel_op_rmsnorm(const void* x, const void* gain, float* y, int n, int n_in, int n_out, int reps,
+                          float eps);
+
+/* gemv_qkv / gemv_block / gemv_gate_up_silu (src/gemv.cuh:36-279) and the
+ * down projection with its residual (src/megakernel.cu:270-290).  w: packed
+ * (MK_OP_LAYOUT_ROWPAIR, or MK_OP_LAYOUT_GATE_UP for kind 2), rows outputs,
+ * k in {256, 512, 1024, 2048, 2816, 3072}; x [n_in][k]; res [n_in][rows]
+ * (kind 1); y [n_out][rows]. */
+int megakernel_op_gemv(const void* w, long long copy_bytes, int n_copies, int rows, int k, int kind, const float* x,
+                       const float* res, int n_in, float* y, int n_out, int reps);
+
+/* apply_rope_inplace (src/attention.cuh:22-44), out of place: x, y
+ * [n][n_heads][head_dim] with instance r at position pos[r % n_in],
+ * angle = pos * theta^(-2i/head_dim) in fp32 (HF convention). */
+int megakernel_op_rope(const float* x, const int* pos, float* y, int n_heads, int head_dim, int n_in, int n_out,
+                       int reps, float theta);
+
+/* lm_head_argmax_phase1/2 (src/sampling.cuh:32-117): logits = E h, token =
+ * argmax with the lowest index on ties.  w: MK_OP_LAYOUT_TILE [vocab][k],
+ * k in {256, 512, 1024}; h [n_in][k]; logits [n_out][vocab] or NULL; keys
+ * [n_out] (workspace, left holding ordered(logit) << 32 | ~index); tokens
+ * [n_out]. */
+int megakernel_op_lmhead_argmax(const void* w, long long copy_bytes, int n_copies, int vocab, int k, const float* h,
+                                int n_in, float* logits, unsigned long long* keys, int* tokens, int n_out,
+                                int reps);
+
+/* Device time of this thread's last megakernel_op_* call (ms). */
+float megakernel_op_last_ms(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,16 @@ SIGNATURES = {
     "megakernel_generate_batch": (c_int, [c_void_p, P_int, c_int, P_int]),
     "megakernel_batch_debug_logits": (c_int, [c_void_p, P_int, P_int, P_float]),
     "megakernel_batch_last_ms": (c_float, [c_void_p]),
+    # operator microbench
+    "megakernel_op_packed_bytes": (c_ll, [c_int, c_int]),
+    "megakernel_op_pack": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p]),
+    "megakernel_op_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float]),
+    "megakernel_op_gemv": (c_int, [c_void_p, c_ll, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int,
+                                   c_void_p, c_int, c_int]),
+    "megakernel_op_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "megakernel_op_lmhead_argmax": (c_int, [c_void_p, c_ll, c_int, c_int, c_int, c_void_p, c_int, c_void_p,
+                                            c_void_p, c_void_p, c_int, c_int]),
+    "megakernel_op_last_ms": (c_float, []),
 }
 
 PRESET_BASELINE, PRESET_QWEN3_06B, PRESET_TINY = 0, 1, 2

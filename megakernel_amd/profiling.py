@@ -4,6 +4,9 @@ Two jobs, both on files rocprofv3 wrote (``--output-format csv``):
 
 * ``stats``: turn ``*_kernel_stats.csv`` into a short text table (the form
   kept under ``profiles/``), prefixed with the command that produced it;
+* ``launches``: per-launch durations from ``*_kernel_trace.csv``, grouped by
+  kernel and grid size (the operator microbench launches each op kernel both
+  with many instances and with one);
 * ``traffic``: combine four ``--pmc`` runs -- FETCH_SIZE and WRITE_SIZE of the
   decode launch, and the same two counters of a plain device copy of known
   size -- into HBM bytes per decode launch.  Each counter is scaled by
@@ -13,6 +16,7 @@ Two jobs, both on files rocprofv3 wrote (``--output-format csv``):
 
 Usage:
   python -m megakernel_amd.profiling stats STATS.csv --command "..." -o OUT.txt
+  python -m megakernel_amd.profiling launches TRACE.csv --match mk::ops:: --command "..." -o OUT.txt
   python -m megakernel_amd.profiling traffic --decode-fetch A.csv --decode-write B.csv \
       --copy-fetch C.csv --copy-write D.csv --copy-bytes N --ctx 1024 --tokens 256 \
       --algorithmic-bytes X -o profiles/decode_traffic.json
@@ -67,6 +71,28 @@ def stats_text(path: str, cmd: str, top: int = 8) -> str:
     return "\n".join(lines) + "\n"
 
 
+def launch_text(path: str, cmd: str, substr: str) -> str:
+    """Per (kernel, grid size) launch durations from a rocprofv3
+    kernel_trace.csv, for kernels whose name contains substr: launches of one
+    kernel with different work (e.g. many instances vs one) have different
+    grids, so each group is one kind of launch."""
+    groups: dict[tuple[str, int], list[float]] = {}
+    for r in _rows(path):
+        name = r.get("Kernel_Name", "")
+        if substr not in name:
+            continue
+        grid = int(r.get("Grid_Size_X", 0)) // max(1, int(r.get("Workgroup_Size_X", 1)))
+        dur = (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) / 1e3
+        groups.setdefault((name, grid), []).append(dur)
+    lines = [f"# command: {cmd}", f"# launches of kernels matching '{substr}', grouped by grid (workgroups)", "",
+             f"{'kernel':60s} {'grid':>6s} {'calls':>6s} {'median us':>10s} {'min us':>10s} {'max us':>10s}"]
+    for (name, grid), d in sorted(groups.items(), key=lambda kv: (kv[0][0], -kv[0][1])):
+        short = name if len(name) <= 60 else name[:57] + "..."
+        lines.append(f"{short:60s} {grid:6d} {len(d):6d} {statistics.median(d):10.2f} {min(d):10.2f} "
+                     f"{max(d):10.2f}")
+    return "\n".join(lines) + "\n"
+
+
 def traffic(args) -> dict:
     dec_f = counter_values(args.decode_fetch, "FETCH_SIZE", DECODE_KERNEL)
     dec_w = counter_values(args.decode_write, "WRITE_SIZE", DECODE_KERNEL)
@@ -103,6 +129,12 @@ def main(argv=None):
     s.add_argument("csv")
     s.add_argument("--command", required=True, help="the command that produced the csv")
     s.add_argument("-o", "--out")
+    s.add_argument("--top", type=int, default=8, help="kernels listed")
+    ln = sub.add_parser("launches")
+    ln.add_argument("csv", help="kernel_trace.csv")
+    ln.add_argument("--command", required=True)
+    ln.add_argument("--match", required=True, help="substring of the kernel names to list")
+    ln.add_argument("-o", "--out")
     t = sub.add_parser("traffic")
     for k in ("decode-fetch", "decode-write", "copy-fetch", "copy-write"):
         t.add_argument(f"--{k}", required=True)
@@ -114,7 +146,13 @@ def main(argv=None):
     t.add_argument("-o", "--out", required=True)
     a = ap.parse_args(argv)
     if a.what == "stats":
-        txt = stats_text(a.csv, a.command)
+        txt = stats_text(a.csv, a.command, a.top)
+        if a.out:
+            with open(a.out, "w") as f:
+                f.write(txt)
+        sys.stdout.write(txt)
+    elif a.what == "launches":
+        txt = launch_text(a.csv, a.command, a.match)
         if a.out:
             with open(a.out, "w") as f:
                 f.write(txt)

@@ -84,3 +84,30 @@ def test_null_handle_errors_are_reported(clib):
     assert clib.megakernel_grid_size(None) == -1
     clib.megakernel_reset(None)  # no-ops, as in the reference
     clib.megakernel_free(None)
+
+
+def test_op_argument_checks(clib):
+    """The operator-microbench entry points reject bad arguments before any
+    GPU work (the pointers below are never dereferenced)."""
+    fake = 0x10000
+    assert clib.megakernel_op_packed_bytes(16, 1024) == 16 * 1024 * 2
+    assert clib.megakernel_op_packed_bytes(15, 1024) == -1
+    assert clib.megakernel_op_pack(None, 16, 256, 0, fake) == -1
+    assert "null" in _lib.last_error(clib)
+    assert clib.megakernel_op_pack(fake, 16, 100, 0, fake) == -1  # row-pair needs k % 256
+    assert clib.megakernel_op_pack(fake, 16, 256, 7, fake) == -1
+    assert "layout" in _lib.last_error(clib)
+    assert clib.megakernel_op_pack(fake, 48, 256, 2, fake) == -1  # gate/up needs rows % 32
+    assert clib.megakernel_op_rmsnorm(fake, fake, fake, 1000, 1, 1, 1, 1e-6) == -1
+    assert clib.megakernel_op_rmsnorm(fake, fake, fake, 1024, 0, 1, 1, 1e-6) == -1
+    assert "n_in" in _lib.last_error(clib)
+    assert clib.megakernel_op_gemv(fake, 0, 1, 2048, 1000, 0, fake, None, 1, fake, 1, 1) == -1
+    assert clib.megakernel_op_gemv(fake, 0, 1, 1024, 2816, 1, fake, None, 1, fake, 1, 1) == -1
+    assert "res" in _lib.last_error(clib)
+    assert clib.megakernel_op_gemv(fake, 1024, 2, 2048, 1024, 0, fake, None, 1, fake, 1, 1) == -1
+    assert "copy_bytes" in _lib.last_error(clib)
+    assert clib.megakernel_op_gemv(fake, 0, 1, 2048, 1024, 5, fake, None, 1, fake, 1, 1) == -1
+    assert clib.megakernel_op_rope(fake, fake, fake, 24, 32, 1, 1, 1, 1e6) == -1
+    assert clib.megakernel_op_lmhead_argmax(fake, 0, 1, 151936, 2048, fake, 1, None, fake, fake, 1, 1) == -1
+    assert clib.megakernel_op_lmhead_argmax(fake, 0, 1, 100, 1024, fake, 1, None, fake, fake, 1, 1) == -1
+    assert clib.megakernel_op_lmhead_argmax(fake, 0, 1, 4096, 1024, fake, 1, None, None, fake, 1, 1) == -1
