@@ -56,6 +56,9 @@ def parse():
                     help="BASELINE configs[1] instead: the operator microbench (each op of a decode step as its "
                          "own launch, repeated in-kernel over >= 512 MiB of rotating weight / input copies)")
     ap.add_argument("--ops-rotate-mib", type=int, default=512, help="size of the rotated copies per op")
+    ap.add_argument("--prefill", type=int, default=0,
+                    help="prefill instead: consume a prompt of this many tokens (from an empty cache) with "
+                         "megakernel_batch_prefill, 16 tokens per weight pass")
     return ap.parse_args()
 
 
@@ -357,10 +360,84 @@ def bench_ops(args):
     print(json.dumps(out))
 
 
+def bench_prefill(args):
+    """Prefill of an N-token prompt (uniform random ids from the seed) into an
+    empty cache with megakernel_batch_prefill: chunks of 16 tokens, each one
+    pass over the layer weights with its tokens as the matrix columns, the LM
+    head once for the next token.  Timed: --reps calls after one warm-up (the
+    position reset to 0 before each), median; inputs resident in HBM.
+    Algorithmic bytes: layer weights once per chunk, the KV read of every
+    token's causal prefix and its append, the LM head once.  Beside it: the
+    same prompt fed token by token through the batch-1 decode kernel (the
+    reference's prefill-by-decode, host/bridge.py:136-163)."""
+    import numpy as np
+
+    from megakernel_amd import launcher
+    from megakernel_amd.batch import BatchEngine
+    from megakernel_amd.bridge import MegakernelEngine
+    from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
+    from megakernel_amd.weights import DeviceWeights
+
+    shape, N = BASELINE, args.prefill
+    rng = np.random.default_rng(args.seed)
+    prompt = [int(t) for t in rng.integers(0, shape.vocab, size=N)]
+    dw = DeviceWeights(shape, args.seed, std=0.02, gain_std=0.0)
+    eng = BatchEngine(dw, 1, N + 16, shape)
+    info = launcher.detect_gpu()
+    eng.prefill(0, prompt)  # warm-up
+    walls, kernels, toks = [], [], []
+    for r in range(args.reps):
+        eng.set_pos(0, 0)
+        eng.lib.megakernel_sync()
+        t0 = time.perf_counter()
+        toks.append(eng.prefill(0, prompt))
+        walls.append(time.perf_counter() - t0)
+        kernels.append(eng.last_ms / 1e3)
+        print(f"# rep {r}: wall {walls[-1] * 1e3:.2f} ms device {kernels[-1] * 1e3:.2f} ms -> "
+              f"{N / walls[-1]:.0f} tok/s; next token {toks[-1]}", file=sys.stderr, flush=True)
+    eng.close()
+    # the same prompt token by token through the batch-1 decode kernel
+    one = MegakernelEngine(shape=shape, max_seq=N + 16, device_weights=dw)
+    one.decode_many(prompt[0], 8)
+    one.reset()
+    eng_t0 = time.perf_counter()
+    for t in prompt:
+        one.decode_token(t)
+    one.lib.megakernel_sync()
+    by_decode = N / (time.perf_counter() - eng_t0)
+    one.close()
+    dw.free()
+    wall, kern = statistics.median(walls), statistics.median(kernels)
+    nchunks = (N + 15) // 16
+    nbytes = (nchunks * shape.n_layers * shape.layer_weight_bytes + 2 * shape.vocab * shape.hidden +
+              2 * shape.hidden + sum(shape.kv_bytes_per_pos * (p + 2) for p in range(N)))
+    achieved = nbytes / kern / 1e9
+    out = {
+        "metric": f"prefill tok/s ({N}-token prompt, empty cache)",
+        "value": round(N / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": N, "warmup": 1,
+        "ms_per_step": round(wall * 1e3 / N, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"Qwen3-0.6B-shaped prefill of a {N}-token prompt in chunks of 16 "
+                               "(megakernel_batch_prefill)", "prompt": N, "chunks": nchunks,
+                   "device": info["name"], "reps": args.reps},
+        "prefill_by_decode_tok_s": round(by_decode, 1),
+        "next_token": toks[-1],
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.prefill:
+        if args.gpus != 1:
+            print(json.dumps({"error": "this build runs on one GPU only"}))
+            sys.exit(2)
+        bench_prefill(args)
         return
     if args.ops:
         if args.gpus != 1:
@@ -376,7 +453,7 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the batch-1 decode path does not "
-                                   "shard (see DESIGN.md); run with --gpus 1"}))
+                                   "shard across GPUs; run with --gpus 1"}))
         sys.exit(2)
     from megakernel_amd import launcher
     from megakernel_amd.bridge import MegakernelEngine

@@ -152,8 +152,8 @@ int megakernel_memcpy(void* dst, const void* src, unsigned long long nbytes, int
 int megakernel_device_info(int* cus, int* wall_clock_khz, char* name, int name_len);
 
 /* ---- batched decode ------------------------------
- * SURVEY's boundary lists megakernel_decode_batch as the additive entry point
- * of the 16-sequence configuration; the reference has no batched path (its
+ * megakernel_decode_batch is the additive entry point of the 16-sequence
+ * configuration; the reference has no batched path (its
  * engine decodes one sequence, src/megakernel.cu:377-413).  A batch handle
  * holds its own weight copy (matrix-core tile layout) and n_seq KV caches;
  * every call advances all n_seq sequences by one greedy step per step.
@@ -192,7 +192,17 @@ int megakernel_generate_batch(void* handle, const int* first_tokens, int n_steps
  * (logits: host float[n_seq * vocab]).  Validation only. */
 int megakernel_batch_debug_logits(void* handle, const int* tokens_in, int* tokens_out, float* logits);
 
-/* Device time of the last megakernel_generate_batch / decode_batch call (ms). */
+/* Prefill (the reference feeds a prompt token by token
+ * through its decode, host/bridge.py:136-163): the n prompt tokens of
+ * sequence seq are consumed at positions pos .. pos + n - 1 in chunks of up
+ * to 16, each chunk one pass over the weights with its tokens as the matrix
+ * columns; token i attends causally to the cache and to tokens < i.  Their
+ * K / V are appended, the position advances by n, *next_token (may be NULL)
+ * receives the greedy token after the last prompt token and logits (may be
+ * NULL; host float[vocab]) its fp32 logits.  Returns 0 or -1. */
+int megakernel_batch_prefill(void* handle, int seq, const int* tokens, int n, int* next_token, float* logits);
+
+/* Device time of the last megakernel_generate_batch / decode_batch / prefill call (ms). */
 float megakernel_batch_last_ms(void* handle);
 
 /* ---- operator microbench ---------------------------

@@ -84,6 +84,19 @@ class BatchEngine:
             self._handle, self._ints(tokens), out, logits.ctypes.data_as(_lib.P_float)), "batch_debug_logits")
         return list(out), logits
 
+    def prefill(self, seq: int, tokens, with_logits: bool = False):
+        """Consume a prompt for sequence seq at its position (chunks of 16
+        tokens, one weight pass each); returns the greedy next token, and its
+        fp32 logits [vocab] when with_logits."""
+        toks = [int(t) for t in tokens]
+        arr = (ctypes.c_int * max(1, len(toks)))(*toks)
+        nxt = ctypes.c_int(-1)
+        logits = np.empty(self.shape.vocab, dtype=np.float32) if with_logits else None
+        _lib.check(self.lib, self.lib.megakernel_batch_prefill(
+            self._handle, seq, arr, len(toks), ctypes.byref(nxt),
+            logits.ctypes.data_as(_lib.P_float) if with_logits else None), "batch_prefill")
+        return (nxt.value, logits) if with_logits else nxt.value
+
     @property
     def last_ms(self) -> float:
         return float(self.lib.megakernel_batch_last_ms(self._handle))

@@ -30,7 +30,7 @@ class ModelShape:
     def with_(self, **kw) -> "ModelShape":
         return replace(self, **kw)
 
-    # ---- byte accounting (algorithmic bytes; SURVEY/BASELINE definitions) ----
+    # ---- byte accounting (algorithmic bytes: weights once + KV read + KV write per token) ----
     @property
     def layer_weight_bytes(self) -> int:
         q, kv = self.n_q_heads * self.head_dim, self.n_kv_heads * self.head_dim

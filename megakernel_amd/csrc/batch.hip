@@ -26,8 +26,12 @@ struct BHandle {
   hipGraphExec_t exec = nullptr;
   float last_ms = 0.f;
   BParams p{};
+  // prefill: the prompt's tokens and positions (max_seq entries each), and
+  // the token / step outputs of its last chunk (kept apart from the decode's)
+  int *pf_tok = nullptr, *pf_pos = nullptr, *pf_out = nullptr, *pf_step = nullptr;
   std::vector<void*> owned;
   int (*launch_step)(BHandle*, const BParams&) = nullptr;
+  int (*launch_prefill)(BHandle*, const BParams&, bool) = nullptr;
 };
 
 static void free_all(BHandle* h) {
@@ -82,11 +86,36 @@ static int launch_step(BHandle* h, const BParams& p) {
   return 0;
 }
 
+// One prefill chunk (p.B <= 16 consecutive prompt tokens of one sequence as
+// the columns): the decode step's kernels with bk_append storing every
+// column's K / V before each layer's attention; the LM head and the token
+// only for the prompt's last chunk.
+template <class S>
+static int launch_prefill(BHandle* h, const BParams& p, bool last) {
+  const int L = h->L;
+  hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
+  for (int l = 0; l < L; ++l) {
+    hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_append<S>, dim3(BMAX * S::NKV), dim3(2 * kWave), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_attn<S>, dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16 * KS_O), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
+  }
+  if (last) {
+    hipLaunchKernelGGL(bk_lm<S>, dim3(h->G), dim3(GT), 0, h->stream, p);
+    hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
+  }
+  HIPCHK(hipGetLastError(), -1);
+  return 0;
+}
+
 template <class S>
 static void set_shape(BHandle* h) {
   h->H = S::H, h->QD = S::QD, h->KVD = S::KVD, h->QKV = S::QKV, h->F = S::F, h->D = S::D, h->NKV = S::NKV;
   h->norm_stride = S::NORM_STRIDE;
   h->launch_step = launch_step<S>;
+  h->launch_prefill = launch_prefill<S>;
 }
 
 static int init_state(BHandle* h, const char* base, const long long* off, int n_off) {
@@ -164,7 +193,9 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
                              256 * 4 + (size_t)(h->H / 16) * (KS_O > KS_DN ? KS_O : KS_DN) * 256 * 4) ||
       alloc(h, &p.tok, (size_t)BMAX * 4) || alloc(h, &p.pos, (size_t)BMAX * 4) ||
       alloc(h, &p.out, (size_t)h->max_steps * BMAX * 4) || alloc(h, &p.step, 64) ||
-      alloc(h, &p.dbg_logits, (size_t)BMAX * h->V * 4))
+      alloc(h, &p.dbg_logits, (size_t)BMAX * h->V * 4) || alloc(h, &h->pf_tok, (size_t)h->S * 4) ||
+      alloc(h, &h->pf_pos, (size_t)h->S * 4) || alloc(h, &h->pf_out, (size_t)BMAX * 4) ||
+      alloc(h, &h->pf_step, 64))
     return -1;
   std::vector<float> invf(h->D / 2);
   for (int i = 0; i < h->D / 2; ++i) invf[i] = 1.0f / powf((float)kRopeTheta, (float)(2 * i) / (float)h->D);
@@ -173,6 +204,7 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
   HIPCHK(hipMemcpyAsync(inv, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, h->stream), -1);
   p.inv_freq = inv;
   p.B = h->B, p.L = L, p.V = h->V;
+  p.prefill = 0;
   HIPCHK(hipStreamSynchronize(h->stream), -1);
   return 0;
 }
@@ -265,6 +297,60 @@ static int run_steps(BHandle* h, const int* first, int n, int* out) {
     for (int i = 0; i < n; ++i)
       for (int b = 0; b < h->B; ++b) out[(size_t)i * h->B + b] = all[(size_t)i * BMAX + b];
   }
+  return 0;
+}
+
+// Prefill n prompt tokens of sequence seq at its position: chunks of up to 16
+// tokens, each one pass over the weights with the tokens as MFMA columns.
+static int run_prefill(BHandle* h, int seq, const int* tokens, int n, int* next_token, float* logits) {
+  if (seq < 0 || seq >= h->B || n < 1) {
+    set_err("prefill: sequence %d outside [0, %d) or n = %d < 1", seq, h->B, n);
+    return -1;
+  }
+  int pos0 = 0;
+  HIPCHK(hipMemcpy(&pos0, h->p.pos + seq, 4, hipMemcpyDeviceToHost), -1);
+  if ((long long)pos0 + n > h->S) {
+    set_err("prefill: sequence %d position %d + %d tokens exceeds KV capacity %d", seq, pos0, n, h->S);
+    return -1;
+  }
+  std::vector<int> t(n), q(n);
+  for (int i = 0; i < n; ++i) {
+    if (tokens[i] < 0 || tokens[i] >= h->V) {
+      set_err("prefill: token %d = %d outside [0, %d)", i, tokens[i], h->V);
+      return -1;
+    }
+    t[i] = tokens[i];
+    q[i] = pos0 + i;
+  }
+  HIPCHK(hipMemcpyAsync(h->pf_tok, t.data(), (size_t)n * 4, hipMemcpyHostToDevice, h->stream), -1);
+  HIPCHK(hipMemcpyAsync(h->pf_pos, q.data(), (size_t)n * 4, hipMemcpyHostToDevice, h->stream), -1);
+  HIPCHK(hipMemsetAsync(h->pf_step, 0, 4, h->stream), -1);
+  HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
+  for (int c0 = 0; c0 < n; c0 += BMAX) {
+    const int cnt = n - c0 < BMAX ? n - c0 : BMAX;
+    const bool last = c0 + cnt == n;
+    BParams pp = h->p;
+    pp.kv = h->p.kv + seq * h->p.kv_seq;  // every column writes and reads this sequence's cache
+    pp.kvt = h->p.kvt + seq * h->p.kv_seq;
+    pp.kv_seq = 0;
+    pp.prefill = 1;
+    pp.B = cnt;
+    pp.tok = h->pf_tok + c0;
+    pp.pos = h->pf_pos + c0;
+    pp.out = h->pf_out;
+    pp.step = h->pf_step;
+    pp.dbg_logits = last && logits ? h->p.dbg_logits : nullptr;
+    if (h->launch_prefill(h, pp, last)) return -1;
+  }
+  HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  HIPCHK(hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1), -1);
+  const int lastcol = (n - 1) % BMAX;
+  if (next_token) HIPCHK(hipMemcpy(next_token, h->pf_out + lastcol, 4, hipMemcpyDeviceToHost), -1);
+  if (logits)
+    HIPCHK(hipMemcpy(logits, h->p.dbg_logits + (size_t)lastcol * h->V, (size_t)h->V * 4, hipMemcpyDeviceToHost), -1);
+  const int pend = pos0 + n;
+  HIPCHK(hipMemcpy(h->p.pos + seq, &pend, 4, hipMemcpyHostToDevice), -1);
   return 0;
 }
 
@@ -415,6 +501,15 @@ int megakernel_batch_debug_logits(void* handle, const int* tokens_in, int* token
     for (int b = 0; b < h->B; ++b) tokens_out[b] = t[b];
   }
   return 0;
+}
+
+int megakernel_batch_prefill(void* handle, int seq, const int* tokens, int n, int* next_token, float* logits) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !tokens) {
+    mk::set_err("null handle or tokens");
+    return -1;
+  }
+  return mk::batch::run_prefill(h, seq, tokens, n, next_token, logits);
 }
 
 float megakernel_batch_last_ms(void* handle) {

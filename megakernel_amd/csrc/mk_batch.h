@@ -80,6 +80,8 @@ struct BParams {
   const float* inv_freq;    // [D/2]
   float* rope;              // [BMAX][2][D/2] cos / sin of the step's position per sequence
   int B, L, V, nsplit_max, max_steps;
+  int prefill;              // 1: the columns are consecutive prompt tokens of one sequence whose
+                            //    K / V bk_append has already stored (kv_seq = 0, shared cache)
 };
 
 // ------------------------------------------------------------ helpers
@@ -479,6 +481,38 @@ __global__ void bk_tok(BParams p) {
   if (b == 0) *p.step = s + 1;
 }
 
+// ------------------------------------------------------------ prefill
+// K / V of every column's position stored before the layer's attention reads
+// the cache: in a prefill the columns are consecutive prompt tokens of ONE
+// sequence (shared cache), and column b attends to the positions of columns
+// < b, which no bk_attn item of the same launch may still be writing.  Same
+// arithmetic as bk_attn's prologue: k = RoPE(k_norm(k)), both stored as bf16
+// (reference kv_cache.cuh:58-78).  One workgroup per (column, kv head): wave
+// 0 stores k, wave 1 stores v.
+template <class S>
+__global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
+  static_assert(S::D == kWave, "one lane per head dimension");
+  constexpr int D = S::D, NKV = S::NKV;
+  const int b = blockIdx.x / NKV, g = blockIdx.x % NKV;
+  if (b >= p.B) return;
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  const int pos = p.pos[b];
+  const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
+  float v = p.qkv[(long long)b * S::QKV + (w == 0 ? S::QD + g * D : S::QD + S::KVD + g * D) + l];
+  if (w == 0) {
+    const float ss = wave_sum(v * v);
+    v = v * rsqrtf(ss / (float)D + kRmsEps) *
+        bf16_to_f32(p.norms[(long long)layer * S::NORM_STRIDE + S::NORM_K + l]);
+    const float partner = lane_xor32(v);
+    const int d = l & 31;
+    const float c = p.rope[(b * 2 + 0) * (D / 2) + d], sn = p.rope[(b * 2 + 1) * (D / 2) + d];
+    v = l < 32 ? v * c - partner * sn : v * c + partner * sn;
+    p.kv[kbase + (long long)pos * D + l] = f32_to_bf16(v);
+  } else {
+    p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = f32_to_bf16(v);
+  }
+}
+
 // ------------------------------------------------------------ attention
 // One item = (sequence b, kv head g, split s) of CH positions; wave w takes
 // the 32-position block 4 s + w.  Both products of a block run on the matrix
@@ -536,7 +570,7 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   const float* src = p.qkv + (long long)b * S::QKV +
                      (w < 2 ? (g * 2 + w) * D : (w == 2 ? S::QD + g * D : S::QD + S::KVD + g * D));
   float v = src[l];
-  const bool own = pos >= s * CH && pos < (s + 1) * CH;
+  const bool own = !p.prefill && pos >= s * CH && pos < (s + 1) * CH;
   if (w < 3) {
     const float ss = wave_sum(v * v);
     const uint16_t* gn = p.norms + (long long)layer * S::NORM_STRIDE + (w < 2 ? S::NORM_Q : S::NORM_K);
@@ -574,8 +608,9 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   for (int q = 0; q < NBW; ++q) {
     const int t0 = 32 * (s * AW * NBW + w + AW * q);
     if (t0 >= n) break;  // uniform over the wave
-    // position pos takes K / V from LDS (this item appended them)
-    if (pos >= t0 && pos < t0 + 32) {
+    // position pos takes K / V from LDS (this item appended them; in a
+    // prefill bk_append stored them before this kernel)
+    if (!p.prefill && pos >= t0 && pos < t0 + 32) {
       const int rp = pos - t0;
       if (c16 == (rp & 15)) {
 #pragma unroll

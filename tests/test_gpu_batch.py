@@ -214,3 +214,100 @@ def test_batch_error_paths():
             eng.close()
     finally:
         dw.free()
+
+
+# ------------------------------------------------------------------ prefill
+def _prefill_case(shape, seed, prefix, prompt_len, other_len, max_seq):
+    """Sequence 1 gets a synthetic prefix of `prefix` positions and then a
+    prompt of prompt_len tokens through megakernel_batch_prefill; sequence 0
+    (other_len cached positions) must be left untouched."""
+    lengths = [other_len, prefix]
+    dw, eng, mo = _setup(shape, seed, lengths, max_seq)
+    rng = np.random.default_rng(seed)
+    prompt = [int(t) for t in rng.integers(0, shape.vocab, size=prompt_len)]
+    before0 = eng.get_kv(0, other_len)
+    _print(f"prefill prefix={prefix} prompt={prompt_len} ({(prompt_len + 15) // 16} chunks)")
+    nxt, logits = eng.prefill(1, prompt, with_logits=True)
+    ref = None
+    for t in prompt:
+        ref = mo.step(1, t)
+    err = float(np.abs(logits - ref["logits"].numpy()).max())
+    _print(f"  next token {nxt} (oracle {ref['token']}), logits max abs err {err:.2e}")
+    assert err <= LOGIT_ABS
+    if nxt != ref["token"]:
+        assert qwen3_ref.top2_margin(ref["logits"]) <= MARGIN
+    assert eng.positions() == [other_len, prefix + prompt_len]
+    # the prompt's K / V against the oracle's: layer 0 depends on each token
+    # alone (bf16 of the same fp32 values: <= 1 ulp on < 1 % of entries);
+    # deeper layers carry the earlier tokens' attention, so they are held to
+    # the per-layer bar (relative L2 <= 1e-2)
+    got = eng.get_kv(1, prefix + prompt_len)[:, :, :, prefix:, :]
+    k, v = mo.caches[1]
+    want = np.stack([k[:, :, prefix:prefix + prompt_len].contiguous().view(torch.int16).numpy(),
+                     v[:, :, prefix:prefix + prompt_len].contiguous().view(torch.int16).numpy()],
+                    axis=1).view(np.uint16)
+    diff = np.abs(got[0].astype(np.int32) - want[0].astype(np.int32))
+    assert diff.max() <= 1, f"layer-0 prompt KV bytes differ by up to {diff.max()} ulp"
+    assert (diff > 0).mean() < 0.01, f"{(diff > 0).mean():.3%} of layer-0 prompt KV entries off by 1 ulp"
+    gf, wf = synth.bf16_bits_to_f32(got), synth.bf16_bits_to_f32(want)
+    for layer in range(1, shape.n_layers):
+        rel = float(np.linalg.norm(gf[layer] - wf[layer]) / np.linalg.norm(wf[layer]))
+        _print(f"  layer {layer} prompt KV rel-L2 {rel:.2e}")
+        assert rel <= 1e-2, f"layer {layer} prompt KV rel-L2 {rel:.3e}"
+    assert np.array_equal(eng.get_kv(0, other_len), before0)
+    return dw, eng, mo, nxt
+
+
+def test_batch_prefill_tiny_multi_chunk():
+    """37 prompt tokens (chunks of 16, 16, 5) after a 40-position prefix,
+    then 3 decode steps of both sequences against the oracle."""
+    dw, eng, mo, nxt = _prefill_case(TINY, 41, prefix=40, prompt_len=37, other_len=9, max_seq=128)
+    try:
+        toks = [3, nxt]
+        for i in range(3):
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(2)]
+            worst = _check_step(logits, out, refs, f"after prefill, step {i}")
+            _print(f"  decode step {i}: worst logits abs err {worst:.2e}")
+            toks = out
+    finally:
+        eng.close()
+        dw.free()
+
+
+@pytest.mark.parametrize("prompt_len", [1, 16])
+def test_batch_prefill_tiny_edges(prompt_len):
+    """One token, and exactly one full chunk, from an empty cache."""
+    dw, eng, _, _ = _prefill_case(TINY, 42 + prompt_len, prefix=0, prompt_len=prompt_len, other_len=0,
+                                  max_seq=64)
+    eng.close()
+    dw.free()
+
+
+def test_batch_prefill_baseline_2l():
+    """BASELINE shapes (2 layers): 70 prompt tokens after a 300-position prefix
+    (chunks straddle the 256-position attention splits)."""
+    shape = BASELINE.with_(n_layers=2, vocab=4096)
+    dw, eng, _, _ = _prefill_case(shape, 43, prefix=300, prompt_len=70, other_len=17, max_seq=400)
+    eng.close()
+    dw.free()
+
+
+def test_batch_prefill_errors():
+    dw = DeviceWeights(TINY, 44)
+    eng = BatchEngine(dw, 2, 32, TINY)
+    try:
+        with pytest.raises(_lib.MegakernelError, match="exceeds KV capacity"):
+            eng.prefill(0, [1] * 33)
+        with pytest.raises(_lib.MegakernelError, match="token"):
+            eng.prefill(0, [1, TINY.vocab])
+        with pytest.raises(_lib.MegakernelError, match="sequence"):
+            eng.prefill(2, [1])
+        with pytest.raises(_lib.MegakernelError):
+            eng.prefill(0, [])
+        assert eng.positions() == [0, 0]
+        eng.prefill(0, [5] * 32)  # fills the capacity exactly
+        assert eng.positions() == [32, 0]
+    finally:
+        eng.close()
+        dw.free()

@@ -34,12 +34,12 @@ def test_byte_accounting():
     assert s.weight_bytes == 971_891_712 == weights.flat_layout(s).total_bytes
     assert s.kv_bytes_per_pos == 57_344 == 2 * 8 * 64 * 2 * 28
     assert s.token_bytes(1024) == 971_891_712 + 57_344 * 1026
-    # 8 TB/s roofline at ctx 1024 (BASELINE.md): 7,762 tok/s
+    # 8 TB/s roofline at ctx 1024: 7,762 tok/s
     assert round(8e12 / s.token_bytes(1024)) == 7762
 
 
 def test_w_o_shape_is_hidden_by_qdim():
-    # the reference's validate_shapes has it transposed; the
+    # the reference's validate_shapes has it transposed (reference host/weight_loader.py:128); the
     # matrix is [out = hidden, in = q_dim] row-major
     assert weights.tensor_dims(config.QWEN3_06B, "w_o") == (1024, 16 * 128)
 
