@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--ctx", type=int, default=1024)
     ap.add_argument("--chunk", type=int, default=0, help="minimum positions per attention work item (0: library default)")
+    ap.add_argument("--merge", type=int, default=0,
+                    help="attention splits per kv head above which the first split merges them (0: library default)")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
@@ -466,6 +468,8 @@ def main():
     eng = MegakernelEngine(shape=shape, max_seq=args.ctx + K + 8, device_weights=dw)
     if args.chunk > 0:
         eng.set_attention_chunk(args.chunk)
+    if args.merge > 0:
+        eng.set_attention_merge(args.merge)
     info = launcher.detect_gpu()
     grid = eng.grid_size
     print(f"# device {info['name']} CUs {info['cu_count']} grid {grid}", file=sys.stderr, flush=True)

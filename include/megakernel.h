@@ -128,8 +128,15 @@ float megakernel_last_kernel_ms(void* handle);
 /* Number of resident workgroups of the decode kernel (one per CU). */
 int megakernel_grid_size(void* handle);
 
-/* Minimum positions per attention work item (default 256). */
+/* Minimum positions per attention work item (default 512). */
 int megakernel_set_attention_chunk(void* handle, int chunk_min);
+
+/* Above this many attention splits per kv head (default 20: contexts beyond
+ * 10,240 positions at the default chunk) the workgroup of each head's first
+ * split merges the head's splits and the O phase reads one merged partial; at
+ * or below it every O workgroup merges the splits itself.  Tuning and testing
+ * only. */
+int megakernel_set_attention_merge(void* handle, int merge_min);
 
 /* Device fill of n bf16 values: bf16(float32(S_i - 131070) * c [+ 1.0f]),
  * S_i the Irwin-Hall(4) sum of the 16-bit fields of splitmix64(key, i). */

@@ -183,6 +183,11 @@ class MegakernelEngine:
         _lib.check(self.lib, self.lib.megakernel_set_attention_chunk(self._handle, chunk_min),
                    "set_attention_chunk")
 
+    def set_attention_merge(self, merge_min: int):
+        """Above merge_min splits per kv head the first split's workgroup merges them (default 20)."""
+        _lib.check(self.lib, self.lib.megakernel_set_attention_merge(self._handle, merge_min),
+                   "set_attention_merge")
+
     @property
     def grid_size(self) -> int:
         return self.lib.megakernel_grid_size(self._handle)

@@ -127,6 +127,7 @@ struct Handle {
   int L = 0, V = 0, S = 0;
   int max_launch_tokens = 0;
   int nsplit_max = 1, chunk_min = 256 * KVB;  // one 32-position block per wave and register set
+  int merge_min = 20;  // above this many splits per kv head the first split's workgroup merges them
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   float last_ms = 0.f;
@@ -152,18 +153,35 @@ struct Handle {
   long long kv_bytes = 0;
   int s_pad = 0;               // KV capacity rounded up to whole 32-position blocks
   uint16_t* kvt = nullptr;     // V^T region inside the kv allocation
-  hipError_t (*launch)(Handle*, const Params&) = nullptr;
+  hipError_t (*launch)(Handle*, const Params&, bool) = nullptr;
 };
 
+// lc: the launch reaches more than merge_min attention splits per kv head;
+// the debug instantiation when the launch records timestamps or validation
+// outputs
 template <class S>
-static hipError_t launch_decode(Handle* h, const Params& p) {
-  hipLaunchKernelGGL(decode_kernel<S>, dim3(h->G), dim3(NT), 0, h->stream, p);
+static hipError_t launch_decode(Handle* h, const Params& p, bool lc) {
+  const int mode = (lc ? 1 : 0) | (p.trace || p.dbg_layers || p.dbg_logits ? 2 : 0);
+  switch (mode) {
+    case 0: hipLaunchKernelGGL((decode_kernel<S, 0>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
+    case 1: hipLaunchKernelGGL((decode_kernel<S, 1>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<S, 2>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
+    default: hipLaunchKernelGGL((decode_kernel<S, 3>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
+  }
   return hipGetLastError();
 }
 
 template <class S>
 static int occupancy_ok(int* nblk) {
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(nblk, decode_kernel<S>, NT, 0) == hipSuccess;
+  int n[4] = {0, 0, 0, 0};
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[0], decode_kernel<S, 0>, NT, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[1], decode_kernel<S, 1>, NT, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[2], decode_kernel<S, 2>, NT, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[3], decode_kernel<S, 3>, NT, 0) != hipSuccess)
+    return 0;
+  *nblk = n[0];
+  for (int i = 1; i < 4; ++i) *nblk = n[i] < *nblk ? n[i] : *nblk;
+  return 1;
 }
 
 static void free_all(Handle* h) {
@@ -228,8 +246,9 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   HIPCHK(hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream), -1);
   // tagged activation words (zero = tag 0, never a valid tag)
   u64** tagged[5] = {&h->x, &h->qkv, &h->part, &h->act, &h->amax};
+  // part: the splits' partials, then one row for a long context's merged partial
   const size_t words[5] = {(size_t)s.H, (size_t)s.QKV,
-                           (size_t)h->nsplit_max * s.NKV * s.part_words, (size_t)s.F / 2,
+                           (size_t)(h->nsplit_max + 1) * s.NKV * s.part_words, (size_t)s.F / 2,
                            (size_t)2 * h->G};
   for (int i = 0; i < 5; ++i) {
     h->tagged_bytes[i] = words[i] * 8;
@@ -385,11 +404,15 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.first_token = first_token;
   p.nsplit_max = h->nsplit_max;
   p.chunk_min = h->chunk_min;
+  p.merge_min = h->merge_min;
   // the packed-pair words (part, act) carry 4-bit tags: start every launch from zeros
   HIPCHK(hipMemsetAsync(h->part, 0, h->tagged_bytes[2], h->stream), -1);
   HIPCHK(hipMemsetAsync(h->act, 0, h->tagged_bytes[3], h->stream), -1);
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
-  HIPCHK(h->launch(h, p), -1);
+  // the long-context instantiation when the launch's last token has more
+  // than merge_min splits per kv head (split counts grow with the position)
+  const bool lc = split_count(h->pos + n, h->chunk_min, h->nsplit_max) > h->merge_min;
+  HIPCHK(h->launch(h, p, lc), -1);
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
   HIPCHK(hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1), -1);
@@ -638,6 +661,16 @@ float megakernel_last_kernel_ms(void* handle) {
 int megakernel_grid_size(void* handle) {
   Handle* h = static_cast<Handle*>(handle);
   return h ? h->G : -1;
+}
+
+int megakernel_set_attention_merge(void* handle, int merge_min) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || merge_min < 1) {
+    mk::set_err("attention merge threshold %d must be >= 1", merge_min);
+    return -1;
+  }
+  h->merge_min = merge_min;
+  return 0;
 }
 
 int megakernel_set_attention_chunk(void* handle, int chunk_min) {

@@ -66,8 +66,9 @@ struct Params {
   uint16_t* kvt;              // V cache, transposed blocks [L][NKV][s_pad/32][D][32] bf16
   u64* x;                     // [H] residual stream (tagged)
   u64* qkv;                   // [QKV] projections of the current layer (tagged)
-  u64* part;                  // [nsplit_max][NKV][GQA*D/2 + GQA] attention partials (packed
-                              //   pairs): unnormalised output, then (max, sum) per q head
+  u64* part;                  // [nsplit_max + 1][NKV][part_words] attention partials (packed
+                              //   pairs): unnormalised output, then (max, sum) per q head; the
+                              //   last row holds the merged partial of a long context
   u64* act;                   // [F/2] silu(gate)*up (packed pairs)
   u64* amax;                  // [2][G] per-workgroup argmax words (token parity)
   int* out_tokens;            // [n_tokens]
@@ -83,6 +84,7 @@ struct Params {
   int n_layers, vocab, max_seq, s_pad;
   int pos0, n_tokens, first_token;
   int nsplit_max, chunk_min;
+  int merge_min;              // above this many splits the last split of a kv head merges them
   int trace_token;
 };
 
@@ -105,6 +107,7 @@ struct Smem {
   float mw[S::GQA][NW], lw[S::GQA][NW];  // attention: per-wave max / sum per q head
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
   u64 amax[NW];
+  float mrg[4][NT];                   // long-context split merge: (max, sum, out0, out1) per thread
 };
 
 // Element `col` of row `row` of a packed [R][K] matrix (K = 32 * KT).
@@ -119,6 +122,24 @@ __device__ __forceinline__ bool block_failed(int failed) {
   if (failed) wg_abort = 1;
   __syncthreads();
   return *static_cast<volatile int*>(&wg_abort) != 0;
+}
+
+// Poll a set of tagged words until they are ready, then consume them:
+// issue(w) loads every word of one round into w (all loads before any test:
+// one round trip per round), ready(w) tests it, consume(w) uses the round
+// that passed.  Returns false when the wait was abandoned.
+template <int N, class Issue, class Ready, class Consume>
+__device__ __forceinline__ bool poll_rounds(const Params& p, Issue issue, Ready ready, Consume consume) {
+  Spin sp;
+  u64 w[N];
+  while (true) {
+    issue(w);
+    if (ready(w)) {
+      consume(w);
+      return true;
+    }
+    if (!sp.step(p.err, p.timeout_ticks)) return false;
+  }
 }
 
 // ------------------------------------------------------------------ GEMV
@@ -596,7 +617,7 @@ __device__ __forceinline__ void gain_load_qk(KV<S>& r, const Params& p, int laye
 // nsplit never decreases as the position grows, so a consumer of split slot
 // s < nsplit only ever finds this layer's word or an older one with another
 // tag there.
-__device__ __forceinline__ int split_count(int n, int chunk_min, int nsplit_max) {
+__host__ __device__ __forceinline__ int split_count(int n, int chunk_min, int nsplit_max) {
   const int nbt = (n + 31) / 32;
   int ns = (n + chunk_min - 1) / chunk_min;
   ns = ns < 1 ? 1 : ns;
@@ -635,7 +656,7 @@ __device__ __forceinline__ Item att_item(int it, int n, int nkv, int chunk_min, 
 //   and, in the split that owns pos, append them to the cache (reference
 //   kv_cache.cuh:58-78; write-through agent-scope stores, read by later
 //   tokens on any XCD).
-template <class S>
+template <class S, int MODE>
 __device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm, const KV<S>& kvr, int layer,
                                                    int pos, int g, bool own, unsigned tg, int tt) {
   constexpr int D = S::D, GQA = S::GQA, DPL = D / kWave;
@@ -668,7 +689,7 @@ __device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm,
       }
     }
   }
-  trace_mark(p, tt, PHASES_PER_LAYER * layer + 1, 0);
+  if constexpr ((MODE & 2) != 0) trace_mark(p, tt, PHASES_PER_LAYER * layer + 1, 0);
   evt(p, tt, layer, EV_ATT_READY);
   const bool append = own && __ballot(failed) == 0ull;  // never append values of a failed wait
   const long long base = kt_base(p, layer, g, S::NKV, D);
@@ -720,17 +741,22 @@ __device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm,
   return !block_failed(failed);
 }
 
+template <class S>
+__device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit, unsigned tg);
+
 // One attention item (kv head g, split s of nsplit over positions [t0, t1)):
 // per-wave online softmax over the wave's blocks on the matrix cores, the NW
 // waves combined in LDS, and the item's partial -- unnormalised output and
 // (max, sum) per q head -- published as packed pairs for the O phase, which
-// merges the splits.  K / V of the wave's first blocks are already in kvr.
-template <class S>
+// merges the splits (MODE bit 0: beyond merge_min splits the first split's
+// workgroup merges them; without it that code is not compiled in).  K / V of
+// the wave's first blocks are already in kvr.
+template <class S, int MODE>
 __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int layer, int pos, int g, int s,
-                                  int t0, int t1, unsigned tg, int tt) {
+                                  int nsplit, int t0, int t1, unsigned tg, int tt) {
   constexpr int D = S::D, GQA = S::GQA, KC = KV<S>::KC, DT = KV<S>::DT;
   static_assert(GQA <= 4, "q heads of a group fit the 16 MFMA rows (4 per head)");
-  if (!attention_prologue<S>(p, sm, kvr, layer, pos, g, t0 <= pos && pos < t1, tg, tt)) return false;
+  if (!attention_prologue<S, MODE>(p, sm, kvr, layer, pos, g, t0 <= pos && pos < t1, tg, tt)) return false;
   evt(p, tt, layer, EV_ATT_ROPE);
   const int tid = ltid(), w = tid / kWave;
   const float scale = 1.0f / sqrtf((float)D);
@@ -870,7 +896,79 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
     if ((2 * pi) % D == 0) ll_put(dst + NPAIR + j, pk_pack(M, ls, t4));
   }
   evt(p, tt, layer, EV_ATT_PARTIAL);
+  if constexpr ((MODE & 1) != 0) {
+    if (nsplit > p.merge_min && s == 0) return attention_merge<S>(p, sm, g, nsplit, tg);
+  }
   return true;
+}
+
+// Long contexts: many splits per kv head would make every O workgroup read
+// and merge all of them (hot lines, several rounds), so the workgroup of
+// split 0 of head g waits for the head's other partials, merges them once and
+// publishes one merged partial (the row after the splits) for the O phase.
+// Each thread reads its output pair from every SGN-th split in one load
+// round; the SGN split groups are combined in LDS.  Same log-sum-exp merge as
+// the O phase's.
+template <class S>
+__device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit, unsigned tg) {
+  constexpr int NPAIR = S::GQA * S::D / 2, WP = part_words<S>();
+  constexpr int SGN = NT / NPAIR, PER = NSPLIT_CAP / SGN;
+  static_assert(NT % NPAIR == 0 && NSPLIT_CAP % SGN == 0, "split groups tile the workgroup");
+  const int tid = ltid();
+  const unsigned t4 = tag4(tg + 1u);
+  const int pi = tid % NPAIR, sg = tid / NPAIR, j = (2 * pi) / S::D;
+  int failed = 0;
+  float M = -INFINITY, o0 = 0.f, o1 = 0.f, L = 0.f;
+  const bool ok = poll_rounds<2 * PER>(
+      p,
+      [&](u64(&w)[2 * PER]) {  // splits past nsplit re-read split 0
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const int sp = sg + u * SGN < nsplit ? sg + u * SGN : 0;
+          const u64* src = p.part + ((long long)sp * S::NKV + g) * WP;
+          w[2 * u] = ll_get(const_cast<u64*>(src) + pi);
+          w[2 * u + 1] = ll_get(const_cast<u64*>(src) + NPAIR + j);
+        }
+      },
+      [&](const u64(&w)[2 * PER]) {
+        bool ready = true;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) ready &= pk_ready(w[2 * u], t4) && pk_ready(w[2 * u + 1], t4);
+        return ready;
+      },
+      [&](const u64(&w)[2 * PER]) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) M = sg + u * SGN < nsplit ? fmaxf(M, pk_lo(w[2 * u + 1])) : M;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const bool on = sg + u * SGN < nsplit;
+          const float f = __expf(pk_lo(w[2 * u + 1]) - M);
+          o0 = on ? fmaf(f, pk_lo(w[2 * u]), o0) : o0;
+          o1 = on ? fmaf(f, pk_hi(w[2 * u]), o1) : o1;
+          L = on ? fmaf(f, pk_hi(w[2 * u + 1]), L) : L;
+        }
+      });
+  if (!ok) failed = 1;
+  sm.mrg[0][tid] = M, sm.mrg[1][tid] = L, sm.mrg[2][tid] = o0, sm.mrg[3][tid] = o1;
+  __syncthreads();
+  if (tid < NPAIR) {
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SGN; ++k) Mx = fmaxf(Mx, sm.mrg[0][tid + k * NPAIR]);  // group 0 always has split 0
+    float a0 = 0.f, a1 = 0.f, ls = 0.f;
+#pragma unroll
+    for (int k = 0; k < SGN; ++k) {
+      const int i = tid + k * NPAIR;
+      const float f = sm.mrg[0][i] == -INFINITY ? 0.f : __expf(sm.mrg[0][i] - Mx);
+      a0 = fmaf(f, sm.mrg[2][i], a0);
+      a1 = fmaf(f, sm.mrg[3][i], a1);
+      ls = fmaf(f, sm.mrg[1][i], ls);
+    }
+    u64* dst = p.part + ((long long)p.nsplit_max * S::NKV + g) * WP;
+    ll_put(dst + pi, pk_pack(a0, a1, t4));
+    if ((2 * pi) % S::D == 0) ll_put(dst + NPAIR + j, pk_pack(Mx, ls, t4));
+  }
+  return !block_failed(failed);
 }
 
 // O phase input: wait for the partials of the nsplit splits of every kv head
@@ -879,8 +977,8 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
 // running max; plus, unless xrows is null, the 16 tagged residual rows of this
 // workgroup's block.  Thread t owns output pairs t + k NT.
 template <class S>
-__device__ __forceinline__ bool fetch_attn(const Params& p, int nsplit, unsigned t4, u64* xrows, unsigned xtag,
-                                           float* dst, float* xres) {
+__device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, u64* xrows,
+                                           unsigned xtag, float* dst, float* xres) {
   constexpr int NPG = S::GQA * S::D / 2;  // pairs per kv head
   constexpr int WP = part_words<S>();
   constexpr int PPT = (S::QD / 2 + NT - 1) / NT;
@@ -907,7 +1005,7 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, int nsplit, unsigned
         for (int u = 0; u < SB; ++u) {
           wa[k][u] = wm[k][u] = 0ull;
           if (s0 + u < nsplit) {
-            u64* src = p.part + ((long long)(s0 + u) * S::NKV + g) * WP;
+            u64* src = const_cast<u64*>(part) + ((long long)(s0 + u) * S::NKV + g) * WP;
             wa[k][u] = ll_get(src + pg);
             wm[k][u] = ll_get(src + NPG + j);
           }
@@ -990,8 +1088,14 @@ __device__ __forceinline__ bool token_from_slots(const Params& p, u64* slots, un
 }
 
 // ------------------------------------------------------------------ kernel
-template <class S>
+// MODE bit 0 (LC): the launch's contexts reach more than merge_min attention
+// splits per kv head (long-context merge and deferred K/V prefetch compiled
+// in); bit 1 (DBG): per-phase timestamps and the validation outputs
+// (dbg_layers, dbg_logits) compiled in.  The host picks the instantiation per
+// launch; the plain one carries neither (fewer live scalar values).
+template <class S, int MODE>
 __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
+  constexpr bool LC = (MODE & 1) != 0, DBG = (MODE & 2) != 0;
   __shared__ Smem<S> sm;
   if (threadIdx.x == 0) wg_abort = 0;
   for (int i = threadIdx.x; i < 16 * S::D; i += NT) (&sm.qb[0][0])[i] = 0;  // unused columns stay 0
@@ -1018,7 +1122,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
 
   int tok = p.first_token;
   for (int t = 0; t < p.n_tokens; ++t) {
-    trace_begin(p, t);
+    if constexpr (DBG) trace_begin(p, t);
     const int pos = p.pos0 + t;
     const unsigned tb = p.tag_base + (unsigned)t * per_token;  // tag of this token's first phase
     if (it_qkv < S::RB_QKV) {
@@ -1038,7 +1142,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       sm.rc[tid] = cs;
       sm.rs[tid] = sn;
     }
-    if (p.dbg_layers && wg == 0)
+    if (DBG && p.dbg_layers && wg == 0)
       for (int i = tid; i < S::H; i += NT) p.dbg_layers[i] = packed_elem<S::KT_H>(p.lmhead, tok, i);
     __syncthreads();
     // attention split: nsplit <= nsplit_max items per kv head, none empty;
@@ -1049,6 +1153,9 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     const Item nxt = att_item(it_att, n + 1, S::NKV, p.chunk_min, p.nsplit_max);
     const int nsplit = cur.nsplit;
     const bool has_att = cur.on;
+    const int kv_at = !LC || nsplit <= p.merge_min
+                          ? 2
+                          : (it_gu < S::RB_F ? 4 : (it_dn < S::RB_H ? 5 : (it_o < S::RB_H ? 3 : 2)));
     if (t == 0) {
       if (has_att) {
         kv_load<S>(rkv, p, 0, cur.g, cur.t0 / 32, (cur.t1 - cur.t0 + 31) / 32, wave_id());
@@ -1076,7 +1183,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         } else {
           embed_norm<S>(p, tok, gq, sm.vec_q, sm.ssw[0], &r);
         }
-        trace_mark(p, t, slot + 0, 0);
+        if constexpr (DBG) trace_mark(p, t, slot + 0, 0);
         {  // the prefetched block
           const float y = blk_dot(rq, sm.vec_q);
           store_rows(sm.rowbuf[0], p.qkv + it_qkv * 16, y * r, tg);
@@ -1087,18 +1194,23 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           const float y = blk_dot(rq, sm.vec_q);
           if (row_owner()) ll_put(p.qkv + rb * 16 + blk_row(), ll_pack(y * r, tg));
         }
-        trace_mark(p, t, slot + 0, 1);
+        if constexpr (DBG) trace_mark(p, t, slot + 0, 1);
       }
       // ---------------- P2: attention partials (prefetch: O)
       if (it_o < S::RB_H) blk_load(ro, wl + S::OFF_O + (long long)it_o * S::KT_Q * 64);
       else blk_forget(ro);
       if (has_att) {
-        if (!attention_compute<S>(p, sm, rkv, layer, pos, cur.g, cur.s, cur.t0, cur.t1, tg, t)) return;
+        if (!attention_compute<S, MODE>(p, sm, rkv, layer, pos, cur.g, cur.s, nsplit, cur.t0, cur.t1, tg, t)) return;
         evt(p, t, layer, EV_ATT_STORED);
-        trace_mark(p, t, slot + 1, 1);
+        if constexpr (DBG) trace_mark(p, t, slot + 1, 1);
       }
-      {  // K/V of this workgroup's next item (next layer, or the next token's
-         // layer 0): a whole layer ahead, so no later poll queues behind it
+      // K/V of this workgroup's next item (next layer, or the next token's
+      // layer 0), a whole layer ahead.  Loads complete in order, so a poll
+      // issued after the prefetch waits for it: with few splits the prefetch
+      // is small and goes right after attention; with many (long contexts,
+      // every workgroup prefetching) it goes after this workgroup's last
+      // item of the layer (kv_at: 2 attention, 3 O, 4 gate/up, 5 down).
+      auto prefetch_kv = [&]() {
         const bool last = layer + 1 == L;
         const Item ni = last ? nxt : cur;
         if (ni.on && (!last || t + 1 < p.n_tokens)) {
@@ -1107,7 +1219,11 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         } else {
           kv_forget<S>(rkv);
         }
+      };
+      if constexpr (LC) {
+        if (kv_at != 2) kv_forget<S>(rkv);
       }
+      if (kv_at == 2) prefetch_kv();
       // ---------------- P3: O projection + residual (prefetch: gate/up + ffn gains)
       if (it_gu < S::RB_F) {
         const u32x4* gp = wl + S::OFF_GU + (long long)(2 * it_gu) * S::KT_H * 64;
@@ -1120,10 +1236,13 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         gains_forget(gf);
       }
       if (it_o < S::RB_H) {
-        if (!fetch_attn<S>(p, nsplit, tag4(tg + 1u), layer > 0 ? p.x + it_o * 16 : nullptr, tg_x, sm.vec_o,
+        // a long context's splits arrive merged (one row after the splits)
+        const bool merged = LC && nsplit > p.merge_min;
+        if (!fetch_attn<S>(p, merged ? p.part + (long long)p.nsplit_max * S::NKV * part_words<S>() : p.part,
+                           merged ? 1 : nsplit, tag4(tg + 1u), layer > 0 ? p.x + it_o * 16 : nullptr, tg_x, sm.vec_o,
                            sm.xres_o))
           return;
-        trace_mark(p, t, slot + 2, 0);
+        if constexpr (DBG) trace_mark(p, t, slot + 2, 0);
         evt(p, t, layer, EV_O_READY);
         const float y = blk_dot(ro, sm.vec_o);
         {
@@ -1132,7 +1251,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           store_rows(sm.rowbuf[1], p.x + it_o * 16, xo + y, tg + 2u);
         }
         evt(p, t, layer, EV_O_STORED);
-        trace_mark(p, t, slot + 2, 1);
+        if constexpr (DBG) trace_mark(p, t, slot + 2, 1);
       }
       for (int rb = it_o + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
         blk_load(ro, wl + S::OFF_O + (long long)rb * S::KT_Q * 64);
@@ -1144,13 +1263,14 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
         }
       }
+      if (kv_at == 3) prefetch_kv();
       // ---------------- P4: gate/up + SiLU (prefetch: down)
       if (it_dn < S::RB_H) blk_load(rd, wl + S::OFF_DOWN + (long long)it_dn * S::KT_F * 64);
       else blk_forget(rd);
       if (it_gu < S::RB_F) {
         float r;
         if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return;
-        trace_mark(p, t, slot + 3, 0);
+        if constexpr (DBG) trace_mark(p, t, slot + 3, 0);
         {  // the prefetched block pair
           const float yg = blk_dot(rg, sm.vec_g);
           const float yu = blk_dot(ru, sm.vec_g);
@@ -1166,7 +1286,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           store_rows_pk(sm.rowbuf[2], p.act + pr * 8, silu_mul(yg * r, yu * r), tag4(tg + 3u));
           __syncthreads();
         }
-        trace_mark(p, t, slot + 3, 1);
+        if constexpr (DBG) trace_mark(p, t, slot + 3, 1);
       }
       // ---------------- P5: down projection + residual (prefetch: next QKV + attn gains)
       if (layer + 1 < L && it_qkv < S::RB_QKV) {
@@ -1176,19 +1296,20 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         blk_forget(rq);
         gains_forget(gq);
       }
+      if (kv_at == 4) prefetch_kv();
       if (it_dn < S::RB_H) {
         if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x + it_dn * 16, tg + 2u, sm.vec_d, sm.xres_d)) return;
-        trace_mark(p, t, slot + 4, 0);
+        if constexpr (DBG) trace_mark(p, t, slot + 4, 0);
         evt(p, t, layer, EV_DN_READY);
         const float y = blk_dot(rd, sm.vec_d);
         {
           const int row = it_dn * 16 + blk_row();
           const float xn = sm.xres_d[blk_row()] + y;
-          if (p.dbg_layers && row_owner()) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
+          if (DBG && p.dbg_layers && row_owner()) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
           store_rows(sm.rowbuf[3], p.x + it_dn * 16, xn, tg + 4u);
         }
         evt(p, t, layer, EV_DN_STORED);
-        trace_mark(p, t, slot + 4, 1);
+        if constexpr (DBG) trace_mark(p, t, slot + 4, 1);
       }
       for (int rb = it_dn + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
         blk_load(rd, wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64);
@@ -1198,9 +1319,10 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           const int row = rb * 16 + blk_row();
           const float xn = sm.xres_d[blk_row()] + y;
           ll_put(p.x + row, ll_pack(xn, tg + 4u));
-          if (p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
+          if (DBG && p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
         }
       }
+      if (kv_at == 5) prefetch_kv();
     }
     // ---------------- final norm + tied LM head + per-workgroup argmax
     // (reference sampling.cuh:32-117)
@@ -1211,7 +1333,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       gains_load(gfin, p.final_norm);
       float rn;
       if (!fetch_norm<S>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return;
-      trace_mark(p, t, PHASES_PER_LAYER * L, 0);
+      if constexpr (DBG) trace_mark(p, t, PHASES_PER_LAYER * L, 0);
       const long long nb = p.vocab / 16;
       const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G;
       u64 best = 0ull;
@@ -1247,7 +1369,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         acc = stride_sum<16>(acc) * rn;
         if (l < 16) {
           const unsigned idx = (unsigned)(b * 16 + l);
-          if (p.dbg_logits) p.dbg_logits[idx] = acc;
+          if (DBG && p.dbg_logits) p.dbg_logits[idx] = acc;
           // key: ordered value | (IDX_MAX - idx) | tag: an unsigned max picks
           // the largest logit and, among equal logits, the lowest index
           // (torch.argmax semantics)
@@ -1267,10 +1389,10 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         for (int i = 0; i < NW; ++i) b = sm.amax[i] > b ? sm.amax[i] : b;
         ll_put(p.amax + (t & 1) * G + wg, b | (u64)tag14(tl));
       }
-      trace_mark(p, t, PHASES_PER_LAYER * L, 1);
+      if constexpr (DBG) trace_mark(p, t, PHASES_PER_LAYER * L, 1);
       __syncthreads();
     }
-    trace_end(p, t);
+    if constexpr (DBG) trace_end(p, t);
   }
   if (wg == 0) {  // the last token's id
     const int t = p.n_tokens;

@@ -81,6 +81,7 @@ def test_null_handle_errors_are_reported(clib):
     assert clib.megakernel_set_pos(None, 0) == -1
     assert clib.megakernel_generate(None, 1, 1, None) == -1
     assert clib.megakernel_set_attention_chunk(None, 64) == -1
+    assert clib.megakernel_set_attention_merge(None, 8) == -1
     assert clib.megakernel_grid_size(None) == -1
     clib.megakernel_reset(None)  # no-ops, as in the reference
     clib.megakernel_free(None)

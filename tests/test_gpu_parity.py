@@ -155,14 +155,20 @@ def test_set_get_kv_roundtrip_and_synthetic_prefill():
         dw.free()
 
 
-@pytest.mark.parametrize("ctx,chunk", [(200, 256), (1500, 64), (5000, 256), (8192, 256), (32768, 256)])
-def test_long_context_split_attention(ctx, chunk):
+@pytest.mark.parametrize("ctx,chunk,merge", [(200, 256, None), (1500, 64, None), (1500, 64, 64), (5000, 256, 4),
+                                             (8192, 256, None), (8192, 256, 8), (32768, 256, None)])
+def test_long_context_split_attention(ctx, chunk, merge):
     """Prefilled cache + multi-split attention vs the oracle (BASELINE configs[3]
-    positions 8192 and 32768 included: 32 splits of up to 32 blocks)."""
+    positions 8192 and 32768 included: 32 splits of up to 32 blocks).  Beyond
+    `merge` splits per kv head (default 20) the first split's workgroup merges
+    them and the O phase reads one merged partial; at or below it every O
+    workgroup merges the splits."""
     shape = BASELINE.with_(n_layers=2, vocab=2048)
     eng, orc, dw = make_pair(shape, 21, ctx + 8)
     try:
         eng.set_attention_chunk(chunk)
+        if merge is not None:
+            eng.set_attention_merge(merge)
         eng.fill_kv_synthetic(ctx, 77)
         ks = np.stack([synth.kv_prefill_bits(77, l, 0, ctx, shape.n_kv_heads, shape.head_dim)
                        for l in range(shape.n_layers)])
@@ -239,12 +245,14 @@ def test_error_paths():
         dw.free()
 
 
-def test_qwen3_preset_head_dim_128():
-    """The reference's own config.cuh shapes (head_dim 128, ffn 3072)."""
+@pytest.mark.parametrize("chunk", [64, 32])
+def test_qwen3_preset_head_dim_128(chunk):
+    """The reference's own config.cuh shapes (head_dim 128, ffn 3072); chunk 32
+    gives 10 splits, merged by the last split."""
     shape = QWEN3_06B.with_(n_layers=2, vocab=2048)
     eng, orc, dw = make_pair(shape, 31, 400)
     try:
-        eng.set_attention_chunk(64)
+        eng.set_attention_chunk(chunk)
         eng.fill_kv_synthetic(300, 5)
         ks = np.stack([synth.kv_prefill_bits(5, l, 0, 300, shape.n_kv_heads, shape.head_dim) for l in range(2)])
         vs = np.stack([synth.kv_prefill_bits(5, l, 1, 300, shape.n_kv_heads, shape.head_dim) for l in range(2)])
