@@ -528,6 +528,7 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   __shared__ __attribute__((aligned(16))) uint16_t kcur[D], vcur[D];   // bf16 K / V of position pos
   __shared__ float rc[D / 2], rsn[D / 2];
   __shared__ float mw[AW][2], lw[AW][2], ow[AW][2][D];
+  __shared__ float cm[AT / (2 * D)][2 * D], cl[AT / (2 * D)][2 * D], co[AT / (2 * D)][2 * D];  // split-group merge
   __shared__ int last;
   const int item = blockIdx.x;
   const int b = item / (NKV * p.nsplit_max), g = (item / p.nsplit_max) % NKV, s = item % p.nsplit_max;
@@ -700,24 +701,58 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   }
   __syncthreads();
   if (!last) return;
-  if (tid < 2 * D) {
-    const int h = tid / D;
+  // 5. the merge: thread (split group sg, output hd) reads output hd of every
+  //    SG-th split, MG splits per load round (all loads of a round issued
+  //    before any is used: one round trip, not one per split); the SG groups
+  //    are then combined in LDS
+  {
+    constexpr int SG = AT / (2 * D), MG = 8;
+    const int hd = tid % (2 * D), sg = tid / (2 * D), h = hd / D;
     const float* base = p.part + ((long long)b * NKV + g) * p.nsplit_max * PW;
-    float M = -INFINITY;
-    for (int i = 0; i < nsplit; ++i)
-      M = fmaxf(M, __hip_atomic_load(base + (long long)i * PW + 2 * D + 2 * h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    float o = 0.f, L = 0.f;
-    for (int i = 0; i < nsplit; ++i) {
-      const float* pi = base + (long long)i * PW;
-      const float f = __expf(__hip_atomic_load(pi + 2 * D + 2 * h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - M);
-      o = fmaf(f, __hip_atomic_load(pi + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), o);
-      L = fmaf(f, __hip_atomic_load(pi + 2 * D + 2 * h + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), L);
+    float M = -INFINITY, o = 0.f, L = 0.f;
+    for (int r0 = 0; r0 < nsplit; r0 += SG * MG) {
+      float mv[MG], lv[MG], ov[MG];
+#pragma unroll
+      for (int u = 0; u < MG; ++u) {
+        const int i = r0 + sg + SG * u;
+        const float* pi = base + (long long)(i < nsplit ? i : 0) * PW;
+        mv[u] = __hip_atomic_load(pi + 2 * D + 2 * h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lv[u] = __hip_atomic_load(pi + 2 * D + 2 * h + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ov[u] = __hip_atomic_load(pi + hd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      float Mb = M;
+#pragma unroll
+      for (int u = 0; u < MG; ++u) Mb = r0 + sg + SG * u < nsplit ? fmaxf(Mb, mv[u]) : Mb;
+      const float sc = M == -INFINITY ? 0.f : __expf(M - Mb);  // o, L are 0 while M is -inf
+      o *= sc, L *= sc;
+#pragma unroll
+      for (int u = 0; u < MG; ++u) {
+        const bool on = r0 + sg + SG * u < nsplit;  // select: skipped words hold anything
+        const float f = __expf(mv[u] - Mb);
+        o = on ? fmaf(f, ov[u], o) : o;
+        L = on ? fmaf(f, lv[u], L) : L;
+      }
+      M = Mb;
     }
-    uint16_t hi, lo;
-    split2(o / L, hi, lo);
-    const long long k = (long long)b * S::QD + g * 2 * D + tid;
-    p.att[k] = hi;
-    p.att[(long long)BMAX * S::QD + k] = lo;
+    cm[sg][hd] = M, cl[sg][hd] = L, co[sg][hd] = o;
+    __syncthreads();
+    if (tid < 2 * D) {
+      float Mx = cm[0][tid];  // group 0 holds split 0
+#pragma unroll
+      for (int k = 1; k < SG; ++k) Mx = fmaxf(Mx, cm[k][tid]);
+      float oo = 0.f, ll = 0.f;
+#pragma unroll
+      for (int k = 0; k < SG; ++k) {
+        const float f = cm[k][tid] == -INFINITY ? 0.f : __expf(cm[k][tid] - Mx);
+        oo = fmaf(f, co[k][tid], oo);
+        ll = fmaf(f, cl[k][tid], ll);
+      }
+      uint16_t hi, lo;
+      split2(oo / ll, hi, lo);
+      const long long k = (long long)b * S::QD + g * 2 * D + tid;
+      p.att[k] = hi;
+      p.att[(long long)BMAX * S::QD + k] = lo;
+    }
   }
 }
 
