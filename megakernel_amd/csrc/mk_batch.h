@@ -33,7 +33,11 @@ namespace batch {
 constexpr int BMAX = 16;       // sequences per step (MFMA columns)
 constexpr int GT = 512;        // threads of the GEMM kernels (8 waves)
 constexpr int GW = GT / kWave;
-constexpr int AT = 256;        // threads of an attention item (4 waves)
+#ifndef MK_BATCH_AT
+#define MK_BATCH_AT 256
+#endif
+constexpr int AT = MK_BATCH_AT;  // threads of an attention item (4 waves)
+static_assert(AT >= 4 * kWave, "the attention prologue takes q0, q1, k and v on waves 0-3");
 constexpr int AW = AT / kWave;
 #ifndef MK_BATCH_NBW
 #define MK_BATCH_NBW 2
@@ -590,7 +594,7 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
       kcur[l] = kb;
       if (own) p.kv[kbase + (long long)pos * D + l] = kb;  // KV append (reference kv_cache.cuh:58-78)
     }
-  } else {
+  } else if (w == 3) {
     const uint16_t vb = f32_to_bf16(v);
     vcur[l] = vb;
     if (own) p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = vb;
