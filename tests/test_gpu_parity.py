@@ -245,14 +245,16 @@ def test_error_paths():
         dw.free()
 
 
-@pytest.mark.parametrize("chunk", [64, 32])
-def test_qwen3_preset_head_dim_128(chunk):
+@pytest.mark.parametrize("chunk,merge", [(64, None), (32, 4)])
+def test_qwen3_preset_head_dim_128(chunk, merge):
     """The reference's own config.cuh shapes (head_dim 128, ffn 3072); chunk 32
-    gives 10 splits, merged by the last split."""
+    gives 10 splits, merged by the first split's workgroup (merge threshold 4)."""
     shape = QWEN3_06B.with_(n_layers=2, vocab=2048)
     eng, orc, dw = make_pair(shape, 31, 400)
     try:
         eng.set_attention_chunk(chunk)
+        if merge is not None:
+            eng.set_attention_merge(merge)
         eng.fill_kv_synthetic(300, 5)
         ks = np.stack([synth.kv_prefill_bits(5, l, 0, 300, shape.n_kv_heads, shape.head_dim) for l in range(2)])
         vs = np.stack([synth.kv_prefill_bits(5, l, 1, 300, shape.n_kv_heads, shape.head_dim) for l in range(2)])
