@@ -199,6 +199,20 @@ int megakernel_generate_batch(void* handle, const int* first_tokens, int n_steps
  * (logits: host float[n_seq * vocab]).  Validation only. */
 int megakernel_batch_debug_logits(void* handle, const int* tokens_in, int* tokens_out, float* logits);
 
+/* Prefill for a batch-1 handle (the reference's generate feeds the prompt
+ * through decode token by token, host/bridge.py:136-163).  attach builds a
+ * prefill context bound to the handle's KV cache: the batched kernels'
+ * matrix-core weight copy (a second copy of the weights) and work buffers,
+ * from the same flat device weights and offsets the handle was built from
+ * (d_weights NULL: the library's own upload, for handles made by
+ * megakernel_init_from_host).  Presets BASELINE and TINY.  prefill consumes n
+ * prompt tokens at the handle's position, 16 per weight pass (the tokens are
+ * the matrix columns, each attending causally to the cache and to the earlier
+ * prompt tokens), advances the position by n and returns the greedy token
+ * after the prompt in *next_token (may be NULL).  Both return 0 or -1. */
+int megakernel_prefill_attach(void* handle, void* d_weights, const long long* offsets, int num_offsets);
+int megakernel_prefill(void* handle, const int* tokens, int n, int* next_token);
+
 /* Prefill (the reference feeds a prompt token by token
  * through its decode, host/bridge.py:136-163): the n prompt tokens of
  * sequence seq are consumed at positions pos .. pos + n - 1 in chunks of up

@@ -7,7 +7,9 @@ benchmark_sweep, close) with three deliberate differences:
 * no torch in the product path: weights are read with numpy and uploaded by
   the library (``megakernel_init_from_host``);
 * ``generate`` prefills the prompt once (the reference prefills it twice,
-  bridge.py:136-163) and can decode all new tokens in one resident launch;
+  bridge.py:136-163) -- with ``prefill=True``, 16 prompt tokens per weight
+  pass on the matrix cores instead of one decode step per token -- and can
+  decode all new tokens in one resident launch;
 * throughput accounting counts KV bytes as well as weight bytes, from the
   model shape instead of a fixed 926e6 constant (bridge.py:229).
 
@@ -30,15 +32,18 @@ class MegakernelEngine:
 
     def __init__(self, weights_path=None, offsets_path=None, lib_path=None, tokenizer=None,
                  shape: ModelShape = BASELINE, max_seq: int | None = None,
-                 device_weights=None):
+                 device_weights=None, prefill: bool = False):
         self.tokenizer = tokenizer
         self.shape = shape
         self.lib = _lib.load(lib_path)
         self.max_seq = max_seq or 33024
+        self._prefill = False
         if device_weights is not None:
             self._init_from_device(device_weights)
         else:
             self._load_weights(weights_path, offsets_path)
+        if prefill:
+            self.attach_prefill(device_weights)
 
     # ------------------------------------------------------------ set-up
     def _load_weights(self, weights_path, offsets_path):
@@ -78,12 +83,38 @@ class MegakernelEngine:
         _lib.check(self.lib, self.lib.megakernel_generate(self._handle, int(first_token), n, out), "generate")
         return list(out)
 
+    def attach_prefill(self, device_weights=None):
+        """Build the prefill context (matrix-core weight copy bound to this
+        handle's KV cache): from device_weights, or from the library's own
+        upload when the engine was loaded from a weights file."""
+        if self._prefill:
+            return
+        if device_weights is not None:
+            arr = device_weights.layout.c_offsets()
+            rc = self.lib.megakernel_prefill_attach(self._handle, ctypes.c_void_p(device_weights.ptr), arr, len(arr))
+        else:
+            rc = self.lib.megakernel_prefill_attach(self._handle, None, None, 0)
+        _lib.check(self.lib, rc, "prefill_attach")
+        self._prefill = True
+
+    def prefill(self, token_ids) -> int:
+        """Consume prompt tokens at the current position, 16 per weight pass;
+        returns the greedy next token."""
+        ids = [int(t) for t in token_ids]
+        arr = (ctypes.c_int * max(1, len(ids)))(*ids)
+        nxt = ctypes.c_int(-1)
+        _lib.check(self.lib, self.lib.megakernel_prefill(self._handle, arr, len(ids), ctypes.byref(nxt)), "prefill")
+        return nxt.value
+
     def generate_ids(self, prompt_ids, max_tokens=100, eos_id=None, one_launch=True):
         """Greedy continuation of token ids.  Returns (generated_ids, tok/s)."""
         self.reset()
-        for tok in prompt_ids[:-1]:
-            self.decode_token(tok)
-        nxt = self.decode_token(prompt_ids[-1])
+        if self._prefill:
+            nxt = self.prefill(prompt_ids)
+        else:
+            for tok in prompt_ids[:-1]:
+                self.decode_token(tok)
+            nxt = self.decode_token(prompt_ids[-1])
         self.lib.megakernel_sync()
         start = time.perf_counter()
         generated = [nxt]

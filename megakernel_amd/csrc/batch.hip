@@ -118,7 +118,10 @@ static void set_shape(BHandle* h) {
   h->launch_prefill = launch_prefill<S>;
 }
 
-static int init_state(BHandle* h, const char* base, const long long* off, int n_off) {
+// ext_kv / ext_kvt: bind to an external single-sequence cache (a prefill
+// context of a batch-1 handle) instead of allocating BMAX caches.
+static int init_state(BHandle* h, const char* base, const long long* off, int n_off, uint16_t* ext_kv = nullptr,
+                      uint16_t* ext_kvt = nullptr) {
   if (n_off < 13 || (n_off - 2) % 11 != 0) {
     set_err("num_offsets=%d is not 2 + 11*layers", n_off);
     return -1;
@@ -173,10 +176,15 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
   h->s_pad = (h->S + 31) / 32 * 32;
   p.s_pad = h->s_pad;
   p.kv_seq = (long long)L * h->NKV * h->s_pad * h->D;
-  uint16_t* kv;
-  if (alloc(h, &kv, (size_t)2 * BMAX * p.kv_seq * 2)) return -1;
-  p.kv = kv;
-  p.kvt = kv + (long long)BMAX * p.kv_seq;
+  if (ext_kv) {
+    p.kv = ext_kv;
+    p.kvt = ext_kvt;
+  } else {
+    uint16_t* kv;
+    if (alloc(h, &kv, (size_t)2 * BMAX * p.kv_seq * 2)) return -1;
+    p.kv = kv;
+    p.kvt = kv + (long long)BMAX * p.kv_seq;
+  }
   h->nsplit_max = (h->S + CH - 1) / CH;
   p.nsplit_max = h->nsplit_max;
   h->max_steps = 1 << 16;
@@ -300,16 +308,14 @@ static int run_steps(BHandle* h, const int* first, int n, int* out) {
   return 0;
 }
 
-// Prefill n prompt tokens of sequence seq at its position: chunks of up to 16
-// tokens, each one pass over the weights with the tokens as MFMA columns.
-static int run_prefill(BHandle* h, int seq, const int* tokens, int n, int* next_token, float* logits) {
-  if (seq < 0 || seq >= h->B || n < 1) {
-    set_err("prefill: sequence %d outside [0, %d) or n = %d < 1", seq, h->B, n);
+// n prompt tokens at positions pos0 .. of sequence seq's cache: chunks of up
+// to 16 tokens, each one pass over the weights with the tokens as MFMA columns.
+static int prefill_chunks(BHandle* h, int seq, const int* tokens, int n, int pos0, int* next_token, float* logits) {
+  if (n < 1) {
+    set_err("prefill: n = %d < 1", n);
     return -1;
   }
-  int pos0 = 0;
-  HIPCHK(hipMemcpy(&pos0, h->p.pos + seq, 4, hipMemcpyDeviceToHost), -1);
-  if ((long long)pos0 + n > h->S) {
+  if (pos0 < 0 || (long long)pos0 + n > h->S) {
     set_err("prefill: sequence %d position %d + %d tokens exceeds KV capacity %d", seq, pos0, n, h->S);
     return -1;
   }
@@ -349,9 +355,50 @@ static int run_prefill(BHandle* h, int seq, const int* tokens, int n, int* next_
   if (next_token) HIPCHK(hipMemcpy(next_token, h->pf_out + lastcol, 4, hipMemcpyDeviceToHost), -1);
   if (logits)
     HIPCHK(hipMemcpy(logits, h->p.dbg_logits + (size_t)lastcol * h->V, (size_t)h->V * 4, hipMemcpyDeviceToHost), -1);
+  return 0;
+}
+
+// Prefill of sequence seq of a batch handle at its position, which advances by n.
+static int run_prefill(BHandle* h, int seq, const int* tokens, int n, int* next_token, float* logits) {
+  if (seq < 0 || seq >= h->B || n < 1) {
+    set_err("prefill: sequence %d outside [0, %d) or n = %d < 1", seq, h->B, n);
+    return -1;
+  }
+  int pos0 = 0;
+  HIPCHK(hipMemcpy(&pos0, h->p.pos + seq, 4, hipMemcpyDeviceToHost), -1);
+  if (prefill_chunks(h, seq, tokens, n, pos0, next_token, logits)) return -1;
   const int pend = pos0 + n;
   HIPCHK(hipMemcpy(h->p.pos + seq, &pend, 4, hipMemcpyHostToDevice), -1);
   return 0;
+}
+
+BHandle* create_prefill_context(int preset, int vocab, int max_seq, const char* d_weights, const long long* offsets,
+                                int num_offsets, uint16_t* kv, uint16_t* kvt) {
+  if (!d_weights || !offsets || !kv || !kvt) {
+    set_err("prefill context: null weights, offsets or cache");
+    return nullptr;
+  }
+  BHandle* h = create(preset, vocab, 1, max_seq);
+  if (!h) return nullptr;
+  if (init_state(h, d_weights, offsets, num_offsets, kv, kvt)) {
+    free_all(h);
+    delete h;
+    return nullptr;
+  }
+  return h;
+}
+
+int prefill_context_run(BHandle* h, const int* tokens, int n, int pos0, int* next_token, float* logits) {
+  return prefill_chunks(h, 0, tokens, n, pos0, next_token, logits);
+}
+
+float prefill_context_ms(BHandle* h) { return h->last_ms; }
+
+void destroy_prefill_context(BHandle* h) {
+  if (!h) return;
+  (void)hipStreamSynchronize(h->stream);
+  free_all(h);
+  delete h;
 }
 
 }  // namespace batch

@@ -148,6 +148,8 @@ struct Handle {
   float* dbg_layers = nullptr;
   float* dbg_logits = nullptr;
   void* owned_flat = nullptr;
+  std::vector<long long> offsets;         // the init offsets (a prefill context built later reuses them)
+  batch::BHandle* prefill = nullptr;      // optional prefill context bound to this handle's KV cache
   unsigned tag_base = 1;  // tag of the next launch's first phase (0 never valid)
   int pos = 0;
   long long kv_bytes = 0;
@@ -185,6 +187,8 @@ static int occupancy_ok(int* nblk) {
 }
 
 static void free_all(Handle* h) {
+  batch::destroy_prefill_context(h->prefill);
+  h->prefill = nullptr;
   void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part,
                   h->act, h->amax, h->out_tokens, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
@@ -438,6 +442,7 @@ static Handle* init_common(const void* d_weights, const long long* offsets, int 
   Handle* h = create(preset, vocab, max_seq);
   if (!h) return nullptr;
   h->owned_flat = owned;
+  if (n_off > 0) h->offsets.assign(offsets, offsets + n_off);
   if (check_occupancy(h) || init_device_state(h, static_cast<const char*>(d_weights), offsets, n_off)) {
     free_all(h);
     delete h;
@@ -661,6 +666,47 @@ float megakernel_last_kernel_ms(void* handle) {
 int megakernel_grid_size(void* handle) {
   Handle* h = static_cast<Handle*>(handle);
   return h ? h->G : -1;
+}
+
+int megakernel_prefill_attach(void* handle, void* d_weights, const long long* offsets, int num_offsets) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  if (h->prefill) return 0;
+  const char* w = static_cast<const char*>(d_weights);
+  if (!w) {  // the library's own upload (megakernel_init_from_host) with the init offsets
+    if (!h->owned_flat) {
+      mk::set_err("prefill_attach: no weight buffer (pass the flat device weights given to init)");
+      return -1;
+    }
+    w = static_cast<const char*>(h->owned_flat);
+    offsets = h->offsets.data();
+    num_offsets = (int)h->offsets.size();
+  }
+  if (!offsets || num_offsets != (int)h->offsets.size()) {
+    mk::set_err("prefill_attach: %d offsets, the handle was built from %zu", num_offsets, h->offsets.size());
+    return -1;
+  }
+  h->prefill = mk::batch::create_prefill_context(h->preset, h->V, h->S, w, offsets, num_offsets, h->kv, h->kvt);
+  return h->prefill ? 0 : -1;
+}
+
+int megakernel_prefill(void* handle, const int* tokens, int n, int* next_token) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !tokens) {
+    mk::set_err("null handle or tokens");
+    return -1;
+  }
+  if (!h->prefill) {
+    mk::set_err("prefill: no prefill context (call megakernel_prefill_attach)");
+    return -1;
+  }
+  if (mk::batch::prefill_context_run(h->prefill, tokens, n, h->pos, next_token, nullptr)) return -1;
+  h->pos += n;
+  h->last_ms = mk::batch::prefill_context_ms(h->prefill);
+  return 0;
 }
 
 int megakernel_set_attention_merge(void* handle, int merge_min) {

@@ -38,4 +38,18 @@ __global__ void synth_kv_kernel(uint16_t* __restrict__ kv, uint16_t* __restrict_
 __global__ void kv_convert_kernel(uint16_t* __restrict__ buf, uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt,
                                   int L, int NKV, int s_pad, int D, int len, int to_cache);
 
+// Prefill context of a batch-1 handle (batch.hip): the batched kernels'
+// matrix-core weight copy and work buffers, bound to an external KV cache in
+// the decode kernel's layout (K [L][NKV][s_pad][D], V^T blocks).
+namespace batch {
+struct BHandle;
+BHandle* create_prefill_context(int preset, int vocab, int max_seq, const char* d_weights, const long long* offsets,
+                                int num_offsets, uint16_t* kv, uint16_t* kvt);
+// n prompt tokens at positions pos0 .. pos0 + n - 1 of the bound cache;
+// next_token (may be null) receives the greedy token after the last one.
+int prefill_context_run(BHandle* h, const int* tokens, int n, int pos0, int* next_token, float* logits);
+float prefill_context_ms(BHandle* h);
+void destroy_prefill_context(BHandle* h);
+}  // namespace batch
+
 }  // namespace mk

@@ -18,7 +18,7 @@ from megakernel_amd import _lib
 from megakernel_amd.config import BASELINE, QWEN3_06B, TINY
 from oracle import qwen3_ref, synth
 
-from ._helpers import check_step, check_tokens_teacher_forced, make_pair, rel_l2
+from ._helpers import check_kv_bf16, check_step, check_tokens_teacher_forced, make_pair, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -265,6 +265,104 @@ def test_qwen3_preset_head_dim_128(chunk, merge):
             ref = orc.step(tok, capture=True)
             check_step(layers, logits, ref, f"qwen3 step {i}")
             tok = ref["token"]
+    finally:
+        eng.close()
+        dw.free()
+
+
+@pytest.mark.parametrize("which,prefix,prompt_len", [("tiny", 20, 37), ("baseline_2l", 300, 70), ("tiny", 0, 1)])
+def test_batch1_prefill_then_decode(which, prefix, prompt_len):
+    """megakernel_prefill on a batch-1 handle (16 prompt tokens per weight
+    pass, the batched kernels on this handle's own cache), then decode: the
+    token after the prompt and the following steps against the oracle stepped
+    through the same prompt; the prompt's layer-0 K / V (which depend on each
+    token alone) equal bf16 of the oracle's (check_kv_bf16)."""
+    shape = TINY if which == "tiny" else BASELINE.with_(n_layers=2, vocab=2048)
+    eng, orc, dw = make_pair(shape, 51, prefix + prompt_len + 16)
+    try:
+        eng.attach_prefill(dw)
+        if prefix:
+            eng.fill_kv_synthetic(prefix, 9)
+            ks = np.stack([synth.kv_prefill_bits(9, l, 0, prefix, shape.n_kv_heads, shape.head_dim)
+                           for l in range(shape.n_layers)])
+            vs = np.stack([synth.kv_prefill_bits(9, l, 1, prefix, shape.n_kv_heads, shape.head_dim)
+                           for l in range(shape.n_layers)])
+            orc.set_kv(ks, vs)
+        rng = np.random.default_rng(prompt_len)
+        prompt = [int(t) for t in rng.integers(0, shape.vocab, size=prompt_len)]
+        print(f"batch-1 prefill {which} prefix {prefix} prompt {prompt_len}", flush=True)
+        nxt = eng.prefill(prompt)
+        assert eng.pos == prefix + prompt_len
+        ref = None
+        for t in prompt:
+            ref = orc.step(t, capture=True)
+        if nxt != ref["token"]:
+            assert qwen3_ref.top2_margin(ref["logits"]) <= 2e-2, f"prefill token {nxt} != oracle {ref['token']}"
+        got = eng.get_kv(prefix + prompt_len)[0, :, :, prefix:, :]  # layer 0: [2][NKV][len][D]
+        want = np.stack([orc.k_cache[0, :, prefix:prefix + prompt_len].contiguous().view(torch.int16).numpy(),
+                         orc.v_cache[0, :, prefix:prefix + prompt_len].contiguous().view(torch.int16).numpy()]
+                        ).view(np.uint16)
+        check_kv_bf16(got, want, "layer-0 prompt KV")
+        tok = ref["token"]
+        for i in range(3):
+            _, layers, logits = eng.debug_forward(tok)
+            r = orc.step(tok, capture=True)
+            check_step(layers, logits, r, f"decode {i} after prefill")
+            tok = r["token"]
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch1_generate_with_prefill_matches_oracle():
+    """generate_ids with the prefill context: the prompt in one call, then the
+    greedy continuation in one resident launch, against the oracle."""
+    shape = TINY
+    eng, orc, dw = make_pair(shape, 52, 128, gain_std=0.0)
+    try:
+        eng.attach_prefill(dw)
+        prompt = synth.prompt_tokens(52, 21, shape.vocab)
+        gen, _ = eng.generate_ids(prompt, max_tokens=12)
+        ref = None
+        for t in prompt:
+            ref = orc.step(t, capture=True)
+        toks = [ref["token"]]
+        margins = [qwen3_ref.top2_margin(ref["logits"])]
+        for _ in range(11):
+            r = orc.step(toks[-1], capture=True)
+            toks.append(r["token"])
+            margins.append(qwen3_ref.top2_margin(r["logits"]))
+        for i, (a, b) in enumerate(zip(gen, toks)):
+            if a != b:  # a near-tie may flip; everything after it is a different continuation
+                assert margins[i] <= 2e-2, f"token {i}: {a} != oracle {b} (margin {margins[i]:.4f})"
+                break
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch1_prefill_errors():
+    shape = TINY
+    eng, _, dw = make_pair(shape, 53, 32)
+    try:
+        with pytest.raises(_lib.MegakernelError, match="attach"):
+            eng.prefill([1, 2])
+        eng.attach_prefill(dw)
+        with pytest.raises(_lib.MegakernelError, match="capacity"):
+            eng.prefill([1] * 33)
+        with pytest.raises(_lib.MegakernelError, match="token"):
+            eng.prefill([shape.vocab])
+        assert eng.pos == 0
+        eng.prefill([3] * 32)
+        assert eng.pos == 32
+    finally:
+        eng.close()
+        dw.free()
+    q = QWEN3_06B.with_(n_layers=1, vocab=256)
+    eng, _, dw = make_pair(q, 54, 16)
+    try:
+        with pytest.raises(_lib.MegakernelError, match="BASELINE and TINY"):
+            eng.attach_prefill(dw)
     finally:
         eng.close()
         dw.free()
