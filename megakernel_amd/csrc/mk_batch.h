@@ -617,10 +617,13 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
     // prefill bk_append stored them before this kernel)
     if (!p.prefill && pos >= t0 && pos < t0 + 32) {
       const int rp = pos - t0;
-      if (c16 == (rp & 15)) {
+      if (c16 == (rp & 15)) {  // register arrays take compile-time indices only
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-          kr[q][rp >> 4][kc] = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
+        for (int kc = 0; kc < 2; ++kc) {
+          const u32x4 kv = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
+          if (rp >> 4) kr[q][1][kc] = kv;
+          else kr[q][0][kc] = kv;
+        }
       }
       if (rg == (rp >> 3)) {
 #pragma unroll
