@@ -106,8 +106,15 @@ class MegakernelEngine:
         _lib.check(self.lib, self.lib.megakernel_prefill(self._handle, arr, len(ids), ctypes.byref(nxt)), "prefill")
         return nxt.value
 
-    def generate_ids(self, prompt_ids, max_tokens=100, eos_id=None, one_launch=True):
-        """Greedy continuation of token ids.  Returns (generated_ids, tok/s)."""
+    def generate_ids(self, prompt_ids, max_tokens=100, eos_id=None, one_launch=True, on_token=None):
+        """Greedy continuation of token ids (reference host/bridge.py:118-192):
+        the prompt is consumed (with the prefill context in one call, else
+        token by token), then up to max_tokens tokens are generated, the EOS
+        token included when it comes.  on_token(id) is called for each
+        generated token as it is produced (token by token then).  Returns
+        (generated_ids, tok/s of the generation loop)."""
+        if not prompt_ids:
+            raise ValueError("empty prompt")
         self.reset()
         if self._prefill:
             nxt = self.prefill(prompt_ids)
@@ -118,12 +125,16 @@ class MegakernelEngine:
         self.lib.megakernel_sync()
         start = time.perf_counter()
         generated = [nxt]
-        if one_launch and eos_id is None and max_tokens > 1:
+        if on_token is not None:
+            on_token(nxt)
+        if one_launch and eos_id is None and on_token is None and max_tokens > 1:
             generated += self.decode_many(nxt, max_tokens - 1)
         else:
             while len(generated) < max_tokens and nxt != eos_id:
                 nxt = self.decode_token(nxt)
                 generated.append(nxt)
+                if on_token is not None:
+                    on_token(nxt)
         self.lib.megakernel_sync()
         elapsed = time.perf_counter() - start
         if eos_id is not None and eos_id in generated:
@@ -131,15 +142,21 @@ class MegakernelEngine:
         return generated, (len(generated) - 1) / elapsed if elapsed > 0 and len(generated) > 1 else 0.0
 
     def generate(self, prompt, max_tokens=100, print_stream=False):
-        """Generate text from a prompt (needs a tokenizer).  Returns (text, tok/s)."""
+        """Generate text from a prompt (reference host/bridge.py:118-192): encode,
+        consume the prompt, greedy decode until EOS or max_tokens (the EOS token
+        included), print each token as it comes when print_stream.  Returns
+        (prompt + generated text with special tokens skipped, tok/s).  Needs a
+        tokenizer (``megakernel_amd.tokenizer``: a local checkpoint's
+        tokenizer.json, or ByteTokenizer for synthetic models)."""
         if self.tokenizer is None:
             raise ValueError("generate(prompt) needs a tokenizer; use generate_ids for token ids")
-        ids = self.tokenizer.encode(prompt)
+        ids = list(self.tokenizer.encode(prompt))
         eos = getattr(self.tokenizer, "eos_token_id", None)
-        gen, tps = self.generate_ids(ids, max_tokens, eos_id=eos, one_launch=eos is None)
+        stream = (lambda t: print(self.tokenizer.decode([t]), end="", flush=True)) if print_stream else None
+        gen, tps = self.generate_ids(ids, max_tokens, eos_id=eos, one_launch=eos is None, on_token=stream)
         if print_stream:
-            print(self.tokenizer.decode(gen))
-        return self.tokenizer.decode(list(ids) + gen, skip_special_tokens=True), tps
+            print()
+        return self.tokenizer.decode(ids + gen, skip_special_tokens=True), tps
 
     def benchmark(self, num_tokens=50, prompt_token=1):
         """Raw per-call decode throughput (one launch + host sync per token)."""

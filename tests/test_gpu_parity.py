@@ -366,3 +366,42 @@ def test_batch1_prefill_errors():
     finally:
         eng.close()
         dw.free()
+
+
+@pytest.mark.parametrize("use_prefill", [False, True])
+def test_generate_text_stops_at_eos(use_prefill, capsys):
+    """MegakernelEngine.generate (reference host/bridge.py:118-192) with a
+    byte tokenizer.  The engine's greedy ids, fed back to the oracle after the
+    same prompt, equal the oracle's argmax wherever its top-1/top-2 margin
+    exceeds 2e-2.  With EOS set to the engine's k-th token (its first
+    occurrence; k >= 2 when the continuation has a new token there) generation
+    stops right after it (EOS included), print_stream prints each token as it
+    comes, and the returned text is the decoded prompt + generation with
+    special tokens skipped."""
+    from megakernel_amd.tokenizer import ByteTokenizer
+    shape = TINY
+    eng, orc, dw = make_pair(shape, 61, 128)
+    try:
+        if use_prefill:
+            eng.attach_prefill(dw)
+        prompt = "greedy decode on gfx950"
+        ids = ByteTokenizer(shape.vocab).encode(prompt)
+        free, _ = eng.generate_ids(ids, max_tokens=12)  # no EOS: 12 tokens
+        for t in ids[:-1]:
+            orc.step(t)
+        check_tokens_teacher_forced([ids[-1]] + free[:-1], free, orc)
+        firsts = [i for i in range(len(free)) if free[i] not in free[:i]]
+        k = next((i for i in firsts if i >= 2), firsts[-1])
+        tok = ByteTokenizer(shape.vocab, eos_token_id=free[k])
+        eng.tokenizer = tok
+        gen, _ = eng.generate_ids(ids, max_tokens=12, eos_id=tok.eos_token_id)
+        assert gen == free[:k + 1], f"with EOS {free[k]}: {gen}, expected {free[:k + 1]}"
+        capsys.readouterr()
+        text, tps = eng.generate(prompt, max_tokens=12, print_stream=True)
+        printed = capsys.readouterr().out
+        assert text == tok.decode(ids + free[:k + 1], skip_special_tokens=True)
+        assert printed == "".join(tok.decode([t]) for t in free[:k + 1]) + "\n"
+        assert k == 0 or tps > 0
+    finally:
+        eng.close()
+        dw.free()
