@@ -523,8 +523,13 @@ __global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
 // cores exactly as the batch-1 kernel does: scores^T = K . Qb with q split into
 // three bf16 parts in rows 4 j + 0..2 (j = q head of the group), and
 // out^T = V^T . Pb with the softmax weights split the same way.
+// Five 256-thread items per CU (<= 102 registers per lane): the 16-sequence
+// step at KV 512-4096 has ~1,100 items; with four per CU the last ~10 % ran
+// as a second, latency-bound residency wave.
+constexpr int ATTN_WAVES_PER_EU = AT == 256 ? 5 : 2;
 template <class S>
-__global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
+__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_PER_EU, ATTN_WAVES_PER_EU))) void bk_attn(
+    BParams p, int layer) {
   static_assert(S::GQA == 2 && S::D == 64, "batched attention is built for 2 q heads of 64 per kv head");
   constexpr int D = S::D, NKV = S::NKV;
   __shared__ __attribute__((aligned(16))) uint16_t qb[16][D];          // q parts (A operand of the scores)
@@ -606,9 +611,6 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
   f32x4 acc[D / 16];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 qa[2];
-#pragma unroll
-  for (int kc = 0; kc < 2; ++kc) qa[kc] = *reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]);
 #pragma unroll
   for (int q = 0; q < NBW; ++q) {
     const int t0 = 32 * (s * AW * NBW + w + AW * q);
@@ -635,7 +637,8 @@ __global__ __launch_bounds__(AT) void bk_attn(BParams p, int layer) {
     for (int h = 0; h < 2; ++h) {
       f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) d4 = mfma(qa[kc], kr[q][h][kc], d4);
+      for (int kc = 0; kc < 2; ++kc)  // q read from LDS per block: registers for a fifth workgroup per CU
+        d4 = mfma(*reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]), kr[q][h][kc], d4);
       const int t = t0 + 16 * h + c16;
       sc[h] = t < n ? ((d4[0] + d4[1]) + d4[2]) * scale : -INFINITY;
     }
