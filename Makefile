@@ -11,7 +11,7 @@ HIPFLAGS   := --offload-arch=$(ARCH) -O3 -std=c++17 -fPIC \
               -Wno-unused-command-line-argument
 CSRC       := megakernel_amd/csrc
 LIB        := megakernel_amd/megakernel.so
-SRCS       := $(CSRC)/megakernel.hip $(CSRC)/batch.hip $(CSRC)/ops.hip
+SRCS       := $(CSRC)/megakernel.hip $(CSRC)/batch.hip $(CSRC)/ops.hip $(CSRC)/selftest.hip
 HDRS       := $(wildcard $(CSRC)/*.h) include/megakernel.h
 
 .PHONY: all lib clean asm

@@ -286,6 +286,15 @@ int megakernel_op_lmhead_argmax(const void* w, long long copy_bytes, int n_copie
 /* Device time of this thread's last megakernel_op_* call (ms). */
 float megakernel_op_last_ms(void);
 
+/* Self-test of the hand-off primitive that replaces the reference's grid
+ * barrier (src/barriers.cuh:38-73): one workgroup per CU runs `rounds`
+ * all-gather rounds of tagged words (full tags and 4-bit packed pairs,
+ * double-buffered by round parity) with the decode kernel's stores and
+ * loads, counting words accepted with the right tag but a wrong value.
+ * *mismatches receives that count (0 expected), *us_per_round (may be NULL)
+ * the mean time of a round.  Returns -1 if a wait timed out. */
+int megakernel_selftest_dataflow(int rounds, int* mismatches, float* us_per_round);
+
 #ifdef __cplusplus
 }
 #endif

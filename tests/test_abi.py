@@ -112,3 +112,5 @@ def test_op_argument_checks(clib):
     assert clib.megakernel_op_lmhead_argmax(fake, 0, 1, 151936, 2048, fake, 1, None, fake, fake, 1, 1) == -1
     assert clib.megakernel_op_lmhead_argmax(fake, 0, 1, 100, 1024, fake, 1, None, fake, fake, 1, 1) == -1
     assert clib.megakernel_op_lmhead_argmax(fake, 0, 1, 4096, 1024, fake, 1, None, None, fake, 1, 1) == -1
+    assert clib.megakernel_selftest_dataflow(0, ctypes.byref(ctypes.c_int()), None) == -1
+    assert "rounds" in _lib.last_error(clib)

@@ -405,3 +405,17 @@ def test_generate_text_stops_at_eos(use_prefill, capsys):
     finally:
         eng.close()
         dw.free()
+
+
+def test_dataflow_handoff_selftest():
+    """The hand-off primitive on its own, across every CU and XCD: 20,000
+    all-gather rounds of tagged words (full tags and 4-bit packed pairs) with
+    the decode kernel's write-through stores and agent-scope polling loads;
+    no word may be accepted with the right tag and a wrong value."""
+    lib = _lib.load()
+    bad, us = ctypes.c_int(-1), ctypes.c_float(0.0)
+    rc = lib.megakernel_selftest_dataflow(20000, ctypes.byref(bad), ctypes.byref(us))
+    print(f"selftest: mismatches {bad.value}, {us.value:.2f} us per all-gather round", flush=True)
+    assert rc == 0, _lib.last_error(lib)
+    assert bad.value == 0
+    assert 0.0 < us.value < 100.0
