@@ -82,3 +82,52 @@ def test_engine_from_converted_checkpoint(tmp_path):
             tok = ref["token"]
     finally:
         eng.close()
+
+
+def _write_tokenizer(d):
+    """A small byte-level BPE tokenizer.json (ids < 300) beside the checkpoint."""
+    from tokenizers import Tokenizer, decoders, models, pre_tokenizers, trainers
+    tok = Tokenizer(models.BPE(unk_token="<unk>"))
+    tok.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False)
+    tok.decoder = decoders.ByteLevel()
+    trainer = trainers.BpeTrainer(vocab_size=300, special_tokens=["<unk>", "<|endoftext|>"],
+                                  initial_alphabet=pre_tokenizers.ByteLevel.alphabet())
+    tok.train_from_iterator(["a persistent kernel decodes one token per step on every CU"] * 40, trainer)
+    tok.save(str(d / "tokenizer.json"))
+    (d / "tokenizer_config.json").write_text(json.dumps({"eos_token": "<|endoftext|>"}))
+
+
+@pytest.mark.gpu
+def test_converted_checkpoint_tokenizer_prefill_generate(tmp_path):
+    """The product surface end to end, offline: a local HF checkpoint and its
+    tokenizer.json -> weights.bin -> engine built from the file with the
+    prefill context (the library's own upload) -> generate(text).  The greedy
+    ids after the prompt, fed back to the oracle, match its argmax wherever
+    the margin exceeds 2e-2; the returned text is the decoded prompt +
+    generation."""
+    from megakernel_amd.bridge import MegakernelEngine
+    from megakernel_amd.tokenizer import load_tokenizer
+
+    from ._helpers import check_tokens_teacher_forced
+    d, _ = _tiny_checkpoint(tmp_path, seed=6)
+    _write_tokenizer(d)
+    wpath = str(tmp_path / "weights.bin")
+    offs_path, shape = weights.convert_safetensors(str(d), wpath)
+    tok = load_tokenizer(str(d))
+    eng = MegakernelEngine(weights_path=wpath, offsets_path=offs_path, shape=shape, max_seq=128, tokenizer=tok,
+                           prefill=True)
+    try:
+        osh = oracle_shape(shape)
+        bits = qwen3_ref.unpack_flat(osh, np.fromfile(wpath, dtype=np.uint8), weights.load_offsets(offs_path))
+        orc = qwen3_ref.Qwen3Oracle(osh, bits, 128)
+        prompt = "a persistent kernel decodes"
+        ids = tok.encode(prompt)
+        gen, _ = eng.generate_ids(ids, max_tokens=8)
+        for t in ids[:-1]:
+            orc.step(t)
+        check_tokens_teacher_forced([ids[-1]] + gen[:-1], gen, orc)
+        gen_eos, _ = eng.generate_ids(ids, max_tokens=8, eos_id=tok.eos_token_id)
+        text, _ = eng.generate(prompt, max_tokens=8)
+        assert text == tok.decode(ids + gen_eos, skip_special_tokens=True)
+    finally:
+        eng.close()
