@@ -143,6 +143,7 @@ struct Handle {
   size_t tagged_bytes[5] = {0, 0, 0, 0, 0};
   int* out_tokens = nullptr;
   int* err = nullptr;
+  int* host_io = nullptr;  // pinned copy of err and out_tokens (same offsets) after a launch
   u64* trace = nullptr;
   float* inv_freq = nullptr;
   float* dbg_layers = nullptr;
@@ -190,10 +191,11 @@ static void free_all(Handle* h) {
   batch::destroy_prefill_context(h->prefill);
   h->prefill = nullptr;
   void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part,
-                  h->act, h->amax, h->out_tokens, h->err, h->inv_freq, h->dbg_layers,
+                  h->act, h->amax, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
     if (q) (void)hipFree(q);
+  if (h->host_io) (void)hipHostFree(h->host_io);
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);
   if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -260,9 +262,11 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
     HIPCHK(hipMemsetAsync(*tagged[i], 0, h->tagged_bytes[i], h->stream), -1);
   }
   h->max_launch_tokens = 1 << 20;
-  HIPCHK(hipMalloc(&h->out_tokens, (size_t)h->max_launch_tokens * 4), -1);
   HIPCHK(hipMalloc(&h->trace, ((size_t)(5 * h->L + 1) * 2 + EVT_N) * h->G * 8), -1);
-  HIPCHK(hipMalloc(&h->err, 256), -1);
+  // error word (256 bytes), then the output tokens: one copy brings both back
+  HIPCHK(hipMalloc(&h->err, 256 + (size_t)h->max_launch_tokens * 4), -1);
+  h->out_tokens = h->err + 64;
+  HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&h->host_io), 256 + (size_t)h->max_launch_tokens * 4), -1);
   HIPCHK(hipMemsetAsync(h->err, 0, 256, h->stream), -1);
   HIPCHK(hipMalloc(&h->dbg_layers, (size_t)(h->L + 1) * s.H * 4), -1);
   HIPCHK(hipMalloc(&h->dbg_logits, (size_t)h->V * 4), -1);
@@ -358,6 +362,20 @@ static int clear_tagged_state(Handle* h) {
   return 0;
 }
 
+// The packed-pair words (part, act) carry 4-bit tags, so a stale word can look
+// current when its tag is a multiple of 15 phases old.  While the position
+// only grows and the split configuration is fixed, that never happens: every
+// act word and every active split slot is rewritten at each layer (5 phases
+// apart, 6 across a token boundary), and split counts never shrink, so a slot
+// that becomes active still holds zeros.  A position that moves backwards, a
+// new cache, or a new split / merge configuration breaks that, and clears them.
+static int clear_pair_words(Handle* h) {
+  HIPCHK(hipMemsetAsync(h->part, 0, h->tagged_bytes[2], h->stream), -1);
+  HIPCHK(hipMemsetAsync(h->act, 0, h->tagged_bytes[3], h->stream), -1);
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  return 0;
+}
+
 // One resident launch decoding n tokens starting at h->pos.
 static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int trace_token = -1) {
   if (n <= 0 || n > h->max_launch_tokens) {
@@ -409,26 +427,25 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.nsplit_max = h->nsplit_max;
   p.chunk_min = h->chunk_min;
   p.merge_min = h->merge_min;
-  // the packed-pair words (part, act) carry 4-bit tags: start every launch from zeros
-  HIPCHK(hipMemsetAsync(h->part, 0, h->tagged_bytes[2], h->stream), -1);
-  HIPCHK(hipMemsetAsync(h->act, 0, h->tagged_bytes[3], h->stream), -1);
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
   // the long-context instantiation when the launch's last token has more
   // than merge_min splits per kv head (split counts grow with the position)
   const bool lc = split_count(h->pos + n, h->chunk_min, h->nsplit_max) > h->merge_min;
   HIPCHK(h->launch(h, p, lc), -1);
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
+  // error word and tokens come back in one copy into pinned memory
+  HIPCHK(hipMemcpyAsync(h->host_io, h->err, 256 + (out_host ? (size_t)n * 4 : 0), hipMemcpyDeviceToHost, h->stream),
+         -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
   HIPCHK(hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1), -1);
-  int err = 0;
-  HIPCHK(hipMemcpy(&err, h->err, 4, hipMemcpyDeviceToHost), -1);
+  const int err = h->host_io[0];
   h->tag_base += (unsigned)n * per_token;  // tags of this launch are never expected again
   if (err != MK_OK) {
     clear_tagged_state(h);
     set_err("decode kernel aborted: %s", err == MK_ERR_TIMEOUT ? "a dataflow wait timed out" : "device error");
     return -1;
   }
-  if (out_host) HIPCHK(hipMemcpy(out_host, h->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost), -1);
+  if (out_host) memcpy(out_host, h->host_io + 64, (size_t)n * 4);
   h->pos += n;
   return 0;
 }
@@ -480,7 +497,7 @@ void megakernel_reset(void* handle) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return;
   (void)hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream);
-  (void)hipStreamSynchronize(h->stream);
+  (void)mk::clear_pair_words(h);
   h->pos = 0;
 }
 
@@ -565,6 +582,7 @@ int megakernel_set_pos(void* handle, int pos) {
     mk::set_err("invalid handle or position %d", pos);
     return -1;
   }
+  if (pos < h->pos && mk::clear_pair_words(h)) return -1;
   h->pos = pos;
   return 0;
 }
@@ -603,6 +621,7 @@ int megakernel_set_kv(void* handle, const void* host_kv, int len) {
     return -1;
   }
   if (len > 0 && kv_transfer(h, const_cast<void*>(host_kv), len, 1)) return -1;
+  if (mk::clear_pair_words(h)) return -1;
   h->pos = len;
   return 0;
 }
@@ -630,6 +649,7 @@ int megakernel_fill_kv_synthetic(void* handle, int len, unsigned long long seed,
     HIPCHK(hipGetLastError(), -1);
     HIPCHK(hipStreamSynchronize(h->stream), -1);
   }
+  if (mk::clear_pair_words(h)) return -1;
   h->pos = len;
   return 0;
 }
@@ -715,6 +735,7 @@ int megakernel_set_attention_merge(void* handle, int merge_min) {
     mk::set_err("attention merge threshold %d must be >= 1", merge_min);
     return -1;
   }
+  if (merge_min != h->merge_min && mk::clear_pair_words(h)) return -1;
   h->merge_min = merge_min;
   return 0;
 }
@@ -725,6 +746,7 @@ int megakernel_set_attention_chunk(void* handle, int chunk_min) {
     mk::set_err("attention chunk %d must be >= 1", chunk_min);
     return -1;
   }
+  if (chunk_min != h->chunk_min && mk::clear_pair_words(h)) return -1;
   h->chunk_min = chunk_min;
   return 0;
 }
