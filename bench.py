@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--merge", type=int, default=0,
                     help="attention splits per kv head above which the first split merges them (0: library default)")
     ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--lmhead-fp8", action="store_true",
+                    help="stream the FP8 (e4m3, power-of-two row scales) copy of the LM head")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
     ap.add_argument("--trace", action="store_true", help="print a per-phase critical-path summary")
@@ -470,6 +472,8 @@ def main():
         eng.set_attention_chunk(args.chunk)
     if args.merge > 0:
         eng.set_attention_merge(args.merge)
+    if args.lmhead_fp8:
+        eng.set_lmhead_fp8(True)
     info = launcher.detect_gpu()
     grid = eng.grid_size
     print(f"# device {info['name']} CUs {info['cu_count']} grid {grid}", file=sys.stderr, flush=True)
@@ -491,9 +495,11 @@ def main():
     wall = statistics.median(walls)
     kern = statistics.median(kernels)
     nbytes = sum(shape.token_bytes(args.ctx + i) for i in range(K))
+    if args.lmhead_fp8:  # 1 byte per LM-head weight instead of 2, plus a 4-byte scale per row
+        nbytes -= K * (shape.vocab * shape.hidden - 4 * shape.vocab)
     achieved = nbytes / kern / 1e9
     traffic = None
-    if os.path.exists(args.traffic_json):
+    if os.path.exists(args.traffic_json) and not args.lmhead_fp8:
         with open(args.traffic_json) as f:
             tj = json.load(f)
         if tj.get("ctx") == args.ctx and tj.get("tokens") == K:
@@ -518,13 +524,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "bf16 (LM head fp8 e4m3)" if args.lmhead_fp8 else "bf16",
         "data": "synthetic",
         "config": {"workload": f"Qwen3-0.6B-shaped batch-1 greedy decode, KV prefilled to {args.ctx}, "
                                f"{K} tokens in one resident launch (BASELINE configs[2])",
                    "ctx": args.ctx, "tokens": K, "batch": 1, "layers": shape.n_layers,
                    "hidden": shape.hidden, "heads": "16q/8kv x 64", "ffn": shape.ffn, "vocab": shape.vocab,
-                   "weights": "bf16 N(0,0.02) (Irwin-Hall(4) approx), unit norm gains",
+                   "weights": "bf16 N(0,0.02) (Irwin-Hall(4) approx), unit norm gains" +
+                              ("; LM head streamed as fp8 e4m3 with power-of-two row scales" if args.lmhead_fp8 else ""),
                    "accumulation": "fp32", "reps": args.reps, "grid": grid,
                    "device": info["name"]},
         "kernel_ms_per_step": round(kern * 1e3 / K, 5),

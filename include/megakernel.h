@@ -138,6 +138,20 @@ int megakernel_set_attention_chunk(void* handle, int chunk_min);
  * only. */
 int megakernel_set_attention_merge(void* handle, int merge_min);
 
+/* FP8 LM head (no counterpart in the reference kernel, which plans FP8
+ * weights in RESEARCH.md:434-436,463).  enable = 1 builds, once, an OCP e4m3
+ * copy of the tied LM head with one power-of-two scale per row (2^e, the
+ * smallest e with max|row| <= 448 * 2^e; weights rounded to nearest even after
+ * the exact scaling) and makes the decode launches stream it: 1 byte per
+ * weight instead of 2 for 32 % of the bytes of a token.  The embedding gather
+ * and the prefill context keep the bf16 table.  enable = 0 returns to bf16.
+ * Returns 0, or -1 (vocab not a multiple of 16, hidden not of 64, no memory). */
+int megakernel_set_lmhead_fp8(void* handle, int enable);
+
+/* The FP8 LM head as built: codes[V * H] row-major e4m3 bytes, scales[V]
+ * (validation).  -1 when it has not been built. */
+int megakernel_get_lmhead_fp8(void* handle, unsigned char* codes, float* scales);
+
 /* Device fill of n bf16 values: bf16(float32(S_i - 131070) * c [+ 1.0f]),
  * S_i the Irwin-Hall(4) sum of the 16-bit fields of splitmix64(key, i). */
 int megakernel_synth_fill(void* d_dst, unsigned long long n, unsigned long long key, float c, int add_one);

@@ -236,6 +236,21 @@ class MegakernelEngine:
         _lib.check(self.lib, self.lib.megakernel_set_attention_merge(self._handle, merge_min),
                    "set_attention_merge")
 
+    def set_lmhead_fp8(self, enable: bool = True):
+        """Stream an FP8 (OCP e4m3, power-of-two row scales) copy of the LM head."""
+        _lib.check(self.lib, self.lib.megakernel_set_lmhead_fp8(self._handle, int(bool(enable))),
+                   "set_lmhead_fp8")
+
+    def lmhead_fp8(self):
+        """(codes uint8 [V, H], scales float32 [V]) of the FP8 LM head."""
+        s = self.shape
+        codes = np.empty((s.vocab, s.hidden), dtype=np.uint8)
+        scales = np.empty(s.vocab, dtype=np.float32)
+        _lib.check(self.lib, self.lib.megakernel_get_lmhead_fp8(
+            self._handle, codes.ctypes.data_as(ctypes.c_void_p),
+            scales.ctypes.data_as(ctypes.POINTER(ctypes.c_float))), "get_lmhead_fp8")
+        return codes, scales
+
     @property
     def grid_size(self) -> int:
         return self.lib.megakernel_grid_size(self._handle)

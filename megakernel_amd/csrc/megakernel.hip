@@ -58,6 +58,37 @@ __global__ void repack_kernel(const u32x4* __restrict__ src, int R, int K, u32x4
   }
 }
 
+// FP8 copy of the LM head (no counterpart in the reference kernel; the
+// reference plans FP8 weights in RESEARCH.md:434-436,463).  One workgroup per
+// 16-row block of the bf16 tiles: row r gets the power-of-two scale 2^e with
+// the smallest e such that max|W[r]| <= 448 * 2^e, and each weight becomes
+// e4m3(W[r][c] * 2^-e) (exact scaling, then round to nearest even).  Output
+// tiles: 1 KiB units of 64 lanes x 16 bytes, lane (q, r) holding row r,
+// columns 64u + 16q .. +15 of unit u.
+__global__ __launch_bounds__(256) void lmhead_fp8_kernel(const u32x4* __restrict__ src, int K,
+                                                         unsigned char* __restrict__ dst, float* __restrict__ scales) {
+  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;  // 16 threads per row (one lane group)
+  const long long rb = blockIdx.x, row = rb * 16 + r;
+  const int KT = K / 32, KT8 = K / 64;
+  const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src + rb * KT * 64);
+  auto elem = [&](int c) {  // bf16 tile layout: unit c/32, lane ((c/8)%4)*16 + r, element c%8
+    return bf16_to_f32(s16[(((c >> 5) * 64) + ((c >> 3) & 3) * 16 + r) * 8 + (c & 7)]);
+  };
+  float amax = 0.f;
+  for (int c = j; c < K; c += 16) amax = fmaxf(amax, fabsf(elem(c)));
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+  int e = 0;
+  if (amax > 0.f) {
+    e = ilogbf(amax) - 8;  // 448 = 1.75 * 2^8
+    if (amax > ldexpf(448.f, e)) ++e;
+  }
+  unsigned char* d = dst + rb * KT8 * 1024;
+  for (int c = j; c < K; c += 16)
+    d[(c >> 6) * 1024 + (((c >> 4) & 3) * 16 + r) * 16 + (c & 15)] = (unsigned char)e4m3_encode(ldexpf(elem(c), -e));
+  if (j == 0) scales[row] = ldexpf(1.f, e);
+}
+
 __global__ void synth_fill_kernel(uint16_t* __restrict__ dst, unsigned long long n, unsigned long long key,
                                   float c, int add_one) {
   for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -137,6 +168,9 @@ struct Handle {
   uint16_t* norms = nullptr;
   uint16_t* final_norm = nullptr;
   u32x4* lmhead = nullptr;
+  u32x4* lmhead8 = nullptr;  // optional FP8 copy of the LM head, built on request
+  float* lm_scale = nullptr;
+  bool lm_fp8 = false;       // the LM head reads lmhead8
   uint16_t* kv = nullptr;
   u64 *x = nullptr, *qkv = nullptr, *part = nullptr, *act = nullptr;
   u64* amax = nullptr;
@@ -161,36 +195,48 @@ struct Handle {
 
 // lc: the launch reaches more than merge_min attention splits per kv head;
 // the debug instantiation when the launch records timestamps or validation
-// outputs
+// outputs; the FP8 LM head when the handle has it switched on
+template <class S, int MODE>
+static void launch_mode(Handle* h, const Params& p) {
+  hipLaunchKernelGGL((decode_kernel<S, MODE>), dim3(h->G), dim3(NT), 0, h->stream, p);
+}
+
 template <class S>
 static hipError_t launch_decode(Handle* h, const Params& p, bool lc) {
-  const int mode = (lc ? 1 : 0) | (p.trace || p.dbg_layers || p.dbg_logits ? 2 : 0);
+  const int mode = (lc ? 1 : 0) | (p.trace || p.dbg_layers || p.dbg_logits ? 2 : 0) | (p.lmhead8 ? 4 : 0);
   switch (mode) {
-    case 0: hipLaunchKernelGGL((decode_kernel<S, 0>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
-    case 1: hipLaunchKernelGGL((decode_kernel<S, 1>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
-    case 2: hipLaunchKernelGGL((decode_kernel<S, 2>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
-    default: hipLaunchKernelGGL((decode_kernel<S, 3>), dim3(h->G), dim3(NT), 0, h->stream, p); break;
+    case 0: launch_mode<S, 0>(h, p); break;
+    case 1: launch_mode<S, 1>(h, p); break;
+    case 2: launch_mode<S, 2>(h, p); break;
+    case 3: launch_mode<S, 3>(h, p); break;
+    case 4: launch_mode<S, 4>(h, p); break;
+    case 5: launch_mode<S, 5>(h, p); break;
+    case 6: launch_mode<S, 6>(h, p); break;
+    default: launch_mode<S, 7>(h, p); break;
   }
   return hipGetLastError();
 }
 
+template <class S, int MODE>
+static int occupancy_of() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<S, MODE>, NT, 0) != hipSuccess) return 0;
+  return n;
+}
+
 template <class S>
 static int occupancy_ok(int* nblk) {
-  int n[4] = {0, 0, 0, 0};
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[0], decode_kernel<S, 0>, NT, 0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[1], decode_kernel<S, 1>, NT, 0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[2], decode_kernel<S, 2>, NT, 0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n[3], decode_kernel<S, 3>, NT, 0) != hipSuccess)
-    return 0;
+  const int n[8] = {occupancy_of<S, 0>(), occupancy_of<S, 1>(), occupancy_of<S, 2>(), occupancy_of<S, 3>(),
+                    occupancy_of<S, 4>(), occupancy_of<S, 5>(), occupancy_of<S, 6>(), occupancy_of<S, 7>()};
   *nblk = n[0];
-  for (int i = 1; i < 4; ++i) *nblk = n[i] < *nblk ? n[i] : *nblk;
+  for (int i = 1; i < 8; ++i) *nblk = n[i] < *nblk ? n[i] : *nblk;
   return 1;
 }
 
 static void free_all(Handle* h) {
   batch::destroy_prefill_context(h->prefill);
   h->prefill = nullptr;
-  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->kv, h->x, h->qkv, h->part,
+  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->kv, h->x, h->qkv, h->part,
                   h->act, h->amax, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
@@ -395,6 +441,8 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.norms = h->norms;
   p.final_norm = h->final_norm;
   p.lmhead = h->lmhead;
+  p.lmhead8 = h->lm_fp8 ? h->lmhead8 : nullptr;
+  p.lm_scale = h->lm_fp8 ? h->lm_scale : nullptr;
   p.kv = h->kv;
   p.kvt = h->kvt;
   p.s_pad = h->s_pad;
@@ -748,6 +796,46 @@ int megakernel_set_attention_chunk(void* handle, int chunk_min) {
   }
   if (chunk_min != h->chunk_min && mk::clear_pair_words(h)) return -1;
   h->chunk_min = chunk_min;
+  return 0;
+}
+
+int megakernel_set_lmhead_fp8(void* handle, int enable) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  if (enable && !h->lmhead8) {
+    const int K = h->sh.H;
+    if (h->V % 16 || K % 64) {
+      mk::set_err("FP8 LM head needs vocab %% 16 == 0 and hidden %% 64 == 0 (vocab %d, hidden %d)", h->V, K);
+      return -1;
+    }
+    HIPCHK(hipMalloc(&h->lmhead8, (size_t)h->V * K), -1);
+    HIPCHK(hipMalloc(&h->lm_scale, (size_t)h->V * 4), -1);
+    hipLaunchKernelGGL(mk::lmhead_fp8_kernel, dim3(h->V / 16), dim3(256), 0, h->stream, h->lmhead, K,
+                       reinterpret_cast<unsigned char*>(h->lmhead8), h->lm_scale);
+    HIPCHK(hipGetLastError(), -1);
+    HIPCHK(hipStreamSynchronize(h->stream), -1);
+  }
+  h->lm_fp8 = enable != 0;
+  return 0;
+}
+
+int megakernel_get_lmhead_fp8(void* handle, unsigned char* codes, float* scales) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !h->lmhead8 || !codes || !scales) {
+    mk::set_err("FP8 LM head not built (megakernel_set_lmhead_fp8) or null output");
+    return -1;
+  }
+  const int K = h->sh.H, KT8 = K / 64;
+  std::vector<unsigned char> tiles((size_t)h->V * K);
+  HIPCHK(hipMemcpy(tiles.data(), h->lmhead8, tiles.size(), hipMemcpyDeviceToHost), -1);
+  HIPCHK(hipMemcpy(scales, h->lm_scale, (size_t)h->V * 4, hipMemcpyDeviceToHost), -1);
+  for (long long row = 0; row < h->V; ++row)
+    for (int c = 0; c < K; ++c)
+      codes[row * K + c] =
+          tiles[((row >> 4) * KT8 + (c >> 6)) * 1024 + (((c >> 4) & 3) * 16 + (row & 15)) * 16 + (c & 15)];
   return 0;
 }
 

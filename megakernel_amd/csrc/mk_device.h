@@ -67,6 +67,37 @@ __device__ __forceinline__ float dot8(u32x4 w, const float* h, float acc) {
   return acc;
 }
 
+// 16 FP8 (OCP e4m3) weights against 16 fp32 inputs: the hardware converts two
+// bytes per instruction (bytes 0-1 / 2-3 of each dword, in order).
+__device__ __forceinline__ float dot16_fp8(u32x4 w, const float* h, float acc) {
+  const unsigned d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[i], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[i], true);
+    acc = fmaf(lo[0], h[4 * i + 0], acc);
+    acc = fmaf(lo[1], h[4 * i + 1], acc);
+    acc = fmaf(hi[0], h[4 * i + 2], acc);
+    acc = fmaf(hi[1], h[4 * i + 3], acc);
+  }
+  return acc;
+}
+
+// OCP e4m3 (bias 7, largest finite 448, no infinities) of x, |x| <= 448,
+// rounded to nearest, ties to even.  Subnormals are m * 2^-9 (m < 8).
+__device__ __forceinline__ unsigned e4m3_encode(float x) {
+  const unsigned s = signbit(x) ? 0x80u : 0u;
+  const float a = fabsf(x);
+  unsigned c;
+  if (a < 0.015625f) {
+    c = (unsigned)rintf(a * 512.0f);  // 0..8; 8 is the smallest normal
+  } else {
+    const int e = ilogbf(a);
+    c = (unsigned)((e + 7) << 3) + (unsigned)rintf(ldexpf(a, 3 - e)) - 8u;
+  }
+  return s | (c > 0x7eu ? 0x7eu : c);
+}
+
 __device__ __forceinline__ u32x4 ld_nt(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
 // Raw buffer loads: a wave-uniform base in a buffer descriptor (SGPRs), a

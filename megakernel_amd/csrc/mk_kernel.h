@@ -62,6 +62,8 @@ struct Params {
   const uint16_t* norms;      // [L][NORM_STRIDE] bf16 gains
   const uint16_t* final_norm; // [H] bf16
   const u32x4* lmhead;        // packed tied embedding [V/16][KT_H][64]
+  const u32x4* lmhead8;       // optional FP8 (e4m3) copy of the LM head [V/16][H/64][64]
+  const float* lm_scale;      // [V] power-of-two row scales of lmhead8
   uint16_t* kv;               // K cache [L][NKV][s_pad][D] bf16
   uint16_t* kvt;              // V cache, transposed blocks [L][NKV][s_pad/32][D][32] bf16
   u64* x;                     // [H] residual stream (tagged)
@@ -1091,11 +1093,13 @@ __device__ __forceinline__ bool token_from_slots(const Params& p, u64* slots, un
 // MODE bit 0 (LC): the launch's contexts reach more than merge_min attention
 // splits per kv head (long-context merge and deferred K/V prefetch compiled
 // in); bit 1 (DBG): per-phase timestamps and the validation outputs
-// (dbg_layers, dbg_logits) compiled in.  The host picks the instantiation per
-// launch; the plain one carries neither (fewer live scalar values).
+// (dbg_layers, dbg_logits) compiled in; bit 2 (F8): the LM head streams the
+// FP8 copy (lmhead8, lm_scale) instead of the bf16 tiles.  The host picks the
+// instantiation per launch; the plain one carries none (fewer live scalar
+// values).
 template <class S, int MODE>
 __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
-  constexpr bool LC = (MODE & 1) != 0, DBG = (MODE & 2) != 0;
+  constexpr bool LC = (MODE & 1) != 0, DBG = (MODE & 2) != 0, F8 = (MODE & 4) != 0;
   __shared__ Smem<S> sm;
   if (threadIdx.x == 0) wg_abort = 0;
   for (int i = threadIdx.x; i < 16 * S::D; i += NT) (&sm.qb[0][0])[i] = 0;  // unused columns stay 0
@@ -1342,8 +1346,12 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         // re-derived per block so the LDS reads of the hidden vector are not
         // hoisted out of the block loop (256 floats per lane would not fit)
         const unsigned lo = lane_id();
-        const float* hv = sm.vec_l + (lo >> 4) * 8;
-        const auto rs = make_rsrc(p.lmhead + b * S::KT_H * 64);  // wave-uniform block base
+        // a 16-row block is KT 1 KiB units of 64 lanes x 16 bytes: lane
+        // (q, r) holds row r, columns q*E .. q*E+E-1 of each 4E-column unit
+        // (E = 8 bf16 or 16 FP8 values)
+        constexpr int E = F8 ? 16 : 8, KT = S::H / (4 * E);
+        const float* hv = sm.vec_l + (lo >> 4) * E;
+        const auto rs = make_rsrc((F8 ? p.lmhead8 : p.lmhead) + b * KT * 64);  // wave-uniform block base
         float acc = 0.f;
         constexpr int U = 16;
         // the first MK_LMHEAD_KEEP_PCT % of each workgroup's blocks are loaded
@@ -1351,22 +1359,29 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         // the rest non-temporally
         const bool keep = (b - b0) * 100 < (b1 - b0) * MK_LMHEAD_KEEP_PCT;
 #pragma unroll 1
-        for (int k0 = 0; k0 < S::KT_H; k0 += U) {
+        for (int k0 = 0; k0 < KT; k0 += U) {
           u32x4 wv[U];
           if (keep) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
-              if (k0 + u < S::KT_H) wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lo * 16u, (unsigned)(k0 + u) * 1024u, MK_LMHEAD_AUX);
+              if (k0 + u < KT) wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lo * 16u, (unsigned)(k0 + u) * 1024u, MK_LMHEAD_AUX);
           } else {
 #pragma unroll
             for (int u = 0; u < U; ++u)
-              if (k0 + u < S::KT_H) wv[u] = buf_ld_nt(rs, lo * 16u, (unsigned)(k0 + u) * 1024u);
+              if (k0 + u < KT) wv[u] = buf_ld_nt(rs, lo * 16u, (unsigned)(k0 + u) * 1024u);
           }
 #pragma unroll
-          for (int u = 0; u < U; ++u)
-            if (k0 + u < S::KT_H) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
+          for (int u = 0; u < U; ++u) {
+            if (k0 + u < KT) {
+              if constexpr (F8)
+                acc = dot16_fp8(wv[u], hv + (k0 + u) * 64, acc);
+              else
+                acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
+            }
+          }
         }
         acc = stride_sum<16>(acc) * rn;
+        if constexpr (F8) acc *= p.lm_scale[b * 16 + (l & 15)];
         if (l < 16) {
           const unsigned idx = (unsigned)(b * 16 + l);
           if (DBG && p.dbg_logits) p.dbg_logits[idx] = acc;

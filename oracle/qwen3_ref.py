@@ -141,6 +141,7 @@ class Qwen3Oracle:
         f = lambda n: bits_to_torch(bits[n]).to(matmul_dtype)  # noqa: E731
         g = lambda n: bits_to_torch(bits[n]).float()           # noqa: E731
         self.embed = f("embedding")
+        self.lm_head = self.embed  # tied; use_fp8_lm_head() swaps in the FP8 copy
         self.final_norm = g("final_norm")
         self.layers = []
         for i in range(shape.n_layers):
@@ -156,6 +157,15 @@ class Qwen3Oracle:
                                    dtype=kv_dtype)
         self.v_cache = torch.zeros_like(self.k_cache)
         self.pos = 0
+
+    def use_fp8_lm_head(self) -> tuple[np.ndarray, np.ndarray]:
+        """Logits from the FP8 (e4m3, power-of-two row scales) copy of the tied
+        table, dequantised exactly (oracle/fp8.py); the embedding gather keeps
+        the bf16 table.  Returns (codes, scales)."""
+        from . import fp8
+        codes, scales = fp8.quantize_rows(self.embed.float().numpy())
+        self.lm_head = torch.from_numpy(fp8.dequantize_rows(codes, scales)).to(self.embed.dtype)
+        return codes, scales
 
     def reset(self) -> None:
         self.k_cache.zero_()
@@ -202,7 +212,7 @@ class Qwen3Oracle:
             if capture:
                 layers_out.append(x.clone())
         hf = rmsnorm(x, self.final_norm, s.eps)
-        logits = self._mv(self.embed, hf)
+        logits = self._mv(self.lm_head, hf)
         nxt = argmax_first(logits)
         self.pos += 1
         out = {"token": nxt}

@@ -187,6 +187,50 @@ def test_long_context_split_attention(ctx, chunk, merge):
         dw.free()
 
 
+def test_reconfigure_and_rewind_between_launches():
+    """The packed-pair hand-off words are not cleared before each launch, only
+    when the position moves back or the split / merge configuration changes.
+    Toggling the merge off for five tokens (the merged row's 4-bit tag then
+    repeats: 5 x 141 phases is a multiple of 15) and back on, then rewinding,
+    must still match the oracle and reproduce earlier steps bit for bit; a
+    rewound resident launch must equal per-token decoding from the same point."""
+    shape = BASELINE.with_(n_layers=2, vocab=2048)
+    ctx = 2000
+    eng, orc, dw = make_pair(shape, 31, ctx + 64)
+    try:
+        eng.set_attention_chunk(64)  # 32 splits per kv head at ctx 2000: above merge_min 20
+        eng.fill_kv_synthetic(ctx, 5)
+        ks = np.stack([synth.kv_prefill_bits(5, l, 0, ctx, shape.n_kv_heads, shape.head_dim)
+                       for l in range(shape.n_layers)])
+        vs = np.stack([synth.kv_prefill_bits(5, l, 1, ctx, shape.n_kv_heads, shape.head_dim)
+                       for l in range(shape.n_layers)])
+        orc.set_kv(ks, vs)
+        tok, first = 9, []
+        for i, merge in enumerate([20, 20, 20, 64, 64, 64, 64, 64, 20, 20]):
+            eng.set_attention_merge(merge)
+            _print(f"step {i} pos {eng.pos} merge_min {merge}")
+            nxt, layers, logits = eng.debug_forward(tok)
+            ref = orc.step(tok, capture=True)
+            check_step(layers, logits, ref, f"step {i} merge_min {merge}")
+            first.append((tok, logits))
+            tok = ref["token"]
+        # rewind to step 1 (same merge_min as then): bitwise the same step
+        eng.set_attention_merge(20)
+        eng.set_pos(ctx + 1)
+        _, _, again = eng.debug_forward(first[1][0])
+        assert np.array_equal(again, first[1][1]), "rewound step differs from the first pass"
+        eng.set_pos(ctx)
+        gen = eng.decode_many(first[0][0], 8)
+        eng.set_pos(ctx)
+        b = [eng.decode_token(first[0][0])]
+        for _ in range(7):
+            b.append(eng.decode_token(b[-1]))
+        assert gen == b, "rewound resident launch and per-token decode disagree"
+    finally:
+        eng.close()
+        dw.free()
+
+
 def test_full_baseline_model_parity():
     """The BASELINE model at full size (28 layers, vocab 151936)."""
     eng, orc, dw = make_pair(BASELINE, 2024, 64, gain_std=0.0, bits_from_device=True)
