@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--merge", type=int, default=0,
                     help="attention splits per kv head above which the first split merges them (0: library default)")
     ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--kv-fp8", action="store_true",
+                    help="FP8 (e4m3) KV cache with a power-of-two scale per K / V row")
     ap.add_argument("--lmhead-fp8", action="store_true",
                     help="stream the FP8 (e4m3, power-of-two row scales) copy of the LM head")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -474,6 +476,8 @@ def main():
         eng.set_attention_merge(args.merge)
     if args.lmhead_fp8:
         eng.set_lmhead_fp8(True)
+    if args.kv_fp8:
+        eng.set_kv_fp8(True)
     info = launcher.detect_gpu()
     grid = eng.grid_size
     print(f"# device {info['name']} CUs {info['cu_count']} grid {grid}", file=sys.stderr, flush=True)
@@ -497,9 +501,12 @@ def main():
     nbytes = sum(shape.token_bytes(args.ctx + i) for i in range(K))
     if args.lmhead_fp8:  # 1 byte per LM-head weight instead of 2, plus a 4-byte scale per row
         nbytes -= K * (shape.vocab * shape.hidden - 4 * shape.vocab)
+    if args.kv_fp8:  # per position: 1 byte per K / V value plus a 4-byte scale per row
+        kv8 = shape.kv_bytes_per_pos // 2 + 2 * 4 * shape.n_kv_heads * shape.n_layers
+        nbytes -= sum((shape.kv_bytes_per_pos - kv8) * (args.ctx + i + 2) for i in range(K))
     achieved = nbytes / kern / 1e9
     traffic = None
-    if os.path.exists(args.traffic_json) and not args.lmhead_fp8:
+    if os.path.exists(args.traffic_json) and not args.lmhead_fp8 and not args.kv_fp8:
         with open(args.traffic_json) as f:
             tj = json.load(f)
         if tj.get("ctx") == args.ctx and tj.get("tokens") == K:
@@ -524,14 +531,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 (LM head fp8 e4m3)" if args.lmhead_fp8 else "bf16",
+        "dtype": "bf16" + "".join(f" ({w} fp8 e4m3)" for w, on in (("LM head", args.lmhead_fp8),
+                                                                     ("KV cache", args.kv_fp8)) if on),
         "data": "synthetic",
         "config": {"workload": f"Qwen3-0.6B-shaped batch-1 greedy decode, KV prefilled to {args.ctx}, "
                                f"{K} tokens in one resident launch (BASELINE configs[2])",
                    "ctx": args.ctx, "tokens": K, "batch": 1, "layers": shape.n_layers,
                    "hidden": shape.hidden, "heads": "16q/8kv x 64", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "bf16 N(0,0.02) (Irwin-Hall(4) approx), unit norm gains" +
-                              ("; LM head streamed as fp8 e4m3 with power-of-two row scales" if args.lmhead_fp8 else ""),
+                              ("; LM head streamed as fp8 e4m3 with power-of-two row scales" if args.lmhead_fp8 else "") +
+                              ("; KV cache fp8 e4m3, power-of-two scale per K / V row" if args.kv_fp8 else ""),
                    "accumulation": "fp32", "reps": args.reps, "grid": grid,
                    "device": info["name"]},
         "kernel_ms_per_step": round(kern * 1e3 / K, 5),

@@ -148,6 +148,19 @@ int megakernel_set_attention_merge(void* handle, int merge_min);
  * Returns 0, or -1 (vocab not a multiple of 16, hidden not of 64, no memory). */
 int megakernel_set_lmhead_fp8(void* handle, int enable);
 
+/* FP8 KV cache (no counterpart in the reference kernel, which plans FP8 KV in
+ * RESEARCH.md:434-436,463).  enable = 1 switches the handle's cache to OCP e4m3
+ * codes with one power-of-two scale per (layer, kv head, position) row of K
+ * and of V (2^e, the smallest e with max|row| <= 448 * 2^e; values rounded to
+ * nearest even after the exact scaling), quantised as they are appended: half
+ * the attention bytes of a token.  The cache is emptied (as megakernel_reset)
+ * in either direction.  set_kv / get_kv / fill_kv_synthetic keep the bf16
+ * reference layout at the boundary (quantised on the way in, exact bf16 of
+ * code x scale on the way out).  Refused while a prefill context is attached
+ * (its kernels write bf16 K/V); megakernel_prefill_attach is refused on an FP8
+ * cache.  Returns 0 or -1. */
+int megakernel_set_kv_fp8(void* handle, int enable);
+
 /* The FP8 LM head as built: codes[V * H] row-major e4m3 bytes, scales[V]
  * (validation).  -1 when it has not been built. */
 int megakernel_get_lmhead_fp8(void* handle, unsigned char* codes, float* scales);

@@ -241,6 +241,11 @@ class MegakernelEngine:
         _lib.check(self.lib, self.lib.megakernel_set_lmhead_fp8(self._handle, int(bool(enable))),
                    "set_lmhead_fp8")
 
+    def set_kv_fp8(self, enable: bool = True):
+        """Switch the KV cache to FP8 (OCP e4m3, power-of-two scale per row of
+        K and V); the cache is emptied and the position reset."""
+        _lib.check(self.lib, self.lib.megakernel_set_kv_fp8(self._handle, int(bool(enable))), "set_kv_fp8")
+
     def lmhead_fp8(self):
         """(codes uint8 [V, H], scales float32 [V]) of the FP8 LM head."""
         s = self.shape

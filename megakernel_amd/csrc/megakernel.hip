@@ -78,11 +78,7 @@ __global__ __launch_bounds__(256) void lmhead_fp8_kernel(const u32x4* __restrict
   for (int c = j; c < K; c += 16) amax = fmaxf(amax, fabsf(elem(c)));
 #pragma unroll
   for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
-  int e = 0;
-  if (amax > 0.f) {
-    e = ilogbf(amax) - 8;  // 448 = 1.75 * 2^8
-    if (amax > ldexpf(448.f, e)) ++e;
-  }
+  const int e = e4m3_row_exp(amax);
   unsigned char* d = dst + rb * KT8 * 1024;
   for (int c = j; c < K; c += 16)
     d[(c >> 6) * 1024 + (((c >> 4) & 3) * 16 + r) * 16 + (c & 15)] = (unsigned char)e4m3_encode(ldexpf(elem(c), -e));
@@ -137,6 +133,70 @@ __global__ void kv_convert_kernel(uint16_t* __restrict__ buf, uint16_t* __restri
   }
 }
 
+// FP8 KV cache (no counterpart in the reference, which plans FP8 KV in
+// RESEARCH.md:434-436,463): rows of the reference layout buf [L][2][NKV][len][D]
+// (bf16) <-> e4m3 codes at the cache's element indices read as byte indices,
+// one power-of-two scale per (layer, kv head, position) row of K and of V.
+// Quantisation as the kernel's append: 2^e with the smallest e such that
+// max|row| <= 448 * 2^e, codes rounded to nearest even after exact scaling.
+__global__ void kv_quant_kernel(const uint16_t* __restrict__ buf, uint8_t* __restrict__ k8, uint8_t* __restrict__ v8,
+                                float* __restrict__ ks, float* __restrict__ vs, int L, int NKV, int s_pad, int D,
+                                int len) {
+  const unsigned long long rows = 2ull * L * NKV * (unsigned long long)len;
+  for (unsigned long long r = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; r < rows;
+       r += (unsigned long long)gridDim.x * blockDim.x) {
+    const long long t = (long long)(r % len);
+    const int g = (int)((r / len) % NKV);
+    const unsigned long long plane = r / ((unsigned long long)len * NKV);  // layer*2 + kv
+    const int l = (int)(plane / 2), kv = (int)(plane % 2);
+    const uint16_t* src = buf + r * D;
+    float amax = 0.f;
+    for (int d = 0; d < D; ++d) amax = fmaxf(amax, fabsf(bf16_to_f32(src[d])));
+    const int e = e4m3_row_exp(amax);
+    for (int d = 0; d < D; ++d) {
+      const uint8_t code = (uint8_t)e4m3_encode(ldexpf(bf16_to_f32(src[d]), -e));
+      if (kv == 0) k8[k_index(l, g, t, d, NKV, s_pad, D)] = code;
+      else v8[vt_index(l, g, t, d, NKV, s_pad, D)] = code;
+    }
+    (kv == 0 ? ks : vs)[((long long)l * NKV + g) * s_pad + t] = ldexpf(1.f, e);
+  }
+}
+
+// FP8 cache -> reference layout, bf16 of code x scale (exact).
+__global__ void kv_dequant_kernel(uint16_t* __restrict__ buf, const uint8_t* __restrict__ k8,
+                                  const uint8_t* __restrict__ v8, const float* __restrict__ ks,
+                                  const float* __restrict__ vs, int L, int NKV, int s_pad, int D, int len) {
+  const unsigned long long total = 2ull * L * NKV * (unsigned long long)len * D;
+  for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (unsigned long long)gridDim.x * blockDim.x) {
+    const int d = (int)(i % D);
+    const long long t = (long long)((i / D) % len);
+    const int g = (int)((i / ((unsigned long long)D * len)) % NKV);
+    const unsigned long long plane = i / ((unsigned long long)D * len * NKV);
+    const int l = (int)(plane / 2), kv = (int)(plane % 2);
+    const unsigned code = kv == 0 ? k8[k_index(l, g, t, d, NKV, s_pad, D)] : v8[vt_index(l, g, t, d, NKV, s_pad, D)];
+    const float sc = (kv == 0 ? ks : vs)[((long long)l * NKV + g) * s_pad + t];
+    buf[i] = f32_to_bf16(__builtin_amdgcn_cvt_pk_f32_fp8((int)code, false)[0] * sc);
+  }
+}
+
+// Synthetic KV of positions [0, len) in the reference layout (the values of
+// synth_kv_kernel).
+__global__ void synth_kv_ref_kernel(uint16_t* __restrict__ buf, int L, int NKV, int D, int len,
+                                    unsigned long long seed, float c) {
+  const unsigned long long per = (unsigned long long)len * NKV * D;
+  const unsigned long long total = per * 2ull * L;
+  for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (unsigned long long)gridDim.x * blockDim.x) {
+    const unsigned long long plane = i / per;
+    const unsigned long long e = i % per;  // (t*NKV + g)*D + d
+    const int d = (int)(e % D);
+    const int g = (int)((e / D) % NKV);
+    const long long t = (long long)(e / ((unsigned long long)D * NKV));
+    buf[((plane * NKV + g) * (unsigned long long)len + t) * D + d] = synth_bf16(sm_h(seed, 0x40000000ull + plane), e, c, 0);
+  }
+}
+
 // -------------------------------------------------------------- the handle
 struct ShapeInfo {
   int H, NQ, NKV, D, F, QD, KVD, QKV, GQA;
@@ -171,6 +231,8 @@ struct Handle {
   u32x4* lmhead8 = nullptr;  // optional FP8 copy of the LM head, built on request
   float* lm_scale = nullptr;
   bool lm_fp8 = false;       // the LM head reads lmhead8
+  float *kscale = nullptr, *vscale = nullptr;  // FP8 KV cache: row scales [L][NKV][s_pad]
+  bool kv_fp8 = false;       // the cache holds e4m3 codes (byte index = bf16 element index)
   uint16_t* kv = nullptr;
   u64 *x = nullptr, *qkv = nullptr, *part = nullptr, *act = nullptr;
   u64* amax = nullptr;
@@ -203,7 +265,8 @@ static void launch_mode(Handle* h, const Params& p) {
 
 template <class S>
 static hipError_t launch_decode(Handle* h, const Params& p, bool lc) {
-  const int mode = (lc ? 1 : 0) | (p.trace || p.dbg_layers || p.dbg_logits ? 2 : 0) | (p.lmhead8 ? 4 : 0);
+  const int mode = (lc ? 1 : 0) | (p.trace || p.dbg_layers || p.dbg_logits ? 2 : 0) | (p.lmhead8 ? 4 : 0) |
+                   (p.kscale ? 8 : 0);
   switch (mode) {
     case 0: launch_mode<S, 0>(h, p); break;
     case 1: launch_mode<S, 1>(h, p); break;
@@ -212,7 +275,15 @@ static hipError_t launch_decode(Handle* h, const Params& p, bool lc) {
     case 4: launch_mode<S, 4>(h, p); break;
     case 5: launch_mode<S, 5>(h, p); break;
     case 6: launch_mode<S, 6>(h, p); break;
-    default: launch_mode<S, 7>(h, p); break;
+    case 7: launch_mode<S, 7>(h, p); break;
+    case 8: launch_mode<S, 8>(h, p); break;
+    case 9: launch_mode<S, 9>(h, p); break;
+    case 10: launch_mode<S, 10>(h, p); break;
+    case 11: launch_mode<S, 11>(h, p); break;
+    case 12: launch_mode<S, 12>(h, p); break;
+    case 13: launch_mode<S, 13>(h, p); break;
+    case 14: launch_mode<S, 14>(h, p); break;
+    default: launch_mode<S, 15>(h, p); break;
   }
   return hipGetLastError();
 }
@@ -226,17 +297,19 @@ static int occupancy_of() {
 
 template <class S>
 static int occupancy_ok(int* nblk) {
-  const int n[8] = {occupancy_of<S, 0>(), occupancy_of<S, 1>(), occupancy_of<S, 2>(), occupancy_of<S, 3>(),
-                    occupancy_of<S, 4>(), occupancy_of<S, 5>(), occupancy_of<S, 6>(), occupancy_of<S, 7>()};
+  const int n[16] = {occupancy_of<S, 0>(),  occupancy_of<S, 1>(),  occupancy_of<S, 2>(),  occupancy_of<S, 3>(),
+                     occupancy_of<S, 4>(),  occupancy_of<S, 5>(),  occupancy_of<S, 6>(),  occupancy_of<S, 7>(),
+                     occupancy_of<S, 8>(),  occupancy_of<S, 9>(),  occupancy_of<S, 10>(), occupancy_of<S, 11>(),
+                     occupancy_of<S, 12>(), occupancy_of<S, 13>(), occupancy_of<S, 14>(), occupancy_of<S, 15>()};
   *nblk = n[0];
-  for (int i = 1; i < 8; ++i) *nblk = n[i] < *nblk ? n[i] : *nblk;
+  for (int i = 1; i < 16; ++i) *nblk = n[i] < *nblk ? n[i] : *nblk;
   return 1;
 }
 
 static void free_all(Handle* h) {
   batch::destroy_prefill_context(h->prefill);
   h->prefill = nullptr;
-  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->kv, h->x, h->qkv, h->part,
+  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->kscale, h->vscale, h->kv, h->x, h->qkv, h->part,
                   h->act, h->amax, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
@@ -443,6 +516,8 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.lmhead = h->lmhead;
   p.lmhead8 = h->lm_fp8 ? h->lmhead8 : nullptr;
   p.lm_scale = h->lm_fp8 ? h->lm_scale : nullptr;
+  p.kscale = h->kv_fp8 ? h->kscale : nullptr;
+  p.vscale = h->kv_fp8 ? h->vscale : nullptr;
   p.kv = h->kv;
   p.kvt = h->kvt;
   p.s_pad = h->s_pad;
@@ -545,6 +620,11 @@ void megakernel_reset(void* handle) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return;
   (void)hipMemsetAsync(h->kv, 0, h->kv_bytes, h->stream);
+  if (h->kscale) {
+    const size_t sb = (size_t)h->L * h->sh.NKV * h->s_pad * 4;
+    (void)hipMemsetAsync(h->kscale, 0, sb, h->stream);
+    (void)hipMemsetAsync(h->vscale, 0, sb, h->stream);
+  }
   (void)mk::clear_pair_words(h);
   h->pos = 0;
 }
@@ -646,8 +726,17 @@ static int kv_transfer(Handle* h, void* host_kv, int len, int to_cache) {
       mk::set_err("KV upload failed");
       break;
     }
-    hipLaunchKernelGGL(mk::kv_convert_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
-                       h->kv, h->kvt, h->L, h->sh.NKV, h->s_pad, h->sh.D, len, to_cache);
+    if (h->kv_fp8 && to_cache)
+      hipLaunchKernelGGL(mk::kv_quant_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                         reinterpret_cast<uint8_t*>(h->kv), reinterpret_cast<uint8_t*>(h->kvt), h->kscale, h->vscale,
+                         h->L, h->sh.NKV, h->s_pad, h->sh.D, len);
+    else if (h->kv_fp8)
+      hipLaunchKernelGGL(mk::kv_dequant_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                         reinterpret_cast<const uint8_t*>(h->kv), reinterpret_cast<const uint8_t*>(h->kvt), h->kscale,
+                         h->vscale, h->L, h->sh.NKV, h->s_pad, h->sh.D, len);
+    else
+      hipLaunchKernelGGL(mk::kv_convert_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                         h->kv, h->kvt, h->L, h->sh.NKV, h->s_pad, h->sh.D, len, to_cache);
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(h->stream) != hipSuccess) {
       mk::set_err("KV layout conversion failed");
       break;
@@ -690,7 +779,22 @@ int megakernel_fill_kv_synthetic(void* handle, int len, unsigned long long seed,
     mk::set_err("invalid fill_kv arguments (len %d)", len);
     return -1;
   }
-  if (len > 0) {
+  if (len > 0 && h->kv_fp8) {  // the bf16 values in the reference layout, then quantised rows
+    const float c = (float)(std * sqrt(3.0) / 65536.0);
+    void* stage = nullptr;
+    HIPCHK(hipMalloc(&stage, (size_t)2 * h->L * h->sh.NKV * (size_t)len * h->sh.D * 2), -1);
+    hipLaunchKernelGGL(mk::synth_kv_ref_kernel, dim3(4096), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                       h->L, h->sh.NKV, h->sh.D, len, seed, c);
+    hipLaunchKernelGGL(mk::kv_quant_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<const uint16_t*>(stage),
+                       reinterpret_cast<uint8_t*>(h->kv), reinterpret_cast<uint8_t*>(h->kvt), h->kscale, h->vscale,
+                       h->L, h->sh.NKV, h->s_pad, h->sh.D, len);
+    const hipError_t e = hipGetLastError() == hipSuccess ? hipStreamSynchronize(h->stream) : hipErrorLaunchFailure;
+    (void)hipFree(stage);
+    if (e != hipSuccess) {
+      mk::set_err("FP8 KV fill failed: %s", hipGetErrorString(e));
+      return -1;
+    }
+  } else if (len > 0) {
     const float c = (float)(std * sqrt(3.0) / 65536.0);
     hipLaunchKernelGGL(mk::synth_kv_kernel, dim3(4096), dim3(256), 0, h->stream, h->kv, h->kvt, h->L, h->sh.NKV,
                        h->s_pad, h->sh.D, len, seed, c);
@@ -743,6 +847,10 @@ int megakernel_prefill_attach(void* handle, void* d_weights, const long long* of
     return -1;
   }
   if (h->prefill) return 0;
+  if (h->kv_fp8) {
+    mk::set_err("prefill context: the handle's KV cache is FP8 (the prefill kernels write bf16 K/V)");
+    return -1;
+  }
   const char* w = static_cast<const char*>(d_weights);
   if (!w) {  // the library's own upload (megakernel_init_from_host) with the init offsets
     if (!h->owned_flat) {
@@ -819,6 +927,26 @@ int megakernel_set_lmhead_fp8(void* handle, int enable) {
     HIPCHK(hipStreamSynchronize(h->stream), -1);
   }
   h->lm_fp8 = enable != 0;
+  return 0;
+}
+
+int megakernel_set_kv_fp8(void* handle, int enable) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  if (enable && h->prefill) {
+    mk::set_err("the FP8 KV cache is not available with a prefill context attached (it writes bf16 K/V)");
+    return -1;
+  }
+  if (enable && !h->kscale) {
+    const size_t sb = (size_t)h->L * h->sh.NKV * h->s_pad * 4;
+    HIPCHK(hipMalloc(&h->kscale, sb), -1);
+    HIPCHK(hipMalloc(&h->vscale, sb), -1);
+  }
+  h->kv_fp8 = enable != 0;
+  megakernel_reset(h);  // a new, empty cache in the chosen format
   return 0;
 }
 

@@ -7,6 +7,7 @@
 namespace mk {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -81,6 +82,38 @@ __device__ __forceinline__ float dot16_fp8(u32x4 w, const float* h, float acc) {
     acc = fmaf(hi[1], h[4 * i + 3], acc);
   }
   return acc;
+}
+
+// 8 FP8 (OCP e4m3) values -> 8 bf16 in the same order.  Exact: an e4m3 value
+// has 4 significant bits, so its fp32 form has zero low halves.
+__device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 r) {
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[i], false);
+    const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[i], true);
+    o[2 * i] = pack_hi16(__float_as_uint(a[0]), __float_as_uint(a[1]));
+    o[2 * i + 1] = pack_hi16(__float_as_uint(b[0]), __float_as_uint(b[1]));
+  }
+  return o;
+}
+
+// u32x2 holding 8 bytes with byte e (0..7) replaced by v (register-only).
+__device__ __forceinline__ u32x2 set_u8(u32x2 x, int e, unsigned v) {
+  const unsigned sh = 8u * (unsigned)(e & 3);
+  u32x2 r = x;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) r[c] = (c == (e >> 2)) ? ((x[c] & ~(0xffu << sh)) | (v << sh)) : x[c];
+  return r;
+}
+
+// Power-of-two scale exponent of a row with absolute maximum amax: the
+// smallest e with amax <= 448 * 2^e (0 for an all-zero row).
+__device__ __forceinline__ int e4m3_row_exp(float amax) {
+  if (!(amax > 0.f)) return 0;
+  int e = ilogbf(amax) - 8;  // 448 = 1.75 * 2^8
+  if (amax > ldexpf(448.f, e)) ++e;
+  return e;
 }
 
 // OCP e4m3 (bias 7, largest finite 448, no infinities) of x, |x| <= 448,

@@ -26,6 +26,8 @@
 // arrive, and computes the current phase from registers loaded one phase
 // earlier.  The wait for the next inputs therefore overlaps the HBM transfer.
 #pragma once
+#include <type_traits>
+
 #include "mk_config.h"
 #include "mk_device.h"
 
@@ -64,6 +66,9 @@ struct Params {
   const u32x4* lmhead;        // packed tied embedding [V/16][KT_H][64]
   const u32x4* lmhead8;       // optional FP8 (e4m3) copy of the LM head [V/16][H/64][64]
   const float* lm_scale;      // [V] power-of-two row scales of lmhead8
+  float* kscale;              // FP8 KV cache (MODE bit 3): power-of-two scale of each K row
+  float* vscale;              //   and V row, [L][NKV][s_pad]; the codes replace the bf16 values
+                              //   at byte index = element index of kv / kvt
   uint16_t* kv;               // K cache [L][NKV][s_pad][D] bf16
   uint16_t* kvt;              // V cache, transposed blocks [L][NKV][s_pad/32][D][32] bf16
   u64* x;                     // [H] residual stream (tagged)
@@ -104,7 +109,8 @@ struct Smem {
   float rowbuf[4][16];                // a block's 16 results, stored by one wave
   __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score A operand
   __attribute__((aligned(16))) uint16_t pb[NW][16][32 * KVB];  // attention: weight parts, output A operand
-  u32x4 kvcur[2][S::D / 8];           // bf16 K/V of the current position
+  u32x4 kvcur[2][S::D / 8];           // bf16 (FP8 cache: e4m3 codes) K/V of the current position
+  float kvcs[2];                      // FP8 cache: scales of the current K / V rows
   __attribute__((aligned(16))) float pv[NW][S::GQA * S::D];  // attention: per-wave unnormalised outputs
   float mw[S::GQA][NW], lw[S::GQA][NW];  // attention: per-wave max / sum per q head
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
@@ -529,12 +535,15 @@ __device__ __forceinline__ bool fetch1(u64* src, int n, float* dst, unsigned tag
 // them in-register and own 16 positions (resp. dims) of head j each.
 // A work item (kv head g, split s) covers whole 32-position blocks
 // [t0, t1); wave w takes the item's blocks w, w + NW, ...
-template <class S>
+template <class S, bool K8 = false>
 struct KV {
   static constexpr int KC = S::D / 32;  // k-steps of the score product
   static constexpr int DT = S::D / 16;  // dim tiles of the output product
-  u32x4 k[KVB][2][KC];  // K of the wave's blocks: [block][16-position half][k-step]
-  u32x4 v[KVB][DT];     // V^T of the blocks: [block][dim tile]
+  // 8 values per lane and operand: bf16 (u32x4) or, for an FP8 cache, e4m3 codes (u32x2)
+  using Reg = typename std::conditional<K8, u32x2, u32x4>::type;
+  Reg k[KVB][2][KC];  // K of the wave's blocks: [block][16-position half][k-step]
+  Reg v[KVB][DT];     // V^T of the blocks: [block][dim tile]
+  float sk[K8 ? KVB : 1][2], sv[K8 ? KVB : 1][2];  // FP8: scales of the lane's score positions
   uint16_t gn[S::D / kWave];  // QK-norm gain(s) of this lane's dim(s) for its wave's head
 };
 
@@ -567,8 +576,8 @@ __device__ __forceinline__ u32x4 buf_ld_kv(__amdgpu_buffer_rsrc_t rs, unsigned v
 // Loads this wave's KVB blocks of an item starting at block index `bi`
 // (item blocks bi, bi + NW, ...; blocks past the item's nb repeat a valid
 // block and are masked by the caller).
-template <class S>
-__device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, int g, int b0, int nb, int bi) {
+template <class S, bool K8>
+__device__ __forceinline__ void kv_load(KV<S, K8>& r, const Params& p, int layer, int g, int b0, int nb, int bi) {
   constexpr int D = S::D;
   const unsigned l = lane_id();
   const long long base = kt_base(p, layer, g, S::NKV, D);
@@ -576,29 +585,58 @@ __device__ __forceinline__ void kv_load(KV<S>& r, const Params& p, int layer, in
   for (int q = 0; q < KVB; ++q) {
     const int bq = bi + q * NW;
     const int blk = b0 + (bq < nb ? bq : 0);
-    const auto rk = make_rsrc(p.kv + base + (long long)blk * 32 * D);
-    const auto rv = make_rsrc(p.kvt + base + (long long)blk * 32 * D);
+    if constexpr (K8) {  // byte index = element index of the bf16 layout
+      const auto rk = make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + base + (long long)blk * 32 * D);
+      const auto rv = make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + base + (long long)blk * 32 * D);
+      const long long sb = ((long long)layer * S::NKV + g) * p.s_pad + (long long)blk * 32;
+      const auto rks = make_rsrc(p.kscale + sb);
+      const auto rvs = make_rsrc(p.vscale + sb);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int kc = 0; kc < KV<S>::KC; ++kc)
-        r.k[q][h][kc] = buf_ld_kv(rk, ((16u * h + (l & 15u)) * D + 32u * kc + 8u * (l >> 4)) * 2u);
+        for (int kc = 0; kc < KV<S, K8>::KC; ++kc)
+          r.k[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b64(
+              rk, (16u * h + (l & 15u)) * D + 32u * kc + 8u * (l >> 4), 0u, 16 | 2);
+        r.sk[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rks, (16u * h + (l & 15u)) * 4u, 0u, 16 | 2));
+        r.sv[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rvs, (16u * h + (l & 15u)) * 4u, 0u, 16 | 2));
+      }
 #pragma unroll
-    for (int dt = 0; dt < KV<S>::DT; ++dt)
-      r.v[q][dt] = buf_ld_kv(rv, ((16u * dt + (l & 15u)) * 32u + 8u * (l >> 4)) * 2u);
+      for (int dt = 0; dt < KV<S, K8>::DT; ++dt)
+        r.v[q][dt] = __builtin_amdgcn_raw_buffer_load_b64(rv, (16u * dt + (l & 15u)) * 32u + 8u * (l >> 4), 0u, 16 | 2);
+    } else {
+      const auto rk = make_rsrc(p.kv + base + (long long)blk * 32 * D);
+      const auto rv = make_rsrc(p.kvt + base + (long long)blk * 32 * D);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kc = 0; kc < KV<S, K8>::KC; ++kc)
+          r.k[q][h][kc] = buf_ld_kv(rk, ((16u * h + (l & 15u)) * D + 32u * kc + 8u * (l >> 4)) * 2u);
+#pragma unroll
+      for (int dt = 0; dt < KV<S, K8>::DT; ++dt)
+        r.v[q][dt] = buf_ld_kv(rv, ((16u * dt + (l & 15u)) * 32u + 8u * (l >> 4)) * 2u);
+    }
   }
 }
 
-template <class S>
-__device__ __forceinline__ void kv_forget(KV<S>& r) {
+template <class S, bool K8>
+__device__ __forceinline__ void kv_forget(KV<S, K8>& r) {
 #pragma unroll
   for (int q = 0; q < KVB; ++q) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int kc = 0; kc < KV<S>::KC; ++kc) r.k[q][h][kc] = __builtin_nondeterministic_value(r.k[q][h][kc]);
+      for (int kc = 0; kc < KV<S, K8>::KC; ++kc) r.k[q][h][kc] = __builtin_nondeterministic_value(r.k[q][h][kc]);
 #pragma unroll
-    for (int dt = 0; dt < KV<S>::DT; ++dt) r.v[q][dt] = __builtin_nondeterministic_value(r.v[q][dt]);
+    for (int dt = 0; dt < KV<S, K8>::DT; ++dt) r.v[q][dt] = __builtin_nondeterministic_value(r.v[q][dt]);
+  }
+  if constexpr (K8) {
+#pragma unroll
+    for (int q = 0; q < KVB; ++q)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        r.sk[q][h] = __builtin_nondeterministic_value(r.sk[q][h]);
+        r.sv[q][h] = __builtin_nondeterministic_value(r.sv[q][h]);
+      }
   }
 #pragma unroll
   for (int c = 0; c < S::D / kWave; ++c) r.gn[c] = __builtin_nondeterministic_value(r.gn[c]);
@@ -606,8 +644,8 @@ __device__ __forceinline__ void kv_forget(KV<S>& r) {
 
 // QK-norm gains of this lane's dims: waves 0..GQA-1 normalise q heads, wave
 // GQA the k head.
-template <class S>
-__device__ __forceinline__ void gain_load_qk(KV<S>& r, const Params& p, int layer) {
+template <class S, bool K8>
+__device__ __forceinline__ void gain_load_qk(KV<S, K8>& r, const Params& p, int layer) {
   const int t_ = ltid(), w = t_ / kWave, l = t_ % kWave;
   const uint16_t* g = p.norms + (long long)layer * S::NORM_STRIDE + (w < S::GQA ? S::NORM_Q : S::NORM_K);
 #pragma unroll
@@ -658,8 +696,35 @@ __device__ __forceinline__ Item att_item(int it, int n, int nkv, int chunk_min, 
 //   and, in the split that owns pos, append them to the cache (reference
 //   kv_cache.cuh:58-78; write-through agent-scope stores, read by later
 //   tokens on any XCD).
+// FP8 cache append of one K or V row (D values, DPL per lane of one wave):
+// the power-of-two scale from the wave's absolute maximum, the e4m3 codes
+// (dim d at byte dst[d * stride]) and the scale, written through to the
+// device-coherent level; the codes and the scale also go to LDS for this
+// token's own attention.
+template <int DPL>
+__device__ __forceinline__ void kv_append_fp8(const float* val, uint8_t* dst, int stride, float* scale_dst,
+                                              uint8_t* lds_codes, float* lds_scale, bool append) {
+  const int l = (int)lane_id();
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) amax = fmaxf(amax, fabsf(val[c]));
+  const int e = e4m3_row_exp(wave_max(amax));
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) {
+    const uint8_t code = (uint8_t)e4m3_encode(ldexpf(val[c], -e));
+    lds_codes[l + c * kWave] = code;
+    if (append)
+      __hip_atomic_store(dst + (long long)(l + c * kWave) * stride, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (l == 0) {
+    *lds_scale = ldexpf(1.f, e);
+    if (append) __hip_atomic_store(scale_dst, ldexpf(1.f, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 template <class S, int MODE>
-__device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm, const KV<S>& kvr, int layer,
+__device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm, const KV<S, (MODE & 8) != 0>& kvr,
+                                                   int layer,
                                                    int pos, int g, bool own, unsigned tg, int tt) {
   constexpr int D = S::D, GQA = S::GQA, DPL = D / kWave;
   const int w = wave_id();
@@ -721,6 +786,10 @@ __device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm,
         sm.qb[4 * w + 1][l + c * kWave] = mid;
         sm.qb[4 * w + 2][l + c * kWave] = lo;
       }
+    } else if constexpr ((MODE & 8) != 0) {
+      kv_append_fp8<DPL>(o, reinterpret_cast<uint8_t*>(p.kv) + base + (long long)pos * D, 1,
+                         p.kscale + ((long long)layer * S::NKV + g) * p.s_pad + pos,
+                         reinterpret_cast<uint8_t*>(sm.kvcur[0]), &sm.kvcs[0], append);
     } else {
       uint16_t* krow = p.kv + base + (long long)pos * D;
 #pragma unroll
@@ -731,13 +800,19 @@ __device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm,
       }
     }
   } else if (w == GQA + 1) {
-    uint16_t* vt = p.kvt + base + (long long)(pos / 32) * 32 * D + (pos % 32);
+    if constexpr ((MODE & 8) != 0) {
+      kv_append_fp8<DPL>(v, reinterpret_cast<uint8_t*>(p.kvt) + base + (long long)(pos / 32) * 32 * D + (pos % 32), 32,
+                         p.vscale + ((long long)layer * S::NKV + g) * p.s_pad + pos,
+                         reinterpret_cast<uint8_t*>(sm.kvcur[1]), &sm.kvcs[1], append);
+    } else {
+      uint16_t* vt = p.kvt + base + (long long)(pos / 32) * 32 * D + (pos % 32);
 #pragma unroll
-    for (int c = 0; c < DPL; ++c) {
-      const uint16_t vb = f32_to_bf16(v[c]);
-      reinterpret_cast<uint16_t*>(sm.kvcur[1])[l + c * kWave] = vb;
-      if (append)
-        __hip_atomic_store(vt + (long long)(l + c * kWave) * 32, vb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int c = 0; c < DPL; ++c) {
+        const uint16_t vb = f32_to_bf16(v[c]);
+        reinterpret_cast<uint16_t*>(sm.kvcur[1])[l + c * kWave] = vb;
+        if (append)
+          __hip_atomic_store(vt + (long long)(l + c * kWave) * 32, vb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
   return !block_failed(failed);
@@ -754,9 +829,10 @@ __device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit,
 // workgroup merges them; without it that code is not compiled in).  K / V of
 // the wave's first blocks are already in kvr.
 template <class S, int MODE>
-__device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int layer, int pos, int g, int s,
-                                  int nsplit, int t0, int t1, unsigned tg, int tt) {
-  constexpr int D = S::D, GQA = S::GQA, KC = KV<S>::KC, DT = KV<S>::DT;
+__device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S, (MODE & 8) != 0>& kvr, int layer, int pos,
+                                  int g, int s, int nsplit, int t0, int t1, unsigned tg, int tt) {
+  constexpr bool K8 = (MODE & 8) != 0;
+  constexpr int D = S::D, GQA = S::GQA, KC = KV<S, K8>::KC, DT = KV<S, K8>::DT;
   static_assert(GQA <= 4, "q heads of a group fit the 16 MFMA rows (4 per head)");
   if (!attention_prologue<S, MODE>(p, sm, kvr, layer, pos, g, t0 <= pos && pos < t1, tg, tt)) return false;
   evt(p, tt, layer, EV_ATT_ROPE);
@@ -782,16 +858,33 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
       const int bp = 32 * (b0 + bi + q * NW);
       if (bi + q * NW < nb && bp <= pos && pos < bp + 32) {
         const int rp = pos - bp;
-        if (c16 == (rp & 15)) {
+        if constexpr (K8) {
+          if (c16 == (rp & 15)) {
+            const u32x2* kc8 = reinterpret_cast<const u32x2*>(sm.kvcur[0]);
 #pragma unroll
-          for (int kc = 0; kc < KC; ++kc)
-            if (rp >> 4) kvr.k[q][1][kc] = sm.kvcur[0][4 * kc + rg];
-            else kvr.k[q][0][kc] = sm.kvcur[0][4 * kc + rg];
-        }
-        if (rg == (rp >> 3)) {
-          const uint16_t* vc = reinterpret_cast<const uint16_t*>(sm.kvcur[1]);
+            for (int kc = 0; kc < KC; ++kc)
+              if (rp >> 4) kvr.k[q][1][kc] = kc8[4 * kc + rg];
+              else kvr.k[q][0][kc] = kc8[4 * kc + rg];
+            if (rp >> 4) kvr.sk[q][1] = sm.kvcs[0], kvr.sv[q][1] = sm.kvcs[1];
+            else kvr.sk[q][0] = sm.kvcs[0], kvr.sv[q][0] = sm.kvcs[1];
+          }
+          if (rg == (rp >> 3)) {
+            const uint8_t* vc = reinterpret_cast<const uint8_t*>(sm.kvcur[1]);
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) kvr.v[q][dt] = set_bf16(kvr.v[q][dt], rp & 7, vc[16 * dt + c16]);
+            for (int dt = 0; dt < DT; ++dt) kvr.v[q][dt] = set_u8(kvr.v[q][dt], rp & 7, vc[16 * dt + c16]);
+          }
+        } else {
+          if (c16 == (rp & 15)) {
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc)
+              if (rp >> 4) kvr.k[q][1][kc] = sm.kvcur[0][4 * kc + rg];
+              else kvr.k[q][0][kc] = sm.kvcur[0][4 * kc + rg];
+          }
+          if (rg == (rp >> 3)) {
+            const uint16_t* vc = reinterpret_cast<const uint16_t*>(sm.kvcur[1]);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) kvr.v[q][dt] = set_bf16(kvr.v[q][dt], rp & 7, vc[16 * dt + c16]);
+          }
         }
       }
     }
@@ -804,10 +897,15 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
       for (int h = 0; h < 2; ++h) {
         f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc)
+        for (int kc = 0; kc < KC; ++kc) {
+          u32x4 kb;
+          if constexpr (K8) kb = fp8x8_to_bf16x8(kvr.k[q][h][kc]);
+          else kb = kvr.k[q][h][kc];
           d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[kc]),
-                                                      __builtin_bit_cast(bf16x8, kvr.k[q][h][kc]), d4, 0, 0, 0);
-        const float v = (d4[0] + d4[1]) + d4[2];
+                                                      __builtin_bit_cast(bf16x8, kb), d4, 0, 0, 0);
+        }
+        float v = (d4[0] + d4[1]) + d4[2];
+        if constexpr (K8) v *= kvr.sk[q][h];  // exact: a power of two
         const int t = 32 * (b0 + bi + q * NW) + 16 * h + c16;
         sc[q][h] = (bi + q * NW < nb && t < t1) ? v * scale : -INFINITY;
         bmax = fmaxf(bmax, sc[q][h]);
@@ -832,7 +930,8 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
       for (int q = 0; q < KVB; ++q)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const Split3 a = split3(sc[q][h]);
+          // FP8 cache: the V row's scale enters with the weight (the sum above stays unscaled)
+          const Split3 a = split3(K8 ? sc[q][h] * kvr.sv[q][h] : sc[q][h]);
           const int o = 32 * q + 16 * h + c16;
           sm.pb[w][4 * rg + 0][o] = (uint16_t)(a.hi >> 16);
           sm.pb[w][4 * rg + 1][o] = (uint16_t)(a.mid >> 16);
@@ -849,8 +948,13 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S>& kvr, int 
       for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
 #pragma unroll
       for (int q = 0; q < KVB; ++q)
+      {
+        u32x4 vb;
+        if constexpr (K8) vb = fp8x8_to_bf16x8(kvr.v[q][dt]);
+        else vb = kvr.v[q][dt];
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa[q]),
-                                                         __builtin_bit_cast(bf16x8, kvr.v[q][dt]), acc[dt], 0, 0, 0);
+                                                         __builtin_bit_cast(bf16x8, vb), acc[dt], 0, 0, 0);
+      }
     }
   }
   evt(p, tt, layer, EV_ATT_SOFTMAX);
@@ -1094,12 +1198,13 @@ __device__ __forceinline__ bool token_from_slots(const Params& p, u64* slots, un
 // splits per kv head (long-context merge and deferred K/V prefetch compiled
 // in); bit 1 (DBG): per-phase timestamps and the validation outputs
 // (dbg_layers, dbg_logits) compiled in; bit 2 (F8): the LM head streams the
-// FP8 copy (lmhead8, lm_scale) instead of the bf16 tiles.  The host picks the
-// instantiation per launch; the plain one carries none (fewer live scalar
-// values).
+// FP8 copy (lmhead8, lm_scale) instead of the bf16 tiles; bit 3 (K8): the KV
+// cache holds e4m3 codes with a power-of-two scale per row (kscale, vscale).
+// The host picks the instantiation per launch; the plain one carries none
+// (fewer live scalar values).
 template <class S, int MODE>
 __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
-  constexpr bool LC = (MODE & 1) != 0, DBG = (MODE & 2) != 0, F8 = (MODE & 4) != 0;
+  constexpr bool LC = (MODE & 1) != 0, DBG = (MODE & 2) != 0, F8 = (MODE & 4) != 0, K8 = (MODE & 8) != 0;
   __shared__ Smem<S> sm;
   if (threadIdx.x == 0) wg_abort = 0;
   for (int i = threadIdx.x; i < 16 * S::D; i += NT) (&sm.qb[0][0])[i] = 0;  // unused columns stay 0
@@ -1118,7 +1223,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
   const int it_att = first_item(wg, off_att, G);
 
   Blk<S::KC_H> rq;      // QKV block
-  KV<S> rkv;            // attention K/V sub-chunk
+  KV<S, K8> rkv;        // attention K/V sub-chunk
   Blk<S::KC_Q> ro;      // O block
   Blk<S::KC_H> rg, ru;  // gate / up blocks
   Blk<S::KC_F> rd;      // down block

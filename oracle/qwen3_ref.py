@@ -135,7 +135,7 @@ class Qwen3Oracle:
 
     def __init__(self, shape: Shape, bits: dict[str, np.ndarray], max_seq: int,
                  matmul_dtype: torch.dtype = torch.float32,
-                 kv_dtype: torch.dtype = torch.bfloat16):
+                 kv_dtype: torch.dtype = torch.bfloat16, kv_fp8: bool = False):
         self.s = shape
         self.max_seq = max_seq
         f = lambda n: bits_to_torch(bits[n]).to(matmul_dtype)  # noqa: E731
@@ -153,8 +153,11 @@ class Qwen3Oracle:
                 w_gate=f(p + "w_gate"), w_up=f(p + "w_up"), w_down=f(p + "w_down")))
         # kv_dtype=bfloat16 is the reference policy; float32 exists only to
         # compare with an fp32-cache forward (the HF golden fixtures).
+        # kv_fp8: the cache holds the exact dequantised FP8 rows (oracle/fp8.py,
+        # one power-of-two scale per (layer, kv head, position) row of K and V).
+        self.kv_fp8 = kv_fp8
         self.k_cache = torch.zeros(shape.n_layers, shape.n_kv_heads, max_seq, shape.head_dim,
-                                   dtype=kv_dtype)
+                                   dtype=torch.float32 if kv_fp8 else kv_dtype)
         self.v_cache = torch.zeros_like(self.k_cache)
         self.pos = 0
 
@@ -175,9 +178,18 @@ class Qwen3Oracle:
     def set_kv(self, k_bits: np.ndarray, v_bits: np.ndarray) -> None:
         """k_bits, v_bits: bf16 bits [L][NKV][len][D] (canonical layout)."""
         n = k_bits.shape[2]
-        self.k_cache[:, :, :n] = bits_to_torch(k_bits).to(self.k_cache.dtype)
-        self.v_cache[:, :, :n] = bits_to_torch(v_bits).to(self.v_cache.dtype)
+        self.k_cache[:, :, :n] = self._kv_rows(bits_to_torch(k_bits).float())
+        self.v_cache[:, :, :n] = self._kv_rows(bits_to_torch(v_bits).float())
         self.pos = n
+
+    def _kv_rows(self, t: torch.Tensor) -> torch.Tensor:
+        """What the cache stores of K / V rows t[..., D]: the values (cast to
+        the cache dtype), or with kv_fp8 the dequantised e4m3 rows."""
+        if not self.kv_fp8:
+            return t.to(self.k_cache.dtype)
+        from . import fp8
+        rows = t.reshape(-1, t.shape[-1]).numpy()
+        return torch.from_numpy(fp8.dequantize_rows(*fp8.quantize_rows(rows))).reshape(t.shape)
 
     @staticmethod
     def _mv(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
@@ -200,8 +212,8 @@ class Qwen3Oracle:
             k = rmsnorm(k, w["k_norm"], s.eps)
             q = rope(q, pos, s.theta)
             k = rope(k, pos, s.theta)
-            self.k_cache[li, :, pos] = k.to(self.k_cache.dtype)
-            self.v_cache[li, :, pos] = v.to(self.v_cache.dtype)
+            self.k_cache[li, :, pos] = self._kv_rows(k)
+            self.v_cache[li, :, pos] = self._kv_rows(v)
             kc = self.k_cache[li, :, :pos + 1].float()
             vc = self.v_cache[li, :, :pos + 1].float()
             o = attention(q, kc, vc).reshape(-1)

@@ -19,7 +19,7 @@ def oracle_shape(s: ModelShape) -> olayout.Shape:
 
 
 def make_pair(shape: ModelShape, seed: int, max_seq: int, gain_std: float = 0.1,
-              bits_from_device: bool = False):
+              bits_from_device: bool = False, kv_fp8: bool = False):
     """(engine, oracle, device_weights) on identical synthetic weights."""
     from megakernel_amd.bridge import MegakernelEngine
     from megakernel_amd.weights import DeviceWeights
@@ -30,7 +30,9 @@ def make_pair(shape: ModelShape, seed: int, max_seq: int, gain_std: float = 0.1,
         bits = qwen3_ref.unpack_flat(osh, dw.to_host(), dw.layout.offsets)
     else:
         bits = qwen3_ref.synthetic_bits(osh, seed, std=0.02, gain_std=gain_std)
-    orc = qwen3_ref.Qwen3Oracle(osh, bits, max_seq)
+    orc = qwen3_ref.Qwen3Oracle(osh, bits, max_seq, kv_fp8=kv_fp8)
+    if kv_fp8:
+        eng.set_kv_fp8(True)
     return eng, orc, dw
 
 

@@ -125,3 +125,130 @@ def test_fp8_lmhead_generate_toggle_and_oracle():
     finally:
         eng.close()
         dw.free()
+
+
+# ---------------------------------------------------------------- FP8 KV cache
+def _synthetic_kv(shape, seed, ctx):
+    ks = np.stack([synth.kv_prefill_bits(seed, l, 0, ctx, shape.n_kv_heads, shape.head_dim)
+                   for l in range(shape.n_layers)])
+    vs = np.stack([synth.kv_prefill_bits(seed, l, 1, ctx, shape.n_kv_heads, shape.head_dim)
+                   for l in range(shape.n_layers)])
+    return ks, vs
+
+
+def _bf16_bits(t) -> np.ndarray:
+    import torch
+    return t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("name,shape", [("tiny", TINY), ("baseline_2l", BASELINE_2L),
+                                        ("qwen3_2l", QWEN3_06B.with_(n_layers=2, vocab=4096))])
+def test_fp8_kv_fill_and_set_exact(name, shape):
+    """fill_kv_synthetic and set_kv quantise each K / V row as the oracle does;
+    get_kv returns bf16 of code x scale, which is exact: bit-equal to the
+    oracle's dequantised rows."""
+    ctx = 300
+    eng, orc, dw = make_pair(shape, 29, ctx + 8, kv_fp8=True)
+    try:
+        _print(f"fp8 kv fill {name}")
+        ks, vs = _synthetic_kv(shape, 41, ctx)
+        orc.set_kv(ks, vs)
+        eng.fill_kv_synthetic(ctx, 41)
+        got = eng.get_kv(ctx)
+        assert np.array_equal(got[:, 0], _bf16_bits(orc.k_cache[:, :, :ctx])), "K codes / scales differ"
+        assert np.array_equal(got[:, 1], _bf16_bits(orc.v_cache[:, :, :ctx])), "V codes / scales differ"
+        # set_kv of other bf16 rows (a wide dynamic range across rows)
+        rng = np.random.default_rng(3)
+        vals = (rng.standard_normal((shape.n_layers, 2, shape.n_kv_heads, 40, shape.head_dim)) *
+                np.exp(rng.uniform(-6, 6, size=(shape.n_layers, 2, shape.n_kv_heads, 40, 1)))).astype(np.float32)
+        import torch
+        bits = _bf16_bits(torch.from_numpy(vals))
+        eng.set_kv(bits)
+        orc.set_kv(bits[:, 0], bits[:, 1])
+        got = eng.get_kv(40)
+        assert np.array_equal(got[:, 0], _bf16_bits(orc.k_cache[:, :, :40]))
+        assert np.array_equal(got[:, 1], _bf16_bits(orc.v_cache[:, :, :40]))
+    finally:
+        eng.close()
+        dw.free()
+
+
+@pytest.mark.parametrize("ctx,chunk", [(100, 512), (1500, 64), (2000, 64)])
+def test_fp8_kv_decode_parity(ctx, chunk):
+    """Decoding over an FP8 cache (split attention; ctx 2000 at chunk 64 runs
+    the long-context merge) against the oracle on the same dequantised cache;
+    the appended rows are the oracle's quantised k / v (the kernel's fp32 k
+    differs in summation order, so a code may sit one step away)."""
+    shape = BASELINE.with_(n_layers=2, vocab=2048)
+    eng, orc, dw = make_pair(shape, 37, ctx + 16, kv_fp8=True)
+    try:
+        eng.set_attention_chunk(chunk)
+        eng.fill_kv_synthetic(ctx, 43)
+        orc.set_kv(*_synthetic_kv(shape, 43, ctx))
+        tok = 5
+        for i in range(4):
+            _print(f"fp8 kv ctx {ctx} chunk {chunk} step {i}")
+            _, layers, logits = eng.debug_forward(tok)
+            ref = orc.step(tok, capture=True)
+            check_step(layers, logits, ref, f"fp8 kv ctx {ctx} step {i}")
+            tok = ref["token"]
+        got = eng.get_kv(ctx + 4)[:, :, :, ctx:].astype(np.uint32)
+        from oracle import synth as osynth
+        gk = osynth.bf16_bits_to_f32(got[:, 0].astype(np.uint16))
+        gv = osynth.bf16_bits_to_f32(got[:, 1].astype(np.uint16))
+        wk = orc.k_cache[:, :, ctx:ctx + 4].numpy()
+        wv = orc.v_cache[:, :, ctx:ctx + 4].numpy()
+        for g_, w_, nm in ((gk, wk, "K"), (gv, wv, "V")):
+            rel = np.linalg.norm(g_ - w_, axis=-1) / np.maximum(np.linalg.norm(w_, axis=-1), 1e-30)
+            assert rel.max() <= 2.0 ** -4, f"appended {nm} rows off by rel-L2 {rel.max():.3e}"
+            assert (g_ != w_).mean() < 0.02, f"{(g_ != w_).mean():.3%} of appended {nm} entries differ"
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_fp8_kv_generate_and_fp8_head_together():
+    """FP8 cache and FP8 LM head together: one resident launch == per-token
+    decoding; greedy tokens agree with the oracle (teacher-forced)."""
+    eng, orc, dw = make_pair(BASELINE_2L, 47, 256, kv_fp8=True)
+    try:
+        eng.set_lmhead_fp8(True)
+        orc.use_fp8_lm_head()
+        prompt = synth.prompt_tokens(47, 6, BASELINE_2L.vocab)
+        for t in prompt[:-1]:
+            eng.decode_token(t)
+        a0 = eng.decode_token(prompt[-1])
+        gen = eng.decode_many(a0, 40)
+        eng.set_pos(len(prompt) - 1)
+        b = [eng.decode_token(prompt[-1])]
+        for _ in range(40):
+            b.append(eng.decode_token(b[-1]))
+        assert [a0] + gen == b, "generate() and per-token decode disagree on the FP8 cache"
+        for t in prompt[:-1]:
+            orc.step(t)
+        same, low = check_tokens_teacher_forced([prompt[-1], a0] + gen[:-1], [a0] + gen, orc)
+        _print(f"fp8 kv + fp8 head teacher-forced: {same} identical, {low} low-margin differences")
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_fp8_kv_and_prefill_context_exclude_each_other():
+    from megakernel_amd import _lib
+    eng, _, dw = make_pair(BASELINE_2L, 53, 64)
+    try:
+        eng.attach_prefill(dw)
+        assert eng.lib.megakernel_set_kv_fp8(eng._handle, 1) == -1
+        assert "prefill" in _lib.last_error(eng.lib)
+    finally:
+        eng.close()
+        dw.free()
+    eng, _, dw = make_pair(BASELINE_2L, 53, 64, kv_fp8=True)
+    try:
+        with pytest.raises(_lib.MegakernelError):
+            eng.attach_prefill(dw)
+        eng.set_kv_fp8(False)
+        eng.attach_prefill(dw)
+    finally:
+        eng.close()
+        dw.free()
