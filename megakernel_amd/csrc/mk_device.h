@@ -84,16 +84,16 @@ __device__ __forceinline__ float dot16_fp8(u32x4 w, const float* h, float acc) {
   return acc;
 }
 
-// 8 FP8 (OCP e4m3) values -> 8 bf16 in the same order.  Exact: an e4m3 value
-// has 4 significant bits, so its fp32 form has zero low halves.
-__device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 r) {
+// 8 FP8 (OCP e4m3) values -> 8 bf16 in the same order, each multiplied by a
+// power of two s.  Exact: an e4m3 value has 4 significant bits.  One
+// instruction per two values (gfx950 v_cvt_scalef32_pk_bf16_fp8).
+__device__ __forceinline__ u32x4 fp8x8_to_bf16x8_scaled(u32x2 r, float s) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   u32x4 o;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[i], false);
-    const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[i], true);
-    o[2 * i] = pack_hi16(__float_as_uint(a[0]), __float_as_uint(a[1]));
-    o[2 * i + 1] = pack_hi16(__float_as_uint(b[0]), __float_as_uint(b[1]));
+    o[2 * i] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[i], s, false));
+    o[2 * i + 1] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[i], s, true));
   }
   return o;
 }

@@ -898,14 +898,13 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S, (MODE & 8)
         f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
-          u32x4 kb;
-          if constexpr (K8) kb = fp8x8_to_bf16x8(kvr.k[q][h][kc]);
+          u32x4 kb;  // FP8: a lane's 8 values share one position, so its K scale enters here
+          if constexpr (K8) kb = fp8x8_to_bf16x8_scaled(kvr.k[q][h][kc], kvr.sk[q][h]);
           else kb = kvr.k[q][h][kc];
           d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[kc]),
                                                       __builtin_bit_cast(bf16x8, kb), d4, 0, 0, 0);
         }
-        float v = (d4[0] + d4[1]) + d4[2];
-        if constexpr (K8) v *= kvr.sk[q][h];  // exact: a power of two
+        const float v = (d4[0] + d4[1]) + d4[2];
         const int t = 32 * (b0 + bi + q * NW) + 16 * h + c16;
         sc[q][h] = (bi + q * NW < nb && t < t1) ? v * scale : -INFINITY;
         bmax = fmaxf(bmax, sc[q][h]);
@@ -950,7 +949,7 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S, (MODE & 8)
       for (int q = 0; q < KVB; ++q)
       {
         u32x4 vb;
-        if constexpr (K8) vb = fp8x8_to_bf16x8(kvr.v[q][dt]);
+        if constexpr (K8) vb = fp8x8_to_bf16x8_scaled(kvr.v[q][dt], 1.0f);  // V scales ride on the weights
         else vb = kvr.v[q][dt];
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa[q]),
                                                          __builtin_bit_cast(bf16x8, vb), acc[dt], 0, 0, 0);
