@@ -195,6 +195,8 @@ def bench_batch(args):
     lengths = [int(x) for x in rng.integers(args.kv_min, args.kv_max + 1, size=B)]
     dw = DeviceWeights(shape, args.seed, std=0.02, gain_std=0.0)
     eng = BatchEngine(dw, B, args.kv_max + max(K, W) + 8, shape)
+    if args.kv_fp8:
+        eng.set_kv_fp8(True)
     info = launcher.detect_gpu()
     first = [int(t) for t in rng.integers(0, shape.vocab, size=B)]
 
@@ -215,7 +217,10 @@ def bench_batch(args):
         print(f"# rep {r}: wall {walls[-1] * 1e3:.2f} ms device {kernels[-1] * 1e3:.2f} ms -> "
               f"{B * K / walls[-1]:.1f} tok/s; last tokens {toks[-1][:4].tolist()}", file=sys.stderr, flush=True)
     wall, kern = statistics.median(walls), statistics.median(kernels)
-    nbytes = sum(shape.weight_bytes + sum(shape.kv_bytes_per_pos * (n + i + 2) for n in lengths) for i in range(K))
+    kvp = shape.kv_bytes_per_pos  # per position; FP8: 1 byte per value plus a 4-byte scale per row
+    if args.kv_fp8:
+        kvp = kvp // 2 + 2 * 4 * shape.n_kv_heads * shape.n_layers
+    nbytes = sum(shape.weight_bytes + sum(kvp * (n + i + 2) for n in lengths) for i in range(K))
     achieved = nbytes / kern / 1e9
     eng.close()
     dw.free()
@@ -223,7 +228,7 @@ def bench_batch(args):
         "metric": f"batched greedy decode tok/s ({B} sequences, KV {args.kv_min}-{args.kv_max})",
         "value": round(B * K / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "vs_baseline": None, "dtype": "bf16 (KV cache fp8 e4m3)" if args.kv_fp8 else "bf16", "data": "synthetic",
         "config": {"workload": f"Qwen3-0.6B-shaped batched decode, {B} sequences, KV lengths {lengths}, "
                                f"{K} steps (BASELINE configs[4])", "sequences": B, "kv_lengths": lengths,
                    "device": info["name"], "reps": args.reps},

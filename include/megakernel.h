@@ -250,6 +250,14 @@ int megakernel_prefill(void* handle, const int* tokens, int n, int* next_token);
  * NULL; host float[vocab]) its fp32 logits.  Returns 0 or -1. */
 int megakernel_batch_prefill(void* handle, int seq, const int* tokens, int n, int* next_token, float* logits);
 
+/* FP8 KV caches for every sequence of a batch handle (no counterpart in the
+ * reference, which plans FP8 KV in RESEARCH.md:434-436,463): the format of
+ * megakernel_set_kv_fp8 (e4m3 codes, one power-of-two scale per K / V row).
+ * Every cache is emptied and every position reset to 0, in either direction;
+ * batch set_kv / get_kv / fill keep the bf16 reference layout; batch prefill is
+ * refused on FP8 caches (its kernels write bf16 K/V).  Returns 0 or -1. */
+int megakernel_batch_set_kv_fp8(void* handle, int enable);
+
 /* Device time of the last megakernel_generate_batch / decode_batch / prefill call (ms). */
 float megakernel_batch_last_ms(void* handle);
 

@@ -30,6 +30,7 @@ struct BHandle {
   // the token / step outputs of its last chunk (kept apart from the decode's)
   int *pf_tok = nullptr, *pf_pos = nullptr, *pf_out = nullptr, *pf_step = nullptr;
   std::vector<void*> owned;
+  float *kscale = nullptr, *vscale = nullptr;  // FP8 cache scales, allocated on first use
   int (*launch_step)(BHandle*, const BParams&) = nullptr;
   int (*launch_prefill)(BHandle*, const BParams&, bool) = nullptr;
 };
@@ -75,7 +76,10 @@ static int launch_step(BHandle* h, const BParams& p) {
   hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
   for (int l = 0; l < L; ++l) {
     hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_attn<S>, dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+    if (p.kscale)
+      hipLaunchKernelGGL((bk_attn<S, true>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+    else
+      hipLaunchKernelGGL((bk_attn<S, false>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
     hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16 * KS_O), dim3(GT), 0, h->stream, p, l);
     hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, p, l);
     hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
@@ -176,6 +180,8 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
   h->s_pad = (h->S + 31) / 32 * 32;
   p.s_pad = h->s_pad;
   p.kv_seq = (long long)L * h->NKV * h->s_pad * h->D;
+  p.sc_seq = (long long)L * h->NKV * h->s_pad;
+  p.kscale = p.vscale = nullptr;
   if (ext_kv) {
     p.kv = ext_kv;
     p.kvt = ext_kvt;
@@ -458,7 +464,23 @@ int megakernel_batch_fill_kv_synthetic(void* handle, int seq, int len, unsigned 
     mk::set_err("invalid fill arguments (sequence %d, len %d)", seq, len);
     return -1;
   }
-  if (len > 0) {
+  if (len > 0 && h->p.kscale) {  // FP8 cache: the bf16 values in the reference layout, then quantised rows
+    const float c = (float)(std * sqrt(3.0) / 65536.0);
+    void* stage = nullptr;
+    HIPCHK(hipMalloc(&stage, (size_t)2 * h->L * h->NKV * (size_t)len * h->D * 2), -1);
+    hipLaunchKernelGGL(mk::synth_kv_ref_kernel, dim3(4096), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                       h->L, h->NKV, h->D, len, seed, c);
+    hipLaunchKernelGGL(mk::kv_quant_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<const uint16_t*>(stage),
+                       reinterpret_cast<uint8_t*>(h->p.kv) + seq * h->p.kv_seq,
+                       reinterpret_cast<uint8_t*>(h->p.kvt) + seq * h->p.kv_seq, h->p.kscale + seq * h->p.sc_seq,
+                       h->p.vscale + seq * h->p.sc_seq, h->L, h->NKV, h->s_pad, h->D, len);
+    const hipError_t e = hipGetLastError() == hipSuccess ? hipStreamSynchronize(h->stream) : hipErrorLaunchFailure;
+    (void)hipFree(stage);
+    if (e != hipSuccess) {
+      mk::set_err("FP8 KV fill failed: %s", hipGetErrorString(e));
+      return -1;
+    }
+  } else if (len > 0) {
     const float c = (float)(std * sqrt(3.0) / 65536.0);
     hipLaunchKernelGGL(mk::synth_kv_kernel, dim3(4096), dim3(256), 0, h->stream, h->p.kv + seq * h->p.kv_seq,
                        h->p.kvt + seq * h->p.kv_seq, h->L, h->NKV, h->s_pad, h->D, len, seed, c);
@@ -478,9 +500,21 @@ static int batch_kv_transfer(BHandle* h, int seq, void* host_kv, int len, int to
       mk::set_err("KV upload failed");
       break;
     }
-    hipLaunchKernelGGL(mk::kv_convert_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
-                       h->p.kv + seq * h->p.kv_seq, h->p.kvt + seq * h->p.kv_seq, h->L, h->NKV, h->s_pad, h->D, len,
-                       to_cache);
+    // FP8: byte index = element index, so sequence seq starts at byte seq * kv_seq
+    uint8_t* k8 = reinterpret_cast<uint8_t*>(h->p.kv) + seq * h->p.kv_seq;
+    uint8_t* v8 = reinterpret_cast<uint8_t*>(h->p.kvt) + seq * h->p.kv_seq;
+    if (h->p.kscale && to_cache)
+      hipLaunchKernelGGL(mk::kv_quant_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<const uint16_t*>(stage),
+                         k8, v8, h->p.kscale + seq * h->p.sc_seq, h->p.vscale + seq * h->p.sc_seq, h->L, h->NKV,
+                         h->s_pad, h->D, len);
+    else if (h->p.kscale)
+      hipLaunchKernelGGL(mk::kv_dequant_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                         k8, v8, h->p.kscale + seq * h->p.sc_seq, h->p.vscale + seq * h->p.sc_seq, h->L, h->NKV,
+                         h->s_pad, h->D, len);
+    else
+      hipLaunchKernelGGL(mk::kv_convert_kernel, dim3(2048), dim3(256), 0, h->stream, static_cast<uint16_t*>(stage),
+                         h->p.kv + seq * h->p.kv_seq, h->p.kvt + seq * h->p.kv_seq, h->L, h->NKV, h->s_pad, h->D,
+                         len, to_cache);
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(h->stream) != hipSuccess) {
       mk::set_err("KV layout conversion failed");
       break;
@@ -556,7 +590,40 @@ int megakernel_batch_prefill(void* handle, int seq, const int* tokens, int n, in
     mk::set_err("null handle or tokens");
     return -1;
   }
+  if (h->p.kscale) {
+    mk::set_err("batch prefill: the KV caches are FP8 (the prefill kernels write bf16 K/V)");
+    return -1;
+  }
   return mk::batch::run_prefill(h, seq, tokens, n, next_token, logits);
+}
+
+int megakernel_batch_set_kv_fp8(void* handle, int enable) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  const size_t sb = (size_t)mk::batch::BMAX * h->p.sc_seq * 4;
+  if (enable && !h->kscale) {
+    if (mk::batch::alloc(h, &h->kscale, sb) || mk::batch::alloc(h, &h->vscale, sb)) return -1;
+  }
+  h->p.kscale = enable ? h->kscale : nullptr;
+  h->p.vscale = enable ? h->vscale : nullptr;
+  // empty caches in the new format, every sequence at position 0, and a step
+  // graph captured again with the matching attention kernel
+  HIPCHK(hipMemsetAsync(h->p.kv, 0, (size_t)mk::batch::BMAX * h->p.kv_seq * 2, h->stream), -1);
+  HIPCHK(hipMemsetAsync(h->p.kvt, 0, (size_t)mk::batch::BMAX * h->p.kv_seq * 2, h->stream), -1);
+  if (h->kscale) {
+    HIPCHK(hipMemsetAsync(h->kscale, 0, sb, h->stream), -1);
+    HIPCHK(hipMemsetAsync(h->vscale, 0, sb, h->stream), -1);
+  }
+  HIPCHK(hipMemsetAsync(h->p.pos, 0, mk::batch::BMAX * 4, h->stream), -1);
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  if (h->exec) (void)hipGraphExecDestroy(h->exec);
+  if (h->graph) (void)hipGraphDestroy(h->graph);
+  h->exec = nullptr;
+  h->graph = nullptr;
+  return 0;
 }
 
 float megakernel_batch_last_ms(void* handle) {

@@ -23,6 +23,8 @@
 // attention merge hands partials between workgroups of one launch (write-through
 // stores, an agent-scope counter, agent-scope loads).
 #pragma once
+#include <type_traits>
+
 #include "mk_config.h"
 #include "mk_device.h"
 #include "mk_host.h"
@@ -63,6 +65,9 @@ struct BParams {
   uint16_t* kv;             // K caches [B][L][NKV][s_pad][D]
   uint16_t* kvt;            // V^T caches [B][L][NKV][s_pad/32][D][32]
   long long kv_seq;         // elements per sequence in each region
+  float* kscale;            // FP8 cache (null: bf16): power-of-two scale per K row and per V
+  float* vscale;            //   row, [B][L][NKV][s_pad]; codes at byte index = element index
+  long long sc_seq;         // scales per sequence
   int s_pad;
   float* x;                 // [BMAX][H] residual streams
   uint16_t* xg;             // [2 consumers][2 planes][BMAX][H] x * gain as bf16 hi / lo parts:
@@ -527,11 +532,15 @@ __global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
 // step at KV 512-4096 has ~1,100 items; with four per CU the last ~10 % ran
 // as a second, latency-bound residency wave.
 constexpr int ATTN_WAVES_PER_EU = AT == 256 ? 5 : 2;
-template <class S>
+template <class S, bool K8 = false>
 __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_PER_EU, ATTN_WAVES_PER_EU))) void bk_attn(
     BParams p, int layer) {
   static_assert(S::GQA == 2 && S::D == 64, "batched attention is built for 2 q heads of 64 per kv head");
   constexpr int D = S::D, NKV = S::NKV;
+  // K8: the FP8 cache (codes converted to bf16 in registers, exact; the K
+  // row scale enters that conversion, the V row scale the softmax weight)
+  using Reg = typename std::conditional<K8, u32x2, u32x4>::type;
+  __shared__ float kcs[2];  // FP8: scales of position pos's K / V rows
   __shared__ __attribute__((aligned(16))) uint16_t qb[16][D];          // q parts (A operand of the scores)
   __shared__ __attribute__((aligned(16))) uint16_t pb[AW][16][32];     // weight parts (A operand of the output)
   __shared__ __attribute__((aligned(16))) uint16_t kcur[D], vcur[D];   // bf16 K / V of position pos
@@ -551,22 +560,44 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
   const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
   // 0. the wave's K / V blocks (4 s + w) + AW * q, q < NBW: issued first, so the
   //    prologue below overlaps them (blocks past the item repeat a valid block)
-  u32x4 kr[NBW][2][2], vr[NBW][D / 16];
+  Reg kr[NBW][2][2], vr[NBW][D / 16];
+  float sk[K8 ? NBW : 1][2], sv[K8 ? NBW : 1][2];  // FP8: scales of the lane's score positions
+  const long long sbase = (long long)b * p.sc_seq + ((long long)layer * NKV + g) * p.s_pad;
 #pragma unroll
   for (int q = 0; q < NBW; ++q) {
     int blk = s * AW * NBW + w + AW * q;
     blk = 32 * blk < n ? blk : s * AW * NBW;
-    const auto rk = make_rsrc(p.kv + kbase + (long long)blk * 32 * D);
-    const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
+    if constexpr (K8) {  // byte index = element index of the bf16 layout
+      const auto rk = make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + kbase + (long long)blk * 32 * D);
+      const auto rv = make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + kbase + (long long)blk * 32 * D);
+      const auto rks = make_rsrc(p.kscale + sbase + (long long)blk * 32);
+      const auto rvs = make_rsrc(p.vscale + sbase + (long long)blk * 32);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-        kr[q][h][kc] =
-            __builtin_amdgcn_raw_buffer_load_b128(rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+        for (int kc = 0; kc < 2; ++kc)
+          kr[q][h][kc] =
+              __builtin_amdgcn_raw_buffer_load_b64(rk, (16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4), 0u, 2);
+        sk[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rks, (16u * h + (lu & 15u)) * 4u, 0u, 2));
+        sv[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rvs, (16u * h + (lu & 15u)) * 4u, 0u, 2));
+      }
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt)
-      vr[q][dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+      for (int dt = 0; dt < D / 16; ++dt)
+        vr[q][dt] = __builtin_amdgcn_raw_buffer_load_b64(rv, (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4), 0u, 2);
+    } else {
+      const auto rk = make_rsrc(p.kv + kbase + (long long)blk * 32 * D);
+      const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+          kr[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b128(
+              rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt)
+        vr[q][dt] =
+            __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+    }
   }
   for (int i = tid; i < 16 * D; i += AT) (&qb[0][0])[i] = 0;
   for (int i = tid; i < AW * 16 * 32; i += AT) (&pb[0][0][0])[i] = 0;
@@ -594,15 +625,35 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
       qb[4 * w + 0][l] = h;
       qb[4 * w + 1][l] = m;
       qb[4 * w + 2][l] = o;
+    } else if constexpr (K8) {  // FP8 append: the row's power-of-two scale from the wave's max
+      const int e = e4m3_row_exp(wave_max(fabsf(v)));
+      const uint8_t code = (uint8_t)e4m3_encode(ldexpf(v, -e));
+      reinterpret_cast<uint8_t*>(kcur)[l] = code;
+      if (l == 0) kcs[0] = ldexpf(1.f, e);
+      if (own) {
+        reinterpret_cast<uint8_t*>(p.kv)[kbase + (long long)pos * D + l] = code;
+        if (l == 0) p.kscale[sbase + pos] = ldexpf(1.f, e);
+      }
     } else {
       const uint16_t kb = f32_to_bf16(v);
       kcur[l] = kb;
       if (own) p.kv[kbase + (long long)pos * D + l] = kb;  // KV append (reference kv_cache.cuh:58-78)
     }
   } else if (w == 3) {
-    const uint16_t vb = f32_to_bf16(v);
-    vcur[l] = vb;
-    if (own) p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = vb;
+    if constexpr (K8) {
+      const int e = e4m3_row_exp(wave_max(fabsf(v)));
+      const uint8_t code = (uint8_t)e4m3_encode(ldexpf(v, -e));
+      reinterpret_cast<uint8_t*>(vcur)[l] = code;
+      if (l == 0) kcs[1] = ldexpf(1.f, e);
+      if (own) {
+        reinterpret_cast<uint8_t*>(p.kvt)[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = code;
+        if (l == 0) p.vscale[sbase + pos] = ldexpf(1.f, e);
+      }
+    } else {
+      const uint16_t vb = f32_to_bf16(v);
+      vcur[l] = vb;
+      if (own) p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = vb;
+    }
   }
   __syncthreads();
   // 2. the wave's blocks: online softmax over them on the matrix cores
@@ -619,17 +670,36 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
     // prefill bk_append stored them before this kernel)
     if (!p.prefill && pos >= t0 && pos < t0 + 32) {
       const int rp = pos - t0;
-      if (c16 == (rp & 15)) {  // register arrays take compile-time indices only
+      if constexpr (K8) {
+        if (c16 == (rp & 15)) {  // register arrays take compile-time indices only
+          const uint8_t* kc8 = reinterpret_cast<const uint8_t*>(kcur);
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          const u32x4 kv = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
-          if (rp >> 4) kr[q][1][kc] = kv;
-          else kr[q][0][kc] = kv;
+          for (int kc = 0; kc < 2; ++kc) {
+            const u32x2 kv = *reinterpret_cast<const u32x2*>(&kc8[32 * kc + 8 * rg]);
+            if (rp >> 4) kr[q][1][kc] = kv;
+            else kr[q][0][kc] = kv;
+          }
+          if (rp >> 4) sk[q][1] = kcs[0], sv[q][1] = kcs[1];
+          else sk[q][0] = kcs[0], sv[q][0] = kcs[1];
         }
-      }
-      if (rg == (rp >> 3)) {
+        if (rg == (rp >> 3)) {
+          const uint8_t* vc8 = reinterpret_cast<const uint8_t*>(vcur);
 #pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) vr[q][dt] = with_bf16(vr[q][dt], rp & 7, vcur[16 * dt + c16]);
+          for (int dt = 0; dt < D / 16; ++dt) vr[q][dt] = set_u8(vr[q][dt], rp & 7, vc8[16 * dt + c16]);
+        }
+      } else {
+        if (c16 == (rp & 15)) {  // register arrays take compile-time indices only
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) {
+            const u32x4 kv = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
+            if (rp >> 4) kr[q][1][kc] = kv;
+            else kr[q][0][kc] = kv;
+          }
+        }
+        if (rg == (rp >> 3)) {
+#pragma unroll
+          for (int dt = 0; dt < D / 16; ++dt) vr[q][dt] = with_bf16(vr[q][dt], rp & 7, vcur[16 * dt + c16]);
+        }
       }
     }
     float sc[2];
@@ -637,8 +707,12 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
     for (int h = 0; h < 2; ++h) {
       f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)  // q read from LDS per block: registers for a fifth workgroup per CU
-        d4 = mfma(*reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]), kr[q][h][kc], d4);
+      for (int kc = 0; kc < 2; ++kc) {  // q read from LDS per block: registers for a fifth workgroup per CU
+        u32x4 kb;
+        if constexpr (K8) kb = fp8x8_to_bf16x8_scaled(kr[q][h][kc], sk[q][h]);
+        else kb = kr[q][h][kc];
+        d4 = mfma(*reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]), kb, d4);
+      }
       const int t = t0 + 16 * h + c16;
       sc[h] = t < n ? ((d4[0] + d4[1]) + d4[2]) * scale : -INFINITY;
     }
@@ -655,7 +729,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
     if (rg < 2) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const Split3 a = split3(sc[h]);
+        const Split3 a = split3(K8 ? sc[h] * sv[q][h] : sc[h]);
         pb[w][4 * rg + 0][16 * h + c16] = (uint16_t)(a.hi >> 16);
         pb[w][4 * rg + 1][16 * h + c16] = (uint16_t)(a.mid >> 16);
         pb[w][4 * rg + 2][16 * h + c16] = (uint16_t)(a.lo >> 16);
@@ -667,7 +741,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
     for (int dt = 0; dt < D / 16; ++dt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
-      acc[dt] = mfma(pa, vr[q][dt], acc[dt]);
+      if constexpr (K8) acc[dt] = mfma(pa, fp8x8_to_bf16x8_scaled(vr[q][dt], 1.0f), acc[dt]);
+      else acc[dt] = mfma(pa, vr[q][dt], acc[dt]);
     }
   }
   // 3. combine the waves into the item's partial

@@ -37,6 +37,15 @@ __global__ void synth_kv_kernel(uint16_t* __restrict__ kv, uint16_t* __restrict_
                                 int D, int len, unsigned long long seed, float c);
 __global__ void kv_convert_kernel(uint16_t* __restrict__ buf, uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt,
                                   int L, int NKV, int s_pad, int D, int len, int to_cache);
+// FP8 cache conversions of one sequence (reference layout buf <-> codes + row scales)
+__global__ void kv_quant_kernel(const uint16_t* __restrict__ buf, uint8_t* __restrict__ k8, uint8_t* __restrict__ v8,
+                                float* __restrict__ ks, float* __restrict__ vs, int L, int NKV, int s_pad, int D,
+                                int len);
+__global__ void kv_dequant_kernel(uint16_t* __restrict__ buf, const uint8_t* __restrict__ k8,
+                                  const uint8_t* __restrict__ v8, const float* __restrict__ ks,
+                                  const float* __restrict__ vs, int L, int NKV, int s_pad, int D, int len);
+__global__ void synth_kv_ref_kernel(uint16_t* __restrict__ buf, int L, int NKV, int D, int len,
+                                    unsigned long long seed, float c);
 
 // Prefill context of a batch-1 handle (batch.hip): the batched kernels'
 // matrix-core weight copy and work buffers, bound to an external KV cache in

@@ -33,10 +33,10 @@ class MultiOracle:
     """One Qwen3Oracle (one copy of the weights) serving several sequences:
     each sequence has its own KV cache tensors and position."""
 
-    def __init__(self, shape, dw, n_seq: int, max_seq: int):
+    def __init__(self, shape, dw, n_seq: int, max_seq: int, kv_fp8: bool = False):
         osh = oracle_shape(shape)
         bits = qwen3_ref.unpack_flat(osh, dw.to_host(), dw.layout.offsets)
-        self.orc = qwen3_ref.Qwen3Oracle(osh, bits, max_seq)
+        self.orc = qwen3_ref.Qwen3Oracle(osh, bits, max_seq, kv_fp8=kv_fp8)
         self.caches = [(self.orc.k_cache.clone(), self.orc.v_cache.clone()) for _ in range(n_seq)]
         self.pos = [0] * n_seq
         self.shape = shape
@@ -50,8 +50,8 @@ class MultiOracle:
         k, v = self.caches[seq]
         k.zero_()
         v.zero_()
-        k[:, :, :length] = qwen3_ref.bits_to_torch(ks)
-        v[:, :, :length] = qwen3_ref.bits_to_torch(vs)
+        k[:, :, :length] = self.orc._kv_rows(qwen3_ref.bits_to_torch(ks).float())
+        v[:, :, :length] = self.orc._kv_rows(qwen3_ref.bits_to_torch(vs).float())
         self.pos[seq] = length
 
     def step(self, seq: int, token: int) -> dict:
@@ -62,10 +62,12 @@ class MultiOracle:
         return r
 
 
-def _setup(shape, seed, lengths, max_seq):
+def _setup(shape, seed, lengths, max_seq, kv_fp8: bool = False):
     dw = DeviceWeights(shape, seed, std=0.02, gain_std=0.1)
     eng = BatchEngine(dw, len(lengths), max_seq, shape)
-    mo = MultiOracle(shape, dw, len(lengths), max_seq)
+    if kv_fp8:
+        eng.set_kv_fp8(True)
+    mo = MultiOracle(shape, dw, len(lengths), max_seq, kv_fp8=kv_fp8)
     for b, n in enumerate(lengths):
         eng.fill_kv_synthetic(b, n, 500 + b)
         mo.prefill(b, n, 500 + b)
@@ -309,3 +311,54 @@ def test_batch_prefill_errors():
     finally:
         eng.close()
         dw.free()
+
+
+# ------------------------------------------------------- FP8 KV caches (batch)
+def test_batch_fp8_kv_16_sequences():
+    """FP8 caches (e4m3, power-of-two row scales) for 16 BASELINE-shaped
+    sequences against per-sequence oracles on the same dequantised caches:
+    eager steps (logits), then graph steps (tokens)."""
+    shape = BASELINE.with_(n_layers=2, vocab=4096)
+    rng = np.random.default_rng(9)
+    lengths = [int(x) for x in rng.integers(0, 700, size=16)]
+    dw, eng, mo = _setup(shape, 35, lengths, 720, kv_fp8=True)
+    try:
+        toks = [int(t) for t in rng.integers(0, shape.vocab, size=16)]
+        for i in range(3):
+            _print(f"batch fp8 kv step {i} lengths {eng.positions()}")
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(16)]
+            worst = _check_step(logits, out, refs, f"fp8 step {i}")
+            _print(f"  worst logits abs err {worst:.2e}")
+            toks = out
+        out = eng.decode(toks)  # the captured step graph
+        refs = [mo.step(b, toks[b]) for b in range(16)]
+        for b, r in enumerate(refs):
+            if out[b] != r["token"]:
+                assert qwen3_ref.top2_margin(r["logits"]) <= MARGIN, f"graph step seq {b}"
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch_fp8_kv_fill_exact_and_prefill_refused():
+    lengths = [0, 40, 129]
+    dw, eng, mo = _setup(TINY, 36, lengths, 256, kv_fp8=True)
+    try:
+        for b, n in enumerate(lengths):
+            if n == 0:
+                continue
+            got = eng.get_kv(b, n)
+            k, v = mo.caches[b]
+            for plane, want in ((0, k), (1, v)):
+                wb = want[:, :, :n].to(torch.bfloat16).contiguous().view(torch.int16).numpy().view(np.uint16)
+                assert np.array_equal(got[:, plane], wb), f"seq {b} plane {plane}: FP8 rows differ"
+        with pytest.raises(_lib.MegakernelError):
+            eng.prefill(0, [1, 2, 3])
+        eng.set_kv_fp8(False)
+        assert eng.positions() == [0, 0, 0]
+        eng.prefill(0, [1, 2, 3])
+    finally:
+        eng.close()
+        dw.free()
+
