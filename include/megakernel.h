@@ -156,9 +156,8 @@ int megakernel_set_lmhead_fp8(void* handle, int enable);
  * the attention bytes of a token.  The cache is emptied (as megakernel_reset)
  * in either direction.  set_kv / get_kv / fill_kv_synthetic keep the bf16
  * reference layout at the boundary (quantised on the way in, exact bf16 of
- * code x scale on the way out).  Refused while a prefill context is attached
- * (its kernels write bf16 K/V); megakernel_prefill_attach is refused on an FP8
- * cache.  Returns 0 or -1. */
+ * code x scale on the way out); megakernel_prefill appends FP8 rows the same
+ * way.  Returns 0 or -1. */
 int megakernel_set_kv_fp8(void* handle, int enable);
 
 /* The FP8 LM head as built: codes[V * H] row-major e4m3 bytes, scales[V]
@@ -254,8 +253,8 @@ int megakernel_batch_prefill(void* handle, int seq, const int* tokens, int n, in
  * reference, which plans FP8 KV in RESEARCH.md:434-436,463): the format of
  * megakernel_set_kv_fp8 (e4m3 codes, one power-of-two scale per K / V row).
  * Every cache is emptied and every position reset to 0, in either direction;
- * batch set_kv / get_kv / fill keep the bf16 reference layout; batch prefill is
- * refused on FP8 caches (its kernels write bf16 K/V).  Returns 0 or -1. */
+ * batch set_kv / get_kv / fill keep the bf16 reference layout; batch prefill
+ * appends FP8 rows.  Returns 0 or -1. */
 int megakernel_batch_set_kv_fp8(void* handle, int enable);
 
 /* Device time of the last megakernel_generate_batch / decode_batch / prefill call (ms). */

@@ -100,8 +100,13 @@ static int launch_prefill(BHandle* h, const BParams& p, bool last) {
   hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
   for (int l = 0; l < L; ++l) {
     hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_append<S>, dim3(BMAX * S::NKV), dim3(2 * kWave), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_attn<S>, dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+    if (p.kscale) {
+      hipLaunchKernelGGL((bk_append<S, true>), dim3(BMAX * S::NKV), dim3(2 * kWave), 0, h->stream, p, l);
+      hipLaunchKernelGGL((bk_attn<S, true>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+    } else {
+      hipLaunchKernelGGL((bk_append<S, false>), dim3(BMAX * S::NKV), dim3(2 * kWave), 0, h->stream, p, l);
+      hipLaunchKernelGGL((bk_attn<S, false>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+    }
     hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16 * KS_O), dim3(GT), 0, h->stream, p, l);
     hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, p, l);
     hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
@@ -342,9 +347,19 @@ static int prefill_chunks(BHandle* h, int seq, const int* tokens, int n, int pos
     const int cnt = n - c0 < BMAX ? n - c0 : BMAX;
     const bool last = c0 + cnt == n;
     BParams pp = h->p;
-    pp.kv = h->p.kv + seq * h->p.kv_seq;  // every column writes and reads this sequence's cache
-    pp.kvt = h->p.kvt + seq * h->p.kv_seq;
+    // every column writes and reads this sequence's cache (FP8: byte index =
+    // element index, so the sequence starts at byte seq * kv_seq)
+    if (h->p.kscale) {
+      pp.kv = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kv) + seq * h->p.kv_seq);
+      pp.kvt = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kvt) + seq * h->p.kv_seq);
+      pp.kscale = h->p.kscale + seq * h->p.sc_seq;
+      pp.vscale = h->p.vscale + seq * h->p.sc_seq;
+    } else {
+      pp.kv = h->p.kv + seq * h->p.kv_seq;
+      pp.kvt = h->p.kvt + seq * h->p.kv_seq;
+    }
     pp.kv_seq = 0;
+    pp.sc_seq = 0;
     pp.prefill = 1;
     pp.B = cnt;
     pp.tok = h->pf_tok + c0;
@@ -394,7 +409,10 @@ BHandle* create_prefill_context(int preset, int vocab, int max_seq, const char* 
   return h;
 }
 
-int prefill_context_run(BHandle* h, const int* tokens, int n, int pos0, int* next_token, float* logits) {
+int prefill_context_run(BHandle* h, const int* tokens, int n, int pos0, int* next_token, float* logits,
+                        float* kscale, float* vscale) {
+  h->p.kscale = kscale;  // the bound cache's FP8 row scales, or null for a bf16 cache
+  h->p.vscale = vscale;
   return prefill_chunks(h, 0, tokens, n, pos0, next_token, logits);
 }
 
@@ -588,10 +606,6 @@ int megakernel_batch_prefill(void* handle, int seq, const int* tokens, int n, in
   BHandle* h = static_cast<BHandle*>(handle);
   if (!h || !tokens) {
     mk::set_err("null handle or tokens");
-    return -1;
-  }
-  if (h->p.kscale) {
-    mk::set_err("batch prefill: the KV caches are FP8 (the prefill kernels write bf16 K/V)");
     return -1;
   }
   return mk::batch::run_prefill(h, seq, tokens, n, next_token, logits);

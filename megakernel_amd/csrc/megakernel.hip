@@ -847,10 +847,6 @@ int megakernel_prefill_attach(void* handle, void* d_weights, const long long* of
     return -1;
   }
   if (h->prefill) return 0;
-  if (h->kv_fp8) {
-    mk::set_err("prefill context: the handle's KV cache is FP8 (the prefill kernels write bf16 K/V)");
-    return -1;
-  }
   const char* w = static_cast<const char*>(d_weights);
   if (!w) {  // the library's own upload (megakernel_init_from_host) with the init offsets
     if (!h->owned_flat) {
@@ -879,7 +875,8 @@ int megakernel_prefill(void* handle, const int* tokens, int n, int* next_token) 
     mk::set_err("prefill: no prefill context (call megakernel_prefill_attach)");
     return -1;
   }
-  if (mk::batch::prefill_context_run(h->prefill, tokens, n, h->pos, next_token, nullptr)) return -1;
+  if (mk::batch::prefill_context_run(h->prefill, tokens, n, h->pos, next_token, nullptr,
+                                     h->kv_fp8 ? h->kscale : nullptr, h->kv_fp8 ? h->vscale : nullptr)) return -1;
   h->pos += n;
   h->last_ms = mk::batch::prefill_context_ms(h->prefill);
   return 0;
@@ -934,10 +931,6 @@ int megakernel_set_kv_fp8(void* handle, int enable) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) {
     mk::set_err("null handle");
-    return -1;
-  }
-  if (enable && h->prefill) {
-    mk::set_err("the FP8 KV cache is not available with a prefill context attached (it writes bf16 K/V)");
     return -1;
   }
   if (enable && !h->kscale) {

@@ -498,8 +498,9 @@ __global__ void bk_tok(BParams p) {
 // arithmetic as bk_attn's prologue: k = RoPE(k_norm(k)), both stored as bf16
 // (reference kv_cache.cuh:58-78).  One workgroup per (column, kv head): wave
 // 0 stores k, wave 1 stores v.
-template <class S>
+template <class S, bool K8 = false>
 __global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
+  // K8: FP8 rows (codes + the row's power-of-two scale from the wave's maximum)
   static_assert(S::D == kWave, "one lane per head dimension");
   constexpr int D = S::D, NKV = S::NKV;
   const int b = blockIdx.x / NKV, g = blockIdx.x % NKV;
@@ -516,9 +517,17 @@ __global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
     const int d = l & 31;
     const float c = p.rope[(b * 2 + 0) * (D / 2) + d], sn = p.rope[(b * 2 + 1) * (D / 2) + d];
     v = l < 32 ? v * c - partner * sn : v * c + partner * sn;
-    p.kv[kbase + (long long)pos * D + l] = f32_to_bf16(v);
+  }
+  const long long at = w == 0 ? kbase + (long long)pos * D + l
+                              : kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32);
+  if constexpr (K8) {
+    const int e = e4m3_row_exp(wave_max(fabsf(v)));
+    reinterpret_cast<uint8_t*>(w == 0 ? p.kv : p.kvt)[at] = (uint8_t)e4m3_encode(ldexpf(v, -e));
+    if (l == 0)
+      (w == 0 ? p.kscale : p.vscale)[(long long)b * p.sc_seq + ((long long)layer * NKV + g) * p.s_pad + pos] =
+          ldexpf(1.f, e);
   } else {
-    p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = f32_to_bf16(v);
+    (w == 0 ? p.kv : p.kvt)[at] = f32_to_bf16(v);
   }
 }
 

@@ -56,7 +56,8 @@ BHandle* create_prefill_context(int preset, int vocab, int max_seq, const char* 
                                 int num_offsets, uint16_t* kv, uint16_t* kvt);
 // n prompt tokens at positions pos0 .. pos0 + n - 1 of the bound cache;
 // next_token (may be null) receives the greedy token after the last one.
-int prefill_context_run(BHandle* h, const int* tokens, int n, int pos0, int* next_token, float* logits);
+int prefill_context_run(BHandle* h, const int* tokens, int n, int pos0, int* next_token, float* logits,
+                        float* kscale, float* vscale);
 float prefill_context_ms(BHandle* h);
 void destroy_prefill_context(BHandle* h);
 }  // namespace batch

@@ -341,7 +341,11 @@ def test_batch_fp8_kv_16_sequences():
         dw.free()
 
 
-def test_batch_fp8_kv_fill_exact_and_prefill_refused():
+def test_batch_fp8_kv_fill_exact_and_prefill():
+    """FP8 fills bit-exact against the oracle; a prompt prefilled into an FP8
+    cache (bk_append quantising each row) gives the oracle's next token and
+    logits on the same dequantised cache, and leaves the other sequences'
+    caches untouched."""
     lengths = [0, 40, 129]
     dw, eng, mo = _setup(TINY, 36, lengths, 256, kv_fp8=True)
     try:
@@ -353,12 +357,24 @@ def test_batch_fp8_kv_fill_exact_and_prefill_refused():
             for plane, want in ((0, k), (1, v)):
                 wb = want[:, :, :n].to(torch.bfloat16).contiguous().view(torch.int16).numpy().view(np.uint16)
                 assert np.array_equal(got[:, plane], wb), f"seq {b} plane {plane}: FP8 rows differ"
-        with pytest.raises(_lib.MegakernelError):
-            eng.prefill(0, [1, 2, 3])
-        eng.set_kv_fp8(False)
-        assert eng.positions() == [0, 0, 0]
-        eng.prefill(0, [1, 2, 3])
+        before2 = eng.get_kv(2, 129)
+        prompt = [int(t) for t in np.random.default_rng(36).integers(0, TINY.vocab, size=37)]
+        nxt, logits = eng.prefill(1, prompt, with_logits=True)
+        ref = None
+        for t in prompt:
+            ref = mo.step(1, t)
+        err = float(np.abs(logits - ref["logits"].numpy()).max())
+        _print(f"fp8 prefill: next token {nxt} (oracle {ref['token']}), logits max abs err {err:.2e}")
+        assert err <= LOGIT_ABS
+        if nxt != ref["token"]:
+            assert qwen3_ref.top2_margin(ref["logits"]) <= MARGIN
+        assert eng.positions() == [0, 40 + 37, 129]
+        assert np.array_equal(eng.get_kv(2, 129), before2)
+        # decode continues on the FP8 caches after the prefill
+        toks = [3, nxt, 5]
+        out, logits = eng.debug_logits(toks)
+        refs = [mo.step(b, toks[b]) for b in range(3)]
+        _check_step(logits, out, refs, "decode after fp8 prefill")
     finally:
         eng.close()
         dw.free()
-

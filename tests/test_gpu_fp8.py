@@ -233,22 +233,33 @@ def test_fp8_kv_generate_and_fp8_head_together():
         dw.free()
 
 
-def test_fp8_kv_and_prefill_context_exclude_each_other():
-    from megakernel_amd import _lib
-    eng, _, dw = make_pair(BASELINE_2L, 53, 64)
+@pytest.mark.parametrize("which,prefix,prompt_len", [("tiny", 20, 37), ("baseline_2l", 300, 70)])
+def test_fp8_kv_batch1_prefill_then_decode(which, prefix, prompt_len):
+    """megakernel_prefill into an FP8 cache (the prefill context appends FP8
+    rows with the handle's scales), then decode, against the oracle on the
+    same dequantised cache."""
+    shape = TINY if which == "tiny" else BASELINE.with_(n_layers=2, vocab=2048)
+    eng, orc, dw = make_pair(shape, 53, prefix + prompt_len + 16, kv_fp8=True)
     try:
         eng.attach_prefill(dw)
-        assert eng.lib.megakernel_set_kv_fp8(eng._handle, 1) == -1
-        assert "prefill" in _lib.last_error(eng.lib)
-    finally:
-        eng.close()
-        dw.free()
-    eng, _, dw = make_pair(BASELINE_2L, 53, 64, kv_fp8=True)
-    try:
-        with pytest.raises(_lib.MegakernelError):
-            eng.attach_prefill(dw)
-        eng.set_kv_fp8(False)
-        eng.attach_prefill(dw)
+        if prefix:
+            eng.fill_kv_synthetic(prefix, 11)
+            orc.set_kv(*_synthetic_kv(shape, 11, prefix))
+        prompt = [int(t) for t in np.random.default_rng(prompt_len).integers(0, shape.vocab, size=prompt_len)]
+        _print(f"fp8 kv batch-1 prefill {which} prefix {prefix} prompt {prompt_len}")
+        nxt = eng.prefill(prompt)
+        assert eng.pos == prefix + prompt_len
+        ref = None
+        for t in prompt:
+            ref = orc.step(t, capture=True)
+        if nxt != ref["token"]:
+            assert qwen3_ref.top2_margin(ref["logits"]) <= 2e-2, f"prefill token {nxt} != oracle {ref['token']}"
+        tok = ref["token"]
+        for i in range(3):
+            _, layers, logits = eng.debug_forward(tok)
+            r = orc.step(tok, capture=True)
+            check_step(layers, logits, r, f"fp8 kv decode {i} after prefill")
+            tok = r["token"]
     finally:
         eng.close()
         dw.free()
