@@ -248,7 +248,10 @@ void run(int wg) {
 int main(int argc, char** argv) {
   drop_mode = argc > 1 && strcmp(argv[1], "drop") == 0;
   alias_mode = argc > 1 && strcmp(argv[1], "alias") == 0;
-  // the kernel clears every tagged buffer (tag 0) before a launch
+  // the host clears every tagged buffer (tag 0) when a handle is created (and
+  // the packed-pair buffers again when the position moves back); consecutive
+  // launches continue the tag sequence, so the T tokens here stand for any
+  // split of them into launches
   for (auto& w : x) w.store(0);
   for (auto& w : qkv) w.store(0);
   for (auto& w : part) w.store(0);
