@@ -83,6 +83,14 @@ def test_null_handle_errors_are_reported(clib):
     assert clib.megakernel_set_attention_chunk(None, 64) == -1
     assert clib.megakernel_set_attention_merge(None, 8) == -1
     assert clib.megakernel_grid_size(None) == -1
+    assert clib.megakernel_set_lmhead_fp8(None, 1) == -1
+    assert "handle" in _lib.last_error(clib)
+    assert clib.megakernel_get_lmhead_fp8(None, None, None) == -1
+    assert "FP8 LM head" in _lib.last_error(clib)
+    assert clib.megakernel_set_kv_fp8(None, 1) == -1
+    assert "handle" in _lib.last_error(clib)
+    assert clib.megakernel_batch_set_kv_fp8(None, 1) == -1
+    assert "handle" in _lib.last_error(clib)
     clib.megakernel_reset(None)  # no-ops, as in the reference
     clib.megakernel_free(None)
 
