@@ -197,6 +197,8 @@ def bench_batch(args):
     eng = BatchEngine(dw, B, args.kv_max + max(K, W) + 8, shape)
     if args.kv_fp8:
         eng.set_kv_fp8(True)
+    if args.lmhead_fp8:
+        eng.set_lmhead_fp8(True)
     info = launcher.detect_gpu()
     first = [int(t) for t in rng.integers(0, shape.vocab, size=B)]
 
@@ -220,7 +222,8 @@ def bench_batch(args):
     kvp = shape.kv_bytes_per_pos  # per position; FP8: 1 byte per value plus a 4-byte scale per row
     if args.kv_fp8:
         kvp = kvp // 2 + 2 * 4 * shape.n_kv_heads * shape.n_layers
-    nbytes = sum(shape.weight_bytes + sum(kvp * (n + i + 2) for n in lengths) for i in range(K))
+    wb = shape.weight_bytes - (shape.vocab * shape.hidden - 4 * shape.vocab if args.lmhead_fp8 else 0)
+    nbytes = sum(wb + sum(kvp * (n + i + 2) for n in lengths) for i in range(K))
     achieved = nbytes / kern / 1e9
     eng.close()
     dw.free()
@@ -228,7 +231,9 @@ def bench_batch(args):
         "metric": f"batched greedy decode tok/s ({B} sequences, KV {args.kv_min}-{args.kv_max})",
         "value": round(B * K / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16 (KV cache fp8 e4m3)" if args.kv_fp8 else "bf16", "data": "synthetic",
+        "vs_baseline": None, "data": "synthetic",
+        "dtype": "bf16" + "".join(f" ({w} fp8 e4m3)" for w, on in (("LM head", args.lmhead_fp8),
+                                                                     ("KV cache", args.kv_fp8)) if on),
         "config": {"workload": f"Qwen3-0.6B-shaped batched decode, {B} sequences, KV lengths {lengths}, "
                                f"{K} steps (BASELINE configs[4])", "sequences": B, "kv_lengths": lengths,
                    "device": info["name"], "reps": args.reps},

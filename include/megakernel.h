@@ -257,6 +257,11 @@ int megakernel_batch_prefill(void* handle, int seq, const int* tokens, int n, in
  * appends FP8 rows.  Returns 0 or -1. */
 int megakernel_batch_set_kv_fp8(void* handle, int enable);
 
+/* FP8 LM head for a batch handle (no counterpart in the reference): the copy
+ * of megakernel_set_lmhead_fp8, built once from the handle's bf16 tiles; the
+ * step graph is captured again.  Returns 0 or -1. */
+int megakernel_batch_set_lmhead_fp8(void* handle, int enable);
+
 /* Device time of the last megakernel_generate_batch / decode_batch / prefill call (ms). */
 float megakernel_batch_last_ms(void* handle);
 

@@ -68,6 +68,7 @@ SIGNATURES = {
     "megakernel_batch_debug_logits": (c_int, [c_void_p, P_int, P_int, P_float]),
     "megakernel_batch_prefill": (c_int, [c_void_p, c_int, P_int, c_int, P_int, P_float]),
     "megakernel_batch_set_kv_fp8": (c_int, [c_void_p, c_int]),
+    "megakernel_batch_set_lmhead_fp8": (c_int, [c_void_p, c_int]),
     "megakernel_batch_last_ms": (c_float, [c_void_p]),
     # operator microbench
     "megakernel_op_packed_bytes": (c_ll, [c_int, c_int]),

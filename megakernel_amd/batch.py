@@ -49,6 +49,11 @@ class BatchEngine:
         the caches are emptied and every position reset to 0."""
         _lib.check(self.lib, self.lib.megakernel_batch_set_kv_fp8(self._handle, int(bool(enable))), "batch_set_kv_fp8")
 
+    def set_lmhead_fp8(self, enable: bool = True):
+        """Stream the FP8 (e4m3, power-of-two row scales) copy of the LM head."""
+        _lib.check(self.lib, self.lib.megakernel_batch_set_lmhead_fp8(self._handle, int(bool(enable))),
+                   "batch_set_lmhead_fp8")
+
     def fill_kv_synthetic(self, seq: int, length: int, seed: int, std: float = 1.0):
         _lib.check(self.lib, self.lib.megakernel_batch_fill_kv_synthetic(self._handle, seq, length, seed, std),
                    "batch_fill_kv_synthetic")

@@ -31,6 +31,8 @@ struct BHandle {
   int *pf_tok = nullptr, *pf_pos = nullptr, *pf_out = nullptr, *pf_step = nullptr;
   std::vector<void*> owned;
   float *kscale = nullptr, *vscale = nullptr;  // FP8 cache scales, allocated on first use
+  u32x4* lmhead8 = nullptr;                     // FP8 LM head copy, built on first use
+  float* lm_scale = nullptr;
   int (*launch_step)(BHandle*, const BParams&) = nullptr;
   int (*launch_prefill)(BHandle*, const BParams&, bool) = nullptr;
 };
@@ -84,7 +86,10 @@ static int launch_step(BHandle* h, const BParams& p) {
     hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, p, l);
     hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
   }
-  hipLaunchKernelGGL(bk_lm<S>, dim3(h->G), dim3(GT), 0, h->stream, p);
+  if (p.lmhead8)
+    hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p);
+  else
+    hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, p);
   hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
   HIPCHK(hipGetLastError(), -1);
   return 0;
@@ -112,7 +117,10 @@ static int launch_prefill(BHandle* h, const BParams& p, bool last) {
     hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
   }
   if (last) {
-    hipLaunchKernelGGL(bk_lm<S>, dim3(h->G), dim3(GT), 0, h->stream, p);
+    if (p.lmhead8)
+      hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p);
+    else
+      hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, p);
     hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
   }
   HIPCHK(hipGetLastError(), -1);
@@ -634,6 +642,34 @@ int megakernel_batch_set_kv_fp8(void* handle, int enable) {
   HIPCHK(hipMemsetAsync(h->p.pos, 0, mk::batch::BMAX * 4, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
   if (h->exec) (void)hipGraphExecDestroy(h->exec);
+  if (h->graph) (void)hipGraphDestroy(h->graph);
+  h->exec = nullptr;
+  h->graph = nullptr;
+  return 0;
+}
+
+int megakernel_batch_set_lmhead_fp8(void* handle, int enable) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  if (enable && !h->lmhead8) {
+    if (h->V % 16 || h->H % 64) {
+      mk::set_err("FP8 LM head needs vocab %% 16 == 0 and hidden %% 64 == 0");
+      return -1;
+    }
+    if (mk::batch::alloc(h, &h->lmhead8, (size_t)h->V * h->H, false) ||
+        mk::batch::alloc(h, &h->lm_scale, (size_t)h->V * 4, false))
+      return -1;
+    hipLaunchKernelGGL(mk::lmhead_fp8_kernel, dim3(h->V / 16), dim3(256), 0, h->stream, h->p.lmhead, h->H,
+                       reinterpret_cast<unsigned char*>(h->lmhead8), h->lm_scale);
+    HIPCHK(hipGetLastError(), -1);
+    HIPCHK(hipStreamSynchronize(h->stream), -1);
+  }
+  h->p.lmhead8 = enable ? h->lmhead8 : nullptr;
+  h->p.lm_scale = enable ? h->lm_scale : nullptr;
+  if (h->exec) (void)hipGraphExecDestroy(h->exec);  // captured again with the matching LM head
   if (h->graph) (void)hipGraphDestroy(h->graph);
   h->exec = nullptr;
   h->graph = nullptr;

@@ -59,6 +59,8 @@ struct BParams {
   const u32x4* wu;          // per layer up
   const u32x4* wd;          // per layer down [H/16][F/32]
   const u32x4* lmhead;      // [V/16][H/32]
+  const u32x4* lmhead8;     // optional FP8 (e4m3) copy [V/16][H/64][64] (bk_lm<S, true>)
+  const float* lm_scale;    // [V] its power-of-two row scales
   long long u_qkv, u_o, u_gu, u_dn;  // 16-byte units per layer of each matrix
   const uint16_t* norms;    // [L][NORM_STRIDE] bf16
   const uint16_t* final_norm;
@@ -396,8 +398,11 @@ __global__ __launch_bounds__(GT) void bk_down(BParams p, int layer) {
 // sampling.cuh:32-117).  Each wave scores whole 16-row blocks; keys are
 // ordered(logit) << 32 | (0xffffffff - index), combined with an atomic max, so
 // the result is the largest logit and, among equal logits, the lowest index.
-template <class S>
+template <class S, bool F8 = false>
 __global__ __launch_bounds__(GT) void bk_lm(BParams p) {
+  // F8: the FP8 copy; a lane's 16 bytes (row l & 15, columns 64 u + 16 kg ..
+  // + 15 of unit u) feed two MFMA k-steps, whose B operands take the same
+  // columns of the hidden state; the row scale enters the conversion
   constexpr int LD = S::H + 8;  // padded LDS rows: the 16 sequences on different banks
   __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * LD], lo[BMAX * LD];
   __shared__ u64 best_w[GW][BMAX];
@@ -421,15 +426,16 @@ __global__ __launch_bounds__(GT) void bk_lm(BParams p) {
   u64 best = 0ull;
   // the wave's blocks rb0, rb0 + stride, ... as a flat sequence of chunks of
   // U tiles; the next chunk's loads are issued before the current one's products
-  constexpr int U = 8, CPB = S::KT_H / U;  // chunks per block
-  static_assert(S::KT_H % U == 0, "whole chunks per block");
+  constexpr int KT = F8 ? S::H / 64 : S::KT_H;  // 1 KiB units per 16-row block
+  constexpr int U = KT < 8 ? KT : 8, CPB = KT / U;  // chunks per block
+  static_assert(KT % U == 0, "whole chunks per block");
   const int rb0 = blockIdx.x * GW + w, stride = gridDim.x * GW;
   const int nblk = rb0 < nb ? (nb - 1 - rb0) / stride + 1 : 0;
   const int nch = nblk * CPB;
   u32x4 cur[U], nxt[U];
   auto load_chunk = [&](int c, u32x4* dst) {
     const int rb = rb0 + (c / CPB) * stride, k0 = (c % CPB) * U;
-    const auto rs = make_rsrc(p.lmhead + (long long)rb * S::KT_H * 64);
+    const auto rs = make_rsrc((F8 ? p.lmhead8 : p.lmhead) + (long long)rb * KT * 64);
 #pragma unroll
     for (int u = 0; u < U; ++u) dst[u] = buf_ld_nt(rs, l * 16u, (unsigned)(k0 + u) * 1024u);
   };
@@ -438,11 +444,26 @@ __global__ __launch_bounds__(GT) void bk_lm(BParams p) {
   for (int c = 0; c < nch; ++c) {
     if (c + 1 < nch) load_chunk(c + 1, nxt);
     const int k0 = (c % CPB) * U;
+    if constexpr (F8) {
+      const float sc = p.lm_scale[(long long)(rb0 + (c / CPB) * stride) * 16 + n];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kt = k0 + u;
-      a0 = mfma(cur[u], *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt), a0);
-      a1 = mfma(cur[u], *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt), a1);
+      for (int u = 0; u < U; ++u) {
+        const int kt = k0 + u;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const u32x4 wb = fp8x8_to_bf16x8_scaled(half ? u32x2{cur[u][2], cur[u][3]} : u32x2{cur[u][0], cur[u][1]}, sc);
+          const int col = 64 * kt + 16 * kg + 8 * half - 8 * kg;  // bo already holds 8 kg
+          a0 = mfma(wb, *reinterpret_cast<const u32x4*>(hi + bo + col), a0);
+          a1 = mfma(wb, *reinterpret_cast<const u32x4*>(lo + bo + col), a1);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kt = k0 + u;
+        a0 = mfma(cur[u], *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt), a0);
+        a1 = mfma(cur[u], *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt), a1);
+      }
     }
     if (c % CPB == CPB - 1) {  // the block is complete
       const int rb = rb0 + (c / CPB) * stride;

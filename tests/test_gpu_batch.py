@@ -378,3 +378,34 @@ def test_batch_fp8_kv_fill_exact_and_prefill():
     finally:
         eng.close()
         dw.free()
+
+
+@pytest.mark.parametrize("which", ["tiny", "baseline_2l"])
+def test_batch_fp8_lmhead(which):
+    """The batched LM head on the FP8 copy (two MFMA k-steps per lane load, the
+    row scale in the conversion) against per-sequence oracles using the same
+    dequantised table; eager steps, then a graph step."""
+    shape = TINY if which == "tiny" else BASELINE.with_(n_layers=2, vocab=4096)
+    rng = np.random.default_rng(12)
+    lengths = [int(x) for x in rng.integers(0, 200, size=16 if which != "tiny" else 4)]
+    dw, eng, mo = _setup(shape, 37, lengths, 256)
+    try:
+        eng.set_lmhead_fp8(True)
+        mo.orc.use_fp8_lm_head()
+        toks = [int(t) for t in rng.integers(0, shape.vocab, size=len(lengths))]
+        for i in range(2):
+            _print(f"batch fp8 head {which} step {i}")
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(len(lengths))]
+            worst = _check_step(logits, out, refs, f"fp8 head step {i}")
+            _print(f"  worst logits abs err {worst:.2e}")
+            toks = out
+        out = eng.decode(toks)
+        refs = [mo.step(b, toks[b]) for b in range(len(lengths))]
+        for b, r in enumerate(refs):
+            if out[b] != r["token"]:
+                assert qwen3_ref.top2_margin(r["logits"]) <= MARGIN, f"graph step seq {b}"
+    finally:
+        eng.close()
+        dw.free()
+
