@@ -3,6 +3,8 @@
 #   make clean
 # Code objects are built for gfx950 only.  Packed-FP32 instructions are turned
 # off for every HIP translation unit (they are not used by hand either).
+# Translation units compile to objects under _build/ (make -j builds them in
+# parallel) and link into one shared library.
 
 HIPCC      ?= /opt/rocm/bin/hipcc
 ARCH       ?= gfx950
@@ -12,6 +14,7 @@ HIPFLAGS   := --offload-arch=$(ARCH) -O3 -std=c++17 -fPIC \
 CSRC       := megakernel_amd/csrc
 LIB        := megakernel_amd/megakernel.so
 SRCS       := $(CSRC)/megakernel.hip $(CSRC)/batch.hip $(CSRC)/ops.hip $(CSRC)/selftest.hip
+OBJS       := $(patsubst $(CSRC)/%.hip,_build/%.o,$(SRCS))
 HDRS       := $(wildcard $(CSRC)/*.h) include/megakernel.h
 
 .PHONY: all lib clean asm
@@ -20,13 +23,18 @@ all: lib
 
 lib: $(LIB)
 
-$(LIB): $(SRCS) $(HDRS)
-	$(HIPCC) $(HIPFLAGS) -shared -Iinclude $(SRCS) -o $@.tmp
+_build/%.o: $(CSRC)/%.hip $(HDRS)
+	@mkdir -p _build
+	$(HIPCC) $(HIPFLAGS) -Iinclude -c $< -o $@
+
+$(LIB): $(OBJS)
+	$(HIPCC) $(HIPFLAGS) -shared $(OBJS) -o $@.tmp
 	mv $@.tmp $@
 
 # Device assembly for inspection (not part of the product).
 asm: $(SRCS) $(HDRS)
-	$(HIPCC) $(HIPFLAGS) -Iinclude --cuda-device-only -S $(SRCS) -o _build/megakernel-gfx950.s
+	@mkdir -p _build
+	$(HIPCC) $(HIPFLAGS) -Iinclude --cuda-device-only -S $(CSRC)/megakernel.hip -o _build/megakernel-gfx950.s
 
 clean:
-	rm -f $(LIB) $(LIB).tmp
+	rm -f $(LIB) $(LIB).tmp $(OBJS)

@@ -43,9 +43,12 @@ extern "C" {
 
 /* Replaces megakernel_init (reference src/megakernel.cu:544-585).
  * d_weights: device pointer to the flat weight buffer; offsets: host array of
- * num_offsets = 2 + 11 * layers byte offsets (310 for 28 layers).  Shapes are
- * the BASELINE preset with vocab MK_DEFAULT_VOCAB and KV capacity
- * MK_DEFAULT_MAX_SEQ.  Returns an opaque handle, or NULL on failure. */
+ * num_offsets = 2 + 11 * layers byte offsets (310 for 28 layers) of the
+ * reference's contiguous weights.bin (host/weight_loader.py:141-192).  The
+ * preset (BASELINE, QWEN3_06B or TINY) and the vocabulary are inferred from
+ * the offset differences; offsets that match no supported shape exactly are
+ * rejected (use megakernel_init_ex).  KV capacity MK_DEFAULT_MAX_SEQ.
+ * Returns an opaque handle, or NULL on failure. */
 void* megakernel_init(void* d_weights, long long* offsets, int num_offsets);
 
 /* Replaces megakernel_decode (reference src/megakernel.cu:588-591).
@@ -74,7 +77,9 @@ void megakernel_sync(void);
 const char* megakernel_last_error(void);
 
 /* megakernel_init with an explicit preset (MK_PRESET_*), vocabulary size
- * (multiple of 16) and KV capacity in positions. */
+ * (multiple of 16) and KV capacity in positions.  When the offsets describe
+ * a contiguous file of another preset or vocabulary the call fails; tensors
+ * of a non-contiguous layout must not overlap at the preset's sizes. */
 void* megakernel_init_ex(void* d_weights, const long long* offsets, int num_offsets, int preset, int vocab,
                          int max_seq);
 

@@ -23,17 +23,21 @@ import time
 import numpy as np
 
 from . import _lib
-from .config import BASELINE, HBM_PEAK_GBPS, ModelShape
-from .weights import load_offsets, ordered_from_dict
+from .config import HBM_PEAK_GBPS, ModelShape
+from .weights import infer_shape, load_offsets, ordered_from_dict
 
 
 class MegakernelEngine:
     """Python wrapper around the megakernel shared library."""
 
     def __init__(self, weights_path=None, offsets_path=None, lib_path=None, tokenizer=None,
-                 shape: ModelShape = BASELINE, max_seq: int | None = None,
+                 shape: ModelShape | None = None, max_seq: int | None = None,
                  device_weights=None, prefill: bool = False):
         self.tokenizer = tokenizer
+        # shape: given, that of device_weights, or inferred from the offsets
+        # file (the reference's bridge passes no shape)
+        if shape is None and device_weights is not None:
+            shape = device_weights.shape
         self.shape = shape
         self.lib = _lib.load(lib_path)
         self.max_seq = max_seq or 33024
@@ -48,6 +52,11 @@ class MegakernelEngine:
     # ------------------------------------------------------------ set-up
     def _load_weights(self, weights_path, offsets_path):
         offs = load_offsets(offsets_path)
+        if self.shape is None:
+            try:
+                self.shape = infer_shape(offs)
+            except ValueError as e:
+                raise _lib.MegakernelError(str(e)) from None
         order = ordered_from_dict(self.shape, offs)
         data = np.fromfile(weights_path, dtype=np.uint8)
         arr = (ctypes.c_longlong * len(order))(*order)

@@ -4,6 +4,7 @@
 // additive extension declared in include/megakernel.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -573,10 +574,103 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   return 0;
 }
 
+// Byte sizes of the tensors of one layer of shape S, in the reference's offset
+// order (attn_norm, w_q, w_k, w_v, q_norm, k_norm, w_o, ffn_norm, w_gate, w_up,
+// w_down; /root/reference/host/weight_loader.py:141-192, bridge.py:86-93).
+template <class S>
+static void layer_tensor_bytes(long long b[11]) {
+  const long long H = S::H, QD = S::QD, KVD = S::KVD, D = S::D, F = S::F;
+  const long long v[11] = {H, QD * H, KVD * H, KVD * H, D, D, H * QD, H, F * H, F * H, H * F};
+  for (int i = 0; i < 11; ++i) b[i] = 2 * v[i];
+}
+
+template <class S>
+static bool contiguous_for(const long long* off, int n_off, int* vocab) {
+  if (n_off < 13 || (n_off - 2) % 11 != 0) return false;
+  long long b[11];
+  layer_tensor_bytes<S>(b);
+  const long long emb = off[1] - off[0];
+  if (emb <= 0 || emb % (2LL * S::H) != 0 || off[2] - off[1] != 2LL * S::H) return false;
+  const int L = (n_off - 2) / 11;
+  for (int l = 0; l < L; ++l) {
+    const long long* o = off + 2 + 11 * l;
+    for (int k = 0; k < 10; ++k)
+      if (o[k + 1] - o[k] != b[k]) return false;
+    if (l + 1 < L && o[11] - o[10] != b[10]) return false;
+  }
+  *vocab = (int)(emb / (2LL * S::H));
+  return true;
+}
+
+// The preset (and vocabulary) whose contiguous weights.bin the offsets
+// describe exactly -- the file the reference's weight loader writes -- or -1.
+static int contiguous_preset(const long long* off, int n_off, int* vocab) {
+  if (contiguous_for<ShapeBaseline>(off, n_off, vocab)) return PRESET_BASELINE;
+  if (contiguous_for<ShapeQwen3>(off, n_off, vocab)) return PRESET_QWEN3_06B;
+  if (contiguous_for<ShapeTiny>(off, n_off, vocab)) return PRESET_TINY;
+  return -1;
+}
+
+static const char* preset_name(int p) {
+  return p == PRESET_BASELINE ? "BASELINE (head_dim 64, ffn 2816)"
+                              : p == PRESET_QWEN3_06B ? "QWEN3_06B (head_dim 128, ffn 3072)" : "TINY";
+}
+
+// Tensors of a non-contiguous layout must not overlap at the preset's sizes
+// (a preset larger than the file's tensors would read into its neighbours).
+template <class S>
+static bool disjoint_for(const long long* off, int n_off, int vocab) {
+  std::vector<std::pair<long long, long long>> iv;
+  iv.reserve(n_off);
+  long long b[11];
+  layer_tensor_bytes<S>(b);
+  iv.push_back({off[0], 2LL * vocab * S::H});
+  iv.push_back({off[1], 2LL * S::H});
+  for (int i = 2; i < n_off; ++i) iv.push_back({off[i], b[(i - 2) % 11]});
+  std::sort(iv.begin(), iv.end());
+  for (size_t i = 1; i < iv.size(); ++i)
+    if (iv[i - 1].first + iv[i - 1].second > iv[i].first) return false;
+  return true;
+}
+
+static bool disjoint(int preset, const long long* off, int n_off, int vocab) {
+  switch (preset) {
+    case PRESET_BASELINE: return disjoint_for<ShapeBaseline>(off, n_off, vocab);
+    case PRESET_QWEN3_06B: return disjoint_for<ShapeQwen3>(off, n_off, vocab);
+    default: return disjoint_for<ShapeTiny>(off, n_off, vocab);
+  }
+}
+
+// preset < 0: infer preset and vocabulary from the offsets (the reference's
+// megakernel_init passes no shape).  An explicit preset must agree with what
+// a contiguous file's offsets imply.
 static Handle* init_common(const void* d_weights, const long long* offsets, int n_off, int preset, int vocab,
                            int max_seq, void* owned) {
   if (!d_weights || !offsets) {
     set_err("null weights or offsets");
+    return nullptr;
+  }
+  if (n_off < 13 || (n_off - 2) % 11 != 0) {
+    set_err("num_offsets=%d is not 2 + 11*layers", n_off);
+    return nullptr;
+  }
+  int inf_vocab = 0;
+  const int inf = contiguous_preset(offsets, n_off, &inf_vocab);
+  if (preset < 0) {
+    if (inf < 0) {
+      set_err("offsets do not describe a contiguous weights.bin of a supported shape (BASELINE, QWEN3_06B, TINY); "
+              "use megakernel_init_ex with an explicit preset");
+      return nullptr;
+    }
+    preset = inf;
+    vocab = inf_vocab;
+  } else if (inf >= 0 && (inf != preset || inf_vocab != vocab)) {
+    set_err("offsets describe a %s file with vocab %d, not preset %s with vocab %d", preset_name(inf), inf_vocab,
+            preset_name(preset), vocab);
+    return nullptr;
+  } else if (inf < 0 && (preset == PRESET_BASELINE || preset == PRESET_QWEN3_06B || preset == PRESET_TINY) &&
+             vocab > 0 && !disjoint(preset, offsets, n_off, vocab)) {
+    set_err("tensors overlap at the sizes of preset %s with vocab %d", preset_name(preset), vocab);
     return nullptr;
   }
   Handle* h = create(preset, vocab, max_seq);
@@ -584,6 +678,7 @@ static Handle* init_common(const void* d_weights, const long long* offsets, int 
   h->owned_flat = owned;
   if (n_off > 0) h->offsets.assign(offsets, offsets + n_off);
   if (check_occupancy(h) || init_device_state(h, static_cast<const char*>(d_weights), offsets, n_off)) {
+    h->owned_flat = nullptr;  // the caller still owns (and frees) the uploaded copy
     free_all(h);
     delete h;
     return nullptr;
@@ -601,8 +696,8 @@ using mk::Handle;
 extern "C" {
 
 void* megakernel_init(void* d_weights, long long* offsets, int num_offsets) {
-  return mk::init_common(d_weights, offsets, num_offsets, mk::PRESET_BASELINE, MK_DEFAULT_VOCAB,
-                         MK_DEFAULT_MAX_SEQ, nullptr);
+  // shape and vocabulary from the offsets of the reference's contiguous file
+  return mk::init_common(d_weights, offsets, num_offsets, -1, 0, MK_DEFAULT_MAX_SEQ, nullptr);
 }
 
 int megakernel_decode(void* handle, int input_token) {

@@ -88,6 +88,35 @@ def load_offsets(offsets_path: str) -> dict[str, int]:
         return {k: int(v) for k, v in json.load(f).items()}
 
 
+def infer_shape(offs: dict[str, int]) -> ModelShape:
+    """The compiled preset (with layer count and vocabulary) whose contiguous
+    weights.bin these offsets describe exactly -- the file the reference's
+    weight loader writes (/root/reference/host/weight_loader.py:141-192).
+    Raises ValueError when no preset matches (the library's megakernel_init
+    applies the same rule)."""
+    from . import config as _cfg
+    n_layers = 0
+    while f"layer.{n_layers}.attn_norm" in offs:
+        n_layers += 1
+    if n_layers == 0 or "embedding" not in offs or "final_norm" not in offs:
+        raise ValueError("offsets lack embedding / final_norm / layer tensors")
+    for preset in (_cfg.BASELINE, _cfg.QWEN3_06B, _cfg.TINY):
+        emb = offs["final_norm"] - offs["embedding"]
+        if emb <= 0 or emb % (2 * preset.hidden):
+            continue
+        cand = preset.with_(n_layers=n_layers, vocab=emb // (2 * preset.hidden))
+        if _contiguous(cand, offs):
+            return cand
+    raise ValueError("offsets do not describe a contiguous weights.bin of a compiled preset "
+                     "(BASELINE, QWEN3_06B, TINY); pass shape= explicitly")
+
+
+def _contiguous(s: ModelShape, offs: dict[str, int]) -> bool:
+    order = ordered_from_dict(s, offs)
+    want = flat_layout(s).ordered_offsets()
+    return all(a - order[0] == b for a, b in zip(order, want))
+
+
 def ordered_from_dict(s: ModelShape, offs: dict[str, int]) -> list[int]:
     out = [offs["embedding"], offs["final_norm"]]
     for i in range(s.n_layers):

@@ -122,3 +122,56 @@ def test_op_argument_checks(clib):
     assert clib.megakernel_op_lmhead_argmax(fake, 0, 1, 4096, 1024, fake, 1, None, None, fake, 1, 1) == -1
     assert clib.megakernel_selftest_dataflow(0, ctypes.byref(ctypes.c_int()), None) == -1
     assert "rounds" in _lib.last_error(clib)
+
+
+def _offsets(shape) -> list[int]:
+    from megakernel_amd.weights import flat_layout
+    return flat_layout(shape).ordered_offsets()
+
+
+def test_init_infers_or_rejects_the_shape_before_gpu_work(clib):
+    """megakernel_init takes no shape (reference src/megakernel.cu:544): the
+    library infers it from the offsets of the contiguous weights.bin, and
+    rejects offsets that match no compiled preset or contradict an explicit
+    one -- before any GPU call (the weight pointer is never dereferenced)."""
+    from megakernel_amd.config import BASELINE, QWEN3_06B
+    fake = ctypes.c_void_p(0x10000)
+    bad = [0, 1, 2] + list(range(100, 100 + 307))  # 310 offsets, no shape's layout
+    arr = (ctypes.c_longlong * len(bad))(*bad)
+    assert clib.megakernel_init(fake, arr, len(bad)) is None
+    assert "contiguous weights.bin" in _lib.last_error(clib)
+    q = _offsets(QWEN3_06B)
+    qa = (ctypes.c_longlong * len(q))(*q)
+    # a QWEN3_06B-shaped file (head_dim 128, ffn 3072) is not read as BASELINE
+    assert clib.megakernel_init_ex(fake, qa, len(q), _lib.PRESET_BASELINE, 151936, 64) is None
+    assert "QWEN3_06B" in _lib.last_error(clib)
+    b = _offsets(BASELINE.with_(vocab=4096))
+    ba = (ctypes.c_longlong * len(b))(*b)
+    assert clib.megakernel_init_ex(fake, ba, len(b), _lib.PRESET_BASELINE, 151936, 64) is None
+    assert "vocab 4096" in _lib.last_error(clib)
+    # a non-contiguous layout whose tensors overlap at the requested preset's sizes
+    over = list(b)
+    over[4] = over[3] + 16  # w_k starts inside w_q
+    oa = (ctypes.c_longlong * len(over))(*over)
+    assert clib.megakernel_init_ex(fake, oa, len(over), _lib.PRESET_BASELINE, 4096, 64) is None
+    assert "overlap" in _lib.last_error(clib)
+    assert clib.megakernel_init(fake, ba, 14) is None  # count is not 2 + 11 * layers
+    assert "num_offsets" in _lib.last_error(clib)
+
+
+def test_engine_infers_shape_from_offsets_file(tmp_path):
+    """MegakernelEngine(weights_path, offsets_path), as the reference bridge
+    is constructed, infers the preset, layer count and vocabulary."""
+    import json
+
+    from megakernel_amd.config import BASELINE, QWEN3_06B, TINY
+    from megakernel_amd.weights import flat_layout, infer_shape
+    for s in (BASELINE, QWEN3_06B, TINY.with_(n_layers=3, vocab=2048)):
+        p = tmp_path / "offs.json"
+        p.write_text(json.dumps(flat_layout(s).offsets))
+        from megakernel_amd.weights import load_offsets
+        assert infer_shape(load_offsets(str(p))) == s
+    offs = dict(flat_layout(BASELINE).offsets)
+    offs["layer.3.w_up"] += 2
+    with pytest.raises(ValueError, match="contiguous"):
+        infer_shape(offs)

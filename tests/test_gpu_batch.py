@@ -409,3 +409,65 @@ def test_batch_fp8_lmhead(which):
         eng.close()
         dw.free()
 
+
+
+def _bench_lengths(seed: int = 2024, kv_min: int = 512, kv_max: int = 4096, n: int = 16):
+    """The lengths bench.py --batch draws (same generator, same order)."""
+    rng = np.random.default_rng(seed)
+    return [int(x) for x in rng.integers(kv_min, kv_max + 1, size=n)], rng
+
+
+@pytest.mark.parametrize("kv_fp8", [False, True])
+def test_batch_bench_lengths_cross_17_splits(kv_fp8):
+    """configs[4] at its real lengths: the 16 cache lengths bench.py draws
+    (seed 2024, uniform in [512, 4096]); the longest sequence is moved to
+    4,090 positions so that the steps carry it past 4,096 positions, i.e. 17
+    attention splits of 256 and a second round of the last split's merge
+    (16 splits per round).  BASELINE shapes, 2 layers, bf16 and FP8 caches."""
+    shape = BASELINE.with_(n_layers=2, vocab=4096)
+    lengths, rng = _bench_lengths()
+    lengths[int(np.argmax(lengths))] = 4090
+    dw, eng, mo = _setup(shape, 36, lengths, 4200, kv_fp8=kv_fp8)
+    try:
+        toks = [int(t) for t in rng.integers(0, shape.vocab, size=16)]
+        for i in range(9):
+            _print(f"batch bench lengths step {i} (fp8 {kv_fp8}): max position {max(eng.positions())}")
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(16)]
+            worst = _check_step(logits, out, refs, f"step {i}")
+            _print(f"  worst logits abs err {worst:.2e}")
+            toks = out
+        assert max(eng.positions()) == 4099
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_batch_full_model_long_sequences():
+    """The full 28-layer model with 6 sequences, 4 of them above 3,000 cached
+    positions (13-16 splits), 2 steps; the oracles' prefixes are the device's
+    own synthetic prefill read back (the prefill itself is bit-exact against
+    the CPU generator, test_batch_kv_append_bytes)."""
+    lengths = [3100, 4001, 3555, 4090, 700, 1]
+    dw = DeviceWeights(BASELINE, 37, std=0.02, gain_std=0.1)
+    eng = BatchEngine(dw, len(lengths), 4100, BASELINE)
+    mo = MultiOracle(BASELINE, dw, len(lengths), 4100)
+    try:
+        for b, n in enumerate(lengths):
+            eng.fill_kv_synthetic(b, n, 600 + b)
+            kv = eng.get_kv(b, n)  # [L][2][NKV][n][D]
+            k, v = mo.caches[b]
+            k[:, :, :n] = qwen3_ref.bits_to_torch(kv[:, 0]).to(k.dtype)
+            v[:, :, :n] = qwen3_ref.bits_to_torch(kv[:, 1]).to(v.dtype)
+            mo.pos[b] = n
+        toks = [1, 2000, 151935, 77, 4096, 65000]
+        for i in range(2):
+            _print(f"batch full model long step {i} positions {eng.positions()}")
+            out, logits = eng.debug_logits(toks)
+            refs = [mo.step(b, toks[b]) for b in range(len(lengths))]
+            worst = _check_step(logits, out, refs, f"step {i}")
+            _print(f"  worst logits abs err {worst:.2e}")
+            toks = out
+    finally:
+        eng.close()
+        dw.free()
