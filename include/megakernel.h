@@ -327,6 +327,18 @@ int megakernel_op_lmhead_argmax(const void* w, long long copy_bytes, int n_copie
                                 int n_in, float* logits, unsigned long long* keys, int* tokens, int n_out,
                                 int reps);
 
+/* megakernel_op_lmhead_argmax without the keys workspace: allocates nothing
+ * (no device allocation, no event, no wait).  It has no counterpart in the
+ * reference; it is for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation.  The keys
+ * live in a static device array of MK_NOALLOC_KEYS_MAX entries per GPU, so
+ * n_out <= MK_NOALLOC_KEYS_MAX (larger calls fail with an error); calls that
+ * overlap on one GPU share that array and race.  The work is enqueued on the
+ * null stream; outputs are complete after the caller synchronises. */
+#define MK_NOALLOC_KEYS_MAX 4096
+int megakernel_op_lmhead_argmax_noalloc(const void* w, long long copy_bytes, int n_copies, int vocab, int k,
+                                        const float* h, int n_in, float* logits, int* tokens, int n_out, int reps);
+
 /* Device time of this thread's last megakernel_op_* call (ms). */
 float megakernel_op_last_ms(void);
 

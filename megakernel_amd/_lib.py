@@ -79,6 +79,8 @@ SIGNATURES = {
     "megakernel_op_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float]),
     "megakernel_op_lmhead_argmax": (c_int, [c_void_p, c_ll, c_int, c_int, c_int, c_void_p, c_int, c_void_p,
                                             c_void_p, c_void_p, c_int, c_int]),
+    "megakernel_op_lmhead_argmax_noalloc": (c_int, [c_void_p, c_ll, c_int, c_int, c_int, c_void_p, c_int,
+                                                    c_void_p, c_void_p, c_int, c_int]),
     "megakernel_op_last_ms": (c_float, []),
     # self-test
     "megakernel_selftest_dataflow": (c_int, [c_int, P_int, P_float]),

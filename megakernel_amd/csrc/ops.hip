@@ -19,6 +19,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "megakernel.h"
 #include "mk_host.h"
 #include "mk_kernel.h"
@@ -347,6 +349,82 @@ static bool gemv_k_ok(int k) {
   return k % 256 == 0 && (c == 1 || c == 2 || c == 4 || c == 8 || c == 11 || c == 12);
 }
 
+
+static bool lmhead_args_ok(const void* w, long long copy_bytes, int n_copies, int vocab, int k, const float* h,
+                           int n_in, const int* tokens, int n_out, int reps) {
+  if (!common_ok(n_in, n_out, reps)) return false;
+  if (!w || !h || !tokens || !aligned16(w) || n_copies < 1 || copy_bytes < 0 || copy_bytes % 16) {
+    set_err("op_lmhead_argmax: null/unaligned pointer, n_copies < 1 or copy_bytes not a multiple of 16");
+    return false;
+  }
+  if (vocab <= 0 || vocab % 16 || vocab > (1 << 30) || (k != 256 && k != 512 && k != 1024)) {
+    set_err("op_lmhead_argmax: vocab=%d (multiple of 16), k=%d (256, 512 or 1024)", vocab, k);
+    return false;
+  }
+  if (n_copies > 1 && copy_bytes < (long long)vocab * k * 2) {
+    set_err("op_lmhead_argmax: copy_bytes %lld < packed matrix bytes %lld", copy_bytes, (long long)vocab * k * 2);
+    return false;
+  }
+  return true;
+}
+
+// Clear the keys (a fill kernel, no memset node), score every row and fold
+// the keys into tokens, on the null stream (not waited for).
+static int lmhead_argmax_enqueue(const void* w, long long copy_bytes, int n_copies, int vocab, int k, const float* h,
+                                 int n_in, float* logits, unsigned long long* keys, int* tokens, int n_out,
+                                 int reps) {
+  const u32x4* wp = static_cast<const u32x4*>(w);
+  const long long cu = copy_bytes / 16;
+  const int tb = 256, nb = (n_out + tb - 1) / tb;
+  hipLaunchKernelGGL(keys_clear_kernel, dim3(nb), dim3(tb), 0, 0, keys, n_out);
+  auto run = [&](auto kern) -> int {
+    const int nb16 = vocab / 16;
+    const int full = grid_for(kern, 0, 1LL << 30);  // resident workgroups
+    if (full < 0) return -1;
+    const int chb = NW * ((nb16 + full * NW - 1) / (full * NW));
+    const int nch = (nb16 + chb - 1) / chb;
+    const int g = full < (long long)reps * nch ? full : (int)((long long)reps * nch);
+    hipLaunchKernelGGL(kern, dim3(g), dim3(NT), 0, 0, wp, cu, n_copies, vocab, h, n_in, logits, keys, n_out, reps,
+                       chb);
+    return 0;
+  };
+  const int rc = k == 256 ? run(lmhead_kernel<8>) : k == 512 ? run(lmhead_kernel<16>) : run(lmhead_kernel<32>);
+  if (rc) return rc;
+  hipLaunchKernelGGL(keys_to_tokens_kernel, dim3(nb), dim3(tb), 0, 0, keys, tokens, n_out);
+  return 0;
+}
+
+// ------------------------------------------- allocation-free LM head argmax
+// The argmax keys of megakernel_op_lmhead_argmax_noalloc live in this
+// file-scope device array instead of a caller workspace.  Every GPU the
+// library runs on holds its own copy until the process ends.  In host code
+// the name `scratch` is only a host-side stand-in: the device address of the
+// current GPU's copy comes from hipGetSymbolAddress, once per device, and is
+// the only form host code passes to kernels.  Calls on one GPU share the
+// array (it keeps the last call's keys; each call clears what it uses), so
+// calls that overlap on one GPU race.
+static __device__ __align__(256) unsigned long long scratch[MK_NOALLOC_KEYS_MAX];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static unsigned long long* g_scratch_dev[kMaxDevices] = {};
+
+static unsigned long long* scratch_keys() {
+  int dev = -1;
+  HIPCHK(hipGetDevice(&dev), nullptr);
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_err("device index %d out of range", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* ptr = nullptr;
+    HIPCHK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), nullptr);
+    g_scratch_dev[dev] = static_cast<unsigned long long*>(ptr);
+  }
+  return g_scratch_dev[dev];
+}
+
 }  // namespace ops
 }  // namespace mk
 
@@ -484,40 +562,29 @@ int megakernel_op_rope(const float* x, const int* pos, float* y, int n_heads, in
 int megakernel_op_lmhead_argmax(const void* w, long long copy_bytes, int n_copies, int vocab, int k, const float* h,
                                 int n_in, float* logits, unsigned long long* keys, int* tokens, int n_out,
                                 int reps) {
-  if (!common_ok(n_in, n_out, reps)) return -1;
-  if (!w || !h || !keys || !tokens || !aligned16(w) || n_copies < 1 || copy_bytes < 0 || copy_bytes % 16) {
-    set_err("op_lmhead_argmax: null/unaligned pointer, n_copies < 1 or copy_bytes not a multiple of 16");
+  if (!lmhead_args_ok(w, copy_bytes, n_copies, vocab, k, h, n_in, tokens, n_out, reps)) return -1;
+  if (!keys) {
+    set_err("op_lmhead_argmax: null keys workspace");
     return -1;
   }
-  if (vocab <= 0 || vocab % 16 || vocab > (1 << 30) || (k != 256 && k != 512 && k != 1024)) {
-    set_err("op_lmhead_argmax: vocab=%d (multiple of 16), k=%d (256, 512 or 1024)", vocab, k);
-    return -1;
-  }
-  if (n_copies > 1 && copy_bytes < (long long)vocab * k * 2) {
-    set_err("op_lmhead_argmax: copy_bytes %lld < packed matrix bytes %lld", copy_bytes, (long long)vocab * k * 2);
-    return -1;
-  }
-  const u32x4* wp = static_cast<const u32x4*>(w);
-  const long long cu = copy_bytes / 16;
   return timed([&]() -> int {
-    const int tb = 256, nb = (n_out + tb - 1) / tb;
-    hipLaunchKernelGGL(keys_clear_kernel, dim3(nb), dim3(tb), 0, 0, keys, n_out);
-    auto run = [&](auto kern) -> int {
-      const int nb16 = vocab / 16;
-      const int full = grid_for(kern, 0, 1LL << 30);  // resident workgroups
-      if (full < 0) return -1;
-      const int chb = NW * ((nb16 + full * NW - 1) / (full * NW));
-      const int nch = (nb16 + chb - 1) / chb;
-      const int g = full < (long long)reps * nch ? full : (int)((long long)reps * nch);
-      hipLaunchKernelGGL(kern, dim3(g), dim3(NT), 0, 0, wp, cu, n_copies, vocab, h, n_in, logits, keys, n_out, reps,
-                         chb);
-      return 0;
-    };
-    const int rc = k == 256 ? run(lmhead_kernel<8>) : k == 512 ? run(lmhead_kernel<16>) : run(lmhead_kernel<32>);
-    if (rc) return rc;
-    hipLaunchKernelGGL(keys_to_tokens_kernel, dim3(nb), dim3(tb), 0, 0, keys, tokens, n_out);
-    return 0;
+    return lmhead_argmax_enqueue(w, copy_bytes, n_copies, vocab, k, h, n_in, logits, keys, tokens, n_out, reps);
   });
+}
+
+int megakernel_op_lmhead_argmax_noalloc(const void* w, long long copy_bytes, int n_copies, int vocab, int k,
+                                        const float* h, int n_in, float* logits, int* tokens, int n_out, int reps) {
+  if (!lmhead_args_ok(w, copy_bytes, n_copies, vocab, k, h, n_in, tokens, n_out, reps)) return -1;
+  if (n_out > MK_NOALLOC_KEYS_MAX) {
+    set_err("op_lmhead_argmax_noalloc: n_out=%d exceeds the static key array (%d entries)", n_out,
+            MK_NOALLOC_KEYS_MAX);
+    return -1;
+  }
+  unsigned long long* keys = scratch_keys();
+  if (!keys) return -1;
+  if (lmhead_argmax_enqueue(w, copy_bytes, n_copies, vocab, k, h, n_in, logits, keys, tokens, n_out, reps)) return -1;
+  HIPCHK(hipGetLastError(), -1);
+  return 0;
 }
 
 float megakernel_op_last_ms(void) { return g_last_ms; }
