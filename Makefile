@@ -13,7 +13,8 @@ HIPFLAGS   := --offload-arch=$(ARCH) -O3 -std=c++17 -fPIC \
               -Wno-unused-command-line-argument
 CSRC       := megakernel_amd/csrc
 LIB        := megakernel_amd/megakernel.so
-SRCS       := $(CSRC)/megakernel.hip $(CSRC)/batch.hip $(CSRC)/ops.hip $(CSRC)/selftest.hip
+SRCS       := $(CSRC)/megakernel.hip $(CSRC)/decode_baseline.hip $(CSRC)/decode_qwen3.hip \
+              $(CSRC)/decode_tiny.hip $(CSRC)/batch.hip $(CSRC)/ops.hip $(CSRC)/selftest.hip
 OBJS       := $(patsubst $(CSRC)/%.hip,_build/%.o,$(SRCS))
 HDRS       := $(wildcard $(CSRC)/*.h) include/megakernel.h
 

@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
     ap.add_argument("--trace", action="store_true", help="print a per-phase critical-path summary")
+    ap.add_argument("--kernel", choices=("auto", "spread"), default="auto",
+                    help="batch-1 decode kernel: auto (class-specialised where it applies) or spread")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 plain device copies of 1 GiB (known bytes) for scaling rocprof counters")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
@@ -488,9 +490,12 @@ def main():
         eng.set_lmhead_fp8(True)
     if args.kv_fp8:
         eng.set_kv_fp8(True)
+    from megakernel_amd import _lib
+    eng.set_decode_kernel(_lib.KERNEL_SPREAD if args.kernel == "spread" else _lib.KERNEL_AUTO)
     info = launcher.detect_gpu()
     grid = eng.grid_size
-    print(f"# device {info['name']} CUs {info['cu_count']} grid {grid}", file=sys.stderr, flush=True)
+    kname = "class" if eng.decode_kernel_for(K) == _lib.KERNEL_CLASS else "spread"
+    print(f"# device {info['name']} CUs {info['cu_count']} grid {grid} kernel {kname}", file=sys.stderr, flush=True)
 
     first = 1
     eng.fill_kv_synthetic(args.ctx, args.seed)

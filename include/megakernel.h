@@ -143,6 +143,20 @@ int megakernel_set_attention_chunk(void* handle, int chunk_min);
  * only. */
 int megakernel_set_attention_merge(void* handle, int merge_min);
 
+/* Which persistent kernel decodes (no counterpart in the reference, whose
+ * kernel has one shape).  MK_KERNEL_AUTO (default): the class-specialised
+ * kernel -- every workgroup keeps one role class for the launch and loads a
+ * role's next weights right after computing it -- whenever a role table
+ * holds all attention items of the launch (up to 4 splits per kv head on the
+ * BASELINE and TINY presets), else the spread kernel; MK_KERNEL_SPREAD: always
+ * the spread kernel.  megakernel_decode_kernel_for reports which kernel a
+ * launch of n_tokens from the current position would use. */
+#define MK_KERNEL_AUTO 0
+#define MK_KERNEL_SPREAD 1
+#define MK_KERNEL_CLASS 2
+int megakernel_set_decode_kernel(void* handle, int variant);
+int megakernel_decode_kernel_for(void* handle, int n_tokens);
+
 /* FP8 LM head (no counterpart in the reference kernel, which plans FP8
  * weights in RESEARCH.md:434-436,463).  enable = 1 builds, once, an OCP e4m3
  * copy of the tied LM head with one power-of-two scale per row (2^e, the

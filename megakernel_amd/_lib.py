@@ -43,6 +43,8 @@ SIGNATURES = {
     "megakernel_grid_size": (c_int, [c_void_p]),
     "megakernel_set_attention_chunk": (c_int, [c_void_p, c_int]),
     "megakernel_set_attention_merge": (c_int, [c_void_p, c_int]),
+    "megakernel_set_decode_kernel": (c_int, [c_void_p, c_int]),
+    "megakernel_decode_kernel_for": (c_int, [c_void_p, c_int]),
     "megakernel_set_lmhead_fp8": (c_int, [c_void_p, c_int]),
     "megakernel_set_kv_fp8": (c_int, [c_void_p, c_int]),
     "megakernel_get_lmhead_fp8": (c_int, [c_void_p, c_void_p, P_float]),
@@ -87,6 +89,7 @@ SIGNATURES = {
 }
 
 PRESET_BASELINE, PRESET_QWEN3_06B, PRESET_TINY = 0, 1, 2
+KERNEL_AUTO, KERNEL_SPREAD, KERNEL_CLASS = 0, 1, 2  # megakernel_set_decode_kernel / _decode_kernel_for
 H2D, D2H, D2D = 0, 1, 2
 
 _cache: dict[str, ctypes.CDLL] = {}

@@ -245,6 +245,17 @@ class MegakernelEngine:
         _lib.check(self.lib, self.lib.megakernel_set_attention_merge(self._handle, merge_min),
                    "set_attention_merge")
 
+    def set_decode_kernel(self, variant: int):
+        """_lib.KERNEL_AUTO (class-specialised kernel where it applies) or
+        _lib.KERNEL_SPREAD (always the spread kernel)."""
+        _lib.check(self.lib, self.lib.megakernel_set_decode_kernel(self._handle, int(variant)), "set_decode_kernel")
+
+    def decode_kernel_for(self, n_tokens: int) -> int:
+        """The kernel (_lib.KERNEL_CLASS or _lib.KERNEL_SPREAD) a launch of
+        n_tokens from the current position uses."""
+        return _lib.check(self.lib, self.lib.megakernel_decode_kernel_for(self._handle, int(n_tokens)),
+                          "decode_kernel_for")
+
     def set_lmhead_fp8(self, enable: bool = True):
         """Stream an FP8 (OCP e4m3, power-of-two row scales) copy of the LM head."""
         _lib.check(self.lib, self.lib.megakernel_set_lmhead_fp8(self._handle, int(bool(enable))),

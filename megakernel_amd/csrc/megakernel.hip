@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -16,6 +17,7 @@
 #include "mk_device.h"
 #include "mk_host.h"
 #include "mk_kernel.h"
+#include "mk_launch.h"
 
 #include "../../include/megakernel.h"
 
@@ -213,6 +215,87 @@ static ShapeInfo shape_info() {
                    S::NORM_STRIDE, S::NORM_ATTN, S::NORM_Q, S::NORM_K, S::NORM_FFN, part_words<S>()};
 }
 
+// Attention splits per kv head up to which the class kernel has role tables.
+constexpr int kMaxClsSplit = 4;
+
+// Role table of the class kernel (mk_cls.h) for `nsplit` attention splits
+// per kv head on G workgroups: attention items on workgroups [0, NKV*nsplit)
+// (item (g, s) on workgroup s*NKV + g: XCD g for 8 kv heads), then QKV +
+// gate/up pairs with kv head g's QKV blocks on XCD g % 8, then gate/up +
+// down, down + O, O (one or two blocks), single roles for whatever has no
+// partner.  False when the shape's blocks do not fit G workgroups this way.
+static bool build_roles(const ShapeInfo& s, int G, int nsplit, std::vector<int>& rows) {
+  const int NA = s.NKV * nsplit, RBQ = s.QKV / 16, RBF = s.F / 16, RBH = s.H / 16;
+  rows.assign((size_t)G * ROLE_INTS, -1);
+  for (int w = 0; w < G; ++w) rows[(size_t)w * ROLE_INTS + RF_CLS] = CLS_IDLE;
+  auto at = [&](int w, int f) -> int& { return rows[(size_t)w * ROLE_INTS + f]; };
+  if (NA > G) return false;
+  int w = 0;
+  for (; w < NA; ++w) {
+    at(w, RF_CLS) = CLS_ATT;
+    at(w, RF_ATT) = w;
+  }
+  // QKV blocks grouped by the XCD of their kv head
+  std::vector<int> by_xcd[8];
+  for (int b = 0; b < RBQ; ++b) {
+    const int row = 16 * b;
+    const int g = row < s.QD ? (row / s.D) / s.GQA : (row < s.QD + s.KVD ? (row - s.QD) / s.D : (row - s.QD - s.KVD) / s.D);
+    by_xcd[g % 8].push_back(b);
+  }
+  size_t next_any = 0;
+  std::vector<char> used(RBQ, 0);
+  auto take_q = [&](int wg) -> int {
+    auto& v = by_xcd[wg % 8];
+    for (int b : v)
+      if (!used[b]) return used[b] = 1, b;
+    for (; next_any < (size_t)RBQ; ++next_any)
+      if (!used[next_any]) return used[next_any] = 1, (int)next_any;
+    return -1;
+  };
+  const int nqg = RBQ < RBF ? RBQ : RBF;
+  if (w + nqg > G) return false;
+  for (int i = 0; i < nqg; ++i, ++w) {
+    at(w, RF_CLS) = CLS_QG;
+    at(w, RF_Q) = take_q(w);
+    at(w, RF_G) = i;
+  }
+  for (int i = nqg; i < RBQ; ++i, ++w) {  // QKV blocks without a gate/up partner
+    if (w >= G) return false;
+    at(w, RF_CLS) = CLS_Q;
+    at(w, RF_Q) = take_q(w);
+  }
+  int d = 0, o = 0;
+  for (int gi = nqg; gi < RBF; ++gi, ++w) {  // gate/up pairs: with a down block while they last
+    if (w >= G) return false;
+    at(w, RF_G) = gi;
+    if (d < RBH) {
+      at(w, RF_CLS) = CLS_DG;
+      at(w, RF_D) = d++;
+    } else {
+      at(w, RF_CLS) = CLS_G;
+    }
+  }
+  for (; d < RBH; ++d, ++w) {  // down blocks: with an O block while they last
+    if (w >= G) return false;
+    at(w, RF_D) = d;
+    if (o < RBH) {
+      at(w, RF_CLS) = CLS_DO;
+      at(w, RF_O0) = o++;
+    } else {
+      at(w, RF_CLS) = CLS_D;
+    }
+  }
+  const int rem_o = RBH - o, rem_w = G - w;
+  if (rem_o > 2 * rem_w) return false;
+  const int two = rem_o > rem_w ? rem_o - rem_w : 0;  // workgroups that take two O blocks
+  for (int i = 0; o < RBH; ++i, ++w) {
+    at(w, RF_CLS) = CLS_O;
+    at(w, RF_O0) = o++;
+    if (i < two) at(w, RF_O1) = o++;
+  }
+  return true;
+}
+
 struct Handle {
   int device = 0, preset = 0, G = 0;
   ShapeInfo sh{};
@@ -253,61 +336,18 @@ struct Handle {
   long long kv_bytes = 0;
   int s_pad = 0;               // KV capacity rounded up to whole 32-position blocks
   uint16_t* kvt = nullptr;     // V^T region inside the kv allocation
-  hipError_t (*launch)(Handle*, const Params&, bool) = nullptr;
+  DecodeLaunch launch = nullptr;
+  // class kernel role tables for 1..kMaxClsSplit attention splits per kv head
+  // ([kMaxClsSplit][G][ROLE_INTS] ints); roles_ok[k]: a table for k splits exists
+  int* roles = nullptr;
+  bool roles_ok[kMaxClsSplit + 1] = {};
+  int kernel_variant = MK_KERNEL_AUTO;
+  int pace_pct = 100;  // class kernel prefetch pacing (environment MK_PACE_PCT at init; 0 = bursts)
 };
 
-// lc: the launch reaches more than merge_min attention splits per kv head;
-// the debug instantiation when the launch records timestamps or validation
-// outputs; the FP8 LM head when the handle has it switched on
-template <class S, int MODE>
-static void launch_mode(Handle* h, const Params& p) {
-  hipLaunchKernelGGL((decode_kernel<S, MODE>), dim3(h->G), dim3(NT), 0, h->stream, p);
-}
-
-template <class S>
-static hipError_t launch_decode(Handle* h, const Params& p, bool lc) {
-  const int mode = (lc ? 1 : 0) | (p.trace || p.dbg_layers || p.dbg_logits ? 2 : 0) | (p.lmhead8 ? 4 : 0) |
-                   (p.kscale ? 8 : 0);
-  switch (mode) {
-    case 0: launch_mode<S, 0>(h, p); break;
-    case 1: launch_mode<S, 1>(h, p); break;
-    case 2: launch_mode<S, 2>(h, p); break;
-    case 3: launch_mode<S, 3>(h, p); break;
-    case 4: launch_mode<S, 4>(h, p); break;
-    case 5: launch_mode<S, 5>(h, p); break;
-    case 6: launch_mode<S, 6>(h, p); break;
-    case 7: launch_mode<S, 7>(h, p); break;
-    case 8: launch_mode<S, 8>(h, p); break;
-    case 9: launch_mode<S, 9>(h, p); break;
-    case 10: launch_mode<S, 10>(h, p); break;
-    case 11: launch_mode<S, 11>(h, p); break;
-    case 12: launch_mode<S, 12>(h, p); break;
-    case 13: launch_mode<S, 13>(h, p); break;
-    case 14: launch_mode<S, 14>(h, p); break;
-    default: launch_mode<S, 15>(h, p); break;
-  }
-  return hipGetLastError();
-}
-
-template <class S, int MODE>
-static int occupancy_of() {
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<S, MODE>, NT, 0) != hipSuccess) return 0;
-  return n;
-}
-
-template <class S>
-static int occupancy_ok(int* nblk) {
-  const int n[16] = {occupancy_of<S, 0>(),  occupancy_of<S, 1>(),  occupancy_of<S, 2>(),  occupancy_of<S, 3>(),
-                     occupancy_of<S, 4>(),  occupancy_of<S, 5>(),  occupancy_of<S, 6>(),  occupancy_of<S, 7>(),
-                     occupancy_of<S, 8>(),  occupancy_of<S, 9>(),  occupancy_of<S, 10>(), occupancy_of<S, 11>(),
-                     occupancy_of<S, 12>(), occupancy_of<S, 13>(), occupancy_of<S, 14>(), occupancy_of<S, 15>()};
-  *nblk = n[0];
-  for (int i = 1; i < 16; ++i) *nblk = n[i] < *nblk ? n[i] : *nblk;
-  return 1;
-}
-
 static void free_all(Handle* h) {
+  if (h->roles) (void)hipFree(h->roles);
+  h->roles = nullptr;
   batch::destroy_prefill_context(h->prefill);
   h->prefill = nullptr;
   void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->kscale, h->vscale, h->kv, h->x, h->qkv, h->part,
@@ -381,6 +421,17 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
     HIPCHK(hipMalloc(tagged[i], h->tagged_bytes[i]), -1);
     HIPCHK(hipMemsetAsync(*tagged[i], 0, h->tagged_bytes[i], h->stream), -1);
   }
+  // role tables of the class kernel (kept on the device; a launch points at one)
+  {
+    std::vector<int> all((size_t)kMaxClsSplit * h->G * ROLE_INTS, 0), one;
+    for (int k = 1; k <= kMaxClsSplit; ++k) {
+      h->roles_ok[k] = build_roles(s, h->G, k, one);
+      if (h->roles_ok[k]) std::copy(one.begin(), one.end(), all.begin() + (size_t)(k - 1) * h->G * ROLE_INTS);
+    }
+    HIPCHK(hipMalloc(&h->roles, all.size() * sizeof(int)), -1);
+    HIPCHK(hipMemcpyAsync(h->roles, all.data(), all.size() * sizeof(int), hipMemcpyHostToDevice, h->stream), -1);
+    HIPCHK(hipStreamSynchronize(h->stream), -1);
+  }
   h->max_launch_tokens = 1 << 20;
   HIPCHK(hipMalloc(&h->trace, ((size_t)(5 * h->L + 1) * 2 + EVT_N) * h->G * 8), -1);
   // error word (256 bytes), then the output tokens: one copy brings both back
@@ -433,18 +484,19 @@ static Handle* create(int preset, int vocab, int max_seq) {
   h->preset = preset;
   h->V = vocab;
   h->S = max_seq;
+  if (const char* e = getenv("MK_PACE_PCT")) h->pace_pct = atoi(e) < 0 ? 0 : atoi(e);
   switch (preset) {
     case PRESET_BASELINE:
       h->sh = shape_info<ShapeBaseline>();
-      h->launch = launch_decode<ShapeBaseline>;
+      h->launch = launch_decode_baseline;
       break;
     case PRESET_QWEN3_06B:
       h->sh = shape_info<ShapeQwen3>();
-      h->launch = launch_decode<ShapeQwen3>;
+      h->launch = launch_decode_qwen3;
       break;
     case PRESET_TINY:
       h->sh = shape_info<ShapeTiny>();
-      h->launch = launch_decode<ShapeTiny>;
+      h->launch = launch_decode_tiny;
       break;
     default:
       set_err("unknown preset %d", preset);
@@ -460,13 +512,13 @@ static Handle* create(int preset, int vocab, int max_seq) {
 }
 
 static int check_occupancy(Handle* h) {
-  int nblk = 0, ok = 0;
+  int nblk = 0;
   switch (h->preset) {
-    case PRESET_BASELINE: ok = occupancy_ok<ShapeBaseline>(&nblk); break;
-    case PRESET_QWEN3_06B: ok = occupancy_ok<ShapeQwen3>(&nblk); break;
-    default: ok = occupancy_ok<ShapeTiny>(&nblk); break;
+    case PRESET_BASELINE: nblk = occupancy_decode_baseline(); break;
+    case PRESET_QWEN3_06B: nblk = occupancy_decode_qwen3(); break;
+    default: nblk = occupancy_decode_tiny(); break;
   }
-  if (!ok || nblk < 1) {
+  if (nblk < 1) {
     set_err("persistent kernel cannot keep one workgroup resident per CU (occupancy %d)", nblk);
     return -1;
   }
@@ -551,11 +603,17 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.nsplit_max = h->nsplit_max;
   p.chunk_min = h->chunk_min;
   p.merge_min = h->merge_min;
+  p.pace_pct = h->pace_pct;
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
   // the long-context instantiation when the launch's last token has more
   // than merge_min splits per kv head (split counts grow with the position)
-  const bool lc = split_count(h->pos + n, h->chunk_min, h->nsplit_max) > h->merge_min;
-  HIPCHK(h->launch(h, p, lc), -1);
+  const int ns_last = split_count(h->pos + n, h->chunk_min, h->nsplit_max);
+  const bool lc = ns_last > h->merge_min;
+  // the class kernel when a role table holds every attention item of the
+  // launch (its attention workgroups serve the last token's split count)
+  const bool cls = h->kernel_variant == MK_KERNEL_AUTO && !lc && ns_last <= kMaxClsSplit && h->roles_ok[ns_last];
+  p.roles = cls ? h->roles + (size_t)(ns_last - 1) * h->G * ROLE_INTS : nullptr;
+  HIPCHK(h->launch(h->G, h->stream, p, lc, cls), -1);
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
   // error word and tokens come back in one copy into pinned memory
   HIPCHK(hipMemcpyAsync(h->host_io, h->err, 256 + (out_host ? (size_t)n * 4 : 0), hipMemcpyDeviceToHost, h->stream),
@@ -986,6 +1044,32 @@ int megakernel_set_attention_merge(void* handle, int merge_min) {
   if (merge_min != h->merge_min && mk::clear_pair_words(h)) return -1;
   h->merge_min = merge_min;
   return 0;
+}
+
+int megakernel_set_decode_kernel(void* handle, int variant) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  if (variant != MK_KERNEL_AUTO && variant != MK_KERNEL_SPREAD) {
+    mk::set_err("unknown decode kernel variant %d", variant);
+    return -1;
+  }
+  h->kernel_variant = variant;
+  return 0;
+}
+
+int megakernel_decode_kernel_for(void* handle, int n_tokens) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || n_tokens < 1) {
+    mk::set_err("null handle or token count < 1");
+    return -1;
+  }
+  const int ns = mk::split_count(h->pos + n_tokens, h->chunk_min, h->nsplit_max);
+  const bool cls = h->kernel_variant == MK_KERNEL_AUTO && ns <= h->merge_min && ns <= mk::kMaxClsSplit &&
+                   h->roles_ok[ns];
+  return cls ? MK_KERNEL_CLASS : MK_KERNEL_SPREAD;
 }
 
 int megakernel_set_attention_chunk(void* handle, int chunk_min) {

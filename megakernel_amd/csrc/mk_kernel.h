@@ -93,6 +93,8 @@ struct Params {
   int nsplit_max, chunk_min;
   int merge_min;              // above this many splits the last split of a kv head merges them
   int trace_token;
+  const int* roles;           // class kernel: [G][ROLE_INTS] role rows (null for the spread kernel)
+  int pace_pct;               // class kernel: prefetch pacing, percent of the default spacing (0: bursts)
 };
 
 template <class S>
@@ -104,7 +106,7 @@ struct Smem {
   float vec_g[S::H];                  // gate/up: x * ffn_norm gain
   float vec_d[S::F];                  // down: SiLU(gate) * up
   float vec_l[S::H];                  // LM head: x * final_norm gain
-  float xres_o[16], xres_d[16];       // residual rows of this workgroup's O / down block
+  float xres_o[32], xres_d[16];       // residual rows of this workgroup's O block(s) / down block
   float ssw[3][NW];                   // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
   float rowbuf[4][16];                // a block's 16 results, stored by one wave
   __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score A operand
@@ -1083,7 +1085,7 @@ __device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit,
 // workgroup's block.  Thread t owns output pairs t + k NT.
 template <class S>
 __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, u64* xrows,
-                                           unsigned xtag, float* dst, float* xres) {
+                                           unsigned xtag, float* dst, float* xres, u64* xrows2 = nullptr) {
   constexpr int NPG = S::GQA * S::D / 2;  // pairs per kv head
   constexpr int WP = part_words<S>();
   constexpr int PPT = (S::QD / 2 + NT - 1) / NT;
@@ -1096,7 +1098,7 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
   for (int k = 0; k < PPT; ++k) M[k] = -INFINITY, L[k] = 0.f, o0[k] = 0.f, o1[k] = 0.f;
   for (int s0 = 0; s0 < nsplit && !failed; s0 += SB) {
     u64 wa[PPT][SB], wm[PPT][SB], wx = 0ull;
-    const bool want_x = s0 == 0 && xrows && tid < 16;
+    const bool want_x = s0 == 0 && ((tid < 16 && xrows) || (tid >= 16 && tid < 32 && xrows2));
     Spin sp;
     while (true) {
       // every load is issued before any is tested (one round trip per poll
@@ -1116,7 +1118,7 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
           }
         }
       }
-      wx = ll_get(xrows ? xrows + (tid & 15) : p.part);
+      wx = ll_get(want_x ? (tid < 16 ? xrows : xrows2) + (tid & 15) : p.part);
       bool ready = true;
 #pragma unroll
       for (int k = 0; k < PPT; ++k)

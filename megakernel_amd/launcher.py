@@ -19,11 +19,11 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def compile_shared_library(arch: str = "gfx950", verbose: bool = False) -> str:
     """Build megakernel_amd/megakernel.so (always recompiles every translation
-    unit, four in parallel)."""
+    unit, eight in parallel)."""
     lib = os.path.join(REPO, "megakernel_amd", "megakernel.so")
     if os.path.exists(lib):
         os.remove(lib)
-    cmd = ["make", "-C", REPO, "-B", "-j4", "lib", f"ARCH={arch}"]
+    cmd = ["make", "-C", REPO, "-B", "-j8", "lib", f"ARCH={arch}"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if verbose or r.returncode != 0:
         print(r.stdout[-4000:], r.stderr[-4000:])

@@ -223,3 +223,31 @@ def test_configs3_full_model_long_context(ctx):
     finally:
         eng.close()
         dw.free()
+
+
+@pytest.mark.parametrize("ctx", [0, 100, 600, 1024, 1500])
+def test_class_kernel_equals_spread_kernel(ctx):
+    """The class-specialised kernel (MK_KERNEL_AUTO at up to 4 splits per kv
+    head) and the spread kernel run the same arithmetic: per-layer residuals,
+    logits and tokens of the same steps are bitwise identical; and the class
+    kernel is the one AUTO picks for these launches."""
+    shape = BASELINE.with_(n_layers=3, vocab=8192)
+    eng, orc, dw = make_pair(shape, 71, ctx + 40)
+    try:
+        if ctx:
+            eng.fill_kv_synthetic(ctx, 9)
+        assert eng.decode_kernel_for(20) == _lib.KERNEL_CLASS
+        runs = []
+        for variant in (_lib.KERNEL_AUTO, _lib.KERNEL_SPREAD):
+            eng.set_decode_kernel(variant)
+            eng.set_pos(ctx)
+            _, layers, logits = eng.debug_forward(5)
+            gen = eng.decode_many(7, 20)
+            runs.append((layers, logits, gen))
+        assert np.array_equal(runs[0][0], runs[1][0]), "per-layer residuals differ"
+        assert np.array_equal(runs[0][1], runs[1][1]), "logits differ"
+        assert runs[0][2] == runs[1][2], "tokens differ"
+        _print(f"ctx {ctx}: class == spread, tokens {runs[0][2][:6]}")
+    finally:
+        eng.close()
+        dw.free()
