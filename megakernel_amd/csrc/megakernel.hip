@@ -219,21 +219,23 @@ static ShapeInfo shape_info() {
 constexpr int kMaxClsSplit = 4;
 
 // Role table of the class kernel (mk_cls.h) for `nsplit` attention splits
-// per kv head on G workgroups: attention items on workgroups [0, NKV*nsplit)
-// (item (g, s) on workgroup s*NKV + g: XCD g for 8 kv heads), then QKV +
-// gate/up pairs with kv head g's QKV blocks on XCD g % 8, then gate/up +
-// down, down + O, O (one or two blocks), single roles for whatever has no
-// partner.  False when the shape's blocks do not fit G workgroups this way.
+// per kv head on G workgroups: attention items (each with an O block) on
+// workgroups [0, NKV*nsplit) (item (g, s) on workgroup s*NKV + g: XCD g for 8
+// kv heads), then QKV + gate/up pairs with kv head g's QKV blocks on XCD
+// g % 8, then gate/up + down, down + O, O (one or two blocks), single roles
+// for whatever has no partner.  False when the shape's blocks do not fit G
+// workgroups this way.
 static bool build_roles(const ShapeInfo& s, int G, int nsplit, std::vector<int>& rows) {
   const int NA = s.NKV * nsplit, RBQ = s.QKV / 16, RBF = s.F / 16, RBH = s.H / 16;
   rows.assign((size_t)G * ROLE_INTS, -1);
   for (int w = 0; w < G; ++w) rows[(size_t)w * ROLE_INTS + RF_CLS] = CLS_IDLE;
   auto at = [&](int w, int f) -> int& { return rows[(size_t)w * ROLE_INTS + f]; };
   if (NA > G) return false;
-  int w = 0;
-  for (; w < NA; ++w) {
+  int w = 0, o = 0;
+  for (; w < NA; ++w) {  // attention items, each with an O block while they last
     at(w, RF_CLS) = CLS_ATT;
     at(w, RF_ATT) = w;
+    if (o < RBH) at(w, RF_O0) = o++;
   }
   // QKV blocks grouped by the XCD of their kv head
   std::vector<int> by_xcd[8];
@@ -264,7 +266,7 @@ static bool build_roles(const ShapeInfo& s, int G, int nsplit, std::vector<int>&
     at(w, RF_CLS) = CLS_Q;
     at(w, RF_Q) = take_q(w);
   }
-  int d = 0, o = 0;
+  int d = 0;
   for (int gi = nqg; gi < RBF; ++gi, ++w) {  // gate/up pairs: with a down block while they last
     if (w >= G) return false;
     at(w, RF_G) = gi;

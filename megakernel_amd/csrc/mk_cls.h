@@ -11,7 +11,7 @@
 //   streaming do not), so each workgroup issues the next weights of a role
 //   right after it has computed and published that role, and the next wait of
 //   the workgroup comes at least one phase later:
-//     ATT  attention only            K/V of the next layer after attention
+//     ATT  attention (P2) + O (P3)   next K/V and next O after O
 //     QG   QKV (P1) + gate/up (P4)   gate/up after QKV, next QKV after gate/up
 //     DG   gate/up (P4) + down (P5)  next gate/up and next down after down
 //     DO   O (P3) + down (P5)        next O and next down after down
@@ -89,7 +89,7 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
   NormIn<S> gfin;
   gains_load(gfin, p.final_norm);
   float rn;
-  if (!fetch_norm<S>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return false;
+  if (!fetch_norm<S, false>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return false;
   if constexpr (DBG) trace_mark(p, t, PHASES_PER_LAYER * p.n_layers, 0);
   const long long nb = p.vocab / 16;
   const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G;
@@ -345,9 +345,10 @@ __device__ __forceinline__ int next_layer(const Params& p, int layer) { return l
 template <class S, int MODE>
 __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int* role) {
   constexpr bool K8 = (MODE & 8) != 0;
-  const int a = role[RF_ATT];
+  const int a = role[RF_ATT], o0 = role[RF_O0];
   const int g = a % S::NKV, s = a / S::NKV;
   KV<S, K8> rkv;
+  Blk<S::KC_Q> ro;
   int tok = p.first_token;
   {
     const Item it = att_item_gs(g, s, p.pos0 + 1, p.chunk_min, p.nsplit_max);
@@ -355,12 +356,13 @@ __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int*
       kv_load<S>(rkv, p, 0, g, it.t0 / 32, (it.t1 - it.t0 + 31) / 32, wave_id());
       gain_load_qk<S>(rkv, p, 0);
     }
+    if (o0 >= 0) ld_o<S>(ro, p, 0, o0);
   }
   const unsigned per_token = (unsigned)(PHASES_PER_LAYER * p.n_layers + 1);
   for (int t = 0; t < p.n_tokens; ++t) {
     if constexpr ((MODE & 2) != 0) trace_begin(p, t);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
-    if (!cls_token_start<S, MODE>(p, sm, t, tb, false, true, &tok)) return;
+    if (!cls_token_start<S, MODE>(p, sm, t, tb, o0 >= 0, true, &tok)) return;
     const int pos = p.pos0 + t;
     const Item cur = att_item_gs(g, s, pos + 1, p.chunk_min, p.nsplit_max);
     const Item nxt = att_item_gs(g, s, pos + 2, p.chunk_min, p.nsplit_max);
@@ -370,12 +372,19 @@ __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int*
         if (!attention_compute<S, MODE>(p, sm, rkv, layer, pos, g, cur.s, cur.nsplit, cur.t0, cur.t1, tg, t)) return;
         if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 1, 1);
       }
-      if (cur.on && has_next(p, t, layer)) {
-        gain_load_qk<S>(rkv, p, layer + 1);
-        kv_load_paced<S>(rkv, p, layer + 1, g, cur.t0 / 32, (cur.t1 - cur.t0 + 31) / 32, pace_units(p, PACE_ATT));
+      // O right after attention (no load in between); the next layer's K/V
+      // and O block after it
+      if (o0 >= 0 && !cls_o<S, MODE>(p, sm, ro, ro, t, layer, o0, -1, cur.nsplit, tok, tg)) return;
+      if (has_next(p, t, layer)) {
+        if (o0 >= 0) ld_o<S>(ro, p, layer + 1, o0, pace_units(p, PACE_ATT));
+        if (cur.on) {
+          gain_load_qk<S>(rkv, p, layer + 1);
+          kv_load_paced<S>(rkv, p, layer + 1, g, cur.t0 / 32, (cur.t1 - cur.t0 + 31) / 32, pace_units(p, PACE_ATT));
+        }
       }
     }
     if (!cls_lm_head<S, MODE>(p, sm, t, tb, [&]() {
+          if (o0 >= 0) ld_o<S>(ro, p, 0, o0);
           if (nxt.on) {
             kv_load<S>(rkv, p, 0, g, nxt.t0 / 32, (nxt.t1 - nxt.t0 + 31) / 32, wave_id());
             gain_load_qk<S>(rkv, p, 0);

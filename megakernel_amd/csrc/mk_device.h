@@ -68,6 +68,47 @@ __device__ __forceinline__ float dot8(u32x4 w, const float* h, float acc) {
   return acc;
 }
 
+// Split-bf16 GEMV input vectors.  A layer GEMV's input x lives in LDS as two
+// bf16 parts, x = hi + lo with hi = RNE(x) and lo = RNE(x - hi) (x - hi is
+// exact; relative error of the pair <= 2^-17), so each weight pair costs one
+// v_dot2c_f32_bf16 per part: one VALU op per weight against two (convert +
+// fma) for fp32 inputs.  Layout: 8 columns per 32-byte group, the group's 4
+// dwords of hi pairs (columns 2i, 2i+1 in the low / high half) then its 4 of
+// lo pairs -- the same 4-byte slot count as an fp32 vector, so the readers'
+// offsets are the fp32 ones.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void xs_put(uint32_t* xs, int e, float v) {
+  uint16_t* h = reinterpret_cast<uint16_t*>(xs);
+  const int g = e >> 3, j = e & 7;
+  const uint16_t hv = f32_to_bf16(v);
+  h[(g * 8 + (j >> 1)) * 2 + (j & 1)] = hv;
+  h[(g * 8 + 4 + (j >> 1)) * 2 + (j & 1)] = f32_to_bf16(v - bf16_to_f32(hv));
+}
+// columns e, e + 1 (e even): one dword of each part
+__device__ __forceinline__ void xs_put_pair(uint32_t* xs, int e, float a, float b) {
+  const int g = e >> 3, i = (e & 7) >> 1;
+  const uint16_t ha = f32_to_bf16(a), hb = f32_to_bf16(b);
+  xs[g * 8 + i] = (uint32_t)ha | ((uint32_t)hb << 16);
+  xs[g * 8 + 4 + i] =
+      (uint32_t)f32_to_bf16(a - bf16_to_f32(ha)) | ((uint32_t)f32_to_bf16(b - bf16_to_f32(hb)) << 16);
+}
+// 8 bf16 weights (one 16-byte unit) against the split group xg (8 dwords).
+// The vectors are unpacked into scalars first: a bit_cast of an ext_vector
+// element (w[c]) compiles to element 0 for every c with this toolchain.
+__device__ __forceinline__ float dot8x(u32x4 w, const uint32_t* xg, float acc) {
+  const u32x4 h = *reinterpret_cast<const u32x4*>(xg);
+  const u32x4 l = *reinterpret_cast<const u32x4*>(xg + 4);
+  const uint32_t wa[4] = {w.x, w.y, w.z, w.w}, ha[4] = {h.x, h.y, h.z, h.w}, la[4] = {l.x, l.y, l.z, l.w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wa[c]), __builtin_bit_cast(bf16x2, ha[c]), acc,
+                                          false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wa[c]), __builtin_bit_cast(bf16x2, la[c]), acc,
+                                          false);
+  }
+  return acc;
+}
+
 // 16 FP8 (OCP e4m3) weights against 16 fp32 inputs: the hardware converts two
 // bytes per instruction (bytes 0-1 / 2-3 of each dword, in order).
 __device__ __forceinline__ float dot16_fp8(u32x4 w, const float* h, float acc) {

@@ -101,11 +101,12 @@ template <class S>
 struct Smem {
   // GEMV input vectors, one per phase type (a phase's GEMV ends without a
   // barrier, so the next phase must not overwrite the vector it reads)
+  // (the four layer GEMV inputs hold split-bf16 pairs, mk_device.h xs_put)
   float vec_q[S::H];                  // QKV: x * attn_norm gain
   float vec_o[S::QD];                 // O: attention output
   float vec_g[S::H];                  // gate/up: x * ffn_norm gain
   float vec_d[S::F];                  // down: SiLU(gate) * up
-  float vec_l[S::H];                  // LM head: x * final_norm gain
+  float vec_l[S::H];                  // LM head: x * final_norm gain (fp32)
   float xres_o[32], xres_d[16];       // residual rows of this workgroup's O block(s) / down block
   float ssw[3][NW];                   // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
   float rowbuf[4][16];                // a block's 16 results, stored by one wave
@@ -186,14 +187,15 @@ __device__ __forceinline__ void blk_forget(Blk<KC>& b) {
 __device__ __forceinline__ int blk_row() { return 2 * wave_id() + (int)(lane_id() >> 5); }
 __device__ __forceinline__ bool row_owner() { return (lane_id() & 31u) == 0u; }
 
-// Dot product of this lane's row with vec (LDS fp32): every lane of the half
-// wave gets the full sum (reduced inside the wave, no LDS exchange).
+// Dot product of this lane's row with vec (LDS, split-bf16 pairs, xs_put):
+// every lane of the half wave gets the full sum (reduced inside the wave, no
+// LDS exchange).
 template <int KC>
 __device__ __forceinline__ float blk_dot(const Blk<KC>& b, const float* vec) {
-  const float* hv = vec + 8 * (int)(lane_id() & 31u);
+  const uint32_t* hv = reinterpret_cast<const uint32_t*>(vec) + 8 * (int)(lane_id() & 31u);
   float acc = 0.f;
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc) acc = dot8(b.w[kc], hv + 256 * kc, acc);
+  for (int kc = 0; kc < KC; ++kc) acc = dot8x(b.w[kc], hv + 256 * kc, acc);
   return sum_xor16(group_sum<16>(acc));
 }
 
@@ -263,9 +265,10 @@ __device__ __forceinline__ bool norm_finish(float ss, float* ssw, int failed, fl
   return true;
 }
 
-// Wait for the tagged H-vector x (one bulk round), store x * gain to dst and
-// return the RMSNorm scale of x.
-template <class S>
+// Wait for the tagged H-vector x (one bulk round), store x * gain to dst
+// (split-bf16 pairs for a layer GEMV, fp32 for the LM head) and return the
+// RMSNorm scale of x.
+template <class S, bool SPLIT = true>
 __device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned tag, const NormIn<S>& n,
                                            float* dst, float* ssw, float* r) {
   constexpr int PER = NormIn<S>::PER;
@@ -298,7 +301,8 @@ __device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned t
     if (i < S::H) {
       const float v = ll_val(wv[k]);
       ss = fmaf(v, v, ss);
-      dst[i] = v * n.g[k];
+      if constexpr (SPLIT) xs_put(reinterpret_cast<uint32_t*>(dst), i, v * n.g[k]);
+      else dst[i] = v * n.g[k];
     }
   }
   return norm_finish(ss, ssw, failed, (float)S::H, r);
@@ -341,8 +345,7 @@ __device__ __forceinline__ bool fetch_pk(const Params& p, u64* src, unsigned t4,
   for (int k = 0; k < PER; ++k) {
     const int i = tid + k * NT;
     if (i < NPK) {
-      dst[2 * i] = pk_lo(wv[k]);
-      dst[2 * i + 1] = pk_hi(wv[k]);
+      xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * i, pk_lo(wv[k]), pk_hi(wv[k]));
     } else if (i < tot) {
       xres[i - NPK] = ll_val(wv[k]);
     }
@@ -362,7 +365,7 @@ __device__ __forceinline__ void embed_norm(const Params& p, int tok, const NormI
     if (i < S::H) {
       const float v = packed_elem<S::KT_H>(p.lmhead, tok, i);
       ss = fmaf(v, v, ss);
-      dst[i] = v * n.g[k];
+      xs_put(reinterpret_cast<uint32_t*>(dst), i, v * n.g[k]);
     }
   }
   (void)norm_finish(ss, ssw, 0, (float)S::H, r);
@@ -1155,10 +1158,7 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
     const int pi = tid + k * NT;
-    if (pi < S::QD / 2) {
-      dst[2 * pi] = o0[k] / L[k];
-      dst[2 * pi + 1] = o1[k] / L[k];
-    }
+    if (pi < S::QD / 2) xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * pi, o0[k] / L[k], o1[k] / L[k]);
   }
   return !block_failed(failed);
 }
@@ -1442,7 +1442,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       NormIn<S> gfin;
       gains_load(gfin, p.final_norm);
       float rn;
-      if (!fetch_norm<S>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return;
+      if (!fetch_norm<S, false>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return;
       if constexpr (DBG) trace_mark(p, t, PHASES_PER_LAYER * L, 0);
       const long long nb = p.vocab / 16;
       const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G;

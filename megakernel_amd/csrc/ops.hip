@@ -34,7 +34,8 @@ enum GemvKind : int { GEMV_PLAIN = 0, GEMV_RESIDUAL = 1, GEMV_GATE_UP = 2 };
 // Work item = (instance r, 16-row block b), items r-major and dealt to
 // workgroups round-robin, so the workgroups in flight stream neighbouring
 // blocks of one weight copy.  The input vector of the item's instance is
-// staged in LDS (fp32) and only reloaded when the instance's input changes.
+// staged in LDS (split-bf16 pairs, as the decode kernel's GEMVs read it) and
+// only reloaded when the instance's input changes.
 // Loads are issued vector first (L2-resident pool), weights second, so the
 // vector's wait does not wait for the weight block (loads return in order).
 template <int KC, int KIND>
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(const u32x4* __restrict__ w, l
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
         const int i = (int)threadIdx.x + k * NT;
-        if (i < K) vec[i] = xv[k];
+        if (i < K) xs_put(reinterpret_cast<uint32_t*>(vec), i, xv[k]);
       }
       __syncthreads();
       have = in;
