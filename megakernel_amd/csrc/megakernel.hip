@@ -415,7 +415,7 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   // tagged activation words (zero = tag 0, never a valid tag)
   u64** tagged[5] = {&h->x, &h->qkv, &h->part, &h->act, &h->amax};
   // part: the splits' partials, then one row for a long context's merged partial
-  const size_t words[5] = {(size_t)s.H, (size_t)s.QKV,
+  const size_t words[5] = {(size_t)s.H / 2, (size_t)s.QKV,
                            (size_t)(h->nsplit_max + 1) * s.NKV * s.part_words, (size_t)s.F / 2,
                            (size_t)2 * h->G};
   for (int i = 0; i < 5; ++i) {
@@ -464,13 +464,13 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
     HIPCHK(hipMemcpyAsync(nl + s.norm_k, base + o[5], (size_t)s.D * 2, hipMemcpyDeviceToDevice, h->stream), -1);
     HIPCHK(hipMemcpyAsync(nl + s.norm_ffn, base + o[7], (size_t)s.H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
     u32x4* qkv = wl + s.off_qkv;
-    if (repack(h, base, o[1], s.QD, s.H, qkv, 1, 0)) return -1;
-    if (repack(h, base, o[2], s.KVD, s.H, qkv, 1, s.QD / 16)) return -1;
-    if (repack(h, base, o[3], s.KVD, s.H, qkv, 1, (s.QD + s.KVD) / 16)) return -1;
-    if (repack(h, base, o[6], s.H, s.QD, wl + s.off_o, 1, 0)) return -1;
-    if (repack(h, base, o[8], s.F, s.H, wl + s.off_gu, 2, 0)) return -1;
-    if (repack(h, base, o[9], s.F, s.H, wl + s.off_gu, 2, 1)) return -1;
-    if (repack(h, base, o[10], s.H, s.F, wl + s.off_down, 1, 0)) return -1;
+    if (repack(h, base, o[1], s.QD, s.H, qkv, 1, 0, 0)) return -1;
+    if (repack(h, base, o[2], s.KVD, s.H, qkv, 1, s.QD / 16, 0)) return -1;
+    if (repack(h, base, o[3], s.KVD, s.H, qkv, 1, (s.QD + s.KVD) / 16, 0)) return -1;
+    if (repack(h, base, o[6], s.H, s.QD, wl + s.off_o, 1, 0, 0)) return -1;
+    if (repack(h, base, o[8], s.F, s.H, wl + s.off_gu, 2, 0, 0)) return -1;
+    if (repack(h, base, o[9], s.F, s.H, wl + s.off_gu, 2, 1, 0)) return -1;
+    if (repack(h, base, o[10], s.H, s.F, wl + s.off_down, 1, 0, 0)) return -1;
   }
   (void)KTH;
   HIPCHK(hipStreamSynchronize(h->stream), -1);
@@ -536,13 +536,18 @@ static int clear_tagged_state(Handle* h) {
   return 0;
 }
 
-// The packed-pair words (part, act) carry 4-bit tags, so a stale word can look
-// current when its tag is a multiple of 15 phases old.  While the position
-// only grows and the split configuration is fixed, that never happens: every
-// act word and every active split slot is rewritten at each layer (5 phases
-// apart, 6 across a token boundary), and split counts never shrink, so a slot
-// that becomes active still holds zeros.  A position that moves backwards, a
-// new cache, or a new split / merge configuration breaks that, and clears them.
+// The packed-pair words (x, part, act) carry 4-bit tags, so a stale word can
+// look current when its tag is a multiple of 15 phases old.  While the
+// position only grows and the split configuration is fixed, that never
+// happens: every act word and every active split slot is rewritten at each
+// layer (5 phases apart, 6 across a token boundary), and split counts never
+// shrink, so a slot that becomes active still holds zeros.  A position that
+// moves backwards, a new cache, or a new split / merge configuration breaks
+// that, and clears them.  x needs no such clear: its words are rewritten twice
+// a layer (after O and after down, 2 and 3 phases apart; the tag sequence
+// runs on across launches), and every reader of x depends on a phase that
+// consumed the whole previous-layer x, so it waits for a write 2 to 6 phases
+// after the word's current one -- never a multiple of 15.
 static int clear_pair_words(Handle* h) {
   HIPCHK(hipMemsetAsync(h->part, 0, h->tagged_bytes[2], h->stream), -1);
   HIPCHK(hipMemsetAsync(h->act, 0, h->tagged_bytes[3], h->stream), -1);

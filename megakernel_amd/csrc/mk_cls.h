@@ -81,7 +81,8 @@ __device__ __forceinline__ bool cls_token_start(const Params& p, Smem<S>& sm, in
 // LM head's wait it would delay that wait, issued before the scoring it would
 // delay this workgroup's share of the LM-head stream.
 template <class S, int MODE, class AfterPoll>
-__device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t, unsigned tb, AfterPoll after_poll) {
+__device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t, unsigned tb, AfterPoll after_poll,
+                                            bool idle = false) {
   constexpr bool DBG = (MODE & 2) != 0, F8 = (MODE & 4) != 0;
   const int G = gridDim.x, wg = blockIdx.x;
   const int tid = ltid(), w = tid / kWave, l = tid % kWave;
@@ -89,6 +90,7 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
   NormIn<S> gfin;
   gains_load(gfin, p.final_norm);
   float rn;
+  if (idle && !wait_last_qkv(p, tl)) return false;  // no role in the last layer
   if (!fetch_norm<S, false>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return false;
   if constexpr (DBG) trace_mark(p, t, PHASES_PER_LAYER * p.n_layers, 0);
   const long long nb = p.vocab / 16;
@@ -166,8 +168,8 @@ __device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const Blk<
     embed_norm<S>(p, tok, gq, sm.vec_q, sm.ssw[0], &r);
   }
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 0);
-  const float y = blk_dot(rq, sm.vec_q);
-  store_rows(sm.rowbuf[0], p.qkv + q * 16, y * r, tg);
+  blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
+  store_block(sm.red[RED_Q], p.qkv + q * 16, r, nullptr, tg);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 1);
   return true;
 }
@@ -179,9 +181,9 @@ __device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const Blk<S
   float r;
   if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 0);
-  const float yg = blk_dot(rg, sm.vec_g);
-  const float yu = blk_dot(ru, sm.vec_g);
-  store_rows_pk(sm.rowbuf[2], p.act + g * 8, silu_mul(yg * r, yu * r), tag4(tg + 3u));
+  blk_mma(rg, sm.vec_g, sm.red[RED_G]);
+  blk_mma(ru, sm.vec_g, sm.red[RED_U]);
+  store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, r, tag4(tg + 3u));
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 1);
   return true;
 }
@@ -191,13 +193,12 @@ __device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const Blk<S
 template <class S, int MODE>
 __device__ __forceinline__ bool cls_down(const Params& p, Smem<S>& sm, const Blk<S::KC_F>& rd, int t, int layer, int d,
                                          unsigned tg) {
-  if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x + d * 16, tg + 2u, sm.vec_d, sm.xres_d)) return false;
+  if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x, d, tag4(tg + 2u), sm.vec_d, sm.xres_d)) return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 0);
-  const float y = blk_dot(rd, sm.vec_d);
-  const int row = d * 16 + blk_row();
-  const float xn = sm.xres_d[blk_row()] + y;
-  if ((MODE & 2) != 0 && p.dbg_layers && row_owner()) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
-  store_rows(sm.rowbuf[3], p.x + d * 16, xn, tg + 4u);
+  blk_mma(rd, sm.vec_d, sm.red[RED_D]);
+  __syncthreads();
+  const int t_ = ltid();
+  if (t_ < 8) down_rows<S>(p, sm, d, t_, (MODE & 2) != 0 ? p.dbg_layers : nullptr, layer, tg + 4u);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 1);
   return true;
 }
@@ -209,21 +210,26 @@ template <class S, int MODE>
 __device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const Blk<S::KC_Q>& ro0, const Blk<S::KC_Q>& ro1,
                                       int t, int layer, int o0, int o1, int nsplit, int tok, unsigned tg) {
   const unsigned tg_x = tg - 1u;
-  if (!fetch_attn<S>(p, p.part, nsplit, tag4(tg + 1u), layer > 0 ? p.x + o0 * 16 : nullptr, tg_x, sm.vec_o,
-                     sm.xres_o, layer > 0 && o1 >= 0 ? p.x + o1 * 16 : nullptr))
+  if (!fetch_attn<S>(p, p.part, nsplit, tag4(tg + 1u), p.x, layer > 0 ? o0 : -1, o1, tag4(tg_x), sm.vec_o,
+                     sm.xres_o))
     return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 0);
-  {
-    const float y = blk_dot(ro0, sm.vec_o);
-    const int row = o0 * 16 + blk_row();
-    const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres_o[blk_row()];
-    store_rows(sm.rowbuf[1], p.x + o0 * 16, xo + y, tg + 2u);
-  }
-  if (o1 >= 0) {
-    const float y = blk_dot(ro1, sm.vec_o);
-    const int row = o1 * 16 + blk_row();
-    const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres_o[16 + blk_row()];
-    store_rows(sm.rowbuf[0], p.x + o1 * 16, xo + y, tg + 2u);
+  blk_mma(ro0, sm.vec_o, sm.red[RED_O0]);
+  if (o1 >= 0) blk_mma(ro1, sm.vec_o, sm.red[RED_O1]);
+  __syncthreads();
+  // threads 0..7: rows 2i, 2i + 1 of block o0, 8..15: of block o1 (one store instruction)
+  const int t_ = ltid(), i = t_ & 7;
+  if (t_ < 8 || (t_ < 16 && o1 >= 0)) {
+    const int ob = t_ < 8 ? o0 : o1, xr = t_ < 8 ? 0 : 16;
+    const float* red = sm.red[t_ < 8 ? RED_O0 : RED_O1];
+    float v[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = 2 * i + e;
+      const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, ob * 16 + r) : sm.xres_o[xr + r];
+      v[e] = xo + red_sum(red, r);
+    }
+    put_x2(p, ob, i, v[0], v[1], tg + 2u);
   }
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 1);
   return true;
@@ -518,7 +524,7 @@ __device__ __forceinline__ void run_idle(const Params& p, Smem<S>& sm) {
     if constexpr ((MODE & 2) != 0) trace_begin(p, t);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
     if (!cls_token_start<S, MODE>(p, sm, t, tb, false, false, &tok)) return;
-    if (!cls_lm_head<S, MODE>(p, sm, t, tb, []() {})) return;
+    if (!cls_lm_head<S, MODE>(p, sm, t, tb, []() {}, true)) return;
     if constexpr ((MODE & 2) != 0) trace_end(p, t);
   }
 }

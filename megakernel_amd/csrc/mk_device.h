@@ -384,9 +384,12 @@ __device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigne
 
 // Packed pair: two values in one tagged word, each rounded to a 19-bit
 // mantissa (relative error <= 2^-20) with a 4-bit tag in its low bits, so a
-// large vector needs half the words.  The 4-bit tag (1..15, never 0) only has
-// to differ from the tag of the previous write to the same word; the buffer
-// is cleared (tag 0) before every launch.
+// large vector needs half the words.  The 4-bit tag (1..15, never 0) is the
+// full tag mod 15 + 1: a reader can only mistake a stale word for current if
+// the word's last write is a multiple of 15 phases older than the awaited
+// one.  The protocol keeps that gap between 1 and 14 phases (every word is
+// rewritten at least once a layer, 5 phases, 6 across a token boundary); the
+// host clears the words (tag 0) wherever a reconfiguration could break it.
 __device__ __forceinline__ unsigned tag4(unsigned tag) { return tag % 15u + 1u; }
 __device__ __forceinline__ unsigned pk_half(float v, unsigned t4) {
   return ((__float_as_uint(v) + 8u) & ~15u) | t4;
@@ -399,6 +402,21 @@ __device__ __forceinline__ bool pk_ready(u64 w, unsigned t4) {
 }
 __device__ __forceinline__ float pk_lo(u64 w) { return __uint_as_float((unsigned)w & ~15u); }
 __device__ __forceinline__ float pk_hi(u64 w) { return __uint_as_float((unsigned)(w >> 32) & ~15u); }
+
+// Two adjacent packed-pair words (16-byte aligned, byte offset off in the
+// buffer rs) in one 16-byte load with agent scope (sc1, as ll_get): a poll
+// round needs half the load instructions of 8-byte loads.  Every 32-bit half
+// carries its own tag, so a half that predates its word's last write never
+// passes for current, however the load is split.  Poll loops put an asm
+// memory clobber at the top of each round so the load is re-issued.
+__device__ __forceinline__ u32x4 pk_get2(__amdgpu_buffer_rsrc_t rs, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0u, 16);
+}
+// Value of one 32-bit half, and whether all four halves carry tag t4.
+__device__ __forceinline__ float pkv(unsigned h) { return __uint_as_float(h & ~15u); }
+__device__ __forceinline__ bool pk2_ready(u32x4 q, unsigned t4) {
+  return (q.x & 15u) == t4 && (q.y & 15u) == t4 && (q.z & 15u) == t4 && (q.w & 15u) == t4;
+}
 
 // Bounded spinning of one thread.  step() returns false when the wait must be
 // abandoned (this thread timed out, or another workgroup already failed).

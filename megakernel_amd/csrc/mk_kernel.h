@@ -71,7 +71,7 @@ struct Params {
                               //   at byte index = element index of kv / kvt
   uint16_t* kv;               // K cache [L][NKV][s_pad][D] bf16
   uint16_t* kvt;              // V cache, transposed blocks [L][NKV][s_pad/32][D][32] bf16
-  u64* x;                     // [H] residual stream (tagged)
+  u64* x;                     // [H/2] residual stream (packed pairs: rows 2i, 2i + 1 in word i)
   u64* qkv;                   // [QKV] projections of the current layer (tagged)
   u64* part;                  // [nsplit_max + 1][NKV][part_words] attention partials (packed
                               //   pairs): unnormalised output, then (max, sum) per q head; the
@@ -97,6 +97,11 @@ struct Params {
   int pace_pct;               // class kernel: prefetch pacing, percent of the default spacing (0: bursts)
 };
 
+// Wave-share buffers of the block products, one per block a phase computes
+// (a phase's product ends without a barrier after its reads, so the next
+// phase's product must not overwrite the shares being summed).
+enum RedBuf : int { RED_Q = 0, RED_O0, RED_O1, RED_G, RED_U, RED_D, RED_N };
+
 template <class S>
 struct Smem {
   // GEMV input vectors, one per phase type (a phase's GEMV ends without a
@@ -109,7 +114,7 @@ struct Smem {
   float vec_l[S::H];                  // LM head: x * final_norm gain (fp32)
   float xres_o[32], xres_d[16];       // residual rows of this workgroup's O block(s) / down block
   float ssw[3][NW];                   // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
-  float rowbuf[4][16];                // a block's 16 results, stored by one wave
+  float red[RED_N][NW * 16];          // block products: each wave's share of the 16 row sums (blk_mma)
   __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score A operand
   __attribute__((aligned(16))) uint16_t pb[NW][16][32 * KVB];  // attention: weight parts, output A operand
   u32x4 kvcur[2][S::D / 8];           // bf16 (FP8 cache: e4m3 codes) K/V of the current position
@@ -182,6 +187,75 @@ __device__ __forceinline__ void blk_forget(Blk<KC>& b) {
   for (int kc = 0; kc < KC; ++kc) b.w[kc] = __builtin_nondeterministic_value(b.w[kc]);
 }
 
+// Block product on the matrix cores (tile-layout blocks, mk_config.h: wave w
+// holds tiles w KC .. w KC + KC - 1, i.e. columns 32 w KC .. 32 (w + 1) KC - 1
+// of all 16 rows, lane l row l & 15 and columns 32 kt + 8 (l >> 4) .. +7 --
+// the A operand of v_mfma_f32_16x16x32_bf16).  The B operand's column 0 holds
+// the hi parts and column 1 the lo parts of the input (split-bf16 staging in
+// LDS, xs_put); the other 14 columns are never loaded: a D column depends only
+// on its own B column, and only columns 0 and 1 are read.  Lanes 0, 16, 32,
+// 48 then hold rows 4 (l >> 4) .. +3 of both columns (lanes l and l + 1), and
+// write their hi + lo sums -- the wave's share of the 16 row sums -- to
+// red[wave][16].  No barrier: red_sum after one reads them.
+template <int KC>
+__device__ __forceinline__ void blk_mma(const Blk<KC>& b, const float* vec, float* red) {
+  const unsigned l = lane_id();
+  const int w = wave_id();
+  const uint32_t* xs = reinterpret_cast<const uint32_t*>(vec) + (w * KC * 4 + (int)(l >> 4)) * 8 + (int)(l & 1u) * 4;
+  u32x4 bx[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) asm volatile("" : "=v"(bx[kc]));  // left as is in columns 2..15
+  if ((l & 14u) == 0u) {  // B columns 0 and 1
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) bx[kc] = *reinterpret_cast<const u32x4*>(xs + kc * 32);
+  }
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b.w[kc]), __builtin_bit_cast(bf16x8, bx[kc]),
+                                                  acc, 0, 0, 0);
+  f32x4 s;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = acc[i] + dpp_sel<DPP_XOR1>(acc[i]);  // column 0 + column 1
+  if ((l & 15u) == 0u) *reinterpret_cast<f32x4*>(red + w * 16 + 4 * (int)(l >> 4)) = s;
+}
+
+// Row t of a block from the NW wave shares in red (after a barrier that
+// follows blk_mma), summed in wave order.
+__device__ __forceinline__ float red_sum(const float* red, int t) {
+  float y = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) y += red[w * 16 + t];
+  return y;
+}
+
+// The 16 rows of a block (red, from blk_mma) times `scale`, plus res[t] unless
+// res is null, published by threads 0..15 as one 128-byte store.  One barrier.
+__device__ __forceinline__ void store_block(const float* red, u64* dst16, float scale, const float* res,
+                                            unsigned tag) {
+  __syncthreads();
+  const int t_ = ltid();
+  if (t_ < 16) {
+    const float y = red_sum(red, t_) * scale;
+    ll_put(dst16 + t_, ll_pack(res ? res[t_] + y : y, tag));
+  }
+}
+
+// SiLU(g) * u (reference utils.cuh:47-61).
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+
+// Gate/up pair: SiLU(g r) * (u r) of the 16 rows (gate shares in rg, up
+// shares in ru), published as 8 packed-pair words.  One barrier.
+__device__ __forceinline__ void store_block_gu(const float* rg, const float* ru, u64* dst8, float r, unsigned t4) {
+  __syncthreads();
+  const int t_ = ltid();
+  if (t_ < 8) {
+    const float a = silu_mul(red_sum(rg, 2 * t_) * r, red_sum(ru, 2 * t_) * r);
+    const float b = silu_mul(red_sum(rg, 2 * t_ + 1) * r, red_sum(ru, 2 * t_ + 1) * r);
+    ll_put(dst8 + t_, pk_pack(a, b, t4));
+  }
+}
+
 // Row of the block this lane's dot product belongs to, and the lane that
 // stores it (lanes 0 and 32).
 __device__ __forceinline__ int blk_row() { return 2 * wave_id() + (int)(lane_id() >> 5); }
@@ -226,27 +300,33 @@ __device__ __forceinline__ float packed_elem(const u32x4* base, int row, int col
 
 // RMSNorm (reference rmsnorm.cuh:87-108) is folded into the GEMVs that consume
 // it: the input vector is stored as x * gain, and the row results are scaled
-// by r = rsqrt(mean(x^2) + eps).  Each thread owns elements tid + k*NT.
+// by r = rsqrt(mean(x^2) + eps).  Each thread owns the element quads
+// 4q .. 4q + 3, q = tid + k*NT (one 16-byte load of two packed x words).
 template <class S>
 struct NormIn {
-  static constexpr int PER = (S::H + NT - 1) / NT;
-  float g[PER];
+  static constexpr int NQ = S::H / 4;              // element quads of x
+  static constexpr int PQ = (NQ + NT - 1) / NT;    // quads per thread
+  float g[4 * PQ];
 };
 
 template <class S>
 __device__ __forceinline__ void gains_forget(NormIn<S>& n) {
 #pragma unroll
-  for (int k = 0; k < NormIn<S>::PER; ++k) n.g[k] = __builtin_nondeterministic_value(n.g[k]);
+  for (int k = 0; k < 4 * NormIn<S>::PQ; ++k) n.g[k] = __builtin_nondeterministic_value(n.g[k]);
 }
 
 // The gains of this thread's elements, loaded before the phase's wait.
 template <class S>
 __device__ __forceinline__ void gains_load(NormIn<S>& n, const uint16_t* gain) {
+  constexpr int NQ = NormIn<S>::NQ;
   const int t_ = ltid();
+  const uint32_t* g2 = reinterpret_cast<const uint32_t*>(gain);
 #pragma unroll
-  for (int k = 0; k < NormIn<S>::PER; ++k) {  // unconditional loads: no wait until the gains are used
-    const int i = t_ + k * NT;
-    n.g[k] = bf16_to_f32(gain[i < S::H ? i : S::H - 1]);
+  for (int k = 0; k < NormIn<S>::PQ; ++k) {  // unconditional loads: no wait until the gains are used
+    const int q = t_ + k * NT < NQ ? t_ + k * NT : NQ - 1;
+    const uint32_t a = g2[2 * q], b = g2[2 * q + 1];
+    n.g[4 * k] = bf16_to_f32((uint16_t)a), n.g[4 * k + 1] = bf16_to_f32((uint16_t)(a >> 16));
+    n.g[4 * k + 2] = bf16_to_f32((uint16_t)b), n.g[4 * k + 3] = bf16_to_f32((uint16_t)(b >> 16));
   }
 }
 
@@ -265,29 +345,44 @@ __device__ __forceinline__ bool norm_finish(float ss, float* ssw, int failed, fl
   return true;
 }
 
-// Wait for the tagged H-vector x (one bulk round), store x * gain to dst
-// (split-bf16 pairs for a layer GEMV, fp32 for the LM head) and return the
-// RMSNorm scale of x.
+// Four values v (elements 4q .. 4q + 3) times their gains into the GEMV input
+// dst: split-bf16 pairs for a layer GEMV, fp32 for the LM head.
+template <bool SPLIT>
+__device__ __forceinline__ void put_quad(float* dst, int q, const float (&v)[4], const float* g) {
+  if constexpr (SPLIT) {
+    xs_put_pair(reinterpret_cast<uint32_t*>(dst), 4 * q, v[0] * g[0], v[1] * g[1]);
+    xs_put_pair(reinterpret_cast<uint32_t*>(dst), 4 * q + 2, v[2] * g[2], v[3] * g[3]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[4 * q + e] = v[e] * g[e];
+  }
+}
+
+// Wait for the packed-pair H-vector x of tag `tag` (one bulk round of 16-byte
+// loads), store x * gain to dst and return the RMSNorm scale of x.
 template <class S, bool SPLIT = true>
-__device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned tag, const NormIn<S>& n,
+__device__ __forceinline__ bool fetch_norm(const Params& p, const u64* src, unsigned tag, const NormIn<S>& n,
                                            float* dst, float* ssw, float* r) {
-  constexpr int PER = NormIn<S>::PER;
+  constexpr int PQ = NormIn<S>::PQ, NQ = NormIn<S>::NQ;
   const int tid = ltid();
+  const unsigned t4 = tag4(tag);
+  const auto rs = make_rsrc(src);
   int failed = 0;
   __syncthreads();  // every wave is done with the LDS of its previous phase
-  u64 wv[PER];
+  u32x4 wv[PQ];
   Spin sp;
   while (true) {
+    asm volatile("" ::: "memory");
     // every load is issued before any is tested (one round trip per poll
-    // round, not one per word); indices past the vector re-read its last word
+    // round); quads past the vector re-read its last quad
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int i = tid + k * NT;
-      wv[k] = ll_get(src + (i < S::H ? i : S::H - 1));
+    for (int k = 0; k < PQ; ++k) {
+      const int q = tid + k * NT;
+      wv[k] = pk_get2(rs, (unsigned)(q < NQ ? q : NQ - 1) * 16u);
     }
     bool ready = true;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) ready &= tid + k * NT >= S::H || ll_tag(wv[k]) == tag;
+    for (int k = 0; k < PQ; ++k) ready &= tid + k * NT >= NQ || pk2_ready(wv[k], t4);
     if (ready) break;
     if (!sp.step(p.err, p.timeout_ticks)) {
       failed = 1;
@@ -296,45 +391,42 @@ __device__ __forceinline__ bool fetch_norm(const Params& p, u64* src, unsigned t
   }
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = tid + k * NT;
-    if (i < S::H) {
-      const float v = ll_val(wv[k]);
-      ss = fmaf(v, v, ss);
-      if constexpr (SPLIT) xs_put(reinterpret_cast<uint32_t*>(dst), i, v * n.g[k]);
-      else dst[i] = v * n.g[k];
+  for (int k = 0; k < PQ; ++k) {
+    const int q = tid + k * NT;
+    if (q < NQ) {
+      const float v[4] = {pkv(wv[k].x), pkv(wv[k].y), pkv(wv[k].z), pkv(wv[k].w)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
+      put_quad<SPLIT>(dst, q, v, n.g + 4 * k);
     }
   }
   return norm_finish(ss, ssw, failed, (float)S::H, r);
 }
 
 // Wait for a packed-pair vector of 2*NPK values (NPK words, 4-bit tag t4) and,
-// unless xrows is null, the 16 tagged residual rows of this workgroup's block,
-// in one bulk round.
+// unless xblk < 0, the 16 residual rows of block xblk of x (8 packed words,
+// tag xt4, threads 0..7), in one bulk round of 8-byte loads (hot lines that
+// many workgroups poll: 16-byte loads made these rounds slower, not faster).
 template <int NPK>
-__device__ __forceinline__ bool fetch_pk(const Params& p, u64* src, unsigned t4, u64* xrows, unsigned xtag,
-                                         float* dst, float* xres) {
-  constexpr int TOT = NPK + 16, PER = (TOT + NT - 1) / NT;
+__device__ __forceinline__ bool fetch_pk(const Params& p, const u64* src, unsigned t4, const u64* x, int xblk,
+                                          unsigned xt4, float* dst, float* xres) {
+  constexpr int PER = (NPK + NT - 1) / NT;
   const int tid = ltid();
-  const int tot = xrows ? TOT : NPK;
+  const bool want_x = xblk >= 0 && tid < 8;
   int failed = 0;
-  __syncthreads();  // every wave is done with the LDS of its previous phase
-  u64 wv[PER];
+  __syncthreads();
+  u64 wv[PER], wx = 0ull;
   Spin sp;
   while (true) {
-    // every load is issued before any is tested (one round trip per poll
-    // round); indices past the inputs re-read word 0 of the vector
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const int i = tid + k * NT;
-      wv[k] = ll_get(i < NPK ? src + i : (i < tot ? xrows + (i - NPK) : src));
+      wv[k] = ll_get(const_cast<u64*>(src) + (i < NPK ? i : NPK - 1));
     }
-    bool ready = true;
+    if (want_x) wx = ll_get(const_cast<u64*>(x) + xblk * 8 + tid);
+    bool ready = !want_x || pk_ready(wx, xt4);
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int i = tid + k * NT;
-      ready &= i < NPK ? pk_ready(wv[k], t4) : (i >= tot || ll_tag(wv[k]) == xtag);
-    }
+    for (int k = 0; k < PER; ++k) ready &= tid + k * NT >= NPK || pk_ready(wv[k], t4);
     if (ready) break;
     if (!sp.step(p.err, p.timeout_ticks)) {
       failed = 1;
@@ -344,11 +436,32 @@ __device__ __forceinline__ bool fetch_pk(const Params& p, u64* src, unsigned t4,
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int i = tid + k * NT;
-    if (i < NPK) {
-      xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * i, pk_lo(wv[k]), pk_hi(wv[k]));
-    } else if (i < tot) {
-      xres[i - NPK] = ll_val(wv[k]);
+    if (i < NPK) xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * i, pk_lo(wv[k]), pk_hi(wv[k]));
+  }
+  if (want_x) xres[2 * tid] = pk_lo(wx), xres[2 * tid + 1] = pk_hi(wx);
+  return !block_failed(failed);
+}
+
+// Wait for the 16 rows of block blk of x (8 packed words, tag t4) into xres.
+__device__ __forceinline__ bool fetch_xrows(const Params& p, const u64* x, int blk, unsigned t4, float* xres) {
+  const int tid = ltid();
+  const auto rx = make_rsrc(x);
+  int failed = 0;
+  __syncthreads();  // every wave is done with the LDS of its previous phase
+  if (tid < 4) {
+    Spin sp;
+    u32x4 w;
+    while (true) {
+      asm volatile("" ::: "memory");
+      w = pk_get2(rx, (unsigned)(blk * 8 + 2 * tid) * 8u);
+      if (pk2_ready(w, t4)) break;
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
     }
+    xres[4 * tid] = pkv(w.x), xres[4 * tid + 1] = pkv(w.y);
+    xres[4 * tid + 2] = pkv(w.z), xres[4 * tid + 3] = pkv(w.w);
   }
   return !block_failed(failed);
 }
@@ -357,21 +470,79 @@ __device__ __forceinline__ bool fetch_pk(const Params& p, u64* src, unsigned t4,
 template <class S>
 __device__ __forceinline__ void embed_norm(const Params& p, int tok, const NormIn<S>& n, float* dst, float* ssw,
                                            float* r) {
+  constexpr int NQ = NormIn<S>::NQ;
   const int tid = ltid();
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < NormIn<S>::PER; ++k) {
-    const int i = tid + k * NT;
-    if (i < S::H) {
-      const float v = packed_elem<S::KT_H>(p.lmhead, tok, i);
-      ss = fmaf(v, v, ss);
-      xs_put(reinterpret_cast<uint32_t*>(dst), i, v * n.g[k]);
+  for (int k = 0; k < NormIn<S>::PQ; ++k) {
+    const int q = tid + k * NT;
+    if (q < NQ) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = packed_elem<S::KT_H>(p.lmhead, tok, 4 * q + e);
+        ss = fmaf(v[e], v[e], ss);
+      }
+      put_quad<true>(dst, q, v, n.g + 4 * k);
     }
   }
   (void)norm_finish(ss, ssw, 0, (float)S::H, r);
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+// A workgroup with no role in the token's last layer reaches the LM head
+// without having consumed x since the previous token, so a packed x word a
+// multiple of 15 phases older than the awaited one could pass the 4-bit tag
+// check.  Such a workgroup first waits for the last layer's QKV output (one
+// word, full 32-bit tag, tag tl - 5): that phase read the whole x at the
+// previous layer's down tag, so every x word is then at most 5 phases older
+// than the LM head's.
+__device__ __forceinline__ bool wait_last_qkv(const Params& p, unsigned tl) {
+  int failed = 0;
+  if (ltid() == 0) {
+    Spin sp;
+    while (ll_tag(ll_get(p.qkv)) != tl - (unsigned)PHASES_PER_LAYER)
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+  }
+  return !block_failed(failed);
+}
+
+// The x words of rows 2i, 2i + 1 of block blk (values a, b), tag of the phase.
+__device__ __forceinline__ void put_x2(const Params& p, int blk, int i, float a, float b, unsigned tag) {
+  ll_put(p.x + blk * 8 + i, pk_pack(a, b, tag4(tag)));
+}
+
+// O block blk (shares in red[RED_O0], residual rows in xres_o, or the
+// embedding row at layer 0) -> x rows 2i, 2i + 1 (thread i < 8).
+template <class S>
+__device__ __forceinline__ void o_rows(const Params& p, Smem<S>& sm, int blk, int i, int layer, int tok,
+                                       unsigned tag) {
+  float v[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int r = 2 * i + e;
+    const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, blk * 16 + r) : sm.xres_o[r];
+    v[e] = xo + red_sum(sm.red[RED_O0], r);
+  }
+  put_x2(p, blk, i, v[0], v[1], tag);
+}
+
+// Down block blk (shares in red[RED_D]) + residual rows xres_d -> x rows 2i,
+// 2i + 1 (thread i < 8); dbg (layer dumps) unless null.
+template <class S>
+__device__ __forceinline__ void down_rows(const Params& p, Smem<S>& sm, int blk, int i, float* dbg, int layer,
+                                          unsigned tag) {
+  float v[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int r = 2 * i + e;
+    v[e] = sm.xres_d[r] + red_sum(sm.red[RED_D], r);
+    if (dbg) dbg[(long long)(layer + 1) * S::H + blk * 16 + r] = v[e];
+  }
+  put_x2(p, blk, i, v[0], v[1], tag);
+}
 
 // Work item i of a phase runs on workgroup (i + off) mod G.
 __device__ __forceinline__ int first_item(int wg, int off, int G) { return (wg + G - (off % G)) % G; }
@@ -417,109 +588,6 @@ __device__ __forceinline__ void trace_end(const Params& p, int t) {
   __syncthreads();
   const int n = (5 * p.n_layers + 1) * 2 + EVT_N;
   for (int i = ltid(); i < n; i += NT) p.trace[(long long)i * gridDim.x + blockIdx.x] = trace_lds[i];
-}
-
-// --------------------------------------------------------- tagged fetches
-// Wait until every word of up to three ranges carries its range's tag and copy
-// the values to LDS.  Inputs of at most B words a thread are polled in bulk:
-// every thread re-reads its words until all carry the tag (one load round trip
-// after the last producer's store lands).  Larger inputs first let wave 0 poll
-// one sentinel word per producer block (every `ss`-th word of a range) so that
-// idle consumers do not flood the memory system, then read in bulk rounds,
-// re-polling a round only if some word is still stale (values and tags of
-// different words become visible in no particular order).
-struct Range {
-  u64* src;
-  int n;
-  float* dst;
-  unsigned tag;
-  int ss;  // sentinel stride (words per producer block)
-};
-
-__device__ __forceinline__ int range_sentinels(const Range& r) { return r.n > 0 ? (r.n + r.ss - 1) / r.ss : 0; }
-
-template <int B>
-__device__ __forceinline__ bool fetch3(Range a, Range b, Range c, const Params& p) {
-  const int tid = ltid();
-  int failed = 0;
-  __syncthreads();  // every wave is done with the LDS of its previous phase
-  // 1. light wait on sentinels (wave 0 only), for inputs that need more than
-  //    one bulk round
-  if (a.n + b.n + c.n > B * NT && tid < kWave) {
-    const int na = range_sentinels(a), nb = range_sentinels(b), nc = range_sentinels(c);
-    const int ns = na + nb + nc;
-    Spin sp;
-    for (int base = 0; base < ns && !failed;) {
-      // all loads of a round are issued before any is tested
-      u64 v[4];
-      unsigned tgk[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = base + tid + k * kWave;
-        tgk[k] = 0u;
-        v[k] = 0ull;
-        if (i < ns) {
-          u64* s;
-          if (i < na) { s = a.src + i * a.ss; tgk[k] = a.tag; }
-          else if (i < na + nb) { s = b.src + (i - na) * b.ss; tgk[k] = b.tag; }
-          else { s = c.src + (i - na - nb) * c.ss; tgk[k] = c.tag; }
-          v[k] = ll_get(s);
-        }
-      }
-      bool ready = true;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) ready &= (base + tid + k * kWave >= ns) || ll_tag(v[k]) == tgk[k];
-      // every lane must see its sentinels ready before the window advances
-      if (__all(ready)) {
-        base += 4 * kWave;
-        continue;
-      }
-      if (!sp.step(p.err, p.timeout_ticks)) failed = 1;
-    }
-  }
-  if (block_failed(failed)) return false;
-  // 2. bulk read with verification
-  const int total = a.n + b.n + c.n;
-  for (int base = 0; base < total && !failed; base += NT * B) {
-    u64 wv[B];
-    Spin sp;
-    while (true) {
-      bool ready = true;
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        int i = base + k * NT + tid;
-        if (i < total) {
-          u64* s = i < a.n ? a.src + i : (i < a.n + b.n ? b.src + (i - a.n) : c.src + (i - a.n - b.n));
-          const unsigned tg = i < a.n ? a.tag : (i < a.n + b.n ? b.tag : c.tag);
-          wv[k] = ll_get(s);
-          ready &= ll_tag(wv[k]) == tg;
-        }
-      }
-      if (ready) break;
-      if (!sp.step(p.err, p.timeout_ticks)) {
-        failed = 1;
-        break;
-      }
-    }
-    if (!failed) {
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        int i = base + k * NT + tid;
-        if (i < total) {
-          float* d = i < a.n ? a.dst + i : (i < a.n + b.n ? b.dst + (i - a.n) : c.dst + (i - a.n - b.n));
-          *d = ll_val(wv[k]);
-        }
-      }
-    }
-  }
-  return !block_failed(failed);
-}
-
-constexpr Range kNoRange = {nullptr, 0, nullptr, 0u, 1};
-
-template <int B>
-__device__ __forceinline__ bool fetch1(u64* src, int n, float* dst, unsigned tag, const Params& p, int ss = 16) {
-  return fetch3<B>(Range{src, n, dst, tag, ss}, kNoRange, kNoRange, p);
 }
 
 // ------------------------------------------------------------ attention
@@ -1084,29 +1152,28 @@ __device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit,
 // O phase input: wait for the partials of the nsplit splits of every kv head
 // and merge them (log-sum-exp, reference attention.cuh:96-140 computes the
 // same softmax in one pass) into dst[QD], in batches of SB splits with a
-// running max; plus, unless xrows is null, the 16 tagged residual rows of this
-// workgroup's block.  Thread t owns output pairs t + k NT.
+// running max; plus, unless xb0 < 0, the 16 residual rows of x block xb0
+// (threads 0..7) and, unless xb1 < 0, of block xb1 (threads 8..15).  Thread t
+// owns output pairs t + k NT (8-byte loads, as fetch_pk).
 template <class S>
-__device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, u64* xrows,
-                                           unsigned xtag, float* dst, float* xres, u64* xrows2 = nullptr) {
-  constexpr int NPG = S::GQA * S::D / 2;  // pairs per kv head
+__device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
+                                            int xb0, int xb1, unsigned xt4, float* dst, float* xres) {
+  constexpr int NPG = S::GQA * S::D / 2;
   constexpr int WP = part_words<S>();
   constexpr int PPT = (S::QD / 2 + NT - 1) / NT;
   constexpr int SB = 8;
   const int tid = ltid();
+  const bool want_x0 = xb0 >= 0 && (tid < 8 || (tid < 16 && xb1 >= 0));
   int failed = 0;
-  __syncthreads();  // every wave is done with the LDS of its previous phase
+  __syncthreads();
   float M[PPT], L[PPT], o0[PPT], o1[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) M[k] = -INFINITY, L[k] = 0.f, o0[k] = 0.f, o1[k] = 0.f;
   for (int s0 = 0; s0 < nsplit && !failed; s0 += SB) {
     u64 wa[PPT][SB], wm[PPT][SB], wx = 0ull;
-    const bool want_x = s0 == 0 && ((tid < 16 && xrows) || (tid >= 16 && tid < 32 && xrows2));
+    const bool want_x = s0 == 0 && want_x0;
     Spin sp;
     while (true) {
-      // every load is issued before any is tested (one round trip per poll
-      // round): the split condition is uniform over the workgroup, pairs past
-      // QD/2 re-read pair 0, and every thread reads a residual word
 #pragma unroll
       for (int k = 0; k < PPT; ++k) {
         const int pi = tid + k * NT < S::QD / 2 ? tid + k * NT : 0;
@@ -1121,32 +1188,31 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
           }
         }
       }
-      wx = ll_get(want_x ? (tid < 16 ? xrows : xrows2) + (tid & 15) : p.part);
-      bool ready = true;
+      if (want_x) wx = ll_get(const_cast<u64*>(x) + (tid < 8 ? xb0 : xb1) * 8 + (tid & 7));
+      bool ready = !want_x || pk_ready(wx, xt4);
 #pragma unroll
       for (int k = 0; k < PPT; ++k)
 #pragma unroll
         for (int u = 0; u < SB; ++u)
           ready &= tid + k * NT >= S::QD / 2 || s0 + u >= nsplit ||
                    (pk_ready(wa[k][u], t4) && pk_ready(wm[k][u], t4));
-      ready &= !want_x || ll_tag(wx) == xtag;
       if (ready) break;
       if (!sp.step(p.err, p.timeout_ticks)) {
         failed = 1;
         break;
       }
     }
-    if (want_x) xres[tid] = ll_val(wx);
+    if (want_x) xres[2 * tid] = pk_lo(wx), xres[2 * tid + 1] = pk_hi(wx);
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       float Mb = M[k];
 #pragma unroll
       for (int u = 0; u < SB; ++u) Mb = s0 + u < nsplit ? fmaxf(Mb, pk_lo(wm[k][u])) : Mb;
-      const float r = __expf(M[k] - Mb);  // 0 on the first batch
+      const float r = __expf(M[k] - Mb);
       o0[k] *= r, o1[k] *= r, L[k] *= r;
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
-        const bool ok = s0 + u < nsplit;  // select, not multiply: skipped words hold anything
+        const bool ok = s0 + u < nsplit;
         const float f = __expf(pk_lo(wm[k][u]) - Mb);
         o0[k] = ok ? fmaf(f, pk_lo(wa[k][u]), o0[k]) : o0[k];
         o1[k] = ok ? fmaf(f, pk_hi(wa[k][u]), o1[k]) : o1[k];
@@ -1263,6 +1329,9 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
     const Item nxt = att_item(it_att, n + 1, S::NKV, p.chunk_min, p.nsplit_max);
     const int nsplit = cur.nsplit;
     const bool has_att = cur.on;
+    // some phase of every layer (the LM head's x poll relies on it, wait_last_qkv)
+    const bool layer_role =
+        has_att || it_qkv < S::RB_QKV || it_o < S::RB_H || it_gu < S::RB_F || it_dn < S::RB_H;
     const int kv_at = !LC || nsplit <= p.merge_min
                           ? 2
                           : (it_gu < S::RB_F ? 4 : (it_dn < S::RB_H ? 5 : (it_o < S::RB_H ? 3 : 2)));
@@ -1295,14 +1364,15 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         }
         if constexpr (DBG) trace_mark(p, t, slot + 0, 0);
         {  // the prefetched block
-          const float y = blk_dot(rq, sm.vec_q);
-          store_rows(sm.rowbuf[0], p.qkv + it_qkv * 16, y * r, tg);
+          blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
+          store_block(sm.red[RED_Q], p.qkv + it_qkv * 16, r, nullptr, tg);
           evt(p, t, layer, EV_QKV_STORED);
         }
         for (int rb = it_qkv + G; rb < S::RB_QKV; rb += G) {  // grids smaller than the block count
           blk_load(rq, wl + S::OFF_QKV + (long long)rb * S::KT_H * 64);
-          const float y = blk_dot(rq, sm.vec_q);
-          if (row_owner()) ll_put(p.qkv + rb * 16 + blk_row(), ll_pack(y * r, tg));
+          __syncthreads();  // the previous block's shares are summed
+          blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
+          store_block(sm.red[RED_Q], p.qkv + rb * 16, r, nullptr, tg);
         }
         if constexpr (DBG) trace_mark(p, t, slot + 0, 1);
       }
@@ -1349,29 +1419,24 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         // a long context's splits arrive merged (one row after the splits)
         const bool merged = LC && nsplit > p.merge_min;
         if (!fetch_attn<S>(p, merged ? p.part + (long long)p.nsplit_max * S::NKV * part_words<S>() : p.part,
-                           merged ? 1 : nsplit, tag4(tg + 1u), layer > 0 ? p.x + it_o * 16 : nullptr, tg_x, sm.vec_o,
+                           merged ? 1 : nsplit, tag4(tg + 1u), p.x, layer > 0 ? it_o : -1, -1, tag4(tg_x), sm.vec_o,
                            sm.xres_o))
           return;
         if constexpr (DBG) trace_mark(p, t, slot + 2, 0);
         evt(p, t, layer, EV_O_READY);
-        const float y = blk_dot(ro, sm.vec_o);
-        {
-          const int row = it_o * 16 + blk_row();
-          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres_o[blk_row()];
-          store_rows(sm.rowbuf[1], p.x + it_o * 16, xo + y, tg + 2u);
-        }
+        blk_mma(ro, sm.vec_o, sm.red[RED_O0]);
+        __syncthreads();
+        if (tid < 8) o_rows<S>(p, sm, it_o, tid, layer, tok, tg + 2u);
         evt(p, t, layer, EV_O_STORED);
         if constexpr (DBG) trace_mark(p, t, slot + 2, 1);
       }
       for (int rb = it_o + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
         blk_load(ro, wl + S::OFF_O + (long long)rb * S::KT_Q * 64);
-        if (layer > 0 && !fetch1<1>(p.x + rb * 16, 16, sm.xres_o, tg_x, p)) return;
-        const float y = blk_dot(ro, sm.vec_o);
-        if (row_owner()) {
-          const int row = rb * 16 + blk_row();
-          const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, row) : sm.xres_o[blk_row()];
-          ll_put(p.x + row, ll_pack(xo + y, tg + 2u));
-        }
+        if (layer > 0 && !fetch_xrows(p, p.x, rb, tag4(tg_x), sm.xres_o)) return;
+        __syncthreads();  // the previous block's shares are summed
+        blk_mma(ro, sm.vec_o, sm.red[RED_O0]);
+        __syncthreads();
+        if (tid < 8) o_rows<S>(p, sm, rb, tid, layer, tok, tg + 2u);
       }
       if (kv_at == 3) prefetch_kv();
       // ---------------- P4: gate/up + SiLU (prefetch: down)
@@ -1382,19 +1447,19 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return;
         if constexpr (DBG) trace_mark(p, t, slot + 3, 0);
         {  // the prefetched block pair
-          const float yg = blk_dot(rg, sm.vec_g);
-          const float yu = blk_dot(ru, sm.vec_g);
-          store_rows_pk(sm.rowbuf[2], p.act + it_gu * 8, silu_mul(yg * r, yu * r), tag4(tg + 3u));
+          blk_mma(rg, sm.vec_g, sm.red[RED_G]);
+          blk_mma(ru, sm.vec_g, sm.red[RED_U]);
+          store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + it_gu * 8, r, tag4(tg + 3u));
           evt(p, t, layer, EV_GU_STORED);
         }
         for (int pr = it_gu + G; pr < S::RB_F; pr += G) {  // grids smaller than the block count
           const u32x4* gp = wl + S::OFF_GU + (long long)(2 * pr) * S::KT_H * 64;
           blk_load(rg, gp);
           blk_load(ru, gp + S::KT_H * 64);
-          const float yg = blk_dot(rg, sm.vec_g);
-          const float yu = blk_dot(ru, sm.vec_g);
-          store_rows_pk(sm.rowbuf[2], p.act + pr * 8, silu_mul(yg * r, yu * r), tag4(tg + 3u));
-          __syncthreads();
+          __syncthreads();  // the previous pair's shares are summed
+          blk_mma(rg, sm.vec_g, sm.red[RED_G]);
+          blk_mma(ru, sm.vec_g, sm.red[RED_U]);
+          store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + pr * 8, r, tag4(tg + 3u));
         }
         if constexpr (DBG) trace_mark(p, t, slot + 3, 1);
       }
@@ -1408,29 +1473,22 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       }
       if (kv_at == 4) prefetch_kv();
       if (it_dn < S::RB_H) {
-        if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x + it_dn * 16, tg + 2u, sm.vec_d, sm.xres_d)) return;
+        if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x, it_dn, tag4(tg + 2u), sm.vec_d, sm.xres_d)) return;
         if constexpr (DBG) trace_mark(p, t, slot + 4, 0);
         evt(p, t, layer, EV_DN_READY);
-        const float y = blk_dot(rd, sm.vec_d);
-        {
-          const int row = it_dn * 16 + blk_row();
-          const float xn = sm.xres_d[blk_row()] + y;
-          if (DBG && p.dbg_layers && row_owner()) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
-          store_rows(sm.rowbuf[3], p.x + it_dn * 16, xn, tg + 4u);
-        }
+        blk_mma(rd, sm.vec_d, sm.red[RED_D]);
+        __syncthreads();
+        if (tid < 8) down_rows<S>(p, sm, it_dn, tid, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
         evt(p, t, layer, EV_DN_STORED);
         if constexpr (DBG) trace_mark(p, t, slot + 4, 1);
       }
       for (int rb = it_dn + G; rb < S::RB_H; rb += G) {  // grids smaller than the block count
         blk_load(rd, wl + S::OFF_DOWN + (long long)rb * S::KT_F * 64);
-        if (!fetch1<1>(p.x + rb * 16, 16, sm.xres_d, tg + 2u, p)) return;
-        const float y = blk_dot(rd, sm.vec_d);
-        if (row_owner()) {
-          const int row = rb * 16 + blk_row();
-          const float xn = sm.xres_d[blk_row()] + y;
-          ll_put(p.x + row, ll_pack(xn, tg + 4u));
-          if (DBG && p.dbg_layers) p.dbg_layers[(long long)(layer + 1) * S::H + row] = xn;
-        }
+        if (!fetch_xrows(p, p.x, rb, tag4(tg + 2u), sm.xres_d)) return;
+        __syncthreads();  // the previous block's shares are summed
+        blk_mma(rd, sm.vec_d, sm.red[RED_D]);
+        __syncthreads();
+        if (tid < 8) down_rows<S>(p, sm, rb, tid, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
       }
       if (kv_at == 5) prefetch_kv();
     }
@@ -1442,6 +1500,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
       NormIn<S> gfin;
       gains_load(gfin, p.final_norm);
       float rn;
+      if (!layer_role && !wait_last_qkv(p, tl)) return;
       if (!fetch_norm<S, false>(p, p.x, tl - 1u, gfin, sm.vec_l, sm.ssw[2], &rn)) return;
       if constexpr (DBG) trace_mark(p, t, PHASES_PER_LAYER * L, 0);
       const long long nb = p.vocab / 16;
