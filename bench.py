@@ -328,7 +328,7 @@ def bench_ops(args):
     n_in = 8
     for name, rows, k, kind in gemvs:
         gu = kind == ops.GEMV_GATE_UP
-        buf, nb, nc = weights(2 * rows if gu else rows, k, ops.LAYOUT_GATE_UP if gu else ops.LAYOUT_ROWPAIR)
+        buf, nb, nc = weights(2 * rows if gu else rows, k, ops.LAYOUT_GATE_UP if gu else ops.LAYOUT_TILE)
         xin = torch.randn((n_in, k), generator=g, device="cuda")
         res = torch.randn((n_in, rows), generator=g, device="cuda") if kind == ops.GEMV_RESIDUAL else None
         y = torch.empty((64, rows), device="cuda")

@@ -297,9 +297,8 @@ float megakernel_batch_last_ms(void* handle);
  * megakernel_last_error() set (arguments are checked before any GPU work).
  * megakernel_op_last_ms() gives the device time of the last call. */
 
-#define MK_OP_LAYOUT_ROWPAIR 0 /* layer matrices (GEMVs): K % 256 == 0 */
-#define MK_OP_LAYOUT_TILE 1    /* LM head 16x32 tiles: K % 32 == 0 */
-#define MK_OP_LAYOUT_GATE_UP 2 /* [gate; up] rows (2F x K) -> interleaved row-pair blocks */
+#define MK_OP_LAYOUT_TILE 1    /* 16x32 tiles (layer matrices, LM head): K % 32 == 0 */
+#define MK_OP_LAYOUT_GATE_UP 2 /* [gate; up] rows (2F x K) -> interleaved tile blocks */
 
 #define MK_OP_GEMV_PLAIN 0     /* y = W x                     (QKV, O) */
 #define MK_OP_GEMV_RESIDUAL 1  /* y = res + W x               (down + residual) */
@@ -320,7 +319,7 @@ int megakernel_op_rmsnorm(const void* x, const void* gain, float* y, int n, int 
 
 /* gemv_qkv / gemv_block / gemv_gate_up_silu (src/gemv.cuh:36-279) and the
  * down projection with its residual (src/megakernel.cu:270-290).  w: packed
- * (MK_OP_LAYOUT_ROWPAIR, or MK_OP_LAYOUT_GATE_UP for kind 2), rows outputs,
+ * (MK_OP_LAYOUT_TILE, or MK_OP_LAYOUT_GATE_UP for kind 2), rows outputs,
  * k in {256, 512, 1024, 2048, 2816, 3072}; x [n_in][k]; res [n_in][rows]
  * (kind 1); y [n_out][rows]. */
 int megakernel_op_gemv(const void* w, long long copy_bytes, int n_copies, int rows, int k, int kind, const float* x,

@@ -66,7 +66,7 @@ static int repack_tiles(BHandle* h, const char* base, long long off, int R, int 
   const int threads = 256;
   const int blocks = (int)((units + threads - 1) / threads < 65536 ? (units + threads - 1) / threads : 65536);
   hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, h->stream,
-                     reinterpret_cast<const u32x4*>(base + off), R, K, dst, 1, 0, 0);
+                     reinterpret_cast<const u32x4*>(base + off), R, K, dst, 1, 0);
   HIPCHK(hipGetLastError(), -1);
   return 0;
 }

@@ -34,29 +34,21 @@ void set_err(const char* fmt, ...) {
 }
 
 // --------------------------------------------------------- device helpers
-// Repack a row-major bf16 matrix W[R][K] into one of the packed layouts of
-// mk_config.h (row_pairs = 1: layer matrices, 0: LM-head tiles).  Destination
-// 16-row block of source block rb is rb * blk_stride + blk_off, so gate/up can
-// be interleaved.  One thread per 16-byte unit.
+// Repack a row-major bf16 matrix W[R][K] into the packed tile layout of
+// mk_config.h.  Destination 16-row block of source block rb is
+// rb * blk_stride + blk_off, so gate/up can be interleaved.  One thread per
+// 16-byte unit.
 __global__ void repack_kernel(const u32x4* __restrict__ src, int R, int K, u32x4* __restrict__ dst,
-                              int blk_stride, int blk_off, int row_pairs) {
-  const int KT = K / 32, KC = K / 256;
+                              int blk_stride, int blk_off) {
+  const int KT = K / 32;
   const long long units = (long long)R * K / 8;
   for (long long u = (long long)blockIdx.x * blockDim.x + threadIdx.x; u < units;
        u += (long long)gridDim.x * blockDim.x) {
     const int lane = (int)(u % 64);
     const long long t = u / 64;
-    const int tin = (int)(t % KT);  // 1 KiB unit inside the block
+    const int tin = (int)(t % KT);  // 1 KiB unit (16 x 32 tile) inside the block
     const long long rb = t / KT;
-    long long row, chunk;           // source row and 16-byte column chunk
-    if (row_pairs) {
-      const int w = tin / KC, kc = tin % KC;
-      row = rb * 16 + 2 * w + (lane >> 5);
-      chunk = (long long)kc * 32 + (lane & 31);
-    } else {
-      row = rb * 16 + (lane & 15);
-      chunk = (long long)tin * 4 + (lane >> 4);
-    }
+    const long long row = rb * 16 + (lane & 15), chunk = (long long)tin * 4 + (lane >> 4);
     dst[((rb * blk_stride + blk_off) * KT + tin) * 64 + lane] = src[row * (K / 8) + chunk];
   }
 }
@@ -364,7 +356,7 @@ static void free_all(Handle* h) {
 }
 
 static int repack(Handle* h, const char* base, long long off, int R, int K, u32x4* dst, int stride,
-                  int blk_off, int row_pairs = 1) {
+                  int blk_off) {
   if (off < 0 || (off & 15)) {
     set_err("weight offset %lld is negative or not 16-byte aligned", off);
     return -1;
@@ -373,7 +365,7 @@ static int repack(Handle* h, const char* base, long long off, int R, int K, u32x
   const int threads = 256;
   const int blocks = (int)((units + threads - 1) / threads < 65536 ? (units + threads - 1) / threads : 65536);
   hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, h->stream,
-                     reinterpret_cast<const u32x4*>(base + off), R, K, dst, stride, blk_off, row_pairs);
+                     reinterpret_cast<const u32x4*>(base + off), R, K, dst, stride, blk_off);
   HIPCHK(hipGetLastError(), -1);
   return 0;
 }
@@ -453,7 +445,7 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
 
   // Repack matrices (offset order: reference megakernel.cu:518-532).
   const int KTH = s.H / 32;
-  if (repack(h, base, off[0], h->V, s.H, h->lmhead, 1, 0, /*row_pairs=*/0)) return -1;
+  if (repack(h, base, off[0], h->V, s.H, h->lmhead, 1, 0)) return -1;
   HIPCHK(hipMemcpyAsync(h->final_norm, base + off[1], (size_t)s.H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
   for (int i = 0; i < h->L; ++i) {
     const long long* o = off + 2 + 11 * i;
@@ -464,13 +456,13 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
     HIPCHK(hipMemcpyAsync(nl + s.norm_k, base + o[5], (size_t)s.D * 2, hipMemcpyDeviceToDevice, h->stream), -1);
     HIPCHK(hipMemcpyAsync(nl + s.norm_ffn, base + o[7], (size_t)s.H * 2, hipMemcpyDeviceToDevice, h->stream), -1);
     u32x4* qkv = wl + s.off_qkv;
-    if (repack(h, base, o[1], s.QD, s.H, qkv, 1, 0, 0)) return -1;
-    if (repack(h, base, o[2], s.KVD, s.H, qkv, 1, s.QD / 16, 0)) return -1;
-    if (repack(h, base, o[3], s.KVD, s.H, qkv, 1, (s.QD + s.KVD) / 16, 0)) return -1;
-    if (repack(h, base, o[6], s.H, s.QD, wl + s.off_o, 1, 0, 0)) return -1;
-    if (repack(h, base, o[8], s.F, s.H, wl + s.off_gu, 2, 0, 0)) return -1;
-    if (repack(h, base, o[9], s.F, s.H, wl + s.off_gu, 2, 1, 0)) return -1;
-    if (repack(h, base, o[10], s.H, s.F, wl + s.off_down, 1, 0, 0)) return -1;
+    if (repack(h, base, o[1], s.QD, s.H, qkv, 1, 0)) return -1;
+    if (repack(h, base, o[2], s.KVD, s.H, qkv, 1, s.QD / 16)) return -1;
+    if (repack(h, base, o[3], s.KVD, s.H, qkv, 1, (s.QD + s.KVD) / 16)) return -1;
+    if (repack(h, base, o[6], s.H, s.QD, wl + s.off_o, 1, 0)) return -1;
+    if (repack(h, base, o[8], s.F, s.H, wl + s.off_gu, 2, 0)) return -1;
+    if (repack(h, base, o[9], s.F, s.H, wl + s.off_gu, 2, 1)) return -1;
+    if (repack(h, base, o[10], s.H, s.F, wl + s.off_down, 1, 0)) return -1;
   }
   (void)KTH;
   HIPCHK(hipStreamSynchronize(h->stream), -1);

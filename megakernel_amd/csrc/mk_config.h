@@ -56,20 +56,14 @@ using ShapeQwen3 = Shape<1024, 16, 8, 128, 3072>;
 using ShapeTiny = Shape<256, 4, 2, 64, 512>;
 
 // ---------------------------------------------------------------------------
-// Packed weight layouts.  Both cut a row-major bf16 matrix W[R][K]
-// (R % 16 == 0) into 16-row blocks of 16*K*2 bytes, block rb's bytes
+// Packed weight layout ("tile"): a row-major bf16 matrix W[R][K] (R % 16 ==
+// 0, K % 32 == 0) is cut into 16-row blocks of 16*K*2 bytes, block rb's bytes
 // contiguous, so a workgroup streams one block with wave-wide 1 KiB loads.
-//
-// Layer matrices ("row-pair" layout, K % 256 == 0): inside block rb, the
-// 1 KiB unit (w, kc) at index w * (K/256) + kc holds rows 16rb + 2w and
-// 16rb + 2w + 1, columns 256kc .. 256kc + 255: 16-byte lane l holds the 8 bf16
-// W[16rb + 2w + (l >> 5)][256kc + 8(l & 31) + e], e = 0..7.  Wave w of the
-// owning workgroup reads exactly its two rows, so a row's dot product is
-// reduced inside one wave (no cross-wave exchange).
-//
-// LM head / embedding ("tile" layout, K % 32 == 0): inside block rb, unit kt
-// holds the 16 x 32 tile at columns 32kt: lane l holds
-// W[16rb + (l & 15)][32kt + 8(l >> 4) + e].  A wave reduces a whole block.
+// Inside block rb, 1 KiB unit kt holds the 16 x 32 tile at columns 32kt: lane
+// l holds W[16rb + (l & 15)][32kt + 8(l >> 4) + e], e = 0..7 -- the A operand
+// of v_mfma_f32_16x16x32_bf16.  Layer GEMVs (K % 256 == 0) give wave w of the
+// owning workgroup the units w K/256 .. (w + 1) K/256 - 1 (a K slice of all 16
+// rows); the LM head's waves reduce whole blocks.
 //
 // Per layer: fused QKV (q rows, then k rows, then v rows) | O | gate/up with
 // blocks interleaved (gate block p at 2p, up block p at 2p+1) | down.

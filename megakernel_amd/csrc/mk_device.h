@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mk_protocol.h"
+
 namespace mk {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -70,13 +72,11 @@ __device__ __forceinline__ float dot8(u32x4 w, const float* h, float acc) {
 
 // Split-bf16 GEMV input vectors.  A layer GEMV's input x lives in LDS as two
 // bf16 parts, x = hi + lo with hi = RNE(x) and lo = RNE(x - hi) (x - hi is
-// exact; relative error of the pair <= 2^-17), so each weight pair costs one
-// v_dot2c_f32_bf16 per part: one VALU op per weight against two (convert +
-// fma) for fp32 inputs.  Layout: 8 columns per 32-byte group, the group's 4
-// dwords of hi pairs (columns 2i, 2i+1 in the low / high half) then its 4 of
-// lo pairs -- the same 4-byte slot count as an fp32 vector, so the readers'
-// offsets are the fp32 ones.
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// exact; relative error of the pair <= 2^-17), the B operand's columns 0 and
+// 1 of the block product (mk_kernel.h blk_mma).  Layout: 8 columns per
+// 32-byte group, the group's 4 dwords of hi pairs (columns 2i, 2i+1 in the
+// low / high half) then its 4 of lo pairs -- one 16-byte load per part and
+// 8 columns, and the same 4-byte slot count as an fp32 vector.
 __device__ __forceinline__ void xs_put(uint32_t* xs, int e, float v) {
   uint16_t* h = reinterpret_cast<uint16_t*>(xs);
   const int g = e >> 3, j = e & 7;
@@ -92,23 +92,6 @@ __device__ __forceinline__ void xs_put_pair(uint32_t* xs, int e, float a, float 
   xs[g * 8 + 4 + i] =
       (uint32_t)f32_to_bf16(a - bf16_to_f32(ha)) | ((uint32_t)f32_to_bf16(b - bf16_to_f32(hb)) << 16);
 }
-// 8 bf16 weights (one 16-byte unit) against the split group xg (8 dwords).
-// The vectors are unpacked into scalars first: a bit_cast of an ext_vector
-// element (w[c]) compiles to element 0 for every c with this toolchain.
-__device__ __forceinline__ float dot8x(u32x4 w, const uint32_t* xg, float acc) {
-  const u32x4 h = *reinterpret_cast<const u32x4*>(xg);
-  const u32x4 l = *reinterpret_cast<const u32x4*>(xg + 4);
-  const uint32_t wa[4] = {w.x, w.y, w.z, w.w}, ha[4] = {h.x, h.y, h.z, h.w}, la[4] = {l.x, l.y, l.z, l.w};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wa[c]), __builtin_bit_cast(bf16x2, ha[c]), acc,
-                                          false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wa[c]), __builtin_bit_cast(bf16x2, la[c]), acc,
-                                          false);
-  }
-  return acc;
-}
-
 // 16 FP8 (OCP e4m3) weights against 16 fp32 inputs: the hardware converts two
 // bytes per instruction (bytes 0-1 / 2-3 of each dword, in order).
 __device__ __forceinline__ float dot16_fp8(u32x4 w, const float* h, float acc) {
@@ -369,39 +352,13 @@ __device__ __forceinline__ uint16_t synth_bf16(unsigned long long key, unsigned 
 // release/acquire fence (L2 write-back / invalidate) and no read-modify-write
 // is needed: a word with the right tag carries the right value.  Waits are
 // bounded: on timeout the error word is set and every workgroup unwinds.
-typedef unsigned long long u64;
+// (encodings and tag arithmetic: mk_protocol.h)
 enum : int { MK_OK = 0, MK_ERR_TIMEOUT = 1 };
 
-__device__ __forceinline__ u64 ll_pack(float v, unsigned tag) {
-  return ((u64)tag << 32) | (u64)__float_as_uint(v);
-}
 __device__ __forceinline__ void ll_put(u64* p, u64 w) {
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ u64 ll_get(u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
-__device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigned)w); }
-
-// Packed pair: two values in one tagged word, each rounded to a 19-bit
-// mantissa (relative error <= 2^-20) with a 4-bit tag in its low bits, so a
-// large vector needs half the words.  The 4-bit tag (1..15, never 0) is the
-// full tag mod 15 + 1: a reader can only mistake a stale word for current if
-// the word's last write is a multiple of 15 phases older than the awaited
-// one.  The protocol keeps that gap between 1 and 14 phases (every word is
-// rewritten at least once a layer, 5 phases, 6 across a token boundary); the
-// host clears the words (tag 0) wherever a reconfiguration could break it.
-__device__ __forceinline__ unsigned tag4(unsigned tag) { return tag % 15u + 1u; }
-__device__ __forceinline__ unsigned pk_half(float v, unsigned t4) {
-  return ((__float_as_uint(v) + 8u) & ~15u) | t4;
-}
-__device__ __forceinline__ u64 pk_pack(float a, float b, unsigned t4) {
-  return ((u64)pk_half(b, t4) << 32) | pk_half(a, t4);
-}
-__device__ __forceinline__ bool pk_ready(u64 w, unsigned t4) {
-  return ((unsigned)w & 15u) == t4 && ((unsigned)(w >> 32) & 15u) == t4;
-}
-__device__ __forceinline__ float pk_lo(u64 w) { return __uint_as_float((unsigned)w & ~15u); }
-__device__ __forceinline__ float pk_hi(u64 w) { return __uint_as_float((unsigned)(w >> 32) & ~15u); }
 
 // Two adjacent packed-pair words (16-byte aligned, byte offset off in the
 // buffer rs) in one 16-byte load with agent scope (sc1, as ll_get): a poll

@@ -32,7 +32,7 @@ __device__ __forceinline__ long long vt_index(int l, int g, long long t, int d, 
 }
 
 __global__ void repack_kernel(const u32x4* __restrict__ src, int R, int K, u32x4* __restrict__ dst,
-                              int blk_stride, int blk_off, int row_pairs);
+                              int blk_stride, int blk_off);
 __global__ void synth_kv_kernel(uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt, int L, int NKV, int s_pad,
                                 int D, int len, unsigned long long seed, float c);
 __global__ void kv_convert_kernel(uint16_t* __restrict__ buf, uint16_t* __restrict__ kv, uint16_t* __restrict__ kvt,

@@ -35,7 +35,6 @@ namespace mk {
 
 constexpr int NT = 512;               // threads per workgroup (8 waves)
 constexpr int NW = NT / kWave;
-constexpr int PHASES_PER_LAYER = 5;
 #ifndef MK_KV_BLOCKS
 #define MK_KV_BLOCKS 2
 #endif
@@ -54,9 +53,7 @@ constexpr int KVB = MK_KV_BLOCKS;
 #endif
 
 constexpr int NSPLIT_CAP = 32;        // max attention splits per kv head
-constexpr int TAG14 = 0x3FFF;         // argmax words carry a 14-bit tag, never 0
-__device__ __forceinline__ unsigned tag14(unsigned tag) { return tag % 16383u + 1u; }
-constexpr int IDX_BITS = 18;          // ... and an 18-bit vocabulary index
+constexpr int IDX_BITS = 18;          // argmax words: 14-bit tag (TAG14) and an 18-bit vocabulary index
 constexpr unsigned IDX_MAX = (1u << IDX_BITS) - 1;
 
 struct Params {
@@ -159,9 +156,9 @@ __device__ __forceinline__ bool poll_rounds(const Params& p, Issue issue, Ready 
 }
 
 // ------------------------------------------------------------------ GEMV
-// One packed 16-row block in the row-pair layout: wave w holds chunks
-// 0..KC-1 of rows 2w, 2w+1; lane l covers row 2w + (l >> 5) and columns
-// 256 kc + 8 (l & 31) .. +8.
+// One packed 16-row block in the tile layout (mk_config.h): wave w holds the
+// 1 KiB units (16 x 32 tiles) w KC .. w KC + KC - 1, lane l of unit kt row
+// l & 15, columns 32 kt + 8 (l >> 4) .. +7.
 template <int KC>
 struct Blk {
   u32x4 w[KC];
@@ -254,39 +251,6 @@ __device__ __forceinline__ void store_block_gu(const float* rg, const float* ru,
     const float b = silu_mul(red_sum(rg, 2 * t_ + 1) * r, red_sum(ru, 2 * t_ + 1) * r);
     ll_put(dst8 + t_, pk_pack(a, b, t4));
   }
-}
-
-// Row of the block this lane's dot product belongs to, and the lane that
-// stores it (lanes 0 and 32).
-__device__ __forceinline__ int blk_row() { return 2 * wave_id() + (int)(lane_id() >> 5); }
-__device__ __forceinline__ bool row_owner() { return (lane_id() & 31u) == 0u; }
-
-// Dot product of this lane's row with vec (LDS, split-bf16 pairs, xs_put):
-// every lane of the half wave gets the full sum (reduced inside the wave, no
-// LDS exchange).
-template <int KC>
-__device__ __forceinline__ float blk_dot(const Blk<KC>& b, const float* vec) {
-  const uint32_t* hv = reinterpret_cast<const uint32_t*>(vec) + 8 * (int)(lane_id() & 31u);
-  float acc = 0.f;
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc) acc = dot8x(b.w[kc], hv + 256 * kc, acc);
-  return sum_xor16(group_sum<16>(acc));
-}
-
-// The 16 row results of a block, published by one wave as one 128-byte store.
-__device__ __forceinline__ void store_rows(float* rowbuf, u64* dst16, float v, unsigned tag) {
-  if (row_owner()) rowbuf[blk_row()] = v;
-  __syncthreads();
-  const int t_ = ltid();
-  if (t_ < 16) ll_put(dst16 + t_, ll_pack(rowbuf[t_], tag));
-}
-
-// The same for a packed-pair vector: 8 words of two values each.
-__device__ __forceinline__ void store_rows_pk(float* rowbuf, u64* dst8, float v, unsigned t4) {
-  if (row_owner()) rowbuf[blk_row()] = v;
-  __syncthreads();
-  const int t_ = ltid();
-  if (t_ < 8) ll_put(dst8 + t_, pk_pack(rowbuf[2 * t_], rowbuf[2 * t_ + 1], t4));
 }
 
 // Element of the tile-layout LM head / embedding (row, col).

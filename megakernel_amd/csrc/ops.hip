@@ -6,8 +6,8 @@
 // so a caller that rotates >= 512 MB of weight copies defeats every cache.
 //
 // The GEMVs use the persistent kernel's own packed layouts and inner loops
-// (row-pair blocks with Blk / blk_load / blk_dot, the LM head's tile stream),
-// so their numbers measure the code the decode runs.  Reference device code
+// (tile blocks with Blk / blk_load / blk_mma, the LM head's tile stream), so
+// their numbers measure the code the decode runs.  Reference device code
 // each op restates:
 //   rmsnorm            src/rmsnorm.cuh:87-108   (rmsnorm_float_in)
 //   gemv (QKV / O)     src/gemv.cuh:118-199, src/gemv.cuh:36-104
@@ -35,7 +35,8 @@ enum GemvKind : int { GEMV_PLAIN = 0, GEMV_RESIDUAL = 1, GEMV_GATE_UP = 2 };
 // workgroups round-robin, so the workgroups in flight stream neighbouring
 // blocks of one weight copy.  The input vector of the item's instance is
 // staged in LDS (split-bf16 pairs, as the decode kernel's GEMVs read it) and
-// only reloaded when the instance's input changes.
+// only reloaded when the instance's input changes; the block product is the
+// decode kernel's (blk_mma on tile-layout blocks, wave shares summed in LDS).
 // Loads are issued vector first (L2-resident pool), weights second, so the
 // vector's wait does not wait for the weight block (loads return in order).
 template <int KC, int KIND>
@@ -45,6 +46,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(const u32x4* __restrict__ w, l
                                                   int n_out, int reps) {
   constexpr int K = KC * 256, KT = K / 32, PER = (K + NT - 1) / NT;
   __shared__ float vec[K];
+  __shared__ float red[2][NW * 16];
   const int RB = rows / 16;
   const long long items = (long long)reps * RB;
   int have = -1;  // input index staged in vec (uniform across the workgroup)
@@ -69,8 +71,8 @@ __global__ __launch_bounds__(NT) void gemv_kernel(const u32x4* __restrict__ w, l
     } else {
       blk_load(bg, wc + (long long)b * KT * 64);
     }
+    __syncthreads();  // the previous item's reads of vec and red are done
     if (reload) {
-      __syncthreads();  // the previous item's reads of vec are done
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
         const int i = (int)threadIdx.x + k * NT;
@@ -79,10 +81,13 @@ __global__ __launch_bounds__(NT) void gemv_kernel(const u32x4* __restrict__ w, l
       __syncthreads();
       have = in;
     }
-    float v = blk_dot(bg, vec);
-    if (KIND == GEMV_GATE_UP) v = silu_mul(v, blk_dot(bu, vec));
-    if (row_owner()) {
-      const int row = b * 16 + blk_row();
+    blk_mma(bg, vec, red[0]);
+    if (KIND == GEMV_GATE_UP) blk_mma(bu, vec, red[1]);
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      const int t = (int)threadIdx.x, row = b * 16 + t;
+      float v = red_sum(red[0], t);
+      if (KIND == GEMV_GATE_UP) v = silu_mul(v, red_sum(red[1], t));
       if (KIND == GEMV_RESIDUAL) v += res[(long long)in * rows + row];
       y[(long long)(r % n_out) * rows + row] = v;
     }
@@ -447,12 +452,11 @@ int megakernel_op_pack(const void* d_src, int rows, int k, int layout, void* d_d
     set_err("op_pack: null or unaligned pointer");
     return -1;
   }
-  if (layout < MK_OP_LAYOUT_ROWPAIR || layout > MK_OP_LAYOUT_GATE_UP) {
+  if (layout != MK_OP_LAYOUT_TILE && layout != MK_OP_LAYOUT_GATE_UP) {
     set_err("op_pack: unknown layout %d", layout);
     return -1;
   }
-  if (rows <= 0 || rows % 16 || k <= 0 || k % (layout == MK_OP_LAYOUT_TILE ? 32 : 256) ||
-      (layout == MK_OP_LAYOUT_GATE_UP && rows % 32)) {
+  if (rows <= 0 || rows % 16 || k <= 0 || k % 32 || (layout == MK_OP_LAYOUT_GATE_UP && rows % 32)) {
     set_err("op_pack: rows=%d k=%d do not fit layout %d", rows, k, layout);
     return -1;
   }
@@ -465,11 +469,10 @@ int megakernel_op_pack(const void* d_src, int rows, int k, int layout, void* d_d
     if (layout == MK_OP_LAYOUT_GATE_UP) {  // gate rows [0, rows/2), up rows [rows/2, rows): blocks interleaved
       const int half = rows / 2;
       const long long hu = (long long)half * k / 8;
-      hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, 0, src, half, k, dst, 2, 0, 1);
-      hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, 0, src + hu, half, k, dst, 2, 1, 1);
+      hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, 0, src, half, k, dst, 2, 0);
+      hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, 0, src + hu, half, k, dst, 2, 1);
     } else {
-      hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, 0, src, rows, k, dst, 1, 0,
-                         layout == MK_OP_LAYOUT_ROWPAIR ? 1 : 0);
+      hipLaunchKernelGGL(repack_kernel, dim3(blocks), dim3(threads), 0, 0, src, rows, k, dst, 1, 0);
     }
     return 0;
   });

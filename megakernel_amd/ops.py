@@ -23,7 +23,7 @@ from __future__ import annotations
 
 from . import _lib
 
-LAYOUT_ROWPAIR, LAYOUT_TILE, LAYOUT_GATE_UP = 0, 1, 2
+LAYOUT_TILE, LAYOUT_GATE_UP = 1, 2
 GEMV_PLAIN, GEMV_RESIDUAL, GEMV_GATE_UP = 0, 1, 2
 
 

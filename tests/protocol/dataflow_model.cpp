@@ -7,7 +7,8 @@
 // until every tag matches.  This program runs the kernel's phase structure on
 // G threads ("workgroups") with the kernel's encodings and tag arithmetic:
 //
-//   x      [H]      full 32-bit tags (residual rows: O and down publish them)
+//   x      [H/2]    packed pairs with 4-bit tags (residual rows 2i, 2i + 1 in
+//                   word i: O and down publish them)
 //   qkv    [QKV]    full 32-bit tags
 //   part   [NS][NKV][W]  packed pairs with 4-bit tags tag % 15 + 1 (attention partials)
 //   act    [F/2]    packed pairs with 4-bit tags (gate/up output)
@@ -24,12 +25,20 @@
 // std::atomic with relaxed order, as in the kernel; ThreadSanitizer checks the
 // model for data races.
 //
-// Usage: dataflow_model [drop | alias]
-//   drop:  one producer omits one word of one phase; every waiting thread must
-//          time out or see the error word and unwind ("timeout detected", 0);
-//   alias: a planted mistake -- 4-bit tags that repeat every 5 phases, so the
-//          gate/up output of consecutive layers carries the same tag; the
-//          model must report stale values (exit 2).
+// The encodings and tag arithmetic are the kernel's own (mk_protocol.h).  G_IDLE
+// of the threads have no role in any layer, like the workgroups of a large grid
+// that only join the LM head: they wait for the last layer's QKV output
+// before polling x (the kernel's wait_last_qkv).
+//
+// Usage: dataflow_model [drop | alias | nogate]
+//   drop:   one producer omits one word of one phase; every waiting thread must
+//           time out or see the error word and unwind ("timeout detected", 0);
+//   alias:  a planted mistake -- 4-bit tags that repeat every 5 phases, so the
+//           gate/up output of consecutive layers carries the same tag; the
+//           model must report stale values (exit 2);
+//   nogate: a planted mistake -- the idle threads poll x without waiting for
+//           the last QKV output, so an x word 15 phases old passes its 4-bit
+//           tag check; the model must report stale values (exit 2).
 // Exit 0 and "ok" without arguments.
 #include <atomic>
 #include <chrono>
@@ -41,49 +50,32 @@
 #include <thread>
 #include <vector>
 
-typedef uint64_t u64;
+#include "../../megakernel_amd/csrc/mk_protocol.h"
 
-constexpr int G = 16;                 // workgroups
+using mk::ll_pack;
+using mk::ll_tag;
+using mk::ll_val;
+using mk::pk_pack;
+using mk::pk_ready;
+using mk::tag14;
+using mk::u64;
+
+constexpr int G_ROLE = 16, G_IDLE = 4;  // workgroups with layer roles / LM head only
+constexpr int G = G_ROLE + G_IDLE;
 constexpr int H = 64, NQ = 4, NKV = 2, D = 16, F = 96;
 constexpr int QD = NQ * D, KVD = NKV * D, QKV = QD + 2 * KVD, GQA = NQ / NKV;
 constexpr int NS = 3;                 // attention splits per kv head
 constexpr int W = GQA * D / 2 + GQA;  // words of one split partial
 constexpr int L = 4, T = 24;          // layers, tokens
-constexpr int PHASES = 5;
+constexpr int PHASES = mk::PHASES_PER_LAYER;
 
-// ---- encodings (the kernel's mk_device.h / mk_kernel.h helpers)
-u64 ll_pack(float v, unsigned tag) {
-  unsigned b;
-  memcpy(&b, &v, 4);
-  return ((u64)tag << 32) | b;
-}
-unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
-float ll_val(u64 w) {
-  unsigned b = (unsigned)w;
-  float v;
-  memcpy(&v, &b, 4);
-  return v;
-}
-bool alias_mode = false;
+bool alias_mode = false, nogate_mode = false;
 // the kernel's tag4; alias mode plants a period of 5 phases (= one layer)
-unsigned tag4(unsigned tag) { return alias_mode ? tag % 5u + 1u : tag % 15u + 1u; }
-unsigned tag14(unsigned tag) { return tag % 16383u + 1u; }
-unsigned pk_half(float v, unsigned t4) {
-  unsigned b;
-  memcpy(&b, &v, 4);
-  return ((b + 8u) & ~15u) | t4;
-}
-u64 pk_pack(float a, float b, unsigned t4) { return ((u64)pk_half(b, t4) << 32) | pk_half(a, t4); }
-bool pk_ready(u64 w, unsigned t4) { return ((unsigned)w & 15u) == t4 && ((unsigned)(w >> 32) & 15u) == t4; }
-float pk_f(unsigned h) {
-  h &= ~15u;
-  float v;
-  memcpy(&v, &h, 4);
-  return v;
-}
+unsigned tag4(unsigned tag) { return alias_mode ? tag % 5u + 1u : mk::tag4(tag); }
+float pk_f(unsigned h) { return mk::f32_from(h & ~15u); }
 
 // ---- shared state
-std::atomic<u64> x[H], qkv[QKV], part[NS * NKV * W], act[F / 2], amax[2 * G];
+std::atomic<u64> x[H / 2], qkv[QKV], part[NS * NKV * W], act[F / 2], amax[2 * G];
 std::atomic<int> err{0}, bad{0};
 std::atomic<long> polls{0};
 bool drop_mode = false;
@@ -129,13 +121,29 @@ void expect(bool c, const char* what, int token, int layer, int i) {
 }
 
 // item -> workgroup offsets as in the kernel (phases on disjoint workgroups)
-int first_item(int wg, int off) { return (wg + G - off % G) % G; }
+int first_item(int wg, int off) { return (wg + G_ROLE - off % G_ROLE) % G_ROLE; }
+
+// Wait for x rows i, i + 1 (word i / 2, i even) of tag `tag` and check them
+// against the values of (token, layer, buf).
+bool need_x2(int i, unsigned tag, int token, int layer, int buf, const char* what) {
+  u64 v;
+  const unsigned t4 = tag4(tag);
+  if (!wait_word(x[i / 2], [&](u64 w) { return pk_ready(w, t4); }, &v)) return false;
+  expect(pk_f((unsigned)v) == val(token, layer, buf, i) && pk_f((unsigned)(v >> 32)) == val(token, layer, buf, i + 1),
+         what, token, layer, i);
+  return true;
+}
+void put_x2(int i, unsigned tag, int token, int layer, int buf) {
+  x[i / 2].store(pk_pack(val(token, layer, buf, i), val(token, layer, buf, i + 1), tag4(tag)), std::memory_order_relaxed);
+}
 
 void run(int wg) {
   Ctx c{wg, std::mt19937(1234 + wg)};
   const unsigned per_token = PHASES * L + 1;
-  const int it_qkv = first_item(wg, G / 4), it_att = first_item(wg, 0), it_o = first_item(wg, 3 * G / 4);
-  const int it_gu = first_item(wg, G / 4), it_dn = first_item(wg, 0);
+  const bool idle = wg >= G_ROLE;
+  const int it_qkv = idle ? G : first_item(wg, G_ROLE / 4), it_att = idle ? G : first_item(wg, 0);
+  const int it_o = idle ? G : first_item(wg, 3 * G_ROLE / 4);
+  const int it_gu = idle ? G : first_item(wg, G_ROLE / 4), it_dn = idle ? G : first_item(wg, 0);
   const int RB_QKV = QKV / 16, RB_H = H / 16, RB_F = F / 16;
   for (int t = 0; t < T; ++t) {
     const unsigned tb = 1 + (unsigned)t * per_token;
@@ -153,11 +161,8 @@ void run(int wg) {
       // P1: QKV rows (needs all of x from the previous layer's down phase)
       if (it_qkv < RB_QKV) {
         if (layer > 0)
-          for (int i = 0; i < H; ++i) {
-            u64 v;
-            if (!wait_word(x[i], [&](u64 w) { return ll_tag(w) == tg - 1u; }, &v)) return;
-            expect(ll_val(v) == val(t, layer - 1, 4, i), "x (down)", t, layer, i);
-          }
+          for (int i = 0; i < H; i += 2)
+            if (!need_x2(i, tg - 1u, t, layer - 1, 4, "x (down)")) return;
         for (int r = it_qkv; r < RB_QKV; r += G)
           for (int i = r * 16; i < r * 16 + 16; ++i) qkv[i].store(ll_pack(val(t, layer, 0, i), tg), std::memory_order_relaxed);
       }
@@ -193,23 +198,16 @@ void run(int wg) {
           expect(pk_f((unsigned)v) == val(t, layer, 1, 2 * k) && pk_f((unsigned)(v >> 32)) == val(t, layer, 1, 2 * k + 1),
                  "part", t, layer, k);
         }
-        for (int i = it_o * 16; i < it_o * 16 + 16; ++i) {
-          if (layer > 0) {
-            u64 v;
-            if (!wait_word(x[i], [&](u64 w) { return ll_tag(w) == tg - 1u; }, &v)) return;
-            expect(ll_val(v) == val(t, layer - 1, 4, i), "x rows (O)", t, layer, i);
-          }
-          x[i].store(ll_pack(val(t, layer, 2, i), tg + 2u), std::memory_order_relaxed);
+        for (int i = it_o * 16; i < it_o * 16 + 16; i += 2) {
+          if (layer > 0 && !need_x2(i, tg - 1u, t, layer - 1, 4, "x rows (O)")) return;
+          put_x2(i, tg + 2u, t, layer, 2);
         }
       }
       c.jitter();
       // P4: gate/up pairs (needs all of x from the O phase)
       if (it_gu < RB_F) {
-        for (int i = 0; i < H; ++i) {
-          u64 v;
-          if (!wait_word(x[i], [&](u64 w) { return ll_tag(w) == tg + 2u; }, &v)) return;
-          expect(ll_val(v) == val(t, layer, 2, i), "x (O)", t, layer, i);
-        }
+        for (int i = 0; i < H; i += 2)
+          if (!need_x2(i, tg + 2u, t, layer, 2, "x (O)")) return;
         const unsigned t4 = tag4(tg + 3u);
         for (int r = it_gu; r < RB_F; r += G)
           for (int i = r * 8; i < r * 8 + 8; ++i)
@@ -225,22 +223,21 @@ void run(int wg) {
           expect(pk_f((unsigned)v) == val(t, layer, 3, 2 * i) && pk_f((unsigned)(v >> 32)) == val(t, layer, 3, 2 * i + 1),
                  "act", t, layer, i);
         }
-        for (int i = it_dn * 16; i < it_dn * 16 + 16; ++i) {
-          u64 v;
-          if (!wait_word(x[i], [&](u64 w) { return ll_tag(w) == tg + 2u; }, &v)) return;
-          expect(ll_val(v) == val(t, layer, 2, i), "x rows (down)", t, layer, i);
-          x[i].store(ll_pack(val(t, layer, 4, i), tg + 4u), std::memory_order_relaxed);
+        for (int i = it_dn * 16; i < it_dn * 16 + 16; i += 2) {
+          if (!need_x2(i, tg + 2u, t, layer, 2, "x rows (down)")) return;
+          put_x2(i, tg + 4u, t, layer, 4);
         }
       }
     }
     // LM head: every workgroup needs all of x from the last down phase and
     // publishes its argmax slot for this token
     const unsigned tl = tb + PHASES * L;
-    for (int i = 0; i < H; ++i) {
+    if (idle && !nogate_mode) {  // wait_last_qkv: the last layer's QKV output, full tag
       u64 v;
-      if (!wait_word(x[i], [&](u64 w) { return ll_tag(w) == tl - 1u; }, &v)) return;
-      expect(ll_val(v) == val(t, L - 1, 4, i), "x (final)", t, L, i);
+      if (!wait_word(qkv[0], [&](u64 w) { return ll_tag(w) == tl - (unsigned)PHASES; }, &v)) return;
     }
+    for (int i = 0; i < H; i += 2)
+      if (!need_x2(i, tl - 1u, t, L - 1, 4, "x (final)")) return;
     amax[(t & 1) * G + wg].store(((u64)t * 1000 + wg) << 14 | tag14(tl), std::memory_order_relaxed);
   }
 }
@@ -248,6 +245,7 @@ void run(int wg) {
 int main(int argc, char** argv) {
   drop_mode = argc > 1 && strcmp(argv[1], "drop") == 0;
   alias_mode = argc > 1 && strcmp(argv[1], "alias") == 0;
+  nogate_mode = argc > 1 && strcmp(argv[1], "nogate") == 0;
   // the host clears every tagged buffer (tag 0) when a handle is created (and
   // the packed-pair buffers again when the position moves back); consecutive
   // launches continue the tag sequence, so the T tokens here stand for any

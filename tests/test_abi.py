@@ -101,9 +101,10 @@ def test_op_argument_checks(clib):
     fake = 0x10000
     assert clib.megakernel_op_packed_bytes(16, 1024) == 16 * 1024 * 2
     assert clib.megakernel_op_packed_bytes(15, 1024) == -1
-    assert clib.megakernel_op_pack(None, 16, 256, 0, fake) == -1
+    assert clib.megakernel_op_pack(None, 16, 256, 1, fake) == -1
     assert "null" in _lib.last_error(clib)
-    assert clib.megakernel_op_pack(fake, 16, 100, 0, fake) == -1  # row-pair needs k % 256
+    assert clib.megakernel_op_pack(fake, 16, 100, 1, fake) == -1  # tiles need k % 32
+    assert clib.megakernel_op_pack(fake, 16, 256, 0, fake) == -1  # no row-pair layout any more
     assert clib.megakernel_op_pack(fake, 16, 256, 7, fake) == -1
     assert "layout" in _lib.last_error(clib)
     assert clib.megakernel_op_pack(fake, 48, 256, 2, fake) == -1  # gate/up needs rows % 32

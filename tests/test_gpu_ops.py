@@ -95,7 +95,7 @@ def _run_gemv(rows, k, kind, n_copies, n_in, reps, seed):
     g = _gen(seed)
     wrows = 2 * rows if kind == ops.GEMV_GATE_UP else rows
     mats = [_bf16((wrows, k), 0.02, g) for _ in range(n_copies)]
-    layout = ops.LAYOUT_GATE_UP if kind == ops.GEMV_GATE_UP else ops.LAYOUT_ROWPAIR
+    layout = ops.LAYOUT_GATE_UP if kind == ops.GEMV_GATE_UP else ops.LAYOUT_TILE
     buf, nb = _packed(mats, layout)
     x = torch.randn((n_in, k), generator=g)
     res = torch.randn((n_in, rows), generator=g) if kind == ops.GEMV_RESIDUAL else None
@@ -216,22 +216,23 @@ def test_op_lmhead_argmax_tiny_k():
 
 
 def test_op_pack_layouts_match_reference_layout():
-    """The packed bytes follow the documented layouts: element (row, col) of a
-    row-pair block and of a tile block sit where mk_config.h says."""
+    """The packed bytes follow the documented layout: element (row, col) of a
+    tile block sits where mk_config.h says, and the gate/up layout interleaves
+    gate block p at 2p and up block p at 2p + 1."""
     g = _gen(14)
-    rows, k = 32, 512
+    rows, k = 64, 512
     w = _bf16((rows, k), 1.0, g)
     wb = w.view(torch.int16).numpy().view(np.uint16)
     out = {}
-    for layout in (ops.LAYOUT_ROWPAIR, ops.LAYOUT_TILE):
+    for layout in (ops.LAYOUT_TILE, ops.LAYOUT_GATE_UP):
         buf, _ = _packed([w], layout)
         out[layout] = buf.cpu().numpy().view(np.uint16)
-    kc_n, kt_n = k // 256, k // 32
-    for row, col in [(0, 0), (1, 7), (2, 8), (17, 300), (31, 511), (15, 256)]:
-        rb, w_, half = row // 16, (row % 16) // 2, row % 2
-        kc, l = col // 256, half * 32 + (col % 256) // 8
-        u = ((rb * kt_n) + w_ * kc_n + kc) * 64 + l
-        assert out[ops.LAYOUT_ROWPAIR][u * 8 + col % 8] == wb[row, col]
+    kt_n, half = k // 32, rows // 2
+    for row, col in [(0, 0), (1, 7), (2, 8), (17, 300), (31, 511), (15, 256), (33, 40), (63, 511)]:
         kt, lt = col // 32, (row % 16) + 16 * ((col % 32) // 8)
-        u = (rb * kt_n + kt) * 64 + lt
+        u = ((row // 16) * kt_n + kt) * 64 + lt
         assert out[ops.LAYOUT_TILE][u * 8 + col % 8] == wb[row, col]
+        # gate rows [0, half): gate block p -> block 2p; up rows [half, rows): up block p -> 2p + 1
+        db = 2 * (row // 16) if row < half else 2 * ((row - half) // 16) + 1
+        u = (db * kt_n + kt) * 64 + lt
+        assert out[ops.LAYOUT_GATE_UP][u * 8 + col % 8] == wb[row, col]

@@ -4,12 +4,15 @@ built with ThreadSanitizer.
 The reference synchronises its phases with grid barriers
 (/root/reference/src/barriers.cuh:38-73), whose invariants are no early
 release and no lost arrival.  This build replaces them with tagged words; the
-model runs the kernel's phase structure, encodings and tag arithmetic on 16
-threads with randomised delays and checks the equivalent invariants: a
+model runs the kernel's phase structure, encodings and tag arithmetic (the
+kernel's own mk_protocol.h) on 20 threads, 4 of them with no layer role (LM
+head only), with randomised delays and checks the equivalent invariants: a
 consumer never accepts a stale or aliased word (every value is a known
 function of token, layer and index), every wait ends, no data race (TSan), and
 a lost word makes every thread unwind through the bounded-wait error path.
-A planted mistake (4-bit tags that repeat every layer) must be caught.
+Two planted mistakes must be caught: 4-bit tags that repeat every layer, and
+role-less workgroups that poll the packed residual stream without first
+waiting for the last layer's QKV output.
 """
 import os
 import shutil
@@ -55,3 +58,9 @@ def test_planted_tag_aliasing_is_caught(model):
     r = _run(model, "alias")
     assert r.returncode == 2, r.stdout + r.stderr[-2000:]
     assert "stale or wrong value" in r.stderr
+
+
+def test_planted_missing_lm_head_gate_is_caught(model):
+    r = _run(model, "nogate")
+    assert r.returncode == 2, r.stdout + r.stderr[-2000:]
+    assert "x (final)" in r.stderr
