@@ -169,7 +169,7 @@ __device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const Blk<
   }
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 0);
   blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
-  store_block(sm.red[RED_Q], p.qkv + q * 16, r, nullptr, tg);
+  store_block(sm.red[RED_Q], p.qkv + q * 16, r, tg);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 1);
   return true;
 }
@@ -181,8 +181,7 @@ __device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const Blk<S
   float r;
   if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 0);
-  blk_mma(rg, sm.vec_g, sm.red[RED_G]);
-  blk_mma(ru, sm.vec_g, sm.red[RED_U]);
+  blk_mma2(rg, ru, sm.vec_g, sm.red[RED_G], sm.red[RED_U]);
   store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, r, tag4(tg + 3u));
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 1);
   return true;
@@ -197,8 +196,7 @@ __device__ __forceinline__ bool cls_down(const Params& p, Smem<S>& sm, const Blk
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 0);
   blk_mma(rd, sm.vec_d, sm.red[RED_D]);
   __syncthreads();
-  const int t_ = ltid();
-  if (t_ < 8) down_rows<S>(p, sm, d, t_, (MODE & 2) != 0 ? p.dbg_layers : nullptr, layer, tg + 4u);
+  if (wave_id() == 0) down_rows<S>(p, sm, d, (MODE & 2) != 0 ? p.dbg_layers : nullptr, layer, tg + 4u);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 1);
   return true;
 }
@@ -214,23 +212,13 @@ __device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const Blk<S:
                      sm.xres_o))
     return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 0);
-  blk_mma(ro0, sm.vec_o, sm.red[RED_O0]);
-  if (o1 >= 0) blk_mma(ro1, sm.vec_o, sm.red[RED_O1]);
+  if (o1 >= 0) blk_mma2(ro0, ro1, sm.vec_o, sm.red[RED_O0], sm.red[RED_O1]);
+  else blk_mma(ro0, sm.vec_o, sm.red[RED_O0]);
   __syncthreads();
-  // threads 0..7: rows 2i, 2i + 1 of block o0, 8..15: of block o1 (one store instruction)
-  const int t_ = ltid(), i = t_ & 7;
-  if (t_ < 8 || (t_ < 16 && o1 >= 0)) {
-    const int ob = t_ < 8 ? o0 : o1, xr = t_ < 8 ? 0 : 16;
-    const float* red = sm.red[t_ < 8 ? RED_O0 : RED_O1];
-    float v[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int r = 2 * i + e;
-      const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, ob * 16 + r) : sm.xres_o[xr + r];
-      v[e] = xo + red_sum(red, r);
-    }
-    put_x2(p, ob, i, v[0], v[1], tg + 2u);
-  }
+  // wave 0: block o0, wave 1: block o1
+  const int w_ = wave_id();
+  if (w_ == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, o0, layer, tok, tg + 2u);
+  else if (w_ == 1 && o1 >= 0) o_rows<S>(p, sm.red[RED_O1], sm.xres_o + 16, o1, layer, tok, tg + 2u);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 1);
   return true;
 }

@@ -193,32 +193,84 @@ __device__ __forceinline__ void blk_forget(Blk<KC>& b) {
 // on its own B column, and only columns 0 and 1 are read.  Lanes 0, 16, 32,
 // 48 then hold rows 4 (l >> 4) .. +3 of both columns (lanes l and l + 1), and
 // write their hi + lo sums -- the wave's share of the 16 row sums -- to
-// red[wave][16].  No barrier: red_sum after one reads them.
+// red[wave][16].  No barrier: the row sums are read after one (red_row4).
+//
+// NB blocks against the same input share the B loads; each block's chain of
+// KC products runs as two interleaved accumulators (even / odd k-steps), so
+// the matrix core has independent products in flight.
 template <int KC>
-__device__ __forceinline__ void blk_mma(const Blk<KC>& b, const float* vec, float* red) {
+__device__ __forceinline__ void mma_b_load(u32x4 (&bx)[KC], const float* vec) {
   const unsigned l = lane_id();
-  const int w = wave_id();
-  const uint32_t* xs = reinterpret_cast<const uint32_t*>(vec) + (w * KC * 4 + (int)(l >> 4)) * 8 + (int)(l & 1u) * 4;
-  u32x4 bx[KC];
+  const uint32_t* xs = reinterpret_cast<const uint32_t*>(vec) + (wave_id() * KC * 4 + (int)(l >> 4)) * 8 + (int)(l & 1u) * 4;
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc) asm volatile("" : "=v"(bx[kc]));  // left as is in columns 2..15
+  for (int kc = 0; kc < KC; ++kc) asm volatile("" : "=v"(bx[kc]));  // columns 2..15: left as they are
   if ((l & 14u) == 0u) {  // B columns 0 and 1
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) bx[kc] = *reinterpret_cast<const u32x4*>(xs + kc * 32);
   }
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int kc = 0; kc < KC; ++kc)
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b.w[kc]), __builtin_bit_cast(bf16x8, bx[kc]),
-                                                  acc, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+__device__ __forceinline__ void mma_share_out(f32x4 a0, f32x4 a1, float* red) {
+  const unsigned l = lane_id();
   f32x4 s;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) s[i] = acc[i] + dpp_sel<DPP_XOR1>(acc[i]);  // column 0 + column 1
-  if ((l & 15u) == 0u) *reinterpret_cast<f32x4*>(red + w * 16 + 4 * (int)(l >> 4)) = s;
+  for (int i = 0; i < 4; ++i) {
+    const float v = a0[i] + a1[i];
+    s[i] = v + dpp_sel<DPP_XOR1>(v);  // column 0 + column 1
+  }
+  if ((l & 15u) == 0u) *reinterpret_cast<f32x4*>(red + wave_id() * 16 + 4 * (int)(l >> 4)) = s;
+}
+template <int KC>
+__device__ __forceinline__ void blk_mma(const Blk<KC>& b, const float* vec, float* red) {
+  u32x4 bx[KC];
+  mma_b_load<KC>(bx, vec);
+  f32x4 e = f32x4{0.f, 0.f, 0.f, 0.f}, o = e;
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    if (kc & 1) o = mma(b.w[kc], bx[kc], o);
+    else e = mma(b.w[kc], bx[kc], e);
+  }
+  mma_share_out(e, o, red);
+}
+template <int KC>
+__device__ __forceinline__ void blk_mma2(const Blk<KC>& b0, const Blk<KC>& b1, const float* vec, float* red0,
+                                         float* red1) {
+  u32x4 bx[KC];
+  mma_b_load<KC>(bx, vec);
+  f32x4 e0 = f32x4{0.f, 0.f, 0.f, 0.f}, o0 = e0, e1 = e0, o1 = e0;
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    if (kc & 1) {
+      o0 = mma(b0.w[kc], bx[kc], o0);
+      o1 = mma(b1.w[kc], bx[kc], o1);
+    } else {
+      e0 = mma(b0.w[kc], bx[kc], e0);
+      e1 = mma(b1.w[kc], bx[kc], e1);
+    }
+  }
+  mma_share_out(e0, o0, red0);
+  mma_share_out(e1, o1, red1);
 }
 
-// Row t of a block from the NW wave shares in red (after a barrier that
-// follows blk_mma), summed in wave order.
+// Row sums of a block product, in one wave (after the barrier that follows
+// blk_mma): lane l adds the shares of waves 2 (l & 3) and 2 (l & 3) + 1 of row
+// l >> 2, then the 4 lanes of the row exchange partials (DPP), so all four end
+// with the same total, summed in a fixed order.
+__device__ __forceinline__ float red_row4(const float* red, unsigned l) {
+  const int r = (int)(l >> 2), w = 2 * (int)(l & 3u);
+  float v = red[w * 16 + r] + red[(w + 1) * 16 + r];
+  v += dpp_sel<DPP_XOR1>(v);
+  v += dpp_sel<DPP_XOR2>(v);
+  return v;
+}
+// Value of lane l + 4 (row r + 1 of red_row4's layout, inside a row of 16 lanes).
+constexpr int DPP_ROW_SHL4 = 0x104;
+
+// Row t of a block from the NW wave shares in red, summed in wave order (one
+// thread per row; off the decode path).
 __device__ __forceinline__ float red_sum(const float* red, int t) {
   float y = 0.f;
 #pragma unroll
@@ -226,30 +278,32 @@ __device__ __forceinline__ float red_sum(const float* red, int t) {
   return y;
 }
 
-// The 16 rows of a block (red, from blk_mma) times `scale`, plus res[t] unless
-// res is null, published by threads 0..15 as one 128-byte store.  One barrier.
-__device__ __forceinline__ void store_block(const float* red, u64* dst16, float scale, const float* res,
-                                            unsigned tag) {
+// SiLU(g) * u (reference utils.cuh:57-61, x / (1 + exp(-x)); the hardware
+// reciprocal, relative error ~1 ulp, in place of the division).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
+// Epilogues, one barrier each, run by wave 0 (lane l: row l >> 2).
+// QKV block: the 16 rows times `scale`, full tagged words.
+__device__ __forceinline__ void store_block(const float* red, u64* dst16, float scale, unsigned tag) {
   __syncthreads();
-  const int t_ = ltid();
-  if (t_ < 16) {
-    const float y = red_sum(red, t_) * scale;
-    ll_put(dst16 + t_, ll_pack(res ? res[t_] + y : y, tag));
+  if (wave_id() == 0) {
+    const unsigned l = lane_id();
+    const float y = red_row4(red, l) * scale;
+    if ((l & 3u) == 0u) ll_put(dst16 + (l >> 2), ll_pack(y, tag));
   }
 }
 
-// SiLU(g) * u (reference utils.cuh:47-61).
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
-
 // Gate/up pair: SiLU(g r) * (u r) of the 16 rows (gate shares in rg, up
-// shares in ru), published as 8 packed-pair words.  One barrier.
+// shares in ru), published as 8 packed-pair words.
 __device__ __forceinline__ void store_block_gu(const float* rg, const float* ru, u64* dst8, float r, unsigned t4) {
   __syncthreads();
-  const int t_ = ltid();
-  if (t_ < 8) {
-    const float a = silu_mul(red_sum(rg, 2 * t_) * r, red_sum(ru, 2 * t_) * r);
-    const float b = silu_mul(red_sum(rg, 2 * t_ + 1) * r, red_sum(ru, 2 * t_ + 1) * r);
-    ll_put(dst8 + t_, pk_pack(a, b, t4));
+  if (wave_id() == 0) {
+    const unsigned l = lane_id();
+    const float a = silu_mul(red_row4(rg, l) * r, red_row4(ru, l) * r);
+    const float b = dpp_sel<DPP_ROW_SHL4>(a);  // the next row
+    if ((l & 7u) == 0u) ll_put(dst8 + (l >> 3), pk_pack(a, b, t4));
   }
 }
 
@@ -473,39 +527,31 @@ __device__ __forceinline__ bool wait_last_qkv(const Params& p, unsigned tl) {
   return !block_failed(failed);
 }
 
-// The x words of rows 2i, 2i + 1 of block blk (values a, b), tag of the phase.
-__device__ __forceinline__ void put_x2(const Params& p, int blk, int i, float a, float b, unsigned tag) {
-  ll_put(p.x + blk * 8 + i, pk_pack(a, b, tag4(tag)));
+// O block blk (shares in red) plus its residual rows xres, or the embedding
+// row at layer 0, -> the block's 8 x words (packed pairs, tag of the phase).
+// One wave (red_row4 layout).
+template <class S>
+__device__ __forceinline__ void o_rows(const Params& p, const float* red, const float* xres, int blk, int layer,
+                                       int tok, unsigned tag) {
+  const unsigned l = lane_id();
+  const int r = (int)(l >> 2);
+  const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, blk * 16 + r) : xres[r];
+  const float a = xo + red_row4(red, l);
+  const float b = dpp_sel<DPP_ROW_SHL4>(a);  // the next row
+  if ((l & 7u) == 0u) ll_put(p.x + blk * 8 + (l >> 3), pk_pack(a, b, tag4(tag)));
 }
 
-// O block blk (shares in red[RED_O0], residual rows in xres_o, or the
-// embedding row at layer 0) -> x rows 2i, 2i + 1 (thread i < 8).
+// Down block blk (shares in red[RED_D]) plus the residual rows xres_d -> the
+// block's 8 x words; dbg (layer dumps) unless null.  One wave.
 template <class S>
-__device__ __forceinline__ void o_rows(const Params& p, Smem<S>& sm, int blk, int i, int layer, int tok,
-                                       unsigned tag) {
-  float v[2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int r = 2 * i + e;
-    const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, blk * 16 + r) : sm.xres_o[r];
-    v[e] = xo + red_sum(sm.red[RED_O0], r);
-  }
-  put_x2(p, blk, i, v[0], v[1], tag);
-}
-
-// Down block blk (shares in red[RED_D]) + residual rows xres_d -> x rows 2i,
-// 2i + 1 (thread i < 8); dbg (layer dumps) unless null.
-template <class S>
-__device__ __forceinline__ void down_rows(const Params& p, Smem<S>& sm, int blk, int i, float* dbg, int layer,
+__device__ __forceinline__ void down_rows(const Params& p, Smem<S>& sm, int blk, float* dbg, int layer,
                                           unsigned tag) {
-  float v[2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int r = 2 * i + e;
-    v[e] = sm.xres_d[r] + red_sum(sm.red[RED_D], r);
-    if (dbg) dbg[(long long)(layer + 1) * S::H + blk * 16 + r] = v[e];
-  }
-  put_x2(p, blk, i, v[0], v[1], tag);
+  const unsigned l = lane_id();
+  const int r = (int)(l >> 2);
+  const float a = sm.xres_d[r] + red_row4(sm.red[RED_D], l);
+  if (dbg && (l & 3u) == 0u) dbg[(long long)(layer + 1) * S::H + blk * 16 + r] = a;
+  const float b = dpp_sel<DPP_ROW_SHL4>(a);
+  if ((l & 7u) == 0u) ll_put(p.x + blk * 8 + (l >> 3), pk_pack(a, b, tag4(tag)));
 }
 
 // Work item i of a phase runs on workgroup (i + off) mod G.
@@ -1329,14 +1375,14 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         if constexpr (DBG) trace_mark(p, t, slot + 0, 0);
         {  // the prefetched block
           blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
-          store_block(sm.red[RED_Q], p.qkv + it_qkv * 16, r, nullptr, tg);
+          store_block(sm.red[RED_Q], p.qkv + it_qkv * 16, r, tg);
           evt(p, t, layer, EV_QKV_STORED);
         }
         for (int rb = it_qkv + G; rb < S::RB_QKV; rb += G) {  // grids smaller than the block count
           blk_load(rq, wl + S::OFF_QKV + (long long)rb * S::KT_H * 64);
           __syncthreads();  // the previous block's shares are summed
           blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
-          store_block(sm.red[RED_Q], p.qkv + rb * 16, r, nullptr, tg);
+          store_block(sm.red[RED_Q], p.qkv + rb * 16, r, tg);
         }
         if constexpr (DBG) trace_mark(p, t, slot + 0, 1);
       }
@@ -1390,7 +1436,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         evt(p, t, layer, EV_O_READY);
         blk_mma(ro, sm.vec_o, sm.red[RED_O0]);
         __syncthreads();
-        if (tid < 8) o_rows<S>(p, sm, it_o, tid, layer, tok, tg + 2u);
+        if (wave_id() == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, it_o, layer, tok, tg + 2u);
         evt(p, t, layer, EV_O_STORED);
         if constexpr (DBG) trace_mark(p, t, slot + 2, 1);
       }
@@ -1400,7 +1446,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         __syncthreads();  // the previous block's shares are summed
         blk_mma(ro, sm.vec_o, sm.red[RED_O0]);
         __syncthreads();
-        if (tid < 8) o_rows<S>(p, sm, rb, tid, layer, tok, tg + 2u);
+        if (wave_id() == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, rb, layer, tok, tg + 2u);
       }
       if (kv_at == 3) prefetch_kv();
       // ---------------- P4: gate/up + SiLU (prefetch: down)
@@ -1411,8 +1457,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return;
         if constexpr (DBG) trace_mark(p, t, slot + 3, 0);
         {  // the prefetched block pair
-          blk_mma(rg, sm.vec_g, sm.red[RED_G]);
-          blk_mma(ru, sm.vec_g, sm.red[RED_U]);
+          blk_mma2(rg, ru, sm.vec_g, sm.red[RED_G], sm.red[RED_U]);
           store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + it_gu * 8, r, tag4(tg + 3u));
           evt(p, t, layer, EV_GU_STORED);
         }
@@ -1421,8 +1466,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
           blk_load(rg, gp);
           blk_load(ru, gp + S::KT_H * 64);
           __syncthreads();  // the previous pair's shares are summed
-          blk_mma(rg, sm.vec_g, sm.red[RED_G]);
-          blk_mma(ru, sm.vec_g, sm.red[RED_U]);
+          blk_mma2(rg, ru, sm.vec_g, sm.red[RED_G], sm.red[RED_U]);
           store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + pr * 8, r, tag4(tg + 3u));
         }
         if constexpr (DBG) trace_mark(p, t, slot + 3, 1);
@@ -1442,7 +1486,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         evt(p, t, layer, EV_DN_READY);
         blk_mma(rd, sm.vec_d, sm.red[RED_D]);
         __syncthreads();
-        if (tid < 8) down_rows<S>(p, sm, it_dn, tid, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
+        if (wave_id() == 0) down_rows<S>(p, sm, it_dn, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
         evt(p, t, layer, EV_DN_STORED);
         if constexpr (DBG) trace_mark(p, t, slot + 4, 1);
       }
@@ -1452,7 +1496,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         __syncthreads();  // the previous block's shares are summed
         blk_mma(rd, sm.vec_d, sm.red[RED_D]);
         __syncthreads();
-        if (tid < 8) down_rows<S>(p, sm, rb, tid, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
+        if (wave_id() == 0) down_rows<S>(p, sm, rb, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
       }
       if (kv_at == 5) prefetch_kv();
     }
