@@ -525,7 +525,11 @@ def main():
         with open(args.traffic_json) as f:
             tj = json.load(f)
         if tj.get("ctx") == args.ctx and tj.get("tokens") == K:
-            traffic = tj.get("hbm_bytes_per_launch")
+            traffic = tj.get("hbm_bytes_per_launch")  # measured for exactly this launch
+        elif tj.get("ctx") == args.ctx and tj.get("traffic_over_algorithmic"):
+            # same context, another token count: the measured traffic / algorithmic
+            # ratio applied to this launch's algorithmic bytes
+            traffic = round(tj["traffic_over_algorithmic"] * nbytes)
 
     if args.trace:
         trace_summary(eng, shape, args, info)

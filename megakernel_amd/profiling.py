@@ -7,6 +7,9 @@ Two jobs, both on files rocprofv3 wrote (``--output-format csv``):
 * ``launches``: per-launch durations from ``*_kernel_trace.csv``, grouped by
   kernel and grid size (the operator microbench launches each op kernel both
   with many instances and with one);
+* ``counters``: per-launch and per-token totals of other ``--pmc`` counters
+  (L2 hits / misses, wave waits, instruction cache) of the decode launch, as
+  a markdown table with the derived ratios;
 * ``traffic``: combine four ``--pmc`` runs -- FETCH_SIZE and WRITE_SIZE of the
   decode launch, and the same two counters of a plain device copy of known
   size -- into HBM bytes per decode launch.  Each counter is scaled by
@@ -17,6 +20,7 @@ Two jobs, both on files rocprofv3 wrote (``--output-format csv``):
 Usage:
   python -m megakernel_amd.profiling stats STATS.csv --command "..." -o OUT.txt
   python -m megakernel_amd.profiling launches TRACE.csv --match mk::ops:: --command "..." -o OUT.txt
+  python -m megakernel_amd.profiling counters A.csv [B.csv ...] --tokens 256 --command "..." -o OUT.md
   python -m megakernel_amd.profiling traffic --decode-fetch A.csv --decode-write B.csv \
       --copy-fetch C.csv --copy-write D.csv --copy-bytes N --ctx 1024 --tokens 256 \
       --algorithmic-bytes X -o profiles/decode_traffic.json
@@ -29,7 +33,7 @@ import json
 import statistics
 import sys
 
-DECODE_KERNEL = "decode_kernel"
+DECODE_KERNELS = ("decode_kernel", "decode_cls_kernel")  # spread / class-specialised decode kernels
 
 
 def _rows(path: str) -> list[dict]:
@@ -48,12 +52,14 @@ def kernel_stats(path: str) -> list[dict]:
     return out
 
 
-def counter_values(path: str, counter: str, kernel_substr: str) -> list[float]:
+def counter_values(path: str, counter: str, kernel_substr) -> list[float]:
     """Per-dispatch values of one counter for kernels whose name contains
-    kernel_substr (summed over rows of the same dispatch)."""
+    kernel_substr (a string or a tuple of alternatives; summed over rows of the
+    same dispatch)."""
+    subs = (kernel_substr,) if isinstance(kernel_substr, str) else tuple(kernel_substr)
     acc: dict[str, float] = {}
     for r in _rows(path):
-        if r.get("Counter_Name") != counter or kernel_substr not in r.get("Kernel_Name", ""):
+        if r.get("Counter_Name") != counter or not any(k in r.get("Kernel_Name", "") for k in subs):
             continue
         key = r.get("Dispatch_Id") or r.get("Correlation_Id") or str(len(acc))
         acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
@@ -94,8 +100,8 @@ def launch_text(path: str, cmd: str, substr: str) -> str:
 
 
 def traffic(args) -> dict:
-    dec_f = counter_values(args.decode_fetch, "FETCH_SIZE", DECODE_KERNEL)
-    dec_w = counter_values(args.decode_write, "WRITE_SIZE", DECODE_KERNEL)
+    dec_f = counter_values(args.decode_fetch, "FETCH_SIZE", DECODE_KERNELS)
+    dec_w = counter_values(args.decode_write, "WRITE_SIZE", DECODE_KERNELS)
     cp_f = counter_values(args.copy_fetch, "FETCH_SIZE", args.copy_kernel)
     cp_w = counter_values(args.copy_write, "WRITE_SIZE", args.copy_kernel)
     if not (dec_f and dec_w and cp_f and cp_w):
@@ -117,9 +123,41 @@ def traffic(args) -> dict:
         "fetch_scale_bytes_per_unit": scale_f, "write_scale_bytes_per_unit": scale_w,
         "fetch_bytes_per_launch": fetch_b, "write_bytes_per_launch": write_b,
         "hbm_bytes_per_launch": fetch_b + write_b,
+        "hbm_bytes_per_token": (fetch_b + write_b) / args.tokens,
         "algorithmic_bytes_per_launch": args.algorithmic_bytes,
         "traffic_over_algorithmic": (fetch_b + write_b) / args.algorithmic_bytes if args.algorithmic_bytes else None,
     }
+
+
+# derived quantities of the counter summary: (label, numerator, denominator)
+DERIVED = [
+    ("L2 (TCC) hit rate", ("TCC_HIT_sum",), ("TCC_HIT_sum", "TCC_MISS_sum")),
+    ("wave-cycles waiting on anything / wave-cycles", ("SQ_WAIT_ANY",), ("SQ_WAVE_CYCLES",)),
+    ("wave-cycles waiting for issue / wave-cycles", ("SQ_WAIT_INST_ANY",), ("SQ_WAVE_CYCLES",)),
+    ("instruction-cache hit rate", ("SQC_ICACHE_HITS",), ("SQC_ICACHE_HITS", "SQC_ICACHE_MISSES")),
+]
+
+
+def counters_text(paths: list[str], cmd: str, tokens: int) -> str:
+    """Per-launch totals of every counter in the given --pmc csv files for the
+    largest decode dispatch, per token, and the derived ratios above."""
+    vals: dict[str, float] = {}
+    for p in paths:
+        names = sorted({r["Counter_Name"] for r in _rows(p)})
+        for c in names:
+            v = counter_values(p, c, DECODE_KERNELS)
+            if v:
+                vals[c] = max(v)
+    lines = [f"# command: {cmd}", "", f"decode launch of {tokens} tokens (largest decode dispatch of each pass)", "",
+             "| counter | per launch | per token |", "|---|---|---|"]
+    for c in sorted(vals):
+        lines.append(f"| {c} | {vals[c]:,.0f} | {vals[c] / tokens:,.1f} |")
+    lines += ["", "| derived | value |", "|---|---|"]
+    for label, num, den in DERIVED:
+        if all(k in vals for k in num + den):
+            n, d = sum(vals[k] for k in num), sum(vals[k] for k in den)
+            lines.append(f"| {label} | {n / d:.4f} |")
+    return "\n".join(lines) + "\n"
 
 
 def main(argv=None):
@@ -144,9 +182,20 @@ def main(argv=None):
     t.add_argument("--tokens", type=int, required=True)
     t.add_argument("--algorithmic-bytes", type=float, default=0.0)
     t.add_argument("-o", "--out", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("csv", nargs="+", help="counter_collection.csv of one or more --pmc passes")
+    c.add_argument("--command", required=True, help="the commands that produced the csv files")
+    c.add_argument("--tokens", type=int, required=True)
+    c.add_argument("-o", "--out")
     a = ap.parse_args(argv)
     if a.what == "stats":
         txt = stats_text(a.csv, a.command, a.top)
+        if a.out:
+            with open(a.out, "w") as f:
+                f.write(txt)
+        sys.stdout.write(txt)
+    elif a.what == "counters":
+        txt = counters_text(a.csv, a.command, a.tokens)
         if a.out:
             with open(a.out, "w") as f:
                 f.write(txt)
