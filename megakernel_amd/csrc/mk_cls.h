@@ -80,9 +80,33 @@ __device__ __forceinline__ bool cls_token_start(const Params& p, Smem<S>& sm, in
 // rows have been scored and its argmax word published: issued before the
 // LM head's wait it would delay that wait, issued before the scoring it would
 // delay this workgroup's share of the LM-head stream.
+// LM head warm start: a workgroup's first LM-head weights do not depend on
+// the final x, so each wave loads the first LM_U units of its first block
+// into registers right after the workgroup's last-layer role (the registers
+// of the next layer's weights are free then); the LM head's first step then
+// starts from registers instead of a cold HBM round trip.
+constexpr int LM_U = 16;  // 1 KiB units in flight per wave in the LM-head loop
+struct LmWarm {
+  u32x4 w[LM_U];
+};
+template <class S, int MODE>
+__device__ __forceinline__ void lm_warm_load(const Params& p, LmWarm& lw) {
+  constexpr bool F8 = (MODE & 4) != 0;
+  constexpr int E = F8 ? 16 : 8, KT = S::H / (4 * E);
+  const int G = gridDim.x, wg = blockIdx.x;
+  const long long nb = p.vocab / 16;
+  const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G, b = b0 + wave_id();
+  if (b >= b1) return;
+  const auto rs = make_rsrc((F8 ? p.lmhead8 : p.lmhead) + b * KT * 64);
+  const unsigned lo = lane_id();
+#pragma unroll
+  for (int u = 0; u < LM_U; ++u)
+    if (u < KT) lw.w[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lo * 16u, (unsigned)u * 1024u, MK_LMHEAD_AUX);
+}
+
 template <class S, int MODE, class AfterPoll>
 __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t, unsigned tb, AfterPoll after_poll,
-                                            bool idle = false) {
+                                            const LmWarm& lw, bool idle = false) {
   constexpr bool DBG = (MODE & 2) != 0, F8 = (MODE & 4) != 0;
   const int G = gridDim.x, wg = blockIdx.x;
   const int tid = ltid(), w = tid / kWave, l = tid % kWave;
@@ -103,12 +127,15 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
     const float* hv = sm.vec_l + (lo >> 4) * E;
     const auto rs = make_rsrc((F8 ? p.lmhead8 : p.lmhead) + b * KT * 64);
     float acc = 0.f;
-    constexpr int U = 16;
+    constexpr int U = LM_U;
     const bool keep = (b - b0) * 100 < (b1 - b0) * MK_LMHEAD_KEEP_PCT;
 #pragma unroll 1
     for (int k0 = 0; k0 < KT; k0 += U) {
       u32x4 wv[U];
-      if (keep) {
+      if (b == b0 + wv_ && k0 == 0) {  // loaded by lm_warm_load
+#pragma unroll
+        for (int u = 0; u < U; ++u) wv[u] = lw.w[u];
+      } else if (keep) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
           if (k0 + u < KT)
@@ -377,13 +404,15 @@ __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int*
         }
       }
     }
+    LmWarm lw;
+    lm_warm_load<S, MODE>(p, lw);
     if (!cls_lm_head<S, MODE>(p, sm, t, tb, [&]() {
           if (o0 >= 0) ld_o<S>(ro, p, 0, o0);
           if (nxt.on) {
             kv_load<S>(rkv, p, 0, g, nxt.t0 / 32, (nxt.t1 - nxt.t0 + 31) / 32, wave_id());
             gain_load_qk<S>(rkv, p, 0);
           }
-        }))
+        }, lw))
       return;
     if constexpr ((MODE & 2) != 0) trace_end(p, t);
   }
@@ -418,10 +447,12 @@ __device__ __forceinline__ void run_qg(const Params& p, Smem<S>& sm, const int* 
         }
       }
     }
+    LmWarm lw;
+    lm_warm_load<S, MODE>(p, lw);
     if (!cls_lm_head<S, MODE>(p, sm, t, tb, [&]() {
           if constexpr (HAS_Q) ld_qkv<S>(rq, gq, p, 0, q);
           else ld_gu<S>(rg, ru, gf, p, 0, gi);
-        }))
+        }, lw))
       return;
     if constexpr ((MODE & 2) != 0) trace_end(p, t);
   }
@@ -463,11 +494,13 @@ __device__ __forceinline__ void run_down(const Params& p, Smem<S>& sm, const int
         ld_down<S>(rd, p, nl, d, u);
       }
     }
+    LmWarm lw;
+    lm_warm_load<S, MODE>(p, lw);
     if (!cls_lm_head<S, MODE>(p, sm, t, tb, [&]() {
           if constexpr (PARTNER == CLS_DG) ld_gu<S>(rg, ru, gf, p, 0, gi);
           if constexpr (PARTNER == CLS_DO) ld_o<S>(ro, p, 0, o0);
           ld_down<S>(rd, p, 0, d);
-        }))
+        }, lw))
       return;
     if constexpr ((MODE & 2) != 0) trace_end(p, t);
   }
@@ -495,10 +528,12 @@ __device__ __forceinline__ void run_o(const Params& p, Smem<S>& sm, const int* r
         if (o1 >= 0) ld_o<S>(rb, p, next_layer(p, layer), o1, pace_units(p, PACE_O));
       }
     }
+    LmWarm lw;
+    lm_warm_load<S, MODE>(p, lw);
     if (!cls_lm_head<S, MODE>(p, sm, t, tb, [&]() {
           ld_o<S>(ra, p, 0, o0);
           if (o1 >= 0) ld_o<S>(rb, p, 0, o1);
-        }))
+        }, lw))
       return;
     if constexpr ((MODE & 2) != 0) trace_end(p, t);
   }
@@ -512,7 +547,9 @@ __device__ __forceinline__ void run_idle(const Params& p, Smem<S>& sm) {
     if constexpr ((MODE & 2) != 0) trace_begin(p, t);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
     if (!cls_token_start<S, MODE>(p, sm, t, tb, false, false, &tok)) return;
-    if (!cls_lm_head<S, MODE>(p, sm, t, tb, []() {}, true)) return;
+    LmWarm lw;
+    lm_warm_load<S, MODE>(p, lw);
+    if (!cls_lm_head<S, MODE>(p, sm, t, tb, []() {}, lw, true)) return;
     if constexpr ((MODE & 2) != 0) trace_end(p, t);
   }
 }
