@@ -70,33 +70,53 @@ def parse():
     return ap.parse_args()
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(dw, shape, seed: int, budget_s: float) -> dict:
     """Oracle (PyTorch, fp32 activations, bf16 weights upcast once to fp32) on
-    the host cores: BASELINE configs[0] = 16-token prompt then greedy decode,
-    timed over as many decode tokens as fit in `budget_s` (at least 3)."""
+    the host cores: torch runs on every core of this
+    process's affinity mask; BASELINE configs[0] = 16-token prompt then greedy
+    decode, three samples of up to budget_s / 3 seconds (at least 3 tokens
+    each), the median reported."""
     import torch
 
     from oracle import layout as olayout
     from oracle import qwen3_ref, synth
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     osh = olayout.Shape(shape.hidden, shape.n_q_heads, shape.n_kv_heads, shape.head_dim, shape.ffn,
                         shape.n_layers, shape.vocab)
     bits = qwen3_ref.unpack_flat(osh, dw.to_host(), dw.layout.offsets)
-    orc = qwen3_ref.Qwen3Oracle(osh, bits, 128)
+    orc = qwen3_ref.Qwen3Oracle(osh, bits, 256)
     prompt = synth.prompt_tokens(seed, 16, shape.vocab)
     for t in prompt[:-1]:
         orc.step(t)
     tok = orc.step(prompt[-1])["token"]
     tok = orc.step(tok)["token"]  # warm-up decode steps
     tok = orc.step(tok)["token"]
-    n, t0 = 0, time.perf_counter()
-    while n < 3 or (time.perf_counter() - t0 < budget_s and n < 64):
-        tok = orc.step(tok)["token"]
-        n += 1
-    dt = time.perf_counter() - t0
-    return {"value": n / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"BASELINE configs[0] (full 28-layer model, 16-token prompt), {n} greedy decode "
-                      f"tokens at positions 18..{17 + n} timed after 2 warm-up tokens; "
-                      "PyTorch CPU oracle, bf16 weights upcast to fp32"}
+    rates, counts = [], []
+    for _ in range(3):
+        n, t0 = 0, time.perf_counter()
+        while n < 3 or (time.perf_counter() - t0 < budget_s / 3 and n < 64):
+            tok = orc.step(tok)["token"]
+            n += 1
+        rates.append(n / (time.perf_counter() - t0))
+        counts.append(n)
+    first = 18
+    return {"value": round(statistics.median(rates), 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "cpu": _cpu_model(), "samples": [round(r, 3) for r in rates],
+            "sample": f"BASELINE configs[0] (full 28-layer model, 16-token prompt), greedy decode after 2 warm-up "
+                      f"tokens: three timed runs of {counts} tokens from position {first}, median; "
+                      f"PyTorch CPU oracle, bf16 weights upcast to fp32, torch.set_num_threads({cores})"}
 
 
 def trace_summary(eng, shape, args, info):
