@@ -46,6 +46,8 @@ def parse():
                     help="FP8 (e4m3) KV cache with a power-of-two scale per K / V row")
     ap.add_argument("--lmhead-fp8", action="store_true",
                     help="stream the FP8 (e4m3, power-of-two row scales) copy of the LM head")
+    ap.add_argument("--layer-fp8", action="store_true",
+                    help="stream fp8 e4m3 copies of the layer matrices (power-of-two row scales; decode only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
     ap.add_argument("--trace", action="store_true", help="print a per-phase critical-path summary")
@@ -471,6 +473,9 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
+    if args.layer_fp8 and (args.batch or args.ops or args.prefill):
+        print(json.dumps({"error": "--layer-fp8 applies to the batch-1 decode line only"}))
+        sys.exit(2)
     if args.prefill:
         if args.gpus != 1:
             print(json.dumps({"error": "this build runs on one GPU only"}))
@@ -510,6 +515,8 @@ def main():
         eng.set_lmhead_fp8(True)
     if args.kv_fp8:
         eng.set_kv_fp8(True)
+    if args.layer_fp8:
+        eng.set_layer_fp8(True)
     from megakernel_amd import _lib
     eng.set_decode_kernel(_lib.KERNEL_SPREAD if args.kernel == "spread" else _lib.KERNEL_AUTO)
     info = launcher.detect_gpu()
@@ -539,9 +546,14 @@ def main():
     if args.kv_fp8:  # per position: 1 byte per K / V value plus a 4-byte scale per row
         kv8 = shape.kv_bytes_per_pos // 2 + 2 * 4 * shape.n_kv_heads * shape.n_layers
         nbytes -= sum((shape.kv_bytes_per_pos - kv8) * (args.ctx + i + 2) for i in range(K))
+    if args.layer_fp8:  # 1 byte per layer weight instead of 2, plus a 4-byte scale per matrix row
+        q, kv = shape.n_q_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim
+        mats = (q + 2 * kv) * shape.hidden + shape.hidden * q + 3 * shape.ffn * shape.hidden
+        rows = (q + 2 * kv) + 2 * shape.hidden + 2 * shape.ffn
+        nbytes -= K * shape.n_layers * (mats - 4 * rows)
     achieved = nbytes / kern / 1e9
     traffic = None
-    if os.path.exists(args.traffic_json) and not args.lmhead_fp8 and not args.kv_fp8:
+    if os.path.exists(args.traffic_json) and not (args.lmhead_fp8 or args.kv_fp8 or args.layer_fp8):
         with open(args.traffic_json) as f:
             tj = json.load(f)
         if tj.get("ctx") == args.ctx and tj.get("tokens") == K:
@@ -570,7 +582,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" + "".join(f" ({w} fp8 e4m3)" for w, on in (("LM head", args.lmhead_fp8),
+        "dtype": "bf16" + "".join(f" ({w} fp8 e4m3)" for w, on in (("layers", args.layer_fp8),
+                                                                     ("LM head", args.lmhead_fp8),
                                                                      ("KV cache", args.kv_fp8)) if on),
         "data": "synthetic",
         "config": {"workload": f"Qwen3-0.6B-shaped batch-1 greedy decode, KV prefilled to {args.ctx}, "
@@ -578,6 +591,8 @@ def main():
                    "ctx": args.ctx, "tokens": K, "batch": 1, "layers": shape.n_layers,
                    "hidden": shape.hidden, "heads": "16q/8kv x 64", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "bf16 N(0,0.02) (Irwin-Hall(4) approx), unit norm gains" +
+                              ("; layer matrices streamed as fp8 e4m3 with power-of-two row scales"
+                               if args.layer_fp8 else "") +
                               ("; LM head streamed as fp8 e4m3 with power-of-two row scales" if args.lmhead_fp8 else "") +
                               ("; KV cache fp8 e4m3, power-of-two scale per K / V row" if args.kv_fp8 else ""),
                    "accumulation": "fp32", "reps": args.reps, "grid": grid,

@@ -183,6 +183,29 @@ int megakernel_set_kv_fp8(void* handle, int enable);
  * (validation).  -1 when it has not been built. */
 int megakernel_get_lmhead_fp8(void* handle, unsigned char* codes, float* scales);
 
+/* FP8 layer weights (no counterpart in the reference kernel, which plans FP8
+ * weights in RESEARCH.md:434-436,463).  enable = 1 builds, once, an OCP e4m3
+ * copy of every layer's QKV, O, gate, up and down matrices with one
+ * power-of-two scale per row (the quantisation of megakernel_set_lmhead_fp8)
+ * and makes decode launches stream it: 1 byte per weight instead of 2 for 68 %
+ * of the bytes of a token.  Norm gains, the embedding and the prefill context
+ * keep bf16.  Served by the class-specialised kernel only: a launch that needs
+ * the spread kernel (megakernel_set_decode_kernel(MK_KERNEL_SPREAD), or more
+ * attention splits per kv head than the class kernel's role tables hold)
+ * returns -1 while it is on.  enable = 0 returns to bf16.  Returns 0 or -1. */
+int megakernel_set_layer_fp8(void* handle, int enable);
+
+/* One FP8 layer matrix as built: codes[R * K] row-major e4m3 bytes and
+ * scales[R] of matrix `which` of layer `layer` (validation): QKV = the fused
+ * q | k | v rows [QD + 2 KVD][H], O [H][QD], GATE / UP [F][H], DOWN [H][F].
+ * -1 when not built or out of range. */
+#define MK_LAYER_QKV 0
+#define MK_LAYER_O 1
+#define MK_LAYER_GATE 2
+#define MK_LAYER_UP 3
+#define MK_LAYER_DOWN 4
+int megakernel_get_layer_fp8(void* handle, int layer, int which, unsigned char* codes, float* scales);
+
 /* Device fill of n bf16 values: bf16(float32(S_i - 131070) * c [+ 1.0f]),
  * S_i the Irwin-Hall(4) sum of the 16-bit fields of splitmix64(key, i). */
 int megakernel_synth_fill(void* d_dst, unsigned long long n, unsigned long long key, float c, int add_one);

@@ -48,6 +48,8 @@ SIGNATURES = {
     "megakernel_set_lmhead_fp8": (c_int, [c_void_p, c_int]),
     "megakernel_set_kv_fp8": (c_int, [c_void_p, c_int]),
     "megakernel_get_lmhead_fp8": (c_int, [c_void_p, c_void_p, P_float]),
+    "megakernel_set_layer_fp8": (c_int, [c_void_p, c_int]),
+    "megakernel_get_layer_fp8": (c_int, [c_void_p, c_int, c_int, c_void_p, P_float]),
     "megakernel_prefill_attach": (c_int, [c_void_p, c_void_p, P_ll, c_int]),
     "megakernel_prefill": (c_int, [c_void_p, P_int, c_int, P_int]),
     "megakernel_synth_fill": (c_int, [c_void_p, c_ull, c_ull, c_float, c_int]),

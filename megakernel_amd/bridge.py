@@ -276,6 +276,27 @@ class MegakernelEngine:
             scales.ctypes.data_as(ctypes.POINTER(ctypes.c_float))), "get_lmhead_fp8")
         return codes, scales
 
+    def set_layer_fp8(self, enable: bool = True):
+        """Stream FP8 (OCP e4m3, power-of-two row scales) copies of the layer
+        matrices (class-specialised kernel only)."""
+        _lib.check(self.lib, self.lib.megakernel_set_layer_fp8(self._handle, int(bool(enable))), "set_layer_fp8")
+
+    LAYER_MATRICES = ("qkv", "o", "gate", "up", "down")
+
+    def layer_fp8(self, layer: int, which: str):
+        """(codes uint8 [R, K], scales float32 [R]) of FP8 layer matrix `which`
+        (one of LAYER_MATRICES; "qkv" is the fused q | k | v rows)."""
+        s = self.shape
+        q, kv = s.n_q_heads * s.head_dim, s.n_kv_heads * s.head_dim
+        rk = {"qkv": (q + 2 * kv, s.hidden), "o": (s.hidden, q), "gate": (s.ffn, s.hidden),
+              "up": (s.ffn, s.hidden), "down": (s.hidden, s.ffn)}[which]
+        codes = np.empty(rk, dtype=np.uint8)
+        scales = np.empty(rk[0], dtype=np.float32)
+        _lib.check(self.lib, self.lib.megakernel_get_layer_fp8(
+            self._handle, int(layer), self.LAYER_MATRICES.index(which), codes.ctypes.data_as(ctypes.c_void_p),
+            scales.ctypes.data_as(ctypes.POINTER(ctypes.c_float))), "get_layer_fp8")
+        return codes, scales
+
     @property
     def grid_size(self) -> int:
         return self.lib.megakernel_grid_size(self._handle)

@@ -80,6 +80,36 @@ __global__ __launch_bounds__(256) void lmhead_fp8_kernel(const u32x4* __restrict
   if (j == 0) scales[row] = ldexpf(1.f, e);
 }
 
+// FP8 copy of the layer weights (opt-in; the same quantisation as the LM
+// head's: power-of-two row scale 2^e, e the smallest with max|W[r]| <= 448 *
+// 2^e, codes e4m3(W[r][c] * 2^-e) rounded to nearest even).  One workgroup per
+// 16-row block (blockIdx.x) of one matrix region of layer blockIdx.y; the
+// region starts at unit `off` of the layer in both formats (bf16: 16-byte
+// units, FP8: 8-byte units) and its blocks hold K / 32 tiles each.  FP8 tile:
+// 512 bytes, lane ((c >> 3) & 3) * 16 + r holding row r, columns 32 u + 8
+// ((c >> 3) & 3) .. +7 of tile u as 8 consecutive bytes.  Scale of block row r
+// at scales[layer * srows_layer + srow + 16 rb + r].
+__global__ __launch_bounds__(256) void layer_fp8_kernel(const u32x4* __restrict__ layers, long long u_layer,
+                                                        long long off, int K, unsigned char* __restrict__ dst8,
+                                                        float* __restrict__ scales, int srows_layer, int srow) {
+  const int r = threadIdx.x >> 4, j = threadIdx.x & 15;  // 16 threads per row
+  const long long rb = blockIdx.x, layer = blockIdx.y;
+  const int KT = K / 32;
+  const long long blk_units = layer * u_layer + off + rb * KT * 64;
+  const uint16_t* s16 = reinterpret_cast<const uint16_t*>(layers + blk_units);
+  auto lane_of = [&](int c) { return ((c >> 3) & 3) * 16 + r; };
+  auto elem = [&](int c) { return bf16_to_f32(s16[((c >> 5) * 64 + lane_of(c)) * 8 + (c & 7)]); };
+  float amax = 0.f;
+  for (int c = j; c < K; c += 16) amax = fmaxf(amax, fabsf(elem(c)));
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+  const int e = e4m3_row_exp(amax);
+  unsigned char* d = dst8 + blk_units * 8;
+  for (int c = j; c < K; c += 16)
+    d[(c >> 5) * 512 + lane_of(c) * 8 + (c & 7)] = (unsigned char)e4m3_encode(ldexpf(elem(c), -e));
+  if (j == 0) scales[layer * srows_layer + srow + rb * 16 + r] = ldexpf(1.f, e);
+}
+
 __global__ void synth_fill_kernel(uint16_t* __restrict__ dst, unsigned long long n, unsigned long long key,
                                   float c, int add_one) {
   for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -196,6 +226,7 @@ __global__ void synth_kv_ref_kernel(uint16_t* __restrict__ buf, int L, int NKV, 
 struct ShapeInfo {
   int H, NQ, NKV, D, F, QD, KVD, QKV, GQA;
   long long u_layer, off_qkv, off_o, off_gu, off_down;
+  int srows_layer, srow_qkv, srow_o, srow_gu, srow_down;  // FP8 row-scale offsets per layer
   int norm_stride, norm_attn, norm_q, norm_k, norm_ffn;
   int part_words;  // words of one attention item's published partial
 };
@@ -204,6 +235,7 @@ template <class S>
 static ShapeInfo shape_info() {
   return ShapeInfo{S::H, S::NQ, S::NKV, S::D, S::F, S::QD, S::KVD, S::QKV, S::GQA,
                    S::U_LAYER, S::OFF_QKV, S::OFF_O, S::OFF_GU, S::OFF_DOWN,
+                   S::SROWS_LAYER, S::SROW_QKV, S::SROW_O, S::SROW_GU, S::SROW_DOWN,
                    S::NORM_STRIDE, S::NORM_ATTN, S::NORM_Q, S::NORM_K, S::NORM_FFN, part_words<S>()};
 }
 
@@ -309,6 +341,9 @@ struct Handle {
   u32x4* lmhead8 = nullptr;  // optional FP8 copy of the LM head, built on request
   float* lm_scale = nullptr;
   bool lm_fp8 = false;       // the LM head reads lmhead8
+  u32x2* layers8 = nullptr;  // optional FP8 copy of the layer weights (same unit offsets, 8-byte units)
+  float* lscale = nullptr;   // its row scales [L][srows_layer]
+  bool layer_fp8 = false;    // the class kernel reads layers8
   float *kscale = nullptr, *vscale = nullptr;  // FP8 KV cache: row scales [L][NKV][s_pad]
   bool kv_fp8 = false;       // the cache holds e4m3 codes (byte index = bf16 element index)
   uint16_t* kv = nullptr;
@@ -336,6 +371,7 @@ struct Handle {
   int* roles = nullptr;
   bool roles_ok[kMaxClsSplit + 1] = {};
   int kernel_variant = MK_KERNEL_AUTO;
+  bool has_cls = false;  // the preset has class-kernel instantiations
   int pace_pct = 100;  // class kernel prefetch pacing (environment MK_PACE_PCT at init; 0 = bursts)
 };
 
@@ -344,7 +380,7 @@ static void free_all(Handle* h) {
   h->roles = nullptr;
   batch::destroy_prefill_context(h->prefill);
   h->prefill = nullptr;
-  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->kscale, h->vscale, h->kv, h->x, h->qkv, h->part,
+  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->layers8, h->lscale, h->kscale, h->vscale, h->kv, h->x, h->qkv, h->part,
                   h->act, h->amax, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
@@ -483,6 +519,7 @@ static Handle* create(int preset, int vocab, int max_seq) {
     case PRESET_BASELINE:
       h->sh = shape_info<ShapeBaseline>();
       h->launch = launch_decode_baseline;
+      h->has_cls = true;
       break;
     case PRESET_QWEN3_06B:
       h->sh = shape_info<ShapeQwen3>();
@@ -491,6 +528,7 @@ static Handle* create(int preset, int vocab, int max_seq) {
     case PRESET_TINY:
       h->sh = shape_info<ShapeTiny>();
       h->launch = launch_decode_tiny;
+      h->has_cls = true;
       break;
     default:
       set_err("unknown preset %d", preset);
@@ -568,6 +606,8 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.lmhead = h->lmhead;
   p.lmhead8 = h->lm_fp8 ? h->lmhead8 : nullptr;
   p.lm_scale = h->lm_fp8 ? h->lm_scale : nullptr;
+  p.layers8 = h->layer_fp8 ? h->layers8 : nullptr;
+  p.lscale = h->layer_fp8 ? h->lscale : nullptr;
   p.kscale = h->kv_fp8 ? h->kscale : nullptr;
   p.vscale = h->kv_fp8 ? h->vscale : nullptr;
   p.kv = h->kv;
@@ -610,8 +650,14 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   const bool lc = ns_last > h->merge_min;
   // the class kernel when a role table holds every attention item of the
   // launch (its attention workgroups serve the last token's split count)
-  const bool cls = h->kernel_variant == MK_KERNEL_AUTO && !lc && ns_last <= kMaxClsSplit && h->roles_ok[ns_last];
+  const bool cls =
+      h->has_cls && h->kernel_variant == MK_KERNEL_AUTO && !lc && ns_last <= kMaxClsSplit && h->roles_ok[ns_last];
   p.roles = cls ? h->roles + (size_t)(ns_last - 1) * h->G * ROLE_INTS : nullptr;
+  if (h->layer_fp8 && !cls) {
+    set_err("FP8 layer weights need the class kernel (automatic variant, at most %d attention splits per kv head; "
+            "this launch needs %d)", kMaxClsSplit, ns_last);
+    return -1;
+  }
   HIPCHK(h->launch(h->G, h->stream, p, lc, cls), -1);
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
   // error word and tokens come back in one copy into pinned memory
@@ -1066,8 +1112,8 @@ int megakernel_decode_kernel_for(void* handle, int n_tokens) {
     return -1;
   }
   const int ns = mk::split_count(h->pos + n_tokens, h->chunk_min, h->nsplit_max);
-  const bool cls = h->kernel_variant == MK_KERNEL_AUTO && ns <= h->merge_min && ns <= mk::kMaxClsSplit &&
-                   h->roles_ok[ns];
+  const bool cls = h->has_cls && h->kernel_variant == MK_KERNEL_AUTO && ns <= h->merge_min &&
+                   ns <= mk::kMaxClsSplit && h->roles_ok[ns];
   return cls ? MK_KERNEL_CLASS : MK_KERNEL_SPREAD;
 }
 
@@ -1102,6 +1148,73 @@ int megakernel_set_lmhead_fp8(void* handle, int enable) {
     HIPCHK(hipStreamSynchronize(h->stream), -1);
   }
   h->lm_fp8 = enable != 0;
+  return 0;
+}
+
+int megakernel_set_layer_fp8(void* handle, int enable) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) {
+    mk::set_err("null handle");
+    return -1;
+  }
+  if (enable && (!h->has_cls || !h->roles_ok[1])) {
+    mk::set_err("FP8 layer weights need the class kernel, which this preset / device does not have");
+    return -1;
+  }
+  if (enable && !h->layers8) {
+    const mk::ShapeInfo& s = h->sh;
+    HIPCHK(hipMalloc(&h->layers8, (size_t)s.u_layer * 8 * h->L), -1);
+    HIPCHK(hipMalloc(&h->lscale, (size_t)s.srows_layer * 4 * h->L), -1);
+    struct Region { long long off; int blocks, K, srow; };
+    const Region reg[4] = {{s.off_qkv, s.QKV / 16, s.H, s.srow_qkv},
+                           {s.off_o, s.H / 16, s.QD, s.srow_o},
+                           {s.off_gu, 2 * (s.F / 16), s.H, s.srow_gu},
+                           {s.off_down, s.H / 16, s.F, s.srow_down}};
+    for (const Region& g : reg)
+      hipLaunchKernelGGL(mk::layer_fp8_kernel, dim3(g.blocks, h->L), dim3(256), 0, h->stream, h->layers, s.u_layer,
+                         g.off, g.K, reinterpret_cast<unsigned char*>(h->layers8), h->lscale, s.srows_layer, g.srow);
+    HIPCHK(hipGetLastError(), -1);
+    HIPCHK(hipStreamSynchronize(h->stream), -1);
+  }
+  h->layer_fp8 = enable != 0;
+  return 0;
+}
+
+int megakernel_get_layer_fp8(void* handle, int layer, int which, unsigned char* codes, float* scales) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !h->layers8 || !codes || !scales) {
+    mk::set_err("FP8 layer weights not built (megakernel_set_layer_fp8) or null output");
+    return -1;
+  }
+  if (layer < 0 || layer >= h->L || which < MK_LAYER_QKV || which > MK_LAYER_DOWN) {
+    mk::set_err("layer %d / matrix %d outside [0, %d) / [%d, %d]", layer, which, h->L, MK_LAYER_QKV, MK_LAYER_DOWN);
+    return -1;
+  }
+  const mk::ShapeInfo& s = h->sh;
+  // rows, K, region offset, block stride / offset (gate and up interleave), scale rows
+  int R = 0, K = 0, bs = 1, bo = 0, srow = 0;
+  long long off = 0;
+  switch (which) {
+    case MK_LAYER_QKV: R = s.QKV, K = s.H, off = s.off_qkv, srow = s.srow_qkv; break;
+    case MK_LAYER_O: R = s.H, K = s.QD, off = s.off_o, srow = s.srow_o; break;
+    case MK_LAYER_GATE: R = s.F, K = s.H, off = s.off_gu, bs = 2, srow = s.srow_gu; break;
+    case MK_LAYER_UP: R = s.F, K = s.H, off = s.off_gu, bs = 2, bo = 1, srow = s.srow_gu; break;
+    default: R = s.H, K = s.F, off = s.off_down, srow = s.srow_down; break;
+  }
+  const int KT = K / 32;
+  const size_t region = (size_t)R * K * (bs == 2 ? 2 : 1);
+  std::vector<unsigned char> tiles(region);
+  std::vector<float> sc((size_t)R * (bs == 2 ? 2 : 1));
+  HIPCHK(hipMemcpy(tiles.data(), reinterpret_cast<const unsigned char*>(h->layers8 + (long long)layer * s.u_layer + off),
+                   region, hipMemcpyDeviceToHost), -1);
+  HIPCHK(hipMemcpy(sc.data(), h->lscale + (size_t)layer * s.srows_layer + srow, sc.size() * 4, hipMemcpyDeviceToHost),
+         -1);
+  for (long long row = 0; row < R; ++row) {
+    const long long blk = (row >> 4) * bs + bo;
+    scales[row] = sc[blk * 16 + (row & 15)];
+    for (int c = 0; c < K; ++c)
+      codes[row * K + c] = tiles[(blk * KT + (c >> 5)) * 512 + (((c >> 3) & 3) * 16 + (row & 15)) * 8 + (c & 7)];
+  }
   return 0;
 }
 

@@ -185,8 +185,8 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
 // ----------------------------------------------------------- phase bodies
 // P1: QKV block q of layer `layer` from the prefetched rq (inputs: x of the
 // previous layer, or the embedding row at layer 0).
-template <class S, int MODE>
-__device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const Blk<S::KC_H>& rq, const NormIn<S>& gq,
+template <class S, int MODE, class BH>
+__device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const BH& rq, const NormIn<S>& gq,
                                         int t, int layer, int q, int tok, unsigned tg) {
   float r;
   if (layer > 0) {
@@ -196,34 +196,35 @@ __device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const Blk<
   }
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 0);
   blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
-  store_block(sm.red[RED_Q], p.qkv + q * 16, r, tg);
+  store_block(sm.red[RED_Q], p.qkv + q * 16, r * row_scale(rq), tg);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 1);
   return true;
 }
 
 // P4: gate/up pair g + SiLU from the prefetched rg / ru (input: x after O).
-template <class S, int MODE>
-__device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const Blk<S::KC_H>& rg, const Blk<S::KC_H>& ru,
+template <class S, int MODE, class BH>
+__device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const BH& rg, const BH& ru,
                                        const NormIn<S>& gf, int t, int layer, int g, unsigned tg) {
   float r;
   if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 0);
   blk_mma2(rg, ru, sm.vec_g, sm.red[RED_G], sm.red[RED_U]);
-  store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, r, tag4(tg + 3u));
+  store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, r, tag4(tg + 3u), row_scale(rg), row_scale(ru));
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 1);
   return true;
 }
 
 // P5: down block d + residual from the prefetched rd (inputs: act and this
 // block's rows of x after O).
-template <class S, int MODE>
-__device__ __forceinline__ bool cls_down(const Params& p, Smem<S>& sm, const Blk<S::KC_F>& rd, int t, int layer, int d,
+template <class S, int MODE, class BF>
+__device__ __forceinline__ bool cls_down(const Params& p, Smem<S>& sm, const BF& rd, int t, int layer, int d,
                                          unsigned tg) {
   if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x, d, tag4(tg + 2u), sm.vec_d, sm.xres_d)) return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 0);
   blk_mma(rd, sm.vec_d, sm.red[RED_D]);
   __syncthreads();
-  if (wave_id() == 0) down_rows<S>(p, sm, d, (MODE & 2) != 0 ? p.dbg_layers : nullptr, layer, tg + 4u);
+  if (wave_id() == 0)
+    down_rows<S>(p, sm, d, (MODE & 2) != 0 ? p.dbg_layers : nullptr, layer, tg + 4u, row_scale(rd));
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 1);
   return true;
 }
@@ -231,8 +232,8 @@ __device__ __forceinline__ bool cls_down(const Params& p, Smem<S>& sm, const Blk
 // P3: O blocks o0 (and o1 >= 0) + residual (inputs: every kv head's split
 // partials, merged here, and the blocks' rows of x, or the embedding row at
 // layer 0).
-template <class S, int MODE>
-__device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const Blk<S::KC_Q>& ro0, const Blk<S::KC_Q>& ro1,
+template <class S, int MODE, class BQ>
+__device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const BQ& ro0, const BQ& ro1,
                                       int t, int layer, int o0, int o1, int nsplit, int tok, unsigned tg) {
   const unsigned tg_x = tg - 1u;
   if (!fetch_attn<S>(p, p.part, nsplit, tag4(tg + 1u), p.x, layer > 0 ? o0 : -1, o1, tag4(tg_x), sm.vec_o,
@@ -244,8 +245,8 @@ __device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const Blk<S:
   __syncthreads();
   // wave 0: block o0, wave 1: block o1
   const int w_ = wave_id();
-  if (w_ == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, o0, layer, tok, tg + 2u);
-  else if (w_ == 1 && o1 >= 0) o_rows<S>(p, sm.red[RED_O1], sm.xres_o + 16, o1, layer, tok, tg + 2u);
+  if (w_ == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, o0, layer, tok, tg + 2u, row_scale(ro0));
+  else if (w_ == 1 && o1 >= 0) o_rows<S>(p, sm.red[RED_O1], sm.xres_o + 16, o1, layer, tok, tg + 2u, row_scale(ro1));
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 1);
   return true;
 }
@@ -280,28 +281,58 @@ __device__ __forceinline__ void blk_load_paced(Blk<KC>& b, const u32x4* __restri
   }
 }
 
+// FP8 variant: 512-byte tiles, 8 bytes per lane, and the row scale of the
+// lane's epilogue row.
+template <int KC>
+__device__ __forceinline__ void blk_load_paced(Blk8<KC>& b, const u32x2* __restrict__ block,
+                                               const float* __restrict__ scales16, int units) {
+  const int w = wave_id();
+  const unsigned lb = lane_id() * 8u;
+  const auto rs = make_rsrc(block);
+  b.s = scales16[lane_id() >> 2];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    b.w[kc] = __builtin_amdgcn_raw_buffer_load_b64(rs, lb, (unsigned)(w * KC + kc) * 512u, 2);
+    if (units) pace_step(units);
+  }
+}
+// Block at unit offset u of the layer weights (the same offset in both
+// formats), scale rows from srow (FP8).
+template <int KC>
+__device__ __forceinline__ void blk_load_at(Blk<KC>& b, const Params& p, long long u, long long srow, int units) {
+  (void)srow;
+  blk_load_paced(b, p.layers + u, units);
+}
+template <int KC>
+__device__ __forceinline__ void blk_load_at(Blk8<KC>& b, const Params& p, long long u, long long srow, int units) {
+  blk_load_paced(b, p.layers8 + u, p.lscale + srow, units);
+}
+
 // Weight block loads of one layer.
-template <class S>
-__device__ __forceinline__ void ld_qkv(Blk<S::KC_H>& rq, NormIn<S>& gq, const Params& p, int layer, int q,
-                                       int units = 0) {
+template <class S, class BH>
+__device__ __forceinline__ void ld_qkv(BH& rq, NormIn<S>& gq, const Params& p, int layer, int q, int units = 0) {
   gains_load(gq, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_ATTN);
-  blk_load_paced(rq, p.layers + (long long)layer * S::U_LAYER + S::OFF_QKV + (long long)q * S::KT_H * 64, units);
+  blk_load_at(rq, p, (long long)layer * S::U_LAYER + S::OFF_QKV + (long long)q * S::KT_H * 64,
+              (long long)layer * S::SROWS_LAYER + S::SROW_QKV + q * 16, units);
 }
-template <class S>
-__device__ __forceinline__ void ld_gu(Blk<S::KC_H>& rg, Blk<S::KC_H>& ru, NormIn<S>& gf, const Params& p, int layer,
-                                      int g, int units = 0) {
-  const u32x4* gp = p.layers + (long long)layer * S::U_LAYER + S::OFF_GU + (long long)(2 * g) * S::KT_H * 64;
+template <class S, class BH>
+__device__ __forceinline__ void ld_gu(BH& rg, BH& ru, NormIn<S>& gf, const Params& p, int layer, int g,
+                                      int units = 0) {
+  const long long u = (long long)layer * S::U_LAYER + S::OFF_GU + (long long)(2 * g) * S::KT_H * 64;
+  const long long sr = (long long)layer * S::SROWS_LAYER + S::SROW_GU + (2 * g) * 16;
   gains_load(gf, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN);
-  blk_load_paced(rg, gp, units);
-  blk_load_paced(ru, gp + S::KT_H * 64, units);
+  blk_load_at(rg, p, u, sr, units);
+  blk_load_at(ru, p, u + S::KT_H * 64, sr + 16, units);
 }
-template <class S>
-__device__ __forceinline__ void ld_o(Blk<S::KC_Q>& ro, const Params& p, int layer, int o, int units = 0) {
-  blk_load_paced(ro, p.layers + (long long)layer * S::U_LAYER + S::OFF_O + (long long)o * S::KT_Q * 64, units);
+template <class S, class BQ>
+__device__ __forceinline__ void ld_o(BQ& ro, const Params& p, int layer, int o, int units = 0) {
+  blk_load_at(ro, p, (long long)layer * S::U_LAYER + S::OFF_O + (long long)o * S::KT_Q * 64,
+              (long long)layer * S::SROWS_LAYER + S::SROW_O + o * 16, units);
 }
-template <class S>
-__device__ __forceinline__ void ld_down(Blk<S::KC_F>& rd, const Params& p, int layer, int d, int units = 0) {
-  blk_load_paced(rd, p.layers + (long long)layer * S::U_LAYER + S::OFF_DOWN + (long long)d * S::KT_F * 64, units);
+template <class S, class BF>
+__device__ __forceinline__ void ld_down(BF& rd, const Params& p, int layer, int d, int units = 0) {
+  blk_load_at(rd, p, (long long)layer * S::U_LAYER + S::OFF_DOWN + (long long)d * S::KT_F * 64,
+              (long long)layer * S::SROWS_LAYER + S::SROW_DOWN + d * 16, units);
 }
 
 // K / V of an attention item's first blocks (kv_load) with a pause after each
@@ -365,11 +396,12 @@ __device__ __forceinline__ int next_layer(const Params& p, int layer) { return l
 
 template <class S, int MODE>
 __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int* role) {
+  constexpr bool W8 = (MODE & 16) != 0;  // FP8 layer weights
   constexpr bool K8 = (MODE & 8) != 0;
   const int a = role[RF_ATT], o0 = role[RF_O0];
   const int g = a % S::NKV, s = a / S::NKV;
   KV<S, K8> rkv;
-  Blk<S::KC_Q> ro;
+  BlkW<S::KC_Q, W8> ro;
   int tok = p.first_token;
   {
     const Item it = att_item_gs(g, s, p.pos0 + 1, p.chunk_min, p.nsplit_max);
@@ -421,8 +453,9 @@ __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int*
 // QKV + gate/up (Q: QKV only, G: gate/up only).
 template <class S, int MODE, bool HAS_Q, bool HAS_G>
 __device__ __forceinline__ void run_qg(const Params& p, Smem<S>& sm, const int* role) {
+  constexpr bool W8 = (MODE & 16) != 0;  // FP8 layer weights
   const int q = role[RF_Q], gi = role[RF_G];
-  Blk<S::KC_H> rq, rg, ru;
+  BlkW<S::KC_H, W8> rq, rg, ru;
   NormIn<S> gq, gf;
   if constexpr (HAS_Q) ld_qkv<S>(rq, gq, p, 0, q);
   if constexpr (!HAS_Q && HAS_G) ld_gu<S>(rg, ru, gf, p, 0, gi);
@@ -462,11 +495,12 @@ __device__ __forceinline__ void run_qg(const Params& p, Smem<S>& sm, const int* 
 // next weights are loaded together with the next down block, after down.
 template <class S, int MODE, int PARTNER>
 __device__ __forceinline__ void run_down(const Params& p, Smem<S>& sm, const int* role) {
+  constexpr bool W8 = (MODE & 16) != 0;  // FP8 layer weights
   const int d = role[RF_D], gi = role[RF_G], o0 = role[RF_O0];
-  Blk<S::KC_F> rd;
-  Blk<S::KC_H> rg, ru;
+  BlkW<S::KC_F, W8> rd;
+  BlkW<S::KC_H, W8> rg, ru;
   NormIn<S> gf;
-  Blk<S::KC_Q> ro;
+  BlkW<S::KC_Q, W8> ro;
   if constexpr (PARTNER == CLS_DG) ld_gu<S>(rg, ru, gf, p, 0, gi);
   if constexpr (PARTNER == CLS_DO) ld_o<S>(ro, p, 0, o0);
   ld_down<S>(rd, p, 0, d);
@@ -509,8 +543,9 @@ __device__ __forceinline__ void run_down(const Params& p, Smem<S>& sm, const int
 // One or two O blocks.
 template <class S, int MODE>
 __device__ __forceinline__ void run_o(const Params& p, Smem<S>& sm, const int* role) {
+  constexpr bool W8 = (MODE & 16) != 0;  // FP8 layer weights
   const int o0 = role[RF_O0], o1 = role[RF_O1];
-  Blk<S::KC_Q> ra, rb;
+  BlkW<S::KC_Q, W8> ra, rb;
   ld_o<S>(ra, p, 0, o0);
   if (o1 >= 0) ld_o<S>(rb, p, 0, o1);
   int tok = p.first_token;

@@ -41,6 +41,12 @@ struct Shape {
   static constexpr long long OFF_GU = U_QKV + U_O;
   static constexpr long long OFF_DOWN = U_QKV + U_O + U_GU;
   static constexpr long long U_LAYER = U_QKV + U_O + U_GU + U_DOWN;
+  // FP8 layer weights (opt-in): the same blocks with one e4m3 byte per weight
+  // (a tile is 512 bytes: the offsets above in 8-byte units), and one fp32
+  // power-of-two scale per packed row: QKV rows | O rows | gate/up rows in
+  // their interleaved block order | down rows.
+  static constexpr int SROW_QKV = 0, SROW_O = QKV, SROW_GU = QKV + H, SROW_DOWN = QKV + H + 2 * F;
+  static constexpr int SROWS_LAYER = QKV + 2 * H + 2 * F;
   // Per-layer norm gains, bf16: attn_norm[H] | q_norm[D] | k_norm[D] | ffn_norm[H]
   static constexpr int NORM_ATTN = 0, NORM_Q = H, NORM_K = H + D, NORM_FFN = H + 2 * D;
   static constexpr int NORM_STRIDE = 2 * H + 2 * D;

@@ -68,6 +68,8 @@ struct Params {
                               //   at byte index = element index of kv / kvt
   uint16_t* kv;               // K cache [L][NKV][s_pad][D] bf16
   uint16_t* kvt;              // V cache, transposed blocks [L][NKV][s_pad/32][D][32] bf16
+  const u32x2* layers8;       // optional FP8 (e4m3) layer weights, the same blocks at one byte per weight
+  const float* lscale;        //   and their power-of-two row scales [L][SROWS_LAYER] (class kernel, MODE bit 16)
   u64* x;                     // [H/2] residual stream (packed pairs: rows 2i, 2i + 1 in word i)
   u64* qkv;                   // [QKV] projections of the current layer (tagged)
   u64* part;                  // [nsplit_max + 1][NKV][part_words] attention partials (packed
@@ -164,6 +166,26 @@ struct Blk {
   u32x4 w[KC];
 };
 
+// The same block with FP8 (e4m3) weights: a tile is 512 bytes, lane l holds
+// the 8 codes of row l & 15, columns 32 kt + 8 (l >> 4) .. +7; s is the
+// power-of-two scale of row l >> 2 (the row lane l finishes in the epilogue).
+template <int KC>
+struct Blk8 {
+  u32x2 w[KC];
+  float s;
+};
+template <int KC, bool W8>
+using BlkW = typename std::conditional<W8, Blk8<KC>, Blk<KC>>::type;
+
+// A operand of one tile: the bf16 weights, or the FP8 codes converted to bf16
+// (exact: every e4m3 value is a bf16 value).
+__device__ __forceinline__ u32x4 a_tile(u32x4 w) { return w; }
+__device__ __forceinline__ u32x4 a_tile(u32x2 w) { return fp8x8_to_bf16x8_scaled(w, 1.0f); }
+template <int KC>
+__device__ __forceinline__ float row_scale(const Blk<KC>&) { return 1.0f; }
+template <int KC>
+__device__ __forceinline__ float row_scale(const Blk8<KC>& b) { return b.s; }
+
 template <int KC>
 __device__ __forceinline__ void blk_load(Blk<KC>& b, const u32x4* __restrict__ block) {
   const int w = wave_id();
@@ -182,6 +204,12 @@ template <int KC>
 __device__ __forceinline__ void blk_forget(Blk<KC>& b) {
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) b.w[kc] = __builtin_nondeterministic_value(b.w[kc]);
+}
+template <int KC>
+__device__ __forceinline__ void blk_forget(Blk8<KC>& b) {
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) b.w[kc] = __builtin_nondeterministic_value(b.w[kc]);
+  b.s = __builtin_nondeterministic_value(b.s);
 }
 
 // Block product on the matrix cores (tile-layout blocks, mk_config.h: wave w
@@ -223,20 +251,20 @@ __device__ __forceinline__ void mma_share_out(f32x4 a0, f32x4 a1, float* red) {
   }
   if ((l & 15u) == 0u) *reinterpret_cast<f32x4*>(red + wave_id() * 16 + 4 * (int)(l >> 4)) = s;
 }
-template <int KC>
-__device__ __forceinline__ void blk_mma(const Blk<KC>& b, const float* vec, float* red) {
+template <int KC, template <int> class B>
+__device__ __forceinline__ void blk_mma(const B<KC>& b, const float* vec, float* red) {
   u32x4 bx[KC];
   mma_b_load<KC>(bx, vec);
   f32x4 e = f32x4{0.f, 0.f, 0.f, 0.f}, o = e;
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
-    if (kc & 1) o = mma(b.w[kc], bx[kc], o);
-    else e = mma(b.w[kc], bx[kc], e);
+    if (kc & 1) o = mma(a_tile(b.w[kc]), bx[kc], o);
+    else e = mma(a_tile(b.w[kc]), bx[kc], e);
   }
   mma_share_out(e, o, red);
 }
-template <int KC>
-__device__ __forceinline__ void blk_mma2(const Blk<KC>& b0, const Blk<KC>& b1, const float* vec, float* red0,
+template <int KC, template <int> class B>
+__device__ __forceinline__ void blk_mma2(const B<KC>& b0, const B<KC>& b1, const float* vec, float* red0,
                                          float* red1) {
   u32x4 bx[KC];
   mma_b_load<KC>(bx, vec);
@@ -244,11 +272,11 @@ __device__ __forceinline__ void blk_mma2(const Blk<KC>& b0, const Blk<KC>& b1, c
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
     if (kc & 1) {
-      o0 = mma(b0.w[kc], bx[kc], o0);
-      o1 = mma(b1.w[kc], bx[kc], o1);
+      o0 = mma(a_tile(b0.w[kc]), bx[kc], o0);
+      o1 = mma(a_tile(b1.w[kc]), bx[kc], o1);
     } else {
-      e0 = mma(b0.w[kc], bx[kc], e0);
-      e1 = mma(b1.w[kc], bx[kc], e1);
+      e0 = mma(a_tile(b0.w[kc]), bx[kc], e0);
+      e1 = mma(a_tile(b1.w[kc]), bx[kc], e1);
     }
   }
   mma_share_out(e0, o0, red0);
@@ -297,11 +325,12 @@ __device__ __forceinline__ void store_block(const float* red, u64* dst16, float 
 
 // Gate/up pair: SiLU(g r) * (u r) of the 16 rows (gate shares in rg, up
 // shares in ru), published as 8 packed-pair words.
-__device__ __forceinline__ void store_block_gu(const float* rg, const float* ru, u64* dst8, float r, unsigned t4) {
+__device__ __forceinline__ void store_block_gu(const float* rg, const float* ru, u64* dst8, float r, unsigned t4,
+                                               float sg = 1.0f, float su = 1.0f) {
   __syncthreads();
   if (wave_id() == 0) {
     const unsigned l = lane_id();
-    const float a = silu_mul(red_row4(rg, l) * r, red_row4(ru, l) * r);
+    const float a = silu_mul(red_row4(rg, l) * (r * sg), red_row4(ru, l) * (r * su));
     const float b = dpp_sel<DPP_ROW_SHL4>(a);  // the next row
     if ((l & 7u) == 0u) ll_put(dst8 + (l >> 3), pk_pack(a, b, t4));
   }
@@ -532,11 +561,11 @@ __device__ __forceinline__ bool wait_last_qkv(const Params& p, unsigned tl) {
 // One wave (red_row4 layout).
 template <class S>
 __device__ __forceinline__ void o_rows(const Params& p, const float* red, const float* xres, int blk, int layer,
-                                       int tok, unsigned tag) {
+                                       int tok, unsigned tag, float rs = 1.0f) {
   const unsigned l = lane_id();
   const int r = (int)(l >> 2);
   const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, blk * 16 + r) : xres[r];
-  const float a = xo + red_row4(red, l);
+  const float a = xo + red_row4(red, l) * rs;
   const float b = dpp_sel<DPP_ROW_SHL4>(a);  // the next row
   if ((l & 7u) == 0u) ll_put(p.x + blk * 8 + (l >> 3), pk_pack(a, b, tag4(tag)));
 }
@@ -545,10 +574,10 @@ __device__ __forceinline__ void o_rows(const Params& p, const float* red, const 
 // block's 8 x words; dbg (layer dumps) unless null.  One wave.
 template <class S>
 __device__ __forceinline__ void down_rows(const Params& p, Smem<S>& sm, int blk, float* dbg, int layer,
-                                          unsigned tag) {
+                                          unsigned tag, float rs = 1.0f) {
   const unsigned l = lane_id();
   const int r = (int)(l >> 2);
-  const float a = sm.xres_d[r] + red_row4(sm.red[RED_D], l);
+  const float a = sm.xres_d[r] + red_row4(sm.red[RED_D], l) * rs;
   if (dbg && (l & 3u) == 0u) dbg[(long long)(layer + 1) * S::H + blk * 16 + r] = a;
   const float b = dpp_sel<DPP_ROW_SHL4>(a);
   if ((l & 7u) == 0u) ll_put(p.x + blk * 8 + (l >> 3), pk_pack(a, b, tag4(tag)));

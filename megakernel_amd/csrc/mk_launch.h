@@ -1,9 +1,9 @@
 // Launch and occupancy of the batch-1 decode kernel, one translation unit per
-// shape preset (decode_<preset>.hip) so the 16 kernel instantiations of each
+// shape preset (decode_<preset>.hip) so the kernel instantiations of each
 // preset compile in parallel.  MODE bits pick the instantiation per launch:
 // 1 the launch reaches more than merge_min attention splits per kv head, 2
 // timestamps or validation outputs are recorded, 4 the FP8 LM head, 8 the FP8
-// KV cache.
+// KV cache, 16 FP8 layer weights (class kernel only).
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -43,7 +43,7 @@ static hipError_t launch_decode(int grid, hipStream_t stream, const Params& p, b
                    (p.kscale ? 8 : 0);
   if constexpr (HAS_CLS) {
     if (cls && !lc) {
-      switch (mode) {
+      switch (mode | (p.layers8 ? 16 : 0)) {
         case 0: launch_cls<S, 0>(grid, stream, p); break;
         case 2: launch_cls<S, 2>(grid, stream, p); break;
         case 4: launch_cls<S, 4>(grid, stream, p); break;
@@ -51,11 +51,20 @@ static hipError_t launch_decode(int grid, hipStream_t stream, const Params& p, b
         case 8: launch_cls<S, 8>(grid, stream, p); break;
         case 10: launch_cls<S, 10>(grid, stream, p); break;
         case 12: launch_cls<S, 12>(grid, stream, p); break;
-        default: launch_cls<S, 14>(grid, stream, p); break;
+        case 14: launch_cls<S, 14>(grid, stream, p); break;
+        case 16: launch_cls<S, 16>(grid, stream, p); break;
+        case 18: launch_cls<S, 18>(grid, stream, p); break;
+        case 20: launch_cls<S, 20>(grid, stream, p); break;
+        case 22: launch_cls<S, 22>(grid, stream, p); break;
+        case 24: launch_cls<S, 24>(grid, stream, p); break;
+        case 26: launch_cls<S, 26>(grid, stream, p); break;
+        case 28: launch_cls<S, 28>(grid, stream, p); break;
+        default: launch_cls<S, 30>(grid, stream, p); break;
       }
       return hipGetLastError();
     }
   }
+  if (p.layers8) return hipErrorInvalidValue;  // the spread kernel reads bf16 layer weights only
   switch (mode) {
     case 0: launch_mode<S, 0>(grid, stream, p); break;
     case 1: launch_mode<S, 1>(grid, stream, p); break;
@@ -100,9 +109,11 @@ static int occupancy_min() {
   int m = n[0];
   for (int i = 1; i < 16; ++i) m = n[i] < m ? n[i] : m;
   if constexpr (HAS_CLS) {
-    const int c[8] = {occupancy_cls<S, 0>(), occupancy_cls<S, 2>(),  occupancy_cls<S, 4>(),  occupancy_cls<S, 6>(),
-                      occupancy_cls<S, 8>(), occupancy_cls<S, 10>(), occupancy_cls<S, 12>(), occupancy_cls<S, 14>()};
-    for (int i = 0; i < 8; ++i) m = c[i] < m ? c[i] : m;
+    const int c[16] = {occupancy_cls<S, 0>(),  occupancy_cls<S, 2>(),  occupancy_cls<S, 4>(),  occupancy_cls<S, 6>(),
+                       occupancy_cls<S, 8>(),  occupancy_cls<S, 10>(), occupancy_cls<S, 12>(), occupancy_cls<S, 14>(),
+                       occupancy_cls<S, 16>(), occupancy_cls<S, 18>(), occupancy_cls<S, 20>(), occupancy_cls<S, 22>(),
+                       occupancy_cls<S, 24>(), occupancy_cls<S, 26>(), occupancy_cls<S, 28>(), occupancy_cls<S, 30>()};
+    for (int i = 0; i < 16; ++i) m = c[i] < m ? c[i] : m;
   }
   return m;
 }

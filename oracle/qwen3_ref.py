@@ -170,6 +170,22 @@ class Qwen3Oracle:
         self.lm_head = torch.from_numpy(fp8.dequantize_rows(codes, scales)).to(self.embed.dtype)
         return codes, scales
 
+    def use_fp8_layers(self) -> list[dict[str, tuple[np.ndarray, np.ndarray]]]:
+        """Every layer matrix replaced by its FP8 copy (e4m3, power-of-two row
+        scales, oracle/fp8.py), dequantised exactly; norm gains stay.  Returns
+        per layer {name: (codes, scales)} with "qkv" the fused q | k | v rows."""
+        from . import fp8
+        out = []
+        for w in self.layers:
+            d = {}
+            for n in ("w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down"):
+                codes, scales = fp8.quantize_rows(w[n].float().numpy())
+                w[n] = torch.from_numpy(fp8.dequantize_rows(codes, scales)).to(w[n].dtype)
+                d[n[2:]] = (codes, scales)
+            d["qkv"] = tuple(np.concatenate([d[k][i] for k in ("q", "k", "v")]) for i in range(2))
+            out.append(d)
+        return out
+
     def reset(self) -> None:
         self.k_cache.zero_()
         self.v_cache.zero_()

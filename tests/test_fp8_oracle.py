@@ -89,3 +89,31 @@ def test_quantize_rows_equals_torch_on_scaled_rows():
     w = (rng.standard_normal((32, 256)) * 0.02).astype(np.float32)
     codes, scales = fp8.quantize_rows(w)
     assert np.array_equal(codes, _torch_codes(w / scales[:, None]))
+
+
+def test_oracle_fp8_layers_row_wise_and_exact_dequantisation():
+    """Qwen3Oracle.use_fp8_layers: the fused "qkv" codes are those of the
+    stacked q | k | v matrix (row-wise quantisation does not mix rows), every
+    dequantised weight is within half an e4m3 step of the bf16 weight (relative
+    2^-4 of its binade, or 2^-10 of the row scale below the normal range), and
+    the matrices the oracle then multiplies by are exactly code x scale."""
+    from oracle import qwen3_ref
+    from oracle.layout import Shape
+    sh = Shape(hidden=256, n_q_heads=4, n_kv_heads=2, head_dim=64, ffn=512, n_layers=2, vocab=512)
+    bits = qwen3_ref.synthetic_bits(sh, 5, std=0.02, gain_std=0.1)
+    orc = qwen3_ref.Qwen3Oracle(sh, bits, 8)
+    orig = [{n: w[n].clone() for n in ("w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down")} for w in orc.layers]
+    q = orc.use_fp8_layers()
+    table = fp8.e4m3_decode_table()
+    for li, w in enumerate(orc.layers):
+        stacked = torch.cat([orig[li]["w_q"], orig[li]["w_k"], orig[li]["w_v"]]).numpy()
+        c, s = fp8.quantize_rows(stacked)
+        assert np.array_equal(q[li]["qkv"][0], c) and np.array_equal(q[li]["qkv"][1], s)
+        for n in ("q", "k", "v", "o", "gate", "up", "down"):
+            codes, scales = q[li][n]
+            a = orig[li]["w_" + n].numpy()
+            b = w["w_" + n].numpy()
+            assert np.array_equal(b, table[codes] * scales[:, None])
+            _, ex = np.frexp(np.where(a != 0, a, 1.0))
+            step = np.maximum(np.ldexp(1.0, ex - 4), scales[:, None] * 2.0 ** -9)
+            assert (np.abs(b - a) <= 0.5 * step).all(), n

@@ -263,3 +263,159 @@ def test_fp8_kv_batch1_prefill_then_decode(which, prefix, prompt_len):
     finally:
         eng.close()
         dw.free()
+
+
+# ------------------------------------------------------------ FP8 layer weights
+@pytest.mark.parametrize("name,shape", [("tiny", TINY), ("baseline_2l", BASELINE_2L)])
+def test_fp8_layer_codes_bit_exact(name, shape):
+    """Every layer matrix (fused QKV, O, gate, up, down) quantised on the
+    device equals the oracle's e4m3 codes and power-of-two row scales bit for
+    bit, read back through megakernel_get_layer_fp8."""
+    eng, orc, dw = make_pair(shape, 47, 32)
+    try:
+        _print(f"fp8 layer codes {name}")
+        eng.set_layer_fp8(True)
+        want = orc.use_fp8_layers()
+        for li in range(shape.n_layers):
+            for m in eng.LAYER_MATRICES:
+                codes, scales = eng.layer_fp8(li, m)
+                wc, ws = want[li][m]
+                assert codes.shape == wc.shape, (li, m)
+                assert np.array_equal(scales, ws), f"layer {li} {m}: row scales differ"
+                diff = codes != wc
+                assert not diff.any(), f"layer {li} {m}: {int(diff.sum())} codes differ (first {np.argwhere(diff)[0]})"
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_fp8_layer_decode_parity():
+    """Decoding with FP8 layer weights against the oracle run on the same
+    dequantised matrices (exact: code x 2^e is a bf16 value), per layer and
+    per logit, at the bf16 path's bars."""
+    eng, orc, dw = make_pair(BASELINE_2L, 53, 128)
+    try:
+        eng.set_layer_fp8(True)
+        orc.use_fp8_layers()
+        prompt = synth.prompt_tokens(53, 6, BASELINE_2L.vocab)
+        tok = prompt[0]
+        for i in range(12):
+            tin = prompt[i] if i < len(prompt) else tok
+            _print(f"fp8 layers step {i} token {tin}")
+            nxt, layers, logits = eng.debug_forward(tin)
+            ref = orc.step(tin, capture=True)
+            check_step(layers, logits, ref, f"fp8 layers step {i}")
+            if nxt != ref["token"]:
+                assert qwen3_ref.top2_margin(ref["logits"]) <= 2e-2
+            tok = nxt
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_fp8_layers_lmhead_and_kv_together():
+    """All three FP8 formats at once (layers, LM head, KV cache) over a split
+    context, against the oracle with all three; then a resident launch equals
+    per-token decoding and switching the layers back to bf16 reproduces the
+    bf16 logits bit for bit."""
+    shape = BASELINE_2L
+    ctx = 700
+    eng, orc, dw = make_pair(shape, 59, ctx + 64, kv_fp8=True)
+    try:
+        eng.set_attention_chunk(256)
+        eng.fill_kv_synthetic(ctx, 61)
+        orc.set_kv(*_synthetic_kv(shape, 61, ctx))
+        _, _, bf16_logits = eng.debug_forward(9)
+        eng.set_pos(ctx)
+        eng.set_layer_fp8(True)
+        eng.set_lmhead_fp8(True)
+        orc.use_fp8_layers()
+        orc.use_fp8_lm_head()
+        tok = 9
+        for i in range(4):
+            _print(f"fp8 layers+head+kv ctx {ctx} step {i}")
+            _, layers, logits = eng.debug_forward(tok)
+            ref = orc.step(tok, capture=True)
+            check_step(layers, logits, ref, f"fp8 all step {i}")
+            tok = ref["token"]
+        eng.set_pos(ctx)
+        a0 = eng.decode_token(9)
+        gen = eng.decode_many(a0, 20)
+        eng.set_pos(ctx)
+        b = [eng.decode_token(9)]
+        for _ in range(20):
+            b.append(eng.decode_token(b[-1]))
+        assert [a0] + gen == b, "generate() and per-token decode disagree with FP8 layers"
+        eng.set_layer_fp8(False)
+        eng.set_lmhead_fp8(False)
+        eng.set_pos(ctx)
+        _, _, back = eng.debug_forward(9)
+        assert np.array_equal(back, bf16_logits), "bf16 logits changed after FP8 layers were switched off"
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_fp8_layers_need_class_kernel():
+    """FP8 layer weights are served by the class-specialised kernel only: the
+    spread kernel variant refuses the launch with a message, the QWEN3 preset
+    (no class kernel) refuses the switch, and the handle keeps working."""
+    from megakernel_amd import _lib
+    eng, orc, dw = make_pair(BASELINE_2L, 67, 64)
+    try:
+        eng.set_layer_fp8(True)
+        eng.set_decode_kernel(_lib.KERNEL_SPREAD)
+        with pytest.raises(RuntimeError, match="class kernel"):
+            eng.decode_token(3)
+        eng.set_decode_kernel(_lib.KERNEL_AUTO)
+        eng.set_pos(0)
+        eng.decode_token(3)
+        assert eng.pos == 1
+    finally:
+        eng.close()
+        dw.free()
+    shape = QWEN3_06B.with_(n_layers=1, vocab=1024)
+    eng, orc, dw = make_pair(shape, 67, 16)
+    try:
+        with pytest.raises(RuntimeError, match="class kernel"):
+            eng.set_layer_fp8(True)
+        eng.decode_token(3)
+    finally:
+        eng.close()
+        dw.free()
+
+
+def test_fp8_layers_full_model_ctx1024():
+    """The FP8 bench line's workload: full BASELINE model, 1,024 prefilled
+    positions, FP8 layers and LM head; every matrix's codes of the first and
+    last layer bit-exact, two debug steps at the bars, then 64 tokens in one
+    resident launch teacher-forced against the FP8 oracle."""
+    ctx = 1024
+    eng, orc, dw = make_pair(BASELINE, 2024, ctx + 80, gain_std=0.0, bits_from_device=True)
+    try:
+        eng.fill_kv_synthetic(ctx, 2024)
+        kv = eng.get_kv(ctx)
+        orc.set_kv(kv[:, 0], kv[:, 1])
+        del kv
+        eng.set_layer_fp8(True)
+        eng.set_lmhead_fp8(True)
+        want = orc.use_fp8_layers()
+        orc.use_fp8_lm_head()
+        for li in (0, BASELINE.n_layers - 1):
+            for m in eng.LAYER_MATRICES:
+                codes, scales = eng.layer_fp8(li, m)
+                assert np.array_equal(scales, want[li][m][1]) and np.array_equal(codes, want[li][m][0]), (li, m)
+        del want
+        tok = 11
+        for i in range(2):
+            _, layers, logits = eng.debug_forward(tok)
+            ref = orc.step(tok, capture=True)
+            l2, la = check_step(layers, logits, ref, f"fp8 full ctx 1024 step {i}")
+            _print(f"fp8 full model step {i}: layer relL2 {l2:.2e} logits abs {la:.2e}")
+            tok = ref["token"]
+        gen = eng.decode_many(tok, 64)
+        same, low = check_tokens_teacher_forced([tok] + gen[:-1], gen, orc)
+        _print(f"fp8 full model, 64 tokens: {same} identical, {low} low-margin")
+    finally:
+        eng.close()
+        dw.free()
