@@ -60,6 +60,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=0,
                     help="BASELINE configs[4] instead: this many independent sequences (<= 16), KV lengths "
                          "uniform in [--kv-min, --kv-max] from --seed, --steps greedy steps each")
+    ap.add_argument("--batch-step", choices=("persistent", "per-phase"), default="per-phase",
+                    help="batched step: every layer in one persistent kernel, or one kernel per phase and layer")
     ap.add_argument("--kv-min", type=int, default=512)
     ap.add_argument("--kv-max", type=int, default=4096)
     ap.add_argument("--ops", action="store_true",
@@ -209,7 +211,7 @@ def bench_batch(args):
     once plus, per sequence, its KV read (positions 0..pos) and append."""
     import numpy as np
 
-    from megakernel_amd import launcher
+    from megakernel_amd import _lib, launcher
     from megakernel_amd.batch import BatchEngine
     from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
     from megakernel_amd.weights import DeviceWeights
@@ -219,6 +221,7 @@ def bench_batch(args):
     lengths = [int(x) for x in rng.integers(args.kv_min, args.kv_max + 1, size=B)]
     dw = DeviceWeights(shape, args.seed, std=0.02, gain_std=0.0)
     eng = BatchEngine(dw, B, args.kv_max + max(K, W) + 8, shape)
+    eng.set_step_kernel(_lib.BATCH_STEP_PER_PHASE if args.batch_step == "per-phase" else _lib.BATCH_STEP_PERSISTENT)
     if args.kv_fp8:
         eng.set_kv_fp8(True)
     if args.lmhead_fp8:
@@ -260,6 +263,7 @@ def bench_batch(args):
                                                                      ("KV cache", args.kv_fp8)) if on),
         "config": {"workload": f"Qwen3-0.6B-shaped batched decode, {B} sequences, KV lengths {lengths}, "
                                f"{K} steps (BASELINE configs[4])", "sequences": B, "kv_lengths": lengths,
+                   "step": args.batch_step,
                    "device": info["name"], "reps": args.reps},
         "steps_per_s": round(K / wall, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -412,7 +416,7 @@ def bench_prefill(args):
     reference's prefill-by-decode, host/bridge.py:136-163)."""
     import numpy as np
 
-    from megakernel_amd import launcher
+    from megakernel_amd import _lib, launcher
     from megakernel_amd.batch import BatchEngine
     from megakernel_amd.bridge import MegakernelEngine
     from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS

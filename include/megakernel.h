@@ -304,6 +304,24 @@ int megakernel_batch_set_kv_fp8(void* handle, int enable);
  * step graph is captured again.  Returns 0 or -1. */
 int megakernel_batch_set_lmhead_fp8(void* handle, int enable);
 
+/* How a batched step runs its layers (no counterpart in the reference):
+ * MK_BATCH_STEP_PER_PHASE (the default) launches one kernel per phase and
+ * layer (five per layer); MK_BATCH_STEP_PERSISTENT runs every layer in one
+ * persistent kernel of two workgroups per CU whose phases hand off through
+ * per-producer flags.  Both compute the same sums in the same order, so
+ * tokens and logits are identical.  Returns 0, or -1 (unknown variant, or the
+ * persistent kernel does not fit two workgroups per CU). */
+#define MK_BATCH_STEP_PERSISTENT 0
+#define MK_BATCH_STEP_PER_PHASE 1
+int megakernel_batch_set_step_kernel(void* handle, int variant);
+
+/* Diagnostics of the persistent step (no counterpart in the reference): one
+ * step as megakernel_decode_batch, recording the device wall clock (100 MHz)
+ * per layer, event and workgroup into stamps[L][11][G] (events: layer start,
+ * then inputs ready / done of QKV, attention, O, gate/up, down; 0 where the
+ * workgroup has no role).  Returns G (the workgroup count), or -1. */
+int megakernel_batch_trace_step(void* handle, const int* tokens_in, unsigned long long* stamps, long long n_stamps);
+
 /* Device time of the last megakernel_generate_batch / decode_batch / prefill call (ms). */
 float megakernel_batch_last_ms(void* handle);
 

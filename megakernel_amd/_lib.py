@@ -73,6 +73,8 @@ SIGNATURES = {
     "megakernel_batch_prefill": (c_int, [c_void_p, c_int, P_int, c_int, P_int, P_float]),
     "megakernel_batch_set_kv_fp8": (c_int, [c_void_p, c_int]),
     "megakernel_batch_set_lmhead_fp8": (c_int, [c_void_p, c_int]),
+    "megakernel_batch_set_step_kernel": (c_int, [c_void_p, c_int]),
+    "megakernel_batch_trace_step": (c_int, [c_void_p, P_int, ctypes.POINTER(ctypes.c_ulonglong), ctypes.c_longlong]),
     "megakernel_batch_last_ms": (c_float, [c_void_p]),
     # operator microbench
     "megakernel_op_packed_bytes": (c_ll, [c_int, c_int]),
@@ -92,6 +94,7 @@ SIGNATURES = {
 
 PRESET_BASELINE, PRESET_QWEN3_06B, PRESET_TINY = 0, 1, 2
 KERNEL_AUTO, KERNEL_SPREAD, KERNEL_CLASS = 0, 1, 2  # megakernel_set_decode_kernel / _decode_kernel_for
+BATCH_STEP_PERSISTENT, BATCH_STEP_PER_PHASE = 0, 1  # megakernel_batch_set_step_kernel
 H2D, D2H, D2D = 0, 1, 2
 
 _cache: dict[str, ctypes.CDLL] = {}

@@ -54,6 +54,27 @@ class BatchEngine:
         _lib.check(self.lib, self.lib.megakernel_batch_set_lmhead_fp8(self._handle, int(bool(enable))),
                    "batch_set_lmhead_fp8")
 
+    def set_step_kernel(self, variant: int):
+        """_lib.BATCH_STEP_PER_PHASE (one kernel per phase and layer, the
+        default) or _lib.BATCH_STEP_PERSISTENT (every layer in one persistent
+        kernel); identical results."""
+        _lib.check(self.lib, self.lib.megakernel_batch_set_step_kernel(self._handle, int(variant)),
+                   "batch_set_step_kernel")
+
+    TRACE_EVENTS = ("start", "qkv_in", "qkv_done", "att_in", "att_done", "o_in", "o_done", "gu_in", "gu_done",
+                    "down_in", "down_done")
+
+    def trace_step(self, tokens, max_workgroups: int = 1024) -> np.ndarray:
+        """One persistent step with device wall-clock stamps (100 MHz):
+        uint64 [layers][len(TRACE_EVENTS)][workgroups], 0 where a workgroup
+        has no role in a phase."""
+        n = self.shape.n_layers * len(self.TRACE_EVENTS) * max_workgroups
+        buf = (ctypes.c_ulonglong * n)()
+        g = _lib.check(self.lib, self.lib.megakernel_batch_trace_step(self._handle, self._ints(tokens), buf, n),
+                       "batch_trace_step")
+        a = np.frombuffer(buf, dtype=np.uint64)[: self.shape.n_layers * len(self.TRACE_EVENTS) * g]
+        return a.reshape(self.shape.n_layers, len(self.TRACE_EVENTS), g).copy()
+
     def fill_kv_synthetic(self, seq: int, length: int, seed: int, std: float = 1.0):
         _lib.check(self.lib, self.lib.megakernel_batch_fill_kv_synthetic(self._handle, seq, length, seed, std),
                    "batch_fill_kv_synthetic")

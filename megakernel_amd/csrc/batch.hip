@@ -34,6 +34,8 @@ struct BHandle {
   u32x4* lmhead8 = nullptr;                     // FP8 LM head copy, built on first use
   float* lm_scale = nullptr;
   int (*launch_step)(BHandle*, const BParams&) = nullptr;
+  int step_variant = MK_BATCH_STEP_PER_PHASE;  // one kernel per phase and layer, or the layers in bk_step
+  bool persistent_ok = false;                  // bk_step fits one workgroup on every CU
   int (*launch_prefill)(BHandle*, const BParams&, bool) = nullptr;
 };
 
@@ -71,12 +73,22 @@ static int repack_tiles(BHandle* h, const char* base, long long off, int R, int 
   return 0;
 }
 
-// One decode step of every sequence: the kernels of mk_batch.h in order.
+// One decode step of every sequence: the kernels of mk_batch.h in order --
+// one kernel per phase and layer (default), or the layers as one persistent
+// bk_step.
 template <class S>
 static int launch_step(BHandle* h, const BParams& p) {
   const int L = h->L;
   hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
-  for (int l = 0; l < L; ++l) {
+  // the final-norm parts: slot L of the persistent step, slot 0 of the per-phase kernels
+  const int lm_slot = h->step_variant == MK_BATCH_STEP_PERSISTENT ? L : 0;
+  if (h->step_variant == MK_BATCH_STEP_PERSISTENT) {
+    if (p.kscale)
+      hipLaunchKernelGGL((bk_step<S, true>), dim3(h->G * STEP_WG_PER_CU), dim3(GT), 0, h->stream, p);
+    else
+      hipLaunchKernelGGL((bk_step<S, false>), dim3(h->G * STEP_WG_PER_CU), dim3(GT), 0, h->stream, p);
+  }
+  for (int l = 0; l < (h->step_variant == MK_BATCH_STEP_PERSISTENT ? 0 : L); ++l) {
     hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, p, l);
     if (p.kscale)
       hipLaunchKernelGGL((bk_attn<S, true>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
@@ -87,9 +99,9 @@ static int launch_step(BHandle* h, const BParams& p) {
     hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
   }
   if (p.lmhead8)
-    hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p);
+    hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p, lm_slot);
   else
-    hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, p);
+    hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, p, lm_slot);
   hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
   HIPCHK(hipGetLastError(), -1);
   return 0;
@@ -118,13 +130,24 @@ static int launch_prefill(BHandle* h, const BParams& p, bool last) {
   }
   if (last) {
     if (p.lmhead8)
-      hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p);
+      hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p, 0);
     else
-      hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, p);
+      hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, p, 0);
     hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
   }
   HIPCHK(hipGetLastError(), -1);
   return 0;
+}
+
+// The persistent step needs every one of its workgroups resident at once:
+// STEP_WG_PER_CU per CU for both cache formats.
+template <class S>
+static bool persistent_fits() {
+  int a = 0, b = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, bk_step<S, false>, GT, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, bk_step<S, true>, GT, 0) != hipSuccess)
+    return false;
+  return a >= STEP_WG_PER_CU && b >= STEP_WG_PER_CU;
 }
 
 template <class S>
@@ -133,6 +156,7 @@ static void set_shape(BHandle* h) {
   h->norm_stride = S::NORM_STRIDE;
   h->launch_step = launch_step<S>;
   h->launch_prefill = launch_prefill<S>;
+  h->persistent_ok = persistent_fits<S>();
 }
 
 // ext_kv / ext_kvt: bind to an external single-sequence cache (a prefill
@@ -208,9 +232,12 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
   p.nsplit_max = h->nsplit_max;
   h->max_steps = 1 << 16;
   p.max_steps = h->max_steps;
-  if (alloc(h, &p.x, (size_t)BMAX * h->H * 4) || alloc(h, &p.qkv, (size_t)BMAX * h->QKV * 4) ||
-      alloc(h, &p.xg, (size_t)4 * BMAX * h->H * 2) || alloc(h, &p.ssq, (size_t)2 * (h->H / 16) * BMAX * 4) ||
-      alloc(h, &p.att, (size_t)2 * BMAX * h->QD * 2) || alloc(h, &p.act, (size_t)2 * BMAX * h->F * 2) ||
+  // activation slots (x_slot .. act_slot in mk_batch.h): L + 1 of x / xg / ssq,
+  // L of qkv / att / act (the per-phase kernels use slot 0)
+  const size_t xs = (size_t)L + 1, ls = (size_t)L;
+  if (alloc(h, &p.x, xs * 2 * BMAX * h->H * 4) || alloc(h, &p.qkv, ls * BMAX * h->QKV * 4) ||
+      alloc(h, &p.xg, xs * 4 * BMAX * h->H * 2) || alloc(h, &p.ssq, xs * 2 * (h->H / 16) * BMAX * 4) ||
+      alloc(h, &p.att, ls * 2 * BMAX * h->QD * 2) || alloc(h, &p.act, ls * 2 * BMAX * h->F * 2) ||
       alloc(h, &p.part, (size_t)BMAX * h->NKV * h->nsplit_max * PW * 4) ||
       alloc(h, &p.cnt, (size_t)BMAX * h->NKV * 4) || alloc(h, &p.keys, (size_t)BMAX * 8) ||
       alloc(h, &p.rope, (size_t)BMAX * h->D * 4) ||
@@ -222,8 +249,12 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
       alloc(h, &p.out, (size_t)h->max_steps * BMAX * 4) || alloc(h, &p.step, 64) ||
       alloc(h, &p.dbg_logits, (size_t)BMAX * h->V * 4) || alloc(h, &h->pf_tok, (size_t)h->S * 4) ||
       alloc(h, &h->pf_pos, (size_t)h->S * 4) || alloc(h, &h->pf_out, (size_t)BMAX * 4) ||
-      alloc(h, &h->pf_step, 64))
+      alloc(h, &h->pf_step, 64) || alloc(h, &p.flags, (size_t)L * FC_N * FLAG_MAX * 4) ||
+      alloc(h, &p.epoch, 64) || alloc(h, &p.err, 256))
     return -1;
+  int wall_khz = 0;
+  HIPCHK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, h->device), -1);
+  p.timeout_ticks = (unsigned long long)(wall_khz > 0 ? wall_khz : 100000) * 10000ull;  // 10 s per hand-off wait
   std::vector<float> invf(h->D / 2);
   for (int i = 0; i < h->D / 2; ++i) invf[i] = 1.0f / powf((float)kRopeTheta, (float)(2 * i) / (float)h->D);
   float* inv;
@@ -287,6 +318,20 @@ static int set_tokens(BHandle* h, const int* tokens) {
   return 0;
 }
 
+// A hand-off wait of the persistent step that gave up (MK_ERR_TIMEOUT in
+// p.err): the error is reported and the step's counters are cleared, so the
+// handle can run again.
+static int check_step_error(BHandle* h) {
+  int err = 0;
+  HIPCHK(hipMemcpy(&err, h->p.err, 4, hipMemcpyDeviceToHost), -1);
+  if (err == 0) return 0;
+  HIPCHK(hipMemset(h->p.err, 0, 4), -1);
+  HIPCHK(hipMemset(h->p.cnt, 0, (size_t)BMAX * h->NKV * 4), -1);
+  HIPCHK(hipMemset(h->p.gcnt, 0, (size_t)(h->F / 16 > h->QKV / 16 ? h->F / 16 : h->QKV / 16) * 4), -1);
+  set_err("batched decode step aborted: a hand-off wait timed out");
+  return -1;
+}
+
 // The step graph: the same kernels with the same arguments every step (the
 // step's inputs live in device memory), captured once.
 static int ensure_graph(BHandle* h) {
@@ -318,6 +363,7 @@ static int run_steps(BHandle* h, const int* first, int n, int* out) {
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
   HIPCHK(hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1), -1);
+  if (check_step_error(h)) return -1;
   if (out) {
     std::vector<int> all((size_t)n * BMAX);
     HIPCHK(hipMemcpy(all.data(), h->p.out, all.size() * 4, hipMemcpyDeviceToHost), -1);
@@ -601,6 +647,7 @@ int megakernel_batch_debug_logits(void* handle, const int* tokens_in, int* token
   if (mk::batch::check_positions(h, 1) || mk::batch::set_tokens(h, tokens_in)) return -1;
   if (h->launch_step(h, h->p)) return -1;  // eager launches, logits written
   HIPCHK(hipStreamSynchronize(h->stream), -1);
+  if (mk::batch::check_step_error(h)) return -1;
   HIPCHK(hipMemcpy(logits, h->p.dbg_logits, (size_t)h->B * h->V * 4, hipMemcpyDeviceToHost), -1);
   if (tokens_out) {
     std::vector<int> t(mk::batch::BMAX);
@@ -673,6 +720,56 @@ int megakernel_batch_set_lmhead_fp8(void* handle, int enable) {
   if (h->graph) (void)hipGraphDestroy(h->graph);
   h->exec = nullptr;
   h->graph = nullptr;
+  return 0;
+}
+
+int megakernel_batch_trace_step(void* handle, const int* tokens_in, unsigned long long* stamps, long long n_stamps) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || !tokens_in || !stamps || h->step_variant != MK_BATCH_STEP_PERSISTENT) {
+    mk::set_err("null handle / tokens / output, or the persistent step is not selected");
+    return -1;
+  }
+  const int G = h->G * mk::batch::STEP_WG_PER_CU;
+  const long long need = (long long)h->L * mk::batch::TR_N * G;
+  if (n_stamps < need) {
+    mk::set_err("trace needs %lld stamps, got %lld", need, n_stamps);
+    return -1;
+  }
+  if (mk::batch::check_positions(h, 1) || mk::batch::set_tokens(h, tokens_in)) return -1;
+  unsigned long long* dev = nullptr;
+  HIPCHK(hipMalloc(&dev, (size_t)need * 8), -1);
+  int rc = -1;
+  do {
+    if (hipMemsetAsync(dev, 0, (size_t)need * 8, h->stream) != hipSuccess) break;
+    mk::batch::BParams p = h->p;
+    p.trace = dev;
+    if (h->launch_step(h, p) || hipStreamSynchronize(h->stream) != hipSuccess) break;
+    if (mk::batch::check_step_error(h)) break;
+    if (hipMemcpy(stamps, dev, (size_t)need * 8, hipMemcpyDeviceToHost) != hipSuccess) break;
+    rc = G;
+  } while (0);
+  (void)hipFree(dev);
+  if (rc < 0) mk::set_err("batched trace step failed");
+  return rc;
+}
+
+int megakernel_batch_set_step_kernel(void* handle, int variant) {
+  BHandle* h = static_cast<BHandle*>(handle);
+  if (!h || (variant != MK_BATCH_STEP_PERSISTENT && variant != MK_BATCH_STEP_PER_PHASE)) {
+    mk::set_err("null handle or unknown step variant %d", variant);
+    return -1;
+  }
+  if (variant == MK_BATCH_STEP_PERSISTENT && !h->persistent_ok) {
+    mk::set_err("the persistent batched step does not fit one workgroup per CU on this device");
+    return -1;
+  }
+  if (variant != h->step_variant) {
+    h->step_variant = variant;
+    if (h->exec) (void)hipGraphExecDestroy(h->exec);  // captured again with the chosen kernels
+    if (h->graph) (void)hipGraphDestroy(h->graph);
+    h->exec = nullptr;
+    h->graph = nullptr;
+  }
   return 0;
 }
 

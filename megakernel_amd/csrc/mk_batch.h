@@ -52,6 +52,21 @@ constexpr int PW = 2 * 64 + 4; // partial words per item for GQA 2, D 64: o[2][6
 // 88 tiles; the others lose more to the reduction than they gain)
 constexpr int KS_QKV = 1, KS_O = 1, KS_GU = 1, KS_DN = 4;
 
+// Hand-off flags of one layer in the single-kernel step (bk_step), one word
+// per producer: QKV blocks, merged (sequence, kv head) attention outputs, O
+// blocks, gate / up blocks, down blocks.  A producer writes the step's epoch
+// into its word after its outputs are acknowledged; a consumer waits until
+// every word it needs holds the epoch.  One writer per word and no atomics:
+// a single counter that every producer incremented serialised the
+// increments at one memory channel (5-10 us per hand-off).
+enum : int { FC_QKV = 0, FC_ATT, FC_O, FC_GU, FC_DN, FC_N };
+constexpr int FLAG_MAX = 256;  // producers per phase (>= F/16, QKV/16, BMAX * NKV)
+// Optional timestamps of bk_step per layer and workgroup: layer start, then
+// inputs ready / done of QKV, attention, O, gate/up and down (a workgroup
+// without a role in a phase leaves that phase's stamps 0).
+enum : int { TR_START = 0, TR_QKV_IN, TR_QKV_DONE, TR_ATT_IN, TR_ATT_DONE, TR_O_IN, TR_O_DONE, TR_GU_IN,
+             TR_GU_DONE, TR_DN_IN, TR_DN_DONE, TR_N };
+
 struct BParams {
   const u32x4* wqkv;        // per layer [QKV/16][H/32] tiles
   const u32x4* wo;          // per layer [H/16][QD/32]
@@ -71,13 +86,15 @@ struct BParams {
   float* vscale;            //   row, [B][L][NKV][s_pad]; codes at byte index = element index
   long long sc_seq;         // scales per sequence
   int s_pad;
-  float* x;                 // [BMAX][H] residual streams
-  uint16_t* xg;             // [2 consumers][2 planes][BMAX][H] x * gain as bf16 hi / lo parts:
+  // activations, per slot (x_slot .. act_slot below: L + 1 slots of x / xg /
+  // ssq, L of qkv / att / act; the per-phase kernels use slot 0)
+  float* x;                 // [slot][2 consumers][BMAX][H] residual streams
+  uint16_t* xg;             // [slot][2 consumers][2 planes][BMAX][H] x * gain as bf16 hi / lo parts:
                             //   consumer 0 = attn_norm of the next QKV (or final_norm), 1 = ffn_norm
-  float* ssq;               // [2 consumers][H/16][BMAX] sums of squares of x per 16-row block
-  float* qkv;               // [BMAX][QKV] raw projections of the current layer
-  uint16_t* att;            // [2][BMAX][QD] merged attention output, bf16 hi / lo parts
-  uint16_t* act;            // [2][BMAX][F] SiLU(g) * u, bf16 hi / lo parts
+  float* ssq;               // [slot][2 consumers][H/16][BMAX] sums of squares of x per 16-row block
+  float* qkv;               // [slot][BMAX][QKV] raw projections
+  uint16_t* att;            // [slot][2][BMAX][QD] merged attention output, bf16 hi / lo parts
+  uint16_t* act;            // [slot][2][BMAX][F] SiLU(g) * u, bf16 hi / lo parts
   float* part;              // [BMAX][NKV][nsplit_max][PW] attention partials
   int* cnt;                 // [BMAX][NKV] finished splits of the current layer
   float* gpart;             // split-K partial block sums of the GEMM kernels
@@ -90,6 +107,11 @@ struct BParams {
   float* dbg_logits;        // optional [BMAX][V]
   const float* inv_freq;    // [D/2]
   float* rope;              // [BMAX][2][D/2] cos / sin of the step's position per sequence
+  int* flags;               // bk_step: [L][FC_N][FLAG_MAX] hand-off flags (epoch of the last write)
+  int* epoch;               // step epoch: bk_embed adds one per step, never reset
+  u64* trace;               // bk_step (optional): [L][TR_N][G] device wall-clock stamps per workgroup
+  int* err;                 // bk_step: MK_ERR_TIMEOUT when a hand-off wait gave up
+  unsigned long long timeout_ticks;  // bk_step: wall-clock ticks a hand-off wait may take
   int B, L, V, nsplit_max, max_steps;
   int prefill;              // 1: the columns are consecutive prompt tokens of one sequence whose
                             //    K / V bk_append has already stored (kv_seq = 0, shared cache)
@@ -123,25 +145,63 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 // sum of squares of its rows.  The consumer sums the H/16 partials in a fixed
 // order, r_b = rsqrt(mean(x_b^2) + eps), and scales its outputs by r_b:
 // W . (x * gain * r) = r * (W . (x * gain)).
+// Activation slots.  The one-kernel step (bk_step) gives every layer its own
+// copy of each activation buffer, so that within a launch every address is
+// written once, before anything reads it: readers then use ordinary cached
+// loads -- no cache can hold a stale copy, since every kernel starts with
+// invalidated caches -- and only the writers' stores are write-through.  The
+// per-phase kernels use slot 0 throughout (kernel boundaries order them).
+// Slot s of x / xg / ssq holds, as consumer c = 0, the hidden state entering
+// layer s with its attention-norm parts (s = L: the final-norm parts), and as
+// c = 1 the state after layer s's O projection with its FFN-norm parts.
 template <class S>
-__device__ __forceinline__ uint16_t* xg_plane(const BParams& p, int c, int lohi) {
-  return p.xg + ((long long)(2 * c + lohi) * BMAX) * S::H;
+__device__ __forceinline__ float* x_slot(const BParams& p, int slot, int c) {
+  return p.x + ((long long)(2 * slot + c) * BMAX) * S::H;
+}
+template <class S>
+__device__ __forceinline__ uint16_t* xg_plane(const BParams& p, int slot, int c, int lohi) {
+  return p.xg + ((long long)(4 * slot + 2 * c + lohi) * BMAX) * S::H;
+}
+template <class S>
+__device__ __forceinline__ float* ssq_slot(const BParams& p, int slot, int c) {
+  return p.ssq + (long long)(2 * slot + c) * (S::H / 16) * BMAX;
+}
+template <class S>
+__device__ __forceinline__ float* qkv_slot(const BParams& p, int slot) {
+  return p.qkv + (long long)slot * BMAX * S::QKV;
+}
+template <class S>
+__device__ __forceinline__ uint16_t* att_slot(const BParams& p, int slot) {
+  return p.att + (long long)slot * 2 * BMAX * S::QD;
+}
+template <class S>
+__device__ __forceinline__ uint16_t* act_slot(const BParams& p, int slot) {
+  return p.act + (long long)slot * 2 * BMAX * S::F;
 }
 
 // Epilogue of an x-producing 16-row block: thread t < 256 holds the new x of
 // row rb * 16 + t / 16, sequence t % 16.  red: >= 256 floats of LDS.
-template <class S>
-__device__ __forceinline__ void publish_x(const BParams& p, int c, const uint16_t* gain, int rb, float xn,
+// Stores of activations handed between workgroups: ordinary between kernels
+// (SC1 false); inside the one-kernel step write-through at agent scope, and
+// flagged on p.flags once acknowledged.
+template <bool SC1, class T>
+__device__ __forceinline__ void st_act(T* a, T v) {
+  if constexpr (SC1) __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *a = v;
+}
+
+template <class S, bool SC1 = false>
+__device__ __forceinline__ void publish_x(const BParams& p, int slot, int c, const uint16_t* gain, int rb, float xn,
                                           float* red) {
-  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
+  const int t = ltid(), row = rb * 16 + t / 16, b = t % 16;
   if (t < 256) {
     const bool on = b < p.B;
     if (on) {
-      p.x[(long long)b * S::H + row] = xn;
+      st_act<SC1>(x_slot<S>(p, slot, c) + (long long)b * S::H + row, xn);
       uint16_t h, o;
       split2(xn * bf16_to_f32(gain[row]), h, o);
-      xg_plane<S>(p, c, 0)[(long long)b * S::H + row] = h;
-      xg_plane<S>(p, c, 1)[(long long)b * S::H + row] = o;
+      st_act<SC1>(xg_plane<S>(p, slot, c, 0) + (long long)b * S::H + row, h);
+      st_act<SC1>(xg_plane<S>(p, slot, c, 1) + (long long)b * S::H + row, o);
     }
     red[t] = on ? xn * xn : 0.f;
   }
@@ -150,18 +210,36 @@ __device__ __forceinline__ void publish_x(const BParams& p, int c, const uint16_
     float ss = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) ss += red[r * 16 + t];
-    p.ssq[((long long)c * (S::H / 16) + rb) * BMAX + t] = ss;
+    st_act<SC1>(ssq_slot<S>(p, slot, c) + (long long)rb * BMAX + t, ss);
   }
 }
 
-// r_b of consumer c for b < BMAX into rr (threads t < BMAX; read after a barrier).
+// r_b of slot / consumer c for b < BMAX into rr[0 .. BMAX) (read after a
+// later barrier).  rr: RR_N floats of LDS; every thread of the workgroup
+// calls this.  Sixteen threads per sequence each sum a run of the H/16 block
+// sums (all their loads in flight together), then one thread per sequence
+// adds the sixteen runs in order.
+constexpr int RR_N = BMAX + 256;
 template <class S>
-__device__ __forceinline__ void rnorm(const BParams& p, int c, float* rr) {
-  const int t = threadIdx.x;
+__device__ __forceinline__ void rnorm(const BParams& p, int slot, int c, float* rr) {
+  constexpr int NB = S::H / 16, PER = (NB + 15) / 16;
+  const int t = ltid();
+  if (t < 256) {
+    const int b = t % 16, k = t / 16;
+    const float* q = ssq_slot<S>(p, slot, c) + b;
+    float v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = k * PER + i < NB ? q[(k * PER + i) * BMAX] : 0.f;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) sum += v[i];
+    rr[BMAX + t] = sum;
+  }
+  __syncthreads();
   if (t < BMAX) {
-    const float* q = p.ssq + (long long)c * (S::H / 16) * BMAX + t;
     float ss = 0.f;
-    for (int rb = 0; rb < S::H / 16; ++rb) ss += q[rb * BMAX];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ss += rr[BMAX + k * 16 + t];
     rr[t] = rsqrtf(ss / (float)S::H + kRmsEps);
   }
 }
@@ -213,6 +291,31 @@ __device__ __forceinline__ f32x4 tiles_mma(const ATiles<NT>& a, const uint16_t* 
   return a0 + a1;
 }
 
+// Two blocks' tiles (gate and up) times the same 16 activation columns: the
+// B operands are loaded once.  Each result equals tiles_mma of that block.
+template <int NT>
+__device__ __forceinline__ void tiles_mma2(const ATiles<NT>& a, const ATiles<NT>& c, const uint16_t* hi,
+                                           const uint16_t* lo, int ld, int kt0, f32x4& ra, f32x4& rc) {
+  const unsigned l = lane_id();
+  const int w = wave_id();
+  const int bo = (int)(l & 15u) * ld + 8 * (int)(l >> 4);
+  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0, c0 = a0, c1 = a0;
+#pragma unroll
+  for (int j = 0; j < ATiles<NT>::TW; ++j) {
+    const int kt = kt0 + w + GW * j;
+    if (w + GW * j < NT) {
+      const u32x4 bh = *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt);
+      const u32x4 bl = *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt);
+      a0 = mfma(a.t[j], bh, a0);
+      a1 = mfma(a.t[j], bl, a1);
+      c0 = mfma(c.t[j], bh, c0);
+      c1 = mfma(c.t[j], bl, c1);
+    }
+  }
+  ra = a0 + a1;
+  rc = c0 + c1;
+}
+
 // K splits of a 16-row block run on KS workgroups; each publishes its block
 // sums (thread t < 256: row t / 16, column t % 16; NV values per thread) with
 // write-through stores, and the workgroup that completes the block (an
@@ -222,7 +325,7 @@ __device__ __forceinline__ f32x4 tiles_mma(const ATiles<NT>& a, const uint16_t* 
 template <int NV>
 __device__ __forceinline__ bool splitk_finish(const BParams& p, int rb, int ks, int KS, float (&v)[NV], int* last) {
   if (KS == 1) return true;  // one workgroup per block: its sums are the totals
-  const int t = threadIdx.x;
+  const int t = ltid();
   float* buf = p.gpart + ((long long)rb * KS) * 256 * NV;
   if (t < 256) {
 #pragma unroll
@@ -276,7 +379,7 @@ __global__ __launch_bounds__(256) void bk_embed(BParams p) {
   __shared__ float xs[S::H];
   const int b = blockIdx.x;
   if (b >= BMAX) return;
-  const int t = threadIdx.x;
+  const int t = ltid();
   const bool on = b < p.B;
   const int t_ = on ? p.tok[b] : 0;
   const int tok = t_ < 0 ? 0 : (t_ >= p.V ? p.V - 1 : t_);  // tokens are validated on the host; never index outside
@@ -287,11 +390,11 @@ __global__ __launch_bounds__(256) void bk_embed(BParams p) {
     const float xv = on ? bf16_to_f32(u[e]) : 0.f;
     xs[k] = xv;
     if (on) {
-      p.x[(long long)b * S::H + k] = xv;
+      x_slot<S>(p, 0, 0)[(long long)b * S::H + k] = xv;
       uint16_t h, o;
       split2(xv * bf16_to_f32(p.norms[S::NORM_ATTN + k]), h, o);
-      xg_plane<S>(p, 0, 0)[(long long)b * S::H + k] = h;
-      xg_plane<S>(p, 0, 1)[(long long)b * S::H + k] = o;
+      xg_plane<S>(p, 0, 0, 0)[(long long)b * S::H + k] = h;
+      xg_plane<S>(p, 0, 0, 1)[(long long)b * S::H + k] = o;
     }
   }
   __syncthreads();
@@ -299,7 +402,7 @@ __global__ __launch_bounds__(256) void bk_embed(BParams p) {
     float ss = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) ss += xs[rb * 16 + r] * xs[rb * 16 + r];
-    p.ssq[(long long)rb * BMAX + b] = ss;
+    ssq_slot<S>(p, 0, 0)[(long long)rb * BMAX + b] = ss;
   }
   if (t < S::D / 2) {  // RoPE angles of this step's position, shared by every layer
     float sn, cs;
@@ -308,90 +411,183 @@ __global__ __launch_bounds__(256) void bk_embed(BParams p) {
     p.rope[(b * 2 + 1) * (S::D / 2) + t] = sn;
   }
   if (t == 0) p.keys[b] = 0ull;
+  if (p.epoch && b == 0 && t == 0) *p.epoch += 1;  // this step's epoch for bk_step's hand-off flags
 }
 
-// rmsnorm(x) -> q|k|v rows of block blockIdx.x for every sequence.
-template <class S>
-__global__ __launch_bounds__(GT) void bk_qkv(BParams p, int layer) {
-  __shared__ float red[GW * 16 * 17];
-  __shared__ float rr[BMAX];
-  __shared__ int last;
+// Hand-off flag of producer `idx` of a phase of the one-kernel step: every
+// thread's stores are acknowledged (write-through) before one thread writes
+// the epoch.
+__device__ __forceinline__ void fc_done(const BParams& p, int layer, int ph, int idx, int ep) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (ltid() == 0)
+    __hip_atomic_store(p.flags + ((long long)layer * FC_N + ph) * FLAG_MAX + idx, ep, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until the flags of producers 0 .. n - 1 of phase ph of `layer` hold
+// epoch ep: wave 0 polls them (up to FLAG_MAX / 64 words per lane, all loads
+// of a round in flight together), the workgroup follows; false when the
+// wait gave up (p.err is set).
+__device__ __forceinline__ bool fc_wait(const BParams& p, int layer, int ph, int n, int ep) {
+  int ok = 1;
+  if (wave_id() == 0) {
+    const auto rs = make_rsrc(p.flags + ((long long)layer * FC_N + ph) * FLAG_MAX);
+    const unsigned l = lane_id();
+    Spin sp;
+    while (true) {
+      int v[FLAG_MAX / kWave];
+#pragma unroll
+      for (int k = 0; k < FLAG_MAX / kWave; ++k)
+        v[k] = (int)l + kWave * k < n ? (int)__builtin_amdgcn_raw_buffer_load_b32(rs, (l + kWave * k) * 4u, 0u, 16) : ep;
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < FLAG_MAX / kWave; ++k) ready &= v[k] == ep;
+      if (__all(ready)) break;
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        ok = 0;
+        break;
+      }
+    }
+  }
+  return __syncthreads_and(ok) != 0;
+}
+
+// The GEMM phases as block functions.  FUSED (bk_step): the block's weight
+// tiles are issued, then `ready()` waits for its inputs, which are read at
+// agent scope, and the outputs are flagged on p.flags; otherwise (one kernel per
+// phase) ready() is trivially true.  Each returns false only when ready()
+// gave up.
+struct NoWait {
+  __device__ __forceinline__ bool operator()() const { return true; }
+};
+
+// rmsnorm(x) -> q|k|v rows of block rb for every sequence.
+template <class S, bool FUSED, class Ready>
+__device__ __forceinline__ bool qkv_block(const BParams& p, int layer, int ep, int rb, int ks, float* red, float* rr, int* last,
+                                          const Ready& ready) {
   constexpr int NT = S::KT_H / KS_QKV;
-  const int rb = blockIdx.x / KS_QKV, ks = blockIdx.x % KS_QKV, kt0 = ks * NT;
+  const int kt0 = ks * NT;
   ATiles<NT> a;
   load_tiles(a, p.wqkv + layer * p.u_qkv + (long long)rb * S::KT_H * 64, kt0);
-  rnorm<S>(p, 0, rr);
-  float v[1] = {block_reduce(tiles_mma(a, xg_plane<S>(p, 0, 0), xg_plane<S>(p, 0, 1), S::H, kt0), red)};
-  if (!splitk_finish(p, rb, ks, KS_QKV, v, &last)) return;
-  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
-  if (t < 256 && b < p.B) p.qkv[(long long)b * S::QKV + row] = v[0] * rr[b];
+  if (!ready()) return false;
+  const int sl = FUSED ? layer : 0;
+  rnorm<S>(p, sl, 0, rr);
+  float v[1] = {block_reduce(tiles_mma<NT>(a, xg_plane<S>(p, sl, 0, 0), xg_plane<S>(p, sl, 0, 1), S::H, kt0), red)};
+  if (!splitk_finish(p, rb, ks, KS_QKV, v, last)) return true;
+  const int t = ltid(), row = rb * 16 + t / 16, b = t % 16;
+  if (t < 256 && b < p.B) st_act<FUSED>(qkv_slot<S>(p, sl) + (long long)b * S::QKV + row, v[0] * rr[b]);
+  if constexpr (FUSED) fc_done(p, layer, FC_QKV, rb, ep);
+  return true;
 }
 
 // O projection + residual: x[b][row] += Wo[row] . att[b]; x published for the FFN norm.
-template <class S>
-__global__ __launch_bounds__(GT) void bk_o(BParams p, int layer) {
-  __shared__ float red[GW * 16 * 17];
-  __shared__ int last;
+template <class S, bool FUSED, class Ready>
+__device__ __forceinline__ bool o_block(const BParams& p, int layer, int ep, int rb, int ks, float* red, int* last,
+                                        const Ready& ready) {
   constexpr int NT = S::KT_Q / KS_O;
-  const int rb = blockIdx.x / KS_O, ks = blockIdx.x % KS_O, kt0 = ks * NT;
+  const int kt0 = ks * NT;
   ATiles<NT> a;
   load_tiles(a, p.wo + layer * p.u_o + (long long)rb * S::KT_Q * 64, kt0);
-  float v[1] = {block_reduce(tiles_mma(a, p.att, p.att + BMAX * S::QD, S::QD, kt0), red)};
-  if (!splitk_finish(p, rb, ks, KS_O, v, &last)) return;
-  const int t = threadIdx.x, b = t % 16;
-  const float xn = t < 256 && b < p.B ? p.x[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
+  if (!ready()) return false;
+  const int sl = FUSED ? layer : 0;
+  const uint16_t* at = att_slot<S>(p, sl);
+  float v[1] = {block_reduce(tiles_mma<NT>(a, at, at + BMAX * S::QD, S::QD, kt0), red)};
+  if (!splitk_finish(p, rb, ks, KS_O, v, last)) return true;
+  const int t = ltid(), b = t % 16;
+  const float xn = t < 256 && b < p.B ? x_slot<S>(p, sl, 0)[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
   __syncthreads();  // red is reused
-  publish_x<S>(p, 1, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, rb, xn, red);
+  publish_x<S, FUSED>(p, sl, 1, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, rb, xn, red);
+  if constexpr (FUSED) fc_done(p, layer, FC_O, rb, ep);
+  return true;
 }
 
-// rmsnorm(x) -> gate and up rows of block blockIdx.x -> SiLU(g) * u parts.
-template <class S>
-__global__ __launch_bounds__(GT) void bk_gu(BParams p, int layer) {
-  __shared__ float red[GW * 16 * 17];
-  __shared__ float rr[BMAX];
-  __shared__ int last;
+// rmsnorm(x) -> gate and up rows of block rb -> SiLU(g) * u parts.
+template <class S, bool FUSED, class Ready>
+__device__ __forceinline__ bool gu_block(const BParams& p, int layer, int ep, int rb, int ks, float* red, float* rr, int* last,
+                                         const Ready& ready) {
   constexpr int NT = S::KT_H / KS_GU;
-  const int rb = blockIdx.x / KS_GU, ks = blockIdx.x % KS_GU, kt0 = ks * NT;
+  const int kt0 = ks * NT;
   const long long off = (long long)rb * S::KT_H * 64;
   ATiles<NT> ag, au;
   load_tiles(ag, p.wg + layer * p.u_gu + off, kt0);
   load_tiles(au, p.wu + layer * p.u_gu + off, kt0);
-  rnorm<S>(p, 1, rr);
-  const uint16_t *hi = xg_plane<S>(p, 1, 0), *lo = xg_plane<S>(p, 1, 1);
+  if (!ready()) return false;
+  const int sl = FUSED ? layer : 0;
+  rnorm<S>(p, sl, 1, rr);
+  const uint16_t *hi = xg_plane<S>(p, sl, 1, 0), *lo = xg_plane<S>(p, sl, 1, 1);
+  f32x4 pg, pu;
+  tiles_mma2<NT>(ag, au, hi, lo, S::H, kt0, pg, pu);
   float v[2];
-  v[0] = block_reduce(tiles_mma(ag, hi, lo, S::H, kt0), red);
+  v[0] = block_reduce(pg, red);
   __syncthreads();
-  v[1] = block_reduce(tiles_mma(au, hi, lo, S::H, kt0), red);
-  if (!splitk_finish(p, rb, ks, KS_GU, v, &last)) return;
-  const int t = threadIdx.x, row = rb * 16 + t / 16, b = t % 16;
+  v[1] = block_reduce(pu, red);
+  if (!splitk_finish(p, rb, ks, KS_GU, v, last)) return true;
+  const int t = ltid(), row = rb * 16 + t / 16, b = t % 16;
   if (t < 256 && b < p.B) {
     const float g = v[0] * rr[b], u = v[1] * rr[b];
     uint16_t h, o;
     split2(g / (1.0f + __expf(-g)) * u, h, o);  // SiLU(g) * u (reference utils.cuh:59-61)
-    p.act[(long long)b * S::F + row] = h;
-    p.act[(long long)(BMAX + b) * S::F + row] = o;
+    st_act<FUSED>(act_slot<S>(p, sl) + (long long)b * S::F + row, h);
+    st_act<FUSED>(act_slot<S>(p, sl) + (long long)(BMAX + b) * S::F + row, o);
   }
+  if constexpr (FUSED) fc_done(p, layer, FC_GU, rb, ep);
+  return true;
 }
 
 // Down projection + residual: x[b][row] += Wd[row] . act[b]; x published for
 // the next layer's attention norm (the final norm after the last layer).
+template <class S, bool FUSED, class Ready>
+__device__ __forceinline__ bool down_block(const BParams& p, int layer, int ep, int rb, int ks, float* red, int* last,
+                                           const Ready& ready) {
+  static_assert(S::KT_F % KS_DN == 0, "whole tiles per K split");
+  constexpr int NT = S::KT_F / KS_DN;
+  const int kt0 = ks * NT;
+  ATiles<NT> a;
+  load_tiles(a, p.wd + layer * p.u_dn + (long long)rb * S::KT_F * 64, kt0);
+  if (!ready()) return false;
+  const int sl = FUSED ? layer : 0;
+  const uint16_t* ac = act_slot<S>(p, sl);
+  float v[1] = {block_reduce(tiles_mma<NT>(a, ac, ac + BMAX * S::F, S::F, kt0), red)};
+  if (!splitk_finish(p, rb, ks, KS_DN, v, last)) return true;
+  const int t = ltid(), b = t % 16;
+  const float xn = t < 256 && b < p.B ? x_slot<S>(p, sl, 1)[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
+  __syncthreads();  // red is reused
+  const uint16_t* gain = layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE + S::NORM_ATTN
+                                         : p.final_norm;
+  publish_x<S, FUSED>(p, FUSED ? layer + 1 : 0, 0, gain, rb, xn, red);
+  if constexpr (FUSED) fc_done(p, layer, FC_DN, rb, ep);
+  return true;
+}
+
+template <class S>
+__global__ __launch_bounds__(GT) void bk_qkv(BParams p, int layer) {
+  __shared__ float red[GW * 16 * 17];
+  __shared__ float rr[RR_N];
+  __shared__ int last;
+  qkv_block<S, false>(p, layer, 0, blockIdx.x / KS_QKV, blockIdx.x % KS_QKV, red, rr, &last, NoWait{});
+}
+
+template <class S>
+__global__ __launch_bounds__(GT) void bk_o(BParams p, int layer) {
+  __shared__ float red[GW * 16 * 17];
+  __shared__ int last;
+  o_block<S, false>(p, layer, 0, blockIdx.x / KS_O, blockIdx.x % KS_O, red, &last, NoWait{});
+}
+
+template <class S>
+__global__ __launch_bounds__(GT) void bk_gu(BParams p, int layer) {
+  __shared__ float red[GW * 16 * 17];
+  __shared__ float rr[RR_N];
+  __shared__ int last;
+  gu_block<S, false>(p, layer, 0, blockIdx.x / KS_GU, blockIdx.x % KS_GU, red, rr, &last, NoWait{});
+}
+
 template <class S>
 __global__ __launch_bounds__(GT) void bk_down(BParams p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ int last;
-  static_assert(S::KT_F % KS_DN == 0, "whole tiles per K split");
-  constexpr int NT = S::KT_F / KS_DN;
-  const int rb = blockIdx.x / KS_DN, ks = blockIdx.x % KS_DN, kt0 = ks * NT;
-  ATiles<NT> a;
-  load_tiles(a, p.wd + layer * p.u_dn + (long long)rb * S::KT_F * 64, kt0);
-  float v[1] = {block_reduce(tiles_mma(a, p.act, p.act + BMAX * S::F, S::F, kt0), red)};
-  if (!splitk_finish(p, rb, ks, KS_DN, v, &last)) return;
-  const int t = threadIdx.x, b = t % 16;
-  const float xn = t < 256 && b < p.B ? p.x[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
-  __syncthreads();  // red is reused
-  const uint16_t* gain = layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE + S::NORM_ATTN
-                                         : p.final_norm;
-  publish_x<S>(p, 0, gain, rb, xn, red);
+  down_block<S, false>(p, layer, 0, blockIdx.x / KS_DN, blockIdx.x % KS_DN, red, &last, NoWait{});
 }
 
 // Final rmsnorm -> tied LM head -> per-sequence argmax (reference
@@ -399,22 +595,22 @@ __global__ __launch_bounds__(GT) void bk_down(BParams p, int layer) {
 // ordered(logit) << 32 | (0xffffffff - index), combined with an atomic max, so
 // the result is the largest logit and, among equal logits, the lowest index.
 template <class S, bool F8 = false>
-__global__ __launch_bounds__(GT) void bk_lm(BParams p) {
+__global__ __launch_bounds__(GT) void bk_lm(BParams p, int slot) {
   // F8: the FP8 copy; a lane's 16 bytes (row l & 15, columns 64 u + 16 kg ..
   // + 15 of unit u) feed two MFMA k-steps, whose B operands take the same
   // columns of the hidden state; the row scale enters the conversion
   constexpr int LD = S::H + 8;  // padded LDS rows: the 16 sequences on different banks
   __shared__ __attribute__((aligned(16))) uint16_t hi[BMAX * LD], lo[BMAX * LD];
   __shared__ u64 best_w[GW][BMAX];
-  __shared__ float rr[BMAX];
+  __shared__ float rr[RR_N];
   {  // the final-norm parts published by the last layer, copied to LDS
-    const uint16_t *gh = xg_plane<S>(p, 0, 0), *gl = xg_plane<S>(p, 0, 1);
+    const uint16_t *gh = xg_plane<S>(p, slot, 0, 0), *gl = xg_plane<S>(p, slot, 0, 1);
     for (int i = threadIdx.x; i < BMAX * S::H / 8; i += GT) {
       const int b = i / (S::H / 8), k = (i % (S::H / 8)) * 8;
       *reinterpret_cast<u32x4*>(hi + b * LD + k) = *reinterpret_cast<const u32x4*>(gh + (long long)b * S::H + k);
       *reinterpret_cast<u32x4*>(lo + b * LD + k) = *reinterpret_cast<const u32x4*>(gl + (long long)b * S::H + k);
     }
-    rnorm<S>(p, 0, rr);
+    rnorm<S>(p, slot, 0, rr);
   }
   __syncthreads();
   const unsigned l = lane_id();
@@ -529,7 +725,7 @@ __global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
   const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
   const int pos = p.pos[b];
   const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
-  float v = p.qkv[(long long)b * S::QKV + (w == 0 ? S::QD + g * D : S::QD + S::KVD + g * D) + l];
+  float v = qkv_slot<S>(p, 0)[(long long)b * S::QKV + (w == 0 ? S::QD + g * D : S::QD + S::KVD + g * D) + l];
   if (w == 0) {
     const float ss = wave_sum(v * v);
     v = v * rsqrtf(ss / (float)D + kRmsEps) *
@@ -558,33 +754,37 @@ __global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
 // cores exactly as the batch-1 kernel does: scores^T = K . Qb with q split into
 // three bf16 parts in rows 4 j + 0..2 (j = q head of the group), and
 // out^T = V^T . Pb with the softmax weights split the same way.
-// Five 256-thread items per CU (<= 102 registers per lane): the 16-sequence
-// step at KV 512-4096 has ~1,100 items; with four per CU the last ~10 % ran
-// as a second, latency-bound residency wave.
-constexpr int ATTN_WAVES_PER_EU = AT == 256 ? 5 : 2;
-template <class S, bool K8 = false>
-__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_PER_EU, ATTN_WAVES_PER_EU))) void bk_attn(
-    BParams p, int layer) {
+template <class S>
+struct AttnLds {
+  static constexpr int D = S::D;
+  float kcs[2];  // FP8: scales of position pos's K / V rows
+  __attribute__((aligned(16))) uint16_t qb[16][D];       // q parts (A operand of the scores)
+  __attribute__((aligned(16))) uint16_t pb[AW][16][32];  // weight parts (A operand of the output)
+  __attribute__((aligned(16))) uint16_t kcur[D], vcur[D];  // K / V of position pos
+  float rc[D / 2], rsn[D / 2];
+  float mw[AW][2], lw[AW][2], ow[AW][2][D];
+  float cm[AT / (2 * D)][2 * D], cl[AT / (2 * D)][2 * D], co[AT / (2 * D)][2 * D];  // split-group merge
+  int last;
+};
+
+// The item's code for AT threads (local thread threadIdx.x % AT).
+// FUSED: inside bk_step, where the two AT-thread halves of a workgroup run
+// two items and share every barrier: `on` false (a half without an item)
+// passes the barriers only; the item reads its layer's qkv slot and writes
+// its layer's att slot (write-through), flagged on p.flags.  Otherwise (bk_attn) one
+// item per workgroup, always on.
+// ready(): as for the GEMM blocks, between the K / V loads and the first read
+// of q / k / v; the return is false only when it gave up.
+template <class S, bool K8, bool FUSED, class Ready>
+__device__ __forceinline__ bool attn_item(const BParams& p, int layer, int ep, AttnLds<S>& sm, bool on, int b, int g,
+                                          int s, int nsplit, int pos, const Ready& ready) {
   static_assert(S::GQA == 2 && S::D == 64, "batched attention is built for 2 q heads of 64 per kv head");
   constexpr int D = S::D, NKV = S::NKV;
   // K8: the FP8 cache (codes converted to bf16 in registers, exact; the K
   // row scale enters that conversion, the V row scale the softmax weight)
   using Reg = typename std::conditional<K8, u32x2, u32x4>::type;
-  __shared__ float kcs[2];  // FP8: scales of position pos's K / V rows
-  __shared__ __attribute__((aligned(16))) uint16_t qb[16][D];          // q parts (A operand of the scores)
-  __shared__ __attribute__((aligned(16))) uint16_t pb[AW][16][32];     // weight parts (A operand of the output)
-  __shared__ __attribute__((aligned(16))) uint16_t kcur[D], vcur[D];   // bf16 K / V of position pos
-  __shared__ float rc[D / 2], rsn[D / 2];
-  __shared__ float mw[AW][2], lw[AW][2], ow[AW][2][D];
-  __shared__ float cm[AT / (2 * D)][2 * D], cl[AT / (2 * D)][2 * D], co[AT / (2 * D)][2 * D];  // split-group merge
-  __shared__ int last;
-  const int item = blockIdx.x;
-  const int b = item / (NKV * p.nsplit_max), g = (item / p.nsplit_max) % NKV, s = item % p.nsplit_max;
-  if (b >= p.B) return;
-  const int pos = p.pos[b], n = pos + 1;
-  const int nsplit = (n + CH - 1) / CH;
-  if (s >= nsplit) return;
-  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+  const int n = on ? pos + 1 : 0;
+  const int tid = ltid() % AT, w = tid / kWave, l = tid % kWave;
   const unsigned lu = (unsigned)l;
   const int c16 = l & 15, rg = l >> 4;
   const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
@@ -593,95 +793,100 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
   Reg kr[NBW][2][2], vr[NBW][D / 16];
   float sk[K8 ? NBW : 1][2], sv[K8 ? NBW : 1][2];  // FP8: scales of the lane's score positions
   const long long sbase = (long long)b * p.sc_seq + ((long long)layer * NKV + g) * p.s_pad;
+  if (on) {
 #pragma unroll
-  for (int q = 0; q < NBW; ++q) {
-    int blk = s * AW * NBW + w + AW * q;
-    blk = 32 * blk < n ? blk : s * AW * NBW;
-    if constexpr (K8) {  // byte index = element index of the bf16 layout
-      const auto rk = make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + kbase + (long long)blk * 32 * D);
-      const auto rv = make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + kbase + (long long)blk * 32 * D);
-      const auto rks = make_rsrc(p.kscale + sbase + (long long)blk * 32);
-      const auto rvs = make_rsrc(p.vscale + sbase + (long long)blk * 32);
+    for (int q = 0; q < NBW; ++q) {
+      int blk = s * AW * NBW + w + AW * q;
+      blk = 32 * blk < n ? blk : s * AW * NBW;
+      if constexpr (K8) {  // byte index = element index of the bf16 layout
+        const auto rk = make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + kbase + (long long)blk * 32 * D);
+        const auto rv = make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + kbase + (long long)blk * 32 * D);
+        const auto rks = make_rsrc(p.kscale + sbase + (long long)blk * 32);
+        const auto rvs = make_rsrc(p.vscale + sbase + (long long)blk * 32);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-          kr[q][h][kc] =
-              __builtin_amdgcn_raw_buffer_load_b64(rk, (16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4), 0u, 2);
-        sk[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rks, (16u * h + (lu & 15u)) * 4u, 0u, 2));
-        sv[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rvs, (16u * h + (lu & 15u)) * 4u, 0u, 2));
+          for (int kc = 0; kc < 2; ++kc)
+            kr[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b64(rk, (16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4),
+                                                                0u, 2);
+          sk[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rks, (16u * h + (lu & 15u)) * 4u, 0u, 2));
+          sv[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rvs, (16u * h + (lu & 15u)) * 4u, 0u, 2));
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+          vr[q][dt] = __builtin_amdgcn_raw_buffer_load_b64(rv, (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4), 0u, 2);
+      } else {
+        const auto rk = make_rsrc(p.kv + kbase + (long long)blk * 32 * D);
+        const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc)
+            kr[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b128(
+                rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+          vr[q][dt] =
+              __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
       }
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt)
-        vr[q][dt] = __builtin_amdgcn_raw_buffer_load_b64(rv, (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4), 0u, 2);
-    } else {
-      const auto rk = make_rsrc(p.kv + kbase + (long long)blk * 32 * D);
-      const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-          kr[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b128(
-              rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt)
-        vr[q][dt] =
-            __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
     }
   }
-  for (int i = tid; i < 16 * D; i += AT) (&qb[0][0])[i] = 0;
-  for (int i = tid; i < AW * 16 * 32; i += AT) (&pb[0][0][0])[i] = 0;
-  if (tid < D / 2) {
-    rc[tid] = p.rope[(b * 2 + 0) * (D / 2) + tid];
-    rsn[tid] = p.rope[(b * 2 + 1) * (D / 2) + tid];
+  for (int i = tid; i < 16 * D; i += AT) (&sm.qb[0][0])[i] = 0;
+  for (int i = tid; i < AW * 16 * 32; i += AT) (&sm.pb[0][0][0])[i] = 0;
+  if (on && tid < D / 2) {
+    sm.rc[tid] = p.rope[(b * 2 + 0) * (D / 2) + tid];
+    sm.rsn[tid] = p.rope[(b * 2 + 1) * (D / 2) + tid];
   }
+  if (!ready()) return false;
   __syncthreads();
   // 1. q heads (waves 0, 1), k (wave 2), v (wave 3) of position pos: QK-norm
   //    (reference rmsnorm.cuh:57-84) and RoPE rotate-half (attention.cuh:22-44)
-  const float* src = p.qkv + (long long)b * S::QKV +
+  const int sl = FUSED ? layer : 0;
+  const float* src = qkv_slot<S>(p, sl) + (long long)b * S::QKV +
                      (w < 2 ? (g * 2 + w) * D : (w == 2 ? S::QD + g * D : S::QD + S::KVD + g * D));
-  float v = src[l];
-  const bool own = !p.prefill && pos >= s * CH && pos < (s + 1) * CH;
-  if (w < 3) {
+  const float v0 = on ? src[l] : 0.f;
+  float v = v0;
+  const bool own = on && !p.prefill && pos >= s * CH && pos < (s + 1) * CH;
+  if (on && w < 3) {
     const float ss = wave_sum(v * v);
     const uint16_t* gn = p.norms + (long long)layer * S::NORM_STRIDE + (w < 2 ? S::NORM_Q : S::NORM_K);
     v = v * rsqrtf(ss / (float)D + kRmsEps) * bf16_to_f32(gn[l]);
     const float partner = lane_xor32(v);
     const int d = l & 31;
-    v = l < 32 ? v * rc[d] - partner * rsn[d] : v * rc[d] + partner * rsn[d];
+    v = l < 32 ? v * sm.rc[d] - partner * sm.rsn[d] : v * sm.rc[d] + partner * sm.rsn[d];
     if (w < 2) {
       uint16_t h, m, o;
       split_bf16(v, h, m, o);
-      qb[4 * w + 0][l] = h;
-      qb[4 * w + 1][l] = m;
-      qb[4 * w + 2][l] = o;
+      sm.qb[4 * w + 0][l] = h;
+      sm.qb[4 * w + 1][l] = m;
+      sm.qb[4 * w + 2][l] = o;
     } else if constexpr (K8) {  // FP8 append: the row's power-of-two scale from the wave's max
       const int e = e4m3_row_exp(wave_max(fabsf(v)));
       const uint8_t code = (uint8_t)e4m3_encode(ldexpf(v, -e));
-      reinterpret_cast<uint8_t*>(kcur)[l] = code;
-      if (l == 0) kcs[0] = ldexpf(1.f, e);
+      reinterpret_cast<uint8_t*>(sm.kcur)[l] = code;
+      if (l == 0) sm.kcs[0] = ldexpf(1.f, e);
       if (own) {
         reinterpret_cast<uint8_t*>(p.kv)[kbase + (long long)pos * D + l] = code;
         if (l == 0) p.kscale[sbase + pos] = ldexpf(1.f, e);
       }
     } else {
       const uint16_t kb = f32_to_bf16(v);
-      kcur[l] = kb;
+      sm.kcur[l] = kb;
       if (own) p.kv[kbase + (long long)pos * D + l] = kb;  // KV append (reference kv_cache.cuh:58-78)
     }
-  } else if (w == 3) {
+  } else if (on && w == 3) {
     if constexpr (K8) {
       const int e = e4m3_row_exp(wave_max(fabsf(v)));
       const uint8_t code = (uint8_t)e4m3_encode(ldexpf(v, -e));
-      reinterpret_cast<uint8_t*>(vcur)[l] = code;
-      if (l == 0) kcs[1] = ldexpf(1.f, e);
+      reinterpret_cast<uint8_t*>(sm.vcur)[l] = code;
+      if (l == 0) sm.kcs[1] = ldexpf(1.f, e);
       if (own) {
         reinterpret_cast<uint8_t*>(p.kvt)[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = code;
         if (l == 0) p.vscale[sbase + pos] = ldexpf(1.f, e);
       }
     } else {
       const uint16_t vb = f32_to_bf16(v);
-      vcur[l] = vb;
+      sm.vcur[l] = vb;
       if (own) p.kvt[kbase + (long long)(pos / 32) * 32 * D + (long long)l * 32 + (pos % 32)] = vb;
     }
   }
@@ -695,25 +900,25 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
 #pragma unroll
   for (int q = 0; q < NBW; ++q) {
     const int t0 = 32 * (s * AW * NBW + w + AW * q);
-    if (t0 >= n) break;  // uniform over the wave
+    if (t0 >= n) break;  // uniform over the wave (every block of an item that is off)
     // position pos takes K / V from LDS (this item appended them; in a
     // prefill bk_append stored them before this kernel)
     if (!p.prefill && pos >= t0 && pos < t0 + 32) {
       const int rp = pos - t0;
       if constexpr (K8) {
         if (c16 == (rp & 15)) {  // register arrays take compile-time indices only
-          const uint8_t* kc8 = reinterpret_cast<const uint8_t*>(kcur);
+          const uint8_t* kc8 = reinterpret_cast<const uint8_t*>(sm.kcur);
 #pragma unroll
           for (int kc = 0; kc < 2; ++kc) {
             const u32x2 kv = *reinterpret_cast<const u32x2*>(&kc8[32 * kc + 8 * rg]);
             if (rp >> 4) kr[q][1][kc] = kv;
             else kr[q][0][kc] = kv;
           }
-          if (rp >> 4) sk[q][1] = kcs[0], sv[q][1] = kcs[1];
-          else sk[q][0] = kcs[0], sv[q][0] = kcs[1];
+          if (rp >> 4) sk[q][1] = sm.kcs[0], sv[q][1] = sm.kcs[1];
+          else sk[q][0] = sm.kcs[0], sv[q][0] = sm.kcs[1];
         }
         if (rg == (rp >> 3)) {
-          const uint8_t* vc8 = reinterpret_cast<const uint8_t*>(vcur);
+          const uint8_t* vc8 = reinterpret_cast<const uint8_t*>(sm.vcur);
 #pragma unroll
           for (int dt = 0; dt < D / 16; ++dt) vr[q][dt] = set_u8(vr[q][dt], rp & 7, vc8[16 * dt + c16]);
         }
@@ -721,14 +926,14 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
         if (c16 == (rp & 15)) {  // register arrays take compile-time indices only
 #pragma unroll
           for (int kc = 0; kc < 2; ++kc) {
-            const u32x4 kv = *reinterpret_cast<const u32x4*>(&kcur[32 * kc + 8 * rg]);
+            const u32x4 kv = *reinterpret_cast<const u32x4*>(&sm.kcur[32 * kc + 8 * rg]);
             if (rp >> 4) kr[q][1][kc] = kv;
             else kr[q][0][kc] = kv;
           }
         }
         if (rg == (rp >> 3)) {
 #pragma unroll
-          for (int dt = 0; dt < D / 16; ++dt) vr[q][dt] = with_bf16(vr[q][dt], rp & 7, vcur[16 * dt + c16]);
+          for (int dt = 0; dt < D / 16; ++dt) vr[q][dt] = with_bf16(vr[q][dt], rp & 7, sm.vcur[16 * dt + c16]);
         }
       }
     }
@@ -741,7 +946,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
         u32x4 kb;
         if constexpr (K8) kb = fp8x8_to_bf16x8_scaled(kr[q][h][kc], sk[q][h]);
         else kb = kr[q][h][kc];
-        d4 = mfma(*reinterpret_cast<const u32x4*>(&qb[c16][32 * kc + 8 * rg]), kb, d4);
+        d4 = mfma(*reinterpret_cast<const u32x4*>(&sm.qb[c16][32 * kc + 8 * rg]), kb, d4);
       }
       const int t = t0 + 16 * h + c16;
       sc[h] = t < n ? ((d4[0] + d4[1]) + d4[2]) * scale : -INFINITY;
@@ -760,13 +965,13 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const Split3 a = split3(K8 ? sc[h] * sv[q][h] : sc[h]);
-        pb[w][4 * rg + 0][16 * h + c16] = (uint16_t)(a.hi >> 16);
-        pb[w][4 * rg + 1][16 * h + c16] = (uint16_t)(a.mid >> 16);
-        pb[w][4 * rg + 2][16 * h + c16] = (uint16_t)(a.lo >> 16);
+        sm.pb[w][4 * rg + 0][16 * h + c16] = (uint16_t)(a.hi >> 16);
+        sm.pb[w][4 * rg + 1][16 * h + c16] = (uint16_t)(a.mid >> 16);
+        sm.pb[w][4 * rg + 2][16 * h + c16] = (uint16_t)(a.lo >> 16);
       }
     }
     asm volatile("" ::: "memory");  // LDS operations of one wave complete in order
-    const u32x4 pa = *reinterpret_cast<const u32x4*>(&pb[w][c16][8 * rg]);
+    const u32x4 pa = *reinterpret_cast<const u32x4*>(&sm.pb[w][c16][8 * rg]);
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) {
 #pragma unroll
@@ -778,25 +983,25 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
   // 3. combine the waves into the item's partial
   if (rg < 2) {
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) ow[w][rg][16 * dt + c16] = (acc[dt][0] + acc[dt][1]) + acc[dt][2];
+    for (int dt = 0; dt < D / 16; ++dt) sm.ow[w][rg][16 * dt + c16] = (acc[dt][0] + acc[dt][1]) + acc[dt][2];
     if (c16 == 0) {
-      mw[w][rg] = m;
-      lw[w][rg] = lsum;
+      sm.mw[w][rg] = m;
+      sm.lw[w][rg] = lsum;
     }
   }
   __syncthreads();
   float* part = p.part + (((long long)b * NKV + g) * p.nsplit_max + s) * PW;
-  if (tid < 2 * D) {
+  if (on && tid < 2 * D) {
     const int h = tid / D, d = tid % D;
-    float M = mw[0][h];
+    float M = sm.mw[0][h];
 #pragma unroll
-    for (int i = 1; i < AW; ++i) M = fmaxf(M, mw[i][h]);
+    for (int i = 1; i < AW; ++i) M = fmaxf(M, sm.mw[i][h]);
     float o = 0.f, L = 0.f;
 #pragma unroll
     for (int i = 0; i < AW; ++i) {
-      const float f = __expf(mw[i][h] - M);
-      o = fmaf(f, ow[i][h][d], o);
-      L = fmaf(f, lw[i][h], L);
+      const float f = __expf(sm.mw[i][h] - M);
+      o = fmaf(f, sm.ow[i][h][d], o);
+      L = fmaf(f, sm.lw[i][h], L);
     }
     __hip_atomic_store(part + tid, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (d == 0) {
@@ -809,13 +1014,18 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    int* c = p.cnt + b * NKV + g;
-    const int done = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = done == nsplit - 1;
-    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed for the next layer
+    bool last = false;
+    if (on) {
+      int* c = p.cnt + b * NKV + g;
+      const int done = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = done == nsplit - 1;
+      if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed for the next layer
+    }
+    sm.last = last;
   }
   __syncthreads();
-  if (!last) return;
+  const bool merge = sm.last;
+  if (!FUSED && !merge) return true;  // one item per workgroup: nothing else shares its barriers
   // 5. the merge: thread (split group sg, output hd) reads output hd of every
   //    SG-th split, MG splits per load round (all loads of a round issued
   //    before any is used: one round trip, not one per split); the SG groups
@@ -825,48 +1035,182 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
     const int hd = tid % (2 * D), sg = tid / (2 * D), h = hd / D;
     const float* base = p.part + ((long long)b * NKV + g) * p.nsplit_max * PW;
     float M = -INFINITY, o = 0.f, L = 0.f;
-    for (int r0 = 0; r0 < nsplit; r0 += SG * MG) {
+    const int ns = merge ? nsplit : 0;
+    for (int r0 = 0; r0 < ns; r0 += SG * MG) {
       float mv[MG], lv[MG], ov[MG];
 #pragma unroll
       for (int u = 0; u < MG; ++u) {
         const int i = r0 + sg + SG * u;
-        const float* pi = base + (long long)(i < nsplit ? i : 0) * PW;
+        const float* pi = base + (long long)(i < ns ? i : 0) * PW;
         mv[u] = __hip_atomic_load(pi + 2 * D + 2 * h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         lv[u] = __hip_atomic_load(pi + 2 * D + 2 * h + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ov[u] = __hip_atomic_load(pi + hd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       float Mb = M;
 #pragma unroll
-      for (int u = 0; u < MG; ++u) Mb = r0 + sg + SG * u < nsplit ? fmaxf(Mb, mv[u]) : Mb;
+      for (int u = 0; u < MG; ++u) Mb = r0 + sg + SG * u < ns ? fmaxf(Mb, mv[u]) : Mb;
       const float sc = M == -INFINITY ? 0.f : __expf(M - Mb);  // o, L are 0 while M is -inf
       o *= sc, L *= sc;
 #pragma unroll
       for (int u = 0; u < MG; ++u) {
-        const bool on = r0 + sg + SG * u < nsplit;  // select: skipped words hold anything
+        const bool on_ = r0 + sg + SG * u < ns;  // select: skipped words hold anything
         const float f = __expf(mv[u] - Mb);
-        o = on ? fmaf(f, ov[u], o) : o;
-        L = on ? fmaf(f, lv[u], L) : L;
+        o = on_ ? fmaf(f, ov[u], o) : o;
+        L = on_ ? fmaf(f, lv[u], L) : L;
       }
       M = Mb;
     }
-    cm[sg][hd] = M, cl[sg][hd] = L, co[sg][hd] = o;
+    sm.cm[sg][hd] = M, sm.cl[sg][hd] = L, sm.co[sg][hd] = o;
     __syncthreads();
-    if (tid < 2 * D) {
-      float Mx = cm[0][tid];  // group 0 holds split 0
+    if (merge && tid < 2 * D) {
+      float Mx = sm.cm[0][tid];  // group 0 holds split 0
 #pragma unroll
-      for (int k = 1; k < SG; ++k) Mx = fmaxf(Mx, cm[k][tid]);
+      for (int k = 1; k < SG; ++k) Mx = fmaxf(Mx, sm.cm[k][tid]);
       float oo = 0.f, ll = 0.f;
 #pragma unroll
       for (int k = 0; k < SG; ++k) {
-        const float f = cm[k][tid] == -INFINITY ? 0.f : __expf(cm[k][tid] - Mx);
-        oo = fmaf(f, co[k][tid], oo);
-        ll = fmaf(f, cl[k][tid], ll);
+        const float f = sm.cm[k][tid] == -INFINITY ? 0.f : __expf(sm.cm[k][tid] - Mx);
+        oo = fmaf(f, sm.co[k][tid], oo);
+        ll = fmaf(f, sm.cl[k][tid], ll);
       }
       uint16_t hi, lo;
       split2(oo / ll, hi, lo);
       const long long k = (long long)b * S::QD + g * 2 * D + tid;
-      p.att[k] = hi;
-      p.att[(long long)BMAX * S::QD + k] = lo;
+      st_act<FUSED>(att_slot<S>(p, sl) + k, hi);
+      st_act<FUSED>(att_slot<S>(p, sl) + (long long)BMAX * S::QD + k, lo);
+    }
+  }
+  if constexpr (FUSED) {  // the merged output is acknowledged before it is counted
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (merge && tid == 0)
+      __hip_atomic_store(p.flags + ((long long)layer * FC_N + FC_ATT) * FLAG_MAX + b * NKV + g, ep, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return true;
+}
+
+// Five 256-thread items per CU (<= 102 registers per lane): the 16-sequence
+// step at KV 512-4096 has ~1,100 items; with four per CU the last ~10 % ran
+// as a second, latency-bound residency wave.
+constexpr int ATTN_WAVES_PER_EU = AT == 256 ? 5 : 2;
+template <class S, bool K8 = false>
+__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_PER_EU, ATTN_WAVES_PER_EU))) void bk_attn(
+    BParams p, int layer) {
+  __shared__ AttnLds<S> sm;
+  const int item = blockIdx.x;
+  const int b = item / (S::NKV * p.nsplit_max), g = (item / p.nsplit_max) % S::NKV, s = item % p.nsplit_max;
+  if (b >= p.B) return;
+  const int pos = p.pos[b];
+  const int nsplit = (pos + 1 + CH - 1) / CH;
+  if (s >= nsplit) return;
+  attn_item<S, K8, false>(p, layer, 0, sm, true, b, g, s, nsplit, pos, NoWait{});
+}
+
+// ------------------------------------------------------------ one-kernel step
+// Workgroups of bk_step per CU (waves per SIMD = 2 x that): two, so twice the
+// attention items run at once (<= 128 registers per lane).
+#ifndef MK_STEP_WG_PER_CU
+#define MK_STEP_WG_PER_CU 2
+#endif
+constexpr int STEP_WG_PER_CU = MK_STEP_WG_PER_CU;
+constexpr int STEP_WAVES_PER_EU = 2 * STEP_WG_PER_CU;
+// Every layer of a decode step in one persistent kernel: STEP_WG_PER_CU
+// workgroups of GT threads per CU (all resident; the host checks the
+// occupancy), each running
+// its share of every phase of a layer in phase order and handing off through
+// p.flags (one word per producer, the step's epoch once its outputs are out):
+//   QKV block rb            on workgroup rb            waits: down of layer - 1 (H/16 blocks)
+//   attention item pairs    pair j on workgroup j % G   waits: every QKV block
+//     (the two AT-thread halves of a workgroup run items 2j and 2j + 1)
+//   O block rb              on workgroup (G - H/16 + rb) % G (G > H/16)
+//                                                      waits: every (sequence, kv head) merged
+//   gate/up block rb        on workgroup rb             waits: every O block
+//   down piece (rb, ks)     on workgroup 4 rb + ks      waits: every gate/up block
+// Each block issues its weight loads before it waits, so the loads overlap
+// the hand-off; every wait is for a phase that precedes it in the order
+// above, and no phase waits for a later one, so the persistent grid cannot
+// deadlock.  The arithmetic is that of the per-phase kernels (same block
+// functions, same summation order): the logits are bit-identical.
+template <class S, bool K8 = false>
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(STEP_WAVES_PER_EU, STEP_WAVES_PER_EU))) void bk_step(
+    BParams p) {
+  static_assert(GT == 2 * AT, "two attention items per workgroup");
+  __shared__ float red[GW * 16 * 17];
+  __shared__ float rr[RR_N];
+  __shared__ int last;
+  __shared__ AttnLds<S> att[2];
+  __shared__ int icum[BMAX + 1], ins[BMAX], ipos[BMAX];
+  const int G = gridDim.x, wg = blockIdx.x;
+  if (threadIdx.x == 0) {  // attention items of the step: sequence b has NKV * nsplit_b, in (b, g, s) order
+    int c = 0;
+    for (int b = 0; b < BMAX; ++b) {
+      const int pos = b < p.B ? p.pos[b] : 0;
+      const int ns = b < p.B ? (pos + 1 + CH - 1) / CH : 0;
+      icum[b] = c;
+      ins[b] = ns;
+      ipos[b] = pos;
+      c += S::NKV * ns;
+    }
+    icum[BMAX] = c;
+  }
+  __syncthreads();
+  const int n_items = icum[BMAX];
+  const int ep = *p.epoch;  // this step's epoch (bk_embed advanced it)
+  u64* const tr = p.trace;
+  int layer = 0;
+  auto stamp = [&](int ev) {
+    if (tr && ltid() == 0) tr[((long long)layer * TR_N + ev) * G + wg] = wall_clock64();
+  };
+  // a wait followed by its "inputs ready" stamp
+  auto waited = [&](bool ok, int ev) {
+    stamp(ev);
+    return ok;
+  };
+  for (; layer < p.L; ++layer) {
+    stamp(TR_START);
+    for (int rb = wg; rb < S::RB_QKV; rb += G) {
+      if (!qkv_block<S, true>(p, layer, ep, rb, 0, red, rr, &last, [&] {
+            return waited(layer == 0 || fc_wait(p, layer - 1, FC_DN, S::RB_H, ep), TR_QKV_IN);
+          }))
+        return;
+      stamp(TR_QKV_DONE);
+    }
+    bool qkv_in = false;  // this layer's QKV count already seen by this workgroup
+    for (int j = wg; 2 * j < n_items; j += G) {
+      const int half = ltid() / AT;
+      const int i = 2 * j + half;
+      const bool on = i < n_items;
+      int b = 0;
+      while (b + 1 < BMAX && icum[b + 1] <= i) ++b;
+      const int r = on ? i - icum[b] : 0, ns = ins[b] > 0 ? ins[b] : 1;
+      if (!attn_item<S, K8, true>(p, layer, ep, att[half], on, b, r / ns, r % ns, ns, ipos[b], [&] {
+            if (qkv_in) return true;
+            qkv_in = waited(fc_wait(p, layer, FC_QKV, S::RB_QKV, ep), TR_ATT_IN);
+            return qkv_in;
+          }))
+        return;
+      stamp(TR_ATT_DONE);
+    }
+    const int o_off = G > S::RB_H ? G - S::RB_H : 0;  // O on the last workgroups (fewest attention pairs)
+    for (int rb = 0; rb < S::RB_H; ++rb)
+      if ((rb + o_off) % G == wg) {
+        if (!o_block<S, true>(p, layer, ep, rb, 0, red, &last,
+                              [&] { return waited(fc_wait(p, layer, FC_ATT, p.B * S::NKV, ep), TR_O_IN); }))
+          return;
+        stamp(TR_O_DONE);
+      }
+    for (int rb = wg; rb < S::RB_F; rb += G) {
+      if (!gu_block<S, true>(p, layer, ep, rb, 0, red, rr, &last,
+                             [&] { return waited(fc_wait(p, layer, FC_O, S::RB_H, ep), TR_GU_IN); }))
+        return;
+      stamp(TR_GU_DONE);
+    }
+    for (int k = wg; k < S::RB_H * KS_DN; k += G) {
+      if (!down_block<S, true>(p, layer, ep, k / KS_DN, k % KS_DN, red, &last,
+                               [&] { return waited(fc_wait(p, layer, FC_GU, S::RB_F, ep), TR_DN_IN); }))
+        return;
+      stamp(TR_DN_DONE);
     }
   }
 }

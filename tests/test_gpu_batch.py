@@ -471,3 +471,46 @@ def test_batch_full_model_long_sequences():
     finally:
         eng.close()
         dw.free()
+
+
+@pytest.mark.parametrize("name,kv_fp8", [("tiny", False), ("baseline_2l", False), ("baseline_2l", True),
+                                         ("baseline_full", False)])
+def test_batch_persistent_step_equals_per_phase_kernels(name, kv_fp8):
+    """The one-kernel step (bk_step: every layer in one persistent kernel,
+    hand-offs through agent-scope counters) and the per-phase kernels compute
+    the same sums in the same order: logits and tokens of 3 debug steps and a
+    6-step graph generate are bit-identical, at the bench's cache lengths
+    (seed 2024, 512-4096 positions: up to 16 attention splits per sequence)."""
+    shape = {"tiny": TINY, "baseline_2l": BASELINE.with_(n_layers=2, vocab=4096),
+             "baseline_full": BASELINE}[name]
+    lengths, rng = _bench_lengths()
+    if name == "tiny":
+        lengths = [0, 5, 127, 200, 31, 32, 33, 255, 256, 257, 400, 511, 1, 90, 300, 64]
+    first = [int(t) for t in rng.integers(0, shape.vocab, size=16)]
+    dw = DeviceWeights(shape, 41, std=0.02, gain_std=0.1)
+    eng = BatchEngine(dw, 16, max(lengths) + 16, shape)
+    try:
+        if kv_fp8:
+            eng.set_kv_fp8(True)
+        runs = {}
+        for variant in (_lib.BATCH_STEP_PER_PHASE, _lib.BATCH_STEP_PERSISTENT):
+            eng.set_step_kernel(variant)
+            for b, n in enumerate(lengths):
+                eng.fill_kv_synthetic(b, n, 700 + b)
+            toks, steps = list(first), []
+            for i in range(3):
+                _print(f"batch step variant {variant} {name} fp8 {kv_fp8} debug step {i}")
+                out, logits = eng.debug_logits(toks)
+                steps.append((list(out), logits.copy()))
+                toks = out
+            gen = eng.generate(toks, 6)
+            runs[variant] = (steps, np.asarray(gen).copy(), eng.positions())
+        (sa, ga, pa), (sb, gb, pb) = runs[_lib.BATCH_STEP_PER_PHASE], runs[_lib.BATCH_STEP_PERSISTENT]
+        for i, ((ta, la), (tb, lb)) in enumerate(zip(sa, sb)):
+            assert ta == tb, f"step {i}: tokens differ"
+            assert np.array_equal(la, lb), f"step {i}: logits differ (max {np.abs(la - lb).max():.3e})"
+        assert np.array_equal(ga, gb), "generated tokens differ"
+        assert pa == pb == [n + 9 for n in lengths]
+    finally:
+        eng.close()
+        dw.free()
