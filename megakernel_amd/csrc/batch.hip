@@ -262,6 +262,7 @@ static int init_state(BHandle* h, const char* base, const long long* off, int n_
   HIPCHK(hipMemcpyAsync(inv, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, h->stream), -1);
   p.inv_freq = inv;
   p.B = h->B, p.L = L, p.V = h->V;
+  if (L >= 64) h->persistent_ok = false;  // the persistent step's split-K tags hold the layer in 6 bits
   p.prefill = 0;
   HIPCHK(hipStreamSynchronize(h->stream), -1);
   return 0;

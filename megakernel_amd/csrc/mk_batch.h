@@ -262,58 +262,62 @@ __device__ __forceinline__ void load_tiles(ATiles<NT>& a, const u32x4* __restric
     a.t[j] = w + GW * j < NT ? buf_ld_nt(rs, l * 16u, (unsigned)(kt0 + w + GW * j) * 1024u) : u32x4{0u, 0u, 0u, 0u};
 }
 
-// The tiles times the 16 activation columns.  B-operand planes: element
-// (n, k) at hi[n * ld + k], lo[n * ld + k].  Lane (kg, n) returns rows
-// 4 kg .. 4 kg + 3 of column n (this wave's share of the K sum).
+// The 16 activation columns of this wave's tiles: the B operands.  Planes:
+// element (n, k) at hi[n * ld + k], lo[n * ld + k].  Loaded on their own, so
+// a block can issue its other loads (norm sums, residual) before it waits.
 template <int NT>
-__device__ __forceinline__ f32x4 tiles_mma(const ATiles<NT>& a, const uint16_t* hi, const uint16_t* lo, int ld,
-                                           int kt0) {
+struct BCols {
+  u32x4 h[ATiles<NT>::TW], l[ATiles<NT>::TW];
+};
+template <int NT>
+__device__ __forceinline__ void load_cols(BCols<NT>& c, const uint16_t* hi, const uint16_t* lo, int ld, int kt0) {
   const unsigned l = lane_id();
   const int w = wave_id();
   const int bo = (int)(l & 15u) * ld + 8 * (int)(l >> 4);
-  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
-  u32x4 bh[ATiles<NT>::TW], bl[ATiles<NT>::TW];
 #pragma unroll
   for (int j = 0; j < ATiles<NT>::TW; ++j) {
     const int kt = kt0 + w + GW * j;
     if (w + GW * j < NT) {
-      bh[j] = *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt);
-      bl[j] = *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt);
+      c.h[j] = *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt);
+      c.l[j] = *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt);
     }
   }
+}
+
+// The tiles times the columns.  Lane (kg, n) returns rows 4 kg .. 4 kg + 3 of
+// column n (this wave's share of the K sum).
+template <int NT>
+__device__ __forceinline__ f32x4 tiles_mma(const ATiles<NT>& a, const BCols<NT>& c) {
+  const int w = wave_id();
+  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
 #pragma unroll
   for (int j = 0; j < ATiles<NT>::TW; ++j) {
     if (w + GW * j < NT) {
-      a0 = mfma(a.t[j], bh[j], a0);
-      a1 = mfma(a.t[j], bl[j], a1);
+      a0 = mfma(a.t[j], c.h[j], a0);
+      a1 = mfma(a.t[j], c.l[j], a1);
     }
   }
   return a0 + a1;
 }
 
-// Two blocks' tiles (gate and up) times the same 16 activation columns: the
-// B operands are loaded once.  Each result equals tiles_mma of that block.
+// Two blocks' tiles (gate and up) times the same columns; each result equals
+// tiles_mma of that block.
 template <int NT>
-__device__ __forceinline__ void tiles_mma2(const ATiles<NT>& a, const ATiles<NT>& c, const uint16_t* hi,
-                                           const uint16_t* lo, int ld, int kt0, f32x4& ra, f32x4& rc) {
-  const unsigned l = lane_id();
+__device__ __forceinline__ void tiles_mma2(const ATiles<NT>& a, const ATiles<NT>& b, const BCols<NT>& c, f32x4& ra,
+                                           f32x4& rb) {
   const int w = wave_id();
-  const int bo = (int)(l & 15u) * ld + 8 * (int)(l >> 4);
-  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0, c0 = a0, c1 = a0;
+  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0, b0 = a0, b1 = a0;
 #pragma unroll
   for (int j = 0; j < ATiles<NT>::TW; ++j) {
-    const int kt = kt0 + w + GW * j;
     if (w + GW * j < NT) {
-      const u32x4 bh = *reinterpret_cast<const u32x4*>(hi + bo + 32 * kt);
-      const u32x4 bl = *reinterpret_cast<const u32x4*>(lo + bo + 32 * kt);
-      a0 = mfma(a.t[j], bh, a0);
-      a1 = mfma(a.t[j], bl, a1);
-      c0 = mfma(c.t[j], bh, c0);
-      c1 = mfma(c.t[j], bl, c1);
+      a0 = mfma(a.t[j], c.h[j], a0);
+      a1 = mfma(a.t[j], c.l[j], a1);
+      b0 = mfma(b.t[j], c.h[j], b0);
+      b1 = mfma(b.t[j], c.l[j], b1);
     }
   }
   ra = a0 + a1;
-  rc = c0 + c1;
+  rb = b0 + b1;
 }
 
 // K splits of a 16-row block run on KS workgroups; each publishes its block
@@ -472,8 +476,10 @@ __device__ __forceinline__ bool qkv_block(const BParams& p, int layer, int ep, i
   load_tiles(a, p.wqkv + layer * p.u_qkv + (long long)rb * S::KT_H * 64, kt0);
   if (!ready()) return false;
   const int sl = FUSED ? layer : 0;
+  BCols<NT> c;
+  load_cols(c, xg_plane<S>(p, sl, 0, 0), xg_plane<S>(p, sl, 0, 1), S::H, kt0);
   rnorm<S>(p, sl, 0, rr);
-  float v[1] = {block_reduce(tiles_mma<NT>(a, xg_plane<S>(p, sl, 0, 0), xg_plane<S>(p, sl, 0, 1), S::H, kt0), red)};
+  float v[1] = {block_reduce(tiles_mma(a, c), red)};
   if (!splitk_finish(p, rb, ks, KS_QKV, v, last)) return true;
   const int t = ltid(), row = rb * 16 + t / 16, b = t % 16;
   if (t < 256 && b < p.B) st_act<FUSED>(qkv_slot<S>(p, sl) + (long long)b * S::QKV + row, v[0] * rr[b]);
@@ -492,10 +498,13 @@ __device__ __forceinline__ bool o_block(const BParams& p, int layer, int ep, int
   if (!ready()) return false;
   const int sl = FUSED ? layer : 0;
   const uint16_t* at = att_slot<S>(p, sl);
-  float v[1] = {block_reduce(tiles_mma<NT>(a, at, at + BMAX * S::QD, S::QD, kt0), red)};
-  if (!splitk_finish(p, rb, ks, KS_O, v, last)) return true;
+  BCols<NT> c;
+  load_cols(c, at, at + BMAX * S::QD, S::QD, kt0);
   const int t = ltid(), b = t % 16;
-  const float xn = t < 256 && b < p.B ? x_slot<S>(p, sl, 0)[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
+  const float xin = t < 256 && b < p.B ? x_slot<S>(p, sl, 0)[(long long)b * S::H + rb * 16 + t / 16] : 0.f;
+  float v[1] = {block_reduce(tiles_mma(a, c), red)};
+  if (!splitk_finish(p, rb, ks, KS_O, v, last)) return true;
+  const float xn = t < 256 && b < p.B ? xin + v[0] : 0.f;
   __syncthreads();  // red is reused
   publish_x<S, FUSED>(p, sl, 1, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, rb, xn, red);
   if constexpr (FUSED) fc_done(p, layer, FC_O, rb, ep);
@@ -514,10 +523,11 @@ __device__ __forceinline__ bool gu_block(const BParams& p, int layer, int ep, in
   load_tiles(au, p.wu + layer * p.u_gu + off, kt0);
   if (!ready()) return false;
   const int sl = FUSED ? layer : 0;
+  BCols<NT> c;
+  load_cols(c, xg_plane<S>(p, sl, 1, 0), xg_plane<S>(p, sl, 1, 1), S::H, kt0);
   rnorm<S>(p, sl, 1, rr);
-  const uint16_t *hi = xg_plane<S>(p, sl, 1, 0), *lo = xg_plane<S>(p, sl, 1, 1);
   f32x4 pg, pu;
-  tiles_mma2<NT>(ag, au, hi, lo, S::H, kt0, pg, pu);
+  tiles_mma2(ag, au, c, pg, pu);
   float v[2];
   v[0] = block_reduce(pg, red);
   __syncthreads();
@@ -548,10 +558,53 @@ __device__ __forceinline__ bool down_block(const BParams& p, int layer, int ep, 
   if (!ready()) return false;
   const int sl = FUSED ? layer : 0;
   const uint16_t* ac = act_slot<S>(p, sl);
-  float v[1] = {block_reduce(tiles_mma<NT>(a, ac, ac + BMAX * S::F, S::F, kt0), red)};
-  if (!splitk_finish(p, rb, ks, KS_DN, v, last)) return true;
+  BCols<NT> c;
+  load_cols(c, ac, ac + BMAX * S::F, S::F, kt0);
   const int t = ltid(), b = t % 16;
-  const float xn = t < 256 && b < p.B ? x_slot<S>(p, sl, 1)[(long long)b * S::H + rb * 16 + t / 16] + v[0] : 0.f;
+  // the residual, read by the workgroup that finishes the block (split 0 in
+  // the one-kernel step, whichever split completes it otherwise)
+  const float xin = (!FUSED || ks == 0) && t < 256 && b < p.B
+                        ? x_slot<S>(p, sl, 1)[(long long)b * S::H + rb * 16 + t / 16]
+                        : 0.f;
+  float v[1] = {block_reduce(tiles_mma(a, c), red)};
+  if constexpr (FUSED) {
+    // K splits 1.. publish their sums as (value, tag) words; split 0 polls
+    // them and adds the splits in order, as splitk_finish does
+    u64* buf = reinterpret_cast<u64*>(p.gpart) + (long long)rb * KS_DN * 256;
+    const unsigned tag = (unsigned)ep * 64u + (unsigned)layer;
+    if (ks != 0) {
+      if (t < 256) __hip_atomic_store(buf + ks * 256 + t, ((u64)tag << 32) | f32_bits(v[0]), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+      return true;
+    }
+    int ok = 1;
+    if (t < 256) {
+      u64 wv[KS_DN - 1];
+      Spin sp;
+      while (true) {
+        bool all = true;
+#pragma unroll
+        for (int k = 1; k < KS_DN; ++k) {
+          wv[k - 1] = __hip_atomic_load(buf + k * 256 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          all &= (unsigned)(wv[k - 1] >> 32) == tag;
+        }
+        if (all) break;
+        if (!sp.step(p.err, p.timeout_ticks)) {
+          ok = 0;
+          break;
+        }
+      }
+      float sum = 0.f;
+      sum += v[0];
+#pragma unroll
+      for (int k = 1; k < KS_DN; ++k) sum += f32_from((unsigned)wv[k - 1]);
+      v[0] = sum;
+    }
+    if (!__syncthreads_and(ok)) return false;
+  } else if (!splitk_finish(p, rb, ks, KS_DN, v, last)) {
+    return true;
+  }
+  const float xn = t < 256 && b < p.B ? xin + v[0] : 0.f;
   __syncthreads();  // red is reused
   const uint16_t* gain = layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE + S::NORM_ATTN
                                          : p.final_norm;
@@ -767,6 +820,80 @@ struct AttnLds {
   int last;
 };
 
+// K / V registers of one item: the wave's NBW 32-position blocks (4 s + w) +
+// AW * q (blocks past the item repeat a valid block).  K8: the FP8 cache
+// (codes converted to bf16 in registers, exact; the K row scale enters that
+// conversion, the V row scale the softmax weight).
+template <class S, bool K8>
+struct AttnKV {
+  using Reg = typename std::conditional<K8, u32x2, u32x4>::type;
+  Reg kr[NBW][2][2], vr[NBW][S::D / 16];
+  float sk[K8 ? NBW : 1][2], sv[K8 ? NBW : 1][2];  // FP8: scales of the lane's score positions
+};
+template <class S, bool K8>
+__device__ __forceinline__ void attn_kv_load(const BParams& p, int layer, bool on, int b, int g, int s, int pos,
+                                             AttnKV<S, K8>& r) {
+  constexpr int D = S::D, NKV = S::NKV;
+  const int n = on ? pos + 1 : 0;
+  const int tid = ltid() % AT, w = tid / kWave, l = tid % kWave;
+  const unsigned lu = (unsigned)l;
+  const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
+  const long long sbase = (long long)b * p.sc_seq + ((long long)layer * NKV + g) * p.s_pad;
+  if (!on) {  // no item: the registers hold nothing (no value carried from an earlier item)
+#pragma unroll
+    for (int q = 0; q < NBW; ++q) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) r.kr[q][h][kc] = __builtin_nondeterministic_value(r.kr[q][h][kc]);
+        if constexpr (K8) {
+          r.sk[q][h] = __builtin_nondeterministic_value(r.sk[q][h]);
+          r.sv[q][h] = __builtin_nondeterministic_value(r.sv[q][h]);
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) r.vr[q][dt] = __builtin_nondeterministic_value(r.vr[q][dt]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < NBW; ++q) {
+    int blk = s * AW * NBW + w + AW * q;
+    blk = 32 * blk < n ? blk : s * AW * NBW;
+    if constexpr (K8) {  // byte index = element index of the bf16 layout
+      const auto rk = make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + kbase + (long long)blk * 32 * D);
+      const auto rv = make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + kbase + (long long)blk * 32 * D);
+      const auto rks = make_rsrc(p.kscale + sbase + (long long)blk * 32);
+      const auto rvs = make_rsrc(p.vscale + sbase + (long long)blk * 32);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+          r.kr[q][h][kc] =
+              __builtin_amdgcn_raw_buffer_load_b64(rk, (16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4), 0u, 2);
+        r.sk[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rks, (16u * h + (lu & 15u)) * 4u, 0u, 2));
+        r.sv[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rvs, (16u * h + (lu & 15u)) * 4u, 0u, 2));
+      }
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt)
+        r.vr[q][dt] = __builtin_amdgcn_raw_buffer_load_b64(rv, (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4), 0u, 2);
+    } else {
+      const auto rk = make_rsrc(p.kv + kbase + (long long)blk * 32 * D);
+      const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+          r.kr[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b128(
+              rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt)
+        r.vr[q][dt] =
+            __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+    }
+  }
+}
+
 // The item's code for AT threads (local thread threadIdx.x % AT).
 // FUSED: inside bk_step, where the two AT-thread halves of a workgroup run
 // two items and share every barrier: `on` false (a half without an item)
@@ -777,60 +904,19 @@ struct AttnLds {
 // of q / k / v; the return is false only when it gave up.
 template <class S, bool K8, bool FUSED, class Ready>
 __device__ __forceinline__ bool attn_item(const BParams& p, int layer, int ep, AttnLds<S>& sm, bool on, int b, int g,
-                                          int s, int nsplit, int pos, const Ready& ready) {
+                                          int s, int nsplit, int pos, AttnKV<S, K8>& kv, const Ready& ready) {
   static_assert(S::GQA == 2 && S::D == 64, "batched attention is built for 2 q heads of 64 per kv head");
   constexpr int D = S::D, NKV = S::NKV;
-  // K8: the FP8 cache (codes converted to bf16 in registers, exact; the K
-  // row scale enters that conversion, the V row scale the softmax weight)
-  using Reg = typename std::conditional<K8, u32x2, u32x4>::type;
+  // K / V of the item's blocks are in kv (attn_kv_load, issued before)
   const int n = on ? pos + 1 : 0;
   const int tid = ltid() % AT, w = tid / kWave, l = tid % kWave;
-  const unsigned lu = (unsigned)l;
   const int c16 = l & 15, rg = l >> 4;
   const long long kbase = (long long)b * p.kv_seq + ((long long)layer * NKV + g) * (long long)p.s_pad * D;
-  // 0. the wave's K / V blocks (4 s + w) + AW * q, q < NBW: issued first, so the
-  //    prologue below overlaps them (blocks past the item repeat a valid block)
-  Reg kr[NBW][2][2], vr[NBW][D / 16];
-  float sk[K8 ? NBW : 1][2], sv[K8 ? NBW : 1][2];  // FP8: scales of the lane's score positions
   const long long sbase = (long long)b * p.sc_seq + ((long long)layer * NKV + g) * p.s_pad;
-  if (on) {
-#pragma unroll
-    for (int q = 0; q < NBW; ++q) {
-      int blk = s * AW * NBW + w + AW * q;
-      blk = 32 * blk < n ? blk : s * AW * NBW;
-      if constexpr (K8) {  // byte index = element index of the bf16 layout
-        const auto rk = make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + kbase + (long long)blk * 32 * D);
-        const auto rv = make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + kbase + (long long)blk * 32 * D);
-        const auto rks = make_rsrc(p.kscale + sbase + (long long)blk * 32);
-        const auto rvs = make_rsrc(p.vscale + sbase + (long long)blk * 32);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-          for (int kc = 0; kc < 2; ++kc)
-            kr[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b64(rk, (16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4),
-                                                                0u, 2);
-          sk[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rks, (16u * h + (lu & 15u)) * 4u, 0u, 2));
-          sv[q][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rvs, (16u * h + (lu & 15u)) * 4u, 0u, 2));
-        }
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt)
-          vr[q][dt] = __builtin_amdgcn_raw_buffer_load_b64(rv, (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4), 0u, 2);
-      } else {
-        const auto rk = make_rsrc(p.kv + kbase + (long long)blk * 32 * D);
-        const auto rv = make_rsrc(p.kvt + kbase + (long long)blk * 32 * D);
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int kc = 0; kc < 2; ++kc)
-            kr[q][h][kc] = __builtin_amdgcn_raw_buffer_load_b128(
-                rk, ((16u * h + (lu & 15u)) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt)
-          vr[q][dt] =
-              __builtin_amdgcn_raw_buffer_load_b128(rv, ((16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
-      }
-    }
-  }
+  auto& kr = kv.kr;
+  auto& vr = kv.vr;
+  auto& sk = kv.sk;
+  auto& sv = kv.sv;
   for (int i = tid; i < 16 * D; i += AT) (&sm.qb[0][0])[i] = 0;
   for (int i = tid; i < AW * 16 * 32; i += AT) (&sm.pb[0][0][0])[i] = 0;
   if (on && tid < D / 2) {
@@ -1104,7 +1190,9 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
   const int pos = p.pos[b];
   const int nsplit = (pos + 1 + CH - 1) / CH;
   if (s >= nsplit) return;
-  attn_item<S, K8, false>(p, layer, 0, sm, true, b, g, s, nsplit, pos, NoWait{});
+  AttnKV<S, K8> kv;
+  attn_kv_load<S, K8>(p, layer, true, b, g, s, pos, kv);
+  attn_item<S, K8, false>(p, layer, 0, sm, true, b, g, s, nsplit, pos, kv, NoWait{});
 }
 
 // ------------------------------------------------------------ one-kernel step
@@ -1121,14 +1209,17 @@ constexpr int STEP_WAVES_PER_EU = 2 * STEP_WG_PER_CU;
 // its share of every phase of a layer in phase order and handing off through
 // p.flags (one word per producer, the step's epoch once its outputs are out):
 //   QKV block rb            on workgroup rb            waits: down of layer - 1 (H/16 blocks)
-//   attention item pairs    pair j on workgroup j % G   waits: every QKV block
+//   attention item pairs    pair j on workgroup (j + QKV/16) % G
+//                                                      waits: every QKV block
 //     (the two AT-thread halves of a workgroup run items 2j and 2j + 1)
 //   O block rb              on workgroup (G - H/16 + rb) % G (G > H/16)
 //                                                      waits: every (sequence, kv head) merged
 //   gate/up block rb        on workgroup rb             waits: every O block
 //   down piece (rb, ks)     on workgroup 4 rb + ks      waits: every gate/up block
-// Each block issues its weight loads before it waits, so the loads overlap
-// the hand-off; every wait is for a phase that precedes it in the order
+//     (split 0 then waits for splits 1-3 of its block, whose sums carry a tag)
+// Each block issues its weight loads before it waits, and every workgroup
+// without a QKV block the K / V loads of its first attention pair at the
+// layer start, so the loads overlap the hand-offs; every wait is for a phase that precedes it in the order
 // above, and no phase waits for a later one, so the persistent grid cannot
 // deadlock.  The arithmetic is that of the per-phase kernels (same block
 // functions, same summation order): the logits are bit-identical.
@@ -1167,28 +1258,61 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(STEP_WAVES_P
     stamp(ev);
     return ok;
   };
+  // pair j on workgroup (j + QKV blocks) % G: the workgroups without a QKV
+  // block take the first pairs; every workgroup issues the K / V loads of its
+  // first pair at the layer start (they only read the cache)
+  const int j0 = (wg - S::RB_QKV % G + G) % G;
+  struct Item {
+    bool on;
+    int b, g, s, ns;
+  };
+  auto item_of = [&](int j) {
+    const int i = 2 * j + ltid() / AT;
+    Item it;
+    it.on = i < n_items;
+    int b = 0;
+    while (b + 1 < BMAX && icum[b + 1] <= i) ++b;
+    const int r = it.on ? i - icum[b] : 0;
+    it.ns = ins[b] > 0 ? ins[b] : 1;
+    it.b = b, it.g = r / it.ns, it.s = r % it.ns;
+    return it;
+  };
   for (; layer < p.L; ++layer) {
     stamp(TR_START);
-    for (int rb = wg; rb < S::RB_QKV; rb += G) {
-      if (!qkv_block<S, true>(p, layer, ep, rb, 0, red, rr, &last, [&] {
-            return waited(layer == 0 || fc_wait(p, layer - 1, FC_DN, S::RB_H, ep), TR_QKV_IN);
-          }))
+    bool qkv_in = false;  // this layer's QKV flags already seen by this workgroup
+    auto qkv_ready = [&] {
+      if (qkv_in) return true;
+      qkv_in = waited(fc_wait(p, layer, FC_QKV, S::RB_QKV, ep), TR_ATT_IN);
+      return qkv_in;
+    };
+    int jn = j0;  // the next attention pair of this workgroup
+    if (wg >= S::RB_QKV && 2 * j0 < n_items) {
+      // no QKV block: the first pair's K / V loads are issued at the layer
+      // start and overlap the QKV phase (a workgroup with a QKV block issues
+      // them after it, in the loop below: both at once do not fit the registers)
+      const Item it = item_of(j0);
+      AttnKV<S, K8> kv;
+      attn_kv_load<S, K8>(p, layer, it.on, it.b, it.g, it.s, ipos[it.b], kv);
+      if (!attn_item<S, K8, true>(p, layer, ep, att[ltid() / AT], it.on, it.b, it.g, it.s, it.ns, ipos[it.b], kv,
+                                  qkv_ready))
         return;
-      stamp(TR_QKV_DONE);
+      stamp(TR_ATT_DONE);
+      jn += G;
+    } else {
+      for (int rb = wg; rb < S::RB_QKV; rb += G) {
+        if (!qkv_block<S, true>(p, layer, ep, rb, 0, red, rr, &last, [&] {
+              return waited(layer == 0 || fc_wait(p, layer - 1, FC_DN, S::RB_H, ep), TR_QKV_IN);
+            }))
+          return;
+        stamp(TR_QKV_DONE);
+      }
     }
-    bool qkv_in = false;  // this layer's QKV count already seen by this workgroup
-    for (int j = wg; 2 * j < n_items; j += G) {
-      const int half = ltid() / AT;
-      const int i = 2 * j + half;
-      const bool on = i < n_items;
-      int b = 0;
-      while (b + 1 < BMAX && icum[b + 1] <= i) ++b;
-      const int r = on ? i - icum[b] : 0, ns = ins[b] > 0 ? ins[b] : 1;
-      if (!attn_item<S, K8, true>(p, layer, ep, att[half], on, b, r / ns, r % ns, ns, ipos[b], [&] {
-            if (qkv_in) return true;
-            qkv_in = waited(fc_wait(p, layer, FC_QKV, S::RB_QKV, ep), TR_ATT_IN);
-            return qkv_in;
-          }))
+    for (int j = jn; 2 * j < n_items; j += G) {
+      const Item it = item_of(j);
+      AttnKV<S, K8> kv;
+      attn_kv_load<S, K8>(p, layer, it.on, it.b, it.g, it.s, ipos[it.b], kv);
+      if (!attn_item<S, K8, true>(p, layer, ep, att[ltid() / AT], it.on, it.b, it.g, it.s, it.ns, ipos[it.b], kv,
+                                  qkv_ready))
         return;
       stamp(TR_ATT_DONE);
     }
@@ -1206,12 +1330,16 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(STEP_WAVES_P
         return;
       stamp(TR_GU_DONE);
     }
-    for (int k = wg; k < S::RB_H * KS_DN; k += G) {
-      if (!down_block<S, true>(p, layer, ep, k / KS_DN, k % KS_DN, red, &last,
-                               [&] { return waited(fc_wait(p, layer, FC_GU, S::RB_F, ep), TR_DN_IN); }))
-        return;
-      stamp(TR_DN_DONE);
-    }
+    // a workgroup with several down pieces runs its split-0 pieces (which
+    // wait for the other splits of their block) after the others
+    for (int pass = 0; pass < 2; ++pass)
+      for (int k = wg; k < S::RB_H * KS_DN; k += G) {
+        if ((k % KS_DN == 0) != (pass == 1)) continue;
+        if (!down_block<S, true>(p, layer, ep, k / KS_DN, k % KS_DN, red, &last,
+                                 [&] { return waited(fc_wait(p, layer, FC_GU, S::RB_F, ep), TR_DN_IN); }))
+          return;
+        stamp(TR_DN_DONE);
+      }
   }
 }
 
