@@ -202,6 +202,35 @@ def calibrate_copy():
     print(json.dumps({"copy_bytes": n * 4, "copies": 5}))
 
 
+def batch_trace_summary(eng, toks, info):
+    """Device timestamps of one persistent batched step (bk_step): per phase,
+    the mean over layers 2.. of (a) the previous phase's last finish -> this
+    phase's last 'inputs ready' and (b) from there to its last finish."""
+    import numpy as np
+    tr = eng.trace_step(toks).astype(np.int64)
+    L = tr.shape[0]
+    us = 1e3 / (info["wall_clock_khz"] or 100000)
+
+    def last(l, e):
+        v = tr[l, e]
+        v = v[v > 0]
+        return float(v.max()) if v.size else float("nan")
+
+    phases = [("qkv", 1, 2), ("attention", 3, 4), ("o", 5, 6), ("gate_up", 7, 8), ("down", 9, 10)]
+    hand = {k: [] for k, _, _ in phases}
+    work = {k: [] for k, _, _ in phases}
+    for l in range(2, L):
+        prev = last(l - 1, 10)
+        for k, i, d in phases:
+            hand[k].append((last(l, i) - prev) * us)
+            work[k].append((last(l, d) - last(l, i)) * us)
+            prev = last(l, d)
+    period = (last(L - 1, 10) - last(1, 10)) * us / (L - 2)
+    out = {k: {"handoff_us": round(float(np.mean(hand[k])), 2), "work_us": round(float(np.mean(work[k])), 2)}
+           for k, _, _ in phases}
+    print(json.dumps({"batch_step_trace": out, "layer_period_us": round(period, 2)}), file=sys.stderr, flush=True)
+
+
 def bench_batch(args):
     """n independent sequences, per-sequence KV lengths
     uniform in [kv_min, kv_max] from the seed (synthetic N(0, 1) prefill), K
@@ -246,6 +275,9 @@ def bench_batch(args):
         print(f"# rep {r}: wall {walls[-1] * 1e3:.2f} ms device {kernels[-1] * 1e3:.2f} ms -> "
               f"{B * K / walls[-1]:.1f} tok/s; last tokens {toks[-1][:4].tolist()}", file=sys.stderr, flush=True)
     wall, kern = statistics.median(walls), statistics.median(kernels)
+    if args.trace and args.batch_step == "persistent":
+        prefill()
+        batch_trace_summary(eng, first, info)
     kvp = shape.kv_bytes_per_pos  # per position; FP8: 1 byte per value plus a 4-byte scale per row
     if args.kv_fp8:
         kvp = kvp // 2 + 2 * 4 * shape.n_kv_heads * shape.n_layers
