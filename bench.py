@@ -46,6 +46,8 @@ def parse():
                     help="FP8 (e4m3) KV cache with a power-of-two scale per K / V row")
     ap.add_argument("--lmhead-fp8", action="store_true",
                     help="stream the FP8 (e4m3, power-of-two row scales) copy of the LM head")
+    ap.add_argument("--lmhead-screened", action="store_true",
+                    help="LM head: FP8 screening + exact bf16 rescoring of the possible argmax rows (bf16 tokens)")
     ap.add_argument("--layer-fp8", action="store_true",
                     help="stream fp8 e4m3 copies of the layer matrices (power-of-two row scales; decode only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -549,11 +551,13 @@ def main():
         eng.set_attention_merge(args.merge)
     if args.lmhead_fp8:
         eng.set_lmhead_fp8(True)
+    from megakernel_amd import _lib
+    if args.lmhead_screened:
+        eng.set_lmhead_fp8(_lib.LMHEAD_SCREENED)
     if args.kv_fp8:
         eng.set_kv_fp8(True)
     if args.layer_fp8:
         eng.set_layer_fp8(True)
-    from megakernel_amd import _lib
     eng.set_decode_kernel(_lib.KERNEL_SPREAD if args.kernel == "spread" else _lib.KERNEL_AUTO)
     info = launcher.detect_gpu()
     grid = eng.grid_size
@@ -579,6 +583,8 @@ def main():
     nbytes = sum(shape.token_bytes(args.ctx + i) for i in range(K))
     if args.lmhead_fp8:  # 1 byte per LM-head weight instead of 2, plus a 4-byte scale per row
         nbytes -= K * (shape.vocab * shape.hidden - 4 * shape.vocab)
+    elif args.lmhead_screened:  # the FP8 head with its scales and bounds (the rescored rows are not counted)
+        nbytes -= K * (shape.vocab * shape.hidden - 8 * shape.vocab)
     if args.kv_fp8:  # per position: 1 byte per K / V value plus a 4-byte scale per row
         kv8 = shape.kv_bytes_per_pos // 2 + 2 * 4 * shape.n_kv_heads * shape.n_layers
         nbytes -= sum((shape.kv_bytes_per_pos - kv8) * (args.ctx + i + 2) for i in range(K))
@@ -589,7 +595,8 @@ def main():
         nbytes -= K * shape.n_layers * (mats - 4 * rows)
     achieved = nbytes / kern / 1e9
     traffic = None
-    if os.path.exists(args.traffic_json) and not (args.lmhead_fp8 or args.kv_fp8 or args.layer_fp8):
+    if os.path.exists(args.traffic_json) and not (args.lmhead_fp8 or args.kv_fp8 or args.layer_fp8 or
+                                                  args.lmhead_screened):
         with open(args.traffic_json) as f:
             tj = json.load(f)
         if tj.get("ctx") == args.ctx and tj.get("tokens") == K:
@@ -627,6 +634,8 @@ def main():
                    "ctx": args.ctx, "tokens": K, "batch": 1, "layers": shape.n_layers,
                    "hidden": shape.hidden, "heads": "16q/8kv x 64", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "bf16 N(0,0.02) (Irwin-Hall(4) approx), unit norm gains" +
+                              ("; LM head screened with its fp8 e4m3 copy, the possible argmax rows rescored "
+                               "in bf16 (the bf16 head's tokens)" if args.lmhead_screened else "") +
                               ("; layer matrices streamed as fp8 e4m3 with power-of-two row scales"
                                if args.layer_fp8 else "") +
                               ("; LM head streamed as fp8 e4m3 with power-of-two row scales" if args.lmhead_fp8 else "") +

@@ -158,13 +158,23 @@ int megakernel_set_decode_kernel(void* handle, int variant);
 int megakernel_decode_kernel_for(void* handle, int n_tokens);
 
 /* FP8 LM head (no counterpart in the reference kernel, which plans FP8
- * weights in RESEARCH.md:434-436,463).  enable = 1 builds, once, an OCP e4m3
- * copy of the tied LM head with one power-of-two scale per row (2^e, the
- * smallest e with max|row| <= 448 * 2^e; weights rounded to nearest even after
- * the exact scaling) and makes the decode launches stream it: 1 byte per
- * weight instead of 2 for 32 % of the bytes of a token.  The embedding gather
- * and the prefill context keep the bf16 table.  enable = 0 returns to bf16.
- * Returns 0, or -1 (vocab not a multiple of 16, hidden not of 64, no memory). */
+ * weights in RESEARCH.md:434-436,463).  A mode other than MK_LMHEAD_BF16
+ * builds, once, an OCP e4m3 copy of the tied LM head with one power-of-two
+ * scale per row (2^e, the smallest e with max|row| <= 448 * 2^e; weights
+ * rounded to nearest even after the exact scaling) and a per-row bound of its
+ * error.  MK_LMHEAD_FP8: decode launches stream the copy, 1 byte per weight
+ * instead of 2 for 32 % of the bytes of a token (logits and tokens of the FP8
+ * weights).  MK_LMHEAD_SCREENED: the copy only screens -- every row whose
+ * FP8 logit plus its error bound reaches the largest FP8 logit minus its
+ * bound is scored again from the bf16 tiles, and the argmax runs over those
+ * exact bf16 logits, so the tokens are the bf16 head's (class-specialised
+ * kernel; the other launches use the bf16 head).  The embedding gather and the
+ * prefill context keep the bf16 table.  MK_LMHEAD_BF16 (0) returns to bf16.
+ * Returns 0, or -1 (unknown mode, vocab not a multiple of 16, hidden not of
+ * 64, no memory). */
+#define MK_LMHEAD_BF16 0
+#define MK_LMHEAD_FP8 1
+#define MK_LMHEAD_SCREENED 2
 int megakernel_set_lmhead_fp8(void* handle, int enable);
 
 /* FP8 KV cache (no counterpart in the reference kernel, which plans FP8 KV in

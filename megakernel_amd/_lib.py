@@ -95,6 +95,7 @@ SIGNATURES = {
 PRESET_BASELINE, PRESET_QWEN3_06B, PRESET_TINY = 0, 1, 2
 KERNEL_AUTO, KERNEL_SPREAD, KERNEL_CLASS = 0, 1, 2  # megakernel_set_decode_kernel / _decode_kernel_for
 BATCH_STEP_PERSISTENT, BATCH_STEP_PER_PHASE = 0, 1  # megakernel_batch_set_step_kernel
+LMHEAD_BF16, LMHEAD_FP8, LMHEAD_SCREENED = 0, 1, 2  # megakernel_set_lmhead_fp8
 H2D, D2H, D2D = 0, 1, 2
 
 _cache: dict[str, ctypes.CDLL] = {}

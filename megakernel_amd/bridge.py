@@ -256,10 +256,13 @@ class MegakernelEngine:
         return _lib.check(self.lib, self.lib.megakernel_decode_kernel_for(self._handle, int(n_tokens)),
                           "decode_kernel_for")
 
-    def set_lmhead_fp8(self, enable: bool = True):
-        """Stream an FP8 (OCP e4m3, power-of-two row scales) copy of the LM head."""
-        _lib.check(self.lib, self.lib.megakernel_set_lmhead_fp8(self._handle, int(bool(enable))),
-                   "set_lmhead_fp8")
+    def set_lmhead_fp8(self, enable=True):
+        """LM head mode: False / _lib.LMHEAD_BF16, True / _lib.LMHEAD_FP8 (stream
+        the FP8 copy: OCP e4m3, power-of-two row scales), or
+        _lib.LMHEAD_SCREENED (the FP8 copy screens the rows, the possible
+        argmax rows are scored again in bf16: the bf16 head's tokens)."""
+        mode = int(enable) if not isinstance(enable, bool) else (_lib.LMHEAD_FP8 if enable else _lib.LMHEAD_BF16)
+        _lib.check(self.lib, self.lib.megakernel_set_lmhead_fp8(self._handle, mode), "set_lmhead_fp8")
 
     def set_kv_fp8(self, enable: bool = True):
         """Switch the KV cache to FP8 (OCP e4m3, power-of-two scale per row of

@@ -711,7 +711,7 @@ int megakernel_batch_set_lmhead_fp8(void* handle, int enable) {
         mk::batch::alloc(h, &h->lm_scale, (size_t)h->V * 4, false))
       return -1;
     hipLaunchKernelGGL(mk::lmhead_fp8_kernel, dim3(h->V / 16), dim3(256), 0, h->stream, h->p.lmhead, h->H,
-                       reinterpret_cast<unsigned char*>(h->lmhead8), h->lm_scale);
+                       reinterpret_cast<unsigned char*>(h->lmhead8), h->lm_scale, nullptr);
     HIPCHK(hipGetLastError(), -1);
     HIPCHK(hipStreamSynchronize(h->stream), -1);
   }

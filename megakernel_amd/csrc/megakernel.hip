@@ -60,8 +60,14 @@ __global__ void repack_kernel(const u32x4* __restrict__ src, int R, int K, u32x4
 // e4m3(W[r][c] * 2^-e) (exact scaling, then round to nearest even).  Output
 // tiles: 1 KiB units of 64 lanes x 16 bytes, lane (q, r) holding row r,
 // columns 64u + 16q .. +15 of unit u.
+// err (optional): per row an upper bound B_r on |W[r] . h - Q[r] . h| / ||h||
+// for any h, Q[r] the dequantised FP8 row, including both products' fp32
+// summation error: B_r = (||W[r] - Q[r]|| + 3 g (||W[r]|| + ||W[r] - Q[r]||))
+// (1 + 2^-12), g = 1.1 (K + 64) 2^-24 (the bound gamma_n n u / (1 - n u) on a
+// length-n fp32 sum, with room); the screened LM head uses it to skip rows.
 __global__ __launch_bounds__(256) void lmhead_fp8_kernel(const u32x4* __restrict__ src, int K,
-                                                         unsigned char* __restrict__ dst, float* __restrict__ scales) {
+                                                         unsigned char* __restrict__ dst, float* __restrict__ scales,
+                                                         float* __restrict__ err) {
   const int r = threadIdx.x >> 4, j = threadIdx.x & 15;  // 16 threads per row (one lane group)
   const long long rb = blockIdx.x, row = rb * 16 + r;
   const int KT = K / 32, KT8 = K / 64;
@@ -75,9 +81,26 @@ __global__ __launch_bounds__(256) void lmhead_fp8_kernel(const u32x4* __restrict
   for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
   const int e = e4m3_row_exp(amax);
   unsigned char* d = dst + rb * KT8 * 1024;
-  for (int c = j; c < K; c += 16)
-    d[(c >> 6) * 1024 + (((c >> 4) & 3) * 16 + r) * 16 + (c & 15)] = (unsigned char)e4m3_encode(ldexpf(elem(c), -e));
+  double rr = 0.0, ww = 0.0;  // squared norms of W[r] - Q[r] and of W[r]
+  for (int c = j; c < K; c += 16) {
+    const int code = e4m3_encode(ldexpf(elem(c), -e));
+    d[(c >> 6) * 1024 + (((c >> 4) & 3) * 16 + r) * 16 + (c & 15)] = (unsigned char)code;
+    const double w = elem(c), q = (double)__builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0] * ldexp(1.0, e);
+    rr += (w - q) * (w - q);
+    ww += w * w;
+  }
   if (j == 0) scales[row] = ldexpf(1.f, e);
+  if (err) {
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      rr += __shfl_xor(rr, m);
+      ww += __shfl_xor(ww, m);
+    }
+    if (j == 0) {
+      const double g = 1.1 * (K + 64) * ldexp(1.0, -24), rn = sqrt(rr), wn = sqrt(ww);
+      err[row] = (float)((rn + 3.0 * g * (wn + rn)) * (1.0 + ldexp(1.0, -12)));
+    }
+  }
 }
 
 // FP8 copy of the layer weights (opt-in; the same quantisation as the LM
@@ -340,7 +363,8 @@ struct Handle {
   u32x4* lmhead = nullptr;
   u32x4* lmhead8 = nullptr;  // optional FP8 copy of the LM head, built on request
   float* lm_scale = nullptr;
-  bool lm_fp8 = false;       // the LM head reads lmhead8
+  float* lm_err = nullptr;   // per-row bound of the FP8 rows' error (lmhead_fp8_kernel)
+  int lm_mode = MK_LMHEAD_BF16;  // bf16, FP8, or FP8 screening + exact bf16 rescoring
   u32x2* layers8 = nullptr;  // optional FP8 copy of the layer weights (same unit offsets, 8-byte units)
   float* lscale = nullptr;   // its row scales [L][srows_layer]
   bool layer_fp8 = false;    // the class kernel reads layers8
@@ -380,7 +404,7 @@ static void free_all(Handle* h) {
   h->roles = nullptr;
   batch::destroy_prefill_context(h->prefill);
   h->prefill = nullptr;
-  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->layers8, h->lscale, h->kscale, h->vscale, h->kv, h->x, h->qkv, h->part,
+  void* ptrs[] = {h->layers, h->norms, h->final_norm, h->lmhead, h->lmhead8, h->lm_scale, h->lm_err, h->layers8, h->lscale, h->kscale, h->vscale, h->kv, h->x, h->qkv, h->part,
                   h->act, h->amax, h->err, h->inv_freq, h->dbg_layers,
                   h->dbg_logits, h->trace, h->owned_flat};
   for (void* q : ptrs)
@@ -445,7 +469,7 @@ static int init_device_state(Handle* h, const char* base, const long long* off, 
   // part: the splits' partials, then one row for a long context's merged partial
   const size_t words[5] = {(size_t)s.H / 2, (size_t)s.QKV,
                            (size_t)(h->nsplit_max + 1) * s.NKV * s.part_words, (size_t)s.F / 2,
-                           (size_t)2 * h->G};
+                           (size_t)4 * h->G};  // amax: [2][G] argmax words, then [2][G] screening thresholds
   for (int i = 0; i < 5; ++i) {
     h->tagged_bytes[i] = words[i] * 8;
     HIPCHK(hipMalloc(tagged[i], h->tagged_bytes[i]), -1);
@@ -604,8 +628,9 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.norms = h->norms;
   p.final_norm = h->final_norm;
   p.lmhead = h->lmhead;
-  p.lmhead8 = h->lm_fp8 ? h->lmhead8 : nullptr;
-  p.lm_scale = h->lm_fp8 ? h->lm_scale : nullptr;
+  p.lmhead8 = h->lm_mode != MK_LMHEAD_BF16 ? h->lmhead8 : nullptr;
+  p.lm_scale = h->lm_mode != MK_LMHEAD_BF16 ? h->lm_scale : nullptr;
+  p.lm_err = nullptr;
   p.layers8 = h->layer_fp8 ? h->layers8 : nullptr;
   p.lscale = h->layer_fp8 ? h->lscale : nullptr;
   p.kscale = h->kv_fp8 ? h->kscale : nullptr;
@@ -653,6 +678,17 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   const bool cls =
       h->has_cls && h->kernel_variant == MK_KERNEL_AUTO && !lc && ns_last <= kMaxClsSplit && h->roles_ok[ns_last];
   p.roles = cls ? h->roles + (size_t)(ns_last - 1) * h->G * ROLE_INTS : nullptr;
+  if (h->lm_mode == MK_LMHEAD_SCREENED) {
+    // the screened LM head runs in the class kernel, and not for validation
+    // outputs (they report every row's bf16 logit); elsewhere the bf16 head
+    // gives the same tokens
+    if (cls && !p.dbg_logits && (h->V / 16 + h->G - 1) / h->G * 16 <= LM_ROWS_MAX) {
+      p.lm_err = h->lm_err;
+    } else {
+      p.lmhead8 = nullptr;
+      p.lm_scale = nullptr;
+    }
+  }
   if (h->layer_fp8 && !cls) {
     set_err("FP8 layer weights need the class kernel (automatic variant, at most %d attention splits per kv head; "
             "this launch needs %d)", kMaxClsSplit, ns_last);
@@ -1134,6 +1170,10 @@ int megakernel_set_lmhead_fp8(void* handle, int enable) {
     mk::set_err("null handle");
     return -1;
   }
+  if (enable < MK_LMHEAD_BF16 || enable > MK_LMHEAD_SCREENED) {
+    mk::set_err("unknown LM head mode %d", enable);
+    return -1;
+  }
   if (enable && !h->lmhead8) {
     const int K = h->sh.H;
     if (h->V % 16 || K % 64) {
@@ -1142,12 +1182,13 @@ int megakernel_set_lmhead_fp8(void* handle, int enable) {
     }
     HIPCHK(hipMalloc(&h->lmhead8, (size_t)h->V * K), -1);
     HIPCHK(hipMalloc(&h->lm_scale, (size_t)h->V * 4), -1);
+    HIPCHK(hipMalloc(&h->lm_err, (size_t)h->V * 4), -1);
     hipLaunchKernelGGL(mk::lmhead_fp8_kernel, dim3(h->V / 16), dim3(256), 0, h->stream, h->lmhead, K,
-                       reinterpret_cast<unsigned char*>(h->lmhead8), h->lm_scale);
+                       reinterpret_cast<unsigned char*>(h->lmhead8), h->lm_scale, h->lm_err);
     HIPCHK(hipGetLastError(), -1);
     HIPCHK(hipStreamSynchronize(h->stream), -1);
   }
-  h->lm_fp8 = enable != 0;
+  h->lm_mode = enable;
   return 0;
 }
 

@@ -104,6 +104,67 @@ __device__ __forceinline__ void lm_warm_load(const Params& p, LmWarm& lw) {
     if (u < KT) lw.w[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lo * 16u, (unsigned)u * 1024u, MK_LMHEAD_AUX);
 }
 
+// ||h|| of the LM head's input (sm.vec_l, x * final_norm gain, in LDS).
+template <class S>
+__device__ __forceinline__ float lm_hnorm(Smem<S>& sm) {
+  const int tid = ltid();
+  float ss = 0.f;
+  for (int i = tid; i < S::H; i += NT) ss = fmaf(sm.vec_l[i], sm.vec_l[i], ss);
+  ss = wave_sum(ss);
+  if (lane_id() == 0) sm.lmw[wave_id()] = ss;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += sm.lmw[i];
+  __syncthreads();
+  return sqrtf(t) * (1.0f + 0x1p-12f);  // rounded up: part of the bound
+}
+
+// Screening threshold: the largest lower bound over all workgroups.  Each
+// workgroup publishes its own as an argmax-style word (ordered value, 14-bit
+// tag) in the second half of p.amax and reads every workgroup's.
+template <class S>
+__device__ __forceinline__ bool lm_threshold(const Params& p, Smem<S>& sm, int t, unsigned tl, float lowmax,
+                                             float* thr) {
+  const int G = gridDim.x, wg = blockIdx.x, tid = ltid(), w = wave_id(), l = (int)lane_id();
+  u64* slots = p.amax + 2 * G + (t & 1) * G;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) lowmax = fmaxf(lowmax, __shfl_xor(lowmax, m));
+  if (l == 0) sm.lmw[w] = lowmax;
+  __syncthreads();
+  if (tid == 0) {
+    float v = sm.lmw[0];
+    for (int i = 1; i < NW; ++i) v = fmaxf(v, sm.lmw[i]);
+    ll_put(slots + wg, ((u64)f32_order_key(v) << 32) | (u64)tag14(tl));
+  }
+  int failed = 0;
+  u64 best = 0ull;
+  for (int i = tid; i < G && !failed; i += NT) {
+    Spin sp;
+    u64 v;
+    while (((v = ll_get(slots + i)) & TAG14) != tag14(tl))
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    best = v > best ? v : best;
+  }
+  if (block_failed(failed)) return false;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const u64 o = __shfl_xor(best, m);
+    best = o > best ? o : best;
+  }
+  if (l == 0) sm.amax[w] = best;
+  __syncthreads();
+  best = sm.amax[0];
+  for (int i = 1; i < NW; ++i) best = sm.amax[i] > best ? sm.amax[i] : best;
+  __syncthreads();
+  const uint32_t k = (uint32_t)(best >> 32);
+  *thr = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);  // inverse of f32_order_key
+  return true;
+}
+
 template <class S, int MODE, class AfterPoll>
 __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t, unsigned tb, AfterPoll after_poll,
                                             const LmWarm& lw, bool idle = false) {
@@ -121,6 +182,13 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
   const long long b0 = (long long)wg * nb / G, b1 = (long long)(wg + 1) * nb / G;
   u64 best = 0ull;
   const int wv_ = wave_id();
+  // screened (FP8 copy + p.lm_err): the FP8 pass keeps, per row, the upper
+  // bound u = l8 + e of the bf16 logit (e = rn ||h|| B_r) and the largest
+  // lower bound l8 - e; the rows that can still hold the argmax are scored
+  // again from the bf16 tiles below
+  const bool screen = F8 && p.lm_err != nullptr;
+  float eh = 0.f, lowmax = -INFINITY;
+  if (screen) eh = rn * lm_hnorm<S>(sm) * (1.0f + 0x1p-12f);
   for (long long b = b0 + wv_; b < b1; b += NW) {
     const unsigned lo = lane_id();
     constexpr int E = F8 ? 16 : 8, KT = S::H / (4 * E);
@@ -159,9 +227,49 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
     if constexpr (F8) acc *= p.lm_scale[b * 16 + (l & 15)];
     if (l < 16) {
       const unsigned idx = (unsigned)(b * 16 + l);
-      if (DBG && p.dbg_logits) p.dbg_logits[idx] = acc;
-      const u64 key = ((u64)f32_order_key(acc) << 32) | ((u64)(IDX_MAX - idx) << 14);
-      best = key > best ? key : best;
+      if (screen) {
+        const float e = eh * p.lm_err[idx];
+        sm.lmu[idx - b0 * 16] = acc + e;
+        lowmax = fmaxf(lowmax, acc - e);
+      } else {
+        if (DBG && p.dbg_logits) p.dbg_logits[idx] = acc;
+        const u64 key = ((u64)f32_order_key(acc) << 32) | ((u64)(IDX_MAX - idx) << 14);
+        best = key > best ? key : best;
+      }
+    }
+  }
+  if (screen) {
+    float thr;
+    if (!lm_threshold<S>(p, sm, t, tl, lowmax, &thr)) return false;
+    // rescoring: a block any of whose rows' bound reaches the threshold is
+    // scored from the bf16 tiles with the bf16 head's arithmetic (the same
+    // dot8 chain over the same units, the same lane sum); every row that can
+    // be the argmax is among them (its bf16 logit >= thr > every skipped
+    // row's upper bound), so the argmax equals the bf16 head's
+    const unsigned lo = lane_id();
+    const float* hv = sm.vec_l + (lo >> 4) * 8;
+    constexpr int KTB = S::KT_H;
+    for (long long b = b0 + wv_; b < b1; b += NW) {
+      const bool cand = __ballot(l < 16 && sm.lmu[b * 16 + l - b0 * 16] >= thr) != 0ull;
+      if (!cand) continue;
+      const auto rs = make_rsrc(p.lmhead + b * KTB * 64);
+      float acc = 0.f;
+#pragma unroll 1
+      for (int k0 = 0; k0 < KTB; k0 += LM_U) {
+        u32x4 wv[LM_U];
+#pragma unroll
+        for (int u = 0; u < LM_U; ++u)
+          if (k0 + u < KTB) wv[u] = buf_ld_nt(rs, lo * 16u, (unsigned)(k0 + u) * 1024u);
+#pragma unroll
+        for (int u = 0; u < LM_U; ++u)
+          if (k0 + u < KTB) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
+      }
+      acc = stride_sum<16>(acc) * rn;
+      if (l < 16) {
+        const unsigned idx = (unsigned)(b * 16 + l);
+        const u64 key = ((u64)f32_order_key(acc) << 32) | ((u64)(IDX_MAX - idx) << 14);
+        best = key > best ? key : best;
+      }
     }
   }
 #pragma unroll

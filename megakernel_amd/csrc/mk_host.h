@@ -45,7 +45,7 @@ __global__ void kv_dequant_kernel(uint16_t* __restrict__ buf, const uint8_t* __r
                                   const uint8_t* __restrict__ v8, const float* __restrict__ ks,
                                   const float* __restrict__ vs, int L, int NKV, int s_pad, int D, int len);
 __global__ void lmhead_fp8_kernel(const u32x4* __restrict__ src, int K, unsigned char* __restrict__ dst,
-                                  float* __restrict__ scales);
+                                  float* __restrict__ scales, float* __restrict__ err);
 __global__ void synth_kv_ref_kernel(uint16_t* __restrict__ buf, int L, int NKV, int D, int len,
                                     unsigned long long seed, float c);
 

@@ -63,6 +63,7 @@ struct Params {
   const u32x4* lmhead;        // packed tied embedding [V/16][KT_H][64]
   const u32x4* lmhead8;       // optional FP8 (e4m3) copy of the LM head [V/16][H/64][64]
   const float* lm_scale;      // [V] power-of-two row scales of lmhead8
+  const float* lm_err;        // [V] error bounds of the FP8 rows: set = screened LM head (class kernel)
   float* kscale;              // FP8 KV cache (MODE bit 3): power-of-two scale of each K row
   float* vscale;              //   and V row, [L][NKV][s_pad]; the codes replace the bf16 values
                               //   at byte index = element index of kv / kvt
@@ -100,6 +101,9 @@ struct Params {
 // (a phase's product ends without a barrier after its reads, so the next
 // phase's product must not overwrite the shares being summed).
 enum RedBuf : int { RED_Q = 0, RED_O0, RED_O1, RED_G, RED_U, RED_D, RED_N };
+// LM-head rows of one workgroup the screened LM head holds bounds for (the
+// host uses the bf16 head when a workgroup would have more)
+constexpr int LM_ROWS_MAX = 1024;
 
 template <class S>
 struct Smem {
@@ -123,6 +127,8 @@ struct Smem {
   float rc[S::D / 2], rs[S::D / 2];   // RoPE cos / sin of this token
   u64 amax[NW];
   float mrg[4][NT];                   // long-context split merge: (max, sum, out0, out1) per thread
+  float lmu[LM_ROWS_MAX];             // screened LM head: upper bounds of this workgroup's row logits
+  float lmw[NW];                      // screened LM head: per-wave partials
 };
 
 // Element `col` of row `row` of a packed [R][K] matrix (K = 32 * KT).

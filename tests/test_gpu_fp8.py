@@ -419,3 +419,41 @@ def test_fp8_layers_full_model_ctx1024():
     finally:
         eng.close()
         dw.free()
+
+
+# -------------------------------------------------------- screened LM head
+@pytest.mark.parametrize("name,ctx", [("baseline_2l", 300), ("baseline_full", 1024)])
+def test_screened_lmhead_tokens_equal_bf16_head(name, ctx):
+    """MK_LMHEAD_SCREENED: the FP8 copy screens the rows, the rows whose bound
+    reaches the threshold are scored again from the bf16 tiles; the argmax is
+    then the bf16 head's, so a resident launch of 64 tokens (and the per-token
+    path) produces exactly the bf16 head's tokens.  The full model also checks
+    them teacher-forced against the oracle."""
+    from megakernel_amd import _lib
+    shape = BASELINE_2L if name == "baseline_2l" else BASELINE
+    eng, orc, dw = make_pair(shape, 71, ctx + 80, gain_std=0.0, bits_from_device=name == "baseline_full")
+    try:
+        eng.fill_kv_synthetic(ctx, 71)
+        ref = eng.decode_many(5, 64)
+        eng.set_lmhead_fp8(_lib.LMHEAD_SCREENED)
+        eng.set_pos(ctx)
+        got = eng.decode_many(5, 64)
+        _print(f"screened {name}: first tokens {got[:6]} / bf16 {ref[:6]}")
+        assert got == ref, f"screened tokens differ from the bf16 head's (first at {next(i for i, (a, b) in enumerate(zip(got, ref)) if a != b)})"
+        eng.set_pos(ctx)
+        per = [eng.decode_token(5)]
+        for _ in range(15):
+            per.append(eng.decode_token(per[-1]))
+        assert per == ref[:16], "per-token screened decoding differs"
+        if name == "baseline_full":
+            kv = eng.get_kv(ctx)
+            orc.set_kv(kv[:, 0], kv[:, 1])
+            del kv
+            same, low = check_tokens_teacher_forced([5] + ref[:-1], ref, orc)
+            _print(f"screened full model, 64 tokens: {same} identical, {low} low-margin")
+        eng.set_lmhead_fp8(_lib.LMHEAD_BF16)
+        eng.set_pos(ctx)
+        assert eng.decode_many(5, 64) == ref
+    finally:
+        eng.close()
+        dw.free()
