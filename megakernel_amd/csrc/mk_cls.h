@@ -241,33 +241,41 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
   if (screen) {
     float thr;
     if (!lm_threshold<S>(p, sm, t, tl, lowmax, &thr)) return false;
-    // rescoring: a block any of whose rows' bound reaches the threshold is
-    // scored from the bf16 tiles with the bf16 head's arithmetic (the same
-    // dot8 chain over the same units, the same lane sum); every row that can
-    // be the argmax is among them (its bf16 logit >= thr > every skipped
-    // row's upper bound), so the argmax equals the bf16 head's
+    // rescoring: every row whose bound reaches the threshold is scored from
+    // the bf16 tiles with the bf16 head's arithmetic -- lane (q, s) of a wave
+    // takes column group q of its row s from every unit (the lane that holds
+    // them in the row's block), the same dot8 chain over the same units and
+    // the same lane sum as the bf16 head's block scoring, so the logit is
+    // bit-identical; every row that can be the argmax is among them (its bf16
+    // logit >= thr > every skipped row's upper bound), so the argmax equals
+    // the bf16 head's.  Sixteen rows per wave at a time.
+    if (tid == 0) sm.lmn = 0;
+    __syncthreads();
+    for (long long b = b0 + wv_; b < b1; b += NW)
+      if (l < 16 && sm.lmu[b * 16 + l - b0 * 16] >= thr) sm.lmc[atomicAdd(&sm.lmn, 1)] = (int)(b * 16 + l);
+    __syncthreads();
+    const int nc = sm.lmn;
     const unsigned lo = lane_id();
     const float* hv = sm.vec_l + (lo >> 4) * 8;
     constexpr int KTB = S::KT_H;
-    for (long long b = b0 + wv_; b < b1; b += NW) {
-      const bool cand = __ballot(l < 16 && sm.lmu[b * 16 + l - b0 * 16] >= thr) != 0ull;
-      if (!cand) continue;
-      const auto rs = make_rsrc(p.lmhead + b * KTB * 64);
+    for (int c0 = wv_ * 16; c0 < nc; c0 += NW * 16) {
+      const int j = c0 + (int)(lo & 15u);
+      const int row = sm.lmc[j < nc ? j : c0];
+      const u32x4* base = p.lmhead + (long long)(row >> 4) * KTB * 64 + (lo >> 4) * 16 + (row & 15);
       float acc = 0.f;
 #pragma unroll 1
       for (int k0 = 0; k0 < KTB; k0 += LM_U) {
         u32x4 wv[LM_U];
 #pragma unroll
         for (int u = 0; u < LM_U; ++u)
-          if (k0 + u < KTB) wv[u] = buf_ld_nt(rs, lo * 16u, (unsigned)(k0 + u) * 1024u);
+          if (k0 + u < KTB) wv[u] = __builtin_nontemporal_load(base + (k0 + u) * 64);
 #pragma unroll
         for (int u = 0; u < LM_U; ++u)
           if (k0 + u < KTB) acc = dot8(wv[u], hv + (k0 + u) * 32, acc);
       }
       acc = stride_sum<16>(acc) * rn;
-      if (l < 16) {
-        const unsigned idx = (unsigned)(b * 16 + l);
-        const u64 key = ((u64)f32_order_key(acc) << 32) | ((u64)(IDX_MAX - idx) << 14);
+      if (lo < 16u && j < nc) {
+        const u64 key = ((u64)f32_order_key(acc) << 32) | ((u64)(IDX_MAX - (unsigned)row) << 14);
         best = key > best ? key : best;
       }
     }

@@ -129,6 +129,8 @@ struct Smem {
   float mrg[4][NT];                   // long-context split merge: (max, sum, out0, out1) per thread
   float lmu[LM_ROWS_MAX];             // screened LM head: upper bounds of this workgroup's row logits
   float lmw[NW];                      // screened LM head: per-wave partials
+  int lmc[LM_ROWS_MAX];               // screened LM head: this workgroup's rows to rescore
+  int lmn;                            //   and their count
 };
 
 // Element `col` of row `row` of a packed [R][K] matrix (K = 32 * KT).

@@ -463,3 +463,31 @@ def test_dataflow_handoff_selftest():
     assert rc == 0, _lib.last_error(lib)
     assert bad.value == 0
     assert 0.0 < us.value < 100.0
+
+
+def test_bridge_benchmark_and_sweep():
+    """MegakernelEngine.benchmark (the reference bridge's per-call loop: five
+    warm-up tokens, reset, num_tokens timed calls) and benchmark_sweep (KV
+    prefilled to each position, one timed resident launch): positive finite
+    rates, the position they leave behind, and bandwidth figures under the
+    HBM peak; the per-call loop's tokens are those of one resident launch."""
+    eng, orc, dw = make_pair(BASELINE_2L, 83, 640)
+    try:
+        tps = eng.benchmark(num_tokens=20, prompt_token=3)
+        _print(f"benchmark: {tps:.1f} tok/s")
+        assert np.isfinite(tps) and tps > 0 and eng.pos == 20
+        eng.reset()
+        per_call = [eng.decode_token(3)]
+        for _ in range(19):
+            per_call.append(eng.decode_token(per_call[-1]))
+        eng.reset()
+        assert eng.decode_many(3, 20) == per_call
+        res = eng.benchmark_sweep(positions=[1, 100, 500], bench_tokens=8)
+        _print("sweep: " + ", ".join(f"{r['position']}: {r['tok_per_sec']:.0f} tok/s" for r in res))
+        assert [r["position"] for r in res] == [1, 100, 500]
+        for r in res:
+            assert r["tok_per_sec"] > 0 and r["latency_us"] > 0 and 0 < r["bw_util"] < 1.0
+        assert eng.pos == 500 + 8
+    finally:
+        eng.close()
+        dw.free()
