@@ -1184,8 +1184,12 @@ template <class S, bool K8 = false>
 __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_PER_EU, ATTN_WAVES_PER_EU))) void bk_attn(
     BParams p, int layer) {
   __shared__ AttnLds<S> sm;
-  const int item = blockIdx.x;
-  const int b = item / (S::NKV * p.nsplit_max), g = (item / p.nsplit_max) % S::NKV, s = item % p.nsplit_max;
+  // workgroup i runs on XCD i % 8: every split of one (sequence, kv head)
+  // pair gets the same XCD, so the merging split reads its partials there
+  static_assert((BMAX * S::NKV) % 8 == 0, "whole (sequence, kv head) pairs per XCD");
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+  const int bg = (slot / p.nsplit_max) * 8 + xcd, s = slot % p.nsplit_max;
+  const int b = bg / S::NKV, g = bg % S::NKV;
   if (b >= p.B) return;
   const int pos = p.pos[b];
   const int nsplit = (pos + 1 + CH - 1) / CH;
