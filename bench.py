@@ -72,7 +72,7 @@ def parse():
     ap.add_argument("--ops-rotate-mib", type=int, default=512, help="size of the rotated copies per op")
     ap.add_argument("--prefill", type=int, default=0,
                     help="prefill instead: consume a prompt of this many tokens (from an empty cache) with "
-                         "megakernel_batch_prefill, 16 tokens per weight pass")
+                         "megakernel_batch_prefill, 64 tokens per weight pass")
     return ap.parse_args()
 
 
@@ -243,7 +243,7 @@ def bench_batch(args):
     import numpy as np
 
     from megakernel_amd import _lib, launcher
-    from megakernel_amd.batch import BatchEngine
+    from megakernel_amd.batch import PREFILL_PASS_TOKENS, BatchEngine
     from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
     from megakernel_amd.weights import DeviceWeights
 
@@ -440,18 +440,18 @@ def bench_ops(args):
 
 def bench_prefill(args):
     """Prefill of an N-token prompt (uniform random ids from the seed) into an
-    empty cache with megakernel_batch_prefill: chunks of 16 tokens, each one
-    pass over the layer weights with its tokens as the matrix columns, the LM
-    head once for the next token.  Timed: --reps calls after one warm-up (the
+    empty cache with megakernel_batch_prefill: passes of 64 tokens (four
+    groups of 16 matrix columns), each one sweep over the layer weights, the
+    LM head once for the next token.  Timed: --reps calls after one warm-up (the
     position reset to 0 before each), median; inputs resident in HBM.
-    Algorithmic bytes: layer weights once per chunk, the KV read of every
+    Algorithmic bytes: layer weights once per pass, the KV read of every
     token's causal prefix and its append, the LM head once.  Beside it: the
     same prompt fed token by token through the batch-1 decode kernel (the
     reference's prefill-by-decode, host/bridge.py:136-163)."""
     import numpy as np
 
     from megakernel_amd import _lib, launcher
-    from megakernel_amd.batch import BatchEngine
+    from megakernel_amd.batch import PREFILL_PASS_TOKENS, BatchEngine
     from megakernel_amd.bridge import MegakernelEngine
     from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
     from megakernel_amd.weights import DeviceWeights
@@ -486,8 +486,8 @@ def bench_prefill(args):
     one.close()
     dw.free()
     wall, kern = statistics.median(walls), statistics.median(kernels)
-    nchunks = (N + 15) // 16
-    nbytes = (nchunks * shape.n_layers * shape.layer_weight_bytes + 2 * shape.vocab * shape.hidden +
+    npasses = (N + PREFILL_PASS_TOKENS - 1) // PREFILL_PASS_TOKENS
+    nbytes = (npasses * shape.n_layers * shape.layer_weight_bytes + 2 * shape.vocab * shape.hidden +
               2 * shape.hidden + sum(shape.kv_bytes_per_pos * (p + 2) for p in range(N)))
     achieved = nbytes / kern / 1e9
     out = {
@@ -495,8 +495,8 @@ def bench_prefill(args):
         "value": round(N / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": N, "warmup": 1,
         "ms_per_step": round(wall * 1e3 / N, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"Qwen3-0.6B-shaped prefill of a {N}-token prompt in chunks of 16 "
-                               "(megakernel_batch_prefill)", "prompt": N, "chunks": nchunks,
+        "config": {"workload": f"Qwen3-0.6B-shaped prefill of a {N}-token prompt in passes of "
+                               f"{PREFILL_PASS_TOKENS} (megakernel_batch_prefill)", "prompt": N, "passes": npasses,
                    "device": info["name"], "reps": args.reps},
         "prefill_by_decode_tok_s": round(by_decode, 1),
         "next_token": toks[-1],

@@ -15,6 +15,9 @@ import numpy as np
 from . import _lib
 from .config import BASELINE, ModelShape
 
+# prompt tokens per weight pass of a prefill: four column groups of 16
+PREFILL_PASS_TOKENS = 64
+
 
 class BatchEngine:
     def __init__(self, device_weights, n_seq: int, max_seq: int, shape: ModelShape = BASELINE,
@@ -116,9 +119,9 @@ class BatchEngine:
         return list(out), logits
 
     def prefill(self, seq: int, tokens, with_logits: bool = False):
-        """Consume a prompt for sequence seq at its position (chunks of 16
-        tokens, one weight pass each); returns the greedy next token, and its
-        fp32 logits [vocab] when with_logits."""
+        """Consume a prompt for sequence seq at its position (passes of
+        PREFILL_PASS_TOKENS tokens, one weight pass each); returns the greedy
+        next token, and its fp32 logits [vocab] when with_logits."""
         toks = [int(t) for t in tokens]
         arr = (ctypes.c_int * max(1, len(toks)))(*toks)
         nxt = ctypes.c_int(-1)

@@ -36,7 +36,15 @@ struct BHandle {
   int (*launch_step)(BHandle*, const BParams&) = nullptr;
   int step_variant = MK_BATCH_STEP_PER_PHASE;  // one kernel per phase and layer, or the layers in bk_step
   bool persistent_ok = false;                  // bk_step fits one workgroup on every CU
-  int (*launch_prefill)(BHandle*, const BParams&, bool) = nullptr;
+  int (*launch_prefill)(BHandle*, const PGroup&, bool) = nullptr;
+  // prefill column groups 1 .. PG_MAX - 1: their own activation buffers (group 0 uses p's)
+  struct GroupBufs {
+    float *x, *ssq, *qkv, *part, *gpart, *rope;
+    uint16_t *xg, *att, *act;
+    int *cnt, *gcnt;
+    u64* keys;
+  } gb[PG_MAX - 1] = {};
+  bool gb_ok = false;
 };
 
 static void free_all(BHandle* h) {
@@ -79,24 +87,29 @@ static int repack_tiles(BHandle* h, const char* base, long long off, int R, int 
 template <class S>
 static int launch_step(BHandle* h, const BParams& p) {
   const int L = h->L;
-  hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
+  PGroup1 g{};  // one column group
+  g.p[0] = p;
+  g.n = 1;
+  hipLaunchKernelGGL((bk_embed<S, PGroup1>), dim3(BMAX), dim3(256), 0, h->stream, g);
   // the final-norm parts: slot L of the persistent step, slot 0 of the per-phase kernels
   const int lm_slot = h->step_variant == MK_BATCH_STEP_PERSISTENT ? L : 0;
   if (h->step_variant == MK_BATCH_STEP_PERSISTENT) {
     if (p.kscale)
-      hipLaunchKernelGGL((bk_step<S, true>), dim3(h->G * STEP_WG_PER_CU), dim3(GT), 0, h->stream, p);
+      hipLaunchKernelGGL((bk_step<S, true>), dim3(h->G * STEP_WG_PER_CU), dim3(GT), 0, h->stream, g);
     else
-      hipLaunchKernelGGL((bk_step<S, false>), dim3(h->G * STEP_WG_PER_CU), dim3(GT), 0, h->stream, p);
+      hipLaunchKernelGGL((bk_step<S, false>), dim3(h->G * STEP_WG_PER_CU), dim3(GT), 0, h->stream, g);
   }
   for (int l = 0; l < (h->step_variant == MK_BATCH_STEP_PERSISTENT ? 0 : L); ++l) {
-    hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL((bk_qkv<S, PGroup1>), dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, g, l);
     if (p.kscale)
-      hipLaunchKernelGGL((bk_attn<S, true>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+      hipLaunchKernelGGL((bk_attn<S, true, PGroup1>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, g,
+                         l);
     else
-      hipLaunchKernelGGL((bk_attn<S, false>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16 * KS_O), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
+      hipLaunchKernelGGL((bk_attn<S, false, PGroup1>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream,
+                         g, l);
+    hipLaunchKernelGGL((bk_o<S, PGroup1>), dim3(S::H / 16 * KS_O), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_gu<S, PGroup1>), dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_down<S, PGroup1>), dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, g, l);
   }
   if (p.lmhead8)
     hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p, lm_slot);
@@ -107,40 +120,48 @@ static int launch_step(BHandle* h, const BParams& p) {
   return 0;
 }
 
-// One prefill chunk (p.B <= 16 consecutive prompt tokens of one sequence as
-// the columns): the decode step's kernels with bk_append storing every
-// column's K / V before each layer's attention; the LM head and the token
-// only for the prompt's last chunk.
+// One prefill pass: up to PG_MAX column groups of <= 16 consecutive prompt
+// tokens of one sequence (64 tokens per pass over the weights): the decode
+// step's kernels with bk_append storing every column's K / V before each
+// layer's attention; the LM head and the token only for the prompt's last
+// pass, on its last group (the one holding the prompt's last token).
 template <class S>
-static int launch_prefill(BHandle* h, const BParams& p, bool last) {
-  const int L = h->L;
-  hipLaunchKernelGGL(bk_embed<S>, dim3(BMAX), dim3(256), 0, h->stream, p);
+static int launch_prefill(BHandle* h, const PGroup& g, bool last) {
+  const int L = h->L, ng = g.n;
+  const BParams& p = g.p[0];
+  hipLaunchKernelGGL((bk_embed<S, PGroup>), dim3(BMAX, ng), dim3(256), 0, h->stream, g);
   for (int l = 0; l < L; ++l) {
-    hipLaunchKernelGGL(bk_qkv<S>, dim3(S::QKV / 16 * KS_QKV), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL((bk_qkv<S, PGroup>), dim3(S::QKV / 16 * KS_QKV, ng), dim3(GT), 0, h->stream, g, l);
     if (p.kscale) {
-      hipLaunchKernelGGL((bk_append<S, true>), dim3(BMAX * S::NKV), dim3(2 * kWave), 0, h->stream, p, l);
-      hipLaunchKernelGGL((bk_attn<S, true>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+      hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
+                         l);
+      hipLaunchKernelGGL((bk_attn<S, true, PGroup>), dim3(BMAX * S::NKV * h->nsplit_max, ng), dim3(AT), 0, h->stream,
+                         g, l);
     } else {
-      hipLaunchKernelGGL((bk_append<S, false>), dim3(BMAX * S::NKV), dim3(2 * kWave), 0, h->stream, p, l);
-      hipLaunchKernelGGL((bk_attn<S, false>), dim3(BMAX * S::NKV * h->nsplit_max), dim3(AT), 0, h->stream, p, l);
+      hipLaunchKernelGGL((bk_append<S, false, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
+                         l);
+      hipLaunchKernelGGL((bk_attn<S, false, PGroup>), dim3(BMAX * S::NKV * h->nsplit_max, ng), dim3(AT), 0, h->stream,
+                         g, l);
     }
-    hipLaunchKernelGGL(bk_o<S>, dim3(S::H / 16 * KS_O), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_gu<S>, dim3(S::F / 16 * KS_GU), dim3(GT), 0, h->stream, p, l);
-    hipLaunchKernelGGL(bk_down<S>, dim3(S::H / 16 * KS_DN), dim3(GT), 0, h->stream, p, l);
+    hipLaunchKernelGGL((bk_o<S, PGroup>), dim3(S::H / 16 * KS_O, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_gu<S, PGroup>), dim3(S::F / 16 * KS_GU, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_down<S, PGroup>), dim3(S::H / 16 * KS_DN, ng), dim3(GT), 0, h->stream, g, l);
   }
   if (last) {
-    if (p.lmhead8)
-      hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, p, 0);
+    const BParams& pl = g.p[ng - 1];
+    if (pl.lmhead8)
+      hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, pl, 0);
     else
-      hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, p, 0);
-    hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, p);
+      hipLaunchKernelGGL((bk_lm<S, false>), dim3(h->G), dim3(GT), 0, h->stream, pl, 0);
+    hipLaunchKernelGGL(bk_tok, dim3(1), dim3(BMAX), 0, h->stream, pl);
   }
   HIPCHK(hipGetLastError(), -1);
   return 0;
 }
+static_assert((ShapeBaseline::QKV / 16) % 8 == 0 && (ShapeBaseline::H / 16) % 8 == 0 &&
+                  (ShapeBaseline::F / 16) % 8 == 0 && (ShapeQwen3::F / 16) % 8 == 0 && (ShapeTiny::F / 16) % 8 == 0,
+              "GEMM grids of whole XCD rounds: a block's column groups share an XCD");
 
-// The persistent step needs every one of its workgroups resident at once:
-// STEP_WG_PER_CU per CU for both cache formats.
 template <class S>
 static bool persistent_fits() {
   int a = 0, b = 0;
@@ -374,9 +395,34 @@ static int run_steps(BHandle* h, const int* first, int n, int* out) {
   return 0;
 }
 
-// n prompt tokens at positions pos0 .. of sequence seq's cache: chunks of up
-// to 16 tokens, each one pass over the weights with the tokens as MFMA columns.
-static int prefill_chunks(BHandle* h, int seq, const int* tokens, int n, int pos0, int* next_token, float* logits) {
+// Activation buffers of prefill column groups 1 .. PG_MAX - 1 (slot 0 sizes:
+// the prefill runs the per-phase kernels), allocated on the first prefill of
+// more than 16 tokens.
+static int ensure_groups(BHandle* h) {
+  if (h->gb_ok) return 0;
+  const size_t gp = (size_t)((h->F / 16) * KS_GU * 2 > (h->QKV / 16) * KS_QKV ? (h->F / 16) * KS_GU * 2
+                                                                              : (h->QKV / 16) * KS_QKV) *
+                        256 * 4 + (size_t)(h->H / 16) * (KS_O > KS_DN ? KS_O : KS_DN) * 256 * 4;
+  const size_t gc = (size_t)(h->F / 16 > h->QKV / 16 ? h->F / 16 : h->QKV / 16) * 4;
+  for (int i = 0; i < PG_MAX - 1; ++i) {
+    BHandle::GroupBufs& b = h->gb[i];
+    if (alloc(h, &b.x, (size_t)2 * BMAX * h->H * 4) || alloc(h, &b.xg, (size_t)4 * BMAX * h->H * 2) ||
+        alloc(h, &b.ssq, (size_t)2 * (h->H / 16) * BMAX * 4) || alloc(h, &b.qkv, (size_t)BMAX * h->QKV * 4) ||
+        alloc(h, &b.att, (size_t)2 * BMAX * h->QD * 2) || alloc(h, &b.act, (size_t)2 * BMAX * h->F * 2) ||
+        alloc(h, &b.part, (size_t)BMAX * h->NKV * h->nsplit_max * PW * 4) ||
+        alloc(h, &b.cnt, (size_t)BMAX * h->NKV * 4) || alloc(h, &b.gpart, gp) || alloc(h, &b.gcnt, gc) ||
+        alloc(h, &b.keys, (size_t)BMAX * 8) || alloc(h, &b.rope, (size_t)BMAX * h->D * 4))
+      return -1;
+  }
+  HIPCHK(hipStreamSynchronize(h->stream), -1);
+  h->gb_ok = true;
+  return 0;
+}
+
+// n prompt tokens at positions pos0 .. of sequence seq's cache: passes of up
+// to 64 tokens (four column groups of 16), each one pass over the weights with
+// the tokens as MFMA columns.
+static int prefill_passes(BHandle* h, int seq, const int* tokens, int n, int pos0, int* next_token, float* logits) {
   if (n < 1) {
     set_err("prefill: n = %d < 1", n);
     return -1;
@@ -398,31 +444,43 @@ static int prefill_chunks(BHandle* h, int seq, const int* tokens, int n, int pos
   HIPCHK(hipMemcpyAsync(h->pf_pos, q.data(), (size_t)n * 4, hipMemcpyHostToDevice, h->stream), -1);
   HIPCHK(hipMemsetAsync(h->pf_step, 0, 4, h->stream), -1);
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
-  for (int c0 = 0; c0 < n; c0 += BMAX) {
-    const int cnt = n - c0 < BMAX ? n - c0 : BMAX;
-    const bool last = c0 + cnt == n;
-    BParams pp = h->p;
-    // every column writes and reads this sequence's cache (FP8: byte index =
-    // element index, so the sequence starts at byte seq * kv_seq)
-    if (h->p.kscale) {
-      pp.kv = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kv) + seq * h->p.kv_seq);
-      pp.kvt = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kvt) + seq * h->p.kv_seq);
-      pp.kscale = h->p.kscale + seq * h->p.sc_seq;
-      pp.vscale = h->p.vscale + seq * h->p.sc_seq;
-    } else {
-      pp.kv = h->p.kv + seq * h->p.kv_seq;
-      pp.kvt = h->p.kvt + seq * h->p.kv_seq;
+  if (n > BMAX && ensure_groups(h)) return -1;
+  for (int c0 = 0; c0 < n; c0 += PG_MAX * BMAX) {
+    PGroup g{};
+    g.n = 0;
+    for (int gi = 0; gi < PG_MAX && c0 + gi * BMAX < n; ++gi) {
+      const int cs = c0 + gi * BMAX, cnt = n - cs < BMAX ? n - cs : BMAX;
+      const bool last = cs + cnt == n;
+      BParams& pp = g.p[gi];
+      pp = h->p;
+      if (gi > 0) {  // the group's own activation buffers
+        const BHandle::GroupBufs& b = h->gb[gi - 1];
+        pp.x = b.x, pp.xg = b.xg, pp.ssq = b.ssq, pp.qkv = b.qkv, pp.att = b.att, pp.act = b.act;
+        pp.part = b.part, pp.cnt = b.cnt, pp.gpart = b.gpart, pp.gcnt = b.gcnt, pp.keys = b.keys, pp.rope = b.rope;
+      }
+      // every column writes and reads this sequence's cache (FP8: byte index =
+      // element index, so the sequence starts at byte seq * kv_seq)
+      if (h->p.kscale) {
+        pp.kv = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kv) + seq * h->p.kv_seq);
+        pp.kvt = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kvt) + seq * h->p.kv_seq);
+        pp.kscale = h->p.kscale + seq * h->p.sc_seq;
+        pp.vscale = h->p.vscale + seq * h->p.sc_seq;
+      } else {
+        pp.kv = h->p.kv + seq * h->p.kv_seq;
+        pp.kvt = h->p.kvt + seq * h->p.kv_seq;
+      }
+      pp.kv_seq = 0;
+      pp.sc_seq = 0;
+      pp.prefill = 1;
+      pp.B = cnt;
+      pp.tok = h->pf_tok + cs;
+      pp.pos = h->pf_pos + cs;
+      pp.out = h->pf_out;
+      pp.step = h->pf_step;
+      pp.dbg_logits = last && logits ? h->p.dbg_logits : nullptr;
+      g.n = gi + 1;
     }
-    pp.kv_seq = 0;
-    pp.sc_seq = 0;
-    pp.prefill = 1;
-    pp.B = cnt;
-    pp.tok = h->pf_tok + c0;
-    pp.pos = h->pf_pos + c0;
-    pp.out = h->pf_out;
-    pp.step = h->pf_step;
-    pp.dbg_logits = last && logits ? h->p.dbg_logits : nullptr;
-    if (h->launch_prefill(h, pp, last)) return -1;
+    if (h->launch_prefill(h, g, c0 + PG_MAX * BMAX >= n)) return -1;
   }
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);
@@ -442,7 +500,7 @@ static int run_prefill(BHandle* h, int seq, const int* tokens, int n, int* next_
   }
   int pos0 = 0;
   HIPCHK(hipMemcpy(&pos0, h->p.pos + seq, 4, hipMemcpyDeviceToHost), -1);
-  if (prefill_chunks(h, seq, tokens, n, pos0, next_token, logits)) return -1;
+  if (prefill_passes(h, seq, tokens, n, pos0, next_token, logits)) return -1;
   const int pend = pos0 + n;
   HIPCHK(hipMemcpy(h->p.pos + seq, &pend, 4, hipMemcpyHostToDevice), -1);
   return 0;
@@ -468,7 +526,7 @@ int prefill_context_run(BHandle* h, const int* tokens, int n, int pos0, int* nex
                         float* kscale, float* vscale) {
   h->p.kscale = kscale;  // the bound cache's FP8 row scales, or null for a bf16 cache
   h->p.vscale = vscale;
-  return prefill_chunks(h, 0, tokens, n, pos0, next_token, logits);
+  return prefill_passes(h, 0, tokens, n, pos0, next_token, logits);
 }
 
 float prefill_context_ms(BHandle* h) { return h->last_ms; }

@@ -117,6 +117,23 @@ struct BParams {
                             //    K / V bk_append has already stored (kv_seq = 0, shared cache)
 };
 
+// Up to PG_MAX column groups that share one pass over the weights: a prefill
+// pass of 64 prompt tokens is four groups of 16 columns, each with its own
+// activation buffers, tokens and positions (the decode step is one group).
+// Every kernel takes the group as blockIdx.y; the GEMM workgroups of one
+// 16-row block differ in blockIdx.y only, so they run on one XCD (grid x a
+// multiple of 8) at about the same time and share the block's weights
+// through that XCD's L2.
+constexpr int PG_MAX = 4;
+template <int N>
+struct PGroupN {
+  static constexpr int NG = N;
+  BParams p[N];
+  int n;  // groups in use, 1 .. N
+};
+using PGroup = PGroupN<PG_MAX>;  // a prefill pass
+using PGroup1 = PGroupN<1>;      // the decode step
+
 // ------------------------------------------------------------ helpers
 // bf16 parts of an fp32 value: hi = RNE(v), lo = RNE(v - hi).
 __device__ __forceinline__ void split2(float v, uint16_t& hi, uint16_t& lo) {
@@ -378,9 +395,10 @@ __device__ __forceinline__ float block_reduce(f32x4 acc, float* red) {
 // ------------------------------------------------------------ kernels
 // x[b] = E[tok[b]] (the tied embedding, gathered from the tile-layout LM head),
 // published for layer 0's QKV.
-template <class S>
-__global__ __launch_bounds__(256) void bk_embed(BParams p) {
+template <class S, class G>
+__global__ __launch_bounds__(256) void bk_embed(G pg) {
   __shared__ float xs[S::H];
+  const BParams& p = pg.p[G::NG > 1 ? blockIdx.y : 0];  // column group
   const int b = blockIdx.x;
   if (b >= BMAX) return;
   const int t = ltid();
@@ -613,34 +631,34 @@ __device__ __forceinline__ bool down_block(const BParams& p, int layer, int ep, 
   return true;
 }
 
-template <class S>
-__global__ __launch_bounds__(GT) void bk_qkv(BParams p, int layer) {
+template <class S, class G>
+__global__ __launch_bounds__(GT) void bk_qkv(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ float rr[RR_N];
   __shared__ int last;
-  qkv_block<S, false>(p, layer, 0, blockIdx.x / KS_QKV, blockIdx.x % KS_QKV, red, rr, &last, NoWait{});
+  qkv_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_QKV, blockIdx.x % KS_QKV, red, rr, &last, NoWait{});
 }
 
-template <class S>
-__global__ __launch_bounds__(GT) void bk_o(BParams p, int layer) {
+template <class S, class G>
+__global__ __launch_bounds__(GT) void bk_o(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ int last;
-  o_block<S, false>(p, layer, 0, blockIdx.x / KS_O, blockIdx.x % KS_O, red, &last, NoWait{});
+  o_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_O, blockIdx.x % KS_O, red, &last, NoWait{});
 }
 
-template <class S>
-__global__ __launch_bounds__(GT) void bk_gu(BParams p, int layer) {
+template <class S, class G>
+__global__ __launch_bounds__(GT) void bk_gu(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ float rr[RR_N];
   __shared__ int last;
-  gu_block<S, false>(p, layer, 0, blockIdx.x / KS_GU, blockIdx.x % KS_GU, red, rr, &last, NoWait{});
+  gu_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_GU, blockIdx.x % KS_GU, red, rr, &last, NoWait{});
 }
 
-template <class S>
-__global__ __launch_bounds__(GT) void bk_down(BParams p, int layer) {
+template <class S, class G>
+__global__ __launch_bounds__(GT) void bk_down(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ int last;
-  down_block<S, false>(p, layer, 0, blockIdx.x / KS_DN, blockIdx.x % KS_DN, red, &last, NoWait{});
+  down_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_DN, blockIdx.x % KS_DN, red, &last, NoWait{});
 }
 
 // Final rmsnorm -> tied LM head -> per-sequence argmax (reference
@@ -768,8 +786,9 @@ __global__ void bk_tok(BParams p) {
 // arithmetic as bk_attn's prologue: k = RoPE(k_norm(k)), both stored as bf16
 // (reference kv_cache.cuh:58-78).  One workgroup per (column, kv head): wave
 // 0 stores k, wave 1 stores v.
-template <class S, bool K8 = false>
-__global__ __launch_bounds__(2 * kWave) void bk_append(BParams p, int layer) {
+template <class S, bool K8, class G>
+__global__ __launch_bounds__(2 * kWave) void bk_append(G pg, int layer) {
+  const BParams& p = pg.p[G::NG > 1 ? blockIdx.y : 0];  // column group
   // K8: FP8 rows (codes + the row's power-of-two scale from the wave's maximum)
   static_assert(S::D == kWave, "one lane per head dimension");
   constexpr int D = S::D, NKV = S::NKV;
@@ -1180,10 +1199,11 @@ __device__ __forceinline__ bool attn_item(const BParams& p, int layer, int ep, A
 // step at KV 512-4096 has ~1,100 items; with four per CU the last ~10 % ran
 // as a second, latency-bound residency wave.
 constexpr int ATTN_WAVES_PER_EU = AT == 256 ? 5 : 2;
-template <class S, bool K8 = false>
+template <class S, bool K8, class G>
 __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_PER_EU, ATTN_WAVES_PER_EU))) void bk_attn(
-    BParams p, int layer) {
+    G pg, int layer) {
   __shared__ AttnLds<S> sm;
+  const BParams& p = pg.p[G::NG > 1 ? blockIdx.y : 0];  // column group
   // workgroup i runs on XCD i % 8: every split of one (sequence, kv head)
   // pair gets the same XCD, so the merging split reads its partials there
   static_assert((BMAX * S::NKV) % 8 == 0, "whole (sequence, kv head) pairs per XCD");
@@ -1229,7 +1249,8 @@ constexpr int STEP_WAVES_PER_EU = 2 * STEP_WG_PER_CU;
 // functions, same summation order): the logits are bit-identical.
 template <class S, bool K8 = false>
 __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(STEP_WAVES_PER_EU, STEP_WAVES_PER_EU))) void bk_step(
-    BParams p) {
+    PGroup1 pg) {
+  const BParams& p = pg.p[0];  // one group
   static_assert(GT == 2 * AT, "two attention items per workgroup");
   __shared__ float red[GW * 16 * 17];
   __shared__ float rr[RR_N];
