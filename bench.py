@@ -72,7 +72,7 @@ def parse():
     ap.add_argument("--ops-rotate-mib", type=int, default=512, help="size of the rotated copies per op")
     ap.add_argument("--prefill", type=int, default=0,
                     help="prefill instead: consume a prompt of this many tokens (from an empty cache) with "
-                         "megakernel_batch_prefill, 64 tokens per weight pass")
+                         "megakernel_batch_prefill, up to 1,024 tokens per weight pass")
     return ap.parse_args()
 
 
@@ -440,9 +440,9 @@ def bench_ops(args):
 
 def bench_prefill(args):
     """Prefill of an N-token prompt (uniform random ids from the seed) into an
-    empty cache with megakernel_batch_prefill: passes of 64 tokens (four
-    groups of 16 matrix columns), each one sweep over the layer weights, the
-    LM head once for the next token.  Timed: --reps calls after one warm-up (the
+    empty cache with megakernel_batch_prefill: passes of up to 1,024 tokens
+    (64 groups of 16 matrix columns), each one sweep over the layer weights,
+    the LM head once for the next token.  Timed: --reps calls after one warm-up (the
     position reset to 0 before each), median; inputs resident in HBM.
     Algorithmic bytes: layer weights once per pass, the KV read of every
     token's causal prefix and its append, the LM head once.  Beside it: the

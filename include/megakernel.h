@@ -294,7 +294,7 @@ int megakernel_prefill(void* handle, const int* tokens, int n, int* next_token);
 /* Prefill (the reference feeds a prompt token by token
  * through its decode, host/bridge.py:136-163): the n prompt tokens of
  * sequence seq are consumed at positions pos .. pos + n - 1 in passes of up
- * to 64 (four groups of 16 matrix columns), each pass one sweep over the
+ * to 1,024 (64 groups of 16 matrix columns), each pass one sweep over the
  * weights; token i attends causally to the cache and to tokens < i.  Their
  * K / V are appended, the position advances by n, *next_token (may be NULL)
  * receives the greedy token after the last prompt token and logits (may be

@@ -15,8 +15,8 @@ import numpy as np
 from . import _lib
 from .config import BASELINE, ModelShape
 
-# prompt tokens per weight pass of a prefill: four column groups of 16
-PREFILL_PASS_TOKENS = 64
+# prompt tokens per weight pass of a prefill: 64 column groups of 16
+PREFILL_PASS_TOKENS = 1024
 
 
 class BatchEngine:

@@ -36,15 +36,12 @@ struct BHandle {
   int (*launch_step)(BHandle*, const BParams&) = nullptr;
   int step_variant = MK_BATCH_STEP_PER_PHASE;  // one kernel per phase and layer, or the layers in bk_step
   bool persistent_ok = false;                  // bk_step fits one workgroup on every CU
-  int (*launch_prefill)(BHandle*, const PGroup&, bool) = nullptr;
-  // prefill column groups 1 .. PG_MAX - 1: their own activation buffers (group 0 uses p's)
-  struct GroupBufs {
-    float *x, *ssq, *qkv, *part, *gpart, *rope;
-    uint16_t *xg, *att, *act;
-    int *cnt, *gcnt;
-    u64* keys;
-  } gb[PG_MAX - 1] = {};
-  bool gb_ok = false;
+  int (*launch_prefill)(BHandle*, const PGroup&, const BParams&, bool) = nullptr;
+  // prefill column groups: one block of activation buffers per group (slot 0
+  // sizes), pf_gstride bytes apart, grown as prompts need more groups
+  char* pf_slab = nullptr;
+  int pf_groups = 0;
+  long long pf_gstride = 0;
 };
 
 static void free_all(BHandle* h) {
@@ -121,26 +118,27 @@ static int launch_step(BHandle* h, const BParams& p) {
 }
 
 // One prefill pass: up to PG_MAX column groups of <= 16 consecutive prompt
-// tokens of one sequence (64 tokens per pass over the weights): the decode
-// step's kernels with bk_append storing every column's K / V before each
-// layer's attention; the LM head and the token only for the prompt's last
-// pass, on its last group (the one holding the prompt's last token).
+// tokens of one sequence (up to 1,024 tokens per pass over the weights): the
+// decode step's kernels with bk_append storing every column's K / V before
+// each layer's attention; the LM head and the token only for the prompt's
+// last pass, on its last group (the one holding the prompt's last token).
+// pl: the parameters of the pass's last group (the LM head's input when last).
 template <class S>
-static int launch_prefill(BHandle* h, const PGroup& g, bool last) {
+static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool last) {
   const int L = h->L, ng = g.n;
-  const BParams& p = g.p[0];
+  const BParams& p = g.p;
   hipLaunchKernelGGL((bk_embed<S, PGroup>), dim3(BMAX, ng), dim3(256), 0, h->stream, g);
   for (int l = 0; l < L; ++l) {
     hipLaunchKernelGGL((bk_qkv<S, PGroup>), dim3(S::QKV / 16 * KS_QKV, ng), dim3(GT), 0, h->stream, g, l);
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL((bk_attn<S, true, PGroup>), dim3(BMAX * S::NKV * h->nsplit_max, ng), dim3(AT), 0, h->stream,
+      hipLaunchKernelGGL((bk_attn<S, true, PGroup>), dim3(BMAX * S::NKV * p.nsplit_max, ng), dim3(AT), 0, h->stream,
                          g, l);
     } else {
       hipLaunchKernelGGL((bk_append<S, false, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL((bk_attn<S, false, PGroup>), dim3(BMAX * S::NKV * h->nsplit_max, ng), dim3(AT), 0, h->stream,
+      hipLaunchKernelGGL((bk_attn<S, false, PGroup>), dim3(BMAX * S::NKV * p.nsplit_max, ng), dim3(AT), 0, h->stream,
                          g, l);
     }
     hipLaunchKernelGGL((bk_o<S, PGroup>), dim3(S::H / 16 * KS_O, ng), dim3(GT), 0, h->stream, g, l);
@@ -148,7 +146,6 @@ static int launch_prefill(BHandle* h, const PGroup& g, bool last) {
     hipLaunchKernelGGL((bk_down<S, PGroup>), dim3(S::H / 16 * KS_DN, ng), dim3(GT), 0, h->stream, g, l);
   }
   if (last) {
-    const BParams& pl = g.p[ng - 1];
     if (pl.lmhead8)
       hipLaunchKernelGGL((bk_lm<S, true>), dim3(h->G), dim3(GT), 0, h->stream, pl, 0);
     else
@@ -395,33 +392,59 @@ static int run_steps(BHandle* h, const int* first, int n, int* out) {
   return 0;
 }
 
-// Activation buffers of prefill column groups 1 .. PG_MAX - 1 (slot 0 sizes:
-// the prefill runs the per-phase kernels), allocated on the first prefill of
-// more than 16 tokens.
-static int ensure_groups(BHandle* h) {
-  if (h->gb_ok) return 0;
-  const size_t gp = (size_t)((h->F / 16) * KS_GU * 2 > (h->QKV / 16) * KS_QKV ? (h->F / 16) * KS_GU * 2
-                                                                              : (h->QKV / 16) * KS_QKV) *
-                        256 * 4 + (size_t)(h->H / 16) * (KS_O > KS_DN ? KS_O : KS_DN) * 256 * 4;
-  const size_t gc = (size_t)(h->F / 16 > h->QKV / 16 ? h->F / 16 : h->QKV / 16) * 4;
-  for (int i = 0; i < PG_MAX - 1; ++i) {
-    BHandle::GroupBufs& b = h->gb[i];
-    if (alloc(h, &b.x, (size_t)2 * BMAX * h->H * 4) || alloc(h, &b.xg, (size_t)4 * BMAX * h->H * 2) ||
-        alloc(h, &b.ssq, (size_t)2 * (h->H / 16) * BMAX * 4) || alloc(h, &b.qkv, (size_t)BMAX * h->QKV * 4) ||
-        alloc(h, &b.att, (size_t)2 * BMAX * h->QD * 2) || alloc(h, &b.act, (size_t)2 * BMAX * h->F * 2) ||
-        alloc(h, &b.part, (size_t)BMAX * h->NKV * h->nsplit_max * PW * 4) ||
-        alloc(h, &b.cnt, (size_t)BMAX * h->NKV * 4) || alloc(h, &b.gpart, gp) || alloc(h, &b.gcnt, gc) ||
-        alloc(h, &b.keys, (size_t)BMAX * 8) || alloc(h, &b.rope, (size_t)BMAX * h->D * 4))
-      return -1;
+// The activation buffers of prefill column groups (group 0's at the slab's
+// start, group gi's gi * pf_gstride bytes later): offsets inside one group's
+// block, in BParams order x, xg, ssq, qkv, att, act, part, cnt, gpart, gcnt,
+// keys, rope.
+static long long group_layout(const BHandle* h, long long off[12]) {
+  const long long gp = (long long)((h->F / 16) * KS_GU * 2 > (h->QKV / 16) * KS_QKV ? (h->F / 16) * KS_GU * 2
+                                                                                  : (h->QKV / 16) * KS_QKV) *
+                           256 * 4 + (long long)(h->H / 16) * (KS_O > KS_DN ? KS_O : KS_DN) * 256 * 4;
+  const long long sz[12] = {(long long)2 * BMAX * h->H * 4,
+                            (long long)4 * BMAX * h->H * 2,
+                            (long long)2 * (h->H / 16) * BMAX * 4,
+                            (long long)BMAX * h->QKV * 4,
+                            (long long)2 * BMAX * h->QD * 2,
+                            (long long)2 * BMAX * h->F * 2,
+                            (long long)BMAX * h->NKV * h->nsplit_max * PW * 4,
+                            (long long)BMAX * h->NKV * 4,
+                            gp,
+                            (long long)(h->F / 16 > h->QKV / 16 ? h->F / 16 : h->QKV / 16) * 4,
+                            (long long)BMAX * 8,
+                            (long long)BMAX * h->D * 4};
+  long long o = 0;
+  for (int i = 0; i < 12; ++i) {
+    off[i] = o;
+    o += (sz[i] + 255) / 256 * 256;
   }
+  return o;
+}
+
+// A slab of ng groups' buffers, cleared (the split counters start at zero and
+// re-arm themselves); a larger prompt replaces it with a larger one.
+static int ensure_groups(BHandle* h, int ng) {
+  if (h->pf_groups >= ng) return 0;
+  long long off[12];
+  const long long stride = group_layout(h, off);
+  if (h->pf_slab) {
+    HIPCHK(hipStreamSynchronize(h->stream), -1);
+    for (size_t i = 0; i < h->owned.size(); ++i)
+      if (h->owned[i] == h->pf_slab) {
+        h->owned.erase(h->owned.begin() + (long)i);
+        break;
+      }
+    HIPCHK(hipFree(h->pf_slab), -1);
+    h->pf_slab = nullptr, h->pf_groups = 0;
+  }
+  if (alloc(h, &h->pf_slab, (size_t)stride * ng)) return -1;
   HIPCHK(hipStreamSynchronize(h->stream), -1);
-  h->gb_ok = true;
+  h->pf_groups = ng, h->pf_gstride = stride;
   return 0;
 }
 
 // n prompt tokens at positions pos0 .. of sequence seq's cache: passes of up
-// to 64 tokens (four column groups of 16), each one pass over the weights with
-// the tokens as MFMA columns.
+// to PG_MAX * 16 tokens (column groups of 16), each one pass over the weights
+// with the tokens as MFMA columns.
 static int prefill_passes(BHandle* h, int seq, const int* tokens, int n, int pos0, int* next_token, float* logits) {
   if (n < 1) {
     set_err("prefill: n = %d < 1", n);
@@ -444,43 +467,52 @@ static int prefill_passes(BHandle* h, int seq, const int* tokens, int n, int pos
   HIPCHK(hipMemcpyAsync(h->pf_pos, q.data(), (size_t)n * 4, hipMemcpyHostToDevice, h->stream), -1);
   HIPCHK(hipMemsetAsync(h->pf_step, 0, 4, h->stream), -1);
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
-  if (n > BMAX && ensure_groups(h)) return -1;
-  for (int c0 = 0; c0 < n; c0 += PG_MAX * BMAX) {
+  const int ngt = (n + BMAX - 1) / BMAX, passes = (ngt + PG_MAX - 1) / PG_MAX;
+  if (ensure_groups(h, ngt < PG_MAX ? ngt : PG_MAX)) return -1;
+  long long off[12];
+  group_layout(h, off);
+  char* slab = h->pf_slab;
+  for (int ps = 0; ps < passes; ++ps) {
+    const int c0 = ps * PG_MAX * BMAX, ntok = n - c0 < PG_MAX * BMAX ? n - c0 : PG_MAX * BMAX;
     PGroup g{};
-    g.n = 0;
-    for (int gi = 0; gi < PG_MAX && c0 + gi * BMAX < n; ++gi) {
-      const int cs = c0 + gi * BMAX, cnt = n - cs < BMAX ? n - cs : BMAX;
-      const bool last = cs + cnt == n;
-      BParams& pp = g.p[gi];
-      pp = h->p;
-      if (gi > 0) {  // the group's own activation buffers
-        const BHandle::GroupBufs& b = h->gb[gi - 1];
-        pp.x = b.x, pp.xg = b.xg, pp.ssq = b.ssq, pp.qkv = b.qkv, pp.att = b.att, pp.act = b.act;
-        pp.part = b.part, pp.cnt = b.cnt, pp.gpart = b.gpart, pp.gcnt = b.gcnt, pp.keys = b.keys, pp.rope = b.rope;
-      }
-      // every column writes and reads this sequence's cache (FP8: byte index =
-      // element index, so the sequence starts at byte seq * kv_seq)
-      if (h->p.kscale) {
-        pp.kv = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kv) + seq * h->p.kv_seq);
-        pp.kvt = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kvt) + seq * h->p.kv_seq);
-        pp.kscale = h->p.kscale + seq * h->p.sc_seq;
-        pp.vscale = h->p.vscale + seq * h->p.sc_seq;
-      } else {
-        pp.kv = h->p.kv + seq * h->p.kv_seq;
-        pp.kvt = h->p.kvt + seq * h->p.kv_seq;
-      }
-      pp.kv_seq = 0;
-      pp.sc_seq = 0;
-      pp.prefill = 1;
-      pp.B = cnt;
-      pp.tok = h->pf_tok + cs;
-      pp.pos = h->pf_pos + cs;
-      pp.out = h->pf_out;
-      pp.step = h->pf_step;
-      pp.dbg_logits = last && logits ? h->p.dbg_logits : nullptr;
-      g.n = gi + 1;
+    BParams& pp = g.p;  // group 0 of the pass
+    pp = h->p;
+    pp.x = reinterpret_cast<float*>(slab + off[0]), pp.xg = reinterpret_cast<uint16_t*>(slab + off[1]);
+    pp.ssq = reinterpret_cast<float*>(slab + off[2]), pp.qkv = reinterpret_cast<float*>(slab + off[3]);
+    pp.att = reinterpret_cast<uint16_t*>(slab + off[4]), pp.act = reinterpret_cast<uint16_t*>(slab + off[5]);
+    pp.part = reinterpret_cast<float*>(slab + off[6]), pp.cnt = reinterpret_cast<int*>(slab + off[7]);
+    pp.gpart = reinterpret_cast<float*>(slab + off[8]), pp.gcnt = reinterpret_cast<int*>(slab + off[9]);
+    pp.keys = reinterpret_cast<u64*>(slab + off[10]), pp.rope = reinterpret_cast<float*>(slab + off[11]);
+    // every column writes and reads this sequence's cache (FP8: byte index =
+    // element index, so the sequence starts at byte seq * kv_seq)
+    if (h->p.kscale) {
+      pp.kv = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kv) + seq * h->p.kv_seq);
+      pp.kvt = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(h->p.kvt) + seq * h->p.kv_seq);
+      pp.kscale = h->p.kscale + seq * h->p.sc_seq;
+      pp.vscale = h->p.vscale + seq * h->p.sc_seq;
+    } else {
+      pp.kv = h->p.kv + seq * h->p.kv_seq;
+      pp.kvt = h->p.kvt + seq * h->p.kv_seq;
     }
-    if (h->launch_prefill(h, g, c0 + PG_MAX * BMAX >= n)) return -1;
+    pp.kv_seq = 0;
+    pp.sc_seq = 0;
+    pp.prefill = 1;
+    // the pass's attention grid: the splits its last position needs (every
+    // kernel of the pass indexes the partials with this count)
+    pp.nsplit_max = (pos0 + c0 + ntok + CH - 1) / CH;
+    pp.tok = h->pf_tok + c0;
+    pp.pos = h->pf_pos + c0;
+    pp.out = h->pf_out;
+    pp.step = h->pf_step;
+    pp.dbg_logits = nullptr;
+    g.gstride = h->pf_gstride;
+    g.n = (ntok + BMAX - 1) / BMAX;
+    g.ntok = ntok;
+    pp.B = ntok < BMAX ? ntok : BMAX;
+    const bool last = ps == passes - 1;
+    BParams pl = group_params(g, g.n - 1);
+    pl.dbg_logits = last && logits ? h->p.dbg_logits : nullptr;
+    if (h->launch_prefill(h, g, pl, last)) return -1;
   }
   HIPCHK(hipEventRecord(h->ev1, h->stream), -1);
   HIPCHK(hipStreamSynchronize(h->stream), -1);

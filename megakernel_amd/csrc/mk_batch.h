@@ -118,21 +118,50 @@ struct BParams {
 };
 
 // Up to PG_MAX column groups that share one pass over the weights: a prefill
-// pass of 64 prompt tokens is four groups of 16 columns, each with its own
-// activation buffers, tokens and positions (the decode step is one group).
+// pass of up to 1,024 prompt tokens is up to 64 groups of 16 columns, each
+// with its own activation buffers, tokens and positions (the decode step is
+// one group).
 // Every kernel takes the group as blockIdx.y; the GEMM workgroups of one
 // 16-row block differ in blockIdx.y only, so they run on one XCD (grid x a
 // multiple of 8) at about the same time and share the block's weights
 // through that XCD's L2.
-constexpr int PG_MAX = 4;
+constexpr int PG_MAX = 64;
 template <int N>
-struct PGroupN {
+struct PGroupN {  // groups in the kernel argument
   static constexpr int NG = N;
   BParams p[N];
   int n;  // groups in use, 1 .. N
 };
-using PGroup = PGroupN<PG_MAX>;  // a prefill pass
-using PGroup1 = PGroupN<1>;      // the decode step
+using PGroup1 = PGroupN<1>;  // the decode step
+// A prefill pass: group 0's parameters; group gi's activation buffers (x, xg,
+// ssq, qkv, att, act, part, cnt, gpart, gcnt, keys, rope) sit gi * gstride
+// bytes after group 0's, its tokens and positions 16 gi entries after them.
+struct PGroup {
+  static constexpr int NG = PG_MAX;
+  BParams p;
+  long long gstride;
+  int n, ntok;  // groups and tokens of the pass
+};
+
+template <class T>
+__host__ __device__ __forceinline__ T* advance(T* q, long long bytes) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(q) + bytes);
+}
+// The parameters of column group gi of a pass (host and device), and of the
+// workgroup's column group (blockIdx.y).
+__host__ __device__ __forceinline__ BParams group_params(const PGroup& g, int gi) {
+  const long long o = gi * g.gstride;
+  BParams q = g.p;
+  q.x = advance(q.x, o), q.xg = advance(q.xg, o), q.ssq = advance(q.ssq, o), q.qkv = advance(q.qkv, o);
+  q.att = advance(q.att, o), q.act = advance(q.act, o), q.part = advance(q.part, o), q.cnt = advance(q.cnt, o);
+  q.gpart = advance(q.gpart, o), q.gcnt = advance(q.gcnt, o), q.keys = advance(q.keys, o);
+  q.rope = advance(q.rope, o);
+  q.tok += BMAX * gi, q.pos += BMAX * gi;
+  q.B = g.ntok - BMAX * gi < BMAX ? g.ntok - BMAX * gi : BMAX;
+  return q;
+}
+__device__ __forceinline__ const BParams& group_of(const PGroup1& g) { return g.p[0]; }
+__device__ __forceinline__ BParams group_of(const PGroup& g) { return group_params(g, blockIdx.y); }
 
 // ------------------------------------------------------------ helpers
 // bf16 parts of an fp32 value: hi = RNE(v), lo = RNE(v - hi).
@@ -398,7 +427,7 @@ __device__ __forceinline__ float block_reduce(f32x4 acc, float* red) {
 template <class S, class G>
 __global__ __launch_bounds__(256) void bk_embed(G pg) {
   __shared__ float xs[S::H];
-  const BParams& p = pg.p[G::NG > 1 ? blockIdx.y : 0];  // column group
+  const BParams& p = group_of(pg);  // column group
   const int b = blockIdx.x;
   if (b >= BMAX) return;
   const int t = ltid();
@@ -636,14 +665,14 @@ __global__ __launch_bounds__(GT) void bk_qkv(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ float rr[RR_N];
   __shared__ int last;
-  qkv_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_QKV, blockIdx.x % KS_QKV, red, rr, &last, NoWait{});
+  qkv_block<S, false>(group_of(p), layer, 0, blockIdx.x / KS_QKV, blockIdx.x % KS_QKV, red, rr, &last, NoWait{});
 }
 
 template <class S, class G>
 __global__ __launch_bounds__(GT) void bk_o(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ int last;
-  o_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_O, blockIdx.x % KS_O, red, &last, NoWait{});
+  o_block<S, false>(group_of(p), layer, 0, blockIdx.x / KS_O, blockIdx.x % KS_O, red, &last, NoWait{});
 }
 
 template <class S, class G>
@@ -651,14 +680,14 @@ __global__ __launch_bounds__(GT) void bk_gu(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ float rr[RR_N];
   __shared__ int last;
-  gu_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_GU, blockIdx.x % KS_GU, red, rr, &last, NoWait{});
+  gu_block<S, false>(group_of(p), layer, 0, blockIdx.x / KS_GU, blockIdx.x % KS_GU, red, rr, &last, NoWait{});
 }
 
 template <class S, class G>
 __global__ __launch_bounds__(GT) void bk_down(G p, int layer) {
   __shared__ float red[GW * 16 * 17];
   __shared__ int last;
-  down_block<S, false>(p.p[G::NG > 1 ? blockIdx.y : 0], layer, 0, blockIdx.x / KS_DN, blockIdx.x % KS_DN, red, &last, NoWait{});
+  down_block<S, false>(group_of(p), layer, 0, blockIdx.x / KS_DN, blockIdx.x % KS_DN, red, &last, NoWait{});
 }
 
 // Final rmsnorm -> tied LM head -> per-sequence argmax (reference
@@ -788,7 +817,7 @@ __global__ void bk_tok(BParams p) {
 // 0 stores k, wave 1 stores v.
 template <class S, bool K8, class G>
 __global__ __launch_bounds__(2 * kWave) void bk_append(G pg, int layer) {
-  const BParams& p = pg.p[G::NG > 1 ? blockIdx.y : 0];  // column group
+  const BParams& p = group_of(pg);  // column group
   // K8: FP8 rows (codes + the row's power-of-two scale from the wave's maximum)
   static_assert(S::D == kWave, "one lane per head dimension");
   constexpr int D = S::D, NKV = S::NKV;
@@ -1203,12 +1232,21 @@ template <class S, bool K8, class G>
 __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_PER_EU, ATTN_WAVES_PER_EU))) void bk_attn(
     G pg, int layer) {
   __shared__ AttnLds<S> sm;
-  const BParams& p = pg.p[G::NG > 1 ? blockIdx.y : 0];  // column group
+  const BParams& p = group_of(pg);  // column group
   // workgroup i runs on XCD i % 8: every split of one (sequence, kv head)
-  // pair gets the same XCD, so the merging split reads its partials there
+  // pair gets the same XCD, so the merging split reads its partials there.
+  // Decode: a pair's splits are consecutive slots of its XCD.  Prefill:
+  // split-major (split 0 of every pair, then split 1, ...), so the splits the
+  // short prefixes leave empty come last instead of landing on every
+  // nsplit_max-th CU slot (measured: with a pass's split count of 4,
+  // pair-major put the always-busy split-0 items on a quarter of each XCD's
+  // CUs and ran 14 % slower; split-major is also 2 % faster than pair-major
+  // with a count of 5, and 3 % slower for the batched decode).
   static_assert((BMAX * S::NKV) % 8 == 0, "whole (sequence, kv head) pairs per XCD");
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-  const int bg = (slot / p.nsplit_max) * 8 + xcd, s = slot % p.nsplit_max;
+  constexpr int PPX = BMAX * S::NKV / 8;  // pairs per XCD
+  const int bg = G::NG > 1 ? (slot % PPX) * 8 + xcd : (slot / p.nsplit_max) * 8 + xcd;
+  const int s = G::NG > 1 ? slot / PPX : slot % p.nsplit_max;
   const int b = bg / S::NKV, g = bg % S::NKV;
   if (b >= p.B) return;
   const int pos = p.pos[b];

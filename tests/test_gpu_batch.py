@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from megakernel_amd import _lib
-from megakernel_amd.batch import BatchEngine
+from megakernel_amd.batch import PREFILL_PASS_TOKENS, BatchEngine
 from megakernel_amd.config import BASELINE, TINY
 from megakernel_amd.weights import DeviceWeights
 from oracle import qwen3_ref, synth
@@ -286,9 +286,21 @@ def test_batch_prefill_tiny_edges(prompt_len):
 
 def test_batch_prefill_baseline_2l():
     """BASELINE shapes (2 layers): 70 prompt tokens after a 300-position prefix
-    (chunks straddle the 256-position attention splits)."""
+    (five column groups of one pass straddle the 256-position attention
+    splits)."""
     shape = BASELINE.with_(n_layers=2, vocab=4096)
     dw, eng, _, _ = _prefill_case(shape, 43, prefix=300, prompt_len=70, other_len=17, max_seq=400)
+    eng.close()
+    dw.free()
+
+
+def test_batch_prefill_baseline_2l_two_passes():
+    """A prompt longer than one pass (PREFILL_PASS_TOKENS): 1,030 tokens after
+    a 100-position prefix are a full pass of 64 column groups and a second
+    pass of one partial group, whose attention reads the first pass's K / V."""
+    assert PREFILL_PASS_TOKENS == 1024
+    shape = BASELINE.with_(n_layers=2, vocab=4096)
+    dw, eng, _, _ = _prefill_case(shape, 45, prefix=100, prompt_len=1030, other_len=5, max_seq=1200)
     eng.close()
     dw.free()
 
