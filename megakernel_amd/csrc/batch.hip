@@ -129,7 +129,7 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
   const BParams& p = g.p;
   hipLaunchKernelGGL((bk_embed<S, PGroup>), dim3(BMAX, ng), dim3(256), 0, h->stream, g);
   for (int l = 0; l < L; ++l) {
-    hipLaunchKernelGGL((bk_qkv<S, PGroup>), dim3(S::QKV / 16 * KS_QKV, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_pqkv<S>, dim3(S::QKV / 16 / PRB_QKV, ng), dim3(GT), 0, h->stream, g, l);
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
@@ -141,9 +141,9 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
       hipLaunchKernelGGL((bk_attn<S, false, PGroup>), dim3(BMAX * S::NKV * p.nsplit_max, ng), dim3(AT), 0, h->stream,
                          g, l);
     }
-    hipLaunchKernelGGL((bk_o<S, PGroup>), dim3(S::H / 16 * KS_O, ng), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL((bk_gu<S, PGroup>), dim3(S::F / 16 * KS_GU, ng), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL((bk_down<S, PGroup>), dim3(S::H / 16 * KS_DN, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_po<S>, dim3(S::H / 16 / PRB_O, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_pgu<S>, dim3(S::F / 16 / PRB_GU, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_pdown<S>, dim3(S::H / 16 / PRB_DN * KS_DN, ng), dim3(GT), 0, h->stream, g, l);
   }
   if (last) {
     if (pl.lmhead8)
@@ -155,9 +155,9 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
   HIPCHK(hipGetLastError(), -1);
   return 0;
 }
-static_assert((ShapeBaseline::QKV / 16) % 8 == 0 && (ShapeBaseline::H / 16) % 8 == 0 &&
-                  (ShapeBaseline::F / 16) % 8 == 0 && (ShapeQwen3::F / 16) % 8 == 0 && (ShapeTiny::F / 16) % 8 == 0,
-              "GEMM grids of whole XCD rounds: a block's column groups share an XCD");
+static_assert((ShapeBaseline::QKV / 16 / PRB_QKV) % 8 == 0 && (ShapeBaseline::H / 16 / PRB_O) % 8 == 0 &&
+                  (ShapeBaseline::F / 16 / PRB_GU) % 8 == 0 && (ShapeBaseline::H / 16 / PRB_DN * KS_DN) % 8 == 0,
+              "prefill GEMM grids of whole XCD rounds: a tile's column groups share an XCD");
 
 template <class S>
 static bool persistent_fits() {

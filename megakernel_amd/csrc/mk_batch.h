@@ -690,6 +690,179 @@ __global__ __launch_bounds__(GT) void bk_down(G p, int layer) {
   down_block<S, false>(group_of(p), layer, 0, blockIdx.x / KS_DN, blockIdx.x % KS_DN, red, &last, NoWait{});
 }
 
+// ------------------------------------------------------------ prefill GEMMs
+// A prefill pass has up to 64 column groups, so each GEMM launch has 64 x the
+// decode step's workgroups and the kernels become bound by what every
+// workgroup re-reads: a 16-row block's workgroup loads its group's whole
+// activation columns (64 KB for K = 1,024).  The prefill kernels give a
+// workgroup RB consecutive 16-row blocks of one group: the columns, the norm
+// factors and the load latency are shared by RB blocks.  Per block the
+// arithmetic is the decode kernels' (same tiles, same products, same
+// cross-wave order).
+
+// RB cross-wave reductions with one barrier: v[r] = block_reduce(acc[r]).
+template <int RB>
+__device__ __forceinline__ void block_reduce_n(const f32x4 (&acc)[RB], float (*red)[GW * 16 * 17], float (&v)[RB]) {
+  const unsigned l = lane_id();
+  const int w = wave_id();
+  const int n = (int)(l & 15u), kg = (int)(l >> 4);
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[r][(w * 16 + 4 * kg + i) * 17 + n] = acc[r][i];
+  __syncthreads();
+  const int t = ltid();
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    float s = 0.f;
+    if (t < 256) {
+#pragma unroll
+      for (int ww = 0; ww < GW; ++ww) s += red[r][(ww * 16 + t / 16) * 17 + t % 16];
+    }
+    v[r] = s;
+  }
+}
+
+constexpr int PRB_QKV = 4, PRB_O = 4, PRB_GU = 2, PRB_DN = 4;  // row blocks per prefill workgroup
+template <class S>
+constexpr bool prefill_tiles_fit() {
+  return (S::QKV / 16) % PRB_QKV == 0 && (S::H / 16) % PRB_O == 0 && (S::F / 16) % PRB_GU == 0 &&
+         (S::H / 16) % PRB_DN == 0 && S::KT_F % KS_DN == 0;
+}
+
+template <class S>
+__global__ __launch_bounds__(GT) void bk_pqkv(PGroup pg, int layer) {
+  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
+  constexpr int RB = PRB_QKV, NT = S::KT_H;
+  __shared__ float red[RB][GW * 16 * 17];
+  __shared__ float rr[RR_N];
+  const BParams p = group_of(pg);
+  const int rb0 = blockIdx.x * RB;
+  ATiles<NT> a[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) load_tiles(a[r], p.wqkv + layer * p.u_qkv + (long long)(rb0 + r) * S::KT_H * 64, 0);
+  BCols<NT> c;
+  load_cols(c, xg_plane<S>(p, 0, 0, 0), xg_plane<S>(p, 0, 0, 1), S::H, 0);
+  rnorm<S>(p, 0, 0, rr);
+  f32x4 acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = tiles_mma(a[r], c);
+  float v[RB];
+  block_reduce_n<RB>(acc, red, v);
+  const int t = ltid(), b = t % 16;
+  if (t < 256 && b < p.B) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      qkv_slot<S>(p, 0)[(long long)b * S::QKV + (rb0 + r) * 16 + t / 16] = v[r] * rr[b];
+  }
+}
+
+template <class S>
+__global__ __launch_bounds__(GT) void bk_po(PGroup pg, int layer) {
+  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
+  constexpr int RB = PRB_O, NT = S::KT_Q;
+  __shared__ float red[RB][GW * 16 * 17];
+  const BParams p = group_of(pg);
+  const int rb0 = blockIdx.x * RB;
+  ATiles<NT> a[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) load_tiles(a[r], p.wo + layer * p.u_o + (long long)(rb0 + r) * S::KT_Q * 64, 0);
+  const uint16_t* at = att_slot<S>(p, 0);
+  BCols<NT> c;
+  load_cols(c, at, at + BMAX * S::QD, S::QD, 0);
+  const int t = ltid(), b = t % 16;
+  float xin[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+    xin[r] = t < 256 && b < p.B ? x_slot<S>(p, 0, 0)[(long long)b * S::H + (rb0 + r) * 16 + t / 16] : 0.f;
+  f32x4 acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = tiles_mma(a[r], c);
+  float v[RB];
+  block_reduce_n<RB>(acc, red, v);
+  __syncthreads();  // red is reused
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const float xn = t < 256 && b < p.B ? xin[r] + v[r] : 0.f;
+    publish_x<S, false>(p, 0, 1, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, rb0 + r, xn, red[r]);
+  }
+}
+
+template <class S>
+__global__ __launch_bounds__(GT) void bk_pgu(PGroup pg, int layer) {
+  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
+  constexpr int RB = PRB_GU, NT = S::KT_H;
+  __shared__ float red[2 * RB][GW * 16 * 17];
+  __shared__ float rr[RR_N];
+  const BParams p = group_of(pg);
+  const int rb0 = blockIdx.x * RB;
+  ATiles<NT> ag[RB], au[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const long long off = (long long)(rb0 + r) * S::KT_H * 64;
+    load_tiles(ag[r], p.wg + layer * p.u_gu + off, 0);
+    load_tiles(au[r], p.wu + layer * p.u_gu + off, 0);
+  }
+  BCols<NT> c;
+  load_cols(c, xg_plane<S>(p, 0, 1, 0), xg_plane<S>(p, 0, 1, 1), S::H, 0);
+  rnorm<S>(p, 0, 1, rr);
+  f32x4 acc[2 * RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) tiles_mma2(ag[r], au[r], c, acc[2 * r], acc[2 * r + 1]);
+  float v[2 * RB];
+  block_reduce_n<2 * RB>(acc, red, v);
+  const int t = ltid(), b = t % 16;
+  if (t < 256 && b < p.B) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int row = (rb0 + r) * 16 + t / 16;
+      const float g = v[2 * r] * rr[b], u = v[2 * r + 1] * rr[b];
+      uint16_t h, o;
+      split2(g / (1.0f + __expf(-g)) * u, h, o);  // SiLU(g) * u (reference utils.cuh:59-61)
+      act_slot<S>(p, 0)[(long long)b * S::F + row] = h;
+      act_slot<S>(p, 0)[(long long)(BMAX + b) * S::F + row] = o;
+    }
+  }
+}
+
+// K splits as the decode's down projection: workgroup (tile, ks) of RB
+// blocks; the last split of a tile adds the KS_DN partials of its RB blocks
+// in split order.
+template <class S>
+__global__ __launch_bounds__(GT) void bk_pdown(PGroup pg, int layer) {
+  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
+  constexpr int RB = PRB_DN, NT = S::KT_F / KS_DN;
+  __shared__ float red[RB][GW * 16 * 17];
+  __shared__ int last;
+  const BParams p = group_of(pg);
+  const int tile = blockIdx.x / KS_DN, ks = blockIdx.x % KS_DN, rb0 = tile * RB, kt0 = ks * NT;
+  ATiles<NT> a[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) load_tiles(a[r], p.wd + layer * p.u_dn + (long long)(rb0 + r) * S::KT_F * 64, kt0);
+  const uint16_t* ac = act_slot<S>(p, 0);
+  BCols<NT> c;
+  load_cols(c, ac, ac + BMAX * S::F, S::F, kt0);
+  const int t = ltid(), b = t % 16;
+  float xin[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+    xin[r] = t < 256 && b < p.B ? x_slot<S>(p, 0, 1)[(long long)b * S::H + (rb0 + r) * 16 + t / 16] : 0.f;
+  f32x4 acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = tiles_mma(a[r], c);
+  float v[RB];
+  block_reduce_n<RB>(acc, red, v);
+  if (!splitk_finish(p, tile, ks, KS_DN, v, &last)) return;
+  __syncthreads();  // red is reused
+  const uint16_t* gain = layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE + S::NORM_ATTN
+                                         : p.final_norm;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const float xn = t < 256 && b < p.B ? xin[r] + v[r] : 0.f;
+    publish_x<S, false>(p, 0, 0, gain, rb0 + r, xn, red[r]);
+  }
+}
+
 // Final rmsnorm -> tied LM head -> per-sequence argmax (reference
 // sampling.cuh:32-117).  Each wave scores whole 16-row blocks; keys are
 // ordered(logit) << 32 | (0xffffffff - index), combined with an atomic max, so
