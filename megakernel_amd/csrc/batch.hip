@@ -138,8 +138,7 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
     } else {
       hipLaunchKernelGGL((bk_append<S, false, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL((bk_attn<S, false, PGroup>), dim3(BMAX * S::NKV * p.nsplit_max, ng), dim3(AT), 0, h->stream,
-                         g, l);
+      hipLaunchKernelGGL(bk_pattn<S>, dim3(S::NKV, ng), dim3(AT), 0, h->stream, g, l);
     }
     hipLaunchKernelGGL(bk_po<S>, dim3(S::H / 16 / PRB_O, ng), dim3(GT), 0, h->stream, g, l);
     hipLaunchKernelGGL(bk_pgu<S>, dim3(S::F / 16 / PRB_GU, ng), dim3(GT), 0, h->stream, g, l);

@@ -1430,6 +1430,187 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
   attn_item<S, K8, false>(p, layer, 0, sm, true, b, g, s, nsplit, pos, kv, NoWait{});
 }
 
+// ------------------------------------------------------------ prefill attention
+// One workgroup per (column group, kv head) of a prefill pass: the group's 16
+// consecutive tokens x 2 q heads = 32 queries against the causal prefix
+// [0, last position of the group], every 32-position K / V block loaded once
+// for all 32 queries (bk_attn loads it once per token).  Wave w takes blocks
+// w, w + 4, ... with an online softmax per query; the four waves' states are
+// combined at the end, so there are no split partials and no merge.  The
+// products are bk_attn's: scores^T = K . Qb with q in three bf16 parts (rows
+// 4 j + 0..2 of a 16-row tile hold query j of the tile), out^T = V^T . Pb
+// with the softmax weights split the same way; eight tiles hold the 32
+// queries (query 2 c + h = token c, q head 2 g + h).
+constexpr int PA_NQ = 2 * BMAX;      // queries of a (group, kv head)
+constexpr int PA_RT = PA_NQ / 4;     // 16-row tiles of their q parts
+template <class S>
+struct PAttnLds {
+  __attribute__((aligned(16))) uint16_t qb[PA_RT][16][S::D];  // q parts (A operand of the scores)
+  union {
+    __attribute__((aligned(16))) uint16_t pb[AW][PA_RT][16][32];  // weight parts (A operand of the output)
+    float ow[AW][PA_NQ][S::D];                                     // the waves' outputs, after the loop
+  };
+  float mw[AW][PA_NQ], lw[AW][PA_NQ];
+};
+
+template <class S>
+__global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
+  static_assert(S::GQA == 2 && S::D == 64 && AT == 4 * kWave, "2 q heads of 64 per kv head, 4 waves");
+  constexpr int D = S::D, NKV = S::NKV, RT = PA_RT;
+  __shared__ PAttnLds<S> sm;
+  // the longest prefixes (the last groups) first: the pass's makespan is
+  // theirs, the short ones fill in behind them
+  const BParams p = group_params(pg, pg.n - 1 - (int)blockIdx.y);
+  const int g = blockIdx.x;
+  const int tid = ltid(), w = tid / kWave, l = tid % kWave;
+  const int c16 = l & 15, rg = l >> 4;
+  const int p0 = p.pos[0], pmax = p0 + p.B - 1;  // the group's tokens are positions p0 .. pmax
+  // 1. q of the 32 queries (wave w: queries 8 w .. 8 w + 7; lane = dimension):
+  //    QK-norm (reference rmsnorm.cuh:57-84) and RoPE rotate-half
+  //    (attention.cuh:22-44), as bk_attn's prologue
+  {
+    const uint16_t* gn = p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_Q;
+    const float gain = bf16_to_f32(gn[l]);
+    const int d = l & 31;
+#pragma unroll 2
+    for (int k = 0; k < 8; ++k) {
+      const int qi = 8 * w + k, col = qi >> 1, j = qi & 1;
+      const bool on = col < p.B;
+      float v = on ? qkv_slot<S>(p, 0)[(long long)col * S::QKV + (g * 2 + j) * D + l] : 0.f;
+      const float ss = wave_sum(v * v);
+      v = on ? v * rsqrtf(ss / (float)D + kRmsEps) * gain : 0.f;
+      const float partner = lane_xor32(v);
+      const float cs = on ? p.rope[(col * 2 + 0) * (D / 2) + d] : 0.f;
+      const float sn = on ? p.rope[(col * 2 + 1) * (D / 2) + d] : 0.f;
+      v = l < 32 ? v * cs - partner * sn : v * cs + partner * sn;
+      uint16_t h, m, o;
+      split_bf16(v, h, m, o);
+      const int rt = qi >> 2, r0 = 4 * (qi & 3);
+      sm.qb[rt][r0 + 0][l] = h;
+      sm.qb[rt][r0 + 1][l] = m;
+      sm.qb[rt][r0 + 2][l] = o;
+      sm.qb[rt][r0 + 3][l] = 0;
+    }
+  }
+  __syncthreads();
+  // 2. the wave's blocks: online softmax per query on the matrix cores; lane
+  //    (rg, c16) holds query 4 rt + rg of tile rt (token 2 rt + rg / 2)
+  const float scale = 1.0f / sqrtf((float)D);
+  const long long kbase = ((long long)layer * NKV + g) * (long long)p.s_pad * D;
+  const auto rk = make_rsrc(p.kv + kbase);
+  const auto rv = make_rsrc(p.kvt + kbase);
+  const unsigned lu = (unsigned)l;
+  float m[RT], lsum[RT];
+  int qpos[RT];
+  f32x4 acc[RT][D / 16];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m[rt] = -INFINITY, lsum[rt] = 0.f;
+    const int col = 2 * rt + (rg >> 1);
+    qpos[rt] = col < p.B ? p0 + col : -1;  // -1: no token (every score masked)
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int nblk = pmax / 32 + 1;
+  for (int kb = w; kb < nblk; kb += AW) {
+    const int t0 = 32 * kb;
+    u32x4 kr[2][2], vr[D / 16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+        kr[h][kc] = __builtin_amdgcn_raw_buffer_load_b128(
+            rk, ((unsigned)(t0 + 16 * h) * D + (lu & 15u) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      vr[dt] = __builtin_amdgcn_raw_buffer_load_b128(
+          rv, ((unsigned)t0 * D + (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      float sc[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+          d4 = mfma(*reinterpret_cast<const u32x4*>(&sm.qb[rt][c16][32 * kc + 8 * rg]), kr[h][kc], d4);
+        const int t = t0 + 16 * h + c16;
+        sc[h] = t <= qpos[rt] ? ((d4[0] + d4[1]) + d4[2]) * scale : -INFINITY;
+      }
+      const float mn = fmaxf(m[rt], group_max<16>(fmaxf(sc[0], sc[1])));
+      // a query none of whose positions so far is visible keeps m = -inf,
+      // weight 0 and scale 1 (no -inf - -inf)
+      const float alpha = mn == -INFINITY ? 1.f : __expf(m[rt] - mn);
+      m[rt] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        sc[h] = mn == -INFINITY ? 0.f : __expf(sc[h] - mn);
+        ps += sc[h];
+      }
+      lsum[rt] = lsum[rt] * alpha + group_sum<16>(ps);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const Split3 a = split3(sc[h]);
+        sm.pb[w][rt][4 * rg + 0][16 * h + c16] = (uint16_t)(a.hi >> 16);
+        sm.pb[w][rt][4 * rg + 1][16 * h + c16] = (uint16_t)(a.mid >> 16);
+        sm.pb[w][rt][4 * rg + 2][16 * h + c16] = (uint16_t)(a.lo >> 16);
+        sm.pb[w][rt][4 * rg + 3][16 * h + c16] = 0;
+      }
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rt][dt][i] *= alpha;
+    }
+    asm volatile("" ::: "memory");  // LDS operations of one wave complete in order
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const u32x4 pa = *reinterpret_cast<const u32x4*>(&sm.pb[w][rt][c16][8 * rg]);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) acc[rt][dt] = mfma(pa, vr[dt], acc[rt][dt]);
+    }
+    asm volatile("" ::: "memory");  // the next block's weight parts are written after these reads
+  }
+  // 3. combine the waves (ow aliases pb: every wave's last reads of pb are
+  //    done at the barrier) and write the merged output as bf16 hi / lo parts
+  __syncthreads();
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int q = 4 * rt + rg;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      sm.ow[w][q][16 * dt + c16] = (acc[rt][dt][0] + acc[rt][dt][1]) + acc[rt][dt][2];
+    if (c16 == 0) {
+      sm.mw[w][q] = m[rt];
+      sm.lw[w][q] = lsum[rt];
+    }
+  }
+  __syncthreads();
+  {
+    const int d = tid % D;
+#pragma unroll
+    for (int k = 0; k < PA_NQ / (AT / D); ++k) {
+      const int q = tid / D + (AT / D) * k, col = q >> 1, j = q & 1;
+      if (col >= p.B) continue;
+      float M = sm.mw[0][q];
+#pragma unroll
+      for (int i = 1; i < AW; ++i) M = fmaxf(M, sm.mw[i][q]);
+      float o = 0.f, L = 0.f;
+#pragma unroll
+      for (int i = 0; i < AW; ++i) {
+        const float f = sm.mw[i][q] == -INFINITY ? 0.f : __expf(sm.mw[i][q] - M);
+        o = fmaf(f, sm.ow[i][q][d], o);
+        L = fmaf(f, sm.lw[i][q], L);
+      }
+      uint16_t hi, lo;
+      split2(o / L, hi, lo);
+      const long long k0 = (long long)col * S::QD + (g * 2 + j) * D + d;
+      att_slot<S>(p, 0)[k0] = hi;
+      att_slot<S>(p, 0)[(long long)BMAX * S::QD + k0] = lo;
+    }
+  }
+}
+
 // ------------------------------------------------------------ one-kernel step
 // Workgroups of bk_step per CU (waves per SIMD = 2 x that): two, so twice the
 // attention items run at once (<= 128 registers per lane).
