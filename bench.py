@@ -444,8 +444,13 @@ def bench_prefill(args):
     (64 groups of 16 matrix columns), each one sweep over the layer weights,
     the LM head once for the next token.  Timed: --reps calls after one warm-up (the
     position reset to 0 before each), median; inputs resident in HBM.
-    Algorithmic bytes: layer weights once per pass, the KV read of every
-    token's causal prefix and its append, the LM head once.  Beside it: the
+    Roofline: with up to 1,024 tokens per weight pass the work is far above
+    the bf16 ridge point (~310 flop per HBM byte), so the bound is the matrix
+    cores: algorithmic flops = 2 x the layer weights' multiply-adds per token
+    + causal attention (QK and PV over each token's prefix) + the LM head once
+    (the kernels' hi / lo activation parts execute about twice these matrix
+    flops).  Also reported: the HBM bytes of one sweep per pass (layer
+    weights, the K / V prefix once, the LM head once).  Beside it: the
     same prompt fed token by token through the batch-1 decode kernel (the
     reference's prefill-by-decode, host/bridge.py:136-163)."""
     import numpy as np
@@ -453,7 +458,7 @@ def bench_prefill(args):
     from megakernel_amd import _lib, launcher
     from megakernel_amd.batch import PREFILL_PASS_TOKENS, BatchEngine
     from megakernel_amd.bridge import MegakernelEngine
-    from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS
+    from megakernel_amd.config import BASELINE, HBM_PEAK_GBPS, MFMA_BF16_PEAK_TFLOPS
     from megakernel_amd.weights import DeviceWeights
 
     shape, N = BASELINE, args.prefill
@@ -487,9 +492,12 @@ def bench_prefill(args):
     dw.free()
     wall, kern = statistics.median(walls), statistics.median(kernels)
     npasses = (N + PREFILL_PASS_TOKENS - 1) // PREFILL_PASS_TOKENS
-    nbytes = (npasses * shape.n_layers * shape.layer_weight_bytes + 2 * shape.vocab * shape.hidden +
-              2 * shape.hidden + sum(shape.kv_bytes_per_pos * (p + 2) for p in range(N)))
-    achieved = nbytes / kern / 1e9
+    head = 2 * shape.vocab * shape.hidden  # LM-head flops of one token
+    flops = sum(shape.token_flops(p) - head for p in range(N)) + head
+    achieved = flops / kern / 1e12
+    pass_end = [min(N, (k + 1) * PREFILL_PASS_TOKENS) for k in range(npasses)]
+    hbm_bytes = (npasses * shape.n_layers * shape.layer_weight_bytes + 2 * shape.vocab * shape.hidden +
+                 sum(shape.kv_bytes_per_pos * e for e in pass_end))
     out = {
         "metric": f"prefill tok/s ({N}-token prompt, empty cache)",
         "value": round(N / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": N, "warmup": 1,
@@ -500,8 +508,10 @@ def bench_prefill(args):
                    "device": info["name"], "reps": args.reps},
         "prefill_by_decode_tok_s": round(by_decode, 1),
         "next_token": toks[-1],
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+        "hbm_sweep": {"bytes": hbm_bytes, "achieved_gbps": round(hbm_bytes / kern / 1e9, 1),
+                      "frac": round(hbm_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)},
     }
     print(json.dumps(out))
 

@@ -14,6 +14,7 @@ LAYER_KEYS = ("attn_norm", "w_q", "w_k", "w_v", "q_norm", "k_norm",
               "w_o", "ffn_norm", "w_gate", "w_up", "w_down")
 
 HBM_PEAK_GBPS = 8000.0  # MI355X published HBM3E peak
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X published dense bf16 matrix peak
 
 
 @dataclass(frozen=True)

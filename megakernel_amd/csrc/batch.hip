@@ -126,10 +126,11 @@ static int launch_step(BHandle* h, const BParams& p) {
 template <class S>
 static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool last) {
   const int L = h->L, ng = g.n;
+  const auto rows = [ng](int cg) { return (ng + cg - 1) / cg; };  // GEMM workgroup rows: cg groups each
   const BParams& p = g.p;
   hipLaunchKernelGGL((bk_embed<S, PGroup>), dim3(BMAX, ng), dim3(256), 0, h->stream, g);
   for (int l = 0; l < L; ++l) {
-    hipLaunchKernelGGL(bk_pqkv<S>, dim3(S::QKV / 16 / PRB_QKV, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_pqkv<S>, dim3(S::QKV / 16 / PRB_QKV, rows(PCG_QKV)), dim3(GT), 0, h->stream, g, l);
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
@@ -140,9 +141,9 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
                          l);
       hipLaunchKernelGGL(bk_pattn<S>, dim3(S::NKV, ng), dim3(AT), 0, h->stream, g, l);
     }
-    hipLaunchKernelGGL(bk_po<S>, dim3(S::H / 16 / PRB_O, ng), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL(bk_pgu<S>, dim3(S::F / 16 / PRB_GU, ng), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL(bk_pdown<S>, dim3(S::H / 16 / PRB_DN * KS_DN, ng), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_po<S>, dim3(S::H / 16 / PRB_O, rows(PCG_O)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_pgu<S>, dim3(S::F / 16 / PRB_GU, rows(PCG_GU)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_pdown<S>, dim3(S::H / 16 / PRB_DN * KS_DN, rows(PCG_DN)), dim3(GT), 0, h->stream, g, l);
   }
   if (last) {
     if (pl.lmhead8)
