@@ -262,8 +262,15 @@ static ShapeInfo shape_info() {
                    S::NORM_STRIDE, S::NORM_ATTN, S::NORM_Q, S::NORM_K, S::NORM_FFN, part_words<S>()};
 }
 
-// Attention splits per kv head up to which the class kernel has role tables.
-constexpr int kMaxClsSplit = 4;
+// Attention splits per kv head up to which the class kernel has role tables
+// (eight splits of eight kv heads: the attention workgroups and the other
+// roles of a BASELINE layer just fit 256 workgroups).
+constexpr int kMaxClsSplit = 8;
+// Largest attention chunk a launch takes to stay in the class kernel (see
+// launch_chunk; measured at ctx 4,096: eight splits of 544 positions in the
+// class kernel 2,451 tok/s, nine of 512 in the spread kernel 2,261; at 8,192
+// eight of 1,088 lose, 1,957 vs 2,104).
+constexpr int kClsChunkMax = 640;
 
 // Role table of the class kernel (mk_cls.h) for `nsplit` attention splits
 // per kv head on G workgroups: attention items (each with an O block) on
@@ -351,6 +358,7 @@ struct Handle {
   int L = 0, V = 0, S = 0;
   int max_launch_tokens = 0;
   int nsplit_max = 1, chunk_min = 256 * KVB;  // one 32-position block per wave and register set
+  int chunk_eff = 0;                           // the attention chunk of the last launch (launch_chunk)
   int merge_min = 20;  // above this many splits per kv head the first split's workgroup merges them
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -609,6 +617,21 @@ static int clear_pair_words(Handle* h) {
   return 0;
 }
 
+// The attention chunk of a launch whose last token sits at position end - 1:
+// the handle's, or, when that needs more splits per kv head than the class
+// kernel's role tables hold while a chunk of at most kClsChunkMax positions
+// would not, the smallest multiple of 32 positions that gives kMaxClsSplit
+// splits (a few longer splits in the class kernel beat more splits in the
+// spread kernel).
+static int launch_chunk(const Handle* h, int end) {
+  const int c = h->chunk_min;
+  if (!h->has_cls || h->kernel_variant != MK_KERNEL_AUTO || !h->roles_ok[kMaxClsSplit] ||
+      split_count(end, c, h->nsplit_max) <= kMaxClsSplit)
+    return c;
+  const int c8 = ((end + kMaxClsSplit - 1) / kMaxClsSplit + 31) / 32 * 32;
+  return c8 > c && c8 <= kClsChunkMax ? c8 : c;
+}
+
 // One resident launch decoding n tokens starting at h->pos.
 static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int trace_token = -1) {
   if (n <= 0 || n > h->max_launch_tokens) {
@@ -665,13 +688,20 @@ static int run(Handle* h, int first_token, int n, int* out_host, bool debug, int
   p.n_tokens = n;
   p.first_token = first_token;
   p.nsplit_max = h->nsplit_max;
-  p.chunk_min = h->chunk_min;
+  // a new split layout starts from cleared pair words (their 4-bit tags are
+  // only unambiguous while a layout's split counts grow)
+  const int chunk = launch_chunk(h, h->pos + n);
+  if (chunk != h->chunk_eff) {
+    if (clear_pair_words(h)) return -1;
+    h->chunk_eff = chunk;
+  }
+  p.chunk_min = chunk;
   p.merge_min = h->merge_min;
   p.pace_pct = h->pace_pct;
   HIPCHK(hipEventRecord(h->ev0, h->stream), -1);
   // the long-context instantiation when the launch's last token has more
   // than merge_min splits per kv head (split counts grow with the position)
-  const int ns_last = split_count(h->pos + n, h->chunk_min, h->nsplit_max);
+  const int ns_last = split_count(h->pos + n, chunk, h->nsplit_max);
   const bool lc = ns_last > h->merge_min;
   // the class kernel when a role table holds every attention item of the
   // launch (its attention workgroups serve the last token's split count)
@@ -1147,7 +1177,7 @@ int megakernel_decode_kernel_for(void* handle, int n_tokens) {
     mk::set_err("null handle or token count < 1");
     return -1;
   }
-  const int ns = mk::split_count(h->pos + n_tokens, h->chunk_min, h->nsplit_max);
+  const int ns = mk::split_count(h->pos + n_tokens, mk::launch_chunk(h, h->pos + n_tokens), h->nsplit_max);
   const bool cls = h->has_cls && h->kernel_variant == MK_KERNEL_AUTO && ns <= h->merge_min &&
                    ns <= mk::kMaxClsSplit && h->roles_ok[ns];
   return cls ? MK_KERNEL_CLASS : MK_KERNEL_SPREAD;

@@ -225,9 +225,9 @@ def test_configs3_full_model_long_context(ctx):
         dw.free()
 
 
-@pytest.mark.parametrize("ctx", [0, 100, 600, 1024, 1500])
+@pytest.mark.parametrize("ctx", [0, 100, 600, 1024, 1500, 3000, 4000])
 def test_class_kernel_equals_spread_kernel(ctx):
-    """The class-specialised kernel (MK_KERNEL_AUTO at up to 4 splits per kv
+    """The class-specialised kernel (MK_KERNEL_AUTO at up to 8 splits per kv
     head) and the spread kernel run the same arithmetic: per-layer residuals,
     logits and tokens of the same steps are bitwise identical; and the class
     kernel is the one AUTO picks for these launches."""

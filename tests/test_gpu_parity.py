@@ -187,6 +187,42 @@ def test_long_context_split_attention(ctx, chunk, merge):
         dw.free()
 
 
+def test_long_context_class_kernel_chunk():
+    """Past eight 512-position splits per kv head the launch widens its
+    attention chunk (at most 640 positions) so that eight splits hold the
+    context and the class kernel runs: ctx 4,200 takes chunks of 544, then
+    launches ending past 4,352 positions take 576 (a new split layout, the
+    packed-pair words cleared between them).  Debug steps at the bars, then
+    three 60-token launches teacher-forced against the oracle."""
+    shape = BASELINE.with_(n_layers=2, vocab=2048)
+    ctx = 4200
+    eng, orc, dw = make_pair(shape, 23, ctx + 256)
+    try:
+        eng.fill_kv_synthetic(ctx, 78)
+        ks = np.stack([synth.kv_prefill_bits(78, l, 0, ctx, shape.n_kv_heads, shape.head_dim)
+                       for l in range(shape.n_layers)])
+        vs = np.stack([synth.kv_prefill_bits(78, l, 1, ctx, shape.n_kv_heads, shape.head_dim)
+                       for l in range(shape.n_layers)])
+        orc.set_kv(ks, vs)
+        assert eng.decode_kernel_for(1) == _lib.KERNEL_CLASS
+        tok = 3
+        for i in range(2):
+            _print(f"ctx {ctx} step {i}")
+            nxt, layers, logits = eng.debug_forward(tok)
+            ref = orc.step(tok, capture=True)
+            check_step(layers, logits, ref, f"ctx {ctx} step {i}")
+            tok = ref["token"]
+        for j in range(3):
+            assert eng.decode_kernel_for(60) == _lib.KERNEL_CLASS
+            gen = eng.decode_many(tok, 60)
+            same, low = check_tokens_teacher_forced([tok] + gen[:-1], gen, orc)
+            _print(f"  launch {j} at {eng.pos - 60}: {same} identical, {low} low-margin")
+            tok = gen[-1]
+    finally:
+        eng.close()
+        dw.free()
+
+
 def test_reconfigure_and_rewind_between_launches():
     """The packed-pair hand-off words are not cleared before each launch, only
     when the position moves back or the split / merge configuration changes.
