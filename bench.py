@@ -640,7 +640,9 @@ def main():
                                                                      ("KV cache", args.kv_fp8)) if on),
         "data": "synthetic",
         "config": {"workload": f"Qwen3-0.6B-shaped batch-1 greedy decode, KV prefilled to {args.ctx}, "
-                               f"{K} tokens in one resident launch (BASELINE configs[2])",
+                               f"{K} tokens in one resident launch" +
+                               {1024: " (BASELINE configs[2])", 8192: " (BASELINE configs[3])",
+                                32768: " (BASELINE configs[3])"}.get(args.ctx, ""),
                    "ctx": args.ctx, "tokens": K, "batch": 1, "layers": shape.n_layers,
                    "hidden": shape.hidden, "heads": "16q/8kv x 64", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "bf16 N(0,0.02) (Irwin-Hall(4) approx), unit norm gains" +
