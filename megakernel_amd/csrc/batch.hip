@@ -130,7 +130,7 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
   const BParams& p = g.p;
   hipLaunchKernelGGL((bk_embed<S, PGroup>), dim3(BMAX, ng), dim3(256), 0, h->stream, g);
   for (int l = 0; l < L; ++l) {
-    hipLaunchKernelGGL(bk_pqkv<S>, dim3(S::QKV / 16 / PRB_QKV, rows(PCG_QKV)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_ptile<S, PT_QKV>), dim3(S::QKV / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
@@ -141,9 +141,9 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
                          l);
       hipLaunchKernelGGL(bk_pattn<S>, dim3(S::NKV, ng), dim3(AT), 0, h->stream, g, l);
     }
-    hipLaunchKernelGGL(bk_po<S>, dim3(S::H / 16 / PRB_O, rows(PCG_O)), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL(bk_pgu<S>, dim3(S::F / 16 / PRB_GU, rows(PCG_GU)), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL(bk_pdown<S>, dim3(S::H / 16 / PRB_DN * KS_DN, rows(PCG_DN)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_ptile<S, PT_O>), dim3(S::H / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL(bk_pgu_t<S>, dim3(S::F / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_ptile<S, PT_DN>), dim3(S::H / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
   }
   if (last) {
     if (pl.lmhead8)
@@ -155,9 +155,11 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
   HIPCHK(hipGetLastError(), -1);
   return 0;
 }
-static_assert((ShapeBaseline::QKV / 16 / PRB_QKV) % 8 == 0 && (ShapeBaseline::H / 16 / PRB_O) % 8 == 0 &&
-                  (ShapeBaseline::F / 16 / PRB_GU) % 8 == 0 && (ShapeBaseline::H / 16 / PRB_DN * KS_DN) % 8 == 0,
-              "prefill GEMM grids of whole XCD rounds: a tile's column groups share an XCD");
+// QKV, O and down grids of whole XCD rounds: a row tile's column-group
+// workgroups share an XCD and its L2 (gate / up has 44 row tiles: its tiles'
+// groups spread over XCDs)
+static_assert((ShapeBaseline::QKV / 16 / PT_MP) % 8 == 0 && (ShapeBaseline::H / 16 / PT_MP) % 8 == 0,
+              "prefill GEMM grids of whole XCD rounds");
 
 template <class S>
 static bool persistent_fits() {

@@ -691,229 +691,236 @@ __global__ __launch_bounds__(GT) void bk_down(G p, int layer) {
 }
 
 // ------------------------------------------------------------ prefill GEMMs
-// A prefill pass has up to 64 column groups, so each GEMM launch has 64 x the
-// decode step's workgroups and the kernels become bound by what every
-// workgroup re-reads: a 16-row block's workgroup loads its group's whole
-// activation columns (64 KB for K = 1,024).  The prefill kernels give a
-// workgroup RB consecutive 16-row blocks of one group: the columns, the norm
-// factors and the load latency are shared by RB blocks.  Per block the
-// arithmetic is the decode kernels' (same tiles, same products, same
-// cross-wave order).
+// A prefill pass has up to 64 column groups (1,024 tokens), so the GEMMs are
+// real matrix products: the decode kernels' one-block workgroups would each
+// re-read their group's activation columns (64 KB for K = 1,024) next to
+// 32 KB of weights, bounded by L2 -> CU traffic.  The prefill kernels tile
+// rows and column groups and stage both operands in LDS.  Per 16 x 16 tile
+// the products are the decode kernels' MFMA tiles (weights as the A operand,
+// the columns' bf16 hi / lo parts as two B operands), accumulated over the
+// whole K by one wave, so no cross-wave reduction is needed.
 
-// RB cross-wave reductions with one barrier: v[r] = block_reduce(acc[r]).
-template <int RB>
-__device__ __forceinline__ void block_reduce_n(const f32x4 (&acc)[RB], float (*red)[GW * 16 * 17], float (&v)[RB]) {
+// Gate / up as an LDS-tiled GEMM: a workgroup computes PT_MP block pairs
+// (16 gate + 16 up rows each) for PT_NG column groups, K in chunks of PT_KC
+// tiles; each chunk's weight tiles and column tiles are staged in LDS once
+// (double-buffered, the next chunk's loads in flight during the current
+// chunk's products), so a weight byte is read from L2 once per PT_NG groups
+// and a column byte once per PT_MP block pairs.  Wave w owns block pair w / 2
+// for groups 2 (w % 2) and 2 (w % 2) + 1 over the whole K; the epilogue runs
+// on its accumulators.
+constexpr int PT_MP = 4, PT_NG = 4, PT_KC = 4;
+template <class S>
+__global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
+  constexpr int NT = S::KT_H, NC = NT / PT_KC;
+  constexpr int AU = 2 * PT_MP * PT_KC * kWave;  // u32x4 of a chunk's weight tiles
+  constexpr int BU = PT_NG * 2 * PT_KC * kWave;  // ... of its column tiles
+  constexpr int LA = AU / GT, LB = BU / GT;      // per thread
+  static_assert(NT % PT_KC == 0 && AU % GT == 0 && BU % GT == 0 && GW == 2 * PT_MP && PT_NG == 4,
+                "tile shape");
+  __shared__ u32x4 sa[2][2 * PT_MP][PT_KC][kWave];   // [buf][gate pairs | up pairs][tile][lane]
+  __shared__ u32x4 sb[2][PT_NG][2][PT_KC][kWave];    // [buf][group][hi / lo][tile][lane]
+  const int rb0 = blockIdx.x * PT_MP, g0 = blockIdx.y * PT_NG, tid = ltid();
+  const int ngr = pg.n - g0 < PT_NG ? pg.n - g0 : PT_NG;  // groups of this tile
+  const BParams p0 = group_params(pg, g0);
+  const u32x4* wgt[2] = {p0.wg + layer * p0.u_gu, p0.wu + layer * p0.u_gu};
+  u32x4 ra[LA], rbv[LB];
+  const auto load = [&](int c) {
+#pragma unroll
+    for (int k = 0; k < LA; ++k) {
+      const int i = tid + GT * k, blk = i / (PT_KC * kWave), kt = (i / kWave) % PT_KC, ln = i % kWave;
+      ra[k] = __builtin_nontemporal_load(wgt[blk / PT_MP] + ((long long)(rb0 + blk % PT_MP) * NT + c * PT_KC + kt) * 64 +
+                                         ln);
+    }
+#pragma unroll
+    for (int k = 0; k < LB; ++k) {
+      const int i = tid + GT * k, gq = i / (2 * PT_KC * kWave), pl = (i / (PT_KC * kWave)) % 2;
+      const int kt = (i / kWave) % PT_KC, ln = i % kWave;
+      rbv[k] = u32x4{0u, 0u, 0u, 0u};
+      if (gq < ngr) {
+        const BParams q = group_params(pg, g0 + gq);
+        rbv[k] = *reinterpret_cast<const u32x4*>(xg_plane<S>(q, 0, 1, pl) + (ln & 15) * S::H +
+                                                 32 * (c * PT_KC + kt) + 8 * (ln >> 4));
+      }
+    }
+  };
+  const auto store = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < LA; ++k) (&sa[buf][0][0][0])[tid + GT * k] = ra[k];
+#pragma unroll
+    for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = rbv[k];
+  };
+  load(0);
+  store(0);
+  __syncthreads();
+  const int w = wave_id(), pw = w / 2, gb = 2 * (w % 2);
   const unsigned l = lane_id();
-  const int w = wave_id();
+  f32x4 acc[2][2][2];  // [group][gate / up][hi / lo part]
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int m = 0; m < 2; ++m) acc[j][m][0] = acc[j][m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < NC; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < NC) load(c + 1);
+#pragma unroll
+    for (int kt = 0; kt < PT_KC; ++kt) {
+      const u32x4 ag = sa[buf][pw][kt][l], au = sa[buf][PT_MP + pw][kt][l];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const u32x4 bh = sb[buf][gb + j][0][kt][l], bl = sb[buf][gb + j][1][kt][l];
+        acc[j][0][0] = mfma(ag, bh, acc[j][0][0]);
+        acc[j][0][1] = mfma(ag, bl, acc[j][0][1]);
+        acc[j][1][0] = mfma(au, bh, acc[j][1][0]);
+        acc[j][1][1] = mfma(au, bl, acc[j][1][1]);
+      }
+    }
+    if (c + 1 < NC) store(buf ^ 1);
+    __syncthreads();
+  }
+  // epilogue: lane (kg, n) holds rows 4 kg .. 4 kg + 3 of column n
   const int n = (int)(l & 15u), kg = (int)(l >> 4);
 #pragma unroll
-  for (int r = 0; r < RB; ++r)
+  for (int j = 0; j < 2; ++j) {
+    if (gb + j >= ngr) break;
+    const BParams p = group_params(pg, g0 + gb + j);
+    constexpr int NB = S::H / 16, PER = NB / 4;
+    const float* q = ssq_slot<S>(p, 0, 1) + n;
+    float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[r][(w * 16 + 4 * kg + i) * 17 + n] = acc[r][i];
-  __syncthreads();
-  const int t = ltid();
+    for (int i = 0; i < PER; ++i) ss += q[(kg * PER + i) * BMAX];
+    ss = sum_xor32(sum_xor16(ss));
+    const float rs = rsqrtf(ss / (float)S::H + kRmsEps);
+    if (n < p.B) {
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    float s = 0.f;
-    if (t < 256) {
-#pragma unroll
-      for (int ww = 0; ww < GW; ++ww) s += red[r][(ww * 16 + t / 16) * 17 + t % 16];
-    }
-    v[r] = s;
-  }
-}
-
-constexpr int PRB_QKV = 4, PRB_O = 4, PRB_GU = 2, PRB_DN = 4;  // row blocks per prefill workgroup
-// column groups per prefill workgroup, its weights kept in registers
-// (measured per layer at 1 / 2 / 4 groups: QKV 36.9 / 38.4 / 35.4 us, O 25.7 /
-// 26.8 / 26.7, gate/up 105.6 / 103.9 / 99.5, down 85.2 / 76.8 / 102.9)
-constexpr int PCG_QKV = 4, PCG_O = 1, PCG_GU = 4, PCG_DN = 2;
-template <class S>
-constexpr bool prefill_tiles_fit() {
-  return (S::QKV / 16) % PRB_QKV == 0 && (S::H / 16) % PRB_O == 0 && (S::F / 16) % PRB_GU == 0 &&
-         (S::H / 16) % PRB_DN == 0 && S::KT_F % KS_DN == 0;
-}
-
-// Workgroup (x, y) of a prefill GEMM: row tile x, column groups y CG ..
-// y CG + CG - 1 of the pass (CG = PCG_*), one after the other with the tile's
-// weights in registers; the next group's columns are loaded while the current
-// group is reduced.
-template <class S>
-__global__ __launch_bounds__(GT) void bk_pqkv(PGroup pg, int layer) {
-  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
-  constexpr int RB = PRB_QKV, NT = S::KT_H;
-  __shared__ float red[RB][GW * 16 * 17];
-  __shared__ float rr[RR_N];
-  const int rb0 = blockIdx.x * RB, g0 = blockIdx.y * PCG_QKV;
-  const BParams p0 = group_params(pg, g0);
-  ATiles<NT> a[RB];
-#pragma unroll
-  for (int r = 0; r < RB; ++r) load_tiles(a[r], p0.wqkv + layer * p0.u_qkv + (long long)(rb0 + r) * S::KT_H * 64, 0);
-  BCols<NT> c[2];
-  load_cols(c[0], xg_plane<S>(p0, 0, 0, 0), xg_plane<S>(p0, 0, 0, 1), S::H, 0);
-#pragma unroll
-  for (int ci = 0; ci < PCG_QKV; ++ci) {
-    if (g0 + ci >= pg.n) break;
-    const BParams p = group_params(pg, g0 + ci);
-    if (ci + 1 < PCG_QKV && g0 + ci + 1 < pg.n) {
-      const BParams pn = group_params(pg, g0 + ci + 1);
-      load_cols(c[(ci + 1) & 1], xg_plane<S>(pn, 0, 0, 0), xg_plane<S>(pn, 0, 0, 1), S::H, 0);
-    }
-    if (ci > 0) __syncthreads();  // the previous group's reads of red / rr are done
-    rnorm<S>(p, 0, 0, rr);
-    f32x4 acc[RB];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) acc[r] = tiles_mma(a[r], c[ci & 1]);
-    float v[RB];
-    block_reduce_n<RB>(acc, red, v);
-    const int t = ltid(), b = t % 16;
-    if (t < 256 && b < p.B) {
-#pragma unroll
-      for (int r = 0; r < RB; ++r)
-        qkv_slot<S>(p, 0)[(long long)b * S::QKV + (rb0 + r) * 16 + t / 16] = v[r] * rr[b];
-    }
-  }
-}
-
-template <class S>
-__global__ __launch_bounds__(GT) void bk_po(PGroup pg, int layer) {
-  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
-  constexpr int RB = PRB_O, NT = S::KT_Q;
-  __shared__ float red[RB][GW * 16 * 17];
-  const int rb0 = blockIdx.x * RB, g0 = blockIdx.y * PCG_O;
-  const BParams p0 = group_params(pg, g0);
-  ATiles<NT> a[RB];
-#pragma unroll
-  for (int r = 0; r < RB; ++r) load_tiles(a[r], p0.wo + layer * p0.u_o + (long long)(rb0 + r) * S::KT_Q * 64, 0);
-  BCols<NT> c[2];
-  {
-    const uint16_t* at = att_slot<S>(p0, 0);
-    load_cols(c[0], at, at + BMAX * S::QD, S::QD, 0);
-  }
-#pragma unroll
-  for (int ci = 0; ci < PCG_O; ++ci) {
-    if (g0 + ci >= pg.n) break;
-    const BParams p = group_params(pg, g0 + ci);
-    if (ci + 1 < PCG_O && g0 + ci + 1 < pg.n) {
-      const BParams pn = group_params(pg, g0 + ci + 1);
-      const uint16_t* at = att_slot<S>(pn, 0);
-      load_cols(c[(ci + 1) & 1], at, at + BMAX * S::QD, S::QD, 0);
-    }
-    const int t = ltid(), b = t % 16;
-    float xin[RB];
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-      xin[r] = t < 256 && b < p.B ? x_slot<S>(p, 0, 0)[(long long)b * S::H + (rb0 + r) * 16 + t / 16] : 0.f;
-    if (ci > 0) __syncthreads();  // the previous group's reads of red are done
-    f32x4 acc[RB];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) acc[r] = tiles_mma(a[r], c[ci & 1]);
-    float v[RB];
-    block_reduce_n<RB>(acc, red, v);
-    __syncthreads();  // red is reused
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const float xn = t < 256 && b < p.B ? xin[r] + v[r] : 0.f;
-      publish_x<S, false>(p, 0, 1, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN, rb0 + r, xn, red[r]);
-    }
-  }
-}
-
-template <class S>
-__global__ __launch_bounds__(GT) void bk_pgu(PGroup pg, int layer) {
-  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
-  constexpr int RB = PRB_GU, NT = S::KT_H;
-  __shared__ float red[2 * RB][GW * 16 * 17];
-  __shared__ float rr[RR_N];
-  const int rb0 = blockIdx.x * RB, g0 = blockIdx.y * PCG_GU;
-  const BParams p0 = group_params(pg, g0);
-  ATiles<NT> ag[RB], au[RB];
-#pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const long long off = (long long)(rb0 + r) * S::KT_H * 64;
-    load_tiles(ag[r], p0.wg + layer * p0.u_gu + off, 0);
-    load_tiles(au[r], p0.wu + layer * p0.u_gu + off, 0);
-  }
-  BCols<NT> c[2];
-  load_cols(c[0], xg_plane<S>(p0, 0, 1, 0), xg_plane<S>(p0, 0, 1, 1), S::H, 0);
-#pragma unroll
-  for (int ci = 0; ci < PCG_GU; ++ci) {
-    if (g0 + ci >= pg.n) break;
-    const BParams p = group_params(pg, g0 + ci);
-    if (ci + 1 < PCG_GU && g0 + ci + 1 < pg.n) {
-      const BParams pn = group_params(pg, g0 + ci + 1);
-      load_cols(c[(ci + 1) & 1], xg_plane<S>(pn, 0, 1, 0), xg_plane<S>(pn, 0, 1, 1), S::H, 0);
-    }
-    if (ci > 0) __syncthreads();  // the previous group's reads of red / rr are done
-    rnorm<S>(p, 0, 1, rr);
-    f32x4 acc[2 * RB];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) tiles_mma2(ag[r], au[r], c[ci & 1], acc[2 * r], acc[2 * r + 1]);
-    float v[2 * RB];
-    block_reduce_n<2 * RB>(acc, red, v);
-    const int t = ltid(), b = t % 16;
-    if (t < 256 && b < p.B) {
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        const int row = (rb0 + r) * 16 + t / 16;
-        const float g = v[2 * r] * rr[b], u = v[2 * r + 1] * rr[b];
+      for (int i = 0; i < 4; ++i) {
+        const int row = (rb0 + pw) * 16 + 4 * kg + i;
+        const float g = (acc[j][0][0][i] + acc[j][0][1][i]) * rs, u = (acc[j][1][0][i] + acc[j][1][1][i]) * rs;
         uint16_t h, o;
         split2(g / (1.0f + __expf(-g)) * u, h, o);  // SiLU(g) * u (reference utils.cuh:59-61)
-        act_slot<S>(p, 0)[(long long)b * S::F + row] = h;
-        act_slot<S>(p, 0)[(long long)(BMAX + b) * S::F + row] = o;
+        act_slot<S>(p, 0)[(long long)n * S::F + row] = h;
+        act_slot<S>(p, 0)[(long long)(BMAX + n) * S::F + row] = o;
       }
     }
   }
 }
 
-// K splits as the decode's down projection: workgroup (tile, ks) of RB
-// blocks; the last split of a (tile, group) adds the KS_DN partials of its RB
-// blocks in split order (each group has its own partials and counters).
-template <class S>
-__global__ __launch_bounds__(GT) void bk_pdown(PGroup pg, int layer) {
-  static_assert(prefill_tiles_fit<S>(), "whole workgroup tiles");
-  constexpr int RB = PRB_DN, NT = S::KT_F / KS_DN;
-  __shared__ float red[RB][GW * 16 * 17];
-  __shared__ int last;
-  const int tile = blockIdx.x / KS_DN, ks = blockIdx.x % KS_DN, rb0 = tile * RB, kt0 = ks * NT;
-  const int g0 = blockIdx.y * PCG_DN;
+// QKV, O and down as LDS-tiled GEMMs, as bk_pgu_t with one weight matrix:
+// PT_MP row blocks x PT_NG column groups per workgroup, wave w owning block
+// w / 2 for groups 2 (w % 2), 2 (w % 2) + 1.  Epilogues: QKV scales by the
+// group's norm factor; O and down add the residual and publish x (the next
+// norm's bf16 parts and per-block sums of squares) as publish_x does.
+enum PtOp : int { PT_QKV = 0, PT_O = 1, PT_DN = 2 };
+template <class S, int OP>
+__global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
+  constexpr int K = OP == PT_QKV ? S::H : (OP == PT_O ? S::QD : S::F);
+  constexpr int NT = K / 32, NC = NT / PT_KC;
+  constexpr int AU = PT_MP * PT_KC * kWave, BU = PT_NG * 2 * PT_KC * kWave;
+  constexpr int LA = AU / GT, LB = BU / GT;
+  static_assert(NT % PT_KC == 0 && AU % GT == 0 && BU % GT == 0 && GW == 2 * PT_MP && PT_NG == 4, "tile shape");
+  __shared__ u32x4 sa[2][PT_MP][PT_KC][kWave];
+  __shared__ u32x4 sb[2][PT_NG][2][PT_KC][kWave];
+  const int rb0 = blockIdx.x * PT_MP, g0 = blockIdx.y * PT_NG, tid = ltid();
+  const int ngr = pg.n - g0 < PT_NG ? pg.n - g0 : PT_NG;
   const BParams p0 = group_params(pg, g0);
-  ATiles<NT> a[RB];
+  const u32x4* wm = OP == PT_QKV ? p0.wqkv + layer * p0.u_qkv
+                                 : (OP == PT_O ? p0.wo + layer * p0.u_o : p0.wd + layer * p0.u_dn);
+  // column planes of group q: hi at plane(q, 0), lo at plane(q, 1), [BMAX][K]
+  const auto plane = [&](const BParams& q, int pl) -> const uint16_t* {
+    if constexpr (OP == PT_QKV) return xg_plane<S>(q, 0, 0, pl);
+    if constexpr (OP == PT_O) return att_slot<S>(q, 0) + (long long)pl * BMAX * S::QD;
+    return act_slot<S>(q, 0) + (long long)pl * BMAX * S::F;
+  };
+  u32x4 ra[LA], rbv[LB];
+  const auto load = [&](int c) {
 #pragma unroll
-  for (int r = 0; r < RB; ++r) load_tiles(a[r], p0.wd + layer * p0.u_dn + (long long)(rb0 + r) * S::KT_F * 64, kt0);
-  BCols<NT> c[2];
-  {
-    const uint16_t* ac = act_slot<S>(p0, 0);
-    load_cols(c[0], ac, ac + BMAX * S::F, S::F, kt0);
-  }
-#pragma unroll
-  for (int ci = 0; ci < PCG_DN; ++ci) {
-    if (g0 + ci >= pg.n) break;
-    const BParams p = group_params(pg, g0 + ci);
-    if (ci + 1 < PCG_DN && g0 + ci + 1 < pg.n) {
-      const BParams pn = group_params(pg, g0 + ci + 1);
-      const uint16_t* ac = act_slot<S>(pn, 0);
-      load_cols(c[(ci + 1) & 1], ac, ac + BMAX * S::F, S::F, kt0);
+    for (int k = 0; k < LA; ++k) {
+      const int i = tid + GT * k, blk = i / (PT_KC * kWave), kt = (i / kWave) % PT_KC, ln = i % kWave;
+      ra[k] = __builtin_nontemporal_load(wm + ((long long)(rb0 + blk) * NT + c * PT_KC + kt) * 64 + ln);
     }
-    const int t = ltid(), b = t % 16;
-    float xin[RB];
 #pragma unroll
-    for (int r = 0; r < RB; ++r)
-      xin[r] = t < 256 && b < p.B ? x_slot<S>(p, 0, 1)[(long long)b * S::H + (rb0 + r) * 16 + t / 16] : 0.f;
-    if (ci > 0) __syncthreads();  // the previous group's reads of red / last are done
-    f32x4 acc[RB];
+    for (int k = 0; k < LB; ++k) {
+      const int i = tid + GT * k, gq = i / (2 * PT_KC * kWave), pl = (i / (PT_KC * kWave)) % 2;
+      const int kt = (i / kWave) % PT_KC, ln = i % kWave;
+      rbv[k] = u32x4{0u, 0u, 0u, 0u};
+      if (gq < ngr)
+        rbv[k] = *reinterpret_cast<const u32x4*>(plane(group_params(pg, g0 + gq), pl) + (ln & 15) * K +
+                                                 32 * (c * PT_KC + kt) + 8 * (ln >> 4));
+    }
+  };
+  const auto store = [&](int buf) {
 #pragma unroll
-    for (int r = 0; r < RB; ++r) acc[r] = tiles_mma(a[r], c[ci & 1]);
-    float v[RB];
-    block_reduce_n<RB>(acc, red, v);
-    if (!splitk_finish(p, tile, ks, KS_DN, v, &last)) continue;
-    __syncthreads();  // red is reused
-    const uint16_t* gain = layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE + S::NORM_ATTN
-                                           : p.final_norm;
+    for (int k = 0; k < LA; ++k) (&sa[buf][0][0][0])[tid + GT * k] = ra[k];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const float xn = t < 256 && b < p.B ? xin[r] + v[r] : 0.f;
-      publish_x<S, false>(p, 0, 0, gain, rb0 + r, xn, red[r]);
+    for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = rbv[k];
+  };
+  load(0);
+  store(0);
+  __syncthreads();
+  const int w = wave_id(), pw = w / 2, gb = 2 * (w % 2);
+  const unsigned l = lane_id();
+  f32x4 acc[2][2];  // [group][hi / lo part]
+#pragma unroll
+  for (int j = 0; j < 2; ++j) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < NC; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < NC) load(c + 1);
+#pragma unroll
+    for (int kt = 0; kt < PT_KC; ++kt) {
+      const u32x4 a = sa[buf][pw][kt][l];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[j][0] = mfma(a, sb[buf][gb + j][0][kt][l], acc[j][0]);
+        acc[j][1] = mfma(a, sb[buf][gb + j][1][kt][l], acc[j][1]);
+      }
+    }
+    if (c + 1 < NC) store(buf ^ 1);
+    __syncthreads();
+  }
+  // epilogue: lane (kg, n) holds rows 4 kg .. 4 kg + 3 of column n
+  const int n = (int)(l & 15u), kg = (int)(l >> 4), rb = rb0 + pw;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (gb + j >= ngr) break;
+    const BParams p = group_params(pg, g0 + gb + j);
+    const bool on = n < p.B;
+    if constexpr (OP == PT_QKV) {
+      constexpr int NB = S::H / 16, PER = NB / 4;
+      const float* q = ssq_slot<S>(p, 0, 0) + n;
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) ss += q[(kg * PER + i) * BMAX];
+      ss = sum_xor32(sum_xor16(ss));
+      const float rs = rsqrtf(ss / (float)S::H + kRmsEps);
+      if (on) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          qkv_slot<S>(p, 0)[(long long)n * S::QKV + rb * 16 + 4 * kg + i] = (acc[j][0][i] + acc[j][1][i]) * rs;
+      }
+    } else {
+      // O: residual stream copy 0 in, copy 1 + the FFN norm's parts out;
+      // down: copy 1 in, copy 0 + the next layer's (or the final) norm out
+      constexpr int CI = OP == PT_O ? 0 : 1, CO = 1 - CI;
+      const uint16_t* gain = OP == PT_O ? p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN
+                                        : (layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE +
+                                                                 S::NORM_ATTN
+                                                           : p.final_norm);
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = rb * 16 + 4 * kg + i;
+        const long long e = (long long)n * S::H + row;
+        const float xn = on ? x_slot<S>(p, 0, CI)[e] + (acc[j][0][i] + acc[j][1][i]) : 0.f;
+        if (on) {
+          x_slot<S>(p, 0, CO)[e] = xn;
+          uint16_t h, o;
+          split2(xn * bf16_to_f32(gain[row]), h, o);
+          xg_plane<S>(p, 0, CO, 0)[e] = h;
+          xg_plane<S>(p, 0, CO, 1)[e] = o;
+        }
+        sq += xn * xn;
+      }
+      sq = sum_xor32(sum_xor16(sq));
+      if (kg == 0) ssq_slot<S>(p, 0, CO)[(long long)rb * BMAX + n] = sq;
     }
   }
 }
