@@ -130,7 +130,8 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
   const BParams& p = g.p;
   hipLaunchKernelGGL((bk_embed<S, PGroup>), dim3(BMAX, ng), dim3(256), 0, h->stream, g);
   for (int l = 0; l < L; ++l) {
-    hipLaunchKernelGGL((bk_ptile<S, PT_QKV>), dim3(S::QKV / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_ptile<S, PT_QKV, PTileQKV>), dim3(S::QKV / 16 / PTileQKV::MP, rows(PTileQKV::NG)), dim3(GT),
+                       0, h->stream, g, l);
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
@@ -141,9 +142,12 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
                          l);
       hipLaunchKernelGGL(bk_pattn<S>, dim3(S::NKV, ng), dim3(AT), 0, h->stream, g, l);
     }
-    hipLaunchKernelGGL((bk_ptile<S, PT_O>), dim3(S::H / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL(bk_pgu_t<S>, dim3(S::F / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
-    hipLaunchKernelGGL((bk_ptile<S, PT_DN>), dim3(S::H / 16 / PT_MP, rows(PT_NG)), dim3(GT), 0, h->stream, g, l);
+    hipLaunchKernelGGL((bk_ptile<S, PT_O, PTileO>), dim3(S::H / 16 / PTileO::MP, rows(PTileO::NG)), dim3(GT), 0,
+                       h->stream, g, l);
+    hipLaunchKernelGGL((bk_pgu_t<S, PTileGU>), dim3(S::F / 16 / PTileGU::MP, rows(PTileGU::NG)), dim3(GT), 0,
+                       h->stream, g, l);
+    hipLaunchKernelGGL((bk_ptile<S, PT_DN, PTileDN>), dim3(S::H / 16 / PTileDN::MP, rows(PTileDN::NG)), dim3(GT), 0,
+                       h->stream, g, l);
   }
   if (last) {
     if (pl.lmhead8)
@@ -158,7 +162,8 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
 // QKV, O and down grids of whole XCD rounds: a row tile's column-group
 // workgroups share an XCD and its L2 (gate / up has 44 row tiles: its tiles'
 // groups spread over XCDs)
-static_assert((ShapeBaseline::QKV / 16 / PT_MP) % 8 == 0 && (ShapeBaseline::H / 16 / PT_MP) % 8 == 0,
+static_assert((ShapeBaseline::QKV / 16 / PTileQKV::MP) % 8 == 0 && (ShapeBaseline::H / 16 / PTileO::MP) % 8 == 0 &&
+                  (ShapeBaseline::H / 16 / PTileDN::MP) % 8 == 0,
               "prefill GEMM grids of whole XCD rounds");
 
 template <class S>

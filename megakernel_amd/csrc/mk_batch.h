@@ -700,47 +700,57 @@ __global__ __launch_bounds__(GT) void bk_down(G p, int layer) {
 // the columns' bf16 hi / lo parts as two B operands), accumulated over the
 // whole K by one wave, so no cross-wave reduction is needed.
 
-// Gate / up as an LDS-tiled GEMM: a workgroup computes PT_MP block pairs
-// (16 gate + 16 up rows each) for PT_NG column groups, K in chunks of PT_KC
-// tiles; each chunk's weight tiles and column tiles are staged in LDS once
-// (double-buffered, the next chunk's loads in flight during the current
-// chunk's products), so a weight byte is read from L2 once per PT_NG groups
-// and a column byte once per PT_MP block pairs.  Wave w owns block pair w / 2
-// for groups 2 (w % 2) and 2 (w % 2) + 1 over the whole K; the epilogue runs
-// on its accumulators.
-constexpr int PT_MP = 4, PT_NG = 4, PT_KC = 4;
-template <class S>
+// Tile shapes: MP row blocks (gate / up: block pairs of 16 gate + 16 up rows)
+// x NG column groups per workgroup, K in chunks of KC tiles; each chunk's
+// weight tiles and column tiles are staged in LDS once (double-buffered, the
+// next chunk's loads in flight during the current chunk's products), so a
+// weight byte is read from L2 once per NG groups and a column byte once per
+// MP blocks.  Wave w owns WB blocks x WGR groups over the whole K; the
+// epilogue runs on its accumulators.
+template <int MP_, int NG_, int KC_, int WB_, int WGR_>
+struct PTile {
+  static constexpr int MP = MP_, NG = NG_, KC = KC_, WB = WB_, WGR = WGR_;
+  static_assert((MP / WB) * (NG / WGR) == GW, "every wave owns whole blocks x groups");
+};
+// (measured per layer, us: gate / up <8,8,2,1,8> 50.4, <8,4,2,1,4> 67.4,
+// <4,8,2,1,4> 71.9, <4,4,4,1,2> 61.6; QKV <8,2,2,1,2> 20.2, <4,4,2,1,2> 22.8,
+// <4,2,4,1,1> 27.5, <4,4,4,1,2> 31.7, <8,8,2,1,8> 33.7; O <4,2,4,1,1> 20.7,
+// <8,1,4,1,1> 20.6, <8,2,4,2,1> 22.1, <4,4,4,1,2> 23.7; down <4,2,4,1,1> 38.5,
+// <8,1,4,1,1> 39.2, <8,2,4,2,1> 41.6, <4,4,4,1,2> 47.7, <2,4,4,1,1> 54.3)
+using PTileGU = PTile<8, 8, 2, 1, 8>;
+using PTileQKV = PTile<8, 2, 2, 1, 2>;
+using PTileO = PTile<4, 2, 4, 1, 1>;
+using PTileDN = PTile<4, 2, 4, 1, 1>;
+
+template <class S, class T>
 __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
-  constexpr int NT = S::KT_H, NC = NT / PT_KC;
-  constexpr int AU = 2 * PT_MP * PT_KC * kWave;  // u32x4 of a chunk's weight tiles
-  constexpr int BU = PT_NG * 2 * PT_KC * kWave;  // ... of its column tiles
-  constexpr int LA = AU / GT, LB = BU / GT;      // per thread
-  static_assert(NT % PT_KC == 0 && AU % GT == 0 && BU % GT == 0 && GW == 2 * PT_MP && PT_NG == 4,
-                "tile shape");
-  __shared__ u32x4 sa[2][2 * PT_MP][PT_KC][kWave];   // [buf][gate pairs | up pairs][tile][lane]
-  __shared__ u32x4 sb[2][PT_NG][2][PT_KC][kWave];    // [buf][group][hi / lo][tile][lane]
-  const int rb0 = blockIdx.x * PT_MP, g0 = blockIdx.y * PT_NG, tid = ltid();
-  const int ngr = pg.n - g0 < PT_NG ? pg.n - g0 : PT_NG;  // groups of this tile
+  constexpr int MP = T::MP, NG = T::NG, KC = T::KC, WB = T::WB, WGR = T::WGR;
+  constexpr int NT = S::KT_H, NC = NT / KC;
+  constexpr int AU = 2 * MP * KC * kWave;  // u32x4 of a chunk's weight tiles
+  constexpr int BU = NG * 2 * KC * kWave;  // ... of its column tiles
+  constexpr int LA = AU / GT, LB = BU / GT;  // per thread
+  static_assert(NT % KC == 0 && AU % GT == 0 && BU % GT == 0, "tile shape");
+  __shared__ u32x4 sa[2][2 * MP][KC][kWave];  // [buf][gate blocks | up blocks][tile][lane]
+  __shared__ u32x4 sb[2][NG][2][KC][kWave];   // [buf][group][hi / lo][tile][lane]
+  const int rb0 = blockIdx.x * MP, g0 = blockIdx.y * NG, tid = ltid();
+  const int ngr = pg.n - g0 < NG ? pg.n - g0 : NG;  // groups of this tile
   const BParams p0 = group_params(pg, g0);
   const u32x4* wgt[2] = {p0.wg + layer * p0.u_gu, p0.wu + layer * p0.u_gu};
   u32x4 ra[LA], rbv[LB];
   const auto load = [&](int c) {
 #pragma unroll
     for (int k = 0; k < LA; ++k) {
-      const int i = tid + GT * k, blk = i / (PT_KC * kWave), kt = (i / kWave) % PT_KC, ln = i % kWave;
-      ra[k] = __builtin_nontemporal_load(wgt[blk / PT_MP] + ((long long)(rb0 + blk % PT_MP) * NT + c * PT_KC + kt) * 64 +
-                                         ln);
+      const int i = tid + GT * k, blk = i / (KC * kWave), kt = (i / kWave) % KC, ln = i % kWave;
+      ra[k] = __builtin_nontemporal_load(wgt[blk / MP] + ((long long)(rb0 + blk % MP) * NT + c * KC + kt) * 64 + ln);
     }
 #pragma unroll
     for (int k = 0; k < LB; ++k) {
-      const int i = tid + GT * k, gq = i / (2 * PT_KC * kWave), pl = (i / (PT_KC * kWave)) % 2;
-      const int kt = (i / kWave) % PT_KC, ln = i % kWave;
+      const int i = tid + GT * k, gq = i / (2 * KC * kWave), pl = (i / (KC * kWave)) % 2;
+      const int kt = (i / kWave) % KC, ln = i % kWave;
       rbv[k] = u32x4{0u, 0u, 0u, 0u};
-      if (gq < ngr) {
-        const BParams q = group_params(pg, g0 + gq);
-        rbv[k] = *reinterpret_cast<const u32x4*>(xg_plane<S>(q, 0, 1, pl) + (ln & 15) * S::H +
-                                                 32 * (c * PT_KC + kt) + 8 * (ln >> 4));
-      }
+      if (gq < ngr)
+        rbv[k] = *reinterpret_cast<const u32x4*>(xg_plane<S>(group_params(pg, g0 + gq), 0, 1, pl) + (ln & 15) * S::H +
+                                                 32 * (c * KC + kt) + 8 * (ln >> 4));
     }
   };
   const auto store = [&](int buf) {
@@ -752,26 +762,31 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
   load(0);
   store(0);
   __syncthreads();
-  const int w = wave_id(), pw = w / 2, gb = 2 * (w % 2);
+  const int w = wave_id(), pw = (w / (NG / WGR)) * WB, gb = (w % (NG / WGR)) * WGR;
   const unsigned l = lane_id();
-  f32x4 acc[2][2][2];  // [group][gate / up][hi / lo part]
+  f32x4 acc[WB][WGR][2][2];  // [block][group][gate / up][hi / lo part]
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int r = 0; r < WB; ++r)
 #pragma unroll
-    for (int m = 0; m < 2; ++m) acc[j][m][0] = acc[j][m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WGR; ++j)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) acc[r][j][m][0] = acc[r][j][m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < NC; ++c) {
     const int buf = c & 1;
     if (c + 1 < NC) load(c + 1);
 #pragma unroll
-    for (int kt = 0; kt < PT_KC; ++kt) {
-      const u32x4 ag = sa[buf][pw][kt][l], au = sa[buf][PT_MP + pw][kt][l];
+    for (int kt = 0; kt < KC; ++kt) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const u32x4 bh = sb[buf][gb + j][0][kt][l], bl = sb[buf][gb + j][1][kt][l];
-        acc[j][0][0] = mfma(ag, bh, acc[j][0][0]);
-        acc[j][0][1] = mfma(ag, bl, acc[j][0][1]);
-        acc[j][1][0] = mfma(au, bh, acc[j][1][0]);
-        acc[j][1][1] = mfma(au, bl, acc[j][1][1]);
+      for (int r = 0; r < WB; ++r) {
+        const u32x4 ag = sa[buf][pw + r][kt][l], au = sa[buf][MP + pw + r][kt][l];
+#pragma unroll
+        for (int j = 0; j < WGR; ++j) {
+          const u32x4 bh = sb[buf][gb + j][0][kt][l], bl = sb[buf][gb + j][1][kt][l];
+          acc[r][j][0][0] = mfma(ag, bh, acc[r][j][0][0]);
+          acc[r][j][0][1] = mfma(ag, bl, acc[r][j][0][1]);
+          acc[r][j][1][0] = mfma(au, bh, acc[r][j][1][0]);
+          acc[r][j][1][1] = mfma(au, bl, acc[r][j][1][1]);
+        }
       }
     }
     if (c + 1 < NC) store(buf ^ 1);
@@ -780,7 +795,7 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
   // epilogue: lane (kg, n) holds rows 4 kg .. 4 kg + 3 of column n
   const int n = (int)(l & 15u), kg = (int)(l >> 4);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < WGR; ++j) {
     if (gb + j >= ngr) break;
     const BParams p = group_params(pg, g0 + gb + j);
     constexpr int NB = S::H / 16, PER = NB / 4;
@@ -792,35 +807,38 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
     const float rs = rsqrtf(ss / (float)S::H + kRmsEps);
     if (n < p.B) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = (rb0 + pw) * 16 + 4 * kg + i;
-        const float g = (acc[j][0][0][i] + acc[j][0][1][i]) * rs, u = (acc[j][1][0][i] + acc[j][1][1][i]) * rs;
-        uint16_t h, o;
-        split2(g / (1.0f + __expf(-g)) * u, h, o);  // SiLU(g) * u (reference utils.cuh:59-61)
-        act_slot<S>(p, 0)[(long long)n * S::F + row] = h;
-        act_slot<S>(p, 0)[(long long)(BMAX + n) * S::F + row] = o;
-      }
+      for (int r = 0; r < WB; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = (rb0 + pw + r) * 16 + 4 * kg + i;
+          const float g = (acc[r][j][0][0][i] + acc[r][j][0][1][i]) * rs;
+          const float u = (acc[r][j][1][0][i] + acc[r][j][1][1][i]) * rs;
+          uint16_t h, o;
+          split2(g / (1.0f + __expf(-g)) * u, h, o);  // SiLU(g) * u (reference utils.cuh:59-61)
+          act_slot<S>(p, 0)[(long long)n * S::F + row] = h;
+          act_slot<S>(p, 0)[(long long)(BMAX + n) * S::F + row] = o;
+        }
     }
   }
 }
 
-// QKV, O and down as LDS-tiled GEMMs, as bk_pgu_t with one weight matrix:
-// PT_MP row blocks x PT_NG column groups per workgroup, wave w owning block
-// w / 2 for groups 2 (w % 2), 2 (w % 2) + 1.  Epilogues: QKV scales by the
+// QKV, O and down as LDS-tiled GEMMs, as bk_pgu_t with one weight matrix.
+// Epilogues: QKV scales by the
 // group's norm factor; O and down add the residual and publish x (the next
 // norm's bf16 parts and per-block sums of squares) as publish_x does.
 enum PtOp : int { PT_QKV = 0, PT_O = 1, PT_DN = 2 };
-template <class S, int OP>
+template <class S, int OP, class T>
 __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
+  constexpr int MP = T::MP, NG = T::NG, KC = T::KC, WB = T::WB, WGR = T::WGR;
   constexpr int K = OP == PT_QKV ? S::H : (OP == PT_O ? S::QD : S::F);
-  constexpr int NT = K / 32, NC = NT / PT_KC;
-  constexpr int AU = PT_MP * PT_KC * kWave, BU = PT_NG * 2 * PT_KC * kWave;
+  constexpr int NT = K / 32, NC = NT / KC;
+  constexpr int AU = MP * KC * kWave, BU = NG * 2 * KC * kWave;
   constexpr int LA = AU / GT, LB = BU / GT;
-  static_assert(NT % PT_KC == 0 && AU % GT == 0 && BU % GT == 0 && GW == 2 * PT_MP && PT_NG == 4, "tile shape");
-  __shared__ u32x4 sa[2][PT_MP][PT_KC][kWave];
-  __shared__ u32x4 sb[2][PT_NG][2][PT_KC][kWave];
-  const int rb0 = blockIdx.x * PT_MP, g0 = blockIdx.y * PT_NG, tid = ltid();
-  const int ngr = pg.n - g0 < PT_NG ? pg.n - g0 : PT_NG;
+  static_assert(NT % KC == 0 && AU % GT == 0 && BU % GT == 0, "tile shape");
+  __shared__ u32x4 sa[2][MP][KC][kWave];
+  __shared__ u32x4 sb[2][NG][2][KC][kWave];
+  const int rb0 = blockIdx.x * MP, g0 = blockIdx.y * NG, tid = ltid();
+  const int ngr = pg.n - g0 < NG ? pg.n - g0 : NG;
   const BParams p0 = group_params(pg, g0);
   const u32x4* wm = OP == PT_QKV ? p0.wqkv + layer * p0.u_qkv
                                  : (OP == PT_O ? p0.wo + layer * p0.u_o : p0.wd + layer * p0.u_dn);
@@ -834,17 +852,17 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
   const auto load = [&](int c) {
 #pragma unroll
     for (int k = 0; k < LA; ++k) {
-      const int i = tid + GT * k, blk = i / (PT_KC * kWave), kt = (i / kWave) % PT_KC, ln = i % kWave;
-      ra[k] = __builtin_nontemporal_load(wm + ((long long)(rb0 + blk) * NT + c * PT_KC + kt) * 64 + ln);
+      const int i = tid + GT * k, blk = i / (KC * kWave), kt = (i / kWave) % KC, ln = i % kWave;
+      ra[k] = __builtin_nontemporal_load(wm + ((long long)(rb0 + blk) * NT + c * KC + kt) * 64 + ln);
     }
 #pragma unroll
     for (int k = 0; k < LB; ++k) {
-      const int i = tid + GT * k, gq = i / (2 * PT_KC * kWave), pl = (i / (PT_KC * kWave)) % 2;
-      const int kt = (i / kWave) % PT_KC, ln = i % kWave;
+      const int i = tid + GT * k, gq = i / (2 * KC * kWave), pl = (i / (KC * kWave)) % 2;
+      const int kt = (i / kWave) % KC, ln = i % kWave;
       rbv[k] = u32x4{0u, 0u, 0u, 0u};
       if (gq < ngr)
         rbv[k] = *reinterpret_cast<const u32x4*>(plane(group_params(pg, g0 + gq), pl) + (ln & 15) * K +
-                                                 32 * (c * PT_KC + kt) + 8 * (ln >> 4));
+                                                 32 * (c * KC + kt) + 8 * (ln >> 4));
     }
   };
   const auto store = [&](int buf) {
@@ -856,30 +874,35 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
   load(0);
   store(0);
   __syncthreads();
-  const int w = wave_id(), pw = w / 2, gb = 2 * (w % 2);
+  const int w = wave_id(), pw = (w / (NG / WGR)) * WB, gb = (w % (NG / WGR)) * WGR;
   const unsigned l = lane_id();
-  f32x4 acc[2][2];  // [group][hi / lo part]
+  f32x4 acc[WB][WGR][2];  // [block][group][hi / lo part]
 #pragma unroll
-  for (int j = 0; j < 2; ++j) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < WB; ++r)
+#pragma unroll
+    for (int j = 0; j < WGR; ++j) acc[r][j][0] = acc[r][j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < NC; ++c) {
     const int buf = c & 1;
     if (c + 1 < NC) load(c + 1);
 #pragma unroll
-    for (int kt = 0; kt < PT_KC; ++kt) {
-      const u32x4 a = sa[buf][pw][kt][l];
+    for (int kt = 0; kt < KC; ++kt) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[j][0] = mfma(a, sb[buf][gb + j][0][kt][l], acc[j][0]);
-        acc[j][1] = mfma(a, sb[buf][gb + j][1][kt][l], acc[j][1]);
+      for (int r = 0; r < WB; ++r) {
+        const u32x4 a = sa[buf][pw + r][kt][l];
+#pragma unroll
+        for (int j = 0; j < WGR; ++j) {
+          acc[r][j][0] = mfma(a, sb[buf][gb + j][0][kt][l], acc[r][j][0]);
+          acc[r][j][1] = mfma(a, sb[buf][gb + j][1][kt][l], acc[r][j][1]);
+        }
       }
     }
     if (c + 1 < NC) store(buf ^ 1);
     __syncthreads();
   }
   // epilogue: lane (kg, n) holds rows 4 kg .. 4 kg + 3 of column n
-  const int n = (int)(l & 15u), kg = (int)(l >> 4), rb = rb0 + pw;
+  const int n = (int)(l & 15u), kg = (int)(l >> 4);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < WGR; ++j) {
     if (gb + j >= ngr) break;
     const BParams p = group_params(pg, g0 + gb + j);
     const bool on = n < p.B;
@@ -893,8 +916,11 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
       const float rs = rsqrtf(ss / (float)S::H + kRmsEps);
       if (on) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          qkv_slot<S>(p, 0)[(long long)n * S::QKV + rb * 16 + 4 * kg + i] = (acc[j][0][i] + acc[j][1][i]) * rs;
+        for (int r = 0; r < WB; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            qkv_slot<S>(p, 0)[(long long)n * S::QKV + (rb0 + pw + r) * 16 + 4 * kg + i] =
+                (acc[r][j][0][i] + acc[r][j][1][i]) * rs;
       }
     } else {
       // O: residual stream copy 0 in, copy 1 + the FFN norm's parts out;
@@ -904,23 +930,27 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
                                         : (layer + 1 < p.L ? p.norms + (long long)(layer + 1) * S::NORM_STRIDE +
                                                                  S::NORM_ATTN
                                                            : p.final_norm);
-      float sq = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = rb * 16 + 4 * kg + i;
-        const long long e = (long long)n * S::H + row;
-        const float xn = on ? x_slot<S>(p, 0, CI)[e] + (acc[j][0][i] + acc[j][1][i]) : 0.f;
-        if (on) {
-          x_slot<S>(p, 0, CO)[e] = xn;
-          uint16_t h, o;
-          split2(xn * bf16_to_f32(gain[row]), h, o);
-          xg_plane<S>(p, 0, CO, 0)[e] = h;
-          xg_plane<S>(p, 0, CO, 1)[e] = o;
+      for (int r = 0; r < WB; ++r) {
+        const int rb = rb0 + pw + r;
+        float sq = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = rb * 16 + 4 * kg + i;
+          const long long e = (long long)n * S::H + row;
+          const float xn = on ? x_slot<S>(p, 0, CI)[e] + (acc[r][j][0][i] + acc[r][j][1][i]) : 0.f;
+          if (on) {
+            x_slot<S>(p, 0, CO)[e] = xn;
+            uint16_t h, o;
+            split2(xn * bf16_to_f32(gain[row]), h, o);
+            xg_plane<S>(p, 0, CO, 0)[e] = h;
+            xg_plane<S>(p, 0, CO, 1)[e] = o;
+          }
+          sq += xn * xn;
         }
-        sq += xn * xn;
+        sq = sum_xor32(sum_xor16(sq));
+        if (kg == 0) ssq_slot<S>(p, 0, CO)[(long long)rb * BMAX + n] = sq;
       }
-      sq = sum_xor32(sum_xor16(sq));
-      if (kg == 0) ssq_slot<S>(p, 0, CO)[(long long)rb * BMAX + n] = sq;
     }
   }
 }
