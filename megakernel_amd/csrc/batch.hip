@@ -140,7 +140,7 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
     } else {
       hipLaunchKernelGGL((bk_append<S, false, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL(bk_pattn<S>, dim3(S::NKV, ng), dim3(AT), 0, h->stream, g, l);
+      hipLaunchKernelGGL(bk_pattn<S>, dim3(S::NKV, ng, PA_SPLIT), dim3(AT), 0, h->stream, g, l);
     }
     hipLaunchKernelGGL((bk_ptile<S, PT_O, PTileO>), dim3(S::H / 16 / PTileO::MP, rows(PTileO::NG)), dim3(GT), 0,
                        h->stream, g, l);

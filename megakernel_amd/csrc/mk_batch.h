@@ -1523,18 +1523,26 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
 }
 
 // ------------------------------------------------------------ prefill attention
-// One workgroup per (column group, kv head) of a prefill pass: the group's 16
-// consecutive tokens x 2 q heads = 32 queries against the causal prefix
-// [0, last position of the group], every 32-position K / V block loaded once
-// for all 32 queries (bk_attn loads it once per token).  Wave w takes blocks
+// PA_SPLIT workgroups per (column group, kv head) of a prefill pass, each
+// taking PA_NQ / 2 of the group's consecutive tokens x 2 q heads = PA_NQ
+// queries against the causal prefix [0, its last position], every
+// 32-position K / V block loaded once for all its queries (bk_attn loads it
+// once per token).  Wave w takes blocks
 // w, w + 4, ... with an online softmax per query; the four waves' states are
 // combined at the end, so there are no split partials and no merge.  The
 // products are bk_attn's: scores^T = K . Qb with q in three bf16 parts (rows
 // 4 j + 0..2 of a 16-row tile hold query j of the tile), out^T = V^T . Pb
-// with the softmax weights split the same way; eight tiles hold the 32
-// queries (query 2 c + h = token c, q head 2 g + h).
-constexpr int PA_NQ = 2 * BMAX;      // queries of a (group, kv head)
-constexpr int PA_RT = PA_NQ / 4;     // 16-row tiles of their q parts
+// with the softmax weights split the same way; PA_RT tiles hold the PA_NQ
+// queries (query 2 c + h = the workgroup's token c, q head 2 g + h).
+#ifndef MK_PATTN_RT
+#define MK_PATTN_RT 4
+#endif
+// 16-row tiles of q parts per workgroup (2 tokens each; measured per layer:
+// 8 tiles 43.8 us at 341 registers, one workgroup per CU; 4 tiles 34.4 us at
+// 201, two per CU; 2 tiles 35.9 us)
+constexpr int PA_RT = MK_PATTN_RT;
+constexpr int PA_NQ = 4 * PA_RT;     // queries of a workgroup
+constexpr int PA_SPLIT = 2 * BMAX / PA_NQ;  // workgroups per (group, kv head)
 template <class S>
 struct PAttnLds {
   __attribute__((aligned(16))) uint16_t qb[PA_RT][16][S::D];  // q parts (A operand of the scores)
@@ -1553,10 +1561,12 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
   // the longest prefixes (the last groups) first: the pass's makespan is
   // theirs, the short ones fill in behind them
   const BParams p = group_params(pg, pg.n - 1 - (int)blockIdx.y);
-  const int g = blockIdx.x;
+  const int g = blockIdx.x, cb = (int)blockIdx.z * (PA_NQ / 2);  // the workgroup's first token of the group
   const int tid = ltid(), w = tid / kWave, l = tid % kWave;
   const int c16 = l & 15, rg = l >> 4;
-  const int p0 = p.pos[0], pmax = p0 + p.B - 1;  // the group's tokens are positions p0 .. pmax
+  if (cb >= p.B) return;
+  const int ce = cb + PA_NQ / 2 < p.B ? cb + PA_NQ / 2 : p.B;
+  const int p0 = p.pos[0], pmax = p0 + ce - 1;  // its tokens are positions p0 + cb .. pmax
   // 1. q of the 32 queries (wave w: queries 8 w .. 8 w + 7; lane = dimension):
   //    QK-norm (reference rmsnorm.cuh:57-84) and RoPE rotate-half
   //    (attention.cuh:22-44), as bk_attn's prologue
@@ -1565,8 +1575,8 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
     const float gain = bf16_to_f32(gn[l]);
     const int d = l & 31;
 #pragma unroll 2
-    for (int k = 0; k < 8; ++k) {
-      const int qi = 8 * w + k, col = qi >> 1, j = qi & 1;
+    for (int k = 0; k < PA_NQ / AW; ++k) {
+      const int qi = (PA_NQ / AW) * w + k, col = cb + (qi >> 1), j = qi & 1;
       const bool on = col < p.B;
       float v = on ? qkv_slot<S>(p, 0)[(long long)col * S::QKV + (g * 2 + j) * D + l] : 0.f;
       const float ss = wave_sum(v * v);
@@ -1598,7 +1608,7 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     m[rt] = -INFINITY, lsum[rt] = 0.f;
-    const int col = 2 * rt + (rg >> 1);
+    const int col = cb + 2 * rt + (rg >> 1);
     qpos[rt] = col < p.B ? p0 + col : -1;  // -1: no token (every score masked)
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1682,7 +1692,7 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
     const int d = tid % D;
 #pragma unroll
     for (int k = 0; k < PA_NQ / (AT / D); ++k) {
-      const int q = tid / D + (AT / D) * k, col = q >> 1, j = q & 1;
+      const int q = tid / D + (AT / D) * k, col = cb + (q >> 1), j = q & 1;
       if (col >= p.B) continue;
       float M = sm.mw[0][q];
 #pragma unroll
