@@ -228,7 +228,7 @@ def _prefill_case(shape, seed, prefix, prompt_len, other_len, max_seq):
     rng = np.random.default_rng(seed)
     prompt = [int(t) for t in rng.integers(0, shape.vocab, size=prompt_len)]
     before0 = eng.get_kv(0, other_len)
-    _print(f"prefill prefix={prefix} prompt={prompt_len} ({(prompt_len + 15) // 16} chunks)")
+    _print(f"prefill prefix={prefix} prompt={prompt_len} ({(prompt_len + 15) // 16} column groups)")
     nxt, logits = eng.prefill(1, prompt, with_logits=True)
     ref = None
     for t in prompt:
@@ -259,7 +259,7 @@ def _prefill_case(shape, seed, prefix, prompt_len, other_len, max_seq):
 
 
 def test_batch_prefill_tiny_multi_chunk():
-    """37 prompt tokens (chunks of 16, 16, 5) after a 40-position prefix,
+    """37 prompt tokens (one pass, column groups of 16, 16, 5) after a 40-position prefix,
     then 3 decode steps of both sequences against the oracle."""
     dw, eng, mo, nxt = _prefill_case(TINY, 41, prefix=40, prompt_len=37, other_len=9, max_seq=128)
     try:

@@ -352,7 +352,7 @@ def test_qwen3_preset_head_dim_128(chunk, merge):
 
 @pytest.mark.parametrize("which,prefix,prompt_len", [("tiny", 20, 37), ("baseline_2l", 300, 70), ("tiny", 0, 1)])
 def test_batch1_prefill_then_decode(which, prefix, prompt_len):
-    """megakernel_prefill on a batch-1 handle (16 prompt tokens per weight
+    """megakernel_prefill on a batch-1 handle (up to 1,024 prompt tokens per weight
     pass, the batched kernels on this handle's own cache), then decode: the
     token after the prompt and the following steps against the oracle stepped
     through the same prompt; the prompt's layer-0 K / V (which depend on each
