@@ -7,8 +7,8 @@ benchmark_sweep, close) with three deliberate differences:
 * no torch in the product path: weights are read with numpy and uploaded by
   the library (``megakernel_init_from_host``);
 * ``generate`` prefills the prompt once (the reference prefills it twice,
-  bridge.py:136-163) -- with ``prefill=True``, 16 prompt tokens per weight
-  pass on the matrix cores instead of one decode step per token -- and can
+  bridge.py:136-163) -- with ``prefill=True``, up to 1,024 prompt tokens per
+  weight pass on the matrix cores instead of one decode step per token -- and can
   decode all new tokens in one resident launch;
 * throughput accounting counts KV bytes as well as weight bytes, from the
   model shape instead of a fixed 926e6 constant (bridge.py:229).
@@ -107,8 +107,8 @@ class MegakernelEngine:
         self._prefill = True
 
     def prefill(self, token_ids) -> int:
-        """Consume prompt tokens at the current position, 16 per weight pass;
-        returns the greedy next token."""
+        """Consume prompt tokens at the current position, up to 1,024 per
+        weight pass; returns the greedy next token."""
         ids = [int(t) for t in token_ids]
         arr = (ctypes.c_int * max(1, len(ids)))(*ids)
         nxt = ctypes.c_int(-1)

@@ -31,7 +31,7 @@ from megakernel_amd.config import BASELINE, QWEN3_06B, TINY
 from megakernel_amd.weights import DeviceWeights, flat_layout
 from oracle import qwen3_ref, synth
 
-from ._helpers import check_step, check_tokens_teacher_forced, make_pair, oracle_shape
+from ._helpers import LOGIT_ABS, MARGIN, check_step, check_tokens_teacher_forced, make_pair, oracle_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -178,6 +178,45 @@ def _prefilled_pair(ctx: int, seed: int, extra: int):
     orc.set_kv(kv[:, 0], kv[:, 1])
     del kv
     return eng, orc, dw
+
+
+def test_prefill_full_model_1024_tokens():
+    """The prefill bench's workload: the full model consumes a 1,024-token
+    prompt (one pass of 64 column groups) from an empty cache through the
+    batch-1 handle's prefill context; the token after it against the oracle
+    stepped through the same prompt (logits within the bar through the batch
+    handle's own prefill, same weights), then 16 decoded tokens
+    teacher-forced."""
+    from megakernel_amd.batch import BatchEngine
+    n = 1024
+    eng, orc, dw = make_pair(BASELINE, 1025, n + 64, gain_std=0.0, bits_from_device=True)
+    try:
+        rng = np.random.default_rng(1025)
+        prompt = [int(t) for t in rng.integers(0, BASELINE.vocab, size=n)]
+        ref = None
+        for i, t in enumerate(prompt):
+            ref = orc.step(t, capture=i == n - 1)
+            if i % 256 == 255:
+                _print(f"  oracle: {i + 1} prompt tokens")
+        be = BatchEngine(dw, 1, n + 16, BASELINE)
+        try:
+            nxt_b, logits = be.prefill(0, prompt, with_logits=True)
+        finally:
+            be.close()
+        err = float(np.abs(logits - ref["logits"].numpy()).max())
+        _print(f"prefill {n}: next token {nxt_b} (oracle {ref['token']}), logits max abs err {err:.2e}")
+        assert err <= LOGIT_ABS
+        if nxt_b != ref["token"]:
+            assert qwen3_ref.top2_margin(ref["logits"]) <= MARGIN
+        eng.attach_prefill(dw)
+        nxt = eng.prefill(prompt)
+        assert nxt == nxt_b and eng.pos == n
+        gen = eng.decode_many(ref["token"], 16)
+        same, low = check_tokens_teacher_forced([ref["token"]] + gen[:-1], gen, orc)
+        _print(f"  16 decoded tokens after the prefill: {same} identical, {low} low-margin")
+    finally:
+        eng.close()
+        dw.free()
 
 
 def test_configs2_full_model_ctx1024_plain_launch():
