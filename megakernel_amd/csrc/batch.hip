@@ -135,12 +135,11 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL((bk_attn<S, true, PGroup>), dim3(BMAX * S::NKV * p.nsplit_max, ng), dim3(AT), 0, h->stream,
-                         g, l);
+      hipLaunchKernelGGL((bk_pattn<S, true>), dim3(S::NKV, ng, PA_SPLIT), dim3(AT), 0, h->stream, g, l);
     } else {
       hipLaunchKernelGGL((bk_append<S, false, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL(bk_pattn<S>, dim3(S::NKV, ng, PA_SPLIT), dim3(AT), 0, h->stream, g, l);
+      hipLaunchKernelGGL((bk_pattn<S, false>), dim3(S::NKV, ng, PA_SPLIT), dim3(AT), 0, h->stream, g, l);
     }
     hipLaunchKernelGGL((bk_ptile<S, PT_O, PTileO>), dim3(S::H / 16 / PTileO::MP, rows(PTileO::NG)), dim3(GT), 0,
                        h->stream, g, l);
@@ -404,19 +403,19 @@ static int run_steps(BHandle* h, const int* first, int n, int* out) {
 // block, in BParams order x, xg, ssq, qkv, att, act, part, cnt, gpart, gcnt,
 // keys, rope.
 static long long group_layout(const BHandle* h, long long off[12]) {
-  const long long gp = (long long)((h->F / 16) * KS_GU * 2 > (h->QKV / 16) * KS_QKV ? (h->F / 16) * KS_GU * 2
-                                                                                  : (h->QKV / 16) * KS_QKV) *
-                           256 * 4 + (long long)(h->H / 16) * (KS_O > KS_DN ? KS_O : KS_DN) * 256 * 4;
+  // the prefill kernels keep no attention partials or split-K sums (their
+  // attention merges in registers, their GEMMs run the whole K): part, cnt,
+  // gpart and gcnt get one line each
   const long long sz[12] = {(long long)2 * BMAX * h->H * 4,
                             (long long)4 * BMAX * h->H * 2,
                             (long long)2 * (h->H / 16) * BMAX * 4,
                             (long long)BMAX * h->QKV * 4,
                             (long long)2 * BMAX * h->QD * 2,
                             (long long)2 * BMAX * h->F * 2,
-                            (long long)BMAX * h->NKV * h->nsplit_max * PW * 4,
-                            (long long)BMAX * h->NKV * 4,
-                            gp,
-                            (long long)(h->F / 16 > h->QKV / 16 ? h->F / 16 : h->QKV / 16) * 4,
+                            256,
+                            256,
+                            256,
+                            256,
                             (long long)BMAX * 8,
                             (long long)BMAX * h->D * 4};
   long long o = 0;
@@ -427,8 +426,8 @@ static long long group_layout(const BHandle* h, long long off[12]) {
   return o;
 }
 
-// A slab of ng groups' buffers, cleared (the split counters start at zero and
-// re-arm themselves); a larger prompt replaces it with a larger one.
+// A slab of ng groups' buffers, cleared; a larger prompt replaces it with a
+// larger one.
 static int ensure_groups(BHandle* h, int ng) {
   if (h->pf_groups >= ng) return 0;
   long long off[12];
@@ -504,9 +503,6 @@ static int prefill_passes(BHandle* h, int seq, const int* tokens, int n, int pos
     pp.kv_seq = 0;
     pp.sc_seq = 0;
     pp.prefill = 1;
-    // the pass's attention grid: the splits its last position needs (every
-    // kernel of the pass indexes the partials with this count)
-    pp.nsplit_max = (pos0 + c0 + ntok + CH - 1) / CH;
     pp.tok = h->pf_tok + c0;
     pp.pos = h->pf_pos + c0;
     pp.out = h->pf_out;

@@ -1508,19 +1508,12 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
   __shared__ AttnLds<S> sm;
   const BParams& p = group_of(pg);  // column group
   // workgroup i runs on XCD i % 8: every split of one (sequence, kv head)
-  // pair gets the same XCD, so the merging split reads its partials there.
-  // Decode: a pair's splits are consecutive slots of its XCD.  Prefill:
-  // split-major (split 0 of every pair, then split 1, ...), so the splits the
-  // short prefixes leave empty come last instead of landing on every
-  // nsplit_max-th CU slot (measured: with a pass's split count of 4,
-  // pair-major put the always-busy split-0 items on a quarter of each XCD's
-  // CUs and ran 14 % slower; split-major is also 2 % faster than pair-major
-  // with a count of 5, and 3 % slower for the batched decode).
+  // pair gets the same XCD, so the merging split reads its partials there; a
+  // pair's splits are consecutive slots of its XCD (split-major numbering,
+  // split 0 of every pair first, measured 3 % slower for the batched decode)
   static_assert((BMAX * S::NKV) % 8 == 0, "whole (sequence, kv head) pairs per XCD");
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-  constexpr int PPX = BMAX * S::NKV / 8;  // pairs per XCD
-  const int bg = G::NG > 1 ? (slot % PPX) * 8 + xcd : (slot / p.nsplit_max) * 8 + xcd;
-  const int s = G::NG > 1 ? slot / PPX : slot % p.nsplit_max;
+  const int bg = (slot / p.nsplit_max) * 8 + xcd, s = slot % p.nsplit_max;
   const int b = bg / S::NKV, g = bg % S::NKV;
   if (b >= p.B) return;
   const int pos = p.pos[b];
@@ -1562,7 +1555,7 @@ struct PAttnLds {
   float mw[AW][PA_NQ], lw[AW][PA_NQ];
 };
 
-template <class S>
+template <class S, bool K8>
 __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
   static_assert(S::GQA == 2 && S::D == 64 && AT == 4 * kWave, "2 q heads of 64 per kv head, 4 waves");
   constexpr int D = S::D, NKV = S::NKV, RT = PA_RT;
@@ -1607,9 +1600,12 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
   // 2. the wave's blocks: online softmax per query on the matrix cores; lane
   //    (rg, c16) holds query 4 rt + rg of tile rt (token 2 rt + rg / 2)
   const float scale = 1.0f / sqrtf((float)D);
+  // K8: the FP8 cache (byte index = element index; codes converted to bf16
+  // exactly with the K row scale, the V row scale enters the softmax weight)
   const long long kbase = ((long long)layer * NKV + g) * (long long)p.s_pad * D;
-  const auto rk = make_rsrc(p.kv + kbase);
-  const auto rv = make_rsrc(p.kvt + kbase);
+  const long long sbase = ((long long)layer * NKV + g) * p.s_pad;
+  const auto rk = K8 ? make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + kbase) : make_rsrc(p.kv + kbase);
+  const auto rv = K8 ? make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + kbase) : make_rsrc(p.kvt + kbase);
   const unsigned lu = (unsigned)l;
   float m[RT], lsum[RT];
   int qpos[RT];
@@ -1626,16 +1622,30 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
   for (int kb = w; kb < nblk; kb += AW) {
     const int t0 = 32 * kb;
     u32x4 kr[2][2], vr[D / 16];
+    float sk[2] = {1.f, 1.f}, sv[2] = {1.f, 1.f};  // K8: the scales of the lane's two score positions
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-        kr[h][kc] = __builtin_amdgcn_raw_buffer_load_b128(
-            rk, ((unsigned)(t0 + 16 * h) * D + (lu & 15u) * D + 32u * kc + 8u * (lu >> 4)) * 2u, 0u, 2);
+      for (int kc = 0; kc < 2; ++kc) {
+        const unsigned e = (unsigned)(t0 + 16 * h) * D + (lu & 15u) * D + 32u * kc + 8u * (lu >> 4);
+        if constexpr (K8)
+          kr[h][kc] = fp8x8_to_bf16x8_scaled(__builtin_amdgcn_raw_buffer_load_b64(rk, e, 0u, 2), 1.0f);
+        else
+          kr[h][kc] = __builtin_amdgcn_raw_buffer_load_b128(rk, e * 2u, 0u, 2);
+      }
+      if constexpr (K8) {
+        sk[h] = p.kscale[sbase + t0 + 16 * h + c16];
+        sv[h] = p.vscale[sbase + t0 + 16 * h + c16];
+      }
+    }
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt)
-      vr[dt] = __builtin_amdgcn_raw_buffer_load_b128(
-          rv, ((unsigned)t0 * D + (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4)) * 2u, 0u, 2);
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const unsigned e = (unsigned)t0 * D + (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4);
+      if constexpr (K8)
+        vr[dt] = fp8x8_to_bf16x8_scaled(__builtin_amdgcn_raw_buffer_load_b64(rv, e, 0u, 2), 1.0f);
+      else
+        vr[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, e * 2u, 0u, 2);
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       float sc[2];
@@ -1646,7 +1656,8 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
         for (int kc = 0; kc < 2; ++kc)
           d4 = mfma(*reinterpret_cast<const u32x4*>(&sm.qb[rt][c16][32 * kc + 8 * rg]), kr[h][kc], d4);
         const int t = t0 + 16 * h + c16;
-        sc[h] = t <= qpos[rt] ? ((d4[0] + d4[1]) + d4[2]) * scale : -INFINITY;
+        // K8: the K row scale (a power of two) multiplies the exact product
+        sc[h] = t <= qpos[rt] ? ((d4[0] + d4[1]) + d4[2]) * sk[h] * scale : -INFINITY;
       }
       const float mn = fmaxf(m[rt], group_max<16>(fmaxf(sc[0], sc[1])));
       // a query none of whose positions so far is visible keeps m = -inf,
@@ -1662,7 +1673,7 @@ __global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
       lsum[rt] = lsum[rt] * alpha + group_sum<16>(ps);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const Split3 a = split3(sc[h]);
+        const Split3 a = split3(K8 ? sc[h] * sv[h] : sc[h]);
         sm.pb[w][rt][4 * rg + 0][16 * h + c16] = (uint16_t)(a.hi >> 16);
         sm.pb[w][rt][4 * rg + 1][16 * h + c16] = (uint16_t)(a.mid >> 16);
         sm.pb[w][rt][4 * rg + 2][16 * h + c16] = (uint16_t)(a.lo >> 16);
