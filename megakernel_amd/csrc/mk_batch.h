@@ -720,6 +720,16 @@ struct PTile {
 // <8,2,4,2,1> 41.6, <4,4,4,1,2> 47.7, <2,4,4,1,1> 54.3.  A wave owning more
 // blocks reads fewer LDS bytes per product.)
 using PTileGU = PTile<8, 8, 2, 4, 2>;
+// gate / up of a pass of at most PT_SMALL_GROUPS groups: the 8 x 8 tile
+// leaves too few workgroups (256 tokens: 44), 8 x 2 four times as many
+// (measured, tok/s, 8 x 8 / 8 x 2: 128 tokens 37,869 / 44,851, 256 tokens
+// 74,028 / 87,756, 512 tokens 138,672 / 154,683, 1,024 tokens 220,199 /
+// 207,877)
+using PTileGUs = PTile<8, 2, 2, 2, 1>;
+#ifndef MK_PT_SMALL_GROUPS
+#define MK_PT_SMALL_GROUPS 32
+#endif
+constexpr int PT_SMALL_GROUPS = MK_PT_SMALL_GROUPS;
 using PTileQKV = PTile<8, 2, 2, 2, 1>;
 using PTileO = PTile<4, 2, 4, 1, 1>;
 using PTileDN = PTile<4, 2, 4, 1, 1>;
