@@ -149,8 +149,12 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
     else
       hipLaunchKernelGGL((bk_pgu_t<S, PTileGUs>), dim3(S::F / 16 / PTileGUs::MP, rows(PTileGUs::NG)), dim3(GT), 0,
                          h->stream, g, l);
-    hipLaunchKernelGGL((bk_ptile<S, PT_DN, PTileDN>), dim3(S::H / 16 / PTileDN::MP, rows(PTileDN::NG)), dim3(GT), 0,
-                       h->stream, g, l);
+    if (ng > PT_SMALL_GROUPS)
+      hipLaunchKernelGGL((bk_ptile<S, PT_DN, PTileDN>), dim3(S::H / 16 / PTileDN::MP, rows(PTileDN::NG)), dim3(GT), 0,
+                         h->stream, g, l);
+    else
+      hipLaunchKernelGGL((bk_ptile<S, PT_DN, PTileDNs>), dim3(S::H / 16 / PTileDNs::MP, rows(PTileDNs::NG)), dim3(GT),
+                         0, h->stream, g, l);
   }
   if (last) {
     if (pl.lmhead8)

@@ -707,10 +707,12 @@ __global__ __launch_bounds__(GT) void bk_down(G p, int layer) {
 // weight byte is read from L2 once per NG groups and a column byte once per
 // MP blocks.  Wave w owns WB blocks x WGR groups over the whole K; the
 // epilogue runs on its accumulators.
-template <int MP_, int NG_, int KC_, int WB_, int WGR_>
+template <int MP_, int NG_, int KC_, int WB_, int WGR_, int PD_ = 2>
 struct PTile {
   static constexpr int MP = MP_, NG = NG_, KC = KC_, WB = WB_, WGR = WGR_;
+  static constexpr int PD = PD_;  // K chunks whose loads are in flight (1 or 2 register sets)
   static_assert((MP / WB) * (NG / WGR) == GW, "every wave owns whole blocks x groups");
+  static_assert(PD == 1 || PD == 2, "one or two register sets");
 };
 // (measured per layer, us: gate / up <8,8,2,4,2> 46.5, <8,8,2,2,4> 47.3,
 // <8,8,2,1,8> 50.2, <8,4,2,1,4> 67.4, <4,8,2,1,4> 71.9, <4,4,4,1,2> 61.6;
@@ -719,7 +721,7 @@ struct PTile {
 // <8,2,4,2,1> 22.1, <4,4,4,1,2> 23.7; down <4,2,4,1,1> 38.5, <8,1,4,1,1> 39.2,
 // <8,2,4,2,1> 41.6, <4,4,4,1,2> 47.7, <2,4,4,1,1> 54.3.  A wave owning more
 // blocks reads fewer LDS bytes per product.)
-using PTileGU = PTile<8, 8, 2, 4, 2>;
+using PTileGU = PTile<8, 8, 2, 4, 2, 1>;  // one register set: 234 VGPRs
 // gate / up of a pass of at most PT_SMALL_GROUPS groups: the 8 x 8 tile
 // leaves too few workgroups (256 tokens: 44), 8 x 2 four times as many
 // (measured, tok/s, 8 x 8 / 8 x 2: 128 tokens 37,869 / 44,851, 256 tokens
@@ -732,7 +734,8 @@ using PTileGUs = PTile<8, 2, 2, 2, 1>;
 constexpr int PT_SMALL_GROUPS = MK_PT_SMALL_GROUPS;
 using PTileQKV = PTile<8, 2, 2, 2, 1>;
 using PTileO = PTile<4, 2, 4, 1, 1>;
-using PTileDN = PTile<4, 2, 4, 1, 1>;
+using PTileDN = PTile<4, 2, 4, 1, 1, 1>;   // one register set: two lose 8 % at 1,024 tokens
+using PTileDNs = PTile<4, 2, 4, 1, 1, 2>;  // passes of at most PT_SMALL_GROUPS groups
 
 template <class S, class T>
 __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
@@ -755,31 +758,33 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
   const int ngr = pg.n - g0 < NG ? pg.n - g0 : NG;  // groups of this tile
   const BParams p0 = group_params(pg, g0);
   const u32x4* wgt[2] = {p0.wg + layer * p0.u_gu, p0.wu + layer * p0.u_gu};
-  u32x4 ra[LA], rbv[LB];
-  const auto load = [&](int c) {
+  u32x4 ra[T::PD][LA], rbv[T::PD][LB];
+  const auto load = [&](int c, u32x4(&xa)[LA], u32x4(&xb)[LB]) {
 #pragma unroll
     for (int k = 0; k < LA; ++k) {
       const int i = tid + GT * k, blk = i / (KC * kWave), kt = (i / kWave) % KC, ln = i % kWave;
-      ra[k] = __builtin_nontemporal_load(wgt[blk / MP] + ((long long)(rb0 + blk % MP) * NT + c * KC + kt) * 64 + ln);
+      xa[k] = __builtin_nontemporal_load(wgt[blk / MP] + ((long long)(rb0 + blk % MP) * NT + c * KC + kt) * 64 + ln);
     }
 #pragma unroll
     for (int k = 0; k < LB; ++k) {
       const int i = tid + GT * k, gq = i / (2 * KC * kWave), pl = (i / (KC * kWave)) % 2;
       const int kt = (i / kWave) % KC, ln = i % kWave;
-      rbv[k] = u32x4{0u, 0u, 0u, 0u};
+      xb[k] = u32x4{0u, 0u, 0u, 0u};
       if (gq < ngr)
-        rbv[k] = *reinterpret_cast<const u32x4*>(xg_plane<S>(group_params(pg, g0 + gq), 0, 1, pl) + (ln & 15) * S::H +
+        xb[k] = *reinterpret_cast<const u32x4*>(xg_plane<S>(group_params(pg, g0 + gq), 0, 1, pl) + (ln & 15) * S::H +
                                                  32 * (c * KC + kt) + 8 * (ln >> 4));
     }
   };
-  const auto store = [&](int buf) {
+  const auto store = [&](int buf, const u32x4(&xa)[LA], const u32x4(&xb)[LB]) {
 #pragma unroll
-    for (int k = 0; k < LA; ++k) (&sa[buf][0][0][0])[tid + GT * k] = ra[k];
+    for (int k = 0; k < LA; ++k) (&sa[buf][0][0][0])[tid + GT * k] = xa[k];
 #pragma unroll
-    for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = rbv[k];
+    for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = xb[k];
   };
-  load(0);
-  store(0);
+  load(0, ra[0], rbv[0]);
+  store(0, ra[0], rbv[0]);
+  if constexpr (T::PD == 2)
+    if (NC > 1) load(1, ra[T::PD - 1], rbv[T::PD - 1]);
   __syncthreads();
   const int w = wave_id(), pw = (w / (NG / WGR)) * WB, gb = (w % (NG / WGR)) * WGR;
   const unsigned l = lane_id();
@@ -790,9 +795,7 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
     for (int j = 0; j < WGR; ++j)
 #pragma unroll
       for (int m = 0; m < 2; ++m) acc[r][j][m][0] = acc[r][j][m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < NC; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < NC) load(c + 1);
+  const auto compute = [&](int buf) {
 #pragma unroll
     for (int kt = 0; kt < KC; ++kt) {
 #pragma unroll
@@ -808,8 +811,29 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
         }
       }
     }
-    if (c + 1 < NC) store(buf ^ 1);
-    __syncthreads();
+  };
+  if constexpr (T::PD == 1) {
+    for (int c = 0; c < NC; ++c) {
+      if (c + 1 < NC) load(c + 1, ra[0], rbv[0]);
+      compute(c & 1);
+      if (c + 1 < NC) store((c + 1) & 1, ra[0], rbv[0]);
+      __syncthreads();
+    }
+  } else {
+    // chunk k sits in register set k & 1, then in LDS buffer k & 1: while a
+    // chunk is multiplied, the next one waits in registers and the one after
+    // it is loading
+    for (int c = 0; c < NC; c += 2) {
+      if (c + 2 < NC) load(c + 2, ra[0], rbv[0]);
+      compute(0);
+      if (c + 1 < NC) store(1, ra[T::PD - 1], rbv[T::PD - 1]);
+      __syncthreads();
+      if (c + 1 >= NC) break;
+      if (c + 3 < NC) load(c + 3, ra[T::PD - 1], rbv[T::PD - 1]);
+      compute(1);
+      if (c + 2 < NC) store(0, ra[0], rbv[0]);
+      __syncthreads();
+    }
   }
   // epilogue: lane (kg, n) holds rows 4 kg .. 4 kg + 3 of column n
   const int n = (int)(l & 15u), kg = (int)(l >> 4);
@@ -867,31 +891,33 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
     if constexpr (OP == PT_O) return att_slot<S>(q, 0) + (long long)pl * BMAX * S::QD;
     return act_slot<S>(q, 0) + (long long)pl * BMAX * S::F;
   };
-  u32x4 ra[LA], rbv[LB];
-  const auto load = [&](int c) {
+  u32x4 ra[T::PD][LA], rbv[T::PD][LB];
+  const auto load = [&](int c, u32x4(&xa)[LA], u32x4(&xb)[LB]) {
 #pragma unroll
     for (int k = 0; k < LA; ++k) {
       const int i = tid + GT * k, blk = i / (KC * kWave), kt = (i / kWave) % KC, ln = i % kWave;
-      ra[k] = __builtin_nontemporal_load(wm + ((long long)(rb0 + blk) * NT + c * KC + kt) * 64 + ln);
+      xa[k] = __builtin_nontemporal_load(wm + ((long long)(rb0 + blk) * NT + c * KC + kt) * 64 + ln);
     }
 #pragma unroll
     for (int k = 0; k < LB; ++k) {
       const int i = tid + GT * k, gq = i / (2 * KC * kWave), pl = (i / (KC * kWave)) % 2;
       const int kt = (i / kWave) % KC, ln = i % kWave;
-      rbv[k] = u32x4{0u, 0u, 0u, 0u};
+      xb[k] = u32x4{0u, 0u, 0u, 0u};
       if (gq < ngr)
-        rbv[k] = *reinterpret_cast<const u32x4*>(plane(group_params(pg, g0 + gq), pl) + (ln & 15) * K +
+        xb[k] = *reinterpret_cast<const u32x4*>(plane(group_params(pg, g0 + gq), pl) + (ln & 15) * K +
                                                  32 * (c * KC + kt) + 8 * (ln >> 4));
     }
   };
-  const auto store = [&](int buf) {
+  const auto store = [&](int buf, const u32x4(&xa)[LA], const u32x4(&xb)[LB]) {
 #pragma unroll
-    for (int k = 0; k < LA; ++k) (&sa[buf][0][0][0])[tid + GT * k] = ra[k];
+    for (int k = 0; k < LA; ++k) (&sa[buf][0][0][0])[tid + GT * k] = xa[k];
 #pragma unroll
-    for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = rbv[k];
+    for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = xb[k];
   };
-  load(0);
-  store(0);
+  load(0, ra[0], rbv[0]);
+  store(0, ra[0], rbv[0]);
+  if constexpr (T::PD == 2)
+    if (NC > 1) load(1, ra[T::PD - 1], rbv[T::PD - 1]);
   __syncthreads();
   const int w = wave_id(), pw = (w / (NG / WGR)) * WB, gb = (w % (NG / WGR)) * WGR;
   const unsigned l = lane_id();
@@ -900,9 +926,7 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
   for (int r = 0; r < WB; ++r)
 #pragma unroll
     for (int j = 0; j < WGR; ++j) acc[r][j][0] = acc[r][j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < NC; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < NC) load(c + 1);
+  const auto compute = [&](int buf) {
 #pragma unroll
     for (int kt = 0; kt < KC; ++kt) {
 #pragma unroll
@@ -915,8 +939,29 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
         }
       }
     }
-    if (c + 1 < NC) store(buf ^ 1);
-    __syncthreads();
+  };
+  if constexpr (T::PD == 1) {
+    for (int c = 0; c < NC; ++c) {
+      if (c + 1 < NC) load(c + 1, ra[0], rbv[0]);
+      compute(c & 1);
+      if (c + 1 < NC) store((c + 1) & 1, ra[0], rbv[0]);
+      __syncthreads();
+    }
+  } else {
+    // chunk k sits in register set k & 1, then in LDS buffer k & 1: while a
+    // chunk is multiplied, the next one waits in registers and the one after
+    // it is loading
+    for (int c = 0; c < NC; c += 2) {
+      if (c + 2 < NC) load(c + 2, ra[0], rbv[0]);
+      compute(0);
+      if (c + 1 < NC) store(1, ra[T::PD - 1], rbv[T::PD - 1]);
+      __syncthreads();
+      if (c + 1 >= NC) break;
+      if (c + 3 < NC) load(c + 3, ra[T::PD - 1], rbv[T::PD - 1]);
+      compute(1);
+      if (c + 2 < NC) store(0, ra[0], rbv[0]);
+      __syncthreads();
+    }
   }
   // epilogue: lane (kg, n) holds rows 4 kg .. 4 kg + 3 of column n
   const int n = (int)(l & 15u), kg = (int)(l >> 4);
