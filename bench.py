@@ -59,6 +59,9 @@ def parse():
                     help="only run 5 plain device copies of 1 GiB (known bytes) for scaling rocprof counters")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_traffic.json"),
                     help="measured HBM bytes per launch (rocprofv3 --pmc), if present")
+    ap.add_argument("--step-traffic-dir", default=os.path.join(ROOT, "profiles"),
+                    help="where the measured HBM bytes per batched step / per prompt live "
+                         "(batch<B>_traffic.json, prefill<N>_traffic.json), if present")
     ap.add_argument("--batch", type=int, default=0,
                     help="BASELINE configs[4] instead: this many independent sequences (<= 16), KV lengths "
                          "uniform in [--kv-min, --kv-max] from --seed, --steps greedy steps each")
@@ -233,6 +236,20 @@ def batch_trace_summary(eng, toks, info):
     print(json.dumps({"batch_step_trace": out, "layer_period_us": round(period, 2)}), file=sys.stderr, flush=True)
 
 
+def measured_traffic(path, key, alg_bytes):
+    """HBM bytes per unit (batched step, prompt) from a step-traffic summary of
+    rocprofv3 --pmc runs (python -m megakernel_amd.profiling step-traffic),
+    when it was measured for this workload (same key): the measured traffic /
+    algorithmic ratio applied to this run's algorithmic bytes per unit."""
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        tj = json.load(f)
+    if tj.get("traffic_key") != key or not tj.get("traffic_over_algorithmic"):
+        return None
+    return round(tj["traffic_over_algorithmic"] * alg_bytes)
+
+
 def bench_batch(args):
     """n independent sequences, per-sequence KV lengths
     uniform in [kv_min, kv_max] from the seed (synthetic N(0, 1) prefill), K
@@ -288,6 +305,11 @@ def bench_batch(args):
     achieved = nbytes / kern / 1e9
     eng.close()
     dw.free()
+    # the workload a measured traffic summary must match (the step count
+    # only shifts the lengths; the ratio to the algorithmic bytes carries over)
+    key = {"what": "batch", "sequences": B, "kv_lengths": lengths, "step": args.batch_step,
+           "kv_fp8": bool(args.kv_fp8), "lmhead_fp8": bool(args.lmhead_fp8)}
+    traffic = measured_traffic(os.path.join(args.step_traffic_dir, f"batch{B}_traffic.json"), key, nbytes / K)
     out = {
         "metric": f"batched greedy decode tok/s ({B} sequences, KV {args.kv_min}-{args.kv_max})",
         "value": round(B * K / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -301,7 +323,8 @@ def bench_batch(args):
                    "device": info["name"], "reps": args.reps},
         "steps_per_s": round(K / wall, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "per": "step"},
+        "algorithmic_bytes_per_unit": round(nbytes / K), "traffic_key": key,
     }
     print(json.dumps(out))
 
@@ -498,6 +521,7 @@ def bench_prefill(args):
     pass_end = [min(N, (k + 1) * PREFILL_PASS_TOKENS) for k in range(npasses)]
     hbm_bytes = (npasses * shape.n_layers * shape.layer_weight_bytes + 2 * shape.vocab * shape.hidden +
                  sum(shape.kv_bytes_per_pos * e for e in pass_end))
+    key = {"what": "prefill", "prompt": N, "pass_tokens": PREFILL_PASS_TOKENS}
     out = {
         "metric": f"prefill tok/s ({N}-token prompt, empty cache)",
         "value": round(N / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": N, "warmup": 1,
@@ -509,9 +533,12 @@ def bench_prefill(args):
         "prefill_by_decode_tok_s": round(by_decode, 1),
         "next_token": toks[-1],
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(os.path.join(args.step_traffic_dir, f"prefill{N}_traffic.json"),
+                                                 key, hbm_bytes), "per": "prompt"},
         "hbm_sweep": {"bytes": hbm_bytes, "achieved_gbps": round(hbm_bytes / kern / 1e9, 1),
                       "frac": round(hbm_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)},
+        "algorithmic_bytes_per_unit": hbm_bytes, "traffic_key": key,
     }
     print(json.dumps(out))
 

@@ -15,7 +15,13 @@ Two jobs, both on files rocprofv3 wrote (``--output-format csv``):
   size -- into HBM bytes per decode launch.  Each counter is scaled by
   (known copy bytes / what that counter read for the copy), which absorbs the
   counter's unit and any per-XCD aggregation quirk.  Written as JSON for
-  ``bench.py`` (``roofline.traffic``).
+  ``bench.py`` (``roofline.traffic``);
+* ``step-traffic``: the same scaling for work that runs as many kernels --
+  a batched decode step, a prefill -- summing FETCH_SIZE / WRITE_SIZE over
+  every dispatch whose name matches ``--kernels`` and dividing by the number
+  of dispatches of ``--unit-kernel`` (one per step or per prompt).  The
+  bench line of the profiled run supplies the algorithmic bytes per unit and
+  the workload key that ``bench.py`` matches before it reports the traffic.
 
 Usage:
   python -m megakernel_amd.profiling stats STATS.csv --command "..." -o OUT.txt
@@ -24,6 +30,9 @@ Usage:
   python -m megakernel_amd.profiling traffic --decode-fetch A.csv --decode-write B.csv \
       --copy-fetch C.csv --copy-write D.csv --copy-bytes N --ctx 1024 --tokens 256 \
       --algorithmic-bytes X -o profiles/decode_traffic.json
+  python -m megakernel_amd.profiling step-traffic --fetch A.csv --write B.csv --copy-fetch C.csv \
+      --copy-write D.csv --copy-bytes N --kernels mk::batch:: --unit-kernel bk_tok \
+      --bench-json BENCH.json -o profiles/batch16_traffic.json
 """
 from __future__ import annotations
 
@@ -129,6 +138,42 @@ def traffic(args) -> dict:
     }
 
 
+def step_traffic(args) -> dict:
+    """HBM bytes per unit (step / prompt) summed over many kernels' dispatches."""
+    f = counter_values(args.fetch, "FETCH_SIZE", args.kernels)
+    w = counter_values(args.write, "WRITE_SIZE", args.kernels)
+    nf = len(counter_values(args.fetch, "FETCH_SIZE", args.unit_kernel))
+    nw = len(counter_values(args.write, "WRITE_SIZE", args.unit_kernel))
+    cp_f = counter_values(args.copy_fetch, "FETCH_SIZE", args.copy_kernel)
+    cp_w = counter_values(args.copy_write, "WRITE_SIZE", args.copy_kernel)
+    if not (f and w and nf and nw and cp_f and cp_w) or nf != nw:
+        raise SystemExit("missing counter rows (fetch / write dispatches, units, copy fetch / write): "
+                         f"{len(f)} {len(w)} {nf} {nw} {len(cp_f)} {len(cp_w)}")
+    bench = None
+    with open(args.bench_json) as fh:  # the bench line among whatever else the run printed
+        for line in fh:
+            if line.startswith("{") and '"traffic_key"' in line:
+                bench = json.loads(line)
+    if bench is None:
+        raise SystemExit(f"no bench line with a traffic_key in {args.bench_json}")
+    alg = float(bench["algorithmic_bytes_per_unit"])
+    scale_f = args.copy_bytes / statistics.median(cp_f)
+    scale_w = args.copy_bytes / statistics.median(cp_w)
+    fetch_b = sum(f) / nf * scale_f
+    write_b = sum(w) / nw * scale_w
+    return {
+        "traffic_key": bench["traffic_key"], "units": nf, "dispatches": len(f),
+        "kernels": args.kernels, "unit_kernel": args.unit_kernel,
+        "copy_bytes": args.copy_bytes,
+        "copy_fetch_counter": statistics.median(cp_f), "copy_write_counter": statistics.median(cp_w),
+        "fetch_scale_bytes_per_unit": scale_f, "write_scale_bytes_per_unit": scale_w,
+        "fetch_bytes_per_unit": fetch_b, "write_bytes_per_unit": write_b,
+        "hbm_bytes_per_unit": fetch_b + write_b,
+        "algorithmic_bytes_per_unit": alg,
+        "traffic_over_algorithmic": (fetch_b + write_b) / alg,
+    }
+
+
 # derived quantities of the counter summary: (label, numerator, denominator)
 DERIVED = [
     ("L2 (TCC) hit rate", ("TCC_HIT_sum",), ("TCC_HIT_sum", "TCC_MISS_sum")),
@@ -182,6 +227,14 @@ def main(argv=None):
     t.add_argument("--tokens", type=int, required=True)
     t.add_argument("--algorithmic-bytes", type=float, default=0.0)
     t.add_argument("-o", "--out", required=True)
+    st = sub.add_parser("step-traffic")
+    for k in ("fetch", "write", "copy-fetch", "copy-write", "bench-json"):
+        st.add_argument(f"--{k}", required=True)
+    st.add_argument("--copy-kernel", default="", help="substring of the copy kernel's name")
+    st.add_argument("--copy-bytes", type=float, required=True, help="bytes read (= bytes written) by one copy")
+    st.add_argument("--kernels", required=True, help="substring of the kernels whose counters are summed")
+    st.add_argument("--unit-kernel", required=True, help="substring of the kernel dispatched once per unit")
+    st.add_argument("-o", "--out", required=True)
     c = sub.add_parser("counters")
     c.add_argument("csv", nargs="+", help="counter_collection.csv of one or more --pmc passes")
     c.add_argument("--command", required=True, help="the commands that produced the csv files")
@@ -207,7 +260,7 @@ def main(argv=None):
                 f.write(txt)
         sys.stdout.write(txt)
     else:
-        res = traffic(a)
+        res = traffic(a) if a.what == "traffic" else step_traffic(a)
         with open(a.out, "w") as f:
             json.dump(res, f, indent=1)
         print(json.dumps(res, indent=1))
