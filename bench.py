@@ -61,7 +61,7 @@ def parse():
                     help="measured HBM bytes per launch (rocprofv3 --pmc), if present")
     ap.add_argument("--step-traffic-dir", default=os.path.join(ROOT, "profiles"),
                     help="where the measured HBM bytes per batched step / per prompt live "
-                         "(batch<B>_traffic.json, prefill<N>_traffic.json), if present")
+                         "(batch<B>[_kvfp8][_lmheadfp8]_traffic.json, prefill<N>_traffic.json), if present")
     ap.add_argument("--batch", type=int, default=0,
                     help="BASELINE configs[4] instead: this many independent sequences (<= 16), KV lengths "
                          "uniform in [--kv-min, --kv-max] from --seed, --steps greedy steps each")
@@ -309,7 +309,8 @@ def bench_batch(args):
     # only shifts the lengths; the ratio to the algorithmic bytes carries over)
     key = {"what": "batch", "sequences": B, "kv_lengths": lengths, "step": args.batch_step,
            "kv_fp8": bool(args.kv_fp8), "lmhead_fp8": bool(args.lmhead_fp8)}
-    traffic = measured_traffic(os.path.join(args.step_traffic_dir, f"batch{B}_traffic.json"), key, nbytes / K)
+    tname = f"batch{B}{'_kvfp8' if args.kv_fp8 else ''}{'_lmheadfp8' if args.lmhead_fp8 else ''}_traffic.json"
+    traffic = measured_traffic(os.path.join(args.step_traffic_dir, tname), key, nbytes / K)
     out = {
         "metric": f"batched greedy decode tok/s ({B} sequences, KV {args.kv_min}-{args.kv_max})",
         "value": round(B * K / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
