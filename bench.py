@@ -137,7 +137,7 @@ def trace_summary(eng, shape, args, info):
     import numpy as np
     L, G = shape.n_layers, eng.grid_size
     n = 5 * L + 1
-    n_evt = 16
+    n_evt = 17 + 5 * 10  # EVT events, the role class, then (enter, 8 wave exits, rounds) per wait site (mk_kernel.h)
     buf = (ctypes.c_ulonglong * ((n * 2 + n_evt) * G))()
     eng.fill_kv_synthetic(args.ctx, args.seed)
     r = eng.lib.megakernel_trace_generate(eng._handle, 1, 8, 4, buf)
@@ -182,6 +182,8 @@ def trace_summary(eng, shape, args, info):
     if not (ev > 0).any():
         print("# (fine-grained events are compiled in with -DMK_TRACE_EVENTS=1)", file=sys.stderr)
         return
+    poll_summary(tr, ev, L // 2, us)
+    ev = ev[:16]
     base = min(ev[e][ev[e] > 0].min() for e in range(len(evn)) if (ev[e] > 0).any())
     print(f"# events of layer {L // 2} (us from the first event; min / median / max over workgroups):",
           file=sys.stderr)
@@ -192,6 +194,50 @@ def trace_summary(eng, shape, args, info):
             v = (v - base) * us
             print(f"#   {evn[e]:12s} n={v.size:3d}  {v.min():7.2f} {np.median(v):7.2f} {v.max():7.2f}",
                   file=sys.stderr)
+
+
+def poll_summary(tr, ev, layer, us):
+    """Hand-off decomposition at each wait site of one layer (MK_TRACE_EVENTS
+    builds): from the producing phase's last store ('done' mark) to the
+    consumer's poll loop exits and its 'inputs ready' mark, with wave 0's poll
+    rounds.  Times in us relative to the last producer store."""
+    import numpy as np
+    classes = ["idle", "att+o", "qkv+gu", "gu+down", "down+o", "o", "qkv", "gu", "down"]
+    role = ev[16].astype(int) - 1
+    sites = [("x->qkv", 0, (layer - 1) * 5 + 4, layer * 5 + 0), ("qkv->attn", 1, layer * 5 + 0, layer * 5 + 1),
+             ("part->o", 2, layer * 5 + 1, layer * 5 + 2), ("x->gate_up", 3, layer * 5 + 2, layer * 5 + 3),
+             ("act->down", 4, layer * 5 + 3, layer * 5 + 4)]
+    print(f"# hand-off decomposition, layer {layer} (us after the last producer store; median / max over "
+          f"consumers):", file=sys.stderr)
+    for name, k, pslot, cslot in sites:
+        base = 17 + k * 10
+        enter, exits, rounds = ev[base], ev[base + 1:base + 9], ev[base + 9]
+        cons = enter > 0
+        pd = tr[pslot, 1]
+        pd = pd[pd > 0]
+        if not cons.any() or pd.size == 0:
+            continue
+        plast, pfirst, pmed = pd.max(), pd.min(), np.median(pd)
+        ex = np.where(exits[:, cons] > 0, exits[:, cons], np.nan)
+        ex_first, ex_last = np.nanmin(ex, axis=0), np.nanmax(ex, axis=0)
+        ready = tr[cslot, 0][cons]
+        rel = lambda v: (v - plast) * us
+        r = rounds[cons]
+        print(f"#   {name:10s} producers {pd.size:3d} (first {rel(pfirst):6.2f} median {rel(pmed):6.2f})  "
+              f"consumers {int(cons.sum()):3d}: enter {np.median(rel(enter[cons])):6.2f}  "
+              f"first wave out {np.median(rel(ex_first)):5.2f}/{rel(ex_first).max():5.2f}  "
+              f"last wave out {np.median(rel(ex_last)):5.2f}/{rel(ex_last).max():5.2f}  "
+              f"ready {np.median(rel(ready)):5.2f}/{rel(ready).max():5.2f}  "
+              f"rounds {np.median(r):4.0f}/{r.max():4.0f}", file=sys.stderr)
+        rc = role[cons]
+        for c in sorted(set(rc.tolist())):
+            m = rc == c
+            if c < 0 or m.sum() == len(rc):
+                continue
+            print(f"#      {classes[c] if c < len(classes) else c:8s} x{int(m.sum()):3d}: enter {np.median(rel(enter[cons][m])):6.2f}  "
+                  f"first wave out {np.median(rel(ex_first[m])):5.2f}  last wave out {np.median(rel(ex_last[m])):5.2f}/"
+                  f"{rel(ex_last[m]).max():5.2f}  ready {np.median(rel(ready[m])):5.2f}/{rel(ready[m]).max():5.2f}  "
+                  f"rounds {np.median(r[m]):4.0f}", file=sys.stderr)
 
 
 def calibrate_copy():

@@ -304,16 +304,15 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
 template <class S, int MODE, class BH>
 __device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const BH& rq, const NormIn<S>& gq,
                                         int t, int layer, int q, int tok, unsigned tg) {
-  float r;
   if (layer > 0) {
-    if (!fetch_norm<S>(p, p.x, tg - 1u, gq, sm.vec_q, sm.ssw[0], &r)) return false;
+    if (!fetch_norm<S>(p, p.x, tg - 1u, gq, sm.vec_q, sm.ssw[0], nullptr, ev_at(t, layer, PS_QKV))) return false;
   } else {
-    embed_norm<S>(p, tok, gq, sm.vec_q, sm.ssw[0], &r);
+    embed_norm<S>(p, tok, gq, sm.vec_q, sm.ssw[0], nullptr);
   }
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 0);
   blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
-  store_block(sm.red[RED_Q], p.qkv + q * 16, r * row_scale(rq), tg);
-  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 1);
+  store_block<true>(sm.red[RED_Q], p.qkv + q * 16, row_scale(rq), tg, sm.ssw[0], 1.0f / S::H);
+  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 1, PUB_WAVE);
   return true;
 }
 
@@ -321,12 +320,12 @@ __device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const BH& 
 template <class S, int MODE, class BH>
 __device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const BH& rg, const BH& ru,
                                        const NormIn<S>& gf, int t, int layer, int g, unsigned tg) {
-  float r;
-  if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], &r)) return false;
+  if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], nullptr, ev_at(t, layer, PS_GU))) return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 0);
   blk_mma2(rg, ru, sm.vec_g, sm.red[RED_G], sm.red[RED_U]);
-  store_block_gu(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, r, tag4(tg + 3u), row_scale(rg), row_scale(ru));
-  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 1);
+  store_block_gu<true>(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, 0.f, tag4(tg + 3u), row_scale(rg), row_scale(ru),
+                 sm.ssw[1], 1.0f / S::H);
+  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 1, PUB_WAVE);
   return true;
 }
 
@@ -335,13 +334,15 @@ __device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const BH& r
 template <class S, int MODE, class BF>
 __device__ __forceinline__ bool cls_down(const Params& p, Smem<S>& sm, const BF& rd, int t, int layer, int d,
                                          unsigned tg) {
-  if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x, d, tag4(tg + 2u), sm.vec_d, sm.xres_d)) return false;
+  if (!fetch_pk<S::F / 2>(p, p.act, tag4(tg + 3u), p.x, d, tag4(tg + 2u), sm.vec_d, sm.xres_d,
+                          ev_at(t, layer, PS_DN)))
+    return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 0);
   blk_mma(rd, sm.vec_d, sm.red[RED_D]);
   __syncthreads();
-  if (wave_id() == 0)
+  if (wave_id() == PUB_WAVE)
     down_rows<S>(p, sm, d, (MODE & 2) != 0 ? p.dbg_layers : nullptr, layer, tg + 4u, row_scale(rd));
-  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 1);
+  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 4, 1, PUB_WAVE);
   return true;
 }
 
@@ -353,17 +354,18 @@ __device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const BQ& ro
                                       int t, int layer, int o0, int o1, int nsplit, int tok, unsigned tg) {
   const unsigned tg_x = tg - 1u;
   if (!fetch_attn<S>(p, p.part, nsplit, tag4(tg + 1u), p.x, layer > 0 ? o0 : -1, o1, tag4(tg_x), sm.vec_o,
-                     sm.xres_o))
+                     sm.xres_o, ev_at(t, layer, PS_O)))
     return false;
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 0);
   if (o1 >= 0) blk_mma2(ro0, ro1, sm.vec_o, sm.red[RED_O0], sm.red[RED_O1]);
   else blk_mma(ro0, sm.vec_o, sm.red[RED_O0]);
   __syncthreads();
-  // wave 0: block o0, wave 1: block o1
+  // wave PUB_WAVE: block o0, the wave before it: block o1
   const int w_ = wave_id();
-  if (w_ == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, o0, layer, tok, tg + 2u, row_scale(ro0));
-  else if (w_ == 1 && o1 >= 0) o_rows<S>(p, sm.red[RED_O1], sm.xres_o + 16, o1, layer, tok, tg + 2u, row_scale(ro1));
-  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 1);
+  if (w_ == PUB_WAVE) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, o0, layer, tok, tg + 2u, row_scale(ro0));
+  else if (w_ == PUB_WAVE - 1 && o1 >= 0)
+    o_rows<S>(p, sm.red[RED_O1], sm.xres_o + 16, o1, layer, tok, tg + 2u, row_scale(ro1));
+  if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 1, PUB_WAVE);
   return true;
 }
 
@@ -529,7 +531,7 @@ __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int*
   }
   const unsigned per_token = (unsigned)(PHASES_PER_LAYER * p.n_layers + 1);
   for (int t = 0; t < p.n_tokens; ++t) {
-    if constexpr ((MODE & 2) != 0) trace_begin(p, t);
+    if constexpr ((MODE & 2) != 0) trace_begin(p, t, role ? role[RF_CLS] : CLS_IDLE);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
     if (!cls_token_start<S, MODE>(p, sm, t, tb, o0 >= 0, true, &tok)) return;
     const int pos = p.pos0 + t;
@@ -578,7 +580,7 @@ __device__ __forceinline__ void run_qg(const Params& p, Smem<S>& sm, const int* 
   int tok = p.first_token;
   const unsigned per_token = (unsigned)(PHASES_PER_LAYER * p.n_layers + 1);
   for (int t = 0; t < p.n_tokens; ++t) {
-    if constexpr ((MODE & 2) != 0) trace_begin(p, t);
+    if constexpr ((MODE & 2) != 0) trace_begin(p, t, role ? role[RF_CLS] : CLS_IDLE);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
     if (!cls_token_start<S, MODE>(p, sm, t, tb, HAS_Q, false, &tok)) return;
     for (int layer = 0; layer < p.n_layers; ++layer) {
@@ -623,7 +625,7 @@ __device__ __forceinline__ void run_down(const Params& p, Smem<S>& sm, const int
   int tok = p.first_token;
   const unsigned per_token = (unsigned)(PHASES_PER_LAYER * p.n_layers + 1);
   for (int t = 0; t < p.n_tokens; ++t) {
-    if constexpr ((MODE & 2) != 0) trace_begin(p, t);
+    if constexpr ((MODE & 2) != 0) trace_begin(p, t, role ? role[RF_CLS] : CLS_IDLE);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
     if (!cls_token_start<S, MODE>(p, sm, t, tb, PARTNER == CLS_DO, false, &tok)) return;
     const int nsplit = split_count(p.pos0 + t + 1, p.chunk_min, p.nsplit_max);
@@ -667,7 +669,7 @@ __device__ __forceinline__ void run_o(const Params& p, Smem<S>& sm, const int* r
   int tok = p.first_token;
   const unsigned per_token = (unsigned)(PHASES_PER_LAYER * p.n_layers + 1);
   for (int t = 0; t < p.n_tokens; ++t) {
-    if constexpr ((MODE & 2) != 0) trace_begin(p, t);
+    if constexpr ((MODE & 2) != 0) trace_begin(p, t, role ? role[RF_CLS] : CLS_IDLE);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
     if (!cls_token_start<S, MODE>(p, sm, t, tb, true, false, &tok)) return;
     const int nsplit = split_count(p.pos0 + t + 1, p.chunk_min, p.nsplit_max);
@@ -695,7 +697,7 @@ __device__ __forceinline__ void run_idle(const Params& p, Smem<S>& sm) {
   int tok = p.first_token;
   const unsigned per_token = (unsigned)(PHASES_PER_LAYER * p.n_layers + 1);
   for (int t = 0; t < p.n_tokens; ++t) {
-    if constexpr ((MODE & 2) != 0) trace_begin(p, t);
+    if constexpr ((MODE & 2) != 0) trace_begin(p, t, CLS_IDLE);
     const unsigned tb = p.tag_base + (unsigned)t * per_token;
     if (!cls_token_start<S, MODE>(p, sm, t, tb, false, false, &tok)) return;
     LmWarm lw;

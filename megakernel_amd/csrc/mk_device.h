@@ -77,20 +77,43 @@ __device__ __forceinline__ float dot8(u32x4 w, const float* h, float acc) {
 // 32-byte group, the group's 4 dwords of hi pairs (columns 2i, 2i+1 in the
 // low / high half) then its 4 of lo pairs -- one 16-byte load per part and
 // 8 columns, and the same 4-byte slot count as an fp32 vector.
+// Split-bf16 parts of two values by the hardware conversion (gfx950
+// v_cvt_pk_bf16_f32, round to nearest even): hi holds RNE(a) in its low half
+// and RNE(b) in its high half, lo the same for a - hi(a), b - hi(b) (exact
+// differences).  Three conversions' worth of work in two instructions plus
+// the differences, where the bit-twiddled RNE took about ten per value.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bf16_hilo2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+  const float ha = __uint_as_float(hi << 16), hb = __uint_as_float(hi & 0xffff0000u);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a - ha, b - hb}, bf16x2_t));
+}
 __device__ __forceinline__ void xs_put(uint32_t* xs, int e, float v) {
   uint16_t* h = reinterpret_cast<uint16_t*>(xs);
   const int g = e >> 3, j = e & 7;
-  const uint16_t hv = f32_to_bf16(v);
-  h[(g * 8 + (j >> 1)) * 2 + (j & 1)] = hv;
-  h[(g * 8 + 4 + (j >> 1)) * 2 + (j & 1)] = f32_to_bf16(v - bf16_to_f32(hv));
+  uint32_t hi, lo;
+  bf16_hilo2(v, 0.f, hi, lo);
+  h[(g * 8 + (j >> 1)) * 2 + (j & 1)] = (uint16_t)hi;
+  h[(g * 8 + 4 + (j >> 1)) * 2 + (j & 1)] = (uint16_t)lo;
 }
 // columns e, e + 1 (e even): one dword of each part
 __device__ __forceinline__ void xs_put_pair(uint32_t* xs, int e, float a, float b) {
   const int g = e >> 3, i = (e & 7) >> 1;
-  const uint16_t ha = f32_to_bf16(a), hb = f32_to_bf16(b);
-  xs[g * 8 + i] = (uint32_t)ha | ((uint32_t)hb << 16);
-  xs[g * 8 + 4 + i] =
-      (uint32_t)f32_to_bf16(a - bf16_to_f32(ha)) | ((uint32_t)f32_to_bf16(b - bf16_to_f32(hb)) << 16);
+  uint32_t hi, lo;
+  bf16_hilo2(a, b, hi, lo);
+  xs[g * 8 + i] = hi;
+  xs[g * 8 + 4 + i] = lo;
+}
+// columns e .. e + 3 (e a multiple of 4): two dwords of each part, one 8-byte
+// LDS store per part
+__device__ __forceinline__ void xs_put_quad(uint32_t* xs, int e, float a, float b, float c, float d) {
+  const int g = e >> 3, i = (e & 7) >> 1;
+  uint32_t h0, l0, h1, l1;
+  bf16_hilo2(a, b, h0, l0);
+  bf16_hilo2(c, d, h1, l1);
+  *reinterpret_cast<u32x2*>(xs + g * 8 + i) = u32x2{h0, h1};
+  *reinterpret_cast<u32x2*>(xs + g * 8 + 4 + i) = u32x2{l0, l1};
 }
 // 16 FP8 (OCP e4m3) weights against 16 fp32 inputs: the hardware converts two
 // bytes per instruction (bytes 0-1 / 2-3 of each dword, in order).
@@ -377,13 +400,20 @@ __device__ __forceinline__ bool pk2_ready(u32x4 q, unsigned t4) {
 
 // Bounded spinning of one thread.  step() returns false when the wait must be
 // abandoned (this thread timed out, or another workgroup already failed).
+// Pause between poll rounds (s_sleep units of 64 clocks).  No pause measured
+// fastest: 1 / 4 / 12 units gave 2,893 / 2,811 / 2,662 tok/s at ctx 1024, and
+// 0 is 0.3 % above 1 -- a hand-off is bound by its detection latency, not by
+// the L2 bandwidth the polls take.
+#ifndef MK_SPIN_SLEEP
+#define MK_SPIN_SLEEP 0
+#endif
 struct Spin {
   u64 t0 = 0;
   unsigned n = 0;
   __device__ __forceinline__ bool step(int* err, u64 timeout_ticks) {
     if (n == 0) t0 = wall_clock64();
     ++n;
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(MK_SPIN_SLEEP);
     if ((n & 1023u) == 0) {
       if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != MK_OK) return false;
       if (wall_clock64() - t0 > timeout_ticks) {

@@ -116,7 +116,7 @@ struct Smem {
   float vec_d[S::F];                  // down: SiLU(gate) * up
   float vec_l[S::H];                  // LM head: x * final_norm gain (fp32)
   float xres_o[32], xres_d[16];       // residual rows of this workgroup's O block(s) / down block
-  float ssw[3][NW];                   // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
+  __attribute__((aligned(16))) float ssw[3][NW];  // RMSNorm sum-of-squares partials (QKV, gate/up, LM head)
   float red[RED_N][NW * 16];          // block products: each wave's share of the 16 row sums (blk_mma)
   __attribute__((aligned(16))) uint16_t qb[16][S::D];  // attention: q parts, score A operand
   __attribute__((aligned(16))) uint16_t pb[NW][16][32 * KVB];  // attention: weight parts, output A operand
@@ -144,8 +144,18 @@ __shared__ int wg_abort;
 __device__ __forceinline__ bool block_failed(int failed) {
   if (failed) wg_abort = 1;
   __syncthreads();
-  return *static_cast<volatile int*>(&wg_abort) != 0;
+  // an LDS read (ds_read): a volatile access compiles to a flat load, which
+  // also waits for every outstanding global load and store of the wave
+  return __hip_atomic_load(&wg_abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
 }
+
+// The wave that runs the one-wave epilogues and publishes a block's results.
+// Stores and loads retire in issue order (one vmcnt counter on gfx9-class
+// CUs), so a wave that polls right after its own write-through publish waits
+// for that store's acknowledgement in its first round; the waits that can
+// follow a publish of the same workgroup directly (act -> down after gate/up)
+// poll with the other waves.
+constexpr int PUB_WAVE = NW - 1;
 
 // Poll a set of tagged words until they are ready, then consume them:
 // issue(w) loads every word of one round into w (all loads before any test:
@@ -163,6 +173,82 @@ __device__ __forceinline__ bool poll_rounds(const Params& p, Issue issue, Ready 
     }
     if (!sp.step(p.err, p.timeout_ticks)) return false;
   }
+}
+
+// Phase trace of one token (profiling only).  Timestamps go to an LDS buffer
+// and are written out once at the end of the traced token, so recording them
+// adds no global stores (and no store waits) inside the phases being timed.
+constexpr int TRACE_MAX_LAYERS = 48;
+// Poll-level events of the traced layer, per wait site: when wave 0 of a
+// consumer entered the wait, when each of its waves left its poll loop and
+// how many rounds wave 0 polled (EVP_PER slots per site after the EVT events).
+enum PollSite : int { PS_QKV = 0, PS_ATT, PS_O, PS_GU, PS_DN, PS_N };
+constexpr int EV_ROLE = 16;  // the workgroup's role class (class kernel), one slot
+constexpr int EVP_BASE = 17, EVP_PER = NW + 2;
+constexpr int EVT_N = EVP_BASE + PS_N * EVP_PER;
+constexpr int TRACE_LDS = (5 * TRACE_MAX_LAYERS + 1) * 2 + EVT_N;
+__shared__ u64 trace_lds[TRACE_LDS];
+
+__device__ __forceinline__ bool tracing(const Params& p, int t) { return p.trace && t == p.trace_token; }
+
+
+__device__ __forceinline__ void trace_mark(const Params& p, int t, int slot, int which, int wave = 0) {
+  if (tracing(p, t) && ltid() == wave * kWave) trace_lds[slot * 2 + which] = wall_clock64();
+}
+
+// Fine-grained events of one layer of the traced token.
+enum Evt : int {
+  EV_ATT_READY = 0, EV_ATT_ROPE, EV_ATT_SOFTMAX, EV_ATT_STORED,
+  EV_ATT_PARTIAL, EV_ATT_GATHERED, EV_O_READY, EV_O_STORED,
+  EV_QKV_STORED, EV_GU_STORED, EV_DN_STORED, EV_DN_READY,
+  EV_ATT_REDUCED, EV_ATT_COMBINED, EV_MERGE_SCALED, EV_MERGE_DONE
+};
+#ifndef MK_TRACE_EVENTS
+#define MK_TRACE_EVENTS 0  // fine-grained events of one layer (investigation builds only)
+#endif
+__device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
+  if (MK_TRACE_EVENTS && tracing(p, t) && layer == p.trace_layer && ltid() == 0)
+    trace_lds[(5 * p.n_layers + 1) * 2 + e] = wall_clock64();
+}
+
+// A wait site of the traced token and layer (site < 0: not recorded).
+struct EvPoll {
+  int t = -1, layer = -1, site = -1;
+};
+__device__ __forceinline__ EvPoll ev_at(int t, int layer, int site) {
+  EvPoll e;
+  if (MK_TRACE_EVENTS) e.t = t, e.layer = layer, e.site = site;
+  return e;
+}
+__device__ __forceinline__ bool ev_on(const Params& p, const EvPoll& e) {
+  return MK_TRACE_EVENTS && e.site >= 0 && tracing(p, e.t) && e.layer == p.trace_layer;
+}
+// wave 0 enters the wait (thread 0)
+__device__ __forceinline__ void evp_enter(const Params& p, const EvPoll& e) {
+  if (ev_on(p, e) && ltid() == 0)
+    trace_lds[(5 * p.n_layers + 1) * 2 + EVP_BASE + e.site * EVP_PER] = wall_clock64();
+}
+// a wave leaves its poll loop (its lane 0); thread 0 also records its rounds
+__device__ __forceinline__ void evp_exit(const Params& p, const EvPoll& e, unsigned rounds) {
+  if (!ev_on(p, e)) return;
+  const int base = (5 * p.n_layers + 1) * 2 + EVP_BASE + e.site * EVP_PER;
+  if ((ltid() & (kWave - 1)) == 0) trace_lds[base + 1 + wave_id()] = wall_clock64();
+  if (ltid() == 0) trace_lds[base + 1 + NW] = rounds;
+}
+
+// Clear before the traced token; write out after it ([entry][G] layout).
+// role: the workgroup's role class + 1 (0: none recorded).
+__device__ __forceinline__ void trace_begin(const Params& p, int t, int role = -1) {
+  if (!tracing(p, t)) return;
+  for (int i = ltid(); i < TRACE_LDS; i += NT) trace_lds[i] = 0ull;
+  __syncthreads();
+  if (ltid() == 0) trace_lds[(5 * p.n_layers + 1) * 2 + EV_ROLE] = (u64)(role + 1);
+}
+__device__ __forceinline__ void trace_end(const Params& p, int t) {
+  if (!tracing(p, t)) return;
+  __syncthreads();
+  const int n = (5 * p.n_layers + 1) * 2 + EVT_N;
+  for (int i = ltid(); i < n; i += NT) p.trace[(long long)i * gridDim.x + blockIdx.x] = trace_lds[i];
 }
 
 // ------------------------------------------------------------------ GEMV
@@ -320,25 +406,47 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
-// Epilogues, one barrier each, run by wave 0 (lane l: row l >> 2).
-// QKV block: the 16 rows times `scale`, full tagged words.
-__device__ __forceinline__ void store_block(const float* red, u64* dst16, float scale, unsigned tag) {
+// RMSNorm scale rsqrt(mean(x^2) + eps) from the NW wave partials of the sum
+// of squares (a fixed summation tree, so every caller gets identical bits).
+static_assert(NW == 8, "norm_scale sums eight wave partials");
+__device__ __forceinline__ float norm_scale(const float* ssw, float inv_h) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(ssw), b = *reinterpret_cast<const f32x4*>(ssw + 4);
+  const float tot = ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
+  return __builtin_amdgcn_rsqf(fmaf(tot, inv_h, kRmsEps));
+}
+
+// Epilogues, one barrier each, run by wave PUB_WAVE (lane l: row l >> 2).
+// With ssw set, the rows are also scaled by norm_scale(ssw, inv_h): the
+// wave partials of the input's sum of squares are read with the block shares,
+// so the norm costs the critical path no LDS round trip of its own.
+// QKV block: the 16 rows times `scale`, full tagged words.  NORM (ssw set):
+// the norm scale is taken here; its LDS reads issue with the shares' reads
+// (one round trip, not two).
+template <bool NORM = false>
+__device__ __forceinline__ void store_block(const float* red, u64* dst16, float scale, unsigned tag,
+                                            const float* ssw = nullptr, float inv_h = 0.f) {
   __syncthreads();
-  if (wave_id() == 0) {
+  if (wave_id() == PUB_WAVE) {
     const unsigned l = lane_id();
-    const float y = red_row4(red, l) * scale;
+    const float sh = red_row4(red, l);
+    const float s = NORM ? scale * norm_scale(ssw, inv_h) : scale;
+    const float y = sh * s;
     if ((l & 3u) == 0u) ll_put(dst16 + (l >> 2), ll_pack(y, tag));
   }
 }
 
 // Gate/up pair: SiLU(g r) * (u r) of the 16 rows (gate shares in rg, up
-// shares in ru), published as 8 packed-pair words.
+// shares in ru), published as 8 packed-pair words.  NORM: r = norm_scale(ssw).
+template <bool NORM = false>
 __device__ __forceinline__ void store_block_gu(const float* rg, const float* ru, u64* dst8, float r, unsigned t4,
-                                               float sg = 1.0f, float su = 1.0f) {
+                                               float sg = 1.0f, float su = 1.0f, const float* ssw = nullptr,
+                                               float inv_h = 0.f) {
   __syncthreads();
-  if (wave_id() == 0) {
+  if (wave_id() == PUB_WAVE) {
     const unsigned l = lane_id();
-    const float a = silu_mul(red_row4(rg, l) * (r * sg), red_row4(ru, l) * (r * su));
+    const float g = red_row4(rg, l), u = red_row4(ru, l);
+    const float rr = NORM ? norm_scale(ssw, inv_h) : r;
+    const float a = silu_mul(g * (rr * sg), u * (rr * su));
     const float b = dpp_sel<DPP_ROW_SHL4>(a);  // the next row
     if ((l & 7u) == 0u) ll_put(dst8 + (l >> 3), pk_pack(a, b, t4));
   }
@@ -385,18 +493,16 @@ __device__ __forceinline__ void gains_load(NormIn<S>& n, const uint16_t* gain) {
   }
 }
 
-// Block-wide sum of squares from per-thread partials -> r.  ssw: NW floats
-// used only by this call site (so no wave can overwrite a slot another wave
-// of a previous call still reads).
+// Block-wide sum of squares from per-thread partials -> r (unless r is null:
+// the epilogue then takes norm_scale(ssw) itself).  ssw: NW floats used only
+// by this call site (so no wave can overwrite a slot another wave of a
+// previous call still reads).
 __device__ __forceinline__ bool norm_finish(float ss, float* ssw, int failed, float h, float* r) {
   const int t_ = ltid();
   ss = wave_sum(ss);
   if (t_ % kWave == 0) ssw[t_ / kWave] = ss;
   if (block_failed(failed)) return false;
-  float tot = 0.f;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) tot += ssw[i];
-  *r = rsqrtf(tot / h + kRmsEps);
+  if (r) *r = norm_scale(ssw, 1.0f / h);
   return true;
 }
 
@@ -405,8 +511,7 @@ __device__ __forceinline__ bool norm_finish(float ss, float* ssw, int failed, fl
 template <bool SPLIT>
 __device__ __forceinline__ void put_quad(float* dst, int q, const float (&v)[4], const float* g) {
   if constexpr (SPLIT) {
-    xs_put_pair(reinterpret_cast<uint32_t*>(dst), 4 * q, v[0] * g[0], v[1] * g[1]);
-    xs_put_pair(reinterpret_cast<uint32_t*>(dst), 4 * q + 2, v[2] * g[2], v[3] * g[3]);
+    xs_put_quad(reinterpret_cast<uint32_t*>(dst), 4 * q, v[0] * g[0], v[1] * g[1], v[2] * g[2], v[3] * g[3]);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[4 * q + e] = v[e] * g[e];
@@ -414,45 +519,52 @@ __device__ __forceinline__ void put_quad(float* dst, int q, const float (&v)[4],
 }
 
 // Wait for the packed-pair H-vector x of tag `tag` (one bulk round of 16-byte
-// loads), store x * gain to dst and return the RMSNorm scale of x.
+// loads), store x * gain to dst and the wave partials of its sum of squares
+// to ssw, and return the RMSNorm scale of x in r (r null: left to the
+// epilogue, norm_scale(ssw)).  Only the threads that own element quads poll
+// (whole waves); the others go straight to the barrier.
 template <class S, bool SPLIT = true>
 __device__ __forceinline__ bool fetch_norm(const Params& p, const u64* src, unsigned tag, const NormIn<S>& n,
-                                           float* dst, float* ssw, float* r) {
+                                           float* dst, float* ssw, float* r, EvPoll ev = EvPoll()) {
   constexpr int PQ = NormIn<S>::PQ, NQ = NormIn<S>::NQ;
   const int tid = ltid();
   const unsigned t4 = tag4(tag);
   const auto rs = make_rsrc(src);
   int failed = 0;
+  float ss = 0.f;
   __syncthreads();  // every wave is done with the LDS of its previous phase
-  u32x4 wv[PQ];
-  Spin sp;
-  while (true) {
-    asm volatile("" ::: "memory");
-    // every load is issued before any is tested (one round trip per poll
-    // round); quads past the vector re-read its last quad
+  evp_enter(p, ev);
+  if (tid < NQ) {
+    u32x4 wv[PQ];
+    Spin sp;
+    while (true) {
+      asm volatile("" ::: "memory");
+      // every load is issued before any is tested (one round trip per poll
+      // round); quads past the vector re-read its last quad
+#pragma unroll
+      for (int k = 0; k < PQ; ++k) {
+        const int q = tid + k * NT;
+        wv[k] = pk_get2(rs, (unsigned)(q < NQ ? q : NQ - 1) * 16u);
+      }
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < PQ; ++k) ready &= tid + k * NT >= NQ || pk2_ready(wv[k], t4);
+      if (ready) break;
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    }
+    evp_exit(p, ev, sp.n + 1);
 #pragma unroll
     for (int k = 0; k < PQ; ++k) {
       const int q = tid + k * NT;
-      wv[k] = pk_get2(rs, (unsigned)(q < NQ ? q : NQ - 1) * 16u);
-    }
-    bool ready = true;
+      if (q < NQ) {
+        const float v[4] = {pkv(wv[k].x), pkv(wv[k].y), pkv(wv[k].z), pkv(wv[k].w)};
 #pragma unroll
-    for (int k = 0; k < PQ; ++k) ready &= tid + k * NT >= NQ || pk2_ready(wv[k], t4);
-    if (ready) break;
-    if (!sp.step(p.err, p.timeout_ticks)) {
-      failed = 1;
-      break;
-    }
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < PQ; ++k) {
-    const int q = tid + k * NT;
-    if (q < NQ) {
-      const float v[4] = {pkv(wv[k].x), pkv(wv[k].y), pkv(wv[k].z), pkv(wv[k].w)};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
-      put_quad<SPLIT>(dst, q, v, n.g + 4 * k);
+        for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
+        put_quad<SPLIT>(dst, q, v, n.g + 4 * k);
+      }
     }
   }
   return norm_finish(ss, ssw, failed, (float)S::H, r);
@@ -462,38 +574,45 @@ __device__ __forceinline__ bool fetch_norm(const Params& p, const u64* src, unsi
 // unless xblk < 0, the 16 residual rows of block xblk of x (8 packed words,
 // tag xt4, threads 0..7), in one bulk round of 8-byte loads (hot lines that
 // many workgroups poll: 16-byte loads made these rounds slower, not faster).
+// (Leaving the publishing wave out of this poll, so that its own store's
+// acknowledgement cannot hold up a round, measured no faster: 2,927 vs 2,934.)
 template <int NPK>
 __device__ __forceinline__ bool fetch_pk(const Params& p, const u64* src, unsigned t4, const u64* x, int xblk,
-                                          unsigned xt4, float* dst, float* xres) {
-  constexpr int PER = (NPK + NT - 1) / NT;
+                                          unsigned xt4, float* dst, float* xres, EvPoll ev = EvPoll()) {
+  constexpr int NPT = NT;  // polling threads
+  constexpr int PER = (NPK + NPT - 1) / NPT;
   const int tid = ltid();
   const bool want_x = xblk >= 0 && tid < 8;
   int failed = 0;
   __syncthreads();
-  u64 wv[PER], wx = 0ull;
-  Spin sp;
-  while (true) {
+  evp_enter(p, ev);
+  if (tid < NPT) {
+    u64 wv[PER], wx = 0ull;
+    Spin sp;
+    while (true) {
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        const int i = tid + k * NPT;
+        wv[k] = ll_get(const_cast<u64*>(src) + (i < NPK ? i : NPK - 1));
+      }
+      if (want_x) wx = ll_get(const_cast<u64*>(x) + xblk * 8 + tid);
+      bool ready = !want_x || pk_ready(wx, xt4);
+#pragma unroll
+      for (int k = 0; k < PER; ++k) ready &= tid + k * NPT >= NPK || pk_ready(wv[k], t4);
+      if (ready) break;
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    }
+    evp_exit(p, ev, sp.n + 1);
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      const int i = tid + k * NT;
-      wv[k] = ll_get(const_cast<u64*>(src) + (i < NPK ? i : NPK - 1));
+      const int i = tid + k * NPT;
+      if (i < NPK) xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * i, pk_lo(wv[k]), pk_hi(wv[k]));
     }
-    if (want_x) wx = ll_get(const_cast<u64*>(x) + xblk * 8 + tid);
-    bool ready = !want_x || pk_ready(wx, xt4);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) ready &= tid + k * NT >= NPK || pk_ready(wv[k], t4);
-    if (ready) break;
-    if (!sp.step(p.err, p.timeout_ticks)) {
-      failed = 1;
-      break;
-    }
+    if (want_x) xres[2 * tid] = pk_lo(wx), xres[2 * tid + 1] = pk_hi(wx);
   }
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = tid + k * NT;
-    if (i < NPK) xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * i, pk_lo(wv[k]), pk_hi(wv[k]));
-  }
-  if (want_x) xres[2 * tid] = pk_lo(wx), xres[2 * tid + 1] = pk_hi(wx);
   return !block_failed(failed);
 }
 
@@ -593,49 +712,6 @@ __device__ __forceinline__ void down_rows(const Params& p, Smem<S>& sm, int blk,
 
 // Work item i of a phase runs on workgroup (i + off) mod G.
 __device__ __forceinline__ int first_item(int wg, int off, int G) { return (wg + G - (off % G)) % G; }
-
-// Phase trace of one token (profiling only).  Timestamps go to an LDS buffer
-// and are written out once at the end of the traced token, so recording them
-// adds no global stores (and no store waits) inside the phases being timed.
-constexpr int TRACE_MAX_LAYERS = 48;
-constexpr int EVT_N = 16;
-constexpr int TRACE_LDS = (5 * TRACE_MAX_LAYERS + 1) * 2 + EVT_N;
-__shared__ u64 trace_lds[TRACE_LDS];
-
-__device__ __forceinline__ bool tracing(const Params& p, int t) { return p.trace && t == p.trace_token; }
-
-
-__device__ __forceinline__ void trace_mark(const Params& p, int t, int slot, int which) {
-  if (tracing(p, t) && ltid() == 0) trace_lds[slot * 2 + which] = wall_clock64();
-}
-
-// Fine-grained events of one layer of the traced token.
-enum Evt : int {
-  EV_ATT_READY = 0, EV_ATT_ROPE, EV_ATT_SOFTMAX, EV_ATT_STORED,
-  EV_ATT_PARTIAL, EV_ATT_GATHERED, EV_O_READY, EV_O_STORED,
-  EV_QKV_STORED, EV_GU_STORED, EV_DN_STORED, EV_DN_READY,
-  EV_ATT_REDUCED, EV_ATT_COMBINED, EV_MERGE_SCALED, EV_MERGE_DONE
-};
-#ifndef MK_TRACE_EVENTS
-#define MK_TRACE_EVENTS 0  // fine-grained events of one layer (investigation builds only)
-#endif
-__device__ __forceinline__ void evt(const Params& p, int t, int layer, int e) {
-  if (MK_TRACE_EVENTS && tracing(p, t) && layer == p.trace_layer && ltid() == 0)
-    trace_lds[(5 * p.n_layers + 1) * 2 + e] = wall_clock64();
-}
-
-// Clear before the traced token; write out after it ([entry][G] layout).
-__device__ __forceinline__ void trace_begin(const Params& p, int t) {
-  if (!tracing(p, t)) return;
-  for (int i = ltid(); i < TRACE_LDS; i += NT) trace_lds[i] = 0ull;
-  __syncthreads();
-}
-__device__ __forceinline__ void trace_end(const Params& p, int t) {
-  if (!tracing(p, t)) return;
-  __syncthreads();
-  const int n = (5 * p.n_layers + 1) * 2 + EVT_N;
-  for (int i = ltid(); i < n; i += NT) p.trace[(long long)i * gridDim.x + blockIdx.x] = trace_lds[i];
-}
 
 // ------------------------------------------------------------ attention
 // KV cache on the device (the C ABI's set/get convert from/to the reference's
@@ -854,6 +930,8 @@ __device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm,
 #pragma unroll
   for (int c = 0; c < DPL; ++c) v[c] = 0.f;
   __syncthreads();  // every wave is done with the LDS of its previous phase
+  const EvPoll ev = ev_at(tt, layer, PS_ATT);
+  evp_enter(p, ev);
   if (w < GQA + 2) {
     u64* src = p.qkv + (w < GQA ? (g * GQA + w) * D : (w == GQA ? S::QD + g * D : S::QD + S::KVD + g * D));
     Spin sp;
@@ -875,6 +953,7 @@ __device__ __forceinline__ bool attention_prologue(const Params& p, Smem<S>& sm,
         break;
       }
     }
+    evp_exit(p, ev, sp.n + 1);
   }
   if constexpr ((MODE & 2) != 0) trace_mark(p, tt, PHASES_PER_LAYER * layer + 1, 0);
   evt(p, tt, layer, EV_ATT_READY);
@@ -1016,13 +1095,17 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S, (MODE & 8)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
+        // a block past the item (the wave has fewer blocks than KVB) is all
+        // -inf below: its products are skipped (a wave-uniform branch)
+        if (bi + q * NW < nb) {
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          u32x4 kb;  // FP8: a lane's 8 values share one position, so its K scale enters here
-          if constexpr (K8) kb = fp8x8_to_bf16x8_scaled(kvr.k[q][h][kc], kvr.sk[q][h]);
-          else kb = kvr.k[q][h][kc];
-          d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[kc]),
-                                                      __builtin_bit_cast(bf16x8, kb), d4, 0, 0, 0);
+          for (int kc = 0; kc < KC; ++kc) {
+            u32x4 kb;  // FP8: a lane's 8 values share one position, so its K scale enters here
+            if constexpr (K8) kb = fp8x8_to_bf16x8_scaled(kvr.k[q][h][kc], kvr.sk[q][h]);
+            else kb = kvr.k[q][h][kc];
+            d4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[kc]),
+                                                        __builtin_bit_cast(bf16x8, kb), d4, 0, 0, 0);
+          }
         }
         const float v = (d4[0] + d4[1]) + d4[2];
         const int t = 32 * (b0 + bi + q * NW) + 16 * h + c16;
@@ -1066,13 +1149,14 @@ __device__ bool attention_compute(const Params& p, Smem<S>& sm, KV<S, (MODE & 8)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
 #pragma unroll
-      for (int q = 0; q < KVB; ++q)
-      {
-        u32x4 vb;
-        if constexpr (K8) vb = fp8x8_to_bf16x8_scaled(kvr.v[q][dt], 1.0f);  // V scales ride on the weights
-        else vb = kvr.v[q][dt];
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa[q]),
-                                                         __builtin_bit_cast(bf16x8, vb), acc[dt], 0, 0, 0);
+      for (int q = 0; q < KVB; ++q) {
+        if (bi + q * NW < nb) {  // a skipped block has weight 0: no product
+          u32x4 vb;
+          if constexpr (K8) vb = fp8x8_to_bf16x8_scaled(kvr.v[q][dt], 1.0f);  // V scales ride on the weights
+          else vb = kvr.v[q][dt];
+          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa[q]),
+                                                           __builtin_bit_cast(bf16x8, vb), acc[dt], 0, 0, 0);
+        }
       }
     }
   }
@@ -1204,7 +1288,8 @@ __device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit,
 // owns output pairs t + k NT (8-byte loads, as fetch_pk).
 template <class S>
 __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
-                                            int xb0, int xb1, unsigned xt4, float* dst, float* xres) {
+                                            int xb0, int xb1, unsigned xt4, float* dst, float* xres,
+                                            EvPoll ev = EvPoll()) {
   constexpr int NPG = S::GQA * S::D / 2;
   constexpr int WP = part_words<S>();
   constexpr int PPT = (S::QD / 2 + NT - 1) / NT;
@@ -1216,6 +1301,8 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
   float M[PPT], L[PPT], o0[PPT], o1[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) M[k] = -INFINITY, L[k] = 0.f, o0[k] = 0.f, o1[k] = 0.f;
+  evp_enter(p, ev);
+  unsigned rounds = 0;
   for (int s0 = 0; s0 < nsplit && !failed; s0 += SB) {
     u64 wa[PPT][SB], wm[PPT][SB], wx = 0ull;
     const bool want_x = s0 == 0 && want_x0;
@@ -1249,6 +1336,7 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
         break;
       }
     }
+    rounds += sp.n + 1;
     if (want_x) xres[2 * tid] = pk_lo(wx), xres[2 * tid + 1] = pk_hi(wx);
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
@@ -1271,8 +1359,12 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
     const int pi = tid + k * NT;
-    if (pi < S::QD / 2) xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * pi, o0[k] / L[k], o1[k] / L[k]);
+    if (pi < S::QD / 2) {
+      const float il = __builtin_amdgcn_rcpf(L[k]);  // one reciprocal (~1 ulp) for both outputs
+      xs_put_pair(reinterpret_cast<uint32_t*>(dst), 2 * pi, o0[k] * il, o1[k] * il);
+    }
   }
+  evp_exit(p, ev, rounds);
   return !block_failed(failed);
 }
 
@@ -1473,7 +1565,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         evt(p, t, layer, EV_O_READY);
         blk_mma(ro, sm.vec_o, sm.red[RED_O0]);
         __syncthreads();
-        if (wave_id() == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, it_o, layer, tok, tg + 2u);
+        if (wave_id() == PUB_WAVE) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, it_o, layer, tok, tg + 2u);
         evt(p, t, layer, EV_O_STORED);
         if constexpr (DBG) trace_mark(p, t, slot + 2, 1);
       }
@@ -1483,7 +1575,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         __syncthreads();  // the previous block's shares are summed
         blk_mma(ro, sm.vec_o, sm.red[RED_O0]);
         __syncthreads();
-        if (wave_id() == 0) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, rb, layer, tok, tg + 2u);
+        if (wave_id() == PUB_WAVE) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, rb, layer, tok, tg + 2u);
       }
       if (kv_at == 3) prefetch_kv();
       // ---------------- P4: gate/up + SiLU (prefetch: down)
@@ -1523,7 +1615,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         evt(p, t, layer, EV_DN_READY);
         blk_mma(rd, sm.vec_d, sm.red[RED_D]);
         __syncthreads();
-        if (wave_id() == 0) down_rows<S>(p, sm, it_dn, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
+        if (wave_id() == PUB_WAVE) down_rows<S>(p, sm, it_dn, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
         evt(p, t, layer, EV_DN_STORED);
         if constexpr (DBG) trace_mark(p, t, slot + 4, 1);
       }
@@ -1533,7 +1625,7 @@ __global__ __launch_bounds__(NT) void decode_kernel(Params p) {
         __syncthreads();  // the previous block's shares are summed
         blk_mma(rd, sm.vec_d, sm.red[RED_D]);
         __syncthreads();
-        if (wave_id() == 0) down_rows<S>(p, sm, rb, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
+        if (wave_id() == PUB_WAVE) down_rows<S>(p, sm, rb, DBG ? p.dbg_layers : nullptr, layer, tg + 4u);
       }
       if (kv_at == 5) prefetch_kv();
     }
