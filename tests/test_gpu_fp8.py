@@ -457,3 +457,38 @@ def test_screened_lmhead_tokens_equal_bf16_head(name, ctx):
     finally:
         eng.close()
         dw.free()
+
+
+def test_screened_threshold_words_never_alias():
+    """The screened LM head's threshold words (second half of the argmax
+    slots) are written only by screened launches; launches with the bf16 head
+    in between advance the phase tags.  Here the gap is chosen so that a
+    14-bit tag would repeat: a screened launch of 8 tokens (TINY: 11 phases
+    per token; its last writes per slot parity are tokens 6 and 7), 8 + 16,373
+    tokens with the bf16 head, then a screened launch whose first two tokens
+    sit 11 * 16,383 phases after those writes.  The words carry the full
+    32-bit tag, so the screened launch waits for its own thresholds and its
+    tokens equal the bf16 head's."""
+    from megakernel_amd import _lib
+    eng, orc, dw = make_pair(TINY, 29, 4200, gain_std=0.0)
+    try:
+        eng.set_lmhead_fp8(_lib.LMHEAD_SCREENED)
+        eng.set_pos(0)
+        first = eng.decode_many(5, 8)  # writes the threshold words
+        eng.set_lmhead_fp8(_lib.LMHEAD_BF16)
+        eng.set_pos(0)
+        ref = eng.decode_many(3, 8)
+        left = 16373
+        while left:
+            n = min(left, 4000)
+            eng.set_pos(0)
+            eng.decode_many(7, n)
+            left -= n
+        eng.set_lmhead_fp8(_lib.LMHEAD_SCREENED)
+        eng.set_pos(0)
+        got = eng.decode_many(3, 8)
+        _print(f"screened after 16,381 bf16-head tokens: {got} / bf16 {ref} (first launch {first[:4]})")
+        assert got == ref
+    finally:
+        eng.close()
+        dw.free()
