@@ -367,6 +367,11 @@ def bench_batch(args):
         "config": {"workload": f"Qwen3-0.6B-shaped batched decode, {B} sequences, KV lengths {lengths}, "
                                f"{K} steps (BASELINE configs[4])", "sequences": B, "kv_lengths": lengths,
                    "step": args.batch_step,
+                   "accumulation": "fp32",
+                   "activations": "fp32 residual streams; GEMM inputs (x * gain, the merged attention output, "
+                                  "SiLU(gate)*up) are published as hi + lo bf16 parts (relative error <= "
+                                  "2^-17); q and the softmax weights enter the matrix cores as hi + mid + lo "
+                                  "parts (exact)",
                    "device": info["name"], "reps": args.reps},
         "steps_per_s": round(K / wall, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -727,6 +732,11 @@ def main():
                               ("; LM head streamed as fp8 e4m3 with power-of-two row scales" if args.lmhead_fp8 else "") +
                               ("; KV cache fp8 e4m3, power-of-two scale per K / V row" if args.kv_fp8 else ""),
                    "accumulation": "fp32", "reps": args.reps, "grid": grid,
+                   "activations": "fp32 within a workgroup; the residual stream, SiLU(gate)*up and the "
+                                  "attention partials cross workgroups rounded to a 19-bit mantissa "
+                                  "(packed pairs, relative error <= 2^-20); layer-GEMV inputs enter the "
+                                  "matrix cores as hi + lo bf16 parts (relative error <= 2^-17); q and "
+                                  "the softmax weights as hi + mid + lo parts (exact)",
                    "device": info["name"]},
         "kernel_ms_per_step": round(kern * 1e3 / K, 5),
         "hbm_gbps_achieved": round(achieved, 1),

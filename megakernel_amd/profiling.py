@@ -179,6 +179,8 @@ DERIVED = [
     ("L2 (TCC) hit rate", ("TCC_HIT_sum",), ("TCC_HIT_sum", "TCC_MISS_sum")),
     ("wave-cycles waiting on anything / wave-cycles", ("SQ_WAIT_ANY",), ("SQ_WAVE_CYCLES",)),
     ("wave-cycles waiting for issue / wave-cycles", ("SQ_WAIT_INST_ANY",), ("SQ_WAVE_CYCLES",)),
+    ("average L2 -> memory read latency (TCC cycles)", ("TCC_EA0_RDREQ_LEVEL_sum",), ("TCC_EA0_RDREQ_sum",)),
+    ("memory reads counted as DRAM requests / all memory reads", ("TCC_EA0_RDREQ_DRAM_sum",), ("TCC_EA0_RDREQ_sum",)),
     ("instruction-cache hit rate", ("SQC_ICACHE_HITS",), ("SQC_ICACHE_HITS", "SQC_ICACHE_MISSES")),
 ]
 
