@@ -669,6 +669,22 @@ def main():
               f"-> {K / walls[-1]:.1f} tok/s; last tokens {toks[-4:]}", file=sys.stderr, flush=True)
     wall = statistics.median(walls)
     kern = statistics.median(kernels)
+    # the per-call path (megakernel_decode: one launch and one host wait per
+    # token, as the reference's decode()), same context and token count; it
+    # includes launch and wait latency and is never the value
+    eng.fill_kv_synthetic(args.ctx, args.seed)
+    tok = first
+    for _ in range(5):
+        tok = eng.decode_token(tok)
+    eng.fill_kv_synthetic(args.ctx, args.seed)
+    eng.lib.megakernel_sync()
+    t0 = time.perf_counter()
+    tok = first
+    for _ in range(K):
+        tok = eng.decode_token(tok)
+    eng.lib.megakernel_sync()
+    per_call = K / (time.perf_counter() - t0)
+    print(f"# per-call path (megakernel_decode x {K}): {per_call:.1f} tok/s", file=sys.stderr, flush=True)
     nbytes = sum(shape.token_bytes(args.ctx + i) for i in range(K))
     if args.lmhead_fp8:  # 1 byte per LM-head weight instead of 2, plus a 4-byte scale per row
         nbytes -= K * (shape.vocab * shape.hidden - 4 * shape.vocab)
@@ -739,6 +755,7 @@ def main():
                                   "the softmax weights as hi + mid + lo parts (exact)",
                    "device": info["name"]},
         "kernel_ms_per_step": round(kern * 1e3 / K, 5),
+        "per_call_tok_s": round(per_call, 1),
         "hbm_gbps_achieved": round(achieved, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic},

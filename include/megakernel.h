@@ -393,8 +393,9 @@ int megakernel_op_lmhead_argmax(const void* w, long long copy_bytes, int n_copie
 
 /* megakernel_op_lmhead_argmax without the keys workspace: allocates nothing
  * (no device allocation, no event, no wait).  It has no counterpart in the
- * reference; it is for callers that cannot allocate -- code under HIP graph
- * capture, tight serving loops, harnesses that forbid allocation.  The keys
+ * reference; it is for callers that cannot allocate -- tight serving loops,
+ * harnesses that forbid allocation.  It enqueues on the null stream, so it is
+ * not meant for code under stream capture (no capture is tested).  The keys
  * live in a static device array of MK_NOALLOC_KEYS_MAX entries per GPU, so
  * n_out <= MK_NOALLOC_KEYS_MAX (larger calls fail with an error); calls that
  * overlap on one GPU share that array and race.  The work is enqueued on the

@@ -485,22 +485,28 @@ def test_batch_full_model_long_sequences():
         dw.free()
 
 
-@pytest.mark.parametrize("name,kv_fp8", [("tiny", False), ("baseline_2l", False), ("baseline_2l", True),
-                                         ("baseline_full", False)])
-def test_batch_persistent_step_equals_per_phase_kernels(name, kv_fp8):
+@pytest.mark.parametrize("name,kv_fp8,n_seq", [("tiny", False, 16), ("baseline_2l", False, 16),
+                                               ("baseline_2l", True, 16), ("baseline_full", False, 16),
+                                               ("tiny", False, 1), ("tiny", False, 5), ("tiny", False, 15),
+                                               ("baseline_2l", False, 1), ("baseline_2l", False, 5),
+                                               ("baseline_2l", False, 15)])
+def test_batch_persistent_step_equals_per_phase_kernels(name, kv_fp8, n_seq):
     """The one-kernel step (bk_step: every layer in one persistent kernel,
     hand-offs through agent-scope counters) and the per-phase kernels compute
     the same sums in the same order: logits and tokens of 3 debug steps and a
     6-step graph generate are bit-identical, at the bench's cache lengths
-    (seed 2024, 512-4096 positions: up to 16 attention splits per sequence)."""
+    (seed 2024, 512-4096 positions: up to 16 attention splits per sequence),
+    for 16 sequences and for 1, 5 and 15 (the first n_seq of the lengths:
+    partial sequence tiles of the step's work split)."""
     shape = {"tiny": TINY, "baseline_2l": BASELINE.with_(n_layers=2, vocab=4096),
              "baseline_full": BASELINE}[name]
     lengths, rng = _bench_lengths()
     if name == "tiny":
         lengths = [0, 5, 127, 200, 31, 32, 33, 255, 256, 257, 400, 511, 1, 90, 300, 64]
-    first = [int(t) for t in rng.integers(0, shape.vocab, size=16)]
+    first = [int(t) for t in rng.integers(0, shape.vocab, size=16)][:n_seq]
+    lengths = lengths[:n_seq]
     dw = DeviceWeights(shape, 41, std=0.02, gain_std=0.1)
-    eng = BatchEngine(dw, 16, max(lengths) + 16, shape)
+    eng = BatchEngine(dw, n_seq, max(lengths) + 16, shape)
     try:
         if kv_fp8:
             eng.set_kv_fp8(True)
@@ -511,7 +517,7 @@ def test_batch_persistent_step_equals_per_phase_kernels(name, kv_fp8):
                 eng.fill_kv_synthetic(b, n, 700 + b)
             toks, steps = list(first), []
             for i in range(3):
-                _print(f"batch step variant {variant} {name} fp8 {kv_fp8} debug step {i}")
+                _print(f"batch step variant {variant} {name} fp8 {kv_fp8} n_seq {n_seq} debug step {i}")
                 out, logits = eng.debug_logits(toks)
                 steps.append((list(out), logits.copy()))
                 toks = out
@@ -523,6 +529,83 @@ def test_batch_persistent_step_equals_per_phase_kernels(name, kv_fp8):
             assert np.array_equal(la, lb), f"step {i}: logits differ (max {np.abs(la - lb).max():.3e})"
         assert np.array_equal(ga, gb), "generated tokens differ"
         assert pa == pb == [n + 9 for n in lengths]
+    finally:
+        eng.close()
+        dw.free()
+
+
+@pytest.mark.parametrize("step", ["per-phase", "persistent"])
+def test_batch_full_model_bench_workload_graph(step):
+    """configs[4] as bench.py --batch 16 runs it: the full 28-layer model
+    (vocab 151936, bench weights: seed 2024, gains 1), 16 sequences at the
+    bench's cache lengths (seed 2024, uniform in [512, 4096]) and synthetic
+    prefixes, the bench's first tokens, stepped through the captured step
+    graph (decode: one replay; generate: chained replays).  Per-sequence
+    oracles hold the device's own prefixes read back (layer 0 of each prefix
+    is checked against the CPU generator first).  Two teacher-forced replays
+    (both sides consume the oracle's tokens), then a two-step generate (the
+    oracles consume the device's tokens); every device token must equal the
+    oracle's argmax unless the oracle's top-1/top-2 margin is within 2e-2, and
+    the K / V rows the four graph steps appended are held to the layer bar
+    (relative L2 <= 1e-2 per layer, bf16 of the same fp32 values in layer 0)."""
+    seed = 2024
+    lengths, rng = _bench_lengths(seed)
+    first = [int(t) for t in rng.integers(0, BASELINE.vocab, size=16)]
+    dw = DeviceWeights(BASELINE, seed, std=0.02, gain_std=0.0)
+    eng = BatchEngine(dw, 16, max(lengths) + 16, BASELINE)
+    mo = MultiOracle(BASELINE, dw, 16, max(lengths) + 16)
+    s = BASELINE
+    try:
+        eng.set_step_kernel(_lib.BATCH_STEP_PER_PHASE if step == "per-phase" else _lib.BATCH_STEP_PERSISTENT)
+        for b, n in enumerate(lengths):
+            eng.fill_kv_synthetic(b, n, seed + 1000 + b)
+            kv = eng.get_kv(b, n)  # [L][2][NKV][n][D]
+            if b in (0, 15):
+                assert np.array_equal(kv[0, 0], synth.kv_prefill_bits(seed + 1000 + b, 0, 0, n, s.n_kv_heads,
+                                                                      s.head_dim)), f"seq {b}: prefix K"
+            k, v = mo.caches[b]
+            k[:, :, :n] = qwen3_ref.bits_to_torch(kv[:, 0]).to(k.dtype)
+            v[:, :, :n] = qwen3_ref.bits_to_torch(kv[:, 1]).to(v.dtype)
+            mo.pos[b] = n
+            del kv
+        _print(f"batch bench workload ({step}): lengths {lengths}")
+        mismatches = 0
+
+        def check(out, refs, label):
+            nonlocal mismatches
+            for b, r in enumerate(refs):
+                if out[b] != r["token"]:
+                    m = qwen3_ref.top2_margin(r["logits"])
+                    gap = float(r["logits"][r["token"]] - r["logits"][out[b]])
+                    assert m <= MARGIN and gap <= MARGIN, (
+                        f"{label} seq {b}: token {out[b]} != oracle {r['token']} (margin {m:.4f})")
+                    mismatches += 1
+
+        toks = list(first)
+        for i in range(2):  # teacher-forced graph replays
+            out = eng.decode(toks)
+            refs = [mo.step(b, toks[b]) for b in range(16)]
+            check(out, refs, f"decode replay {i}")
+            _print(f"  replay {i}: tokens {out[:4]}... oracle {[r['token'] for r in refs[:4]]}...")
+            toks = [r["token"] for r in refs]
+        gen = eng.generate(toks, 2)  # chained replays
+        for i in range(2):
+            refs = [mo.step(b, toks[b]) for b in range(16)]
+            check(gen[i].tolist(), refs, f"generate step {i}")
+            toks = gen[i].tolist()
+        _print(f"  generate: {gen[:, :4].tolist()}; low-margin mismatches {mismatches} of 64")
+        assert eng.positions() == [n + 4 for n in lengths] == mo.pos
+        for b in (0, 5, 10, 15):  # the rows the graph steps appended
+            n = lengths[b]
+            got = eng.get_kv(b, n + 4)[:, :, :, n:, :]
+            k, v = mo.caches[b]
+            want = np.stack([k[:, :, n:n + 4].contiguous().view(torch.int16).numpy(),
+                             v[:, :, n:n + 4].contiguous().view(torch.int16).numpy()], axis=1).view(np.uint16)
+            check_kv_bf16(got[0], want[0], f"seq {b} layer-0 KV of the graph steps")
+            gf, wf = synth.bf16_bits_to_f32(got), synth.bf16_bits_to_f32(want)
+            rel = [float(np.linalg.norm(gf[l] - wf[l]) / np.linalg.norm(wf[l])) for l in range(s.n_layers)]
+            _print(f"  seq {b}: appended KV worst layer rel-L2 {max(rel):.2e}")
+            assert max(rel) <= 1e-2, f"seq {b}: appended KV rel-L2 {max(rel):.3e}"
     finally:
         eng.close()
         dw.free()
