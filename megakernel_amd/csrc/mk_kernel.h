@@ -616,6 +616,7 @@ __device__ __forceinline__ bool fetch_pk(const Params& p, const u64* src, unsign
   return !block_failed(failed);
 }
 
+
 // Wait for the 16 rows of block blk of x (8 packed words, tag t4) into xres.
 __device__ __forceinline__ bool fetch_xrows(const Params& p, const u64* x, int blk, unsigned t4, float* xres) {
   const int tid = ltid();
@@ -1285,15 +1286,17 @@ __device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit,
 // same softmax in one pass) into dst[QD], in batches of SB splits with a
 // running max; plus, unless xb0 < 0, the 16 residual rows of x block xb0
 // (threads 0..7) and, unless xb1 < 0, of block xb1 (threads 8..15).  Thread t
-// owns output pairs t + k NT (8-byte loads, as fetch_pk).
-template <class S>
-__device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
-                                            int xb0, int xb1, unsigned xt4, float* dst, float* xres,
-                                            EvPoll ev = EvPoll()) {
+// owns output pairs t + k NT (8-byte loads, as fetch_pk).  A batch's slots
+// past nsplit are skipped by wave-uniform branches; fetch_attn picks SB from
+// the split count, so the registers and the merge arithmetic of a round are
+// those of the splits that exist (the merge sits between the last poll round
+// and the O products, on the critical path).
+template <class S, int SB>
+__device__ __forceinline__ bool fetch_attn_sb(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
+                                               int xb0, int xb1, unsigned xt4, float* dst, float* xres, EvPoll ev) {
   constexpr int NPG = S::GQA * S::D / 2;
   constexpr int WP = part_words<S>();
   constexpr int PPT = (S::QD / 2 + NT - 1) / NT;
-  constexpr int SB = 8;
   const int tid = ltid();
   const bool want_x0 = xb0 >= 0 && (tid < 8 || (tid < 16 && xb1 >= 0));
   int failed = 0;
@@ -1338,20 +1341,24 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
     }
     rounds += sp.n + 1;
     if (want_x) xres[2 * tid] = pk_lo(wx), xres[2 * tid + 1] = pk_hi(wx);
+    const int nb = nsplit - s0 < SB ? nsplit - s0 : SB;  // splits in this batch (wave-uniform)
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       float Mb = M[k];
 #pragma unroll
-      for (int u = 0; u < SB; ++u) Mb = s0 + u < nsplit ? fmaxf(Mb, pk_lo(wm[k][u])) : Mb;
+      for (int u = 0; u < SB; ++u) {
+        if (u >= nb) break;
+        Mb = fmaxf(Mb, pk_lo(wm[k][u]));
+      }
       const float r = __expf(M[k] - Mb);
       o0[k] *= r, o1[k] *= r, L[k] *= r;
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
-        const bool ok = s0 + u < nsplit;
+        if (u >= nb) break;
         const float f = __expf(pk_lo(wm[k][u]) - Mb);
-        o0[k] = ok ? fmaf(f, pk_lo(wa[k][u]), o0[k]) : o0[k];
-        o1[k] = ok ? fmaf(f, pk_hi(wa[k][u]), o1[k]) : o1[k];
-        L[k] = ok ? fmaf(f, pk_hi(wm[k][u]), L[k]) : L[k];
+        o0[k] = fmaf(f, pk_lo(wa[k][u]), o0[k]);
+        o1[k] = fmaf(f, pk_hi(wa[k][u]), o1[k]);
+        L[k] = fmaf(f, pk_hi(wm[k][u]), L[k]);
       }
       M[k] = Mb;
     }
@@ -1366,6 +1373,19 @@ __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int
   }
   evp_exit(p, ev, rounds);
   return !block_failed(failed);
+}
+
+// Batch size by split count: 2, 3 or 4 splits in one batch (the class
+// kernel's contexts up to 2,048 positions), batches of 4 up to 8 splits, of 8
+// beyond (the spread kernel's long contexts).
+template <class S>
+__device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
+                                            int xb0, int xb1, unsigned xt4, float* dst, float* xres,
+                                            EvPoll ev = EvPoll()) {
+  if (nsplit <= 2) return fetch_attn_sb<S, 2>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+  if (nsplit == 3) return fetch_attn_sb<S, 3>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+  if (nsplit <= 8) return fetch_attn_sb<S, 4>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+  return fetch_attn_sb<S, 8>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
 }
 
 // argmax over the G per-workgroup words of a token (tag t14): the token id.
