@@ -34,6 +34,10 @@
 
 namespace mk {
 
+// Gains of the layer GEMV inputs in the per-wave staging layout (fetch_norm_nb).
+template <class S>
+using GIn = NormInW<S>;
+
 enum RoleClass : int { CLS_IDLE = 0, CLS_ATT, CLS_QG, CLS_DG, CLS_DO, CLS_O, CLS_Q, CLS_G, CLS_D, CLS_N };
 // Role row: class, then item indices (-1: none).  att: kv head att % NKV,
 // split att / NKV.
@@ -305,31 +309,31 @@ __device__ __forceinline__ bool cls_lm_head(const Params& p, Smem<S>& sm, int t,
 // P1: QKV block q of layer `layer` from the prefetched rq (inputs: x of the
 // previous layer, or the embedding row at layer 0).
 template <class S, int MODE, class BH>
-__device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const BH& rq, const NormIn<S>& gq,
+__device__ __forceinline__ bool cls_qkv(const Params& p, Smem<S>& sm, const BH& rq, const GIn<S>& gq,
                                         int t, int layer, int q, int tok, unsigned tg) {
   if (layer > 0) {
-    if (!fetch_norm<S>(p, p.x, tg - 1u, gq, sm.vec_q, sm.ssw[0], nullptr, ev_at(t, layer, PS_QKV))) return false;
+    fetch_norm_nb<S>(p, p.x, tg - 1u, gq, sm.vec_q, sm.ssw[0], ev_at(t, layer, PS_QKV));
   } else {
-    embed_norm<S>(p, tok, gq, sm.vec_q, sm.ssw[0], nullptr);
+    embed_norm_nb<S>(p, tok, gq, sm.vec_q, sm.ssw[0]);
   }
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 0);
   blk_mma(rq, sm.vec_q, sm.red[RED_Q]);
-  store_block<true>(sm.red[RED_Q], p.qkv + q * 16, row_scale(rq), tg, sm.ssw[0], 1.0f / S::H);
+  const bool ok = store_block<true>(sm.red[RED_Q], p.qkv + q * 16, row_scale(rq), tg, sm.ssw[0], 1.0f / S::H);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 0, 1, PUB_WAVE);
-  return true;
+  return ok;
 }
 
 // P4: gate/up pair g + SiLU from the prefetched rg / ru (input: x after O).
 template <class S, int MODE, class BH>
 __device__ __forceinline__ bool cls_gu(const Params& p, Smem<S>& sm, const BH& rg, const BH& ru,
-                                       const NormIn<S>& gf, int t, int layer, int g, unsigned tg) {
-  if (!fetch_norm<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], nullptr, ev_at(t, layer, PS_GU))) return false;
+                                       const GIn<S>& gf, int t, int layer, int g, unsigned tg) {
+  fetch_norm_nb<S>(p, p.x, tg + 2u, gf, sm.vec_g, sm.ssw[1], ev_at(t, layer, PS_GU));
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 0);
   blk_mma2(rg, ru, sm.vec_g, sm.red[RED_G], sm.red[RED_U]);
-  store_block_gu<true>(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, 0.f, tag4(tg + 3u), row_scale(rg), row_scale(ru),
-                 sm.ssw[1], 1.0f / S::H);
+  const bool ok = store_block_gu<true>(sm.red[RED_G], sm.red[RED_U], p.act + g * 8, 0.f, tag4(tg + 3u), row_scale(rg),
+                                       row_scale(ru), sm.ssw[1], 1.0f / S::H);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 3, 1, PUB_WAVE);
-  return true;
+  return ok;
 }
 
 // P5: down block d + residual from the prefetched rd (inputs: act and this
@@ -358,20 +362,22 @@ template <class S, int MODE, class BQ>
 __device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const BQ& ro0, const BQ& ro1,
                                       int t, int layer, int o0, int o1, int nsplit, int tok, unsigned tg) {
   const unsigned tg_x = tg - 1u;
-  if (!fetch_attn<S>(p, p.part, nsplit, tag4(tg + 1u), p.x, layer > 0 ? o0 : -1, o1, tag4(tg_x), sm.vec_o,
-                     sm.xres_o, ev_at(t, layer, PS_O)))
-    return false;
+  fetch_attn_nb<S>(p, p.part, nsplit, tag4(tg + 1u), p.x, layer > 0 ? o0 : -1, o1, tag4(tg_x), sm.vec_o,
+                   sm.xres_o, ev_at(t, layer, PS_O));
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 0);
   if (o1 >= 0) blk_mma2(ro0, ro1, sm.vec_o, sm.red[RED_O0], sm.red[RED_O1]);
   else blk_mma(ro0, sm.vec_o, sm.red[RED_O0]);
   __syncthreads();
+  // the abort flag is read with the block shares (one LDS round trip); rows
+  // of an abandoned wait are not published
+  const bool ok = !block_aborted();
   // wave PUB_WAVE: block o0, the wave before it: block o1
   const int w_ = wave_id();
-  if (w_ == PUB_WAVE) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, o0, layer, tok, tg + 2u, row_scale(ro0));
+  if (w_ == PUB_WAVE) o_rows<S>(p, sm.red[RED_O0], sm.xres_o, o0, layer, tok, tg + 2u, row_scale(ro0), ok);
   else if (w_ == PUB_WAVE - 1 && o1 >= 0)
-    o_rows<S>(p, sm.red[RED_O1], sm.xres_o + 16, o1, layer, tok, tg + 2u, row_scale(ro1));
+    o_rows<S>(p, sm.red[RED_O1], sm.xres_o + 16, o1, layer, tok, tg + 2u, row_scale(ro1), ok);
   if constexpr ((MODE & 2) != 0) trace_mark(p, t, PHASES_PER_LAYER * layer + 2, 1, PUB_WAVE);
-  return true;
+  return ok;
 }
 
 // Prefetch pacing.  A class's next weights are loaded while the workgroup is
@@ -433,17 +439,17 @@ __device__ __forceinline__ void blk_load_at(Blk8<KC>& b, const Params& p, long l
 
 // Weight block loads of one layer.
 template <class S, class BH>
-__device__ __forceinline__ void ld_qkv(BH& rq, NormIn<S>& gq, const Params& p, int layer, int q, int units = 0) {
-  gains_load(gq, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_ATTN);
+__device__ __forceinline__ void ld_qkv(BH& rq, GIn<S>& gq, const Params& p, int layer, int q, int units = 0) {
+  gains_load_w(gq, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_ATTN);
   blk_load_at(rq, p, (long long)layer * S::U_LAYER + S::OFF_QKV + (long long)q * S::KT_H * 64,
               (long long)layer * S::SROWS_LAYER + S::SROW_QKV + q * 16, units);
 }
 template <class S, class BH>
-__device__ __forceinline__ void ld_gu(BH& rg, BH& ru, NormIn<S>& gf, const Params& p, int layer, int g,
+__device__ __forceinline__ void ld_gu(BH& rg, BH& ru, GIn<S>& gf, const Params& p, int layer, int g,
                                       int units = 0) {
   const long long u = (long long)layer * S::U_LAYER + S::OFF_GU + (long long)(2 * g) * S::KT_H * 64;
   const long long sr = (long long)layer * S::SROWS_LAYER + S::SROW_GU + (2 * g) * 16;
-  gains_load(gf, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN);
+  gains_load_w(gf, p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_FFN);
   blk_load_at(rg, p, u, sr, units);
   blk_load_at(ru, p, u + S::KT_H * 64, sr + 16, units);
 }
@@ -579,7 +585,7 @@ __device__ __forceinline__ void run_qg(const Params& p, Smem<S>& sm, const int* 
   constexpr bool W8 = (MODE & 16) != 0;  // FP8 layer weights
   const int q = role[RF_Q], gi = role[RF_G];
   BlkW<S::KC_H, W8> rq, rg, ru;
-  NormIn<S> gq, gf;
+  GIn<S> gq, gf;
   if constexpr (HAS_Q) ld_qkv<S>(rq, gq, p, 0, q);
   if constexpr (!HAS_Q && HAS_G) ld_gu<S>(rg, ru, gf, p, 0, gi);
   int tok = p.first_token;
@@ -622,7 +628,7 @@ __device__ __forceinline__ void run_down(const Params& p, Smem<S>& sm, const int
   const int d = role[RF_D], gi = role[RF_G], o0 = role[RF_O0];
   BlkW<S::KC_F, W8> rd;
   BlkW<S::KC_H, W8> rg, ru;
-  NormIn<S> gf;
+  GIn<S> gf;
   BlkW<S::KC_Q, W8> ro;
   if constexpr (PARTNER == CLS_DG) ld_gu<S>(rg, ru, gf, p, 0, gi);
   if constexpr (PARTNER == CLS_DO) ld_o<S>(ro, p, 0, o0);

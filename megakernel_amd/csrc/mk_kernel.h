@@ -148,6 +148,11 @@ __device__ __forceinline__ bool block_failed(int failed) {
   // also waits for every outstanding global load and store of the wave
   return __hip_atomic_load(&wg_abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
 }
+// The abort flag after a barrier that follows every thread's last chance to
+// set it.
+__device__ __forceinline__ bool block_aborted() {
+  return __hip_atomic_load(&wg_abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+}
 
 // The wave that runs the one-wave epilogues and publishes a block's results.
 // Stores and loads retire in issue order (one vmcnt counter on gfx9-class
@@ -423,33 +428,37 @@ __device__ __forceinline__ float norm_scale(const float* ssw, float inv_h) {
 // the norm scale is taken here; its LDS reads issue with the shares' reads
 // (one round trip, not two).
 template <bool NORM = false>
-__device__ __forceinline__ void store_block(const float* red, u64* dst16, float scale, unsigned tag,
+__device__ __forceinline__ bool store_block(const float* red, u64* dst16, float scale, unsigned tag,
                                             const float* ssw = nullptr, float inv_h = 0.f) {
   __syncthreads();
+  const bool ok = !block_aborted();  // read with the shares (one LDS round trip)
   if (wave_id() == PUB_WAVE) {
     const unsigned l = lane_id();
     const float sh = red_row4(red, l);
     const float s = NORM ? scale * norm_scale(ssw, inv_h) : scale;
     const float y = sh * s;
-    if ((l & 3u) == 0u) ll_put(dst16 + (l >> 2), ll_pack(y, tag));
+    if (ok && (l & 3u) == 0u) ll_put(dst16 + (l >> 2), ll_pack(y, tag));
   }
+  return ok;
 }
 
 // Gate/up pair: SiLU(g r) * (u r) of the 16 rows (gate shares in rg, up
 // shares in ru), published as 8 packed-pair words.  NORM: r = norm_scale(ssw).
 template <bool NORM = false>
-__device__ __forceinline__ void store_block_gu(const float* rg, const float* ru, u64* dst8, float r, unsigned t4,
+__device__ __forceinline__ bool store_block_gu(const float* rg, const float* ru, u64* dst8, float r, unsigned t4,
                                                float sg = 1.0f, float su = 1.0f, const float* ssw = nullptr,
                                                float inv_h = 0.f) {
   __syncthreads();
+  const bool ok = !block_aborted();  // read with the shares (one LDS round trip)
   if (wave_id() == PUB_WAVE) {
     const unsigned l = lane_id();
     const float g = red_row4(rg, l), u = red_row4(ru, l);
     const float rr = NORM ? norm_scale(ssw, inv_h) : r;
     const float a = silu_mul(g * (rr * sg), u * (rr * su));
     const float b = dpp_sel<DPP_ROW_SHL4>(a);  // the next row
-    if ((l & 7u) == 0u) ll_put(dst8 + (l >> 3), pk_pack(a, b, t4));
+    if (ok && (l & 7u) == 0u) ll_put(dst8 + (l >> 3), pk_pack(a, b, t4));
   }
+  return ok;
 }
 
 // Element of the tile-layout LM head / embedding (row, col).
@@ -570,6 +579,85 @@ __device__ __forceinline__ bool fetch_norm(const Params& p, const u64* src, unsi
   return norm_finish(ss, ssw, failed, (float)S::H, r);
 }
 
+// Barrier-free form of fetch_norm for the layer GEMVs (class kernel): wave w
+// waits for the QW = H / (4 NW) element quads that are its own block
+// products' input columns (lanes 0 .. QW - 1, one 16-byte load each), stages
+// them and its wave partial of the sum of squares (ssw[w], read by the
+// epilogue after its barrier); no barrier before the products (LDS
+// operations of one wave complete in order).  Every LDS word it writes was
+// last read in this workgroup's previous phase of the same type, before that
+// phase's epilogue published the rows the awaited x depends on.  An
+// abandoned wait sets the abort flag (read by the epilogue).
+template <class S>
+struct NormInW {
+  float g[4];
+};
+template <class S>
+__device__ __forceinline__ void gains_load_w(NormInW<S>& n, const uint16_t* gain) {
+  constexpr int QW = S::H / 4 / NW;
+  const int l = (int)lane_id(), q = wave_id() * QW + (l < QW ? l : QW - 1);
+  const uint32_t* g2 = reinterpret_cast<const uint32_t*>(gain);
+  const uint32_t a = g2[2 * q], b = g2[2 * q + 1];
+  n.g[0] = bf16_to_f32((uint16_t)a), n.g[1] = bf16_to_f32((uint16_t)(a >> 16));
+  n.g[2] = bf16_to_f32((uint16_t)b), n.g[3] = bf16_to_f32((uint16_t)(b >> 16));
+}
+template <class S>
+__device__ __forceinline__ void fetch_norm_nb(const Params& p, const u64* src, unsigned tag, const NormInW<S>& n,
+                                              float* dst, float* ssw, EvPoll ev = EvPoll()) {
+  constexpr int QW = S::H / 4 / NW;
+  static_assert(S::H % (4 * NW) == 0 && QW <= kWave, "a wave's input quads fit its lanes");
+  const int w = wave_id(), l = (int)lane_id();
+  const unsigned t4 = tag4(tag);
+  const auto rs = make_rsrc(src);
+  int failed = 0;
+  float ss = 0.f;
+  evp_enter(p, ev);
+  if (l < QW) {
+    const int q = w * QW + l;
+    u32x4 wv;
+    Spin sp;
+    while (true) {
+      asm volatile("" ::: "memory");
+      wv = pk_get2(rs, (unsigned)q * 16u);
+      if (pk2_ready(wv, t4)) break;
+      if (!sp.step(p.err, p.timeout_ticks)) {
+        failed = 1;
+        break;
+      }
+    }
+    evp_exit(p, ev, sp.n + 1);
+    const float v[4] = {pkv(wv.x), pkv(wv.y), pkv(wv.z), pkv(wv.w)};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
+    put_quad<true>(dst, q, v, n.g);
+  }
+  ss = wave_sum(ss);
+  if (l == 0) ssw[w] = ss;
+  if (failed) wg_abort = 1;
+  asm volatile("" ::: "memory");  // staging stores before the wave's B-operand reads
+}
+// Layer 0: wave w gathers its input quads of the embedding row of `tok`.
+template <class S>
+__device__ __forceinline__ void embed_norm_nb(const Params& p, int tok, const NormInW<S>& n, float* dst, float* ssw) {
+  constexpr int QW = S::H / 4 / NW;
+  const int w = wave_id(), l = (int)lane_id();
+  float ss = 0.f;
+  if (l < QW) {
+    const int q = w * QW + l;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = packed_elem<S::KT_H>(p.lmhead, tok, 4 * q + e);
+      ss = fmaf(v[e], v[e], ss);
+    }
+    put_quad<true>(dst, q, v, n.g);
+  }
+  ss = wave_sum(ss);
+  if (l == 0) ssw[w] = ss;
+  asm volatile("" ::: "memory");
+}
+
+
 // Wait for a packed-pair vector of 2*NPK values (NPK words, 4-bit tag t4) and,
 // unless xblk < 0, the 16 residual rows of block xblk of x (8 packed words,
 // tag xt4, threads 0..7), in one bulk round of 8-byte loads (hot lines that
@@ -689,13 +777,13 @@ __device__ __forceinline__ bool wait_last_qkv(const Params& p, unsigned tl) {
 // One wave (red_row4 layout).
 template <class S>
 __device__ __forceinline__ void o_rows(const Params& p, const float* red, const float* xres, int blk, int layer,
-                                       int tok, unsigned tag, float rs = 1.0f) {
+                                       int tok, unsigned tag, float rs = 1.0f, bool ok = true) {
   const unsigned l = lane_id();
   const int r = (int)(l >> 2);
   const float xo = layer == 0 ? packed_elem<S::KT_H>(p.lmhead, tok, blk * 16 + r) : xres[r];
   const float a = xo + red_row4(red, l) * rs;
   const float b = dpp_sel<DPP_ROW_SHL4>(a);  // the next row
-  if ((l & 7u) == 0u) ll_put(p.x + blk * 8 + (l >> 3), pk_pack(a, b, tag4(tag)));
+  if (ok && (l & 7u) == 0u) ll_put(p.x + blk * 8 + (l >> 3), pk_pack(a, b, tag4(tag)));
 }
 
 // Down block blk (shares in red[RED_D]) plus the residual rows xres_d -> the
@@ -1292,7 +1380,7 @@ __device__ bool attention_merge(const Params& p, Smem<S>& sm, int g, int nsplit,
 // those of the splits that exist (the merge sits between the last poll round
 // and the O products, on the critical path).
 template <class S, int SB>
-__device__ __forceinline__ bool fetch_attn_sb(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
+__device__ __forceinline__ int fetch_attn_core(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
                                                int xb0, int xb1, unsigned xt4, float* dst, float* xres, EvPoll ev) {
   constexpr int NPG = S::GQA * S::D / 2;
   constexpr int WP = part_words<S>();
@@ -1300,7 +1388,6 @@ __device__ __forceinline__ bool fetch_attn_sb(const Params& p, const u64* part, 
   const int tid = ltid();
   const bool want_x0 = xb0 >= 0 && (tid < 8 || (tid < 16 && xb1 >= 0));
   int failed = 0;
-  __syncthreads();
   float M[PPT], L[PPT], o0[PPT], o1[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) M[k] = -INFINITY, L[k] = 0.f, o0[k] = 0.f, o1[k] = 0.f;
@@ -1372,20 +1459,49 @@ __device__ __forceinline__ bool fetch_attn_sb(const Params& p, const u64* part, 
     }
   }
   evp_exit(p, ev, rounds);
-  return !block_failed(failed);
+  return failed;
 }
 
 // Batch size by split count: 2, 3 or 4 splits in one batch (the class
 // kernel's contexts up to 2,048 positions), batches of 4 up to 8 splits, of 8
 // beyond (the spread kernel's long contexts).
 template <class S>
+__device__ __forceinline__ int fetch_attn_any(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
+                                              int xb0, int xb1, unsigned xt4, float* dst, float* xres, EvPoll ev) {
+  if (nsplit <= 2) return fetch_attn_core<S, 2>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+  if (nsplit == 3) return fetch_attn_core<S, 3>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+  if (nsplit <= 8) return fetch_attn_core<S, 4>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+  return fetch_attn_core<S, 8>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+}
+
+// Workgroup-synchronous form (spread kernel): a barrier before (every wave is
+// done with the LDS of its previous phase) and after (the staged input is
+// complete; false when a wait was abandoned).
+template <class S>
 __device__ __forceinline__ bool fetch_attn(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
                                             int xb0, int xb1, unsigned xt4, float* dst, float* xres,
                                             EvPoll ev = EvPoll()) {
-  if (nsplit <= 2) return fetch_attn_sb<S, 2>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
-  if (nsplit == 3) return fetch_attn_sb<S, 3>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
-  if (nsplit <= 8) return fetch_attn_sb<S, 4>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
-  return fetch_attn_sb<S, 8>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev);
+  __syncthreads();
+  return !block_failed(fetch_attn_any<S>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev));
+}
+
+// Barrier-free form (class kernel).  When the pairs are as many as the
+// threads (BASELINE: QD / 2 = 512), thread t stages pair t, so wave w stages
+// exactly the QD / NW input columns its own block products read (LDS
+// operations of one wave complete in order): no barrier before the products.
+// No barrier before the wait either: every LDS word this phase writes (its
+// staged input, block shares, residual rows) was last read in this
+// workgroup's previous O phase, before that phase's epilogue stored the x
+// rows that this phase's partials depend on.  A wait abandoned by any thread
+// sets the workgroup's abort flag; the caller reads it after its epilogue
+// barrier (block_aborted).
+template <class S>
+__device__ __forceinline__ void fetch_attn_nb(const Params& p, const u64* part, int nsplit, unsigned t4, const u64* x,
+                                              int xb0, int xb1, unsigned xt4, float* dst, float* xres,
+                                              EvPoll ev = EvPoll()) {
+  if (fetch_attn_any<S>(p, part, nsplit, t4, x, xb0, xb1, xt4, dst, xres, ev)) wg_abort = 1;
+  if constexpr (S::QD / 2 != NT) __syncthreads();  // a wave's pairs are not its own input columns
+  else asm volatile("" ::: "memory");              // staging stores before the wave's B-operand reads
 }
 
 // argmax over the G per-workgroup words of a token (tag t14): the token id.
