@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--layer-fp8", action="store_true",
                     help="stream fp8 e4m3 copies of the layer matrices (power-of-two row scales; decode only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-per-call", action="store_true",
+                    help="skip the per-call (one launch per token) measurement, e.g. under a profiler")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound of the CPU baseline sample")
     ap.add_argument("--trace", action="store_true", help="print a per-phase critical-path summary")
     ap.add_argument("--kernel", choices=("auto", "spread"), default="auto",
@@ -672,19 +674,21 @@ def main():
     # the per-call path (megakernel_decode: one launch and one host wait per
     # token, as the reference's decode()), same context and token count; it
     # includes launch and wait latency and is never the value
-    eng.fill_kv_synthetic(args.ctx, args.seed)
-    tok = first
-    for _ in range(5):
-        tok = eng.decode_token(tok)
-    eng.fill_kv_synthetic(args.ctx, args.seed)
-    eng.lib.megakernel_sync()
-    t0 = time.perf_counter()
-    tok = first
-    for _ in range(K):
-        tok = eng.decode_token(tok)
-    eng.lib.megakernel_sync()
-    per_call = K / (time.perf_counter() - t0)
-    print(f"# per-call path (megakernel_decode x {K}): {per_call:.1f} tok/s", file=sys.stderr, flush=True)
+    per_call = None
+    if not args.no_per_call:
+        eng.fill_kv_synthetic(args.ctx, args.seed)
+        tok = first
+        for _ in range(5):
+            tok = eng.decode_token(tok)
+        eng.fill_kv_synthetic(args.ctx, args.seed)
+        eng.lib.megakernel_sync()
+        t0 = time.perf_counter()
+        tok = first
+        for _ in range(K):
+            tok = eng.decode_token(tok)
+        eng.lib.megakernel_sync()
+        per_call = K / (time.perf_counter() - t0)
+        print(f"# per-call path (megakernel_decode x {K}): {per_call:.1f} tok/s", file=sys.stderr, flush=True)
     nbytes = sum(shape.token_bytes(args.ctx + i) for i in range(K))
     if args.lmhead_fp8:  # 1 byte per LM-head weight instead of 2, plus a 4-byte scale per row
         nbytes -= K * (shape.vocab * shape.hidden - 4 * shape.vocab)
@@ -755,7 +759,7 @@ def main():
                                   "the softmax weights as hi + mid + lo parts (exact)",
                    "device": info["name"]},
         "kernel_ms_per_step": round(kern * 1e3 / K, 5),
-        "per_call_tok_s": round(per_call, 1),
+        "per_call_tok_s": round(per_call, 1) if per_call is not None else None,
         "hbm_gbps_achieved": round(achieved, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic},
