@@ -386,10 +386,13 @@ __device__ __forceinline__ bool cls_o(const Params& p, Smem<S>& sm, const BQ& ro
 // the cross-XCD hand-off loads of the phase that runs meanwhile.  So each
 // wave issues one 1 KiB load per step and sleeps between steps, spreading a
 // class's bytes over most of its idle window.  Spacing per step (units of
-// s_sleep 1, 64 clocks) by class and window, scaled by p.pace_pct.
+// s_sleep 1, 64 clocks) by class and window, scaled by p.pace_pct.  The
+// spacings follow the layer period: they were set for an 11.7 us layer and
+// taken to 70 % when the layer fell to ~10 us (3,127 -> 3,166 tok/s; 130 % of
+// the old values lost 8 %, 0 % -- bursts -- 3 %).
 enum PaceSlot : int { PACE_QG_GU = 0, PACE_QG_Q, PACE_DG, PACE_DO, PACE_O, PACE_ATT, PACE_N };
 __device__ __forceinline__ int pace_units(const Params& p, int slot) {
-  constexpr int base[PACE_N] = {13, 11, 11, 9, 19, 15};
+  constexpr int base[PACE_N] = {9, 8, 8, 6, 13, 10};
   return base[slot] * p.pace_pct / 100;
 }
 __device__ __forceinline__ void pace_step(int units) {
