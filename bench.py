@@ -204,7 +204,7 @@ def poll_summary(tr, ev, layer, us):
     consumer's poll loop exits and its 'inputs ready' mark, with wave 0's poll
     rounds.  Times in us relative to the last producer store."""
     import numpy as np
-    classes = ["idle", "att+o", "qkv+gu", "gu+down", "down+o", "o", "qkv", "gu", "down"]
+    classes = ["idle", "att+o", "qkv+gu", "gu+down", "down+o", "o", "qkv", "gu", "down", "att"]
     role = ev[16].astype(int) - 1
     sites = [("x->qkv", 0, (layer - 1) * 5 + 4, layer * 5 + 0), ("qkv->attn", 1, layer * 5 + 0, layer * 5 + 1),
              ("part->o", 2, layer * 5 + 1, layer * 5 + 2), ("x->gate_up", 3, layer * 5 + 2, layer * 5 + 3),

@@ -11,6 +11,8 @@
 //   streaming do not), so each workgroup issues the next weights of a role
 //   right after it has computed and published that role, and the next wait of
 //   the workgroup comes at least one phase later:
+//     A    attention (P2)            next K/V after attention (the default
+//                                    where the O blocks fit elsewhere)
 //     ATT  attention (P2) + O (P3)   next K/V and next O after O
 //     QG   QKV (P1) + gate/up (P4)   gate/up after QKV, next QKV after gate/up
 //     DG   gate/up (P4) + down (P5)  next gate/up and next down after down
@@ -38,7 +40,7 @@ namespace mk {
 template <class S>
 using GIn = NormInW<S>;
 
-enum RoleClass : int { CLS_IDLE = 0, CLS_ATT, CLS_QG, CLS_DG, CLS_DO, CLS_O, CLS_Q, CLS_G, CLS_D, CLS_N };
+enum RoleClass : int { CLS_IDLE = 0, CLS_ATT, CLS_QG, CLS_DG, CLS_DO, CLS_O, CLS_Q, CLS_G, CLS_D, CLS_A, CLS_N };
 // Role row: class, then item indices (-1: none).  att: kv head att % NKV,
 // split att / NKV.
 enum RoleField : int { RF_CLS = 0, RF_Q, RF_G, RF_O0, RF_O1, RF_D, RF_ATT, RF_PAD, ROLE_INTS };
@@ -526,11 +528,11 @@ __device__ __forceinline__ void kv_load_paced(KV<S, K8>& r, const Params& p, int
 __device__ __forceinline__ bool has_next(const Params& p, int t, int layer) { return layer + 1 < p.n_layers; }
 __device__ __forceinline__ int next_layer(const Params& p, int layer) { return layer + 1; }
 
-template <class S, int MODE>
+template <class S, int MODE, bool HAS_O = true>
 __device__ __forceinline__ void run_att(const Params& p, Smem<S>& sm, const int* role) {
   constexpr bool W8 = (MODE & 16) != 0;  // FP8 layer weights
   constexpr bool K8 = (MODE & 8) != 0;
-  const int a = role[RF_ATT], o0 = role[RF_O0];
+  const int a = role[RF_ATT], o0 = HAS_O ? role[RF_O0] : -1;
   const int g = a % S::NKV, s = a / S::NKV;
   KV<S, K8> rkv;
   BlkW<S::KC_Q, W8> ro;
@@ -733,6 +735,7 @@ __global__ __launch_bounds__(NT) void decode_cls_kernel(Params p) {
   const int* role = p.roles + blockIdx.x * ROLE_INTS;
   switch (role[RF_CLS]) {
     case CLS_ATT: run_att<S, MODE>(p, sm, role); break;
+    case CLS_A: run_att<S, MODE, false>(p, sm, role); break;
     case CLS_QG: run_qg<S, MODE, true, true>(p, sm, role); break;
     case CLS_Q: run_qg<S, MODE, true, false>(p, sm, role); break;
     case CLS_G: run_qg<S, MODE, false, true>(p, sm, role); break;
