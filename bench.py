@@ -724,7 +724,7 @@ def main():
     dw.free()
 
     out = {
-        "metric": METRIC,
+        "metric": METRIC if args.ctx == 1024 else METRIC.replace("ctx 1024", f"ctx {args.ctx}"),
         "value": round(K / wall, 2),
         "unit": "tok/s",
         "n_gpus": 1,
