@@ -135,11 +135,11 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL((bk_pattn<S, true>), dim3(S::NKV, ng, PA_SPLIT), dim3(AT), 0, h->stream, g, l);
+      hipLaunchKernelGGL((bk_pattn<S, true>), dim3(S::NKV, ng), dim3(PC_AW * kWave), 0, h->stream, g, l);
     } else {
       hipLaunchKernelGGL((bk_append<S, false, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);
-      hipLaunchKernelGGL((bk_pattn<S, false>), dim3(S::NKV, ng, PA_SPLIT), dim3(AT), 0, h->stream, g, l);
+      hipLaunchKernelGGL((bk_pattn<S, false>), dim3(S::NKV, ng), dim3(PC_AW * kWave), 0, h->stream, g, l);
     }
     hipLaunchKernelGGL((bk_ptile<S, PT_O, PTileO>), dim3(S::H / 16 / PTileO::MP, rows(PTileO::NG)), dim3(GT), 0,
                        h->stream, g, l);

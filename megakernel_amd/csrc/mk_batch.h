@@ -707,13 +707,58 @@ __global__ __launch_bounds__(GT) void bk_down(G p, int layer) {
 // weight byte is read from L2 once per NG groups and a column byte once per
 // MP blocks.  Wave w owns WB blocks x WGR groups over the whole K; the
 // epilogue runs on its accumulators.
-template <int MP_, int NG_, int KC_, int WB_, int WGR_, int PD_ = 2>
+template <int MP_, int NG_, int KC_, int WB_, int WGR_, int PD_ = 2, int NS_ = 0>
 struct PTile {
   static constexpr int MP = MP_, NG = NG_, KC = KC_, WB = WB_, WGR = WGR_;
   static constexpr int PD = PD_;  // K chunks whose loads are in flight (1 or 2 register sets)
+  // NS > 0: no register staging; NS LDS stages filled by direct-to-LDS loads
+  // (pt_pipeline), NS - 1 chunks in flight
+  static constexpr int NS = NS_;
   static_assert((MP / WB) * (NG / WGR) == GW, "every wave owns whole blocks x groups");
   static_assert(PD == 1 || PD == 2, "one or two register sets");
+  static_assert(NS == 0 || NS >= 2, "two stages at least");
 };
+
+// One 16-byte load per lane straight into LDS (global_load_lds_dwordx4):
+// lane l's bytes land at dst + 16 l, dst being the wave's (uniform) address,
+// passed in M0.  It counts on vmcnt like any vector load and writes no
+// register.  Inline assembly, so that the compiler does not add its own
+// conservative wait for every such load in flight before each LDS read: the
+// caller waits for exactly the loads it needs (wait_vmcnt).
+__device__ __forceinline__ void lds_load16(const void* src, void* dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)dst);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// The K loop of a tiled GEMM over NS LDS stages filled by direct loads:
+// chunk c goes to stage c % NS, issued NS - 1 chunks ahead (issue(c, stage),
+// NI loads per lane).  Before multiplying chunk c a wave waits until its own
+// loads of chunk c have landed (vmcnt: the later chunks' loads may stay in
+// flight); the barrier after it makes every wave's share visible and retires
+// the stage the next issue overwrites (multiplied in the previous iteration,
+// whose LDS reads every wave has consumed before reaching the barrier).  The
+// plain s_barrier: __syncthreads()' fence would wait for every load in
+// flight.
+template <int NS, int NC, int NI, class Issue, class Compute>
+__device__ __forceinline__ void pt_pipeline(const Issue& issue, const Compute& compute) {
+  static_assert(NC >= NS - 1, "the prologue fills NS - 1 stages");
+#pragma unroll
+  for (int c = 0; c < NS - 1; ++c) issue(c, c);
+  for (int c = 0; c < NC; ++c) {
+    if (c + NS - 1 <= NC) wait_vmcnt<(NS - 2) * NI>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (c + NS - 1 < NC) issue(c + NS - 1, (c + NS - 1) % NS);
+    compute(c % NS);
+  }
+  asm volatile("" ::: "memory");
+}
 // (measured per layer, us: gate / up <8,8,2,4,2> 46.5, <8,8,2,2,4> 47.3,
 // <8,8,2,1,8> 50.2, <8,4,2,1,4> 67.4, <4,8,2,1,4> 71.9, <4,4,4,1,2> 61.6;
 // QKV <8,2,2,2,1> 19.5, <8,2,2,1,2> 20.1, <4,4,2,1,2> 22.8, <4,2,4,1,1> 27.5,
@@ -721,7 +766,10 @@ struct PTile {
 // <8,2,4,2,1> 22.1, <4,4,4,1,2> 23.7; down <4,2,4,1,1> 38.5, <8,1,4,1,1> 39.2,
 // <8,2,4,2,1> 41.6, <4,4,4,1,2> 47.7, <2,4,4,1,1> 54.3.  A wave owning more
 // blocks reads fewer LDS bytes per product.)
-using PTileGU = PTile<8, 8, 2, 4, 2, 1>;  // one register set: 234 VGPRs
+// gate / up: direct-to-LDS loads, K chunks of one tile, four stages (three
+// chunks in flight): 44.0 -> 40.3 us against <8,8,2,4,2> with one register
+// set (234 VGPRs)
+using PTileGU = PTile<8, 8, 1, 4, 2, 1, 4>;
 // gate / up of a pass of at most PT_SMALL_GROUPS groups: the 8 x 8 tile
 // leaves too few workgroups (256 tokens: 44), 8 x 2 four times as many
 // (measured, tok/s, 8 x 8 / 8 x 2: 128 tokens 37,869 / 44,851, 256 tokens
@@ -732,8 +780,12 @@ using PTileGUs = PTile<8, 2, 2, 2, 1>;
 #define MK_PT_SMALL_GROUPS 32
 #endif
 constexpr int PT_SMALL_GROUPS = MK_PT_SMALL_GROUPS;
-using PTileQKV = PTile<8, 2, 2, 2, 1>;
-using PTileO = PTile<4, 2, 4, 1, 1>;
+// QKV and O with direct-to-LDS loads (QKV three stages: four, 96 KB of LDS,
+// leave one workgroup per CU and took 18.1 -> 21.1 us; O four stages of two
+// tiles 20.9 -> 20.0 us); down keeps register staging (four direct-load
+// stages measured 38.4 -> 38.7 us)
+using PTileQKV = PTile<8, 2, 2, 2, 1, 2, 3>;
+using PTileO = PTile<4, 2, 2, 1, 1, 2, 4>;
 using PTileDN = PTile<4, 2, 4, 1, 1, 1>;   // one register set: two lose 8 % at 1,024 tokens
 using PTileDNs = PTile<4, 2, 4, 1, 1, 2>;  // passes of at most PT_SMALL_GROUPS groups
 
@@ -745,8 +797,9 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
   constexpr int BU = NG * 2 * KC * kWave;  // ... of its column tiles
   constexpr int LA = AU / GT, LB = BU / GT;  // per thread
   static_assert(NT % KC == 0 && AU % GT == 0 && BU % GT == 0, "tile shape");
-  __shared__ u32x4 sa[2][2 * MP][KC][kWave];  // [buf][gate blocks | up blocks][tile][lane]
-  __shared__ u32x4 sb[2][NG][2][KC][kWave];   // [buf][group][hi / lo][tile][lane]
+  constexpr int NSB = T::NS > 0 ? T::NS : 2;
+  __shared__ u32x4 sa[NSB][2 * MP][KC][kWave];  // [buf][gate blocks | up blocks][tile][lane]
+  __shared__ u32x4 sb[NSB][NG][2][KC][kWave];   // [buf][group][hi / lo][tile][lane]
   // workgroup i runs on XCD i % 8: tiles (r, c) numbered r * ct + c are dealt
   // to XCDs in contiguous runs, so a row tile's column tiles share an XCD's L2
   // (its 22 row tiles are no multiple of 8; with the plain grid order a
@@ -781,11 +834,30 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
 #pragma unroll
     for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = xb[k];
   };
-  load(0, ra[0], rbv[0]);
-  store(0, ra[0], rbv[0]);
-  if constexpr (T::PD == 2)
-    if (NC > 1) load(1, ra[T::PD - 1], rbv[T::PD - 1]);
-  __syncthreads();
+  // direct loads: wave w moves whole 1 KB tiles w, w + 8, ... of a chunk
+  const auto issue = [&](int c, int buf) {
+    const int w = wave_id(), ln = (int)lane_id();
+#pragma unroll
+    for (int k = 0; k < LA; ++k) {
+      const int t = w + GW * k, blk = t / KC, kt = t % KC;
+      lds_load16(wgt[blk / MP] + ((long long)(rb0 + blk % MP) * NT + c * KC + kt) * 64 + ln, &sa[buf][blk][kt][0]);
+    }
+#pragma unroll
+    for (int k = 0; k < LB; ++k) {
+      const int t = w + GW * k, gq = t / (2 * KC), pl = (t / KC) % 2, kt = t % KC;
+      const int gs = gq < ngr ? gq : 0;  // a group past the pass reads group 0 (its columns are never stored)
+      lds_load16(xg_plane<S>(group_params(pg, g0 + gs), 0, 1, pl) + (ln & 15) * S::H + 32 * (c * KC + kt) +
+                     8 * (ln >> 4),
+                 &sb[buf][gq][pl][kt][0]);
+    }
+  };
+  if constexpr (T::NS == 0) {
+    load(0, ra[0], rbv[0]);
+    store(0, ra[0], rbv[0]);
+    if constexpr (T::PD == 2)
+      if (NC > 1) load(1, ra[T::PD - 1], rbv[T::PD - 1]);
+    __syncthreads();
+  }
   const int w = wave_id(), pw = (w / (NG / WGR)) * WB, gb = (w % (NG / WGR)) * WGR;
   const unsigned l = lane_id();
   f32x4 acc[WB][WGR][2][2];  // [block][group][gate / up][hi / lo part]
@@ -812,7 +884,9 @@ __global__ __launch_bounds__(GT) void bk_pgu_t(PGroup pg, int layer) {
       }
     }
   };
-  if constexpr (T::PD == 1) {
+  if constexpr (T::NS > 0) {
+    pt_pipeline<T::NS, NC, LA + LB>(issue, compute);
+  } else if constexpr (T::PD == 1) {
     for (int c = 0; c < NC; ++c) {
       if (c + 1 < NC) load(c + 1, ra[0], rbv[0]);
       compute(c & 1);
@@ -878,8 +952,9 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
   constexpr int AU = MP * KC * kWave, BU = NG * 2 * KC * kWave;
   constexpr int LA = AU / GT, LB = BU / GT;
   static_assert(NT % KC == 0 && AU % GT == 0 && BU % GT == 0, "tile shape");
-  __shared__ u32x4 sa[2][MP][KC][kWave];
-  __shared__ u32x4 sb[2][NG][2][KC][kWave];
+  constexpr int NSB = T::NS > 0 ? T::NS : 2;
+  __shared__ u32x4 sa[NSB][MP][KC][kWave];
+  __shared__ u32x4 sb[NSB][NG][2][KC][kWave];
   const int rb0 = blockIdx.x * MP, g0 = blockIdx.y * NG, tid = ltid();
   const int ngr = pg.n - g0 < NG ? pg.n - g0 : NG;
   const BParams p0 = group_params(pg, g0);
@@ -914,11 +989,29 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
 #pragma unroll
     for (int k = 0; k < LB; ++k) (&sb[buf][0][0][0][0])[tid + GT * k] = xb[k];
   };
-  load(0, ra[0], rbv[0]);
-  store(0, ra[0], rbv[0]);
-  if constexpr (T::PD == 2)
-    if (NC > 1) load(1, ra[T::PD - 1], rbv[T::PD - 1]);
-  __syncthreads();
+  // direct loads: wave w moves whole 1 KB tiles w, w + 8, ... of a chunk
+  const auto issue = [&](int c, int buf) {
+    const int w = wave_id(), ln = (int)lane_id();
+#pragma unroll
+    for (int k = 0; k < LA; ++k) {
+      const int t = w + GW * k, blk = t / KC, kt = t % KC;
+      lds_load16(wm + ((long long)(rb0 + blk) * NT + c * KC + kt) * 64 + ln, &sa[buf][blk][kt][0]);
+    }
+#pragma unroll
+    for (int k = 0; k < LB; ++k) {
+      const int t = w + GW * k, gq = t / (2 * KC), pl = (t / KC) % 2, kt = t % KC;
+      const int gs = gq < ngr ? gq : 0;  // a group past the pass reads group 0 (its columns are never stored)
+      lds_load16(plane(group_params(pg, g0 + gs), pl) + (ln & 15) * K + 32 * (c * KC + kt) + 8 * (ln >> 4),
+                 &sb[buf][gq][pl][kt][0]);
+    }
+  };
+  if constexpr (T::NS == 0) {
+    load(0, ra[0], rbv[0]);
+    store(0, ra[0], rbv[0]);
+    if constexpr (T::PD == 2)
+      if (NC > 1) load(1, ra[T::PD - 1], rbv[T::PD - 1]);
+    __syncthreads();
+  }
   const int w = wave_id(), pw = (w / (NG / WGR)) * WB, gb = (w % (NG / WGR)) * WGR;
   const unsigned l = lane_id();
   f32x4 acc[WB][WGR][2];  // [block][group][hi / lo part]
@@ -940,7 +1033,9 @@ __global__ __launch_bounds__(GT) void bk_ptile(PGroup pg, int layer) {
       }
     }
   };
-  if constexpr (T::PD == 1) {
+  if constexpr (T::NS > 0) {
+    pt_pipeline<T::NS, NC, LA + LB>(issue, compute);
+  } else if constexpr (T::PD == 1) {
     for (int c = 0; c < NC; ++c) {
       if (c + 1 < NC) load(c + 1, ra[0], rbv[0]);
       compute(c & 1);
@@ -1580,204 +1675,302 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(ATTN_WAVES_P
 }
 
 // ------------------------------------------------------------ prefill attention
-// PA_SPLIT workgroups per (column group, kv head) of a prefill pass, each
-// taking PA_NQ / 2 of the group's consecutive tokens x 2 q heads = PA_NQ
-// queries against the causal prefix [0, its last position], every
-// 32-position K / V block loaded once for all its queries (bk_attn loads it
-// once per token).  Wave w takes blocks
-// w, w + 4, ... with an online softmax per query; the four waves' states are
-// combined at the end, so there are no split partials and no merge.  The
-// products are bk_attn's: scores^T = K . Qb with q in three bf16 parts (rows
-// 4 j + 0..2 of a 16-row tile hold query j of the tile), out^T = V^T . Pb
-// with the softmax weights split the same way; PA_RT tiles hold the PA_NQ
-// queries (query 2 c + h = the workgroup's token c, q head 2 g + h).
-#ifndef MK_PATTN_RT
-#define MK_PATTN_RT 4
+// One workgroup of PC_AW waves per (kv head g, column group): the group's
+// <= 16 tokens x 2 q heads = 32 queries (query q: token q / 2, head 2 g + q % 2)
+// as two 16-column tiles; wave w takes the 32-position K / V blocks w, w +
+// PC_AW, ... of the causal prefix [0, the group's last position] with an
+// online softmax per query, and the waves' states are combined at the end.
+// Products (v_mfma_f32_16x16x32_bf16):
+//   scores^T (16 positions x 16 queries) = K (A operand: the cache rows as
+//     loaded) . Q^T (B operand: q in NPART bf16 parts, one product each);
+//   out^T (16 dims x 16 queries) += V^T (A operand: the transposed cache, the
+//     block's positions in the order the scores leave them in a lane) . P^T
+//     (B operand: the softmax weights in NPART parts, built in registers).
+// A lane holds 4 positions x 1 query of each 16-position score tile: the
+// block max takes two cross-lane steps, the row sums stay per lane until the
+// end, and the weights never pass through LDS.  NPART 3: q and the weights
+// split exactly (hi + mid + lo by truncation); 2: hi + lo (RNE), relative
+// error <= 2^-17.
+// (measured per layer at 1,024 tokens, us: 8 waves 22.6 against 4 waves
+// 20.9; three K / V register sets 23.2 against two 20.6; two parts 20.8
+// against three 21.6; a timing probe limited to one block per workgroup
+// 9.0, so about half is the prologue, the merge and the launch; the earlier
+// kernel with q
+// as the A operand -- 4 queries per 16-row tile, the weights through LDS --
+// 34.0.)
+#ifndef MK_PATTN_NPART
+#define MK_PATTN_NPART 3
 #endif
-// 16-row tiles of q parts per workgroup (2 tokens each; measured per layer:
-// 8 tiles 43.8 us at 341 registers, one workgroup per CU; 4 tiles 34.4 us at
-// 201, two per CU; 2 tiles 35.9 us)
-constexpr int PA_RT = MK_PATTN_RT;
-constexpr int PA_NQ = 4 * PA_RT;     // queries of a workgroup
-constexpr int PA_SPLIT = 2 * BMAX / PA_NQ;  // workgroups per (group, kv head)
-template <class S>
-struct PAttnLds {
-  __attribute__((aligned(16))) uint16_t qb[PA_RT][16][S::D];  // q parts (A operand of the scores)
-  union {
-    __attribute__((aligned(16))) uint16_t pb[AW][PA_RT][16][32];  // weight parts (A operand of the output)
-    float ow[AW][PA_NQ][S::D];                                     // the waves' outputs, after the loop
-  };
-  float mw[AW][PA_NQ], lw[AW][PA_NQ];
-};
-
+constexpr int PC_AW = 4;         // waves of a workgroup
+constexpr int PC_NQ = 2 * BMAX;  // queries of a workgroup (a column group x 2 q heads)
 template <class S, bool K8>
-__global__ __launch_bounds__(AT) void bk_pattn(PGroup pg, int layer) {
-  static_assert(S::GQA == 2 && S::D == 64 && AT == 4 * kWave, "2 q heads of 64 per kv head, 4 waves");
-  constexpr int D = S::D, NKV = S::NKV, RT = PA_RT;
-  __shared__ PAttnLds<S> sm;
-  // the longest prefixes (the last groups) first: the pass's makespan is
-  // theirs, the short ones fill in behind them
-  const BParams p = group_params(pg, pg.n - 1 - (int)blockIdx.y);
-  const int g = blockIdx.x, cb = (int)blockIdx.z * (PA_NQ / 2);  // the workgroup's first token of the group
-  const int tid = ltid(), w = tid / kWave, l = tid % kWave;
-  const int c16 = l & 15, rg = l >> 4;
-  if (cb >= p.B) return;
-  const int ce = cb + PA_NQ / 2 < p.B ? cb + PA_NQ / 2 : p.B;
-  const int p0 = p.pos[0], pmax = p0 + ce - 1;  // its tokens are positions p0 + cb .. pmax
-  // 1. q of the 32 queries (wave w: queries 8 w .. 8 w + 7; lane = dimension):
-  //    QK-norm (reference rmsnorm.cuh:57-84) and RoPE rotate-half
-  //    (attention.cuh:22-44), as bk_attn's prologue
-  {
-    const uint16_t* gn = p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_Q;
-    const float gain = bf16_to_f32(gn[l]);
-    const int d = l & 31;
-#pragma unroll 2
-    for (int k = 0; k < PA_NQ / AW; ++k) {
-      const int qi = (PA_NQ / AW) * w + k, col = cb + (qi >> 1), j = qi & 1;
-      const bool on = col < p.B;
-      float v = on ? qkv_slot<S>(p, 0)[(long long)col * S::QKV + (g * 2 + j) * D + l] : 0.f;
-      const float ss = wave_sum(v * v);
-      v = on ? v * rsqrtf(ss / (float)D + kRmsEps) * gain : 0.f;
-      const float partner = lane_xor32(v);
-      const float cs = on ? p.rope[(col * 2 + 0) * (D / 2) + d] : 0.f;
-      const float sn = on ? p.rope[(col * 2 + 1) * (D / 2) + d] : 0.f;
-      v = l < 32 ? v * cs - partner * sn : v * cs + partner * sn;
-      uint16_t h, m, o;
-      split_bf16(v, h, m, o);
-      const int rt = qi >> 2, r0 = 4 * (qi & 3);
-      sm.qb[rt][r0 + 0][l] = h;
-      sm.qb[rt][r0 + 1][l] = m;
-      sm.qb[rt][r0 + 2][l] = o;
-      sm.qb[rt][r0 + 3][l] = 0;
+struct PcKV {  // one block's K / V operands of a lane, as loaded (K8: FP8 codes, converted at use)
+  using Reg = typename std::conditional<K8, u32x2, u32x4>::type;
+  Reg k[2][2];  // [16-position half][32-dim chunk]
+  Reg v[S::D / 16];  // [16-dim tile]: positions (4 gq .. 4 gq + 3, 16 + 4 gq .. 16 + 4 gq + 3)
+  f32x4 sk[2], sv[2];  // K8: row scales of the lane's score positions t0 + 16 h + 4 gq + i
+};
+// bf16 operand of a loaded register: FP8 codes converted exactly (scale 1)
+__device__ __forceinline__ u32x4 pc_op(u32x4 r) { return r; }
+__device__ __forceinline__ u32x4 pc_op(u32x2 r) { return fp8x8_to_bf16x8_scaled(r, 1.0f); }
+template <class S, bool K8>
+__device__ __forceinline__ void pc_load(const BParams& p, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                        long long sbase, int t0, unsigned c16, unsigned gq, PcKV<S, K8>& r) {
+  constexpr int D = S::D;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const unsigned e = ((unsigned)t0 + 16u * h + c16) * D + 32u * kc + 8u * gq;
+      if constexpr (K8)
+        r.k[h][kc] = __builtin_amdgcn_raw_buffer_load_b64(rk, e, 0u, 2);
+      else
+        r.k[h][kc] = __builtin_amdgcn_raw_buffer_load_b128(rk, e * 2u, 0u, 2);
+    }
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) {
+    const unsigned e = (unsigned)t0 * D + (16u * dt + c16) * 32u + 4u * gq;
+    if constexpr (K8) {
+      r.v[dt] = u32x2{__builtin_amdgcn_raw_buffer_load_b32(rv, e, 0u, 2),
+                      __builtin_amdgcn_raw_buffer_load_b32(rv, e + 16u, 0u, 2)};
+    } else {
+      const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, e * 2u, 0u, 2);
+      const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(rv, (e + 16u) * 2u, 0u, 2);
+      r.v[dt] = u32x4{a[0], a[1], b[0], b[1]};
     }
   }
-  __syncthreads();
-  // 2. the wave's blocks: online softmax per query on the matrix cores; lane
-  //    (rg, c16) holds query 4 rt + rg of tile rt (token 2 rt + rg / 2)
-  const float scale = 1.0f / sqrtf((float)D);
-  // K8: the FP8 cache (byte index = element index; codes converted to bf16
-  // exactly with the K row scale, the V row scale enters the softmax weight)
+  if constexpr (K8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      r.sk[h] = *reinterpret_cast<const f32x4*>(p.kscale + sbase + t0 + 16 * h + 4 * (int)gq);
+      r.sv[h] = *reinterpret_cast<const f32x4*>(p.vscale + sbase + t0 + 16 * h + 4 * (int)gq);
+    }
+  }
+}
+// 8 fp32 values -> NPART bf16x8 parts (3: exact truncation split; 2: RNE hi + lo)
+template <int NPART>
+__device__ __forceinline__ void pc_parts(const float (&x)[8], u32x4 (&o)[NPART]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (NPART == 3) {
+      const Split3 a = split3(x[2 * e]), b = split3(x[2 * e + 1]);
+      o[0][e] = pack_hi16(a.hi, b.hi);
+      o[1][e] = pack_hi16(a.mid, b.mid);
+      o[2][e] = pack_hi16(a.lo, b.lo);
+    } else {
+      uint32_t hi, lo;
+      bf16_hilo2(x[2 * e], x[2 * e + 1], hi, lo);
+      o[0][e] = hi;
+      o[1][e] = lo;
+    }
+  }
+}
+template <class S, bool K8, int NPART = MK_PATTN_NPART>
+__global__ __launch_bounds__(PC_AW * kWave) void bk_pattn(PGroup pg, int layer) {
+  static_assert(S::GQA == 2 && S::D == 64, "2 q heads of 64 per kv head");
+  static_assert(NPART == 2 || NPART == 3, "two or three bf16 parts");
+  constexpr int D = S::D, NKV = S::NKV, AWc = PC_AW, NT = PC_AW * kWave, QT = PC_NQ / 16;
+  constexpr int QP = D + 8;  // padded q row (elements)
+  // q is multiplied by log2(e) / sqrt(D) before it is split, so a score is
+  // already the exponent of 2 of its softmax weight
+  constexpr float kLog2Scale = 1.4426950408889634f / 8.0f;
+  static_assert(D == 64, "1 / sqrt(D) = 1 / 8");
+  __shared__ __attribute__((aligned(16))) uint16_t qs[NPART][PC_NQ][QP];
+  __shared__ float ow[AWc][PC_NQ][D + 4];  // padded rows: the lanes of one store hit distinct banks
+  __shared__ float mw[AWc][PC_NQ], lw[AWc][PC_NQ];
+  // the longest prefixes (the last groups) first
+  const BParams p = group_params(pg, pg.n - 1 - (int)blockIdx.y);
+  const int g = blockIdx.x, tid = ltid(), w = wave_id(), l = (int)lane_id();
+  const unsigned c16 = (unsigned)l & 15u, gq = (unsigned)l >> 4;
   const long long kbase = ((long long)layer * NKV + g) * (long long)p.s_pad * D;
   const long long sbase = ((long long)layer * NKV + g) * p.s_pad;
   const auto rk = K8 ? make_rsrc(reinterpret_cast<const uint8_t*>(p.kv) + kbase) : make_rsrc(p.kv + kbase);
   const auto rv = K8 ? make_rsrc(reinterpret_cast<const uint8_t*>(p.kvt) + kbase) : make_rsrc(p.kvt + kbase);
-  const unsigned lu = (unsigned)l;
-  float m[RT], lsum[RT];
-  int qpos[RT];
-  f32x4 acc[RT][D / 16];
+  // the wave's first block is loading during the prologue, issued before the
+  // group's position is read (block w lies inside the cache whatever the
+  // prefix; unused when the prefix is shorter)
+  PcKV<S, K8> cur, nxt;
+  if (32 * w + 32 <= p.s_pad) pc_load<S, K8>(p, rk, rv, sbase, 32 * w, c16, gq, cur);
+  __builtin_amdgcn_sched_barrier(0);
+  const int p0 = p.pos[0], pmax = p0 + p.B - 1, nblk = pmax / 32 + 1;
+  // 1. q of the 32 queries (wave w: queries NQW w .. NQW w + NQW - 1; lane =
+  //    dimension): QK-norm (reference rmsnorm.cuh:57-84) and RoPE
+  //    rotate-half (attention.cuh:22-44), as bk_attn's prologue; every
+  //    query's loads are issued before the first is used
+  {
+    constexpr int NQW = PC_NQ / AWc;
+    const uint16_t* gn = p.norms + (long long)layer * S::NORM_STRIDE + S::NORM_Q;
+    const float gain = bf16_to_f32(gn[l]);
+    const int d = l & 31;
+    float qv[NQW], qc[NQW], qn[NQW];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    m[rt] = -INFINITY, lsum[rt] = 0.f;
-    const int col = cb + 2 * rt + (rg >> 1);
-    qpos[rt] = col < p.B ? p0 + col : -1;  // -1: no token (every score masked)
+    for (int k = 0; k < NQW; ++k) {
+      const int q = NQW * w + k, col = q >> 1, j = q & 1;
+      const bool on = col < p.B;
+      qv[k] = on ? qkv_slot<S>(p, 0)[(long long)col * S::QKV + (g * 2 + j) * D + l] : 0.f;
+      qc[k] = on ? p.rope[(col * 2 + 0) * (D / 2) + d] : 0.f;
+      qn[k] = on ? p.rope[(col * 2 + 1) * (D / 2) + d] : 0.f;
+    }
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < NQW; ++k) {
+      const int q = NQW * w + k, col = q >> 1;
+      const bool on = col < p.B;
+      float v = qv[k];
+      const float ss = wave_sum(v * v);
+      v = on ? v * rsqrtf(ss / (float)D + kRmsEps) * gain : 0.f;
+      const float partner = lane_xor32(v);
+      const float cs = qc[k], sn = qn[k];
+      v = l < 32 ? v * cs - partner * sn : v * cs + partner * sn;
+      v *= kLog2Scale;  // scores in log2 units, softmax scale included
+      if constexpr (NPART == 3) {
+        uint16_t h, m, o;
+        split_bf16(v, h, m, o);
+        qs[0][q][l] = h, qs[1][q][l] = m, qs[2][q][l] = o;
+      } else {
+        uint32_t h, o;
+        bf16_hilo2(v, 0.f, h, o);
+        qs[0][q][l] = (uint16_t)h, qs[1][q][l] = (uint16_t)o;
+      }
+    }
   }
-  const int nblk = pmax / 32 + 1;
-  for (int kb = w; kb < nblk; kb += AW) {
-    const int t0 = 32 * kb;
-    u32x4 kr[2][2], vr[D / 16];
-    float sk[2] = {1.f, 1.f}, sv[2] = {1.f, 1.f};  // K8: the scales of the lane's two score positions
+  __syncthreads();
+  // the q parts as B operands, held for the whole loop
+  u32x4 qb[QT][NPART][2];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int pt = 0; pt < NPART; ++pt)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+        qb[qt][pt][kc] = *reinterpret_cast<const u32x4*>(&qs[pt][16 * qt + c16][32 * kc + 8 * gq]);
+  // 2. the wave's blocks
+  float m[QT], ls[QT];
+  int qpos[QT];
+  f32x4 acc[QT][D / 16];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m[qt] = -INFINITY, ls[qt] = 0.f;
+    const int col = (16 * qt + (int)c16) >> 1;
+    qpos[qt] = col < p.B ? p0 + col : -1;  // -1: no token (every score masked)
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // the first position of a tile's queries when all its 8 tokens exist, else
+  // -1: a block that ends at or before it is visible to every query of the
+  // tile (no mask)
+  int qmin[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) qmin[qt] = 8 * qt + 7 < p.B ? p0 + 8 * qt : -1;
+  // one query tile's products and online-softmax step on a block (r: its K /
+  // V operands); MASK: the causal mask and the guards of a query that has no
+  // visible position yet
+  const auto step = [&](auto mask_c, int qt, int t0, const PcKV<S, K8>& r) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask_c)::value;
+    float sc[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+      f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const unsigned e = (unsigned)(t0 + 16 * h) * D + (lu & 15u) * D + 32u * kc + 8u * (lu >> 4);
-        if constexpr (K8)
-          kr[h][kc] = fp8x8_to_bf16x8_scaled(__builtin_amdgcn_raw_buffer_load_b64(rk, e, 0u, 2), 1.0f);
-        else
-          kr[h][kc] = __builtin_amdgcn_raw_buffer_load_b128(rk, e * 2u, 0u, 2);
-      }
-      if constexpr (K8) {
-        sk[h] = p.kscale[sbase + t0 + 16 * h + c16];
-        sv[h] = p.vscale[sbase + t0 + 16 * h + c16];
-      }
-    }
+      for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      const unsigned e = (unsigned)t0 * D + (16u * dt + (lu & 15u)) * 32u + 8u * (lu >> 4);
-      if constexpr (K8)
-        vr[dt] = fp8x8_to_bf16x8_scaled(__builtin_amdgcn_raw_buffer_load_b64(rv, e, 0u, 2), 1.0f);
-      else
-        vr[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, e * 2u, 0u, 2);
-    }
+        for (int pt = 0; pt < NPART; ++pt) d4 = mfma(pc_op(r.k[h][kc]), qb[qt][pt][kc], d4);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      float sc[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        f32x4 d4 = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-          d4 = mfma(*reinterpret_cast<const u32x4*>(&sm.qb[rt][c16][32 * kc + 8 * rg]), kr[h][kc], d4);
-        const int t = t0 + 16 * h + c16;
+      for (int i = 0; i < 4; ++i) {
         // K8: the K row scale (a power of two) multiplies the exact product
-        sc[h] = t <= qpos[rt] ? ((d4[0] + d4[1]) + d4[2]) * sk[h] * scale : -INFINITY;
+        const float x = K8 ? d4[i] * r.sk[h][i] : d4[i];
+        sc[h][i] = MASK && t0 + 16 * h + 4 * (int)gq + i > qpos[qt] ? -INFINITY : x;
       }
-      const float mn = fmaxf(m[rt], group_max<16>(fmaxf(sc[0], sc[1])));
-      // a query none of whose positions so far is visible keeps m = -inf,
-      // weight 0 and scale 1 (no -inf - -inf)
-      const float alpha = mn == -INFINITY ? 1.f : __expf(m[rt] - mn);
-      m[rt] = mn;
-      float ps = 0.f;
+    }
+    float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    bm = max_xor32(max_xor16(bm));
+    const float mo = m[qt], mn = fmaxf(mo, bm);
+    m[qt] = mn;
+    float pw[8], ps = 0.f;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        sc[h] = mn == -INFINITY ? 0.f : __expf(sc[h] - mn);
-        ps += sc[h];
-      }
-      lsum[rt] = lsum[rt] * alpha + group_sum<16>(ps);
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const Split3 a = split3(K8 ? sc[h] * sv[h] : sc[h]);
-        sm.pb[w][rt][4 * rg + 0][16 * h + c16] = (uint16_t)(a.hi >> 16);
-        sm.pb[w][rt][4 * rg + 1][16 * h + c16] = (uint16_t)(a.mid >> 16);
-        sm.pb[w][rt][4 * rg + 2][16 * h + c16] = (uint16_t)(a.lo >> 16);
-        sm.pb[w][rt][4 * rg + 3][16 * h + c16] = 0;
+      for (int i = 0; i < 4; ++i) {
+        // a query none of whose positions so far is visible keeps m = -inf
+        // and weight 0 (no -inf - -inf)
+        const float e = MASK && mn == -INFINITY ? 0.f : exp2f(sc[h][i] - mn);
+        ps += e;
+        pw[4 * h + i] = K8 ? e * r.sv[h][i] : e;  // the V row scale enters the weight
       }
+    // the running state is rescaled only when some query's maximum grew (the
+    // factor is exactly 1 otherwise).  The branch is taken by the whole wave:
+    // a query still without a visible position (mn = mo = -inf) keeps factor
+    // 1, not exp2(-inf - -inf)
+    if (__builtin_amdgcn_ballot_w64(mn != mo)) {
+      const float alpha = MASK && mn == -INFINITY ? 1.f : exp2f(mo - mn);
+      ls[qt] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[rt][dt][i] *= alpha;
+        for (int i = 0; i < 4; ++i) acc[qt][dt][i] *= alpha;
     }
-    asm volatile("" ::: "memory");  // LDS operations of one wave complete in order
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const u32x4 pa = *reinterpret_cast<const u32x4*>(&sm.pb[w][rt][c16][8 * rg]);
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) acc[rt][dt] = mfma(pa, vr[dt], acc[rt][dt]);
-    }
-    asm volatile("" ::: "memory");  // the next block's weight parts are written after these reads
-  }
-  // 3. combine the waves (ow aliases pb: every wave's last reads of pb are
-  //    done at the barrier) and write the merged output as bf16 hi / lo parts
-  __syncthreads();
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int q = 4 * rt + rg;
+    ls[qt] += ps;
+    u32x4 pb[NPART];
+    pc_parts<NPART>(pw, pb);
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt)
-      sm.ow[w][q][16 * dt + c16] = (acc[rt][dt][0] + acc[rt][dt][1]) + acc[rt][dt][2];
-    if (c16 == 0) {
-      sm.mw[w][q] = m[rt];
-      sm.lw[w][q] = lsum[rt];
+#pragma unroll
+      for (int pt = 0; pt < NPART; ++pt) acc[qt][dt] = mfma(pc_op(r.v[dt]), pb[pt], acc[qt][dt]);
+  };
+  const auto block = [&](int t0, const PcKV<S, K8>& r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      if (t0 + 31 <= qmin[qt]) step(std::false_type{}, qt, t0, r);
+      else step(std::true_type{}, qt, t0, r);
+    }
+  };
+  // two register sets in turn (no copy between them: a copy would wait for
+  // the next block's loads before the current block's products).  Every
+  // iteration issues both sets' loads (past the prefix they repeat its last
+  // block, unused), so that each product waits for exactly its own block's
+  // loads: with a conditional issue the compiler's waits, merged over both
+  // paths, also waited for the block after.
+  // The scheduling barriers keep the loads where they are: the scheduler
+  // otherwise sinks them to their first use.
+  for (int kb = w; kb < nblk; kb += 2 * AWc) {
+    pc_load<S, K8>(p, rk, rv, sbase, 32 * min(kb + AWc, nblk - 1), c16, gq, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    block(32 * kb, cur);
+    if (kb + AWc >= nblk) break;
+    pc_load<S, K8>(p, rk, rv, sbase, 32 * min(kb + 2 * AWc, nblk - 1), c16, gq, cur);
+    __builtin_amdgcn_sched_barrier(0);
+    block(32 * (kb + AWc), nxt);
+  }
+  // 3. combine the waves and write the output as bf16 hi / lo parts
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int q = 16 * qt + (int)c16;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ow[w][q][16 * dt + 4 * gq + i] = acc[qt][dt][i];
+    const float lt = sum_xor32(sum_xor16(ls[qt]));
+    if (gq == 0) {
+      mw[w][q] = m[qt];
+      lw[w][q] = lt;
     }
   }
   __syncthreads();
   {
     const int d = tid % D;
 #pragma unroll
-    for (int k = 0; k < PA_NQ / (AT / D); ++k) {
-      const int q = tid / D + (AT / D) * k, col = cb + (q >> 1), j = q & 1;
+    for (int k = 0; k < PC_NQ / (NT / D); ++k) {
+      const int q = tid / D + (NT / D) * k, col = q >> 1, j = q & 1;
       if (col >= p.B) continue;
-      float M = sm.mw[0][q];
+      float M = mw[0][q];
 #pragma unroll
-      for (int i = 1; i < AW; ++i) M = fmaxf(M, sm.mw[i][q]);
+      for (int i = 1; i < AWc; ++i) M = fmaxf(M, mw[i][q]);
       float o = 0.f, L = 0.f;
 #pragma unroll
-      for (int i = 0; i < AW; ++i) {
-        const float f = sm.mw[i][q] == -INFINITY ? 0.f : __expf(sm.mw[i][q] - M);
-        o = fmaf(f, sm.ow[i][q][d], o);
-        L = fmaf(f, sm.lw[i][q], L);
+      for (int i = 0; i < AWc; ++i) {
+        const float f = mw[i][q] == -INFINITY ? 0.f : exp2f(mw[i][q] - M);
+        o = fmaf(f, ow[i][q][d], o);
+        L = fmaf(f, lw[i][q], L);
       }
       uint16_t hi, lo;
       split2(o / L, hi, lo);
