@@ -141,8 +141,12 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
                          l);
       hipLaunchKernelGGL((bk_pattn<S, false>), dim3(S::NKV, ng), dim3(PC_AW * kWave), 0, h->stream, g, l);
     }
-    hipLaunchKernelGGL((bk_ptile<S, PT_O, PTileO>), dim3(S::H / 16 / PTileO::MP, rows(PTileO::NG)), dim3(GT), 0,
-                       h->stream, g, l);
+    if (ng > PT_SMALL_GROUPS)
+      hipLaunchKernelGGL((bk_ptile<S, PT_O, PTileO>), dim3(S::H / 16 / PTileO::MP, rows(PTileO::NG)), dim3(GT), 0,
+                         h->stream, g, l);
+    else
+      hipLaunchKernelGGL((bk_ptile<S, PT_O, PTileOs>), dim3(S::H / 16 / PTileOs::MP, rows(PTileOs::NG)), dim3(GT), 0,
+                         h->stream, g, l);
     if (ng > PT_SMALL_GROUPS)
       hipLaunchKernelGGL((bk_pgu_t<S, PTileGU>), dim3(S::F / 16 / PTileGU::MP, rows(PTileGU::NG)), dim3(GT), 0,
                          h->stream, g, l);

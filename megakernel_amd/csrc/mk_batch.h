@@ -780,13 +780,18 @@ using PTileGUs = PTile<8, 2, 2, 2, 1>;
 #define MK_PT_SMALL_GROUPS 32
 #endif
 constexpr int PT_SMALL_GROUPS = MK_PT_SMALL_GROUPS;
-// QKV and O with direct-to-LDS loads (QKV three stages: four, 96 KB of LDS,
-// leave one workgroup per CU and took 18.1 -> 21.1 us; O four stages of two
-// tiles 20.9 -> 20.0 us); down keeps register staging (four direct-load
-// stages measured 38.4 -> 38.7 us)
+// Direct-to-LDS loads (us per layer at 1,024 tokens): QKV three stages of
+// two tiles (four, 96 KB of LDS, leave one workgroup per CU: 18.1 -> 21.1;
+// chunks of four tiles 19.5); O and down 8 x 2 tiles, chunks of four tiles,
+// three stages (144 KB: one workgroup per CU, 256 workgroups), each wave 2
+// blocks x 1 group: O 20.9 -> 18.9, down 38.4 -> 32.3 (register-staged 4 x 2
+// tiles before; down 4 x 2 with four direct-load stages 38.7, 8 x 2 with
+// chunks of two tiles and three / four / six stages 33.2 / 33.0 / 35.1, 4 x 4
+// 35.8)
 using PTileQKV = PTile<8, 2, 2, 2, 1, 2, 3>;
-using PTileO = PTile<4, 2, 2, 1, 1, 2, 4>;
-using PTileDN = PTile<4, 2, 4, 1, 1, 1>;   // one register set: two lose 8 % at 1,024 tokens
+using PTileO = PTile<8, 2, 4, 2, 1, 2, 3>;
+using PTileOs = PTile<4, 2, 2, 1, 1, 2, 4>;  // passes of at most PT_SMALL_GROUPS groups (twice the workgroups)
+using PTileDN = PTile<8, 2, 4, 2, 1, 1, 3>;
 using PTileDNs = PTile<4, 2, 4, 1, 1, 2>;  // passes of at most PT_SMALL_GROUPS groups
 
 template <class S, class T>
