@@ -130,8 +130,12 @@ static int launch_prefill(BHandle* h, const PGroup& g, const BParams& pl, bool l
   const BParams& p = g.p;
   hipLaunchKernelGGL((bk_embed<S, PGroup>), dim3(BMAX, ng), dim3(256), 0, h->stream, g);
   for (int l = 0; l < L; ++l) {
-    hipLaunchKernelGGL((bk_ptile<S, PT_QKV, PTileQKV>), dim3(S::QKV / 16 / PTileQKV::MP, rows(PTileQKV::NG)), dim3(GT),
-                       0, h->stream, g, l);
+    if (ng > PT_SMALL_GROUPS)
+      hipLaunchKernelGGL((bk_ptile<S, PT_QKV, PTileQKV>), dim3(S::QKV / 16 / PTileQKV::MP, rows(PTileQKV::NG)),
+                         dim3(GT), 0, h->stream, g, l);
+    else
+      hipLaunchKernelGGL((bk_ptile<S, PT_QKV, PTileQKVs>), dim3(S::QKV / 16 / PTileQKVs::MP, rows(PTileQKVs::NG)),
+                         dim3(GT), 0, h->stream, g, l);
     if (p.kscale) {
       hipLaunchKernelGGL((bk_append<S, true, PGroup>), dim3(BMAX * S::NKV, ng), dim3(2 * kWave), 0, h->stream, g,
                          l);

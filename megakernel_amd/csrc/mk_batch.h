@@ -788,7 +788,8 @@ constexpr int PT_SMALL_GROUPS = MK_PT_SMALL_GROUPS;
 // tiles before; down 4 x 2 with four direct-load stages 38.7, 8 x 2 with
 // chunks of two tiles and three / four / six stages 33.2 / 33.0 / 35.1, 4 x 4
 // 35.8)
-using PTileQKV = PTile<8, 2, 2, 2, 1, 2, 3>;
+using PTileQKV = PTile<16, 2, 2, 4, 1, 2, 3>;  // 17.5 -> 16.7 us against 8 x 2 (16 x 2 with chunks of four: 18.9)
+using PTileQKVs = PTile<8, 2, 2, 2, 1, 2, 3>;  // passes of at most PT_SMALL_GROUPS groups
 using PTileO = PTile<8, 2, 4, 2, 1, 2, 3>;
 using PTileOs = PTile<4, 2, 2, 1, 1, 2, 4>;  // passes of at most PT_SMALL_GROUPS groups (twice the workgroups)
 using PTileDN = PTile<8, 2, 4, 2, 1, 1, 3>;
