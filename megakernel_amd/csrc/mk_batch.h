@@ -783,14 +783,17 @@ constexpr int PT_SMALL_GROUPS = MK_PT_SMALL_GROUPS;
 // Direct-to-LDS loads (us per layer at 1,024 tokens): QKV three stages of
 // two tiles (four, 96 KB of LDS, leave one workgroup per CU: 18.1 -> 21.1;
 // chunks of four tiles 19.5); O and down 8 x 2 tiles, chunks of four tiles,
-// three stages (144 KB: one workgroup per CU, 256 workgroups), each wave 2
-// blocks x 1 group: O 20.9 -> 18.9, down 38.4 -> 32.3 (register-staged 4 x 2
+// three stages (144 KB: one workgroup per CU, 256 workgroups): O 20.9 ->
+// 18.9, down 38.4 -> 32.3 (register-staged 4 x 2
 // tiles before; down 4 x 2 with four direct-load stages 38.7, 8 x 2 with
 // chunks of two tiles and three / four / six stages 33.2 / 33.0 / 35.1, 4 x 4
-// 35.8)
+// 35.8).  Each wave owns 1 block x 2 groups in O and 2 blocks x 1 group in
+// down: with 2 x 1 the epilogue's rows reach memory about twice (17.7 MB
+// written per launch against 8.7 MB of output, WRITE_SIZE), with 1 x 2 once,
+// at the same O time and 0.8 us more for down.
 using PTileQKV = PTile<16, 2, 2, 4, 1, 2, 3>;  // 17.5 -> 16.7 us against 8 x 2 (16 x 2 with chunks of four: 18.9)
 using PTileQKVs = PTile<8, 2, 2, 2, 1, 2, 3>;  // passes of at most PT_SMALL_GROUPS groups
-using PTileO = PTile<8, 2, 4, 2, 1, 2, 3>;
+using PTileO = PTile<8, 2, 4, 1, 2, 2, 3>;  // each wave 1 block x 2 groups (2 x 1 wrote its outputs twice)
 using PTileOs = PTile<4, 2, 2, 1, 1, 2, 4>;  // passes of at most PT_SMALL_GROUPS groups (twice the workgroups)
 using PTileDN = PTile<8, 2, 4, 2, 1, 1, 3>;
 using PTileDNs = PTile<4, 2, 4, 1, 1, 2>;  // passes of at most PT_SMALL_GROUPS groups
