@@ -724,7 +724,10 @@ struct PTile {
 // passed in M0.  It counts on vmcnt like any vector load and writes no
 // register.  Inline assembly, so that the compiler does not add its own
 // conservative wait for every such load in flight before each LDS read: the
-// caller waits for exactly the loads it needs (wait_vmcnt).
+// caller waits for exactly the loads it needs (wait_vmcnt).  M0 is declared
+// clobbered (the compiler warns, M0 being reserved); the GEMM kernels that
+// use this have no other M0 user (no compiler-issued LDS DMA, no indirect
+// register indexing: every register array index is a compile-time constant).
 __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
   const unsigned m0 = __builtin_amdgcn_readfirstlane(
       (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)dst);
