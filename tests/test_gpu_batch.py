@@ -305,6 +305,18 @@ def test_batch_prefill_baseline_2l_two_passes():
     dw.free()
 
 
+def test_batch_prefill_baseline_2l_odd_large_pass():
+    """A pass of 33 column groups (520 tokens after a 37-position prefix): the
+    large-pass GEMM tiles (more than 32 groups) with column tiles that are
+    only partly filled (2-group tiles of QKV / O / down and 8-group tiles of
+    gate / up each end on one group, the last group half full), so the
+    direct-to-LDS K loops load a stand-in group for the missing ones."""
+    shape = BASELINE.with_(n_layers=2, vocab=4096)
+    dw, eng, _, _ = _prefill_case(shape, 46, prefix=37, prompt_len=520, other_len=3, max_seq=600)
+    eng.close()
+    dw.free()
+
+
 def test_batch_prefill_errors():
     dw = DeviceWeights(TINY, 44)
     eng = BatchEngine(dw, 2, 32, TINY)
